@@ -1,0 +1,242 @@
+/*
+ * pfa_hip.h -- C ABI of libpfa_hip.so, the MI355X (gfx950) kernels behind the
+ * ASPA (Adaptive Sparse Proto Attention) forward path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, sizes and a hipStream_t passed as void*;
+ *   - enqueues work on that stream and returns without synchronising;
+ *   - allocates nothing: scratch memory is passed in as a caller-owned
+ *     workspace whose size is obtained from the matching *_workspace_size();
+ *   - returns 0 on success, a positive hipError_t value when a HIP call
+ *     failed, or a negative PFA_E_* code for an argument error.  The message
+ *     of the most recent failure on the calling thread is available from
+ *     pfa_last_error_string().
+ *
+ * Index conventions: token indices, packed row offsets and candidate lists
+ * are int32 on the device.  Tensors the reference exposes as int64 are
+ * widened by the Python layer only where its public API returns them.
+ *
+ * Each declaration names the reference function (file:line, relative to the
+ * Proteus-Flux-Attention source tree) whose behaviour it replaces.
+ */
+#ifndef PFA_HIP_H
+#define PFA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------- */
+#define PFA_OK 0
+#define PFA_E_INVALID (-1)      /* bad size / flag / pointer combination   */
+#define PFA_E_UNSUPPORTED (-2)  /* valid request this build does not cover */
+#define PFA_E_WORKSPACE (-3)    /* workspace smaller than required         */
+
+/* ---- element type tags ---------------------------------------------- */
+#define PFA_F32 0
+#define PFA_BF16 1
+#define PFA_F16 2
+#define PFA_I8 3   /* symmetric int8 with a float scale per head */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int pfa_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* pfa_last_error_string(void);
+
+/* ====================================================================
+ * Router: SwitchRouter logits+softmax, prototype prior, blend, usage boost,
+ * renormalisation, importance and head top-k in one pass over x.
+ * Replaces SwitchRouter.forward (src/proteus_attention/models/aspa.py:149-157),
+ * AdaptiveSparseAttention._route_tokens (aspa.py:628-690), the importance
+ * blend (aspa.py:1521-1530), gate->head aggregation (aspa.py:1540-1542) and
+ * torch.topk over heads (aspa.py:1590-1591).  Ties in the head top-k go to
+ * the lowest head index.
+ *
+ *   x            (n_tok, C) in x_dtype (PFA_F32 / PFA_BF16 / PFA_F16)
+ *   w_router     (G, C) in x_dtype              (head_router.linear.weight)
+ *   proto_norm   (G, C) f32, rows already L2-normalised, or NULL (proto off)
+ *   conf_weight  (G) f32 = routing_confidence + 1e-6, or NULL
+ *   usage_bias   (G) f32 = softmax(-(usage+1e-6)), or NULL (boost off)
+ *   gate_to_head (G) int32, values in [0, H)
+ *   outputs (NULL allowed for any of the optional ones):
+ *     gate_probs (n_tok, G) f32, sim (n_tok) f32, blend (n_tok) f32,
+ *     importance (n_tok) f32 (required), head_idx (n_tok, topk) int32
+ *     (required), head_score (n_tok, topk) f32.
+ * ==================================================================== */
+int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G,
+                    const void* w_router, const float* proto_norm,
+                    const float* conf_weight, const float* usage_bias,
+                    const int32_t* gate_to_head, int H, int topk,
+                    float proto_temp, float proto_threshold, float proto_blend,
+                    float usage_boost, float* gate_probs, float* sim,
+                    float* blend, float* importance, int32_t* head_idx,
+                    float* head_score, void* stream);
+
+/* ====================================================================
+ * Prototype EMA statistics (aspa.py:692-718): per slice of tokens the
+ * partial sums  sum_t gate[t,g]*x[t,c]  (columns 0..C-1) and
+ * sum_t gate[t,g]  (column C), laid out (n_parts, G, C+1) f32, then summed
+ * in a fixed order into (G, C+1).  Replaces the (G,BT)@(BT,C) product of
+ * aspa.py:703-707 without materialising x in f32.
+ * ==================================================================== */
+int pfa_proto_partial_count(int64_t n_tok, int* n_parts);
+int pfa_proto_accumulate(const void* x, int x_dtype, int64_t n_tok, int C,
+                         int G, const float* gate_probs, float* partial,
+                         int n_parts, void* stream);
+int pfa_proto_partial_reduce(const float* partial, int n_parts, int G, int C,
+                             float* out, void* stream);
+
+/* ====================================================================
+ * Token top-k: per batch row keep the `need` highest importance tokens
+ * (ties -> lowest index), need = clamp(max(keep_count, #(imp >= threshold),
+ * guard), 1, T); the first `guard` tokens are always kept.
+ * Replaces AdaptiveSparseAttention._select_active_tokens
+ * (aspa.py:790-842).  importance (B, T) f32 -> mask (B, T) uint8.
+ * ==================================================================== */
+int pfa_token_topk(const float* importance, int B, int64_t T, int64_t keep_count,
+                   int guard, float threshold, uint8_t* mask_out, void* stream);
+
+/* ====================================================================
+ * Row packing.  Builds the (B*H, T) activity mask from the head top-k
+ * indices and an optional token mask, compacts active (batch, head) pairs
+ * and packs active (head, token) rows in row-major order (ascending token
+ * within a head).
+ * Replaces the mask build (aspa.py:1593-1606), active-head compaction
+ * (aspa.py:1704-1726) and _pack_active_rows
+ * (src/proteus_attention/kernels/sparse_attn.py:924-947).
+ *
+ *   head_idx    (B*T, topk) int32 (router output)
+ *   token_mask  (B, T) uint8 or NULL
+ *   mask_out    (B*H, T) uint8, required
+ *   active_heads_out (B*H) int32  : compact id -> b*H+h (first P valid)
+ *   row_offsets_out  (B*H + 1) int32 : exclusive scan over active heads
+ *   token_idx_out    (B*H*T) int32 capacity : token of each packed row
+ *   row_head_out     (B*H*T) int32 capacity : compact head of each row
+ *   summary_out (4) int32 : {P, N, max_rows, 0}
+ * The workspace holds per-(head, block) counts.
+ * ==================================================================== */
+int pfa_pack_workspace_size(int B, int H, int64_t T, size_t* bytes);
+int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* token_mask,
+                  int B, int H, int64_t T, uint8_t* mask_out,
+                  int32_t* active_heads_out, int32_t* row_offsets_out,
+                  int32_t* token_idx_out, int32_t* row_head_out,
+                  int32_t* summary_out, void* workspace, size_t ws_bytes,
+                  void* stream);
+
+/* Same packing from an arbitrary (P, T) uint8 mask (the operator-level
+ * entry point aspa_sparse_attention packs its own active_mask). Heads are
+ * NOT compacted: compact id == mask row. */
+int pfa_pack_mask(const uint8_t* mask, int P, int64_t T, int32_t* row_offsets_out,
+                  int32_t* token_idx_out, int32_t* row_head_out,
+                  int32_t* summary_out, void* workspace, size_t ws_bytes,
+                  void* stream);
+
+/* ====================================================================
+ * Prototype candidates: for every token t of every batch row b, the
+ * indices of the min(t+1, K) largest proto_scores[b, 0..t] (ties -> lowest
+ * index), written sorted by index into (B, T, K) int32.
+ * Replaces the (rows, T) masked topk of _shortlist_prepare_proto_candidates
+ * (sparse_attn.py:260-300) by a blocked prefix top-k.
+ * ==================================================================== */
+int pfa_proto_prefix_workspace_size(int B, int64_t T, int K, size_t* bytes);
+int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T,
+                          int64_t score_stride, int K, int32_t* sets_out,
+                          void* workspace, size_t ws_bytes, void* stream);
+
+/* ====================================================================
+ * Shortlist candidate builder (packed rows).
+ * Replaces build_packed_shortlist_candidates (sparse_attn.py:457-596) and
+ * build_shortlist_candidates (sparse_attn.py:376-454): per row the union of
+ * the local window, strided anchors, prototype top-k and optional extra
+ * candidates, clamped to [0, min(row, seq_len-1)], the row itself appended,
+ * sorted ascending, de-duplicated, truncated to the smallest L values and
+ * padded with the row index; lengths = max(count, 1).
+ *
+ *   rows (N) int32 (tokens, each in [0, seq_len)), row_batch (N) int32 or
+ *     NULL (batch 0)
+ *   local_w: effective window min(linear_window, L, local_cap), 0 = no
+ *     local piece;  anchor_slots: min(anchor_cap, L, max(1, seq_len)),
+ *     0 = no anchors (sparse_attn.py:413-429)
+ *   proto_sets (B, proto_len, proto_k) int32 from pfa_proto_prefix_topk, or
+ *     NULL; row t uses set min(t, proto_len-1)
+ *   extra (N, extra_width) int32 + extra_len (N) int32, or NULL
+ *   cand_out (N, L) int32 or int64 (cand_is_i64), len_out (N) int32/int64
+ * ==================================================================== */
+int pfa_shortlist_build(const int32_t* rows, const int32_t* row_batch, int64_t N,
+                        int64_t seq_len, int L, int local_w, int anchor_stride,
+                        int anchor_slots, const int32_t* proto_sets,
+                        int proto_k, int64_t proto_len, const int32_t* extra,
+                        const int32_t* extra_len, int extra_width,
+                        void* cand_out, int cand_is_i64, void* len_out,
+                        int len_is_i64, void* stream);
+
+/* ====================================================================
+ * Packed sparse attention (online softmax), fused gather and scatter.
+ * Replaces the Triton _shortlist_attention_kernel (sparse_attn.py:597-921)
+ * and the PyTorch fallback _fallback_sparse_attention
+ * (sparse_attn.py:950-1046) behind aspa_sparse_attention
+ * (sparse_attn.py:1373-1646).
+ *
+ * Tensors q/k/v/out are addressed as [b][h][t][d] through element strides
+ * so that (B*H, T, D) head-major buffers and the (B, T, 3, H, D) output of
+ * the QKV projection are both read in place:
+ *   addr(bh, t, d) = base + (bh / H) * s_b + (bh % H) * s_h + t * s_t + d
+ * Row r (packed) belongs to compact head row_head[r] whose global index is
+ * head_map[row_head[r]] (head_map NULL: identity) and queries token
+ * token_idx[r].
+ *
+ * Key set of row r:
+ *   cand != NULL : cand[r, 0 .. len[r])                (candidate branch)
+ *   cand == NULL, mask == NULL : keys 0 .. token_idx[r] (implicit causal)
+ *   cand == NULL, mask != NULL : keys 0 .. head_max_token[head] with the
+ *       additive (T, T) mask row token_idx[r] added (mask_dtype).
+ * With a mask in the candidate branch, mask[token, cand] is added.
+ * Scores are scaled by `scale`; for PFA_I8 inputs element values are
+ * multiplied by the per-global-head scales q_scale/k_scale/v_scale.
+ * A row with no finite score produces NaN, as softmax over all -inf does.
+ * ==================================================================== */
+typedef struct pfa_tensor4 {
+  void* ptr;
+  int64_t s_b, s_h, s_t; /* element strides; d is contiguous */
+} pfa_tensor4;
+
+int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
+                        int in_dtype, pfa_tensor4 out, int out_dtype, int H,
+                        int64_t T, int D, const int32_t* token_idx,
+                        const int32_t* row_head, const int32_t* head_map,
+                        int64_t N, const int32_t* cand, int64_t cand_stride,
+                        const int32_t* cand_len, const void* mask,
+                        int mask_dtype, const int32_t* head_max_token,
+                        float scale, const float* q_scale, const float* k_scale,
+                        const float* v_scale, void* stream);
+
+/* Per compact head, the largest token among its packed rows (needed by the
+ * explicit-mask branch: sparse_attn.py:1010-1015). */
+int pfa_head_max_token(const int32_t* token_idx, const int32_t* row_offsets,
+                       int P, int32_t* out, void* stream);
+
+/* ====================================================================
+ * RoPE on the q and k thirds of a (B, T, 3C) QKV projection, in place.
+ * Replaces _apply_rope_embedding (aspa.py:606-618): interleaved (even,
+ * odd) pairs rotated with cos/sin tables (T, D) in the same dtype, each
+ * product and the sum rounded to that dtype as the reference's
+ * elementwise ops do.
+ * ==================================================================== */
+int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D,
+                        const void* cos_tab, const void* sin_tab, void* stream);
+
+/* ====================================================================
+ * Fill: write zeros into `bytes` of device memory with a vector-store
+ * kernel (usable where memset nodes are not wanted).
+ * ==================================================================== */
+int pfa_zero_fill(void* ptr, size_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PFA_HIP_H */

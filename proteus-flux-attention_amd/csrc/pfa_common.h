@@ -1,0 +1,159 @@
+// Shared device helpers and host-side error plumbing for libpfa_hip.so.
+// gfx950 (CDNA4) only: wave64, 160 KiB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/pfa_hip.h"
+
+namespace pfa {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------
+// Host: error reporting.  The message lives in a thread-local string so
+// that concurrent callers on different threads do not overwrite it.
+// ---------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define PFA_CHECK_ARG(cond, ...)          \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::pfa::set_error(__VA_ARGS__);      \
+      return PFA_E_INVALID;               \
+    }                                     \
+  } while (0)
+
+#define PFA_CHECK_LAUNCH(what)                                              \
+  do {                                                                      \
+    hipError_t _e = hipGetLastError();                                      \
+    if (_e != hipSuccess) {                                                 \
+      ::pfa::set_error("%s: launch failed: %s", what, hipGetErrorString(_e)); \
+      return (int)_e;                                                       \
+    }                                                                       \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------------
+// Device: scalar conversions.  bf16 is handled as raw uint16 bits.
+// f32 -> bf16 rounds to nearest even (NaN kept quiet).
+// ---------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __half_as_ushort(__float2half(f));
+}
+
+// Round a float to the precision of a storage type and back (emulates an
+// elementwise op whose result tensor has that dtype).
+template <int DT>
+__device__ __forceinline__ float round_to(float f) {
+  if constexpr (DT == PFA_BF16) return bf16_to_f32(f32_to_bf16(f));
+  else if constexpr (DT == PFA_F16) return f16_to_f32(f32_to_f16(f));
+  else return f;
+}
+
+template <int DT> struct Elem;
+template <> struct Elem<PFA_F32> { using T = float; };
+template <> struct Elem<PFA_BF16> { using T = uint16_t; };
+template <> struct Elem<PFA_F16> { using T = uint16_t; };
+template <> struct Elem<PFA_I8> { using T = int8_t; };
+
+template <int DT>
+__device__ __forceinline__ float load_f(const typename Elem<DT>::T* p) {
+  if constexpr (DT == PFA_F32) return *p;
+  else if constexpr (DT == PFA_BF16) return bf16_to_f32(*p);
+  else if constexpr (DT == PFA_F16) return f16_to_f32(*p);
+  else return (float)(*p);
+}
+template <int DT>
+__device__ __forceinline__ void store_f(typename Elem<DT>::T* p, float f) {
+  if constexpr (DT == PFA_F32) *p = f;
+  else if constexpr (DT == PFA_BF16) *p = f32_to_bf16(f);
+  else if constexpr (DT == PFA_F16) *p = f32_to_f16(f);
+}
+
+// Load 8 consecutive elements (d .. d+7) as floats; the address must be
+// aligned to 8 elements.
+template <int DT>
+__device__ __forceinline__ void load8(const typename Elem<DT>::T* p, float (&o)[8]) {
+  if constexpr (DT == PFA_F32) {
+    const float4* q = reinterpret_cast<const float4*>(p);
+    float4 a = q[0], b = q[1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else if constexpr (DT == PFA_BF16) {
+    uint4 a = *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else if constexpr (DT == PFA_F16) {
+    uint4 a = *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xffffu));
+      o[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
+    }
+  } else {
+    uint2 a = *reinterpret_cast<const uint2*>(p);
+    uint32_t w[2] = {a.x, a.y};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      o[i] = (float)(int8_t)((w[i >> 2] >> (8 * (i & 3))) & 0xffu);
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(typename Elem<DT>::T* p, const float (&v)[8]) {
+  if constexpr (DT == PFA_F32) {
+    float4* q = reinterpret_cast<float4*>(p);
+    q[0] = make_float4(v[0], v[1], v[2], v[3]);
+    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint16_t lo, hi;
+      if constexpr (DT == PFA_BF16) { lo = f32_to_bf16(v[2 * i]); hi = f32_to_bf16(v[2 * i + 1]); }
+      else { lo = f32_to_f16(v[2 * i]); hi = f32_to_f16(v[2 * i + 1]); }
+      w[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Orders LDS/global accesses of the lanes of one wave (a wave-local barrier;
+// kernels that keep per-wave LDS regions use it instead of __syncthreads).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Order used by every top-k in this library: larger value first, equal
+// values -> smaller index first.  NaN compares as smaller than anything.
+__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+  return (va > vb) || (va == vb && ia < ib) || (vb != vb && va == va);
+}
+
+}  // namespace pfa

@@ -1,0 +1,128 @@
+// Library plumbing: version, thread-local error string, zero fill, RoPE.
+#include <cstdarg>
+#include <cstdio>
+
+#include "pfa_common.h"
+
+namespace pfa {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+// Vector-store zero fill: 16 bytes per lane per step, grid-stride.
+__global__ void __launch_bounds__(256) zero_fill_kernel(uint4* p, size_t n16) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t step = (size_t)gridDim.x * blockDim.x;
+  for (; i < n16; i += step) p[i] = make_uint4(0, 0, 0, 0);
+}
+__global__ void zero_fill_tail(uint8_t* p, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// RoPE in place on the q and k thirds of a (B, T, 3, H, D) buffer.  One
+// thread handles one (even, odd) pair of one head of q or k:
+//   out_even = r(r(x_e*cos_e) + r(-x_o*sin_e)),  out_odd = r(r(x_o*cos_o) + r(x_e*sin_o))
+// where r() rounds to the tensor dtype, matching q*cos + rotate_half(q)*sin
+// evaluated as three elementwise ops in that dtype.
+template <int DT>
+__global__ void __launch_bounds__(256) rope_kernel(typename Elem<DT>::T* qkv, int64_t n_pairs, int64_t T,
+                                                   int H, int D, const typename Elem<DT>::T* cos_tab,
+                                                   const typename Elem<DT>::T* sin_tab) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_pairs) return;
+  const int half = D / 2;
+  const int C = H * D;
+  int64_t pair = i % half;
+  int64_t rest = i / half;
+  int h = (int)(rest % H);
+  rest /= H;
+  int which = (int)(rest % 2);  // 0 = q, 1 = k
+  int64_t bt = rest / 2;
+  int64_t t = bt % T;
+  typename Elem<DT>::T* base = qkv + bt * (3 * (int64_t)C) + which * C + h * D + 2 * pair;
+  float xe = load_f<DT>(base), xo = load_f<DT>(base + 1);
+  float ce = load_f<DT>(cos_tab + t * D + 2 * pair), co = load_f<DT>(cos_tab + t * D + 2 * pair + 1);
+  float se = load_f<DT>(sin_tab + t * D + 2 * pair), so = load_f<DT>(sin_tab + t * D + 2 * pair + 1);
+  float e = round_to<DT>(round_to<DT>(xe * ce) + round_to<DT>(-xo * se));
+  float o = round_to<DT>(round_to<DT>(xo * co) + round_to<DT>(xe * so));
+  store_f<DT>(base, e);
+  store_f<DT>(base + 1, o);
+}
+
+}  // namespace pfa
+
+using namespace pfa;
+
+extern "C" int pfa_version(void) { return 100; }
+
+extern "C" const char* pfa_last_error_string(void) { return g_last_error.c_str(); }
+
+extern "C" int pfa_zero_fill(void* ptr, size_t bytes, void* stream) {
+  clear_error();
+  if (bytes == 0) return PFA_OK;
+  PFA_CHECK_ARG(ptr != nullptr, "pfa_zero_fill: null pointer");
+  hipStream_t s = as_stream(stream);
+  size_t head_pad = (16 - ((uintptr_t)ptr & 15)) & 15;
+  if (head_pad > bytes) head_pad = bytes;
+  if (head_pad) {
+    zero_fill_tail<<<1, 16, 0, s>>>((uint8_t*)ptr, head_pad);
+    PFA_CHECK_LAUNCH("pfa_zero_fill");
+  }
+  uint8_t* body = (uint8_t*)ptr + head_pad;
+  size_t rem = bytes - head_pad;
+  size_t n16 = rem / 16;
+  if (n16) {
+    size_t blocks = (n16 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    zero_fill_kernel<<<(unsigned)blocks, 256, 0, s>>>((uint4*)body, n16);
+    PFA_CHECK_LAUNCH("pfa_zero_fill");
+  }
+  size_t tail = rem - n16 * 16;
+  if (tail) {
+    zero_fill_tail<<<1, 16, 0, s>>>(body + n16 * 16, tail);
+    PFA_CHECK_LAUNCH("pfa_zero_fill");
+  }
+  return PFA_OK;
+}
+
+extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D,
+                                   const void* cos_tab, const void* sin_tab, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(qkv && cos_tab && sin_tab, "pfa_rope_qk_inplace: null pointer");
+  PFA_CHECK_ARG(B >= 0 && T >= 0 && H > 0 && D > 0 && D % 2 == 0,
+                "pfa_rope_qk_inplace: bad shape B=%d T=%lld H=%d D=%d", B, (long long)T, H, D);
+  int64_t n_pairs = (int64_t)B * T * 2 * H * (D / 2);
+  if (n_pairs == 0) return PFA_OK;
+  unsigned blocks = (unsigned)((n_pairs + 255) / 256);
+  hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case PFA_F32:
+      rope_kernel<PFA_F32><<<blocks, 256, 0, s>>>((float*)qkv, n_pairs, T, H, D, (const float*)cos_tab,
+                                                   (const float*)sin_tab);
+      break;
+    case PFA_BF16:
+      rope_kernel<PFA_BF16><<<blocks, 256, 0, s>>>((uint16_t*)qkv, n_pairs, T, H, D,
+                                                    (const uint16_t*)cos_tab, (const uint16_t*)sin_tab);
+      break;
+    case PFA_F16:
+      rope_kernel<PFA_F16><<<blocks, 256, 0, s>>>((uint16_t*)qkv, n_pairs, T, H, D,
+                                                   (const uint16_t*)cos_tab, (const uint16_t*)sin_tab);
+      break;
+    default:
+      set_error("pfa_rope_qk_inplace: unsupported dtype %d", dtype);
+      return PFA_E_UNSUPPORTED;
+  }
+  PFA_CHECK_LAUNCH("pfa_rope_qk_inplace");
+  return PFA_OK;
+}

@@ -1,0 +1,398 @@
+// Token top-k (radix select) and row packing.
+#include "pfa_common.h"
+
+namespace pfa {
+
+// ---------------------------------------------------------------------
+// Token top-k.  One workgroup per batch row.  The `need` largest values are
+// found with a 4 x 8-bit radix select on order-preserving 32-bit keys; of the
+// values equal to the cut value, the lowest indices are taken (an ordered
+// scan over the row).  Replaces the per-batch torch.topk loop of
+// aspa.py:823-840.
+// ---------------------------------------------------------------------
+constexpr int kTopkThreads = 1024;
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ int block_sum_int(int v, int* red) {
+  // wave64 reduce then across waves (<= 16 waves)
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  int nw = (blockDim.x + 63) >> 6;
+  int s = 0;
+  for (int i = 0; i < nw; ++i) s += red[i];
+  return s;
+}
+
+__global__ void __launch_bounds__(kTopkThreads)
+token_topk_kernel(const float* __restrict__ imp, int64_t T, int64_t keep_count, int guard, float threshold,
+                  uint8_t* __restrict__ mask) {
+  __shared__ int hist[256];
+  __shared__ int red[16];
+  __shared__ uint32_t s_prefix;
+  __shared__ int64_t s_remaining;
+  const int b = blockIdx.x;
+  const float* row = imp + (int64_t)b * T;
+  uint8_t* mrow = mask + (int64_t)b * T;
+
+  int64_t need = keep_count;
+  if (threshold > 0.f) {
+    int cnt = 0;
+    for (int64_t i = threadIdx.x; i < T; i += blockDim.x) cnt += (row[i] >= threshold) ? 1 : 0;
+    int64_t c = block_sum_int(cnt, red);
+    if (c > need) need = c;
+  }
+  if (guard > need) need = guard;
+  if (need < 1) need = 1;
+  if (need > T) need = T;
+
+  if (need >= T) {
+    for (int64_t i = threadIdx.x; i < T; i += blockDim.x) mrow[i] = 1;
+    return;
+  }
+
+  uint32_t prefix = 0, pmask = 0;
+  int64_t remaining = need;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < T; i += blockDim.x) {
+      uint32_t k = order_key(row[i]);
+      if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 0xffu], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int64_t acc = 0;
+      int bin = 0;
+      for (bin = 255; bin >= 0; --bin) {
+        if (acc + hist[bin] >= remaining) break;
+        acc += hist[bin];
+      }
+      s_prefix = prefix | ((uint32_t)bin << shift);
+      s_remaining = remaining - acc;
+    }
+    __syncthreads();
+    prefix = s_prefix;
+    remaining = s_remaining;
+    pmask |= 0xffu << shift;
+    __syncthreads();
+  }
+  // prefix == key of the need-th largest value; `remaining` elements equal
+  // to it are taken, lowest index first.
+  const uint32_t cut = prefix;
+  int64_t carry = 0;
+  __shared__ int wave_tot[16];
+  for (int64_t base = 0; base < T; base += blockDim.x) {
+    int64_t i = base + threadIdx.x;
+    uint32_t k = (i < T) ? order_key(row[i]) : 0u;
+    int eq = (i < T && k == cut) ? 1 : 0;
+    // inclusive scan of eq across the block
+    int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    int v = eq;
+    for (int off = 1; off < 64; off <<= 1) {
+      int n = __shfl_up(v, off, 64);
+      if (lane >= off) v += n;
+    }
+    if (lane == 63) wave_tot[wid] = v;
+    __syncthreads();
+    int before = 0, total = 0;
+    int nw = blockDim.x >> 6;
+    for (int w = 0; w < nw; ++w) {
+      if (w < wid) before += wave_tot[w];
+      total += wave_tot[w];
+    }
+    int64_t rank = carry + before + v - eq;  // exclusive rank among equal keys
+    if (i < T) {
+      bool sel = (k > cut) || (eq && rank < remaining) || (i < guard);
+      mrow[i] = sel ? 1 : 0;
+    }
+    carry += total;
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------
+// Row packing.  Tiles of kPackTile tokens of one (batch*head) row.
+// ---------------------------------------------------------------------
+constexpr int kPackThreads = 256;
+constexpr int kPackTile = 1024;  // 4 tokens per thread
+
+__global__ void __launch_bounds__(kPackThreads)
+pack_count_routed(const int32_t* __restrict__ head_idx, int topk, const uint8_t* __restrict__ token_mask, int H,
+                  int64_t T, int nblk, uint8_t* __restrict__ mask_out, int32_t* __restrict__ blockcounts) {
+  __shared__ int red[16];
+  const int blk = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / H, h = bh % H;
+  int cnt = 0;
+  for (int j = 0; j < kPackTile / kPackThreads; ++j) {
+    int64_t t = (int64_t)blk * kPackTile + j * kPackThreads + threadIdx.x;
+    if (t < T) {
+      int64_t bt = (int64_t)b * T + t;
+      bool act = token_mask == nullptr || token_mask[bt] != 0;
+      bool sel = false;
+      for (int kk = 0; kk < topk; ++kk) sel |= head_idx[bt * topk + kk] == h;
+      act = act && sel;
+      mask_out[(int64_t)bh * T + t] = act ? 1 : 0;
+      cnt += act ? 1 : 0;
+    }
+  }
+  int s = block_sum_int(cnt, red);
+  if (threadIdx.x == 0) blockcounts[(int64_t)bh * nblk + blk] = s;
+}
+
+__global__ void __launch_bounds__(kPackThreads)
+pack_count_mask(const uint8_t* __restrict__ mask, int64_t T, int nblk, int32_t* __restrict__ blockcounts) {
+  __shared__ int red[16];
+  const int blk = blockIdx.x, bh = blockIdx.y;
+  int cnt = 0;
+  for (int j = 0; j < kPackTile / kPackThreads; ++j) {
+    int64_t t = (int64_t)blk * kPackTile + j * kPackThreads + threadIdx.x;
+    if (t < T) cnt += mask[(int64_t)bh * T + t] ? 1 : 0;
+  }
+  int s = block_sum_int(cnt, red);
+  if (threadIdx.x == 0) blockcounts[(int64_t)bh * nblk + blk] = s;
+}
+
+// Single workgroup: per-row totals, optional compaction of empty rows,
+// row_offsets, and per-(row, tile) base offsets written over blockcounts.
+__global__ void __launch_bounds__(1024)
+pack_scan_kernel(int32_t* __restrict__ blockcounts, int BH, int nblk, int compact, int32_t* __restrict__ totals,
+                 int32_t* __restrict__ compact_id, int32_t* __restrict__ active_heads,
+                 int32_t* __restrict__ row_offsets, int32_t* __restrict__ summary) {
+  __shared__ int wave_tot[16];
+  __shared__ int s_carry_p, s_carry_n, s_max;
+  if (threadIdx.x == 0) { s_carry_p = 0; s_carry_n = 0; s_max = 0; }
+  for (int bh = threadIdx.x; bh < BH; bh += blockDim.x) {
+    int64_t tot = 0;
+    for (int j = 0; j < nblk; ++j) tot += blockcounts[(int64_t)bh * nblk + j];
+    totals[bh] = (int32_t)tot;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int base = 0; base < BH; base += blockDim.x) {
+    int bh = base + threadIdx.x;
+    int tot = (bh < BH) ? totals[bh] : 0;
+    int act = (bh < BH) && (!compact || tot > 0);
+    // scan (act, tot) jointly: two scans
+    int va = act, vn = act ? tot : 0;
+    for (int off = 1; off < 64; off <<= 1) {
+      int na = __shfl_up(va, off, 64), nn = __shfl_up(vn, off, 64);
+      if (lane >= off) { va += na; vn += nn; }
+    }
+    __shared__ int wave_n[16];
+    if (lane == 63) { wave_tot[wid] = va; wave_n[wid] = vn; }
+    __syncthreads();
+    int ba = 0, bn = 0, ta = 0, tn = 0;
+    for (int w = 0; w < nw; ++w) {
+      if (w < wid) { ba += wave_tot[w]; bn += wave_n[w]; }
+      ta += wave_tot[w];
+      tn += wave_n[w];
+    }
+    int cp = s_carry_p, cn = s_carry_n;
+    if (bh < BH) {
+      if (act) {
+        int id = cp + ba + va - 1;
+        int off = cn + bn + vn - tot;
+        compact_id[bh] = id;
+        if (active_heads) active_heads[id] = bh;
+        row_offsets[id] = off;
+        atomicMax(&s_max, tot);
+      } else {
+        compact_id[bh] = -1;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) { s_carry_p = cp + ta; s_carry_n = cn + tn; }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    row_offsets[s_carry_p] = s_carry_n;
+    summary[0] = s_carry_p;
+    summary[1] = s_carry_n;
+    summary[2] = s_max;
+    summary[3] = 0;
+  }
+  __syncthreads();
+  // per-tile bases
+  for (int bh = threadIdx.x; bh < BH; bh += blockDim.x) {
+    int id = compact_id[bh];
+    if (id < 0) continue;
+    int run = row_offsets[id];
+    for (int j = 0; j < nblk; ++j) {
+      int c = blockcounts[(int64_t)bh * nblk + j];
+      blockcounts[(int64_t)bh * nblk + j] = run;
+      run += c;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kPackThreads)
+pack_fill_kernel(const uint8_t* __restrict__ mask, int64_t T, int nblk, const int32_t* __restrict__ bases,
+                 const int32_t* __restrict__ compact_id, int32_t* __restrict__ token_idx,
+                 int32_t* __restrict__ row_head) {
+  __shared__ int wave_tot[4];
+  const int blk = blockIdx.x, bh = blockIdx.y;
+  const int id = compact_id[bh];
+  if (id < 0) return;
+  int run = bases[(int64_t)bh * nblk + blk];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int j = 0; j < kPackTile / kPackThreads; ++j) {
+    int64_t t = (int64_t)blk * kPackTile + j * kPackThreads + threadIdx.x;
+    int act = (t < T && mask[(int64_t)bh * T + t]) ? 1 : 0;
+    int v = act;
+    for (int off = 1; off < 64; off <<= 1) {
+      int n = __shfl_up(v, off, 64);
+      if (lane >= off) v += n;
+    }
+    if (lane == 63) wave_tot[wid] = v;
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < kPackThreads / 64; ++w) {
+      if (w < wid) before += wave_tot[w];
+      total += wave_tot[w];
+    }
+    if (act) {
+      int pos = run + before + v - 1;
+      token_idx[pos] = (int32_t)t;
+      row_head[pos] = id;
+    }
+    run += total;
+    __syncthreads();
+  }
+}
+
+__global__ void head_max_token_kernel(const int32_t* __restrict__ token_idx, const int32_t* __restrict__ row_offsets,
+                                      int P, int32_t* __restrict__ out) {
+  __shared__ int red;
+  const int p = blockIdx.x;
+  if (threadIdx.x == 0) red = -1;
+  __syncthreads();
+  int m = -1;
+  for (int r = row_offsets[p] + threadIdx.x; r < row_offsets[p + 1]; r += blockDim.x) m = max(m, token_idx[r]);
+  atomicMax(&red, m);
+  __syncthreads();
+  if (threadIdx.x == 0) out[p] = red;
+}
+
+struct PackWs {
+  int32_t* blockcounts;
+  int32_t* totals;
+  int32_t* compact_id;
+};
+
+static size_t pack_ws_bytes(int64_t BH, int64_t T, int* nblk_out) {
+  int64_t nblk = (T + kPackTile - 1) / kPackTile;
+  if (nblk < 1) nblk = 1;
+  if (nblk_out) *nblk_out = (int)nblk;
+  size_t a = (size_t)BH * nblk * 4;
+  a = (a + 255) & ~(size_t)255;
+  size_t b = ((size_t)BH * 4 + 255) & ~(size_t)255;
+  return a + 2 * b;
+}
+
+static PackWs carve(void* ws, int64_t BH, int nblk) {
+  PackWs w;
+  size_t a = (size_t)BH * nblk * 4;
+  a = (a + 255) & ~(size_t)255;
+  size_t b = ((size_t)BH * 4 + 255) & ~(size_t)255;
+  w.blockcounts = (int32_t*)ws;
+  w.totals = (int32_t*)((char*)ws + a);
+  w.compact_id = (int32_t*)((char*)ws + a + b);
+  return w;
+}
+
+}  // namespace pfa
+
+using namespace pfa;
+
+extern "C" int pfa_token_topk(const float* importance, int B, int64_t T, int64_t keep_count, int guard,
+                              float threshold, uint8_t* mask_out, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(importance && mask_out && B >= 0 && T >= 0, "pfa_token_topk: bad arguments");
+  if (B == 0 || T == 0) return PFA_OK;
+  token_topk_kernel<<<B, kTopkThreads, 0, as_stream(stream)>>>(importance, T, keep_count, guard < 0 ? 0 : guard,
+                                                                threshold, mask_out);
+  PFA_CHECK_LAUNCH("pfa_token_topk");
+  return PFA_OK;
+}
+
+extern "C" int pfa_pack_workspace_size(int B, int H, int64_t T, size_t* bytes) {
+  clear_error();
+  PFA_CHECK_ARG(bytes && B >= 0 && H > 0 && T >= 0, "pfa_pack_workspace_size: bad arguments");
+  *bytes = pack_ws_bytes((int64_t)B * H, T, nullptr);
+  return PFA_OK;
+}
+
+extern "C" int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* token_mask, int B, int H, int64_t T,
+                             uint8_t* mask_out, int32_t* active_heads_out, int32_t* row_offsets_out,
+                             int32_t* token_idx_out, int32_t* row_head_out, int32_t* summary_out, void* workspace,
+                             size_t ws_bytes, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(head_idx && mask_out && row_offsets_out && token_idx_out && row_head_out && summary_out && workspace,
+                "pfa_pack_rows: null pointer");
+  PFA_CHECK_ARG(B > 0 && H > 0 && T > 0 && topk >= 1 && topk <= H, "pfa_pack_rows: bad sizes");
+  PFA_CHECK_ARG((int64_t)B * H * T < (int64_t)INT32_MAX, "pfa_pack_rows: B*H*T exceeds int32 row indexing");
+  int nblk;
+  int64_t BH = (int64_t)B * H;
+  size_t need = pack_ws_bytes(BH, T, &nblk);
+  if (ws_bytes < need) {
+    set_error("pfa_pack_rows: workspace %zu < %zu", ws_bytes, need);
+    return PFA_E_WORKSPACE;
+  }
+  PackWs w = carve(workspace, BH, nblk);
+  hipStream_t s = as_stream(stream);
+  dim3 grid(nblk, (unsigned)BH);
+  pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts);
+  PFA_CHECK_LAUNCH("pfa_pack_rows/count");
+  pack_scan_kernel<<<1, 1024, 0, s>>>(w.blockcounts, (int)BH, nblk, 1, w.totals, w.compact_id, active_heads_out,
+                                      row_offsets_out, summary_out);
+  PFA_CHECK_LAUNCH("pfa_pack_rows/scan");
+  pack_fill_kernel<<<grid, kPackThreads, 0, s>>>(mask_out, T, nblk, w.blockcounts, w.compact_id, token_idx_out,
+                                                 row_head_out);
+  PFA_CHECK_LAUNCH("pfa_pack_rows/fill");
+  return PFA_OK;
+}
+
+extern "C" int pfa_pack_mask(const uint8_t* mask, int P, int64_t T, int32_t* row_offsets_out, int32_t* token_idx_out,
+                             int32_t* row_head_out, int32_t* summary_out, void* workspace, size_t ws_bytes,
+                             void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(mask && row_offsets_out && token_idx_out && row_head_out && summary_out && workspace,
+                "pfa_pack_mask: null pointer");
+  PFA_CHECK_ARG(P > 0 && T > 0, "pfa_pack_mask: bad sizes");
+  PFA_CHECK_ARG((int64_t)P * T < (int64_t)INT32_MAX, "pfa_pack_mask: P*T exceeds int32 row indexing");
+  int nblk;
+  size_t need = pack_ws_bytes(P, T, &nblk);
+  if (ws_bytes < need) {
+    set_error("pfa_pack_mask: workspace %zu < %zu", ws_bytes, need);
+    return PFA_E_WORKSPACE;
+  }
+  PackWs w = carve(workspace, P, nblk);
+  hipStream_t s = as_stream(stream);
+  dim3 grid(nblk, (unsigned)P);
+  pack_count_mask<<<grid, kPackThreads, 0, s>>>(mask, T, nblk, w.blockcounts);
+  PFA_CHECK_LAUNCH("pfa_pack_mask/count");
+  pack_scan_kernel<<<1, 1024, 0, s>>>(w.blockcounts, P, nblk, 0, w.totals, w.compact_id, nullptr, row_offsets_out,
+                                      summary_out);
+  PFA_CHECK_LAUNCH("pfa_pack_mask/scan");
+  pack_fill_kernel<<<grid, kPackThreads, 0, s>>>(mask, T, nblk, w.blockcounts, w.compact_id, token_idx_out,
+                                                 row_head_out);
+  PFA_CHECK_LAUNCH("pfa_pack_mask/fill");
+  return PFA_OK;
+}
+
+extern "C" int pfa_head_max_token(const int32_t* token_idx, const int32_t* row_offsets, int P, int32_t* out,
+                                  void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(token_idx && row_offsets && out && P >= 0, "pfa_head_max_token: bad arguments");
+  if (P == 0) return PFA_OK;
+  head_max_token_kernel<<<P, 256, 0, as_stream(stream)>>>(token_idx, row_offsets, P, out);
+  PFA_CHECK_LAUNCH("pfa_head_max_token");
+  return PFA_OK;
+}

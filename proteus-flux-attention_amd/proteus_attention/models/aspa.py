@@ -1,0 +1,1225 @@
+"""Adaptive Sparse Proto Attention (ASPA) module on the MI355X kernels.
+
+Host-side mirror of ``src/proteus_attention/models/aspa.py`` of the
+reference: the same ``ModelConfig`` attribute bag, the same constructor
+knobs, schedules and telemetry dictionaries, and the same forward semantics.
+All per-token and per-row work runs in libpfa_hip.so:
+
+=====================================  ======================================
+reference step (aspa.py)               device work here
+=====================================  ======================================
+router + proto prior (628-690)         ``pfa_router_topk`` (one pass over x)
+importance (1521-1530)                 same kernel
+head top-k + mask (1590-1606)          same kernel + ``pfa_pack_rows``
+token top-k (790-842)                  ``pfa_token_topk``
+QKV / out projections                  torch Linear (hipBLASLt GEMMs)
+RoPE (606-618)                         ``pfa_rope_qk_inplace`` (in the QKV buffer)
+packing (1704-1756)                    ``pfa_pack_rows``
+shortlist candidates (1269-1284)       ``pfa_proto_prefix_topk`` + ``pfa_shortlist_build``
+sparse attention + scatter (1287-1302,
+1802-1807, 1841-1842)                  ``pfa_sparse_attn_fwd`` writing (B,T,H,D)
+prototype EMA (692-718)                ``pfa_proto_accumulate`` + reduce
+=====================================  ======================================
+
+The attention kernel reads q/k/v straight out of the (B, T, 3, H, D) QKV
+projection and writes each active row into its (B, T, H, D) slot, so the
+reference's permute/index_select/index_copy/zeros passes disappear.
+
+Out of scope (kept for API compatibility only): the memory bank
+(aspa.py:932-1035; its candidates are clamped to the row itself by the
+builder, so it never changes outputs — updates are not performed here) and
+training-mode attention dropout.
+"""
+from __future__ import annotations
+
+import math
+import time
+import warnings
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import _hip
+from ..kernels import sparse_attn as _sa
+from ..kernels.sparse_attn import (
+    _record_backend,
+    get_last_backend,
+    get_last_backend_info,
+)
+
+
+class ModelConfig:
+    """Attribute bag with the reference defaults (aspa.py:33-72)."""
+
+    _DEFAULTS: Dict[str, Any] = {
+        "vocab_size": 0,
+        "n_ctx": 0,
+        "n_layer": 0,
+        "n_head": 1,
+        "d_model": 0,
+        "p_dropout": 0.0,
+        "bias": False,
+        "attn_variant": "standard",
+        "moe_n_experts": 0,
+        "attn_mode": "auto",
+        "attn_linear_L": 512,
+        "attn_linear_window": 512,
+        "attn_linear_anchor_stride": 256,
+        "attn_linear_head_k": 2,
+        "attn_linear_switch_ctx": 20000,
+        "attn_linear_latency_budget_ms": None,
+        "attn_linear_policy": "local+anchors",
+        "attn_use_rope": True,
+        "attn_rope_base": 10000.0,
+        "attn_router_top_p": 0.9,
+    }
+
+    def __init__(self, **kwargs: Any) -> None:
+        merged = dict(self._DEFAULTS)
+        merged.update(kwargs)
+        self.__dict__.update(merged)
+
+    def to_dict(self) -> Dict[str, Any]:
+        return dict(self.__dict__)
+
+
+class LayerNorm(nn.Module):
+    """LayerNorm with optional bias (aspa.py:75-85)."""
+
+    def __init__(self, ndim: int, bias: bool, eps: float = 1e-5) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(ndim))
+        self.bias = nn.Parameter(torch.zeros(ndim)) if bias else None
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.layer_norm(x, x.shape[-1:], self.weight, self.bias, eps=self.eps)
+
+
+class RMSNorm(nn.Module):
+    """RMS normalisation (aspa.py:88-99)."""
+
+    def __init__(self, ndim: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(ndim))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.weight * (x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + self.eps))
+
+
+def _build_norm(config: ModelConfig) -> nn.Module:
+    kind = str(getattr(config, "norm_type", "layernorm") or "layernorm").lower()
+    eps = float(getattr(config, "norm_eps", 1e-5))
+    if kind == "rmsnorm":
+        return RMSNorm(config.d_model, eps=eps)
+    return LayerNorm(config.d_model, bias=bool(getattr(config, "bias", False)), eps=eps)
+
+
+class MLP(nn.Module):
+    """Feed-forward block of AdaptiveSparseAttentionBlock (aspa.py:114-132)."""
+
+    def __init__(self, config: ModelConfig) -> None:
+        super().__init__()
+        hidden = int(getattr(config, "mlp_hidden_mult", 4)) * config.d_model
+        self.fc1 = nn.Linear(config.d_model, hidden, bias=bool(config.bias))
+        self.act = nn.GELU()
+        self.fc2 = nn.Linear(hidden, config.d_model, bias=bool(config.bias))
+        self.dropout = nn.Dropout(config.p_dropout)
+        self.last_aux_loss: Optional[torch.Tensor] = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.dropout(self.fc2(self.act(self.fc1(x))))
+
+
+class SwitchRouter(nn.Module):
+    """Router parameters (aspa.py:135-157).  Its math runs inside the fused
+    router kernel; ``forward`` is kept for API compatibility and runs the
+    same computation with torch ops on the module's device."""
+
+    def __init__(self, d_model: int, n_gates: int, noise_std: float = 0.0) -> None:
+        super().__init__()
+        self.linear = nn.Linear(d_model, n_gates, bias=False)
+        self.noise_std = float(noise_std)
+
+    def forward(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        logits = self.linear(x)
+        if self.training and self.noise_std > 0.0:
+            logits = logits + torch.randn_like(logits) * self.noise_std
+        probs = F.softmax(logits, dim=-1)
+        scores, indices = torch.max(probs, dim=-1)
+        return indices, scores, probs
+
+
+def _flag(value: Any) -> bool:
+    return bool(value)
+
+
+def _policy_tokens(raw: str) -> set:
+    text = str(raw or "local+anchors").lower().replace("|", ",").replace("+", ",")
+    toks = {p.strip() for p in text.split(",") if p.strip()}
+    return toks or {"local", "anchors"}
+
+
+class AdaptiveSparseAttention(nn.Module):
+    """ASPA layer (reference aspa.py:170-1932) on MI355X kernels."""
+
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        g = lambda name, default=None: getattr(config, name, default)  # noqa: E731
+        self.d_model = config.d_model
+        self.bias = _flag(g("bias", False))
+
+        # --- head counts and schedule (aspa.py:183-224) ---
+        h_total = int(g("attn_h_total", 0) or g("n_head", 1) or 1)
+        if h_total <= 0:
+            h_total = max(1, int(g("n_head", 1)))
+        self.h_total = h_total
+        if self.d_model % self.h_total != 0:
+            raise ValueError("d_model must be divisible by the total number of attention heads (attn_h_total)")
+        base_active = int(g("attn_h_active", 0))
+        if base_active <= 0 or base_active > h_total:
+            base_active = max(1, min(4, h_total))
+        amax = int(g("attn_h_active_max", 0) or 0)
+        amax = min(16, h_total) if amax <= 0 else amax
+        amax = max(1, min(amax, h_total))
+        amin = int(g("attn_h_active_min", 0) or 0)
+        amin = max(1, min(2, amax)) if amin <= 0 else amin
+        amin = max(1, min(amin, amax))
+        self.h_active_min, self.h_active_max = amin, amax
+        self.h_active = max(amin, min(base_active, amax))
+        curve = g("attn_active_curve", None)
+        try:
+            curve_val = float(curve) if curve is not None else 0.25
+        except (TypeError, ValueError):
+            curve_val = 0.25
+        self.h_active_curve = 1.0 if curve_val <= 0.0 else curve_val
+        self.force_dense_when_full = _flag(g("attn_force_dense_when_full", False))
+        self.d_head = self.d_model // self.h_total
+
+        # --- RoPE (aspa.py:226-247) ---
+        self.use_rope = _flag(g("attn_use_rope", True))
+        rope_base = float(g("attn_rope_base", 10000.0) or 10000.0)
+        self.rope_base = rope_base if rope_base > 0.0 else 10000.0
+        if self.use_rope and self.d_head % 2 != 0:
+            warnings.warn("Disabling RoPE because attention head dimension is not even.", RuntimeWarning)
+            self.use_rope = False
+        inv_freq = 1.0 / (self.rope_base ** (torch.arange(0, self.d_head, 2, dtype=torch.float32)
+                                             / max(self.d_head, 1)))
+        self.register_buffer("_rope_inv_freq", inv_freq, persistent=False)
+        self._rope_cache: Dict[Tuple[str, int, str], Tuple[int, torch.Tensor, torch.Tensor]] = {}
+
+        self.dropout = nn.Dropout(config.p_dropout)
+        self.use_sdpa = _flag(g("use_sdpa", True))
+        self.router_reg_lambda = float(g("attn_router_lambda", 0.0) or 0.0)
+        self.router_reg_beta = float(g("attn_router_beta", 1.0) or 1.0)
+        self.router_reg_mode = str(g("attn_router_reg_mode", "entropy"))
+        try:
+            top_p = float(g("attn_router_top_p", 0.0))
+        except (TypeError, ValueError):
+            top_p = 0.0
+        if not math.isfinite(top_p):
+            top_p = 0.0
+        self.router_top_p = max(0.0, min(top_p, 1.0))
+        mode = str(g("attn_mode", "auto") or "auto").lower()
+        self.mode_setting = mode if mode in {"auto", "subquad", "linear"} else "auto"
+
+        # --- shortlist length schedule (aspa.py:274-306) ---
+        self.linear_L = max(1, int(g("attn_linear_L", 512) or 512))
+        sched = str(g("attn_linear_L_schedule", "fixed") or "fixed").lower()
+        self.linear_L_schedule = sched if sched in {"fixed", "sqrt", "log", "mem_cap"} else "fixed"
+        self.linear_L_base = max(1, int(g("attn_linear_L_base", self.linear_L) or self.linear_L))
+        lmin_default = min(64, self.linear_L_base)
+        self.linear_L_min = max(1, int(g("attn_linear_L_min", lmin_default) or lmin_default))
+        lmax_cfg = g("attn_linear_L_max", self.linear_L)
+        self.linear_L_max = max(self.linear_L_min, int(lmax_cfg if lmax_cfg is not None else self.linear_L))
+        self.linear_L_scale_init = max(0.1, float(g("attn_linear_L_scale", 1.0) or 1.0))
+        smax_default = max(1.0, self.linear_L_scale_init)
+        self.linear_L_scale_max = float(g("attn_linear_L_scale_max", smax_default) or smax_default)
+        self._linear_scale_min = max(0.05, self.linear_L_min / max(1.0, self.linear_L_base))
+        self._linear_L_scale_runtime = self.linear_L_scale_init
+        self.linear_latency_shrink = min(max(float(g("attn_linear_latency_shrink", 0.8) or 0.8), 0.1), 0.99)
+        self.linear_latency_growth = max(1.0, float(g("attn_linear_latency_growth", 1.05) or 1.05))
+        mem_budget = g("attn_linear_mem_budget_mb", None)
+        self.linear_mem_budget_mb = float(mem_budget) if mem_budget is not None else None
+
+        # --- piece fractions (aspa.py:307-378) ---
+        f_local = max(0.0, min(1.0, float(g("attn_linear_piece_local_frac", 0.6) or 0.6)))
+        f_anchor = max(0.0, min(1.0, float(g("attn_linear_piece_anchor_frac", 0.3) or 0.3)))
+        f_proto = float(g("attn_linear_piece_proto_frac", max(0.0, 1.0 - f_local - f_anchor)))
+        f_proto = max(0.0, min(1.0, f_proto))
+        tot = f_local + f_anchor + f_proto
+        if tot <= 0.0:
+            f_local, f_anchor, f_proto, tot = 1.0, 0.0, 0.0, 1.0
+        f_local /= tot
+        f_anchor /= tot
+        f_proto = max(0.0, 1.0 - f_local - f_anchor)
+        window_hint = int(g("attn_linear_window", self.linear_L_base) or self.linear_L_base)
+        if window_hint <= 0:
+            window_hint = self.linear_L_base
+        self.linear_window_base = max(1, window_hint)
+        self.linear_window = self.linear_window_base
+        stride = int(g("attn_linear_anchor_stride", g("attn_linear_anchors_every", 256)) or 0)
+        self.linear_anchor_stride = max(0, stride)
+        self.linear_head_k = max(1, min(int(g("attn_linear_head_k", 2) or 2), self.h_total))
+        self.linear_switch_ctx = max(0, int(g("attn_linear_switch_ctx", 20000) or 20000))
+        lat = g("attn_linear_latency_budget_ms", None)
+        self.linear_latency_budget_ms = float(lat) if lat is not None else None
+        toks = _policy_tokens(g("attn_linear_policy", "local+anchors"))
+        self.linear_policy_tokens = toks
+        self.linear_use_anchors = bool(toks & {"anchors", "anchor", "global"})
+        self.linear_use_proto = bool(toks & {"proto", "prototype", "semantic", "dna"})
+        self.linear_use_local = bool(toks & {"local", "window"}) or not (self.linear_use_anchors or self.linear_use_proto)
+        f_local = f_local if self.linear_use_local else 0.0
+        f_anchor = f_anchor if self.linear_use_anchors else 0.0
+        f_proto = f_proto if self.linear_use_proto else 0.0
+        psum = f_local + f_anchor + f_proto
+        if psum <= 0.0:
+            f_local, f_anchor, f_proto = 1.0, 0.0, 0.0
+        else:
+            f_local /= psum
+            f_anchor /= psum
+            f_proto = max(0.0, 1.0 - f_local - f_anchor)
+        self.linear_piece_local_frac = f_local
+        self.linear_piece_anchor_frac = f_anchor
+        self.linear_piece_proto_frac = f_proto
+        self._linear_runtime: Optional[dict] = None
+        self._linear_runtime_seq_len: Optional[int] = None
+        self._linear_runtime_alpha: Optional[float] = None
+        self._current_alpha: float = 0.0
+        try:
+            cutoff = float(g("attn_dense_alpha_cutoff", 0.0))
+        except (TypeError, ValueError):
+            cutoff = 0.25
+        self.dense_alpha_cutoff = float(max(0.0, min(0.95, cutoff)))
+
+        # --- memory bank: accepted, not executed (see module docstring) ---
+        self.memory_enabled = _flag(g("attn_memory_enable", False))
+        slots = int(g("attn_memory_slots", 0) or 0)
+        if slots <= 0:
+            self.memory_enabled = False
+            slots = 1
+        if self.memory_enabled:
+            warnings.warn("attn_memory_enable: the memory bank is not executed by the MI355X build; "
+                          "its candidates never reach attention in the reference either.", RuntimeWarning)
+        self.memory_slots = slots
+        self.memory_decay = float(max(0.0, min(1.0, float(g("attn_memory_decay", 0.9) or 0.9))))
+        self.register_buffer("memory_keys", torch.zeros(h_total, slots, self.d_head), persistent=False)
+        self.register_buffer("memory_values", torch.zeros(h_total, slots, self.d_head), persistent=False)
+        self.register_buffer("memory_counts", torch.zeros(h_total, slots), persistent=False)
+        self.register_buffer("memory_ptr", torch.zeros(h_total, dtype=torch.long), persistent=False)
+
+        # --- per-head int8 quantisation (aspa.py:395-437) ---
+        self.quantize_sparse_int8 = _flag(g("attn_quantize_int8", False))
+        qmode = str(g("attn_quantize_int8_mode", "max") or "max").lower()
+        self.quantize_sparse_int8_mode = qmode if qmode in {"max", "percentile", "ema_percentile"} else "max"
+        self.quantize_sparse_int8_percentile = min(max(float(g("attn_quantize_int8_percentile", 1.0) or 1.0), 0.0), 1.0)
+        self.quantize_sparse_int8_ema_decay = min(max(float(g("attn_quantize_int8_ema_decay", 0.9) or 0.9), 0.0), 0.9999)
+        for name in ("_quant_ema_q", "_quant_ema_k", "_quant_ema_v"):
+            self.register_buffer(name, torch.zeros(h_total), persistent=False)
+        self._quant_ema_flags = {"_quant_ema_q": False, "_quant_ema_k": False, "_quant_ema_v": False}
+
+        # --- sequence schedule (aspa.py:438-476) ---
+        low = int(g("attn_active_seq_low", 0) or 0)
+        high = int(g("attn_active_seq_high", 0) or 0)
+        if low <= 0:
+            low = max(64, self.d_head)
+        if high <= 0:
+            high = int(g("n_ctx", 0) or (low * 4))
+        if high < low:
+            high = low
+        self.seq_low, self.seq_high = low, high
+        dense_hint = g("attn_small_seq_dense", None)
+        try:
+            dense_cut = int(dense_hint) if dense_hint is not None else max(0, low // 2)
+        except (TypeError, ValueError):
+            dense_cut = max(0, low // 2)
+        self.small_seq_dense = max(0, dense_cut)
+        self._density_ema: Optional[float] = None
+        self._last_density: Optional[float] = None
+        self._last_target_k: Optional[int] = None
+        thr_hint = g("attn_force_dense_threshold", None)
+        thr = float(thr_hint) if thr_hint is not None else None
+        self._dense_threshold: Optional[float] = thr if (thr is not None and thr > 0.0) else None
+
+        # --- router + gate->head map (aspa.py:478-489) ---
+        gates = int(g("attn_gates", 0))
+        if gates <= 0:
+            gates = max(h_total, self.h_active_max, self.h_active) * 2
+        self.attn_gates = max(gates, h_total, self.h_active_max)
+        self.head_router = SwitchRouter(self.d_model, self.attn_gates,
+                                        noise_std=float(g("attn_router_noise_std", 0.01)))
+        gate_to_head = self._default_mapping(self.attn_gates, h_total)
+        self.register_buffer("gate_to_head", gate_to_head, persistent=False)
+        self.register_buffer("gate_to_head_onehot", F.one_hot(gate_to_head, num_classes=h_total).to(torch.float32),
+                             persistent=False)
+        self._shortlist_alpha_override: Optional[float] = None
+
+        self.qkv = nn.Linear(self.d_model, 3 * self.d_model, bias=self.bias)
+        self.proj = nn.Linear(self.d_model, self.d_model, bias=self.bias)
+
+        # --- telemetry / caches (aspa.py:497-567) ---
+        self.last_head_stats: Optional[dict] = None
+        self._last_sparse_state: Optional[dict] = None
+        self._cached_active_mask: Optional[torch.Tensor] = None
+        self._cached_packing = None
+        self.last_aux_loss: Optional[torch.Tensor] = None
+        self.last_router_reg: Optional[torch.Tensor] = None
+        self._latency_ema: Optional[float] = None
+        self.track_latency = _flag(g("attn_track_latency", True))
+        self.proto_enabled = _flag(g("attn_proto_enable", False))
+        self.proto_decay = float(g("attn_proto_decay", 0.97))
+        self.proto_threshold = float(g("attn_proto_threshold", 0.25))
+        self.proto_blend = float(g("attn_proto_blend", 0.6))
+        self.proto_temp = float(max(g("attn_proto_temp", 0.2), 1e-3))
+        self.proto_usage_boost = float(max(g("attn_proto_usage_boost", 0.0), 0.0))
+        self.proto_init_scale = float(g("attn_proto_init_scale", 0.02))
+        if self.proto_enabled:
+            self.register_buffer("routing_prototypes",
+                                 torch.randn(self.attn_gates, self.d_model, dtype=torch.float32) * self.proto_init_scale)
+            self.register_buffer("routing_usage_ema", torch.zeros(self.attn_gates, dtype=torch.float32))
+            self.register_buffer("routing_confidence", torch.zeros(self.attn_gates, dtype=torch.float32))
+        else:
+            self.routing_prototypes = None  # type: ignore[assignment]
+            self.routing_usage_ema = None  # type: ignore[assignment]
+            self.routing_confidence = None  # type: ignore[assignment]
+        self._last_proto_stats: Optional[dict] = None
+        self.token_sparse = _flag(g("attn_token_sparse", False))
+        keep = min(max(float(g("attn_token_keep_ratio", 1.0) or 1.0), 0.0), 1.0)
+        self.token_keep_ratio_base = keep
+        self._token_keep_ratio_runtime: Optional[float] = None
+        ksched = str(g("attn_linear_token_keep_schedule", "sqrt") or "sqrt").lower()
+        self.linear_token_keep_schedule = ksched if ksched in {"fixed", "sqrt", "log"} else "sqrt"
+        kmin = float(g("attn_linear_token_keep_min_ratio", 0.2) or 0.2)
+        self.linear_token_keep_ratio_min = min(max(kmin, 0.0), keep)
+        self.linear_token_keep_ratio_ref = int(g("attn_linear_token_keep_ref", 2048) or 2048)
+        min_keep = max(0, int(g("attn_token_keep_min", 0) or 0))
+        guard = max(0, int(g("attn_token_keep_guard", 1) or 1))
+        self.token_keep_guard = guard
+        self.token_keep_min = max(min_keep, guard if self.token_sparse else min_keep)
+        self.token_keep_threshold = float(max(0.0, float(g("attn_token_keep_threshold", 0.0) or 0.0)))
+        self._last_token_importance: Optional[torch.Tensor] = None
+        self._last_token_mask: Optional[torch.Tensor] = None
+        self._last_token_blend: Optional[torch.Tensor] = None
+        self._last_token_similarity: Optional[torch.Tensor] = None
+        self._last_shortlist_backend_info: Optional[Dict[str, object]] = None
+        self._last_batch_size: Optional[int] = None
+        self.last_head_consensus: Optional[torch.Tensor] = None
+        self._last_gate_probs: Optional[torch.Tensor] = None
+        self._last_shortlist_lengths: Optional[torch.Tensor] = None
+
+    # ------------------------------------------------------------------
+    # RoPE tables (aspa.py:576-604)
+    # ------------------------------------------------------------------
+    @staticmethod
+    def _rope_rotate_half(x: torch.Tensor) -> torch.Tensor:
+        return torch.stack((-x[..., 1::2], x[..., ::2]), dim=-1).reshape_as(x)
+
+    def _rope_factors(self, seq_len: int, device: torch.device, dtype: torch.dtype):
+        if seq_len <= 0:
+            raise ValueError("RoPE requires a positive sequence length.")
+        key = (device.type, int(device.index) if device.index is not None else -1, str(dtype))
+        cached = self._rope_cache.get(key)
+        if cached is None or cached[0] < seq_len:
+            inv = self._rope_inv_freq.to(device=device)
+            pos = torch.arange(seq_len, device=device, dtype=inv.dtype)
+            ang = torch.outer(pos, inv)
+            cos = torch.repeat_interleave(ang.cos(), 2, dim=-1).to(dtype)
+            sin = torch.repeat_interleave(ang.sin(), 2, dim=-1).to(dtype)
+            cached = (seq_len, cos, sin)
+            self._rope_cache[key] = cached
+        return cached[1][:seq_len], cached[2][:seq_len]
+
+    @staticmethod
+    def _default_mapping(gates: int, heads: int) -> torch.Tensor:
+        heads = max(1, heads)
+        idx = torch.arange(gates, dtype=torch.long)
+        return torch.clamp((idx * heads) // max(gates, 1), 0, heads - 1)
+
+    # ------------------------------------------------------------------
+    # schedules (aspa.py:731-930, 1037-1173) -- host arithmetic
+    # ------------------------------------------------------------------
+    def _choose_active_k(self, seq_len: int) -> int:
+        if seq_len <= self.seq_low:
+            target = self.h_active_max
+        elif seq_len >= self.seq_high:
+            target = self.h_active_min
+        else:
+            ratio = float(seq_len - self.seq_low) / float(max(1, self.seq_high - self.seq_low))
+            if self.h_active_curve != 1.0:
+                ratio = max(0.0, min(1.0, ratio)) ** self.h_active_curve
+            target = int(math.floor(self.h_active_max - ratio * (self.h_active_max - self.h_active_min) + 1e-6))
+        target = max(self.h_active_min, min(target, self.h_active_max))
+        self._last_target_k = target
+        return target
+
+    def _nucleus_head_count(self, head_probs: torch.Tensor, target_p: float, max_cap: int) -> int:
+        if max_cap <= 1:
+            return max(1, max_cap)
+        probs = head_probs.detach().to(torch.float32)
+        if probs.numel() == 0:
+            return 1
+        mean = probs.mean(dim=(0, 1))
+        if mean.numel() == 0:
+            return 1
+        mean = torch.where(torch.isfinite(mean), mean, torch.zeros_like(mean)).cpu()
+        total = float(mean.sum())
+        if total <= 0.0:
+            return 1
+        cum = torch.cumsum(torch.sort(mean, descending=True).values, dim=0)
+        keep = int((cum < total * float(target_p)).sum())
+        if keep < mean.numel():
+            keep += 1
+        return min(max_cap, max(1, keep))
+
+    def _update_density(self, value: float) -> None:
+        value = float(max(0.0, value))
+        self._last_density = value
+        self._density_ema = value if self._density_ema is None else 0.8 * self._density_ema + 0.2 * value
+
+    def _density_threshold(self) -> Optional[float]:
+        return self._dense_threshold
+
+    def _set_linear_scale(self, value: float) -> None:
+        lo = self._linear_scale_min
+        hi = max(lo, self.linear_L_scale_max)
+        self._linear_L_scale_runtime = float(min(max(value, lo), hi))
+        self._linear_runtime_seq_len = None
+        self._linear_runtime_alpha = None
+
+    def adjust_linear_L_scale(self, factor: float) -> None:
+        if factor == 0.0:
+            return
+        self._set_linear_scale(self._linear_L_scale_runtime * factor)
+
+    def _linear_token_keep_ratio(self, seq_len: int) -> float:
+        if not self.token_sparse:
+            return self.token_keep_ratio_base
+        base = self.token_keep_ratio_base
+        ref = max(1, self.linear_token_keep_ratio_ref)
+        seq = max(1, int(seq_len))
+        if self.linear_token_keep_schedule == "sqrt":
+            ratio = base * math.sqrt(ref / float(seq))
+        elif self.linear_token_keep_schedule == "log":
+            ratio = base * (math.log2(ref + 1.0) / math.log2(seq + 1.0))
+        else:
+            ratio = base
+        return float(max(min(base, self.linear_token_keep_ratio_min), min(base, ratio)))
+
+    def _get_shortlist_alpha(self, seq_len: int) -> float:
+        if self._shortlist_alpha_override is not None:
+            return float(max(0.0, min(1.0, self._shortlist_alpha_override)))
+        seq_len = int(max(1, seq_len))
+        low = max(1, int(self.seq_low))
+        high = max(low + 1, int(self.linear_switch_ctx)) if self.linear_switch_ctx > 0 else max(low + 1, seq_len)
+        if seq_len <= low:
+            return 0.0
+        if seq_len >= high:
+            return 1.0
+        return float((seq_len - low) / (high - low))
+
+    def _compute_cvt_alpha(self, seq_len: int) -> float:
+        seq_len = int(max(1, seq_len))
+        setting = str(self.mode_setting or "").lower()
+        if setting == "linear":
+            alpha = 1.0
+        elif setting == "subquad":
+            alpha = 0.0
+        else:
+            alpha = self._get_shortlist_alpha(seq_len)
+        if self.linear_latency_budget_ms is not None and self._latency_ema is not None:
+            budget, lat = self.linear_latency_budget_ms, self._latency_ema
+            if lat > budget * 1.05:
+                if self._linear_L_scale_runtime > self._linear_scale_min + 1e-3:
+                    self.adjust_linear_L_scale(self.linear_latency_shrink)
+                alpha = 1.0
+            elif lat < budget * 0.80 and seq_len < max(1, self.linear_switch_ctx):
+                if self._linear_L_scale_runtime < self.linear_L_scale_max:
+                    self.adjust_linear_L_scale(self.linear_latency_growth)
+                alpha = min(alpha, 0.0)
+        if self.linear_switch_ctx > 0:
+            if self._current_alpha >= 0.95 and seq_len >= max(1, int(self.linear_switch_ctx * 0.75)):
+                alpha = max(alpha, 0.95)
+            if seq_len >= self.linear_switch_ctx:
+                alpha = 1.0
+        return float(max(0.0, min(1.0, alpha)))
+
+    def set_shortlist_alpha(self, value: float) -> None:
+        """Override the shortlist slider (0 = dense, 1 = linear)."""
+        self._shortlist_alpha_override = float(max(0.0, min(1.0, value)))
+        self._linear_runtime = None
+        self._linear_runtime_seq_len = None
+        self._linear_runtime_alpha = None
+
+    def _compute_effective_linear_params(self, seq_len: int, batch_size: Optional[int], alpha: float) -> dict:
+        seq_len = max(1, int(seq_len))
+        coeff = float(max(1.0, self.linear_L_base))
+        sched = self.linear_L_schedule
+        if sched == "sqrt":
+            base_val = coeff * math.sqrt(float(seq_len))
+        elif sched == "log":
+            base_val = coeff * math.log2(float(seq_len) + 1.0)
+        elif sched == "mem_cap" and self.linear_mem_budget_mb:
+            heads_est = max(1, int(getattr(self, "_last_target_k", self.linear_head_k)))
+            batch_est = max(1, int(batch_size) if batch_size is not None else 1)
+            denom = heads_est * batch_est * seq_len * max(1, self.d_head) * 8
+            cap = int(self.linear_mem_budget_mb * 1024 * 1024 // denom) if denom > 0 else self.linear_L_max
+            base_val = max(1, min(cap, self.linear_L_max))
+        else:
+            base_val = coeff
+        eff = max(self.linear_L_min, min(self.linear_L_max, int(math.ceil(self._linear_L_scale_runtime * max(1.0, base_val)))))
+        window = min(self.linear_window_base, eff)
+        dense_cap = int(min(seq_len, max(self.linear_L_min, self.linear_window_base + seq_len // 32)))
+        dense_cap = max(self.linear_L_min, min(self.linear_L_max, dense_cap))
+        eff = max(self.linear_L_min, min(self.linear_L_max, int(alpha * eff + (1.0 - alpha) * dense_cap)))
+        window_dense = max(1, min(seq_len, max(self.linear_window_base, seq_len // 8)))
+        window = max(1, min(eff, int(alpha * window + (1.0 - alpha) * window_dense)))
+        use = (self.linear_use_local, self.linear_use_anchors, self.linear_use_proto)
+        dense_w = (0.85 if use[0] else 0.0, 0.10 if use[1] else 0.0, 0.05 if use[2] else 0.0)
+        frac = (self.linear_piece_local_frac, self.linear_piece_anchor_frac, self.linear_piece_proto_frac)
+        target_w = tuple(f if u else 0.0 for f, u in zip(frac, use))
+        w = [(1.0 - alpha) * d + alpha * t for d, t in zip(dense_w, target_w)]
+        total = sum(w)
+        if total <= 0.0:
+            w, total = [1.0, 0.0, 0.0], 1.0
+        w_local = w[0] / total
+        w_anchor = w[1] / total
+        w_proto = max(0.0, 1.0 - w_local - w_anchor)
+        caps = [int(round(eff * w_local)) if use[0] else 0,
+                int(round(eff * w_anchor)) if use[1] else 0,
+                int(round(eff * w_proto)) if use[2] else 0]
+        total_caps = sum(caps)
+        if total_caps > eff and total_caps > 0:
+            caps = [int(max(0, math.floor(c * (eff / total_caps)))) for c in caps]
+            total_caps = sum(caps)
+        remaining = eff - total_caps
+        for i in range(3):
+            if remaining <= 0:
+                break
+            if not use[i]:
+                continue
+            caps[i] += 1
+            remaining -= 1
+        if remaining > 0:
+            caps[0 if use[0] else 1 if use[1] else 2] += remaining
+        if use[0]:
+            caps[0] = min(caps[0], window)
+            if caps[0] <= 0 and eff > 0:
+                caps[0] = min(window, max(1, eff // 4))
+        if use[1] and caps[1] < 0:
+            caps[1] = 0
+        if use[2] and caps[2] < 0:
+            caps[2] = 0
+        return {
+            "effective_L": eff,
+            "local_cap": max(0, int(caps[0])),
+            "anchor_cap": max(0, int(caps[1])),
+            "proto_cap": max(0, int(caps[2])),
+            "window": max(1, int(window)),
+            "shortlist_alpha": float(alpha),
+        }
+
+    def _prepare_linear_runtime(self, seq_len: int, batch_size: Optional[int], alpha: float) -> dict:
+        if (self._linear_runtime is not None and self._linear_runtime_seq_len == seq_len
+                and self._linear_runtime_alpha is not None and abs(self._linear_runtime_alpha - float(alpha)) < 1e-4):
+            return self._linear_runtime
+        alpha = float(max(0.0, min(1.0, alpha)))
+        p = self._compute_effective_linear_params(seq_len, batch_size, alpha)
+        self.linear_L = p["effective_L"]
+        self.linear_window = p["window"]
+        runtime = dict(p)
+        runtime["anchor_stride"] = self.linear_anchor_stride
+        self._linear_runtime = runtime
+        self._linear_runtime_seq_len = seq_len
+        self._linear_runtime_alpha = alpha
+        return runtime
+
+    # ------------------------------------------------------------------
+    # int8 per-head quantisation (aspa.py:1312-1363)
+    # ------------------------------------------------------------------
+    def _quantize_per_head_int8(self, tensor: torch.Tensor, ema_buffer: str) -> Tuple[torch.Tensor, torch.Tensor]:
+        if tensor.dim() != 3:
+            raise ValueError("Expected a rank-3 tensor for per-head quantization")
+        flat = tensor.to(torch.float32).reshape(tensor.size(0), -1)
+        absf = flat.abs()
+        mode = self.quantize_sparse_int8_mode
+        if mode == "max" or self.quantize_sparse_int8_percentile <= 0.0:
+            base = absf.amax(dim=1, keepdim=True)
+        else:
+            base = torch.quantile(absf, self.quantize_sparse_int8_percentile, dim=1, keepdim=True)
+            base = torch.where(base > 0.0, base, absf.amax(dim=1, keepdim=True))
+        if mode == "ema_percentile":
+            decay = self.quantize_sparse_int8_ema_decay
+            ema = getattr(self, ema_buffer)
+            if ema is None or ema.numel() != flat.size(0) or not self._quant_ema_flags.get(ema_buffer, False):
+                ema = absf.amax(dim=1)
+            else:
+                ema = ema.to(tensor.device, dtype=torch.float32)
+            updated = decay * ema + (1.0 - decay) * base.squeeze(1)
+            setattr(self, ema_buffer, updated.detach())
+            self._quant_ema_flags[ema_buffer] = True
+            base = updated.unsqueeze(1)
+        scales = torch.clamp(base / 127.0, min=1e-6)
+        quant = torch.clamp((flat / scales).round(), -127.0, 127.0).to(torch.int8).view_as(tensor)
+        return quant.contiguous(), scales.squeeze(1).to(torch.float32).contiguous()
+
+    # ------------------------------------------------------------------
+    # device stages
+    # ------------------------------------------------------------------
+    def _proto_inputs(self, device: torch.device):
+        """G-sized prototype tensors the router kernel consumes (aspa.py:636-663)."""
+        if not (self.proto_enabled and self.routing_prototypes is not None):
+            return None, None, None
+        pn = F.normalize(self.routing_prototypes.to(device=device, dtype=torch.float32), dim=-1, eps=1e-6).contiguous()
+        conf = None
+        if self.routing_confidence is not None:
+            conf = (self.routing_confidence.view(-1) + 1e-6).to(torch.float32).contiguous()
+        usage = None
+        if self.proto_usage_boost > 0.0 and self.routing_usage_ema is not None:
+            usage = torch.softmax(-(self.routing_usage_ema + 1e-6), dim=0).to(torch.float32).contiguous()
+        return pn, conf, usage
+
+    def _route_device(self, x2d: torch.Tensor, topk: int, need_head_scores: bool = True):
+        """Fused router: gate probs, sim, blend, importance, head top-k."""
+        lib = _hip.lib()
+        device = x2d.device
+        n_tok, C = x2d.shape
+        G, H = self.attn_gates, self.h_total
+        w = self.head_router.linear.weight
+        if w.dtype != x2d.dtype:
+            w = w.to(x2d.dtype)
+        w = w.contiguous()
+        pn, conf, usage = self._proto_inputs(device)
+        gate = torch.empty(n_tok, G, dtype=torch.float32, device=device)
+        imp = torch.empty(n_tok, dtype=torch.float32, device=device)
+        sim = torch.empty(n_tok, dtype=torch.float32, device=device) if pn is not None else None
+        blend = torch.empty(n_tok, dtype=torch.float32, device=device) if pn is not None else None
+        hidx = torch.empty(n_tok, topk, dtype=torch.int32, device=device)
+        hsc = torch.empty(n_tok, topk, dtype=torch.float32, device=device) if need_head_scores else None
+        g2h = self.gate_to_head.to(device=device, dtype=torch.int32).contiguous()
+        with _hip.TIMER.timed("router_topk"):
+            rc = lib.pfa_router_topk(
+            _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(w), _hip.ptr(pn), _hip.ptr(conf),
+            _hip.ptr(usage), _hip.ptr(g2h), H, topk, float(self.proto_temp), float(self.proto_threshold),
+            float(self.proto_blend), float(self.proto_usage_boost), _hip.ptr(gate), _hip.ptr(sim), _hip.ptr(blend),
+            _hip.ptr(imp), _hip.ptr(hidx), _hip.ptr(hsc), _hip.stream_ptr(device))
+        _hip.check(rc, "pfa_router_topk")
+        return gate, sim, blend, imp, hidx, hsc
+
+    def _select_active_tokens(self, importance: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        """Token keep mask (aspa.py:790-842) via pfa_token_topk."""
+        if not self.token_sparse or importance is None or importance.dim() != 2:
+            return None
+        B, T = importance.shape
+        if T == 0:
+            return None
+        ratio = float(self._token_keep_ratio_runtime if self._token_keep_ratio_runtime is not None
+                      else self.token_keep_ratio_base)
+        device = importance.device
+        if ratio >= 0.999 and self.token_keep_threshold <= 0.0:
+            mask = torch.ones(B, T, dtype=torch.bool, device=device)
+            self._last_token_mask = mask
+            return mask
+        guard = min(max(0, self.token_keep_guard), T)
+        min_keep = max(min(max(0, self.token_keep_min), T), guard)
+        keep = int(torch.tensor(ratio * T, dtype=torch.float32).round().item())
+        if min_keep > 0:
+            keep = max(keep, min_keep)
+        keep = max(1, min(keep, T))
+        _hip.require_device(importance, what="_select_active_tokens")
+        imp = importance.to(torch.float32).contiguous()
+        mask8 = torch.empty(B, T, dtype=torch.uint8, device=device)
+        rc = _hip.lib().pfa_token_topk(_hip.ptr(imp), B, T, keep, guard, float(self.token_keep_threshold),
+                                       _hip.ptr(mask8), _hip.stream_ptr(device))
+        _hip.check(rc, "pfa_token_topk")
+        mask = mask8.view(torch.bool)
+        self._last_token_mask = mask
+        return mask
+
+    def _update_routing_prototypes(self, token_feats: torch.Tensor, gate_probs: torch.Tensor) -> None:
+        """Prototype / usage / confidence EMA (aspa.py:692-718)."""
+        if not (self.proto_enabled and self.routing_prototypes is not None
+                and self.routing_usage_ema is not None and self.routing_confidence is not None):
+            return
+        with torch.no_grad():
+            lib = _hip.lib()
+            x2d = token_feats.detach().reshape(-1, self.d_model)
+            if x2d.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                x2d = x2d.to(torch.float32)
+            x2d = x2d.contiguous()
+            probs = gate_probs.detach().to(torch.float32).reshape(-1, self.attn_gates).contiguous()
+            device = x2d.device
+            n_tok, C, G = x2d.size(0), self.d_model, self.attn_gates
+            nparts = _hip.ctypes.c_int(0)
+            _hip.check(lib.pfa_proto_partial_count(n_tok, _hip.ctypes.byref(nparts)), "pfa_proto_partial_count")
+            partial = torch.empty(nparts.value, G, C + 1, dtype=torch.float32, device=device)
+            _hip.check(lib.pfa_proto_accumulate(_hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G,
+                                                _hip.ptr(probs), _hip.ptr(partial), nparts.value,
+                                                _hip.stream_ptr(device)), "pfa_proto_accumulate")
+            sums = torch.empty(G, C + 1, dtype=torch.float32, device=device)
+            _hip.check(lib.pfa_proto_partial_reduce(_hip.ptr(partial), nparts.value, G, C, _hip.ptr(sums),
+                                                    _hip.stream_ptr(device)), "pfa_proto_partial_reduce")
+            weighted, counts = sums[:, :C], sums[:, C]
+            mask = counts > 1e-6
+            maskf = mask.to(torch.float32).unsqueeze(-1)
+            mean = torch.where(mask.unsqueeze(-1), weighted / counts.clamp_min(1e-30).unsqueeze(-1),
+                               torch.zeros_like(weighted))
+            decay = self.proto_decay
+            proto = self.routing_prototypes
+            new_proto = proto * decay + mean.to(proto.dtype) * (1.0 - decay)
+            proto.copy_(torch.where(mask.unsqueeze(-1), new_proto, proto))
+            usage = self.routing_usage_ema
+            usage.mul_(decay)
+            usage.add_(torch.where(mask, counts * (1.0 - decay), torch.zeros_like(counts)).to(usage.dtype))
+            conf = self.routing_confidence
+            conf.mul_(decay)
+            conf.add_((maskf.squeeze(-1) * (1.0 - decay)).to(conf.dtype))
+            self._proto_update_mask = mask
+            del maskf
+
+    # ------------------------------------------------------------------
+    def _full_rows(self, B: int, T: int, device: torch.device):
+        """All (b, h, t) rows active: packed layout for the dense branches."""
+        BH = B * self.h_total
+        token_idx = torch.arange(T, device=device, dtype=torch.int32).repeat(BH)
+        row_head = torch.arange(BH, device=device, dtype=torch.int32).repeat_interleave(T)
+        return token_idx, row_head
+
+    def _attend_dense_causal(self, qkv: torch.Tensor, B: int, T: int, out: torch.Tensor) -> None:
+        """Every head and token, keys 0..t (force-dense / dense fast path).
+        Equivalent to the reference's (T,T) triu(-inf) mask without
+        materialising it (aspa.py:1664-1677, 1365-1396)."""
+        H, D = self.h_total, self.d_head
+        token_idx, row_head = self._full_rows(B, T, qkv.device)
+        q5 = qkv.view(B, T, 3, H, D)
+        out4 = out.view(B, T, H, D)
+        _sa._attn_launch(_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
+                         _hip.tensor4(q5[:, :, 2], H, "bthd"), qkv.dtype, _hip.tensor4(out4, H, "bthd"), out.dtype,
+                         H, T, D, token_idx, row_head, None, None, None, None, None, 1.0 / math.sqrt(D),
+                         (None, None, None), qkv.device)
+
+    def _project_qkv(self, x: torch.Tensor) -> torch.Tensor:
+        B, T, C = x.shape
+        qkv = self.qkv(x).contiguous()  # (B, T, 3C) = (B, T, 3, H, D)
+        if self.use_rope:
+            cos, sin = self._rope_factors(T, x.device, qkv.dtype)
+            cos, sin = cos.contiguous(), sin.contiguous()
+            with _hip.TIMER.timed("rope_qk"):
+                rc = _hip.lib().pfa_rope_qk_inplace(_hip.ptr(qkv), _hip.dtype_tag(qkv.dtype), B, T, self.h_total,
+                                                 self.d_head, _hip.ptr(cos), _hip.ptr(sin),
+                                                 _hip.stream_ptr(x.device))
+            _hip.check(rc, "pfa_rope_qk_inplace")
+        return qkv
+
+    def _forward_dense_fastpath(self, x: torch.Tensor) -> torch.Tensor:
+        """Dense causal attention for short sequences (aspa.py:1365-1440)."""
+        B, T, C = x.shape
+        qkv = self._project_qkv(x)
+        attn = torch.empty(B, T, C, dtype=qkv.dtype, device=x.device)
+        self._attend_dense_causal(qkv, B, T, attn)
+        y = self.dropout(self.proj(attn))
+        self._last_target_k = self.h_total
+        self._last_sparse_state = {
+            "mode": "dense_fastpath", "backend": "hip_dense", "max_rows": T, "density": 1.0,
+            "target_k": self.h_total,
+            "force_dense_threshold": None if self._dense_threshold is None else float(self._dense_threshold),
+            "cutoff": int(self.small_seq_dense), "quantized": False, "token_keep_fraction": 1.0,
+        }
+        self._update_density(1.0)
+        self.last_head_stats = {
+            "top_k": int(self.h_total), "mean_gate_prob": 1.0, "router_entropy": 0.0,
+            "mean_active_per_token": float(self.h_total), "unique_heads": int(self.h_total),
+            "active_fraction": 1.0, "max_active_rows": int(T), "max_active_density": 1.0,
+            "target_k": int(self.h_total), "seq_len": int(T), "active_min": int(self.h_active_min),
+            "active_max": int(self.h_active_max),
+            "force_dense_threshold": None if self._dense_threshold is None else float(self._dense_threshold),
+            "active_curve": float(self.h_active_curve), "token_keep_fraction": 1.0,
+            "router_top_p": float(self.router_top_p), "nucleus_k": int(self.h_total), "top_a_consensus": True,
+        }
+        self.last_router_reg = None
+        return y
+
+    # ------------------------------------------------------------------
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        B, T, C = x.shape
+        device = x.device
+        _hip.require_device(x, what="AdaptiveSparseAttention.forward")
+        if self.training and float(self.dropout.p) > 0.0:
+            raise NotImplementedError("training-mode attention dropout is not provided by the HIP forward path")
+        self.last_aux_loss = None
+        self._last_token_importance = None
+        self._last_token_mask = None
+        self._last_token_blend = None
+        if not self.proto_enabled:
+            self._last_token_similarity = None
+        ev0 = ev1 = None
+        if self.track_latency:
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
+        self._last_batch_size = B
+
+        def finish(label: str) -> None:
+            if self.track_latency and ev0 is not None:
+                ev1.record()
+                ev1.synchronize()
+                ms = float(ev0.elapsed_time(ev1))
+                self._latency_ema = ms if self._latency_ema is None else 0.8 * self._latency_ema + 0.2 * ms
+                if self.last_head_stats is not None:
+                    self.last_head_stats["latency_ms"] = ms
+                if self._last_sparse_state is not None:
+                    self._last_sparse_state["latency_ms"] = ms
+            if self.last_head_stats is not None:
+                self.last_head_stats["mode_setting"] = self.mode_setting
+                self.last_head_stats["mode_selected"] = label
+            if self._last_sparse_state is not None:
+                self._last_sparse_state["mode_selected"] = label
+
+        if self.small_seq_dense and T <= self.small_seq_dense:
+            y = self._forward_dense_fastpath(x)
+            finish("dense_fastpath")
+            return y
+
+        alpha = self._compute_cvt_alpha(T)
+        self._current_alpha = alpha
+        if self.token_sparse:
+            blend_ratio = (1.0 - alpha) * float(self.token_keep_ratio_base) + alpha * float(self._linear_token_keep_ratio(T))
+            self._token_keep_ratio_runtime = float(max(0.0, min(1.0, blend_ratio)))
+        else:
+            self._token_keep_ratio_runtime = None
+
+        # head count (aspa.py:1574-1589); nucleus count needs head probs, so
+        # the router is run with topk chosen after it when top_p > 0.
+        dense_topk = self._choose_active_k(T)
+        x2d = x.reshape(B * T, C)
+        if not x2d.is_contiguous():
+            x2d = x2d.contiguous()
+        if x2d.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise ValueError(f"unsupported input dtype {x.dtype}")
+        adaptive_topk = dense_topk
+        # One router pass ranks dense_topk heads per token (best first); the
+        # nucleus / alpha blend below can only shrink k, and the first k of a
+        # ranked list are the top-k under the same total order.
+        gate, sim, blend, imp, hidx_all, hsc_all = self._route_device(x2d, dense_topk)
+        if self.router_top_p > 0.0:
+            head_probs = gate.view(B, T, -1) @ self.gate_to_head_onehot.to(device=device, dtype=gate.dtype)
+            nucleus_k = self._nucleus_head_count(head_probs, self.router_top_p, dense_topk)
+            adaptive_topk = max(self.h_active_min, min(dense_topk, nucleus_k))
+        linear_topk = max(1, min(adaptive_topk, self.linear_head_k))
+        topk = max(1, int(round((1.0 - alpha) * float(adaptive_topk) + alpha * float(linear_topk))))
+        topk = min(adaptive_topk, topk)
+        self._last_target_k = topk
+        if topk == dense_topk:
+            hidx, hsc = hidx_all, hsc_all
+        else:
+            hidx = hidx_all[:, :topk].contiguous()
+            hsc = hsc_all[:, :topk].contiguous()
+        gate_probs = gate.view(B, T, self.attn_gates)
+        self._last_gate_probs = gate_probs
+        if sim is not None:
+            self._last_token_similarity = sim.view(B, T)
+            self._last_token_blend = blend.view(B, T)
+        else:
+            self._last_token_similarity = None
+            self._last_token_blend = None
+        self._last_proto_stats = None
+        importance = imp.view(B, T)
+        self._last_token_importance = importance
+        token_mask = self._select_active_tokens(importance)
+        self._last_token_mask = token_mask
+
+        router_reg = self._router_regulariser(gate_probs)
+
+        # pack rows on the device (mask, active heads, row offsets)
+        lib = _hip.lib()
+        H = self.h_total
+        BH = B * H
+        mask8 = torch.empty(BH, T, dtype=torch.uint8, device=device)
+        active_heads = torch.empty(BH, dtype=torch.int32, device=device)
+        row_offsets = torch.empty(BH + 1, dtype=torch.int32, device=device)
+        token_idx = torch.empty(BH * T, dtype=torch.int32, device=device)
+        row_head = torch.empty(BH * T, dtype=torch.int32, device=device)
+        summary = torch.empty(4, dtype=torch.int32, device=device)
+        ws = _sa._workspace(_sa._size_out(lib.pfa_pack_workspace_size, B, H, T), device)
+        tm8 = token_mask.view(torch.uint8) if token_mask is not None else None
+        with _hip.TIMER.timed("pack_rows"):
+            rc = lib.pfa_pack_rows(_hip.ptr(hidx), topk, _hip.ptr(tm8), B, H, T, _hip.ptr(mask8), _hip.ptr(active_heads),
+                               _hip.ptr(row_offsets), _hip.ptr(token_idx), _hip.ptr(row_head), _hip.ptr(summary),
+                               _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device))
+        _hip.check(rc, "pfa_pack_rows")
+        summ = summary.cpu()
+        P, N, max_rows = int(summ[0]), int(summ[1]), int(summ[2])
+        density_est = float(max_rows) / float(max(1, T))
+        self._update_density(density_est)
+        density_threshold = self._density_threshold()
+        all_rows_active = N == BH * T
+        prefer_dense = alpha <= self.dense_alpha_cutoff and not self.quantize_sparse_int8
+        force_dense, dense_reason = False, None
+        if prefer_dense:
+            force_dense, dense_reason = True, "alpha"
+        if density_threshold is not None and density_est >= density_threshold:
+            force_dense = True
+            dense_reason = dense_reason or "density"
+        elif all_rows_active and self.force_dense_when_full:
+            force_dense = True
+            dense_reason = dense_reason or "full"
+        if alpha >= 0.95:
+            if dense_reason == "alpha":
+                dense_reason = None
+            force_dense = False
+
+        qkv = self._project_qkv(x)
+        attn = torch.zeros(B, T, C, dtype=qkv.dtype, device=device)
+        D = self.d_head
+        mode_label = "sparse"
+        if force_dense:
+            self._cached_active_mask = None
+            self._cached_packing = None
+            self._attend_dense_causal(qkv, B, T, attn)
+            if dense_reason == "alpha":
+                mode_label = "dense_alpha"
+            elif P == BH:
+                mode_label = "dense"
+            else:
+                mode_label = "dense_auto"
+            _record_backend("hip_dense", device=str(device), heads=BH, tokens=T, max_rows=T, quantized=False)
+            self._last_sparse_state = {
+                "mode": mode_label, "backend": get_last_backend(), "max_rows": max_rows, "density": density_est,
+                "target_k": int(topk),
+                "force_dense_threshold": None if density_threshold is None else float(density_threshold),
+                "quantized": False, "token_keep_fraction": None, "mode_setting": self.mode_setting,
+                "mode_selected": f"cvt(alpha={alpha:.2f})", "shortlist_alpha": float(alpha),
+                "dense_reason": dense_reason,
+            }
+        elif P == 0 or N == 0:
+            dense_reason = None
+            self._cached_active_mask = None
+            self._cached_packing = None
+            self._last_sparse_state = {
+                "mode": "dense", "backend": "not_invoked", "max_rows": max_rows, "density": density_est,
+                "target_k": int(topk),
+                "force_dense_threshold": None if density_threshold is None else float(density_threshold),
+                "quantized": False, "token_keep_fraction": None, "mode_setting": self.mode_setting,
+                "mode_selected": f"cvt(alpha={alpha:.2f})", "shortlist_alpha": float(alpha),
+                "dense_reason": dense_reason,
+            }
+        else:
+            dense_reason = None
+            mode_label = "shortlist"
+            tok = token_idx[:N]
+            rh = row_head[:N]
+            heads = active_heads[:P]
+            self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets[:P + 1], alpha)
+            backend_info = self._last_shortlist_backend_info or get_last_backend_info()
+            state = {
+                "mode": mode_label, "backend": str(backend_info.get("name", "shortlist")),
+                "active_head_indices": heads.to(torch.int64), "head_idx": rh, "token_idx": tok,
+                "row_offsets": row_offsets[:P + 1], "max_rows": int(max_rows), "density": density_est,
+                "target_k": int(topk),
+                "force_dense_threshold": None if density_threshold is None else float(density_threshold),
+                "cache_hit": False, "quantized": bool(self.quantize_sparse_int8 and not self.training),
+                "token_keep_fraction": None, "mode_setting": self.mode_setting,
+                "mode_selected": f"cvt(alpha={alpha:.2f})", "shortlist_alpha": float(alpha),
+                "linear_L": int(self.linear_L), "linear_window": int(self.linear_window),
+                "linear_anchor_stride": int(self.linear_anchor_stride),
+            }
+            state["linear_shortlist_backend"] = backend_info.get("name")
+            det = backend_info.get("details")
+            if isinstance(det, dict):
+                for key, val in det.items():
+                    state[f"linear_shortlist_{key}"] = val
+            self._last_sparse_state = state
+        if force_dense and token_mask is not None:
+            attn.view(B, T, H, D).mul_(token_mask.view(B, T, 1, 1).to(attn.dtype))
+        self.last_head_consensus = None if self.training else attn.detach()
+        y = self.dropout(self.proj(attn))
+
+        self._finish_stats(gate_probs, hsc, hidx, token_mask, topk, adaptive_topk, max_rows, density_est,
+                           density_threshold, alpha, mode_label, dense_reason, N, B, T)
+        self.last_router_reg = router_reg
+        self._update_routing_prototypes(x, gate_probs)
+        finish(f"cvt(alpha={alpha:.2f})::{mode_label}")
+        if self.linear_mem_budget_mb and device.type == "cuda":
+            allocated = torch.cuda.memory_allocated(device) / (1024 * 1024)
+            if allocated > self.linear_mem_budget_mb * 1.1:
+                self.adjust_linear_L_scale(self.linear_latency_shrink)
+            elif allocated < self.linear_mem_budget_mb * 0.6:
+                self.adjust_linear_L_scale(self.linear_latency_growth)
+        return y
+
+    def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha) -> None:
+        """Candidate build + candidate attention (aspa.py:1175-1310)."""
+        H, D = self.h_total, self.d_head
+        device = qkv.device
+        runtime = self._prepare_linear_runtime(T, B, alpha)
+        L = int(runtime["effective_L"])
+        local_w, slots, proto_cap_val = _sa._resolve_caps(
+            L, runtime["window"], runtime["anchor_stride"], self.linear_use_local, self.linear_use_anchors,
+            self.linear_use_proto and self._last_token_similarity is not None, T, runtime["local_cap"],
+            runtime["anchor_cap"], runtime["proto_cap"])
+        sets = None
+        row_batch = None
+        if self.linear_use_proto and self._last_token_similarity is not None and proto_cap_val > 0:
+            K = min(L, proto_cap_val, T)
+            if K > 0:
+                sets = _sa._proto_prefix_sets(self._last_token_similarity, K)
+                row_batch = (heads.index_select(0, row_head) // H).to(torch.int32) if B > 1 else None
+        cand, lens = _sa._shortlist_build_device(token_idx, row_batch, T, L, local_w, runtime["anchor_stride"], slots,
+                                                 sets)
+        self._last_shortlist_lengths = lens
+        use_quant = bool(self.quantize_sparse_int8 and not self.training)
+        q5 = qkv.view(B, T, 3, H, D)
+        out4 = _hip.tensor4(attn.view(B, T, H, D), H, "bthd")
+        if use_quant:
+            # Per-head int8 of the active heads (aspa.py:1258-1267): the
+            # compact (P, T, D) tensors are quantised, attended, and the
+            # (P, T, D) result is scattered into the (B, T, H, D) output.
+            P = heads.numel()
+            hsel = heads.to(torch.int64)
+            comp = [q5[:, :, i].permute(0, 2, 1, 3).reshape(B * H, T, D).index_select(0, hsel) for i in range(3)]
+            qi, qs = self._quantize_per_head_int8(comp[0], "_quant_ema_q")
+            ki, ks = self._quantize_per_head_int8(comp[1], "_quant_ema_k")
+            vi, vs = self._quantize_per_head_int8(comp[2], "_quant_ema_v")
+            outc = torch.zeros(P, T, D, dtype=qkv.dtype, device=device)
+            _sa._attn_launch(_hip.tensor4(qi, P), _hip.tensor4(ki, P), _hip.tensor4(vi, P), torch.int8,
+                             _hip.tensor4(outc, P), qkv.dtype, P, T, D, token_idx, row_head, None, cand, lens, None,
+                             None, 1.0 / math.sqrt(D), (qs, ks, vs), device)
+            full = torch.zeros(B * H, T, D, dtype=qkv.dtype, device=device)
+            full.index_copy_(0, hsel, outc)
+            attn.copy_(full.view(B, H, T, D).permute(0, 2, 1, 3).reshape(B, T, H * D))
+        else:
+            _sa._attn_launch(_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
+                             _hip.tensor4(q5[:, :, 2], H, "bthd"), qkv.dtype, out4, qkv.dtype, H, T, D, token_idx,
+                             row_head, heads, cand, lens, None, None, 1.0 / math.sqrt(D), (None, None, None), device)
+        _record_backend("hip", device=str(device), heads=int(heads.numel()), tokens=T,
+                        rows=int(token_idx.numel()), L=L, quantized=use_quant, candidates=True)
+        self._last_shortlist_backend_info = get_last_backend_info()
+
+    def _router_regulariser(self, gate_probs: torch.Tensor) -> Optional[torch.Tensor]:
+        """Router regularisation terms (aspa.py:1543-1573, 1608-1614)."""
+        if self.router_reg_lambda <= 0.0:
+            return None
+        parts = {p.strip() for p in str(self.router_reg_mode or "").lower().replace("|", ",").replace("+", ",").split(",")
+                 if p.strip()} or {"entropy"}
+        terms = []
+        if parts & {"entropy", "ent"}:
+            terms.append((gate_probs.clamp_min(1e-9).log() * gate_probs).sum(dim=-1).mean())
+        if parts & {"l1", "l_1"}:
+            terms.append((gate_probs.sum(dim=-1) ** self.router_reg_beta).mean())
+        if not terms:
+            return None
+        total = terms[0]
+        for t in terms[1:]:
+            total = total + t
+        return self.router_reg_lambda * total
+
+    def _finish_stats(self, gate_probs, head_scores, head_idx, token_mask, topk, adaptive_topk, max_rows, density_est,
+                      density_threshold, alpha, mode_label, dense_reason, N, B, T) -> None:
+        """Telemetry dictionaries (aspa.py:1857-1916) with one host readback."""
+        H = self.h_total
+        with torch.no_grad():
+            gp = gate_probs.float()
+            entropy = -(gp.clamp_min(1e-9).log() * gp).sum(dim=-1).mean()
+            # numerator over every token's top-k scores, denominator over
+            # the active (token-masked) entries, as aspa.py:1860-1866
+            keep_frac = (token_mask.to(torch.float32).mean() if token_mask is not None
+                         else torch.ones((), device=gp.device))
+            score_sum = head_scores.sum() if head_scores is not None else torch.zeros((), device=gp.device)
+            sel = torch.zeros(H, device=gp.device, dtype=torch.float32)
+            sel.index_add_(0, head_idx.view(-1).to(torch.int64),
+                           (token_mask.view(-1, 1).expand(-1, topk).reshape(-1).to(torch.float32)
+                            if token_mask is not None else torch.ones(head_idx.numel(), device=gp.device)))
+            extras = [entropy, keep_frac, score_sum, (sel > 0).sum().to(torch.float32)]
+            if self._last_token_similarity is not None:
+                extras += [self._last_token_similarity.mean(), self._last_token_blend.mean(),
+                           (self._last_token_blend > 0).sum().to(torch.float32)]
+            vals = torch.stack([e.to(torch.float32) for e in extras]).cpu().tolist()
+        entropy_v, keep_v, score_v, uniq_v = vals[0], vals[1], vals[2], vals[3]
+        denom = max(1.0, float(N))
+        if self._last_sparse_state is not None:
+            self._last_sparse_state["token_keep_fraction"] = float(keep_v)
+        self.last_head_stats = {
+            "top_k": int(topk),
+            "mean_gate_prob": float(score_v / denom),
+            "router_entropy": float(entropy_v),
+            "mean_active_per_token": float(N) / float(max(1, B * T)),
+            "unique_heads": int(uniq_v),
+            "active_fraction": float(N) / float(max(1, B * T * H)),
+            "max_active_rows": int(max_rows),
+            "max_active_density": float(density_est),
+            "target_k": int(self._last_target_k or topk),
+            "seq_len": int(T),
+            "active_min": int(self.h_active_min),
+            "active_max": int(self.h_active_max),
+            "force_dense_threshold": None if density_threshold is None else float(density_threshold),
+            "active_curve": float(self.h_active_curve),
+            "token_keep_fraction": float(keep_v),
+            "mode": mode_label,
+            "mode_selected": f"cvt(alpha={alpha:.2f})",
+            "shortlist_alpha": float(alpha),
+            "router_top_p": float(self.router_top_p),
+            "nucleus_k": int(adaptive_topk),
+            "top_a_consensus": True,
+        }
+        if dense_reason is not None:
+            self.last_head_stats["dense_reason"] = dense_reason
+        if alpha > 0.0:
+            self.last_head_stats["linear_L"] = int(self.linear_L)
+            self.last_head_stats["linear_window"] = int(self.linear_window)
+            self.last_head_stats["linear_anchor_stride"] = int(self.linear_anchor_stride)
+            info = self._last_shortlist_backend_info or get_last_backend_info()
+            if info.get("name") is not None:
+                self.last_head_stats["linear_shortlist_backend"] = info.get("name")
+                det = info.get("details")
+                if isinstance(det, dict):
+                    for key, val in det.items():
+                        self.last_head_stats[f"linear_shortlist_{key}"] = val
+        if len(vals) > 4:
+            self._last_proto_stats = {"max_sim_mean": float(vals[4]), "blend_mean": float(vals[5]),
+                                      "active_tokens": int(vals[6])}
+            self.last_head_stats["proto"] = dict(self._last_proto_stats)
+            self.last_head_stats["dna"] = dict(self._last_proto_stats)
+
+
+class AdaptiveSparseProtoAttention(AdaptiveSparseAttention):
+    """AdaptiveSparseAttention with prototype routing enabled (aspa.py:1935-1944)."""
+
+    def __init__(self, config: ModelConfig):
+        if not getattr(config, "attn_proto_enable", False):
+            try:
+                setattr(config, "attn_proto_enable", True)
+            except Exception:  # noqa: BLE001
+                pass
+        super().__init__(config)
+
+
+class AdaptiveSparseAttentionBlock(nn.Module):
+    """Pre-norm block around ASPA (aspa.py:1947-1990)."""
+
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        self.ln1 = _build_norm(config)
+        if bool(getattr(config, "attn_proto_enable", False)):
+            self.attn = AdaptiveSparseProtoAttention(config)
+        else:
+            self.attn = AdaptiveSparseAttention(config)
+        self.ln2 = _build_norm(config)
+        self.mlp = MLP(config)
+        self._is_moe = False
+        self.last_aux_loss = None
+        self.last_moe_stats = None
+        self.last_router_reg = None
+        self.last_head_stats = None
+        self.last_sparse_state = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = x + self.attn(self.ln1(x))
+        x = x + self.mlp(self.ln2(x))
+        self.last_aux_loss = getattr(self.mlp, "last_aux_loss", None)
+        self.last_router_reg = getattr(self.attn, "last_router_reg", None)
+        self.last_moe_stats = None
+        self.last_head_stats = getattr(self.attn, "last_head_stats", None)
+        self.last_sparse_state = getattr(self.attn, "_last_sparse_state", None)
+        return x

@@ -1,0 +1,444 @@
+"""Chunked Shortlist pipeline (reference tools/chunked_shortlist.py:88-827).
+
+Two passes over a long sequence: every chunk runs an ASPA forward on the
+device, promotes its most salient tokens, the promoted tokens of all chunks
+are merged into a global shortlist (sorted by position), and a final ASPA
+pass runs over the reduced sequence.
+
+Same configuration, result and metric types as the reference.  Host staging
+(pinned RAM or a disk memmap) follows the reference; chunk copies go through
+a reused device buffer.  Chunk salience is the router importance of the chunk
+model (device tensors); the reference's norm-score fallback only applies when
+no importance is available.
+"""
+from __future__ import annotations
+
+import contextlib
+import logging
+import math
+import os
+import tempfile
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Any, Dict, Iterable, List, Literal, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from ..kernels.sparse_attn import get_last_backend_info
+from ..models.aspa import AdaptiveSparseAttention, ModelConfig
+from . import chunk_select
+
+LOGGER = logging.getLogger(__name__)
+
+# The reference caps chunks at 65,536 tokens because of a Triton/ROCm compiler
+# limit (reference chunked_shortlist.py:51-53).  The HIP kernels have no such
+# limit; the constant and its validation are kept for configuration parity.
+MAX_SHORTLIST_CHUNK_TOKENS = 65_536
+BYTES_PER_MB = 1024.0 * 1024.0
+
+
+def _system_available_ram() -> Optional[int]:
+    try:
+        import psutil  # type: ignore
+
+        return int(psutil.virtual_memory().available)
+    except Exception:  # noqa: BLE001
+        pass
+    try:
+        return int(os.sysconf("SC_PAGE_SIZE") * os.sysconf("SC_AVPHYS_PAGES"))
+    except (AttributeError, ValueError, TypeError, OSError):
+        return None
+
+
+def _sanitize_mapping(mapping: Dict[str, Any]) -> Dict[str, Any]:
+    out: Dict[str, Any] = {}
+    for key, value in mapping.items():
+        if isinstance(value, torch.Tensor):
+            out[key] = value.detach().cpu().item() if value.numel() == 1 else value.detach().cpu().tolist()
+        elif isinstance(value, dict):
+            out[key] = _sanitize_mapping(value)
+        else:
+            out[key] = value
+    return out
+
+
+def _build_model_config(seq_len: int, d_model: int, *, heads: int, sparse_ratio: float, shortlist_alpha: float,
+                        router_top_p: float) -> ModelConfig:
+    """Chunk / final model recipe (reference chunked_shortlist.py:88-137)."""
+
+    return ModelConfig(
+        vocab_size=0, n_ctx=seq_len, n_layer=1, n_head=heads, d_model=d_model, p_dropout=0.0, bias=False,
+        attn_variant="aspa", attn_h_total=heads, attn_h_active=heads, attn_h_active_min=heads,
+        attn_h_active_max=heads, attn_active_seq_low=max(128, seq_len // 4), attn_active_seq_high=seq_len,
+        attn_mode="linear", attn_token_sparse=True, attn_token_keep_ratio=max(0.0, min(1.0, sparse_ratio)),
+        attn_token_keep_min=max(4, int(seq_len * sparse_ratio * 0.5)), attn_token_keep_guard=4,
+        attn_token_keep_threshold=0.0, attn_linear_L=256, attn_linear_L_base=256, attn_linear_L_min=64,
+        attn_linear_L_max=256, attn_linear_switch_ctx=max(512, min(seq_len, 4096)),
+        attn_linear_policy="local+anchors", attn_proto_enable=True, attn_proto_threshold=0.2, attn_proto_blend=0.5,
+        attn_proto_temp=0.3, attn_linear_token_keep_schedule="sqrt", attn_linear_token_keep_min_ratio=0.05,
+        attn_track_latency=False, attn_small_seq_dense=0, use_sdpa=False, attn_shortlist_alpha=shortlist_alpha,
+        attn_router_top_p=router_top_p,
+    )
+
+
+def _select_top_tokens(model: AdaptiveSparseAttention, global_offset: int, *, per_chunk_budget: int,
+                       nucleus_top_p: float) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+    """Chunk salience (reference chunked_shortlist.py:140-172): the chunk
+    model's importance, non-kept tokens at -inf, nucleus-selected."""
+
+    importance = getattr(model, "_last_token_importance", None)
+    if importance is None or importance.device.type != "cuda":
+        return None
+    scores = importance.squeeze(0).to(torch.float32)
+    mask = getattr(model, "_last_token_mask", None)
+    sel = chunk_select.nucleus_select(scores, per_chunk_budget, nucleus_top_p,
+                                      keep_mask=mask.squeeze(0) if mask is not None else None)
+    if sel is None:
+        return None
+    values, indices = sel
+    finite = torch.isfinite(values)
+    if not bool(finite.any()):
+        return None
+    return values[finite], indices[finite] + int(global_offset)
+
+
+def _nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float):
+    """Reference chunked_shortlist.py:175-208 (device kernel)."""
+
+    if scores.ndim != 1:
+        raise ValueError("scores tensor must be 1-D for nucleus selection.")
+    return chunk_select.nucleus_select(scores, max_tokens, top_p)
+
+
+def _finalise_indices(scores: torch.Tensor, indices: torch.Tensor, *, max_tokens: int):
+    """Reference chunked_shortlist.py:211-254 (device kernel)."""
+
+    if scores.numel() == 0 or indices.numel() == 0:
+        raise RuntimeError("No candidate tokens captured during chunking.")
+    keep_idx, keep_scores = chunk_select.finalise(scores, indices, max_tokens)
+    return keep_idx.to("cpu"), keep_scores.to("cpu")
+
+
+def _chunk_iter(total_len: int, chunk_len: int) -> Iterable[Tuple[int, int]]:
+    for start in range(0, total_len, chunk_len):
+        yield start, min(total_len, start + chunk_len)
+
+
+@dataclass
+class ChunkSummary:
+    index: int
+    start: int
+    end: int
+    promoted: Sequence[int] = field(default_factory=list)
+    scores: Sequence[float] = field(default_factory=list)
+
+
+@dataclass
+class ChunkedShortlistMetrics:
+    original_tokens: int
+    retained_tokens: int
+    retention_ratio: float
+    chunk_count: int
+    device: str
+    chunk_time_ms: Optional[float] = None
+    final_time_ms: Optional[float] = None
+    total_time_ms: Optional[float] = None
+    peak_memory_mb: Optional[float] = None
+    used_fallback: bool = False
+    chunk_tokens_per_s: Optional[float] = None
+    final_tokens_per_s: Optional[float] = None
+    total_tokens_per_s: Optional[float] = None
+    storage_mode: str = "cpu"
+    host_required_mb: Optional[float] = None
+    host_allocated_mb: Optional[float] = None
+    host_limit_mb: Optional[float] = None
+    storage_reason: Optional[str] = None
+
+
+@dataclass
+class ChunkedShortlistResult:
+    keep_indices: torch.Tensor
+    keep_scores: torch.Tensor
+    reduced_sequence: torch.Tensor
+    metrics: ChunkedShortlistMetrics
+    chunks: Sequence[ChunkSummary]
+    final_output: Optional[torch.Tensor] = None
+    final_stats: Optional[Dict[str, Any]] = None
+    backend_info: Optional[Dict[str, Any]] = None
+
+
+@dataclass
+class ChunkedShortlistConfig:
+    seq_len: int
+    d_model: int
+    chunk_len: int
+    buffer_tokens: int
+    per_chunk_budget: int
+    device: torch.device
+    heads: int = 8
+    nucleus_top_p: float = 0.9
+    chunk_sparse_ratio: float = 0.05
+    final_sparse_ratio: float = 0.5
+    seed: Optional[int] = 7
+    report_latency: bool = False
+    progress: bool = False
+    run_final_pass: bool = True
+    shortlist_alpha: float = 1.0
+    storage: Literal["cpu", "disk", "auto"] = "auto"
+    temp_dir: Optional[Path] = None
+    ram_limit_bytes: Optional[int] = None
+
+    def validate(self) -> None:
+        """Reference chunked_shortlist.py:337-366."""
+        if self.seq_len <= 0:
+            raise ValueError("seq_len must be positive.")
+        if self.d_model <= 0:
+            raise ValueError("d_model must be positive.")
+        if self.chunk_len <= 0:
+            raise ValueError("chunk_len must be positive.")
+        if self.chunk_len > MAX_SHORTLIST_CHUNK_TOKENS:
+            raise ValueError(f"chunk_len={self.chunk_len} exceeds MAX_SHORTLIST_CHUNK_TOKENS="
+                             f"{MAX_SHORTLIST_CHUNK_TOKENS}.")
+        if self.buffer_tokens <= 0:
+            raise ValueError("buffer_tokens must be positive.")
+        if self.per_chunk_budget <= 0:
+            raise ValueError("per_chunk_budget must be positive.")
+        if not (0.0 < float(self.nucleus_top_p) <= 1.0):
+            raise ValueError("nucleus_top_p must be within (0, 1].")
+        if self.chunk_sparse_ratio <= 0.0:
+            raise ValueError("chunk_sparse_ratio must be positive.")
+        if self.final_sparse_ratio <= 0.0:
+            raise ValueError("final_sparse_ratio must be positive.")
+        if not (0.0 <= self.shortlist_alpha <= 1.0):
+            raise ValueError("shortlist_alpha must be within [0, 1].")
+        if self.storage not in {"cpu", "disk", "auto"}:
+            raise ValueError("storage must be 'cpu', 'disk', or 'auto'.")
+        if self.ram_limit_bytes is not None and self.ram_limit_bytes <= 0:
+            raise ValueError("ram_limit_bytes must be positive when provided.")
+
+
+class ChunkedShortlistRunner:
+    """Runs the two-pass pipeline (reference chunked_shortlist.py:369-827)."""
+
+    def __init__(self, config: ChunkedShortlistConfig, *, logger: Optional[logging.Logger] = None) -> None:
+        self.config = config
+        self.config.validate()
+        self.logger = logger or LOGGER
+
+    def _stage(self, sequence: Optional[torch.Tensor]):
+        """Host staging (reference chunked_shortlist.py:417-560)."""
+        cfg = self.config
+        if sequence is not None:
+            if sequence.dim() != 3:
+                raise ValueError("sequence tensor must have shape (B, T, D)")
+            if sequence.size(1) < cfg.seq_len:
+                raise ValueError(f"sequence length {sequence.size(1)} smaller than configured seq_len {cfg.seq_len}")
+            if sequence.size(2) != cfg.d_model:
+                raise ValueError(f"sequence hidden size {sequence.size(2)} does not match d_model={cfg.d_model}")
+            if sequence.size(0) != 1:
+                raise ValueError("Chunked Shortlist runner currently expects batch size of 1.")
+            source = sequence[:, :cfg.seq_len].detach()
+            base_dtype = source.dtype
+        else:
+            source = None
+            base_dtype = torch.get_default_dtype()
+        elem = torch.tensor([], dtype=base_dtype).element_size()
+        required = int(cfg.seq_len * cfg.d_model * elem)
+        available = _system_available_ram()
+        limit = cfg.ram_limit_bytes if cfg.ram_limit_bytes is not None else available
+        mode, reason = cfg.storage, None
+        if mode == "auto":
+            if limit is not None and required > limit:
+                mode, reason = "disk", f"required={required:,}B exceeds limit={limit:,}B; staging on disk"
+            else:
+                mode = "cpu"
+                if limit is not None:
+                    reason = f"limit={limit:,}B, required={required:,}B"
+        elif mode == "cpu":
+            if cfg.ram_limit_bytes is not None and required > cfg.ram_limit_bytes:
+                mode, reason = "disk", (f"required={required:,}B exceeds ram_limit={cfg.ram_limit_bytes:,}B; "
+                                        "staging on disk")
+        else:
+            mode = "disk"
+        st = {"mode": mode, "reason": reason, "required": required, "limit": limit, "dtype": base_dtype,
+              "memmap": None, "path": None, "pinned": False}
+        on_gpu = cfg.device.type == "cuda"
+        if mode == "cpu":
+            if source is not None:
+                base = source.to("cpu", dtype=base_dtype)
+            else:
+                gen = torch.Generator(device="cpu")
+                if cfg.seed is not None:
+                    gen.manual_seed(int(cfg.seed))
+                base = torch.randn(1, cfg.seq_len, cfg.d_model, generator=gen).to(base_dtype)
+            st["allocated"] = int(base.numel() * base.element_size())
+            if on_gpu:
+                base = base.pin_memory()
+                st["pinned"] = True
+            st["fetch"] = lambda s, e: base[:, s:e]
+            st["gather"] = lambda idx: base[:, idx]
+            st["dataset"] = required
+        else:
+            tmp_dir = Path(cfg.temp_dir) if cfg.temp_dir is not None else Path(tempfile.gettempdir())
+            tmp_dir.mkdir(parents=True, exist_ok=True)
+            handle = tempfile.NamedTemporaryFile(dir=tmp_dir, prefix="chunked_shortlist_", suffix=".mmap",
+                                                 delete=False)
+            handle.close()
+            path = Path(handle.name)
+            mm = np.memmap(path, dtype=np.float32, mode="w+", shape=(cfg.seq_len, cfg.d_model))
+            rows = max(1, min(cfg.chunk_len, int((64 * 1024 * 1024) / max(cfg.d_model * 4, 1))))
+            gen = torch.Generator(device="cpu")
+            if cfg.seed is not None:
+                gen.manual_seed(int(cfg.seed))
+            for s in range(0, cfg.seq_len, rows):
+                e = min(cfg.seq_len, s + rows)
+                if source is not None:
+                    mm[s:e] = source[:, s:e].to("cpu", dtype=torch.float32).squeeze(0).numpy()
+                else:
+                    mm[s:e] = torch.randn(e - s, cfg.d_model, generator=gen).to(torch.float32).numpy()
+            mm.flush()
+            st.update(memmap=mm, path=path, allocated=int(rows * cfg.d_model * 4),
+                      dataset=int(cfg.seq_len * cfg.d_model * 4))
+            st["fetch"] = lambda s, e: torch.from_numpy(np.asarray(mm[s:e])).to(base_dtype).unsqueeze(0)
+            st["gather"] = lambda idx: torch.from_numpy(np.asarray(mm[idx.cpu().numpy()])).to(base_dtype).unsqueeze(0)
+        return st
+
+    def run(self, sequence: Optional[torch.Tensor] = None) -> ChunkedShortlistResult:
+        cfg = self.config
+        device = cfg.device
+        st = self._stage(sequence)
+        base_dtype = st["dtype"]
+        self.logger.info("Host staging: %s (%s)", st["mode"], st["reason"])
+        try:
+            chunk_model = AdaptiveSparseAttention(_build_model_config(
+                cfg.chunk_len, cfg.d_model, heads=cfg.heads, sparse_ratio=cfg.chunk_sparse_ratio,
+                shortlist_alpha=cfg.shortlist_alpha, router_top_p=cfg.nucleus_top_p)).to(device=device,
+                                                                                         dtype=base_dtype).eval()
+            chunk_model.use_sdpa = False
+            chunk_model.set_shortlist_alpha(float(cfg.shortlist_alpha))
+            chunk_buf = torch.empty(1, cfg.chunk_len, cfg.d_model, device=device, dtype=base_dtype)
+            with torch.inference_mode():
+                chunk_model(torch.randn(1, cfg.chunk_len, cfg.d_model, device=device, dtype=base_dtype))
+            if device.type == "cuda":
+                torch.cuda.synchronize()
+            scores_all: List[torch.Tensor] = []
+            idx_all: List[torch.Tensor] = []
+            summaries: List[ChunkSummary] = []
+            used_fallback = False
+            ev_c0 = ev_c1 = None
+            if cfg.report_latency and device.type == "cuda":
+                ev_c0, ev_c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                ev_c0.record()
+            t_start = time.perf_counter()
+            t_chunks = t_start
+            for ci, (s, e) in enumerate(_chunk_iter(cfg.seq_len, cfg.chunk_len)):
+                n = e - s
+                chunk_buf[:, :n].copy_(st["fetch"](s, e), non_blocking=st["pinned"])
+                if n < cfg.chunk_len:
+                    chunk_buf[:, n:].zero_()
+                with torch.inference_mode():
+                    chunk_model(chunk_buf[:, :n])
+                promoted = _select_top_tokens(chunk_model, s, per_chunk_budget=cfg.per_chunk_budget,
+                                              nucleus_top_p=cfg.nucleus_top_p)
+                if promoted is None:
+                    sel = _nucleus_select(chunk_buf[0, :n].detach().norm(dim=-1).to(torch.float32),
+                                          cfg.per_chunk_budget, cfg.nucleus_top_p)
+                    if sel is None:
+                        continue
+                    vals, rel = sel
+                    sc, ix = vals, rel.to(torch.long) + s
+                    used_fallback = True
+                else:
+                    sc, ix = promoted
+                scores_all.append(sc)
+                idx_all.append(ix)
+                summaries.append(ChunkSummary(index=ci, start=s, end=e, promoted=ix.tolist(),
+                                              scores=[float(v) for v in sc.tolist()]))
+                t_chunks = time.perf_counter()
+            if not scores_all:
+                raise RuntimeError("Chunked pipeline selected zero tokens; adjust per_chunk_budget or sparse ratios.")
+            if ev_c1 is not None:
+                ev_c1.record()
+            keep_idx, keep_scores = _finalise_indices(torch.cat(scores_all), torch.cat(idx_all),
+                                                      max_tokens=cfg.buffer_tokens)
+            reduced = st["gather"](keep_idx.to(torch.long)).to(device, non_blocking=st["pinned"])
+            chunk_ms = None
+            if ev_c0 is not None:
+                torch.cuda.synchronize()
+                chunk_ms = float(ev_c0.elapsed_time(ev_c1))
+            if chunk_ms is None:
+                chunk_ms = float((t_chunks - t_start) * 1000.0)
+            chunk_tps = float(cfg.seq_len * 1000.0 / chunk_ms) if chunk_ms > 0 else None
+            final_out = final_stats = backend_info = None
+            final_ms = peak_mb = final_tps = None
+            t_final_end = t_chunks
+            if cfg.run_final_pass:
+                t_f0 = time.perf_counter()
+                final_model = AdaptiveSparseAttention(_build_model_config(
+                    reduced.size(1), cfg.d_model, heads=cfg.heads, sparse_ratio=cfg.final_sparse_ratio,
+                    shortlist_alpha=cfg.shortlist_alpha, router_top_p=cfg.nucleus_top_p)).to(
+                        device=device, dtype=base_dtype).eval()
+                final_model.use_sdpa = False
+                final_model.set_shortlist_alpha(float(cfg.shortlist_alpha))
+                ev_f0 = ev_f1 = None
+                if device.type == "cuda":
+                    torch.cuda.reset_peak_memory_stats(device)
+                    if cfg.report_latency:
+                        ev_f0, ev_f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        ev_f0.record()
+                with torch.inference_mode():
+                    final_out = final_model(reduced).detach()
+                t_final_end = time.perf_counter()
+                backend_info = get_last_backend_info()
+                raw = getattr(final_model, "last_head_stats", {}) or {}
+                state = getattr(final_model, "_last_sparse_state", {}) or {}
+                final_stats = _sanitize_mapping(raw) if isinstance(raw, dict) else {}
+                if isinstance(state, dict) and state:
+                    final_stats = dict(final_stats or {})
+                    final_stats["sparse_state"] = _sanitize_mapping(state)
+                if ev_f1 is not None:
+                    ev_f1.record()
+                if device.type == "cuda":
+                    torch.cuda.synchronize()
+                    peak_mb = torch.cuda.max_memory_allocated(device) / BYTES_PER_MB
+                    if ev_f0 is not None:
+                        final_ms = float(ev_f0.elapsed_time(ev_f1))
+                if final_ms is None:
+                    final_ms = float((t_final_end - t_f0) * 1000.0)
+                if final_ms and final_ms > 0:
+                    final_tps = float(keep_idx.numel() * 1000.0 / final_ms)
+            total = t_final_end - t_start
+            metrics = ChunkedShortlistMetrics(
+                original_tokens=cfg.seq_len, retained_tokens=int(keep_idx.numel()),
+                retention_ratio=float(keep_idx.numel() / max(cfg.seq_len, 1)), chunk_count=len(summaries),
+                device=str(device), chunk_time_ms=chunk_ms, final_time_ms=final_ms, total_time_ms=float(total * 1e3),
+                peak_memory_mb=peak_mb, used_fallback=used_fallback, chunk_tokens_per_s=chunk_tps,
+                final_tokens_per_s=final_tps, total_tokens_per_s=float(cfg.seq_len / total) if total > 0 else None,
+                storage_mode=st["mode"], host_required_mb=st["dataset"] / BYTES_PER_MB,
+                host_allocated_mb=st["allocated"] / BYTES_PER_MB if st.get("allocated") is not None else None,
+                host_limit_mb=st["limit"] / BYTES_PER_MB if st["limit"] is not None else None,
+                storage_reason=st["reason"])
+            self.logger.info("Chunked Shortlist retained %s/%s tokens (%.3f) across %s chunks",
+                             metrics.retained_tokens, metrics.original_tokens, metrics.retention_ratio,
+                             metrics.chunk_count)
+            return ChunkedShortlistResult(keep_indices=keep_idx, keep_scores=keep_scores, reduced_sequence=reduced,
+                                          metrics=metrics, chunks=summaries, final_output=final_out,
+                                          final_stats=final_stats, backend_info=backend_info)
+        finally:
+            if st.get("memmap") is not None:
+                st["memmap"].flush()
+            if st.get("path") is not None:
+                with contextlib.suppress(OSError):
+                    os.remove(st["path"])
+
+
+__all__ = [
+    "ChunkedShortlistConfig",
+    "ChunkedShortlistMetrics",
+    "ChunkedShortlistResult",
+    "ChunkedShortlistRunner",
+    "ChunkSummary",
+    "MAX_SHORTLIST_CHUNK_TOKENS",
+]

@@ -1,0 +1,494 @@
+"""GPU parity: every kernel of libpfa_hip.so against the CPU oracle and the
+reference's golden vectors, through the product's Python API / C ABI.
+
+Tolerances: index/selection outputs bit-exact (ties -> lowest index, which
+the oracle implements; golden comparisons exclude positions whose reference
+value is tied at the selection boundary); attention outputs 1e-4 max-abs in
+f32 and 2e-2 max-abs in bf16."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import aspa_oracle as O
+from oracle import c_oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 2e-2
+
+
+def _say(msg: str) -> None:
+    print(f"[gpu-parity] {msg}", flush=True)
+
+
+# ---------------------------------------------------------------------------
+# shortlist builder
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tag", ["l", "la", "lp", "ap"])
+def test_builder_small_golden(dev, golden, tag):
+    from proteus_attention.kernels.sparse_attn import build_shortlist_candidates
+
+    z = golden(f"builder_small_{tag}")
+    ul, ua, up = (bool(v) for v in z["use"])
+    c, l = build_shortlist_candidates(torch.from_numpy(z["rows"]).to(dev), 64, max_candidates=16, linear_window=12,
+                                      anchor_stride=4, use_local=ul, use_anchors=ua,
+                                      proto_scores=torch.from_numpy(z["scores"]).to(dev) if up else None)
+    assert c.dtype == torch.int64 and l.dtype == torch.int64
+    assert np.array_equal(c.cpu().numpy(), z["cand"])
+    assert np.array_equal(l.cpu().numpy(), z["lengths"])
+
+
+def test_builder_packed_golden(dev, golden):
+    from proteus_attention.kernels.sparse_attn import build_packed_shortlist_candidates
+
+    z = golden("builder_packed_T4096")
+    L, w, s, lc, ac, pc = (int(v) for v in z["kw"])
+    c, l = build_packed_shortlist_candidates(
+        torch.from_numpy(z["rows"]).to(dev), torch.from_numpy(z["row_batch"]).to(dev), 4096, max_candidates=L,
+        linear_window=w, anchor_stride=s, use_local=True, use_anchors=True,
+        proto_scores=torch.from_numpy(z["sims"]).to(dev), local_cap=lc, anchor_cap=ac, proto_cap=pc)
+    assert np.array_equal(c.cpu().numpy(), z["cand"])
+    assert np.array_equal(l.cpu().numpy(), z["lengths"])
+
+
+def test_builder_truncate_golden(dev, golden):
+    from proteus_attention.kernels.sparse_attn import build_shortlist_candidates
+
+    z = golden("builder_truncate")
+    L, w, s, lc, ac, pc = (int(v) for v in z["kw"])
+    c, l = build_shortlist_candidates(torch.from_numpy(z["rows"]).to(dev), 2048, max_candidates=L, linear_window=w,
+                                      anchor_stride=s, use_local=True, use_anchors=True,
+                                      proto_scores=torch.from_numpy(z["sims"]).to(dev), local_cap=lc, anchor_cap=ac,
+                                      proto_cap=pc)
+    assert np.array_equal(c.cpu().numpy(), z["cand"])
+    assert np.array_equal(l.cpu().numpy(), z["lengths"])
+
+
+@pytest.mark.parametrize("T,L,w,s,ac,pc", [(700, 64, 20, 9, 30, 25), (300, 300, 300, 0, 0, 300), (1, 4, 2, 1, 2, 2),
+                                           (1000, 200, 1, 3, 180, 150)])
+def test_builder_ties_and_edges_vs_oracle(dev, T, L, w, s, ac, pc):
+    from proteus_attention.kernels.sparse_attn import build_shortlist_candidates
+
+    g = torch.Generator().manual_seed(T + L)
+    rows = torch.randint(0, T, (min(400, 4 * T),), generator=g)
+    rows[0] = 0
+    rows[-1] = T - 1
+    sc = torch.randint(0, 5, (T,), generator=g).float()  # heavy ties
+    kw = dict(max_candidates=L, linear_window=w, anchor_stride=s, use_local=True, use_anchors=s > 0,
+              local_cap=w, anchor_cap=ac, proto_cap=pc)
+    c, l = build_shortlist_candidates(rows.to(dev), T, proto_scores=sc.to(dev), **kw)
+    oc, ol = O.build_shortlist(rows, T, proto_scores=sc, **kw)
+    assert torch.equal(c.cpu(), oc)
+    assert torch.equal(l.cpu(), ol)
+
+
+def test_builder_extra_candidates_vs_oracle(dev):
+    from proteus_attention.kernels.sparse_attn import build_packed_shortlist_candidates
+
+    g = torch.Generator().manual_seed(77)
+    T = 500
+    rows = torch.sort(torch.randint(0, T, (120,), generator=g)).values
+    extra = torch.randint(-5, T + 50, (120, 12), generator=g)
+    elen = torch.randint(0, 13, (120,), generator=g)
+    kw = dict(max_candidates=40, linear_window=8, anchor_stride=16, use_local=True, use_anchors=True,
+              anchor_cap=10)
+    c, l = build_packed_shortlist_candidates(rows.to(dev), None, T, extra_candidates=extra.to(dev),
+                                             extra_lengths=elen.to(dev), **kw)
+    oc, ol = O.build_shortlist(rows, T, extra_candidates=extra, extra_lengths=elen, **kw)
+    assert torch.equal(c.cpu(), oc)
+    assert torch.equal(l.cpu(), ol)
+
+
+@pytest.mark.parametrize("T,L,K,A", [(65536, 2048, 205, 614)])
+def test_builder_config3_full_size_vs_c_oracle(dev, T, L, K, A):
+    """Config 3 builder (N = 2*T rows, L = 2048) bit-exact against the C
+    oracle on every row, plus size-independent properties."""
+    from proteus_attention.kernels import sparse_attn as sa
+
+    _say(f"builder cfg3 T={T} L={L}")
+    g = torch.Generator().manual_seed(3)
+    sims = torch.rand(1, T, generator=g)
+    heads = torch.stack([torch.randperm(8, generator=g)[:2] for _ in range(1)])
+    rows = torch.cat([torch.arange(T), torch.arange(T)]).to(torch.int32)
+    sets = sa._proto_prefix_sets(sims.to(dev), K)
+    cand, lens = sa._shortlist_build_device(rows.to(dev), None, T, L, 512, 256, A, sets)
+    cand, lens = cand.cpu().numpy(), lens.cpu().numpy()
+    sub = np.arange(0, 2 * T, 7)
+    oc, ol = c_oracle.shortlist_build(rows.numpy()[sub], None, T, L, 512, 256, A, sims.numpy(), K)
+    assert np.array_equal(cand[sub], oc)
+    assert np.array_equal(lens[sub], ol)
+    # properties on all rows: strictly increasing prefix, tail == row, window present
+    r = rows.numpy()
+    ln = lens.astype(np.int64)
+    assert np.all(ln >= 1) and np.all(ln <= L)
+    idx = np.arange(L)[None, :]
+    valid = idx < ln[:, None]
+    diffs = np.diff(cand.astype(np.int64), axis=1)
+    assert np.all(diffs[valid[:, 1:]] > 0)
+    assert np.all(cand[~valid] == np.broadcast_to(r[:, None], cand.shape)[~valid])
+    assert np.all(cand[np.arange(2 * T), ln - 1] == r)
+    del heads
+
+
+def test_proto_prefix_sets_vs_brute_force(dev):
+    from proteus_attention.kernels import sparse_attn as sa
+
+    g = torch.Generator().manual_seed(8)
+    for T, K in ((300, 7), (130, 64), (200, 200), (65, 1)):
+        s = torch.randint(0, 9, (2, T), generator=g).float()
+        sets = sa._proto_prefix_sets(s.to(dev), K).cpu()
+        for b in range(2):
+            exp = O.proto_prefix_sets(s[b], K)
+            assert torch.equal(sets[b].long(), exp), (T, K, b)
+
+
+# ---------------------------------------------------------------------------
+# router, token top-k, packing, RoPE
+# ---------------------------------------------------------------------------
+
+def _weights(B, T, C, H, outlier=0.0):
+    from configs import make_inputs
+
+    x, g = make_inputs(B, T, C, seed=0, outlier_frac=outlier)
+    ws = []
+    for shape in ((H, C), (H, C), (3 * C, C), (C, C)):
+        tmp = torch.empty(shape)
+        torch.nn.init.xavier_normal_(tmp, generator=g)
+        ws.append(tmp)
+    return x, ws
+
+
+def _run_router(dev, x, w, protos, conf, dt, topk, H, temp=0.2, thr=0.25, blend=0.6):
+    from proteus_attention import _hip
+
+    lib = _hip.lib()
+    n, C = x.reshape(-1, x.size(-1)).shape
+    G = w.size(0)
+    xd = x.reshape(n, C).to(dev, dt).contiguous()
+    wd = w.to(dev, dt).contiguous()
+    pn = torch.nn.functional.normalize(protos.to(torch.float32), dim=-1, eps=1e-6).to(dev).contiguous()
+    cw = (conf + 1e-6).to(torch.float32).to(dev)
+    outs = [torch.empty(n, G, device=dev), torch.empty(n, device=dev), torch.empty(n, device=dev),
+            torch.empty(n, device=dev), torch.empty(n, topk, device=dev, dtype=torch.int32),
+            torch.empty(n, topk, device=dev)]
+    g2h = O.default_gate_map(G, H).to(torch.int32).to(dev)
+    rc = lib.pfa_router_topk(_hip.ptr(xd), _hip.dtype_tag(dt), n, C, G, _hip.ptr(wd), _hip.ptr(pn), _hip.ptr(cw),
+                             None, _hip.ptr(g2h), H, topk, temp, thr, blend, 0.0, *[_hip.ptr(o) for o in outs],
+                             _hip.stream_ptr(dev))
+    _hip.check(rc, "router")
+    return [o.cpu() for o in outs]
+
+
+@pytest.mark.parametrize("name,B,T,C,dt,outlier", [
+    ("module_cfg1", 1, 1024, 256, torch.float32, 0.0),
+    ("module_cfg2_T2048", 2, 2048, 512, torch.bfloat16, 0.0),
+    ("module_short_T4096_bf16", 1, 4096, 512, torch.bfloat16, 0.01),
+])
+def test_router_vs_golden_and_oracle(dev, golden, name, B, T, C, dt, outlier):
+    z = golden(name)
+    x, ws = _weights(B, T, C, 8, outlier)
+    conf = torch.zeros(8, dtype=dt)
+    gate, sim, bl, imp, hidx, hsc = _run_router(dev, x.to(dt), ws[0].to(dt), ws[1].to(dt).float(), conf, dt, 2, 8)
+    og, osim, obl, oimp = O.route_tokens(x.to(dt), ws[0].to(dt), ws[1].to(dt), conf, None, proto_temp=0.2,
+                                         proto_threshold=0.25, proto_blend=0.6, usage_boost=0.0)
+    n = B * T
+    ref_g = torch.from_numpy(z["gate_probs"]).reshape(n, -1)
+    # gate probabilities: f32 to accumulation-order rounding; bf16 logits may
+    # land on the other side of a bf16 rounding boundary for a few tokens
+    if dt == torch.float32:
+        assert torch.allclose(gate, ref_g, atol=2e-6, rtol=0)
+        assert torch.allclose(imp, torch.from_numpy(z["importance"]).reshape(n), atol=2e-6, rtol=0)
+    else:
+        bad = (gate - ref_g).abs().amax(1) > 1e-6
+        assert int(bad.sum()) <= max(4, n // 500), int(bad.sum())
+    assert torch.allclose(sim, torch.from_numpy(z["sim"]).reshape(n), atol=2e-6, rtol=0)
+    # head top-k: exactly the oracle's lowest-index rule applied to our probs
+    _, oidx = O.topk_lowest(gate, 2)
+    assert torch.equal(hidx.long(), oidx)
+    # and the reference's choice wherever its probs are untied at the boundary
+    srt = torch.sort(ref_g, 1, descending=True).values
+    untied = (srt[:, 1] != srt[:, 2]) & (srt[:, 0] != srt[:, 1])
+    _, ridx = O.topk_lowest(ref_g, 2)
+    same = torch.sort(hidx.long(), 1).values == torch.sort(ridx, 1).values
+    agree = same.all(1) | ~untied
+    assert int((~agree).sum()) <= (0 if dt == torch.float32 else max(4, n // 500))
+
+
+def test_token_topk_vs_oracle(dev):
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    g = torch.Generator().manual_seed(12)
+    imp = torch.randint(0, 40, (3, 5000), generator=g).float() / 40.0  # many ties
+    m = AdaptiveSparseAttention(ModelConfig(d_model=64, n_head=4, attn_h_total=4, attn_token_sparse=True,
+                                            attn_token_keep_ratio=0.25, attn_token_keep_guard=3,
+                                            attn_token_keep_threshold=0.9))
+    m._token_keep_ratio_runtime = 0.25
+    mask = m._select_active_tokens(imp.to(dev)).cpu()
+    exp = O.select_active_tokens(imp, 0.25, m.token_keep_min, 3, 0.9)
+    assert torch.equal(mask, exp)
+
+
+def test_token_topk_golden(dev, golden):
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    z = golden("module_cfg2_T2048")
+    imp = torch.from_numpy(z["importance"])
+    m = AdaptiveSparseAttention(ModelConfig(d_model=64, n_head=4, attn_h_total=4, attn_token_sparse=True,
+                                            attn_token_keep_ratio=0.25))
+    m._token_keep_ratio_runtime = 0.25
+    mask = m._select_active_tokens(imp.to(dev)).cpu()
+    ref = torch.from_numpy(z["token_mask"]).bool()
+    assert torch.equal(mask.sum(1), ref.sum(1))
+    need = int(torch.tensor(0.25 * imp.size(1), dtype=torch.float32).round())
+    for b in range(imp.size(0)):
+        diff = mask[b] != ref[b]
+        if diff.any():  # only tokens tied at the cut value may differ
+            cut = torch.sort(imp[b], descending=True).values[need - 1]
+            assert bool((imp[b][diff] == cut).all())
+
+
+def test_pack_vs_oracle(dev):
+    from proteus_attention.kernels.sparse_attn import _pack_active_rows
+
+    g = torch.Generator().manual_seed(13)
+    for P, T, p in ((5, 3000, 0.3), (16, 700, 0.05), (3, 1, 1.0), (7, 2049, 0.0)):
+        m = torch.rand(P, T, generator=g) < p
+        got = _pack_active_rows(m.to(dev))
+        exp = O.pack_active_rows(m)
+        if exp is None:
+            assert got is None
+            continue
+        assert torch.equal(got[0].cpu(), exp[0]) and torch.equal(got[1].cpu(), exp[1])
+        assert torch.equal(got[2].cpu(), exp[2]) and got[3] == exp[3]
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_rope_kernel_bitwise(dev, dt):
+    from proteus_attention import _hip
+
+    g = torch.Generator().manual_seed(14)
+    B, T, H, D = 2, 37, 4, 16
+    qkv = torch.randn(B, T, 3 * H * D, generator=g).to(dt)
+    cos, sin = O.rope_tables(T, D, 10000.0, dt)
+    d = qkv.to(dev).contiguous()
+    rc = _hip.lib().pfa_rope_qk_inplace(_hip.ptr(d), _hip.dtype_tag(dt), B, T, H, D, _hip.ptr(cos.to(dev)),
+                                         _hip.ptr(sin.to(dev)), _hip.stream_ptr(dev))
+    _hip.check(rc, "rope")
+    got = d.cpu().view(B, T, 3, H, D)
+    ref = qkv.view(B, T, 3, H, D)
+    assert torch.equal(got[:, :, 0], O.apply_rope(ref[:, :, 0], cos, sin))
+    assert torch.equal(got[:, :, 1], O.apply_rope(ref[:, :, 1], cos, sin))
+    assert torch.equal(got[:, :, 2], ref[:, :, 2])
+
+
+# ---------------------------------------------------------------------------
+# attention operator
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tag", ["f32", "bf16"])
+def test_attention_vs_golden(dev, golden, tag):
+    from proteus_attention.kernels.sparse_attn import aspa_sparse_attention, get_last_backend
+
+    z = golden(f"attn_{tag}")
+    dt = torch.float32 if tag == "f32" else torch.bfloat16
+    tol = TOL_F32 if tag == "f32" else TOL_BF16
+    q, k, v = (torch.from_numpy(z[n]).to(dt).to(dev) for n in ("q", "k", "v"))
+    mask = torch.from_numpy(z["mask"]).bool().to(dev)
+    T = q.size(1)
+    causal = torch.triu(torch.full((T, T), float("-inf")), diagonal=1).to(dev)
+    out = aspa_sparse_attention(q, k, v, active_mask=mask.unsqueeze(-1))
+    assert get_last_backend() == "hip" and out.dtype == dt
+    assert (out.float().cpu() - torch.from_numpy(z["out_nocand"])).abs().max() <= tol
+    out = aspa_sparse_attention(q, k, v, active_mask=mask.unsqueeze(-1), causal_mask=causal)
+    assert (out.float().cpu() - torch.from_numpy(z["out_mask"])).abs().max() <= tol
+    out = aspa_sparse_attention(q, k, v, active_mask=mask.unsqueeze(-1),
+                                shortlist_candidates=torch.from_numpy(z["cand"]).to(dev),
+                                shortlist_lengths=torch.from_numpy(z["lengths"]).to(dev))
+    assert (out.float().cpu() - torch.from_numpy(z["out_cand"])).abs().max() <= tol
+    # f32 restatement of the same operator (diagnostic: tighter for bf16)
+    ref32 = O.sparse_attention(q.cpu(), k.cpu(), v.cpu(), active_mask=mask.cpu(),
+                               shortlist_candidates=torch.from_numpy(z["cand"]),
+                               shortlist_lengths=torch.from_numpy(z["lengths"]), compute_dtype=torch.float32)
+    assert (out.float().cpu() - ref32.float()).abs().max() <= (2e-5 if tag == "f32" else 8e-3)
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 5, 24])
+def test_attention_head_dims_vs_oracle(dev, D):
+    from proteus_attention.kernels.sparse_attn import aspa_sparse_attention
+
+    g = torch.Generator().manual_seed(D)
+    BH, T = 3, 150
+    q, k, v = (torch.randn(BH, T, D, generator=g) for _ in range(3))
+    m = torch.rand(BH, T, generator=g) > 0.5
+    causal = torch.triu(torch.full((T, T), float("-inf")), diagonal=1)
+    out = aspa_sparse_attention(q.to(dev), k.to(dev), v.to(dev), active_mask=m.to(dev), causal_mask=causal.to(dev))
+    ref = O.sparse_attention(q, k, v, active_mask=m, causal_mask=causal)
+    assert (out.cpu() - ref).abs().max() <= TOL_F32
+
+
+def test_attention_int8_vs_oracle(dev):
+    from proteus_attention.kernels.sparse_attn import aspa_sparse_attention
+
+    g = torch.Generator().manual_seed(42)
+    q, k, v = (torch.randn(4, 33, 16, generator=g) for _ in range(3))
+    m = torch.rand(4, 33, generator=g) > 0.4
+    causal = torch.triu(torch.full((33, 33), float("-inf")), diagonal=1)
+    (qi, qs), (ki, ks), (vi, vs) = (O.quantize_per_head_int8(t) for t in (q, k, v))
+    out = aspa_sparse_attention(qi.to(dev), ki.to(dev), vi.to(dev), active_mask=m.to(dev),
+                                causal_mask=causal.to(dev), q_scale=qs.to(dev), k_scale=ks.to(dev),
+                                v_scale=vs.to(dev), out_dtype=torch.float32)
+    ref = O.sparse_attention(qi, ki, vi, active_mask=m, causal_mask=causal, q_scale=qs, k_scale=ks, v_scale=vs,
+                             out_dtype=torch.float32)
+    assert (out.cpu() - ref).abs().max() <= TOL_F32
+    fp = O.sparse_attention(q, k, v, active_mask=m, causal_mask=causal)
+    d = (out.cpu() - fp).abs()
+    assert d.mean() < 0.05 and d.max() < 0.2  # reference tests/test_aspa.py:250-305 bound
+
+
+def test_attention_all_inactive_and_empty(dev):
+    from proteus_attention.kernels.sparse_attn import aspa_sparse_attention, get_last_backend
+
+    q = torch.randn(2, 9, 32, device=dev)
+    out = aspa_sparse_attention(q, q, q, active_mask=torch.zeros(2, 9, 1, device=dev))
+    assert get_last_backend() == "empty" and torch.count_nonzero(out) == 0
+
+
+# ---------------------------------------------------------------------------
+# module forward
+# ---------------------------------------------------------------------------
+
+def _module(cfg, B, T, C, dt, dev, outlier=0.0):
+    from configs import init_weights, make_inputs
+
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    torch.manual_seed(1234)
+    m = AdaptiveSparseAttention(ModelConfig(**cfg))
+    x, g = make_inputs(B, T, C, seed=0, outlier_frac=outlier)
+    init_weights(m, g)
+    m = m.to(device=dev, dtype=dt).eval()
+    return m, x.to(dt).to(dev)
+
+
+def _active_heads_per_token(token_idx, row_offsets, heads, B, H, T):
+    act = torch.zeros(B * H, T, dtype=torch.bool)
+    offs = row_offsets.tolist()
+    for p, bh in enumerate(heads.tolist()):
+        act[bh, token_idx[offs[p]:offs[p + 1]]] = True
+    return act.view(B, H, T).permute(0, 2, 1)  # (B, T, H)
+
+
+@pytest.mark.parametrize("name,maker,B,T,C,dt,outlier", [
+    ("module_cfg1", "sparse", 1, 1024, 256, torch.float32, 0.0),
+    ("module_cfg2_T2048", "sparse", 2, 2048, 512, torch.bfloat16, 0.0),
+    ("module_short_T4096_f32", "short", 1, 4096, 512, torch.float32, 0.01),
+    ("module_short_T4096_bf16", "short", 1, 4096, 512, torch.bfloat16, 0.01),
+])
+def test_module_forward_vs_golden(dev, golden, name, maker, B, T, C, dt, outlier):
+    from configs import shortlist_cfg, sparse_cfg
+
+    _say(f"module {name}")
+    z = golden(name)
+    cfg = sparse_cfg(T, C, 8) if maker == "sparse" else shortlist_cfg(T, C, 8, 1024, 256, 64)
+    m, x = _module(cfg, B, T, C, dt, dev, outlier)
+    with torch.no_grad():
+        y = m(x)
+    assert m.last_head_stats["mode"] == str(z["mode"]) == "shortlist"
+    st = m._last_sparse_state
+    ours = _active_heads_per_token(st["token_idx"].cpu().long(), st["row_offsets"].cpu().long(),
+                                   st["active_head_indices"].cpu(), B, 8, T)
+    ref = _active_heads_per_token(torch.from_numpy(z["packed_token_idx"]), torch.from_numpy(z["packed_row_offsets"]),
+                                  torch.from_numpy(z["active_head_indices"]), B, 8, T)
+    same_tok = (ours == ref).all(-1)  # (B, T)
+    frac = float(same_tok.float().mean())
+    _say(f"{name}: tokens with identical head selection {frac:.5f}")
+    assert frac >= (1.0 if dt == torch.float32 else 0.99)
+    stride = int(z["token_stride"])
+    yr = torch.from_numpy(z["y"])
+    yo = y.float().cpu()[:, ::stride]
+    sel = same_tok[:, ::stride]
+    tol = TOL_F32 if dt == torch.float32 else TOL_BF16
+    err = (yo - yr).abs().amax(-1)[sel].max()
+    _say(f"{name}: max-abs err on matched tokens {float(err):.3e}")
+    assert float(err) <= tol
+    # post-forward prototype EMA state
+    assert torch.allclose(m.routing_prototypes.float().cpu(), torch.from_numpy(z["protos_after"]), atol=1e-5,
+                          rtol=1e-4 if dt == torch.float32 else 1e-2)
+    assert torch.allclose(m.routing_usage_ema.float().cpu(), torch.from_numpy(z["usage_after"]), rtol=1e-4,
+                          atol=1e-4 if dt == torch.float32 else 1e-1)
+
+
+def test_module_dense_paths_vs_oracle(dev):
+    """subquad mode (force-dense) and the small-sequence dense fast path
+    equal dense causal attention of the projected q/k/v."""
+    from configs import COMMON
+
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    g = torch.Generator().manual_seed(5)
+    B, T, C, H = 2, 96, 64, 4
+    base = dict(COMMON, d_model=C, n_head=H, attn_h_total=H, attn_gates=H, attn_use_rope=False,
+                attn_token_sparse=False)
+    x = torch.randn(B, T, C, generator=g)
+    for cfg in (dict(base, attn_mode="subquad"), dict(base, attn_small_seq_dense=128)):
+        torch.manual_seed(0)
+        m = AdaptiveSparseAttention(ModelConfig(**cfg)).eval()
+        with torch.no_grad():
+            qkv = m.qkv(x).view(B, T, 3, H, C // H)
+            q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3).reshape(B * H, T, C // H) for i in range(3))
+            att = O.causal_attention_f32(q, k, v).view(B, H, T, C // H).permute(0, 2, 1, 3).reshape(B, T, C)
+            exp = m.proj(att)
+            y = m.to(dev)(x.to(dev)).cpu()
+        assert (y - exp).abs().max() <= TOL_F32
+
+
+def test_dropin_mha_gpu(dev):
+    from proteus_attention import CausalASPAMultiheadAttention
+
+    torch.manual_seed(0)
+    mha = CausalASPAMultiheadAttention(64, 4, attn_mode="linear", attn_linear_L=64, attn_linear_window=32).to(dev)
+    x = torch.randn(2, 50, 64, device=dev)
+    pad = torch.zeros(2, 50, dtype=torch.bool, device=dev)
+    pad[1, 40:] = True
+    out, w = mha(x, key_padding_mask=pad, need_weights=True)
+    assert out.shape == x.shape and w.shape == (2, 50, 50)
+    assert torch.count_nonzero(out[1, 40:]) == 0
+    assert torch.isfinite(out).all()
+
+
+# ---------------------------------------------------------------------------
+# chunk selection
+# ---------------------------------------------------------------------------
+
+def test_chunk_select_vs_golden(dev, golden):
+    from proteus_attention.tools import chunk_select
+
+    z = golden("chunk_select")
+    s = torch.from_numpy(z["scores"]).to(dev)
+    v, i = chunk_select.nucleus_select(s, 512, 1.0)
+    assert np.array_equal(i.cpu().numpy(), z["i_p1"]) and np.array_equal(v.cpu().numpy(), z["v_p1"])
+    v, i = chunk_select.nucleus_select(s * 4.0, 512, 0.9)
+    assert np.array_equal(i.cpu().numpy(), z["i_p09"])
+    ki, ks = chunk_select.finalise(torch.from_numpy(z["all_scores"]).to(dev), torch.from_numpy(z["all_idx"]).to(dev),
+                                   4096)
+    assert np.array_equal(ki.cpu().numpy(), z["keep_idx"]) and np.array_equal(ks.cpu().numpy(), z["keep_scores"])
+
+
+def test_chunked_runner_small_gpu(dev):
+    from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
+
+    cfg = ChunkedShortlistConfig(seq_len=4096, d_model=64, chunk_len=1024, buffer_tokens=256, per_chunk_budget=128,
+                                 device=dev, heads=4, nucleus_top_p=1.0, storage="cpu")
+    res = ChunkedShortlistRunner(cfg).run()
+    k = res.keep_indices
+    assert k.numel() <= 256 and torch.all(k[1:] > k[:-1])
+    seq = torch.randn(1, 4096, 64, generator=torch.Generator().manual_seed(7))
+    assert res.metrics.used_fallback is False
+    assert res.final_output is not None and torch.isfinite(res.final_output).all()
+    del seq

@@ -1,0 +1,251 @@
+"""CPU: pin the oracle against the reference's golden vectors, brute force
+and closed forms.  These tests never touch the product package."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import aspa_oracle as O
+from oracle import c_oracle
+
+
+# ---------------------------------------------------------------------------
+# selection helpers
+# ---------------------------------------------------------------------------
+
+def test_topk_lowest_brute_force():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randint(0, 5, (300, 8), generator=g).float()
+    _, idx = O.topk_lowest(x, 3)
+    for r in range(x.size(0)):
+        order = sorted(range(8), key=lambda j: (-x[r, j].item(), j))[:3]
+        assert idx[r].tolist() == order
+
+
+def test_select_active_tokens_matches_golden_when_untied(golden):
+    z = golden("module_cfg1")
+    imp = torch.from_numpy(z["importance"])
+    ref_mask = torch.from_numpy(z["token_mask"]).bool()
+    T = imp.size(1)
+    mine = O.select_active_tokens(imp, 0.25, 1, 1, 0.0)
+    # positions whose value equals the cut value may legitimately differ
+    need = int(torch.tensor(0.25 * T, dtype=torch.float32).round())
+    cut = torch.sort(imp[0], descending=True).values[need - 1]
+    differ = (mine != ref_mask)[0]
+    assert int(mine.sum()) == int(ref_mask.sum())
+    assert bool((imp[0][differ] == cut).all()) or not bool(differ.any())
+    assert mine[0, 0]  # guard
+
+
+def test_pack_closed_form():
+    g = torch.Generator().manual_seed(3)
+    m = torch.rand(5, 40, generator=g) > 0.5
+    m[2] = False
+    h, t, offs, mx = O.pack_active_rows(m)
+    assert offs[-1] == int(m.sum())
+    for p in range(5):
+        toks = t[offs[p]:offs[p + 1]]
+        assert toks.tolist() == m[p].nonzero().flatten().tolist()
+    assert mx == int(m.sum(1).max())
+
+
+# ---------------------------------------------------------------------------
+# shortlist builder
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tag", ["l", "la", "lp", "ap"])
+def test_builder_small_matches_reference(golden, tag):
+    z = golden(f"builder_small_{tag}")
+    ul, ua, up = (bool(v) for v in z["use"])
+    rows = torch.from_numpy(z["rows"])
+    c, l = O.build_shortlist(rows, 64, max_candidates=16, linear_window=12, anchor_stride=4, use_local=ul,
+                             use_anchors=ua, proto_scores=torch.from_numpy(z["scores"]) if up else None)
+    assert np.array_equal(c.numpy(), z["cand"])
+    assert np.array_equal(l.numpy(), z["lengths"])
+
+
+def test_builder_packed_realistic_matches_reference(golden):
+    z = golden("builder_packed_T4096")
+    L, w, s, lc, ac, pc = (int(v) for v in z["kw"])
+    rows = torch.from_numpy(z["rows"])
+    rb = torch.from_numpy(z["row_batch"])
+    c, l = O.build_shortlist(rows, 4096, max_candidates=L, linear_window=w, anchor_stride=s, use_local=True,
+                             use_anchors=True, proto_scores=torch.from_numpy(z["sims"]), row_batch_ids=rb,
+                             local_cap=lc, anchor_cap=ac, proto_cap=pc)
+    assert np.array_equal(c.numpy(), z["cand"])
+    assert np.array_equal(l.numpy(), z["lengths"])
+    # C oracle on the same rows
+    K = min(L, pc, 4096)
+    cc, cl = c_oracle.shortlist_build(z["rows"].astype(np.int32), z["row_batch"].astype(np.int32), 4096, L,
+                                      min(w, L, lc), s, min(ac, L, 4096), z["sims"], K)
+    assert np.array_equal(cc, z["cand"])
+    assert np.array_equal(cl, z["lengths"])
+
+
+def test_builder_truncation_matches_reference(golden):
+    z = golden("builder_truncate")
+    L, w, s, lc, ac, pc = (int(v) for v in z["kw"])
+    c, l = O.build_shortlist(torch.from_numpy(z["rows"]), 2048, max_candidates=L, linear_window=w, anchor_stride=s,
+                             use_local=True, use_anchors=True, proto_scores=torch.from_numpy(z["sims"]),
+                             local_cap=lc, anchor_cap=ac, proto_cap=pc)
+    assert np.array_equal(c.numpy(), z["cand"])
+    assert np.array_equal(l.numpy(), z["lengths"])
+    assert int(l.max()) == L  # the case does truncate
+
+
+def test_builder_closed_forms():
+    """Local window alone is [max(0,t-w+1) .. t]; anchors alone are the
+    distinct max(t - s*j, 0) plus t (the reference test's restatement)."""
+    rows = torch.tensor([0, 3, 11, 40, 99])
+    c, l = O.build_shortlist(rows, 100, max_candidates=20, linear_window=8, anchor_stride=0, use_local=True,
+                             use_anchors=False)
+    for i, t in enumerate(rows.tolist()):
+        exp = list(range(max(0, t - 7), t + 1))
+        assert c[i, :len(exp)].tolist() == exp and int(l[i]) == len(exp)
+        assert all(v == t for v in c[i, len(exp):].tolist())
+    c, l = O.build_shortlist(rows, 100, max_candidates=20, linear_window=1, anchor_stride=7, use_local=False,
+                             use_anchors=True)
+    for i, t in enumerate(rows.tolist()):
+        exp = sorted({max(t - 7 * j, 0) for j in range(1, 21)} | {t})
+        assert c[i, :len(exp)].tolist() == exp and int(l[i]) == len(exp)
+
+
+def test_proto_prefix_sets_brute_force():
+    g = torch.Generator().manual_seed(5)
+    s = torch.randint(0, 6, (70,), generator=g).float()  # many ties
+    K = 9
+    sets = O.proto_prefix_sets(s, K)
+    for t in range(70):
+        c = min(t + 1, K)
+        best = sorted(range(t + 1), key=lambda j: (-s[j].item(), j))[:c]
+        assert sets[t, :c].tolist() == sorted(best)
+
+
+def test_c_oracle_matches_torch_oracle_with_ties():
+    g = torch.Generator().manual_seed(9)
+    T = 500
+    rows = torch.randint(0, T, (300,), generator=g)
+    s = torch.randint(0, 7, (T,), generator=g).float()
+    c, l = O.build_shortlist(rows, T, max_candidates=64, linear_window=20, anchor_stride=9, use_local=True,
+                             use_anchors=True, proto_scores=s, local_cap=20, anchor_cap=30, proto_cap=25)
+    cc, cl = c_oracle.shortlist_build(rows.numpy().astype(np.int32), None, T, 64, 20, 9, 30, s.numpy(), 25)
+    assert np.array_equal(cc, c.numpy().astype(np.int32))
+    assert np.array_equal(cl, l.numpy().astype(np.int32))
+
+
+def test_oracle_detects_planted_mistake():
+    """A plausible slip (anchor offsets starting at j=0) is caught by the
+    golden vectors."""
+    rows = torch.tensor([5, 17, 33])
+    good, _ = O.build_shortlist(rows, 64, max_candidates=16, linear_window=1, anchor_stride=4, use_local=False,
+                                use_anchors=True)
+    bad = torch.stack([torch.clamp(rows - 4 * j, min=0) for j in range(0, 16)], 1)
+    assert not torch.equal(good[:, :5], torch.sort(bad, 1).values[:, :5])
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tag,tol", [("f32", 2e-5), ("bf16", 0.0)])
+def test_sparse_attention_matches_reference(golden, tag, tol):
+    z = golden(f"attn_{tag}")
+    dt = torch.float32 if tag == "f32" else torch.bfloat16
+    q, k, v = (torch.from_numpy(z[n]).to(dt) for n in ("q", "k", "v"))
+    mask = torch.from_numpy(z["mask"]).bool()
+    T = q.size(1)
+    causal = torch.triu(torch.full((T, T), float("-inf")), diagonal=1)
+    out = O.sparse_attention(q, k, v, active_mask=mask)
+    assert torch.allclose(out.float(), torch.from_numpy(z["out_nocand"]), atol=tol + 1e-6, rtol=0)
+    out = O.sparse_attention(q, k, v, active_mask=mask, causal_mask=causal)
+    assert torch.allclose(out.float(), torch.from_numpy(z["out_mask"]), atol=tol + 1e-6, rtol=0)
+    out = O.sparse_attention(q, k, v, active_mask=mask, shortlist_candidates=torch.from_numpy(z["cand"]),
+                             shortlist_lengths=torch.from_numpy(z["lengths"]))
+    assert torch.allclose(out.float(), torch.from_numpy(z["out_cand"]), atol=tol + 1e-6, rtol=0)
+
+
+def test_sparse_attention_closed_form_and_sdpa():
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(3, 6, 5, generator=g) for _ in range(3))
+    causal = torch.triu(torch.full((6, 6), float("-inf")), diagonal=1)
+    out = O.sparse_attention(q, k, v, causal_mask=causal)
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=causal.unsqueeze(0))
+    assert torch.allclose(out, ref, atol=1e-6)
+    # manual per-row softmax on a partial mask
+    m = torch.rand(3, 6, generator=g) > 0.4
+    out = O.sparse_attention(q, k, v, active_mask=m, causal_mask=causal)
+    for h in range(3):
+        for t in range(6):
+            if not m[h, t]:
+                assert torch.all(out[h, t] == 0)
+            else:
+                s = (k[h, : t + 1] @ q[h, t]) / math.sqrt(5)
+                exp = torch.softmax(s, 0) @ v[h, : t + 1]
+                assert torch.allclose(out[h, t], exp, atol=1e-5)
+
+
+def test_candidates_covering_prefix_equal_causal():
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(2, 40, 8, generator=g) for _ in range(3))
+    rows = torch.arange(40).repeat(2)
+    c, l = O.build_shortlist(rows, 40, max_candidates=40, linear_window=40, anchor_stride=0, use_local=True,
+                             use_anchors=False)
+    out = O.sparse_attention(q, k, v, shortlist_candidates=c, shortlist_lengths=l)
+    assert torch.allclose(out, O.causal_attention_f32(q, k, v), atol=1e-5)
+
+
+def test_quantize_per_head_closed_form():
+    g = torch.Generator().manual_seed(4)
+    t = torch.randn(3, 10, 4, generator=g)
+    qv, s = O.quantize_per_head_int8(t)
+    assert torch.allclose(s, t.reshape(3, -1).abs().amax(1) / 127.0)
+    assert int(qv.abs().max()) == 127
+    assert torch.allclose(qv.float() * s.view(-1, 1, 1), t, atol=float(s.max()) / 2 + 1e-7)
+
+
+# ---------------------------------------------------------------------------
+# router
+# ---------------------------------------------------------------------------
+
+def _module_weights(B, T, C, H, outlier=0.0):
+    from configs import make_inputs
+
+    x, g = make_inputs(B, T, C, seed=0, outlier_frac=outlier)
+    ws = []
+    for shape in ((H, C), (H, C), (3 * C, C), (C, C)):
+        tmp = torch.empty(shape)
+        torch.nn.init.xavier_normal_(tmp, generator=g)
+        ws.append(tmp)
+    return x, ws
+
+
+def _digest(*ts):
+    import hashlib
+
+    h = hashlib.sha256()
+    for t in ts:
+        h.update(t.float().contiguous().numpy().tobytes())
+    return h.hexdigest()
+
+
+@pytest.mark.parametrize("name,B,T,C,dt,outlier", [
+    ("module_cfg1", 1, 1024, 256, torch.float32, 0.0),
+    ("module_cfg2_T2048", 2, 2048, 512, torch.bfloat16, 0.0),
+    ("module_short_T4096_f32", 1, 4096, 512, torch.float32, 0.01),
+    ("module_short_T4096_bf16", 1, 4096, 512, torch.bfloat16, 0.01),
+])
+def test_router_oracle_matches_reference(golden, name, B, T, C, dt, outlier):
+    z = golden(name)
+    x, ws = _module_weights(B, T, C, 8, outlier)
+    assert _digest(x) == str(z["x_sha256"])
+    assert _digest(*ws) == str(z["w_sha256"])
+    gate, sim, blend, imp = O.route_tokens(x.to(dt), ws[0].to(dt), ws[1].to(dt), torch.zeros(8, dtype=dt),
+                                           None, proto_temp=0.2, proto_threshold=0.25, proto_blend=0.6,
+                                           usage_boost=0.0)
+    assert torch.allclose(gate, torch.from_numpy(z["gate_probs"]), atol=1e-6, rtol=0)
+    assert torch.allclose(imp, torch.from_numpy(z["importance"]), atol=1e-6, rtol=0)
+    assert torch.allclose(sim, torch.from_numpy(z["sim"]), atol=1e-6, rtol=0)
