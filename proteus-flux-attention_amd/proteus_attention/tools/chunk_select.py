@@ -55,16 +55,22 @@ def nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float,
 
 
 def finalise(scores: torch.Tensor, indices: torch.Tensor, max_tokens: int) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Global shortlist: best score per position, best ``max_tokens``
-    positions, returned sorted by position (int64, with their scores)."""
+    """Global shortlist: one entry per position, the first ``max_tokens``
+    entries in descending score order, returned sorted by position (int64,
+    with their scores).
+
+    A position listed more than once is represented by its LAST entry in
+    score order (its lowest score): the reference sorts the composite key
+    ``index*(n+1) - order_position`` ascending and keeps the first of each
+    group (chunked_shortlist.py:233-243), which is the latest one.  Chunks
+    are disjoint, so in the pipeline itself positions never repeat."""
 
     order = _order_desc(scores.to(torch.float32))
     s_ord = scores[order]
     i_ord = indices[order].to(torch.long)
     n = i_ord.numel()
     pos = torch.arange(n, device=i_ord.device, dtype=torch.long)
-    # first occurrence (in score order) of every position
-    by_idx = torch.sort(i_ord * (n + 1) + pos).indices
+    by_idx = torch.sort(i_ord * (n + 1) - pos).indices
     sorted_idx = i_ord[by_idx]
     first = torch.ones_like(sorted_idx, dtype=torch.bool)
     first[1:] = sorted_idx[1:] != sorted_idx[:-1]

@@ -277,8 +277,9 @@ def test_rope_kernel_bitwise(dev, dt):
     qkv = torch.randn(B, T, 3 * H * D, generator=g).to(dt)
     cos, sin = O.rope_tables(T, D, 10000.0, dt)
     d = qkv.to(dev).contiguous()
-    rc = _hip.lib().pfa_rope_qk_inplace(_hip.ptr(d), _hip.dtype_tag(dt), B, T, H, D, _hip.ptr(cos.to(dev)),
-                                         _hip.ptr(sin.to(dev)), _hip.stream_ptr(dev))
+    cd, sd = cos.to(dev), sin.to(dev)  # keep the device tables alive across the launch
+    rc = _hip.lib().pfa_rope_qk_inplace(_hip.ptr(d), _hip.dtype_tag(dt), B, T, H, D, _hip.ptr(cd), _hip.ptr(sd),
+                                         _hip.stream_ptr(dev))
     _hip.check(rc, "rope")
     got = d.cpu().view(B, T, 3, H, D)
     ref = qkv.view(B, T, 3, H, D)
