@@ -57,24 +57,33 @@ const char* pfa_last_error_string(void);
  * the lowest head index.
  *
  *   x            (n_tok, C) in x_dtype (PFA_F32 / PFA_BF16 / PFA_F16)
- *   w_router     (G, C) in x_dtype              (head_router.linear.weight)
- *   proto_norm   (G, C) f32, rows already L2-normalised, or NULL (proto off)
+ *   w_packed     (C, 2*Gp) f32 with Gp = pfa_router_gate_pad(G), channel-
+ *                interleaved: w_packed[c][g] = head_router.linear.weight[g][c]
+ *                (its x_dtype value) and w_packed[c][Gp+g] = the L2-
+ *                normalised prototype P[g][c]; padding gates are zero.  With
+ *                use_proto == 0 only the first Gp columns are read.
  *   conf_weight  (G) f32 = routing_confidence + 1e-6, or NULL
  *   usage_bias   (G) f32 = softmax(-(usage+1e-6)), or NULL (boost off)
  *   gate_to_head (G) int32, values in [0, H)
  *   outputs (NULL allowed for any of the optional ones):
  *     gate_probs (n_tok, G) f32, sim (n_tok) f32, blend (n_tok) f32,
  *     importance (n_tok) f32 (required), head_idx (n_tok, topk) int32
- *     (required), head_score (n_tok, topk) f32.
+ *     (required, each row ranked best first), head_score (n_tok, topk) f32,
+ *     stats_partial (n_blocks, 8) f32: per workgroup the sums of router
+ *     entropy, max prototype similarity, blend, count(blend > 0) and top-k
+ *     head scores (telemetry of aspa.py:1857-1916); n_blocks from
+ *     pfa_router_block_count().
  * ==================================================================== */
+int pfa_router_gate_pad(int G);
+int pfa_router_block_count(int64_t n_tok, int* n_blocks);
 int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G,
-                    const void* w_router, const float* proto_norm,
+                    const float* w_packed, int use_proto,
                     const float* conf_weight, const float* usage_bias,
                     const int32_t* gate_to_head, int H, int topk,
                     float proto_temp, float proto_threshold, float proto_blend,
                     float usage_boost, float* gate_probs, float* sim,
                     float* blend, float* importance, int32_t* head_idx,
-                    float* head_score, void* stream);
+                    float* head_score, float* stats_partial, void* stream);
 
 /* ====================================================================
  * Prototype EMA statistics (aspa.py:692-718): per slice of tokens the
@@ -89,6 +98,14 @@ int pfa_proto_accumulate(const void* x, int x_dtype, int64_t n_tok, int C,
                          int n_parts, void* stream);
 int pfa_proto_partial_reduce(const float* partial, int n_parts, int G, int C,
                              float* out, void* stream);
+
+/* EMA step of aspa.py:700-716 from the reduced (G, C+1) sums: for gates with
+ * count > 1e-6, protos = decay*protos + (1-decay)*mean; usage = decay*usage
+ * (+ (1-decay)*count); confidence = decay*confidence (+ (1-decay)); every
+ * op rounded to the buffers' dtype (PFA_F32 / PFA_BF16 / PFA_F16). */
+int pfa_proto_ema_update(const float* sums, int G, int C, float decay,
+                         void* protos, void* usage, void* confidence,
+                         int dtype, void* stream);
 
 /* ====================================================================
  * Token top-k: per batch row keep the `need` highest importance tokens
@@ -116,6 +133,8 @@ int pfa_token_topk(const float* importance, int B, int64_t T, int64_t keep_count
  *   row_offsets_out  (B*H + 1) int32 : exclusive scan over active heads
  *   token_idx_out    (B*H*T) int32 capacity : token of each packed row
  *   row_head_out     (B*H*T) int32 capacity : compact head of each row
+ *   row_of_out       (B*H, T) int32 or NULL : packed row of (b*H+h, t), -1
+ *                    when inactive (used by the residue-class anchor pass)
  *   summary_out (4) int32 : {P, N, max_rows, 0}
  * The workspace holds per-(head, block) counts.
  * ==================================================================== */
@@ -124,8 +143,8 @@ int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* token_mask,
                   int B, int H, int64_t T, uint8_t* mask_out,
                   int32_t* active_heads_out, int32_t* row_offsets_out,
                   int32_t* token_idx_out, int32_t* row_head_out,
-                  int32_t* summary_out, void* workspace, size_t ws_bytes,
-                  void* stream);
+                  int32_t* row_of_out, int32_t* summary_out, void* workspace,
+                  size_t ws_bytes, void* stream);
 
 /* Same packing from an arbitrary (P, T) uint8 mask (the operator-level
  * entry point aspa_sparse_attention packs its own active_mask). Heads are
@@ -138,14 +157,19 @@ int pfa_pack_mask(const uint8_t* mask, int P, int64_t T, int32_t* row_offsets_ou
 /* ====================================================================
  * Prototype candidates: for every token t of every batch row b, the
  * indices of the min(t+1, K) largest proto_scores[b, 0..t] (ties -> lowest
- * index), written sorted by index into (B, T, K) int32.
+ * index), written sorted by index into (B, T, K) int32 (entries past
+ * min(t+1, K) hold t).  Optionally evict_out (B, T) int32: the first token
+ * at which position p is no longer among the prefix top-K (INT32_MAX if
+ * never, p if it never enters), so that p is in the set of token t exactly
+ * when p <= t < evict[p].
  * Replaces the (rows, T) masked topk of _shortlist_prepare_proto_candidates
  * (sparse_attn.py:260-300) by a blocked prefix top-k.
  * ==================================================================== */
 int pfa_proto_prefix_workspace_size(int B, int64_t T, int K, size_t* bytes);
 int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T,
                           int64_t score_stride, int K, int32_t* sets_out,
-                          void* workspace, size_t ws_bytes, void* stream);
+                          int32_t* evict_out, void* workspace, size_t ws_bytes,
+                          void* stream);
 
 /* ====================================================================
  * Shortlist candidate builder (packed rows).
@@ -213,6 +237,33 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                         int mask_dtype, const int32_t* head_max_token,
                         float scale, const float* q_scale, const float* k_scale,
                         const float* v_scale, void* stream);
+
+/* ====================================================================
+ * Shortlist attention without materialised candidates (bf16, D = 64).
+ * Same result as pfa_shortlist_build followed by pfa_sparse_attn_fwd for the
+ * module's packed rows when no row is truncated (local_w + anchors below the
+ * window + proto_k + 1 <= L, checked by the caller): each row attends to its
+ * window [t - min(t+1, local_w) + 1, t], its strided anchors below the window
+ * and its prototype prefix set below the window (proto_sets/proto_evict from
+ * pfa_proto_prefix_topk), with the zero anchor, all on bf16 MFMA.
+ * Replaces sparse_attn.py:457-596 + 597-921 on the module path
+ * (aspa.py:1269-1302).
+ *   row_of (B*H, T) from pfa_pack_rows; summary from pfa_pack_rows ({P,...});
+ *   head_map (P_cap) compact -> b*H+h; partials (N, pfa_shortlist_attn_part_
+ *   floats()) f32 scratch for the anchor pass; lengths (N) int32 or NULL
+ *   receives each row's candidate count (the builder's lengths).
+ * ==================================================================== */
+int pfa_shortlist_attn_part_floats(void);
+int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
+                           pfa_tensor4 out, int dtype, int H, int64_t T, int D,
+                           const int32_t* token_idx, const int32_t* row_head,
+                           const int32_t* head_map, int64_t N, int P_cap,
+                           const int32_t* summary, const int32_t* row_of,
+                           int local_w, int anchor_stride, int anchor_slots,
+                           const int32_t* proto_sets, int proto_k,
+                           int64_t proto_len, const int32_t* proto_evict,
+                           float scale, float* partials, int32_t* lengths,
+                           void* stream);
 
 /* Per compact head, the largest token among its packed rows (needed by the
  * explicit-mask branch: sparse_attn.py:1010-1015). */

@@ -4,6 +4,9 @@
 
 #include "pfa_common.h"
 
+// Elementwise RoPE arithmetic must round each product separately.
+#pragma clang fp contract(off)
+
 namespace pfa {
 
 static thread_local std::string g_last_error;
@@ -31,10 +34,42 @@ __global__ void zero_fill_tail(uint8_t* p, size_t n) {
 }
 
 // RoPE in place on the q and k thirds of a (B, T, 3, H, D) buffer.  One
-// thread handles one (even, odd) pair of one head of q or k:
+// thread rotates 4 (even, odd) pairs = 8 consecutive elements of one head of
+// q or k (16-byte loads of x, cos and sin):
 //   out_even = r(r(x_e*cos_e) + r(-x_o*sin_e)),  out_odd = r(r(x_o*cos_o) + r(x_e*sin_o))
 // where r() rounds to the tensor dtype, matching q*cos + rotate_half(q)*sin
-// evaluated as three elementwise ops in that dtype.
+// evaluated as three elementwise ops in that dtype.  D must be a multiple
+// of 8 (the host falls back to the per-pair kernel otherwise).
+template <int DT>
+__global__ void __launch_bounds__(256) rope8_kernel(typename Elem<DT>::T* qkv, int64_t n_groups, int64_t T, int H,
+                                                    int D, const typename Elem<DT>::T* cos_tab,
+                                                    const typename Elem<DT>::T* sin_tab) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_groups) return;
+  const int per_head = D / 8;
+  const int C = H * D;
+  int64_t gidx = i % per_head;
+  int64_t rest = i / per_head;
+  int h = (int)(rest % H);
+  rest /= H;
+  int which = (int)(rest % 2);
+  int64_t bt = rest / 2;
+  int64_t t = bt % T;
+  typename Elem<DT>::T* base = qkv + bt * (3 * (int64_t)C) + which * C + h * D + 8 * gidx;
+  float xv[8], cv[8], sv[8], o[8];
+  load8<DT>(base, xv);
+  load8<DT>(cos_tab + t * D + 8 * gidx, cv);
+  load8<DT>(sin_tab + t * D + 8 * gidx, sv);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    float xe = xv[2 * p], xo = xv[2 * p + 1];
+    o[2 * p] = round_to<DT>(round_to<DT>(xe * cv[2 * p]) + round_to<DT>(-xo * sv[2 * p]));
+    o[2 * p + 1] = round_to<DT>(round_to<DT>(xo * cv[2 * p + 1]) + round_to<DT>(xe * sv[2 * p + 1]));
+  }
+  store8<DT>(base, o);
+}
+
+// Per-pair variant for head dims that are not a multiple of 8.
 template <int DT>
 __global__ void __launch_bounds__(256) rope_kernel(typename Elem<DT>::T* qkv, int64_t n_pairs, int64_t T,
                                                    int H, int D, const typename Elem<DT>::T* cos_tab,
@@ -102,10 +137,36 @@ extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H
   PFA_CHECK_ARG(qkv && cos_tab && sin_tab, "pfa_rope_qk_inplace: null pointer");
   PFA_CHECK_ARG(B >= 0 && T >= 0 && H > 0 && D > 0 && D % 2 == 0,
                 "pfa_rope_qk_inplace: bad shape B=%d T=%lld H=%d D=%d", B, (long long)T, H, D);
+  hipStream_t s = as_stream(stream);
+  const bool vec = (D % 8) == 0 && ((uintptr_t)qkv % 16) == 0 && ((uintptr_t)cos_tab % 16) == 0 &&
+                   ((uintptr_t)sin_tab % 16) == 0;
+  if (vec) {
+    int64_t n_groups = (int64_t)B * T * 2 * H * (D / 8);
+    if (n_groups == 0) return PFA_OK;
+    unsigned blocks = (unsigned)((n_groups + 255) / 256);
+    switch (dtype) {
+      case PFA_F32:
+        rope8_kernel<PFA_F32><<<blocks, 256, 0, s>>>((float*)qkv, n_groups, T, H, D, (const float*)cos_tab,
+                                                      (const float*)sin_tab);
+        break;
+      case PFA_BF16:
+        rope8_kernel<PFA_BF16><<<blocks, 256, 0, s>>>((uint16_t*)qkv, n_groups, T, H, D,
+                                                       (const uint16_t*)cos_tab, (const uint16_t*)sin_tab);
+        break;
+      case PFA_F16:
+        rope8_kernel<PFA_F16><<<blocks, 256, 0, s>>>((uint16_t*)qkv, n_groups, T, H, D,
+                                                      (const uint16_t*)cos_tab, (const uint16_t*)sin_tab);
+        break;
+      default:
+        set_error("pfa_rope_qk_inplace: unsupported dtype %d", dtype);
+        return PFA_E_UNSUPPORTED;
+    }
+    PFA_CHECK_LAUNCH("pfa_rope_qk_inplace");
+    return PFA_OK;
+  }
   int64_t n_pairs = (int64_t)B * T * 2 * H * (D / 2);
   if (n_pairs == 0) return PFA_OK;
   unsigned blocks = (unsigned)((n_pairs + 255) / 256);
-  hipStream_t s = as_stream(stream);
   switch (dtype) {
     case PFA_F32:
       rope_kernel<PFA_F32><<<blocks, 256, 0, s>>>((float*)qkv, n_pairs, T, H, D, (const float*)cos_tab,

@@ -1,11 +1,7 @@
 // Router: per-token gate probabilities, prototype prior, importance and
-// head top-k, plus the partial sums of the prototype EMA update.
+// head top-k; the prototype EMA statistics and update.
 //
-// Mapping: one lane per token.  Router weights and normalised prototypes
-// are staged once per workgroup in LDS as f32, interleaved per channel
-// (lds[c][0..G) = W[:, c], lds[c][G..2G) = P[:, c]) so that every lane of a
-// wave reads the same LDS words (broadcast, no bank conflicts) while it
-// streams its own token row from HBM with 16-byte loads.
+// Mapping: one lane per token, one wave per workgroup (see router_kernel).
 //
 // Arithmetic follows the reference op by op (aspa.py:135-157, 628-690,
 // 1521-1530, 1540-1542): logits are rounded to the input dtype, the router
@@ -19,145 +15,182 @@
 
 namespace pfa {
 
-constexpr int kRouterThreads = 256;
-constexpr int kRouterLdsBytes = 64 * 1024;
+constexpr int kRouterTok = 64;  // tokens per workgroup (one per lane)
 
-template <int DT, int GMAX, bool LDS>
-__global__ void __launch_bounds__(kRouterThreads)
+// Router weights come pre-packed per channel as f32, wpk[c][0..GP) = W[:, c]
+// and wpk[c][GP..2GP) = P[:, c] (GP = gates padded to 8/16/32/64, padding
+// zero).  All lanes of a wave walk the channels in lock step, so the weight
+// addresses are wave-uniform and 4-byte aligned: they are read with scalar
+// loads and feed the FMAs as SGPR operands.  Each lane streams its own token
+// row with 16-byte loads.  NW waves split the channels of the same 64 tokens
+// and combine their partial dot products through LDS; wave 0 runs the
+// epilogue.
+template <int DT, int GP, bool PROTO, int NW>
+__global__ void __launch_bounds__(64 * NW)
 router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, int G,
-              const typename Elem<DT>::T* __restrict__ w_router, const float* __restrict__ proto_norm,
-              const float* __restrict__ conf_weight, const float* __restrict__ usage_bias,
-              const int32_t* __restrict__ gate_to_head, int H, int topk, float proto_temp,
-              float proto_threshold, float proto_blend, float usage_boost, float* __restrict__ gate_probs,
-              float* __restrict__ sim_out, float* __restrict__ blend_out, float* __restrict__ importance,
-              int32_t* __restrict__ head_idx, float* __restrict__ head_score) {
-  extern __shared__ float lds_w[];  // [C][2G]
-  const bool use_proto = proto_norm != nullptr;
-  const int G2 = 2 * G;
-  if constexpr (LDS) {
-    for (int i = threadIdx.x; i < C * G; i += blockDim.x) {
-      int g = i / C, c = i % C;
-      lds_w[c * G2 + g] = load_f<DT>(w_router + i);
-      lds_w[c * G2 + G + g] = use_proto ? proto_norm[i] : 0.f;
-    }
-    __syncthreads();
-  }
-
-  for (int64_t tok = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;; tok += (int64_t)gridDim.x * blockDim.x) {
-    // Uniform loop exit per workgroup is not required (no barriers below).
-    if (tok >= n_tok) break;
-    const typename Elem<DT>::T* xr = x + tok * C;
-    float logit[GMAX], dotp[GMAX];
+              const float* __restrict__ wpk, const float* __restrict__ conf_weight,
+              const float* __restrict__ usage_bias, const int32_t* __restrict__ gate_to_head, int H, int topk,
+              float proto_temp, float proto_threshold, float proto_blend, float usage_boost,
+              float* __restrict__ gate_probs, float* __restrict__ sim_out, float* __restrict__ blend_out,
+              float* __restrict__ importance, int32_t* __restrict__ head_idx, float* __restrict__ head_score,
+              float* __restrict__ stats) {
+  constexpr int NV = 2 * GP + 1;  // logits, proto dots, sum of squares
+  constexpr int WS = PROTO ? 2 * GP : GP;
+  __shared__ float red[(NW > 1) ? (NW - 1) * 64 * NV : 1];
+  const int lane = threadIdx.x & 63;
+  // wave index made explicitly wave-uniform so the channel loop (and with it
+  // every weight address) lives in scalar registers
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t tok = (int64_t)blockIdx.x * kRouterTok + lane;
+  const bool live = tok < n_tok;
+  const typename Elem<DT>::T* xr = x + (live ? tok : 0) * C;
+  float acc[NV];
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) { logit[g] = 0.f; dotp[g] = 0.f; }
-    float sq = 0.f;
+  for (int i = 0; i < NV; ++i) acc[i] = 0.f;
 
-    auto accum = [&](int c, float xv) {
-      sq = __builtin_fmaf(xv, xv, sq);
+  const int cw = C / NW;  // channels of this wave (host guarantees C % (32*NW) == 0 when NW > 1)
+  const int cbeg = wid * cw;
+  if ((cw % 32) == 0) {
+    float xa[4][8], xb[4][8];
 #pragma unroll
-      for (int g = 0; g < GMAX; ++g) {
-        if (g < G) {
-          float wv, pv;
-          if constexpr (LDS) { wv = lds_w[c * G2 + g]; pv = lds_w[c * G2 + G + g]; }
-          else {
-            wv = load_f<DT>(w_router + (int64_t)g * C + c);
-            pv = use_proto ? proto_norm[(int64_t)g * C + c] : 0.f;
+    for (int u = 0; u < 4; ++u) load8<DT>(xr + cbeg + 8 * u, xa[u]);
+    for (int c0 = cbeg; c0 < cbeg + cw; c0 += 32) {
+      const bool more = c0 + 32 < cbeg + cw;
+      if (more) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load8<DT>(xr + c0 + 32 + 8 * u, xb[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xv = xa[u][j];
+          const float* w = wpk + (int64_t)(c0 + 8 * u + j) * WS;
+          acc[NV - 1] = __builtin_fmaf(xv, xv, acc[NV - 1]);
+#pragma unroll
+          for (int g = 0; g < GP; ++g) acc[g] = __builtin_fmaf(xv, w[g], acc[g]);
+          if constexpr (PROTO) {
+#pragma unroll
+            for (int g = 0; g < GP; ++g) acc[GP + g] = __builtin_fmaf(xv, w[GP + g], acc[GP + g]);
           }
-          logit[g] = __builtin_fmaf(xv, wv, logit[g]);
-          dotp[g] = __builtin_fmaf(xv, pv, dotp[g]);
         }
       }
-    };
-
-    if ((C % 8) == 0 && (DT != PFA_F32 || true)) {
-      for (int c0 = 0; c0 < C; c0 += 8) {
-        float xv[8];
-        load8<DT>(xr + c0, xv);
+      if (more) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) accum(c0 + j, xv[j]);
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xa[u][j] = xb[u][j];
       }
-    } else {
-      for (int c = 0; c < C; ++c) accum(c, load_f<DT>(xr + c));
     }
-
-    // --- SwitchRouter: logits in x dtype, softmax in f32 rounded to x dtype.
-    float gate[GMAX];
-    float lmax = -INFINITY;
+  } else {
+    for (int c = cbeg; c < cbeg + cw; ++c) {
+      const float xv = load_f<DT>(xr + c);
+      const float* w = wpk + (int64_t)c * WS;
+      acc[NV - 1] = __builtin_fmaf(xv, xv, acc[NV - 1]);
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g)
-      if (g < G) { logit[g] = round_to<DT>(logit[g]); lmax = fmaxf(lmax, logit[g]); }
-    float lsum = 0.f;
+      for (int g = 0; g < GP; ++g) acc[g] = __builtin_fmaf(xv, w[g], acc[g]);
+      if constexpr (PROTO) {
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g)
-      if (g < G) { gate[g] = expf(logit[g] - lmax); lsum = lsum + gate[g]; }
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g)
-      if (g < G) gate[g] = round_to<DT>(gate[g] / lsum);
-
-    float sim_max = 0.f, blend_scalar = 0.f;
-    if (use_proto) {
-      float nrm = sqrtf(sq);
-      float inv_den = fmaxf(nrm, 1e-6f);
-      float sims[GMAX];
-      sim_max = -INFINITY;
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) { sims[g] = dotp[g] / inv_den; sim_max = fmaxf(sim_max, sims[g]); }
-      // proto_probs = softmax(sims / temp)
-      float pp[GMAX];
-      float smax = -INFINITY;
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) { pp[g] = sims[g] / proto_temp; smax = fmaxf(smax, pp[g]); }
-      float ssum = 0.f;
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) { pp[g] = expf(pp[g] - smax); ssum = ssum + pp[g]; }
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) pp[g] = pp[g] / ssum;
-      float den = fmaxf(1e-6f, 1.0f - proto_threshold);
-      blend_scalar = fminf(fmaxf((sim_max - proto_threshold) / den, 0.f), 1.f);
-      if (conf_weight != nullptr) {
-        float cs = 0.f;
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g)
-          if (g < G) { pp[g] = pp[g] * conf_weight[g]; cs = cs + pp[g]; }
-        cs = fmaxf(cs, 1e-6f);
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g)
-          if (g < G) pp[g] = pp[g] / cs;
+        for (int g = 0; g < GP; ++g) acc[GP + g] = __builtin_fmaf(xv, w[GP + g], acc[GP + g]);
       }
-      float blend = proto_blend * blend_scalar;
-      float one_m = 1.0f - blend;
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) gate[g] = gate[g] * one_m + pp[g] * blend;
-      if (usage_bias != nullptr && usage_boost > 0.f) {
-        float scale_u = (1.0f - blend_scalar) * usage_boost;
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g)
-          if (g < G) gate[g] = gate[g] + usage_bias[g] * scale_u;
-      }
-      float gs = 0.f;
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) { gate[g] = fmaxf(gate[g], 0.f); gs = gs + gate[g]; }
-      gs = fmaxf(gs, 1e-6f);
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) gate[g] = gate[g] / gs;
     }
-
-    float gmax = -INFINITY;
+  }
+  if constexpr (NW > 1) {
+    if (wid > 0) {
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g)
-      if (g < G) gmax = fmaxf(gmax, gate[g]);
-    float imp = use_proto ? (gmax * (1.0f - blend_scalar) + sim_max * blend_scalar) : gmax;
+      for (int i = 0; i < NV; ++i) red[((wid - 1) * NV + i) * 64 + lane] = acc[i];
+    }
+    __syncthreads();
+    if (wid > 0) return;
+#pragma unroll
+    for (int w = 1; w < NW; ++w)
+#pragma unroll
+      for (int i = 0; i < NV; ++i) acc[i] = acc[i] + red[((w - 1) * NV + i) * 64 + lane];
+  }
+  float* logit = acc;
+  float* dotp = acc + GP;
+  const float sq = acc[NV - 1];
 
+  // --- SwitchRouter: logits in x dtype, softmax in f32 rounded to x dtype.
+  float gate[GP];
+  float lmax = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < GP; ++g)
+    if (g < G) { logit[g] = round_to<DT>(logit[g]); lmax = fmaxf(lmax, logit[g]); }
+  float lsum = 0.f;
+#pragma unroll
+  for (int g = 0; g < GP; ++g) {
+    gate[g] = 0.f;
+    if (g < G) { gate[g] = expf(logit[g] - lmax); lsum = lsum + gate[g]; }
+  }
+#pragma unroll
+  for (int g = 0; g < GP; ++g)
+    if (g < G) gate[g] = round_to<DT>(gate[g] / lsum);
+
+  float sim_max = 0.f, blend_scalar = 0.f;
+  if constexpr (PROTO) {
+    float inv_den = fmaxf(sqrtf(sq), 1e-6f);
+    float sims[GP];
+    sim_max = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) { sims[g] = dotp[g] / inv_den; sim_max = fmaxf(sim_max, sims[g]); }
+    float pp[GP];
+    float smax = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) { pp[g] = sims[g] / proto_temp; smax = fmaxf(smax, pp[g]); }
+    float ssum = 0.f;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) { pp[g] = expf(pp[g] - smax); ssum = ssum + pp[g]; }
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) pp[g] = pp[g] / ssum;
+    float den = fmaxf(1e-6f, 1.0f - proto_threshold);
+    blend_scalar = fminf(fmaxf((sim_max - proto_threshold) / den, 0.f), 1.f);
+    if (conf_weight != nullptr) {
+      float cs = 0.f;
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) { pp[g] = pp[g] * conf_weight[g]; cs = cs + pp[g]; }
+      cs = fmaxf(cs, 1e-6f);
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) pp[g] = pp[g] / cs;
+    }
+    float blend = proto_blend * blend_scalar;
+    float one_m = 1.0f - blend;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) gate[g] = gate[g] * one_m + pp[g] * blend;
+    if (usage_bias != nullptr && usage_boost > 0.f) {
+      float scale_u = (1.0f - blend_scalar) * usage_boost;
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) gate[g] = gate[g] + usage_bias[g] * scale_u;
+    }
+    float gs = 0.f;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) { gate[g] = fmaxf(gate[g], 0.f); gs = gs + gate[g]; }
+    gs = fmaxf(gs, 1e-6f);
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) gate[g] = gate[g] / gs;
+  }
+
+  float gmax = -INFINITY, ent = 0.f;
+#pragma unroll
+  for (int g = 0; g < GP; ++g)
+    if (g < G) { gmax = fmaxf(gmax, gate[g]); ent = ent + logf(fmaxf(gate[g], 1e-9f)) * gate[g]; }
+  float imp = PROTO ? (gmax * (1.0f - blend_scalar) + sim_max * blend_scalar) : gmax;
+
+  float score_sum = 0.f;
+  if (live) {
     if (gate_probs) {
 #pragma unroll
-      for (int g = 0; g < GMAX; ++g)
+      for (int g = 0; g < GP; ++g)
         if (g < G) gate_probs[tok * G + g] = gate[g];
     }
     if (sim_out) sim_out[tok] = sim_max;
@@ -165,15 +198,15 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
     importance[tok] = imp;
 
     // head_probs = gate_probs @ onehot(gate_to_head); top-k (ties -> lower head).
-    float hp[GMAX];
+    float hp[GP];
 #pragma unroll
-    for (int h = 0; h < GMAX; ++h) hp[h] = 0.f;
+    for (int h = 0; h < GP; ++h) hp[h] = 0.f;
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
+    for (int g = 0; g < GP; ++g) {
       if (g < G) {
         int hg = gate_to_head[g];
 #pragma unroll
-        for (int h = 0; h < GMAX; ++h)
+        for (int h = 0; h < GP; ++h)
           if (h == hg) hp[h] = hp[h] + gate[g];
       }
     }
@@ -182,7 +215,7 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
       float bv = 0.f;
       int bi = -1;
 #pragma unroll
-      for (int h = 0; h < GMAX; ++h) {
+      for (int h = 0; h < GP; ++h) {
         if (h < H && !((taken >> h) & 1ull)) {
           if (bi < 0 || better(hp[h], h, bv, bi)) { bv = hp[h]; bi = h; }
         }
@@ -190,15 +223,49 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
       taken |= 1ull << bi;
       head_idx[tok * topk + j] = bi;
       if (head_score) head_score[tok * topk + j] = bv;
+      score_sum += bv;
+    }
+  }
+  if (stats) {
+    // per-workgroup telemetry partials: entropy, sim, blend, #blend>0, top-k score sum
+    float v[5] = {live ? -ent : 0.f, live ? sim_max : 0.f, live ? blend_scalar : 0.f,
+                  (live && blend_scalar > 0.f) ? 1.f : 0.f, score_sum};
+#pragma unroll
+    for (int i = 0; i < 5; ++i)
+      for (int off = 32; off > 0; off >>= 1) v[i] += __shfl_xor(v[i], off, 64);
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 5; ++i) stats[(int64_t)blockIdx.x * 8 + i] = v[i];
     }
   }
 }
 
-// Prototype EMA partial sums: part p accumulates, for a contiguous slice of
-// tokens, sum_t gate[t,g]*x[t,c] (columns 0..C-1) and sum_t gate[t,g]
-// (column C).  Threads stride over channels so x rows are read coalesced.
+// Prototype EMA partial sums: part p accumulates, for a slice of 64 tokens,
+// sum_t gate[t,g]*x[t,c] (columns 0..C-1) and sum_t gate[t,g] (column C).
+// A thread owns a pair of channels (one 4-byte load per token, coalesced
+// across the workgroup); the gate row of the current token is wave-uniform
+// (scalar loads); eight tokens are in flight per step, and thousands of
+// 4-wave workgroups keep the CUs busy.
 constexpr int kEmaThreads = 256;
-constexpr int kEmaMaxParts = 1024;
+constexpr int kEmaTok = 64;
+constexpr int kEmaMaxParts = 4096;
+
+template <int DT>
+__device__ __forceinline__ void load2(const typename Elem<DT>::T* p, bool two, float& a, float& b) {
+  if constexpr (DT == PFA_F32) {
+    a = p[0];
+    b = two ? p[1] : 0.f;
+  } else {
+    if (two && (((uintptr_t)p & 3) == 0)) {
+      uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+      if constexpr (DT == PFA_BF16) { a = __uint_as_float(w << 16); b = __uint_as_float(w & 0xffff0000u); }
+      else { a = f16_to_f32((uint16_t)(w & 0xffffu)); b = f16_to_f32((uint16_t)(w >> 16)); }
+    } else {
+      a = load_f<DT>(p);
+      b = two ? load_f<DT>(p + 1) : 0.f;
+    }
+  }
+}
 
 template <int DT, int GMAX>
 __global__ void __launch_bounds__(kEmaThreads)
@@ -208,19 +275,62 @@ proto_accum_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, in
   const int64_t t0 = (int64_t)part * tok_per_part;
   const int64_t t1 = min(n_tok, t0 + tok_per_part);
   float* out = partial + (int64_t)part * G * (C + 1);
-  for (int c = threadIdx.x; c <= C; c += blockDim.x) {
-    float acc[GMAX];
+  const int npair = (C + 1) / 2;
+  for (int cp = threadIdx.x; cp < npair; cp += blockDim.x) {
+    const int c0 = 2 * cp;
+    const bool two = c0 + 1 < C;
+    float a0[GMAX], a1[GMAX];
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) acc[g] = 0.f;
-    for (int64_t t = t0; t < t1; ++t) {
-      float xv = (c < C) ? load_f<DT>(x + t * C + c) : 1.0f;
+    for (int g = 0; g < GMAX; ++g) { a0[g] = 0.f; a1[g] = 0.f; }
+    int64_t t = t0;
+    for (; t + 8 <= t1; t += 8) {
+      float x0[8], x1[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) load2<DT>(x + (t + u) * C + c0, two, x0[u], x1[u]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float* pr = gate_probs + (t + u) * G;
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g)
+          if (g < G) {
+            a0[g] = __builtin_fmaf(pr[g], x0[u], a0[g]);
+            a1[g] = __builtin_fmaf(pr[g], x1[u], a1[g]);
+          }
+      }
+    }
+    for (; t < t1; ++t) {
+      float x0, x1;
+      load2<DT>(x + t * C + c0, two, x0, x1);
+      const float* pr = gate_probs + t * G;
 #pragma unroll
       for (int g = 0; g < GMAX; ++g)
-        if (g < G) acc[g] = __builtin_fmaf(gate_probs[t * G + g], xv, acc[g]);
+        if (g < G) {
+          a0[g] = __builtin_fmaf(pr[g], x0, a0[g]);
+          a1[g] = __builtin_fmaf(pr[g], x1, a1[g]);
+        }
     }
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g)
-      if (g < G) out[(int64_t)g * (C + 1) + c] = acc[g];
+    for (int g = 0; g < GMAX; ++g) {
+      if (g < G) {
+        out[(int64_t)g * (C + 1) + c0] = a0[g];
+        if (two) out[(int64_t)g * (C + 1) + c0 + 1] = a1[g];
+      }
+    }
+  }
+  // column C (sum of gate probabilities) by wave 0
+  if (threadIdx.x < 64) {
+    float cs[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) cs[g] = 0.f;
+    for (int64_t t = t0 + threadIdx.x; t < t1; t += 64)
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g)
+        if (g < G) cs[g] += gate_probs[t * G + g];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      for (int off = 32; off > 0; off >>= 1) cs[g] += __shfl_xor(cs[g], off, 64);
+      if (g < G && threadIdx.x == 0) out[(int64_t)g * (C + 1) + C] = cs[g];
+    }
   }
 }
 
@@ -228,38 +338,85 @@ __global__ void partial_reduce_kernel(const float* __restrict__ partial, int n_p
                                       float* __restrict__ out) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= width) return;
-  float s = 0.f;
-  for (int p = 0; p < n_parts; ++p) s = s + partial[(int64_t)p * width + i];
-  out[i] = s;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int p = 0;
+  for (; p + 4 <= n_parts; p += 4) {
+    s0 = s0 + partial[(int64_t)p * width + i];
+    s1 = s1 + partial[(int64_t)(p + 1) * width + i];
+    s2 = s2 + partial[(int64_t)(p + 2) * width + i];
+    s3 = s3 + partial[(int64_t)(p + 3) * width + i];
+  }
+  for (; p < n_parts; ++p) s0 = s0 + partial[(int64_t)p * width + i];
+  out[i] = (s0 + s1) + (s2 + s3);
+}
+
+// EMA update of prototypes / usage / confidence from the reduced sums
+// (aspa.py:700-716), each product and sum rounded to the buffer dtype as the
+// reference's in-place tensor ops do.  One thread per (gate, channel).
+template <int DT>
+__global__ void proto_ema_update_kernel(const float* __restrict__ sums, int G, int C, float decay,
+                                        typename Elem<DT>::T* __restrict__ protos,
+                                        typename Elem<DT>::T* __restrict__ usage,
+                                        typename Elem<DT>::T* __restrict__ conf) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)G * C) return;
+  const int g = (int)(i / C), c = (int)(i % C);
+  const float cnt = sums[(int64_t)g * (C + 1) + C];
+  const bool upd = cnt > 1e-6f;
+  const float om = 1.0f - decay;
+  if (upd) {
+    float mean = round_to<DT>(sums[(int64_t)g * (C + 1) + c] / cnt);
+    float p = load_f<DT>(protos + i);
+    store_f<DT>(protos + i, round_to<DT>(round_to<DT>(p * decay) + round_to<DT>(mean * om)));
+  }
+  if (c == 0) {
+    float u = round_to<DT>(load_f<DT>(usage + g) * decay);
+    if (upd) u = round_to<DT>(u + cnt * om);
+    store_f<DT>(usage + g, u);
+    float cf = round_to<DT>(load_f<DT>(conf + g) * decay);
+    if (upd) cf = round_to<DT>(cf + om);
+    store_f<DT>(conf + g, cf);
+  }
+}
+
+static int gate_pad(int G) { return G <= 8 ? 8 : G <= 16 ? 16 : G <= 32 ? 32 : 64; }
+
+template <int DT, int GP, bool PROTO>
+static void launch_router_gp(const void* x, int64_t n_tok, int C, int G, const float* wpk, const float* cw,
+                             const float* ub, const int32_t* g2h, int H, int topk, float temp, float thr, float pb,
+                             float boost, float* gp, float* sim, float* bl, float* imp, int32_t* hi, float* hs,
+                             float* stats, hipStream_t s) {
+  using ET = typename Elem<DT>::T;
+  unsigned blocks = (unsigned)((n_tok + kRouterTok - 1) / kRouterTok);
+  if (GP <= 16 && C % 128 == 0)
+    router_kernel<DT, GP, PROTO, 4><<<blocks, 256, 0, s>>>((const ET*)x, n_tok, C, G, wpk, cw, ub, g2h, H, topk,
+                                                           temp, thr, pb, boost, gp, sim, bl, imp, hi, hs, stats);
+  else
+    router_kernel<DT, GP, PROTO, 1><<<blocks, 64, 0, s>>>((const ET*)x, n_tok, C, G, wpk, cw, ub, g2h, H, topk,
+                                                          temp, thr, pb, boost, gp, sim, bl, imp, hi, hs, stats);
 }
 
 template <int DT>
-static int launch_router(const void* x, int64_t n_tok, int C, int G, const void* w, const float* pn,
-                         const float* cw, const float* ub, const int32_t* g2h, int H, int topk, float temp,
-                         float thr, float pb, float boost, float* gp, float* sim, float* bl, float* imp,
-                         int32_t* hi, float* hs, hipStream_t s) {
-  using ET = typename Elem<DT>::T;
-  size_t lds = (size_t)C * 2 * G * sizeof(float);
-  bool use_lds = lds <= (size_t)kRouterLdsBytes;
-  int64_t blocks = (n_tok + kRouterThreads - 1) / kRouterThreads;
-  if (blocks > 2048) blocks = 2048;
-  if (blocks < 1) blocks = 1;
-#define PFA_ROUTER_LAUNCH(GM)                                                                          \
-  do {                                                                                                 \
-    if (use_lds)                                                                                       \
-      router_kernel<DT, GM, true><<<(unsigned)blocks, kRouterThreads, lds, s>>>(                       \
-          (const ET*)x, n_tok, C, G, (const ET*)w, pn, cw, ub, g2h, H, topk, temp, thr, pb, boost, gp, \
-          sim, bl, imp, hi, hs);                                                                       \
-    else                                                                                               \
-      router_kernel<DT, GM, false><<<(unsigned)blocks, kRouterThreads, 0, s>>>(                        \
-          (const ET*)x, n_tok, C, G, (const ET*)w, pn, cw, ub, g2h, H, topk, temp, thr, pb, boost, gp, \
-          sim, bl, imp, hi, hs);                                                                       \
+static int launch_router(const void* x, int64_t n_tok, int C, int G, const float* wpk, bool proto, const float* cw,
+                         const float* ub, const int32_t* g2h, int H, int topk, float temp, float thr, float pb,
+                         float boost, float* gp, float* sim, float* bl, float* imp, int32_t* hi, float* hs,
+                         float* stats, hipStream_t s) {
+#define PFA_R(GPV)                                                                                             \
+  do {                                                                                                         \
+    if (proto)                                                                                                 \
+      launch_router_gp<DT, GPV, true>(x, n_tok, C, G, wpk, cw, ub, g2h, H, topk, temp, thr, pb, boost, gp, sim, \
+                                      bl, imp, hi, hs, stats, s);                                              \
+    else                                                                                                       \
+      launch_router_gp<DT, GPV, false>(x, n_tok, C, G, wpk, cw, ub, g2h, H, topk, temp, thr, pb, boost, gp,    \
+                                       sim, bl, imp, hi, hs, stats, s);                                        \
   } while (0)
-  if (G <= 8) PFA_ROUTER_LAUNCH(8);
-  else if (G <= 16) PFA_ROUTER_LAUNCH(16);
-  else if (G <= 32) PFA_ROUTER_LAUNCH(32);
-  else PFA_ROUTER_LAUNCH(64);
-#undef PFA_ROUTER_LAUNCH
+  switch (gate_pad(G)) {
+    case 8: PFA_R(8); break;
+    case 16: PFA_R(16); break;
+    case 32: PFA_R(32); break;
+    default: PFA_R(64); break;
+  }
+#undef PFA_R
   PFA_CHECK_LAUNCH("pfa_router_topk");
   return PFA_OK;
 }
@@ -278,41 +435,51 @@ static void launch_accum(const void* x, int64_t n_tok, int C, int G, const float
 
 using namespace pfa;
 
-extern "C" int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G, const void* w_router,
-                               const float* proto_norm, const float* conf_weight, const float* usage_bias,
-                               const int32_t* gate_to_head, int H, int topk, float proto_temp,
-                               float proto_threshold, float proto_blend, float usage_boost, float* gate_probs,
-                               float* sim, float* blend, float* importance, int32_t* head_idx, float* head_score,
+extern "C" int pfa_router_gate_pad(int G) { return gate_pad(G); }
+
+extern "C" int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G, const float* w_packed,
+                               int use_proto, const float* conf_weight, const float* usage_bias,
+                               const int32_t* gate_to_head, int H, int topk, float proto_temp, float proto_threshold,
+                               float proto_blend, float usage_boost, float* gate_probs, float* sim, float* blend,
+                               float* importance, int32_t* head_idx, float* head_score, float* stats_partial,
                                void* stream) {
   clear_error();
   PFA_CHECK_ARG(n_tok >= 0 && C > 0 && G > 0 && G <= 64 && H > 0 && H <= G && topk >= 1 && topk <= H,
                 "pfa_router_topk: bad sizes n_tok=%lld C=%d G=%d H=%d topk=%d", (long long)n_tok, C, G, H, topk);
-  PFA_CHECK_ARG(x && w_router && gate_to_head && importance && head_idx, "pfa_router_topk: null pointer");
+  PFA_CHECK_ARG(x && w_packed && gate_to_head && importance && head_idx, "pfa_router_topk: null pointer");
   if (n_tok == 0) return PFA_OK;
   hipStream_t s = as_stream(stream);
+  const bool pr = use_proto != 0;
   switch (x_dtype) {
     case PFA_F32:
-      return launch_router<PFA_F32>(x, n_tok, C, G, w_router, proto_norm, conf_weight, usage_bias, gate_to_head, H,
-                                    topk, proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim,
-                                    blend, importance, head_idx, head_score, s);
+      return launch_router<PFA_F32>(x, n_tok, C, G, w_packed, pr, conf_weight, usage_bias, gate_to_head, H, topk,
+                                    proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim, blend,
+                                    importance, head_idx, head_score, stats_partial, s);
     case PFA_BF16:
-      return launch_router<PFA_BF16>(x, n_tok, C, G, w_router, proto_norm, conf_weight, usage_bias, gate_to_head,
-                                     H, topk, proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim,
-                                     blend, importance, head_idx, head_score, s);
+      return launch_router<PFA_BF16>(x, n_tok, C, G, w_packed, pr, conf_weight, usage_bias, gate_to_head, H, topk,
+                                     proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim, blend,
+                                     importance, head_idx, head_score, stats_partial, s);
     case PFA_F16:
-      return launch_router<PFA_F16>(x, n_tok, C, G, w_router, proto_norm, conf_weight, usage_bias, gate_to_head, H,
-                                    topk, proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim,
-                                    blend, importance, head_idx, head_score, s);
+      return launch_router<PFA_F16>(x, n_tok, C, G, w_packed, pr, conf_weight, usage_bias, gate_to_head, H, topk,
+                                    proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim, blend,
+                                    importance, head_idx, head_score, stats_partial, s);
     default:
       set_error("pfa_router_topk: unsupported dtype %d", x_dtype);
       return PFA_E_UNSUPPORTED;
   }
 }
 
+extern "C" int pfa_router_block_count(int64_t n_tok, int* n_blocks) {
+  clear_error();
+  PFA_CHECK_ARG(n_blocks != nullptr && n_tok >= 0, "pfa_router_block_count: bad arguments");
+  *n_blocks = (int)((n_tok + kRouterTok - 1) / kRouterTok);
+  return PFA_OK;
+}
+
 extern "C" int pfa_proto_partial_count(int64_t n_tok, int* n_parts) {
   clear_error();
   PFA_CHECK_ARG(n_parts != nullptr && n_tok >= 0, "pfa_proto_partial_count: bad arguments");
-  int64_t parts = (n_tok + 255) / 256;
+  int64_t parts = (n_tok + kEmaTok - 1) / kEmaTok;
   if (parts > kEmaMaxParts) parts = kEmaMaxParts;
   if (parts < 1) parts = 1;
   *n_parts = (int)parts;
@@ -345,5 +512,33 @@ extern "C" int pfa_proto_partial_reduce(const float* partial, int n_parts, int G
   int64_t width = (int64_t)G * (C + 1);
   partial_reduce_kernel<<<(unsigned)((width + 255) / 256), 256, 0, as_stream(stream)>>>(partial, n_parts, width, out);
   PFA_CHECK_LAUNCH("pfa_proto_partial_reduce");
+  return PFA_OK;
+}
+
+extern "C" int pfa_proto_ema_update(const float* sums, int G, int C, float decay, void* protos, void* usage,
+                                    void* confidence, int dtype, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(sums && protos && usage && confidence && G > 0 && C > 0, "pfa_proto_ema_update: bad arguments");
+  int64_t n = (int64_t)G * C;
+  unsigned blocks = (unsigned)((n + 255) / 256);
+  hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case PFA_F32:
+      proto_ema_update_kernel<PFA_F32><<<blocks, 256, 0, s>>>(sums, G, C, decay, (float*)protos, (float*)usage,
+                                                               (float*)confidence);
+      break;
+    case PFA_BF16:
+      proto_ema_update_kernel<PFA_BF16><<<blocks, 256, 0, s>>>(sums, G, C, decay, (uint16_t*)protos,
+                                                                (uint16_t*)usage, (uint16_t*)confidence);
+      break;
+    case PFA_F16:
+      proto_ema_update_kernel<PFA_F16><<<blocks, 256, 0, s>>>(sums, G, C, decay, (uint16_t*)protos,
+                                                               (uint16_t*)usage, (uint16_t*)confidence);
+      break;
+    default:
+      set_error("pfa_proto_ema_update: unsupported dtype %d", dtype);
+      return PFA_E_UNSUPPORTED;
+  }
+  PFA_CHECK_LAUNCH("pfa_proto_ema_update");
   return PFA_OK;
 }

@@ -125,7 +125,8 @@ constexpr int kPackTile = 1024;  // 4 tokens per thread
 
 __global__ void __launch_bounds__(kPackThreads)
 pack_count_routed(const int32_t* __restrict__ head_idx, int topk, const uint8_t* __restrict__ token_mask, int H,
-                  int64_t T, int nblk, uint8_t* __restrict__ mask_out, int32_t* __restrict__ blockcounts) {
+                  int64_t T, int nblk, uint8_t* __restrict__ mask_out, int32_t* __restrict__ blockcounts,
+                  int32_t* __restrict__ row_of) {
   __shared__ int red[16];
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
@@ -139,6 +140,7 @@ pack_count_routed(const int32_t* __restrict__ head_idx, int topk, const uint8_t*
       for (int kk = 0; kk < topk; ++kk) sel |= head_idx[bt * topk + kk] == h;
       act = act && sel;
       mask_out[(int64_t)bh * T + t] = act ? 1 : 0;
+      if (row_of != nullptr) row_of[(int64_t)bh * T + t] = -1;
       cnt += act ? 1 : 0;
     }
   }
@@ -235,7 +237,7 @@ pack_scan_kernel(int32_t* __restrict__ blockcounts, int BH, int nblk, int compac
 __global__ void __launch_bounds__(kPackThreads)
 pack_fill_kernel(const uint8_t* __restrict__ mask, int64_t T, int nblk, const int32_t* __restrict__ bases,
                  const int32_t* __restrict__ compact_id, int32_t* __restrict__ token_idx,
-                 int32_t* __restrict__ row_head) {
+                 int32_t* __restrict__ row_head, int32_t* __restrict__ row_of) {
   __shared__ int wave_tot[4];
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int id = compact_id[bh];
@@ -261,6 +263,7 @@ pack_fill_kernel(const uint8_t* __restrict__ mask, int64_t T, int nblk, const in
       int pos = run + before + v - 1;
       token_idx[pos] = (int32_t)t;
       row_head[pos] = id;
+      if (row_of != nullptr) row_of[(int64_t)bh * T + t] = pos;
     }
     run += total;
     __syncthreads();
@@ -331,8 +334,8 @@ extern "C" int pfa_pack_workspace_size(int B, int H, int64_t T, size_t* bytes) {
 
 extern "C" int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* token_mask, int B, int H, int64_t T,
                              uint8_t* mask_out, int32_t* active_heads_out, int32_t* row_offsets_out,
-                             int32_t* token_idx_out, int32_t* row_head_out, int32_t* summary_out, void* workspace,
-                             size_t ws_bytes, void* stream) {
+                             int32_t* token_idx_out, int32_t* row_head_out, int32_t* row_of_out,
+                             int32_t* summary_out, void* workspace, size_t ws_bytes, void* stream) {
   clear_error();
   PFA_CHECK_ARG(head_idx && mask_out && row_offsets_out && token_idx_out && row_head_out && summary_out && workspace,
                 "pfa_pack_rows: null pointer");
@@ -348,13 +351,14 @@ extern "C" int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* t
   PackWs w = carve(workspace, BH, nblk);
   hipStream_t s = as_stream(stream);
   dim3 grid(nblk, (unsigned)BH);
-  pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts);
+  pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts,
+                                                  row_of_out);
   PFA_CHECK_LAUNCH("pfa_pack_rows/count");
   pack_scan_kernel<<<1, 1024, 0, s>>>(w.blockcounts, (int)BH, nblk, 1, w.totals, w.compact_id, active_heads_out,
                                       row_offsets_out, summary_out);
   PFA_CHECK_LAUNCH("pfa_pack_rows/scan");
   pack_fill_kernel<<<grid, kPackThreads, 0, s>>>(mask_out, T, nblk, w.blockcounts, w.compact_id, token_idx_out,
-                                                 row_head_out);
+                                                 row_head_out, row_of_out);
   PFA_CHECK_LAUNCH("pfa_pack_rows/fill");
   return PFA_OK;
 }
@@ -382,7 +386,7 @@ extern "C" int pfa_pack_mask(const uint8_t* mask, int P, int64_t T, int32_t* row
                                       summary_out);
   PFA_CHECK_LAUNCH("pfa_pack_mask/scan");
   pack_fill_kernel<<<grid, kPackThreads, 0, s>>>(mask, T, nblk, w.blockcounts, w.compact_id, token_idx_out,
-                                                 row_head_out);
+                                                 row_head_out, nullptr);
   PFA_CHECK_LAUNCH("pfa_pack_mask/fill");
   return PFA_OK;
 }

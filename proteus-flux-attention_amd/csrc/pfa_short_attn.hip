@@ -1,0 +1,536 @@
+// Shortlist attention on bf16 MFMA, driven by the structure of the
+// candidate sets instead of materialised candidate lists.
+//
+// For packed row r (compact head p, token t) the reference's candidate set
+// (sparse_attn.py:376-596, no truncation) is the disjoint union of
+//   W(t) = [lo, t]                       local window, lo = t - min(t+1, w) + 1
+//   A(t) = { t - s*j : j0 <= j <= min(slots, t/s) }   strided anchors below lo
+//   X(t) = proto positions below lo that are not strided anchors, plus the
+//          clamped anchor 0 when max(t - s*slots, 0) == 0 is not itself a
+//          strided anchor ("zero anchor")
+// and a position p belongs to the prototype prefix set of t exactly when
+// p <= t < evict[p] (evict from pfa_proto_prefix_topk).
+//
+// Pass 1, short_anchor_kernel: one workgroup per (compact head, residue class
+// c = t mod s).  The anchors of every row of the class lie on the strided
+// key sequence c, c+s, c+2s, ...; row M = (t-c)/s uses keys
+// m in [max(0, M-slots), M-j0], so the class is a banded attention over one
+// shared key sequence.  Writes unnormalised online-softmax partials
+// (max, sum, acc[64]) per row.
+//
+// Pass 2, short_main_kernel: one workgroup per 64 consecutive packed rows.
+// Rows of one head whose tokens span less than w share the window union
+// [lo_first, t_last] and all their prototype keys lie in the prefix set of
+// the first row (anything newer than t_first is inside every window), so a
+// "segment" of rows streams those keys once, masks per (row, key), merges the
+// anchor partial and writes the normalised bf16 row into [b][h][t][:].
+//
+// Tiles: 4 waves x 16 query rows, 64 keys per tile staged in LDS (K row-
+// major, V transposed, rows padded to 72 elements: conflict-free 16-lane
+// reads).  Each wave computes S^T = K Q^T and O^T += V^T P^T with
+// v_mfma_f32_16x16x32_bf16, so a lane owns one query row throughout: the
+// softmax max/sum need only two cross-lane shuffles.
+#include "pfa_common.h"
+
+namespace pfa {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+constexpr int kRows = 64;   // query rows per workgroup
+constexpr int kTile = 64;   // keys per tile
+constexpr int kLd = 72;     // padded LDS row, bf16 elements
+constexpr int kPartW = 68;  // floats per partial row: m, l, pad, pad, acc[64]
+constexpr int kMaxProto = 1024;
+constexpr int kMaxClassRows = 4096;
+
+struct ShortArgs {
+  pfa_tensor4 q, k, v, out;
+  int H;
+  int64_t T;
+  const int32_t* token_idx;
+  const int32_t* row_head;
+  const int32_t* head_map;
+  int64_t N;
+  int local_w, stride, slots;
+  const int32_t* sets;   // (B, plen, K) or null
+  int K;
+  int64_t plen;
+  const int32_t* evict;  // (B, plen) or null
+  const int32_t* row_of; // (B*H, T)
+  const int32_t* summary;
+  float* part;           // (N, kPartW)
+  int32_t* lengths;      // (N) or null
+  float scale_log2;
+};
+
+struct QState {
+  float m, l;
+  f32x4_t acc[4];
+  int cnt;
+};
+
+__device__ __forceinline__ int64_t win_lo(int64_t t, int w) {
+  int64_t wl = t + 1 < w ? t + 1 : w;
+  return t - wl + 1;
+}
+
+__device__ __forceinline__ bool strided_anchor(int64_t t, int64_t p, int s, int slots) {
+  if (s <= 0 || slots <= 0 || p >= t) return false;
+  int64_t d = t - p;
+  return (d % s) == 0 && d / s <= slots;
+}
+
+__device__ __forceinline__ bool zero_anchor(int64_t t, int s, int slots) {
+  if (s <= 0 || slots <= 0) return false;
+  int64_t q = t / s;
+  return slots > q && !((t % s) == 0 && q >= 1);
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); }
+
+// Stage keys kpos[0..63] (valid positions) of one head into Ks / Vt.
+__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
+                                          int64_t ks_t, int64_t vs_t, int64_t key, uint16_t* Ks, uint16_t* Vt) {
+  const int tid = threadIdx.x;
+  const int j = tid >> 2, qd = tid & 3;
+  const uint4* ksrc = reinterpret_cast<const uint4*>(kb + key * ks_t + 16 * qd);
+  const uint4* vsrc = reinterpret_cast<const uint4*>(vb + key * vs_t + 16 * qd);
+  uint4 k0 = ksrc[0], k1 = ksrc[1], v0 = vsrc[0], v1 = vsrc[1];
+  uint4* kd = reinterpret_cast<uint4*>(Ks + j * kLd + 16 * qd);
+  kd[0] = k0;
+  kd[1] = k1;
+  const uint32_t vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    Vt[(16 * qd + 2 * e) * kLd + j] = (uint16_t)(vw[e] & 0xffffu);
+    Vt[(16 * qd + 2 * e + 1) * kLd + j] = (uint16_t)(vw[e] >> 16);
+  }
+}
+
+// One 64-key tile for the 16 query rows of this wave.  mask(kl) decides
+// whether tile key kl (0..63) is a candidate of this lane's query row.
+template <class MaskF>
+__device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_t* Ks, const uint16_t* Vt,
+                                          float scale_log2, MaskF mask, QState& st) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
+  float s[4][4];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc) {
+      bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(Ks + (16 * kb + r16) * kLd + 32 * dc + 8 * g);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[dc], c, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = mask(16 * kb + 4 * g + i);
+      s[kb][i] = ok ? c[i] * scale_log2 : -INFINITY;
+      st.cnt += ok ? 1 : 0;
+      tmax = fmaxf(tmax, s[kb][i]);
+    }
+  }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  const float mn = fmaxf(st.m, tmax);
+  float alpha = 1.f;
+  float psum = 0.f;
+  if (mn != -INFINITY) {
+    alpha = exp2f(st.m - mn);  // st.m == -inf -> 0
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[kb][i] = exp2f(s[kb][i] - mn);  // -inf -> 0
+        psum += s[kb][i];
+      }
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[kb][i] = 0.f;
+  }
+  st.l = st.l * alpha + psum;
+  st.m = mn;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.acc[db][i] *= alpha;
+  // P is split into bf16 hi + lo parts (two MFMAs per V block), so the P.V
+  // product keeps ~16 significant bits of each probability instead of 8.
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    uint16_t ph[8], pl[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a0 = s[2 * kc][i], a1 = s[2 * kc + 1][i];
+      ph[i] = bf16_bits(a0);
+      ph[4 + i] = bf16_bits(a1);
+      pl[i] = bf16_bits(a0 - bf16_to_f32(ph[i]));
+      pl[4 + i] = bf16_bits(a1 - bf16_to_f32(ph[4 + i]));
+    }
+    bf16x8_t pbh, pbl;
+    __builtin_memcpy(&pbh, ph, 16);
+    __builtin_memcpy(&pbl, pl, 16);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint16_t* vr = Vt + (16 * db + r16) * kLd + 32 * kc + 4 * g;
+      uint2 lo8 = *reinterpret_cast<const uint2*>(vr);
+      uint2 hi8 = *reinterpret_cast<const uint2*>(vr + 16);
+      uint32_t w4[4] = {lo8.x, lo8.y, hi8.x, hi8.y};
+      bf16x8_t va;
+      __builtin_memcpy(&va, w4, 16);
+      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pbh, st.acc[db], 0, 0, 0);
+      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pbl, st.acc[db], 0, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[2]) {
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int dc = 0; dc < 2; ++dc) {
+    uint4 w = *reinterpret_cast<const uint4*>(qrow + 32 * dc + 8 * g);
+    __builtin_memcpy(&qf[dc], &w, 16);
+  }
+}
+
+__device__ __forceinline__ void init_state(QState& st) {
+  st.m = -INFINITY;
+  st.l = 0.f;
+  st.cnt = 0;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) st.acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+}
+
+__device__ __forceinline__ int64_t xcd_block(int64_t P, int64_t nblk) {
+  int64_t per = nblk / 8;
+  return (P % 8) * per + P / 8;
+}
+
+// ---------------------------------------------------------------------
+// Pass 1: anchors per (residue class, compact head)
+// ---------------------------------------------------------------------
+__global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
+  __shared__ __align__(16) uint16_t Ks[kTile * kLd];
+  __shared__ __align__(16) uint16_t Vt[64 * kLd];
+  __shared__ int32_t cls_m[kMaxClassRows];
+  __shared__ int32_t cls_r[kMaxClassRows];
+  __shared__ int s_count;
+  __shared__ int wave_cnt[4];
+
+  const int c = blockIdx.x;
+  const int p = blockIdx.y;
+  const int P = a.summary[0];
+  if (p >= P) return;
+  const int s = a.stride;
+  if (c >= s || (int64_t)c >= a.T) return;
+  const int bh = a.head_map ? a.head_map[p] : p;
+  const int64_t bb = bh / a.H, hh = bh % a.H;
+  const int64_t Mmax = (a.T - 1 - c) / s;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+
+  // compact the active rows of this class (ascending M)
+  if (tid == 0) s_count = 0;
+  __syncthreads();
+  for (int64_t base = 0; base <= Mmax; base += 256) {
+    const int64_t M = base + tid;
+    int r = -1;
+    if (M <= Mmax) r = a.row_of[(int64_t)bh * a.T + c + (int64_t)s * M];
+    const bool act = r >= 0;
+    const uint64_t bal = __ballot(act);
+    if (lane == 0) wave_cnt[wid] = __popcll(bal);
+    __syncthreads();
+    int before = s_count;
+    for (int w = 0; w < wid; ++w) before += wave_cnt[w];
+    if (act) {
+      const int pos = before + __popcll(bal & ((1ull << lane) - 1ull));
+      cls_m[pos] = (int32_t)M;
+      cls_r[pos] = r;
+    }
+    __syncthreads();
+    if (tid == 0) s_count += wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+    __syncthreads();
+  }
+  const int nrows = s_count;
+  const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
+  const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
+  const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
+
+  for (int c0 = 0; c0 < nrows; c0 += kRows) {
+    const int qs = 16 * wid + (lane & 15);
+    const bool qv = c0 + qs < nrows;
+    const int64_t Mq = qv ? cls_m[c0 + qs] : 0;
+    const int rq = qv ? cls_r[c0 + qs] : 0;
+    const int64_t tq = c + (int64_t)s * Mq;
+    const int64_t j0 = (tq - win_lo(tq, a.local_w)) / s + 1;
+    const int64_t hi_q = qv ? Mq - j0 : -1;
+    const int64_t lo_q = Mq - a.slots > 0 ? Mq - a.slots : 0;
+    // key range of the chunk (lo/hi are non-decreasing in M)
+    const int last = min(nrows, c0 + kRows) - 1;
+    const int64_t Mf = cls_m[c0], Ml = cls_m[last];
+    const int64_t mlo = Mf - a.slots > 0 ? Mf - a.slots : 0;
+    const int64_t tl = c + (int64_t)s * Ml;
+    const int64_t mhi = Ml - ((tl - win_lo(tl, a.local_w)) / s + 1);
+    bf16x8_t qf[2];
+    load_q(qb + tq * a.q.s_t, qf);
+    QState st;
+    init_state(st);
+    for (int64_t m0 = mlo; m0 <= mhi; m0 += kTile) {
+      const int64_t mk = min(m0 + (tid >> 2), mhi);
+      load_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * mk, Ks, Vt);
+      __syncthreads();
+      tile_step(qf, Ks, Vt, a.scale_log2,
+                [&](int kl) {
+                  const int64_t m = m0 + kl;
+                  return m <= mhi && m >= lo_q && m <= hi_q;
+                },
+                st);
+      __syncthreads();
+    }
+    float lt = st.l;
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    if (qv) {
+      float* pr = a.part + (int64_t)rq * kPartW;
+      const int g = lane >> 4;
+      if (g == 0) { pr[0] = st.m; pr[1] = lt; }
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        *reinterpret_cast<f32x4_t*>(pr + 4 + 16 * db + 4 * g) = st.acc[db];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------
+// Pass 2: window + prototype keys per segment of consecutive rows
+// ---------------------------------------------------------------------
+__global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_part) {
+  __shared__ __align__(16) uint16_t Ks[kTile * kLd];
+  __shared__ __align__(16) uint16_t Vt[64 * kLd];
+  __shared__ int64_t r_t[kRows];
+  __shared__ int32_t r_p[kRows];
+  __shared__ int32_t seg_begin[kRows + 1];
+  __shared__ int s_nseg;
+  __shared__ int32_t plist[kMaxProto + 1];
+  __shared__ int32_t pev[kMaxProto + 1];
+  __shared__ int s_plen;
+
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t r0 = lb * kRows;
+  if (r0 >= a.N) return;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int w = a.local_w;
+  if (tid < kRows) {
+    const int64_t r = r0 + tid;
+    r_t[tid] = r < a.N ? (int64_t)a.token_idx[r] : -1;
+    r_p[tid] = r < a.N ? a.row_head[r] : -1;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int n = 0;
+    int i = 0;
+    while (i < kRows && r_t[i] >= 0) {
+      seg_begin[n++] = i;
+      const int64_t t0 = r_t[i];
+      const int p0 = r_p[i];
+      ++i;
+      while (i < kRows && r_t[i] >= 0 && r_p[i] == p0 && r_t[i] - t0 < w) ++i;
+    }
+    seg_begin[n] = i;
+    s_nseg = n;
+  }
+  __syncthreads();
+  const int nseg = s_nseg;
+  const int qs = 16 * wid + (lane & 15);
+  const int g = lane >> 4;
+
+  for (int sg = 0; sg < nseg; ++sg) {
+    const int s0 = seg_begin[sg], s1 = seg_begin[sg + 1];
+    const int p = r_p[s0];
+    const int bh = a.head_map ? a.head_map[p] : p;
+    const int64_t bb = bh / a.H, hh = bh % a.H;
+    const int64_t t_first = r_t[s0], t_last = r_t[s1 - 1];
+    const int64_t lo_first = win_lo(t_first, w), lo_last = win_lo(t_last, w);
+    const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
+    const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
+    const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
+
+    // prototype key list: prefix set of t_first below lo_last, then key 0
+    if (tid < 64) {
+      int n = 0;
+      if (a.sets != nullptr) {
+        const int64_t prow = t_first < a.plen - 1 ? t_first : a.plen - 1;
+        const int32_t* S = a.sets + (bb * a.plen + prow) * a.K;
+        for (int base = 0; base < a.K; base += 64) {
+          const int j = base + lane;
+          const int32_t v = j < a.K ? S[j] : INT32_MAX;
+          const bool below = j < a.K && v < lo_last;
+          const uint64_t bal = __ballot(below);
+          if (below) {
+            plist[n + j - base] = v;
+            pev[n + j - base] = a.evict[bb * a.plen + v];
+          }
+          n += __popcll(bal);
+          if (bal != ~0ull) break;
+        }
+      }
+      if (lo_last > 0 && a.stride > 0 && a.slots > 0) {
+        // append key 0 for the zero-anchor rule unless the (ascending) list
+        // already starts with it; order inside the list does not matter
+        wave_sync();
+        const int32_t first = n > 0 ? plist[0] : -1;
+        if (first != 0) {
+          if (lane == 0) {
+            plist[n] = 0;
+            pev[n] = -1;  // not in the prototype set: only the zero-anchor rule applies
+          }
+          ++n;
+        }
+      }
+      if (lane == 0) s_plen = n;
+    }
+    __syncthreads();
+    const int plen = s_plen;
+
+    // this lane's query row
+    const bool qv = qs >= s0 && qs < s1;
+    const int64_t tq = qv ? r_t[qs] : t_first;
+    const int64_t loq = win_lo(tq, w);
+    const bool zf = qv && zero_anchor(tq, a.stride, a.slots) && loq > 0;
+    bf16x8_t qf[2];
+    load_q(qb + tq * a.q.s_t, qf);
+    QState st;
+    init_state(st);
+
+    // window tiles [lo_first, t_last]
+    for (int64_t k0 = lo_first; k0 <= t_last; k0 += kTile) {
+      const int64_t key = min(k0 + (tid >> 2), t_last);
+      load_tile(kb, vb, a.k.s_t, a.v.s_t, key, Ks, Vt);
+      __syncthreads();
+      tile_step(qf, Ks, Vt, a.scale_log2,
+                [&](int kl) {
+                  const int64_t kp = k0 + kl;
+                  return qv && kp <= tq && kp >= loq;
+                },
+                st);
+      __syncthreads();
+    }
+    // prototype (and zero-anchor) tiles
+    for (int j0 = 0; j0 < plen; j0 += kTile) {
+      const int jj = min(j0 + (tid >> 2), plen - 1);
+      load_tile(kb, vb, a.k.s_t, a.v.s_t, (int64_t)plist[jj], Ks, Vt);
+      __syncthreads();
+      tile_step(qf, Ks, Vt, a.scale_log2,
+                [&](int kl) {
+                  const int j = j0 + kl;
+                  if (!qv || j >= plen) return false;
+                  const int64_t kp = plist[j];
+                  if (kp >= loq) return false;
+                  const bool in_proto = (int64_t)pev[j] > tq && !strided_anchor(tq, kp, a.stride, a.slots);
+                  return in_proto || (kp == 0 && zf);
+                },
+                st);
+      __syncthreads();
+    }
+
+    // merge the anchor partial, normalise, write
+    float lt = st.l;
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    int ct = st.cnt;
+    ct += __shfl_xor(ct, 16, 64);
+    ct += __shfl_xor(ct, 32, 64);
+    if (qv) {
+      const int64_t r = r0 + qs;
+      float m = st.m;
+      float fa = 1.f, fb = 0.f, lp = 0.f;
+      f32x4_t pacc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      if (use_part) {
+        const float* pr = a.part + r * kPartW;
+        const float ma = pr[0];
+        lp = pr[1];
+#pragma unroll
+        for (int db = 0; db < 4; ++db) pacc[db] = *reinterpret_cast<const f32x4_t*>(pr + 4 + 16 * db + 4 * g);
+        const float mm = fmaxf(m, ma);
+        fa = (m == -INFINITY) ? 0.f : exp2f(m - mm);
+        fb = (ma == -INFINITY) ? 0.f : exp2f(ma - mm);
+      }
+      const float den = lt * fa + lp * fb;
+      const float inv = 1.f / den;
+      uint16_t* op = (uint16_t*)a.out.ptr + bb * a.out.s_b + hh * a.out.s_h + tq * a.out.s_t;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        uint16_t o4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o4[i] = f32_to_bf16((st.acc[db][i] * fa + pacc[db][i] * fb) * inv);
+        *reinterpret_cast<uint2*>(op + 16 * db + 4 * g) =
+            make_uint2((uint32_t)o4[0] | ((uint32_t)o4[1] << 16), (uint32_t)o4[2] | ((uint32_t)o4[3] << 16));
+      }
+      if (a.lengths != nullptr && g == 0) {
+        int64_t na = 0;
+        if (a.stride > 0 && a.slots > 0) {
+          const int64_t M = tq / a.stride;
+          const int64_t j0 = (tq - loq) / a.stride + 1;
+          const int64_t hi = M - j0, lo = M - a.slots > 0 ? M - a.slots : 0;
+          na = hi >= lo ? hi - lo + 1 : 0;
+        }
+        a.lengths[r] = (int32_t)(ct + na);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace pfa
+
+using namespace pfa;
+
+extern "C" int pfa_shortlist_attn_part_floats(void) { return kPartW; }
+
+extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_tensor4 out, int dtype, int H,
+                                      int64_t T, int D, const int32_t* token_idx, const int32_t* row_head,
+                                      const int32_t* head_map, int64_t N, int P_cap, const int32_t* summary,
+                                      const int32_t* row_of, int local_w, int anchor_stride, int anchor_slots,
+                                      const int32_t* proto_sets, int proto_k, int64_t proto_len,
+                                      const int32_t* proto_evict, float scale, float* partials, int32_t* lengths,
+                                      void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(dtype == PFA_BF16 && D == 64, "pfa_shortlist_attn_fwd: bf16 and D=64 only (got dtype %d D %d)", dtype,
+                D);
+  PFA_CHECK_ARG(H > 0 && T > 0 && N >= 0 && P_cap > 0 && local_w >= 1, "pfa_shortlist_attn_fwd: bad sizes");
+  if (N == 0) return PFA_OK;
+  PFA_CHECK_ARG(q.ptr && k.ptr && v.ptr && out.ptr && token_idx && row_head && summary,
+                "pfa_shortlist_attn_fwd: null pointer");
+  PFA_CHECK_ARG(proto_sets == nullptr || (proto_k > 0 && proto_k <= kMaxProto && proto_evict && proto_len > 0),
+                "pfa_shortlist_attn_fwd: prototype table (K <= %d with evict) required", kMaxProto);
+  const bool anchors = anchor_stride > 0 && anchor_slots > 0;
+  PFA_CHECK_ARG(!anchors || (row_of && partials), "pfa_shortlist_attn_fwd: anchors need row_of and partials");
+  PFA_CHECK_ARG(!anchors || (T - 1) / anchor_stride + 1 <= kMaxClassRows,
+                "pfa_shortlist_attn_fwd: T/stride exceeds %d", kMaxClassRows);
+  auto al = [](const pfa_tensor4& x) {
+    return ((uintptr_t)x.ptr % 16) == 0 && x.s_b % 8 == 0 && x.s_h % 8 == 0 && x.s_t % 8 == 0;
+  };
+  PFA_CHECK_ARG(al(q) && al(k) && al(v) && al(out), "pfa_shortlist_attn_fwd: tensors must be 16-byte aligned");
+  ShortArgs a;
+  a.q = q; a.k = k; a.v = v; a.out = out;
+  a.H = H; a.T = T; a.token_idx = token_idx; a.row_head = row_head; a.head_map = head_map; a.N = N;
+  a.local_w = local_w; a.stride = anchor_stride; a.slots = anchor_slots;
+  a.sets = proto_sets; a.K = proto_k; a.plen = proto_len; a.evict = proto_evict;
+  a.row_of = row_of; a.summary = summary; a.part = partials; a.lengths = lengths;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t s = as_stream(stream);
+  if (anchors) {
+    dim3 grid((unsigned)((int64_t)anchor_stride < T ? (int64_t)anchor_stride : T), (unsigned)P_cap);
+    short_anchor_kernel<<<grid, 256, 0, s>>>(a);
+    PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
+  }
+  int64_t blocks = (N + kRows - 1) / kRows;
+  blocks = (blocks + 7) / 8 * 8;
+  PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_shortlist_attn_fwd: too many rows");
+  short_main_kernel<<<(unsigned)blocks, 256, 0, s>>>(a, anchors ? 1 : 0);
+  PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/main");
+  return PFA_OK;
+}

@@ -71,9 +71,11 @@ __device__ __forceinline__ void wave_bitonic_best_first(float& v, int& i) {
 
 __global__ void __launch_bounds__(64)
 prefix_block_sort(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int K,
-                  float* __restrict__ oval, int32_t* __restrict__ oidx, int32_t* __restrict__ olen) {
+                  float* __restrict__ oval, int32_t* __restrict__ oidx, int32_t* __restrict__ olen,
+                  int32_t* __restrict__ evict) {
   const int j = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   int64_t t = (int64_t)j * kBlk + lane;
+  if (evict != nullptr && t < T) evict[(int64_t)b * T + t] = INT32_MAX;
   float v = -INFINITY;
   int i = INT32_MAX;
   if (t < T) { v = scores[(int64_t)b * stride + t]; i = (int)t; }
@@ -153,7 +155,7 @@ __device__ void lds_sort_by_index(float* v, int32_t* ix, int cap) {
 __global__ void __launch_bounds__(64)
 prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int K, int cap,
                   const float* __restrict__ pval, const int32_t* __restrict__ pidx, const int32_t* __restrict__ plen,
-                  int32_t* __restrict__ sets) {
+                  int32_t* __restrict__ sets, int32_t* __restrict__ evict) {
   extern __shared__ char smem[];
   float* v = (float*)smem;
   int32_t* ix = (int32_t*)(v + cap);
@@ -195,8 +197,10 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
         else take = better(wv, wi, ov, oi);
         if (take) { wv = ov; wi = oi; wp = op; }
       }
-      if (better(s, (int)t, wv, wi)) {
-        // remove position wp (shift left), append t at n-1
+      if (!better(s, (int)t, wv, wi)) {
+        if (evict != nullptr && lane == 0) evict[(int64_t)b * T + t] = (int32_t)t;  // never enters
+      } else {
+        if (evict != nullptr && lane == 0) evict[(int64_t)b * T + wi] = (int32_t)t;  // wi leaves at t
         float tv[4];
         int ti[4];
         int cnt = 0;
@@ -423,7 +427,8 @@ extern "C" int pfa_proto_prefix_workspace_size(int B, int64_t T, int K, size_t* 
 }
 
 extern "C" int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T, int64_t score_stride, int K,
-                                     int32_t* sets_out, void* workspace, size_t ws_bytes, void* stream) {
+                                     int32_t* sets_out, int32_t* evict_out, void* workspace, size_t ws_bytes,
+                                     void* stream) {
   clear_error();
   PFA_CHECK_ARG(proto_scores && sets_out && workspace && B > 0 && T > 0 && K > 0 && K <= 4096,
                 "pfa_proto_prefix_topk: bad arguments (B=%d T=%lld K=%d)", B, (long long)T, K);
@@ -437,7 +442,8 @@ extern "C" int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T
   PrefixWs w = carve_prefix(workspace, B, nb, K);
   hipStream_t s = as_stream(stream);
   dim3 grid((unsigned)nb, (unsigned)B);
-  prefix_block_sort<<<grid, 64, 0, s>>>(proto_scores, T, score_stride, (int)nb, K, w.val[0], w.idx[0], w.len[0]);
+  prefix_block_sort<<<grid, 64, 0, s>>>(proto_scores, T, score_stride, (int)nb, K, w.val[0], w.idx[0], w.len[0],
+                                             evict_out);
   PFA_CHECK_LAUNCH("pfa_proto_prefix_topk/sort");
   int cur = 0;
   for (int64_t d = 1; d < nb; d <<= 1) {
@@ -451,7 +457,7 @@ extern "C" int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T
   size_t lds = (size_t)cap * 8;
   PFA_CHECK_ARG(lds <= 160 * 1024, "pfa_proto_prefix_topk: K=%d too large for LDS", K);
   prefix_block_walk<<<grid, 64, lds, s>>>(proto_scores, T, score_stride, (int)nb, K, cap, w.val[cur], w.idx[cur],
-                                          w.len[cur], sets_out);
+                                          w.len[cur], sets_out, evict_out);
   PFA_CHECK_LAUNCH("pfa_proto_prefix_topk/walk");
   return PFA_OK;
 }

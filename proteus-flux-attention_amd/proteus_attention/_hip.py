@@ -27,7 +27,10 @@ _DTYPE_TAG = {
 EXPORTED_SYMBOLS = (
     "pfa_version",
     "pfa_last_error_string",
+    "pfa_router_gate_pad",
+    "pfa_router_block_count",
     "pfa_router_topk",
+    "pfa_proto_ema_update",
     "pfa_proto_partial_count",
     "pfa_proto_accumulate",
     "pfa_proto_partial_reduce",
@@ -39,6 +42,8 @@ EXPORTED_SYMBOLS = (
     "pfa_proto_prefix_topk",
     "pfa_shortlist_build",
     "pfa_sparse_attn_fwd",
+    "pfa_shortlist_attn_part_floats",
+    "pfa_shortlist_attn_fwd",
     "pfa_head_max_token",
     "pfa_rope_qk_inplace",
     "pfa_zero_fill",
@@ -71,21 +76,27 @@ _sz = ctypes.c_size_t
 _SIGNATURES = {
     "pfa_version": ([], _i32),
     "pfa_last_error_string": ([], ctypes.c_char_p),
-    "pfa_router_topk": ([_vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32,
-                         _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "pfa_router_gate_pad": ([_i32], _i32),
+    "pfa_router_block_count": ([_i64, ctypes.POINTER(_i32)], _i32),
+    "pfa_router_topk": ([_vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _i32,
+                         _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "pfa_proto_ema_update": ([_vp, _i32, _i32, _f32, _vp, _vp, _vp, _i32, _vp], _i32),
     "pfa_proto_partial_count": ([_i64, ctypes.POINTER(_i32)], _i32),
     "pfa_proto_accumulate": ([_vp, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _vp], _i32),
     "pfa_proto_partial_reduce": ([_vp, _i32, _i32, _i32, _vp, _vp], _i32),
     "pfa_token_topk": ([_vp, _i32, _i64, _i64, _i32, _f32, _vp, _vp], _i32),
     "pfa_pack_workspace_size": ([_i32, _i32, _i64, ctypes.POINTER(_sz)], _i32),
-    "pfa_pack_rows": ([_vp, _i32, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
+    "pfa_pack_rows": ([_vp, _i32, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_pack_mask": ([_vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_proto_prefix_workspace_size": ([_i32, _i64, _i32, ctypes.POINTER(_sz)], _i32),
-    "pfa_proto_prefix_topk": ([_vp, _i32, _i64, _i64, _i32, _vp, _vp, _sz, _vp], _i32),
+    "pfa_proto_prefix_topk": ([_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_shortlist_build": ([_vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i64, _vp, _vp, _i32,
                              _vp, _i32, _vp, _i32, _vp], _i32),
     "pfa_sparse_attn_fwd": ([Tensor4, Tensor4, Tensor4, _i32, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp,
                              _i64, _vp, _i64, _vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp], _i32),
+    "pfa_shortlist_attn_part_floats": ([], _i32),
+    "pfa_shortlist_attn_fwd": ([Tensor4, Tensor4, Tensor4, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp, _i64,
+                                _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i64, _vp, _f32, _vp, _vp, _vp], _i32),
     "pfa_head_max_token": ([_vp, _vp, _i32, _vp, _vp], _i32),
     "pfa_rope_qk_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
     "pfa_zero_fill": ([_vp, _sz, _vp], _i32),

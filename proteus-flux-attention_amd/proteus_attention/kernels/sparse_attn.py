@@ -117,10 +117,11 @@ def _pack_active_rows(
 # shortlist candidates
 # ---------------------------------------------------------------------------
 
-def _proto_prefix_sets(scores: torch.Tensor, K: int) -> torch.Tensor:
+def _proto_prefix_sets(scores: torch.Tensor, K: int, with_evict: bool = False):
     """Per (batch, token) the top-min(t+1, K) score positions <= t, sorted.
 
-    scores: (B, T_s) f32 on the device.  Returns (B, T_s, K) int32.
+    scores: (B, T_s) f32 on the device.  Returns (B, T_s, K) int32, and with
+    ``with_evict`` also the (B, T_s) int32 eviction tokens.
     """
 
     lib = _hip.lib()
@@ -129,11 +130,12 @@ def _proto_prefix_sets(scores: torch.Tensor, K: int) -> torch.Tensor:
     B, Ts = scores.shape
     ws = _workspace(_size_out(lib.pfa_proto_prefix_workspace_size, B, Ts, K), device)
     sets = torch.empty(B, Ts, K, dtype=torch.int32, device=device)
+    evict = torch.empty(B, Ts, dtype=torch.int32, device=device) if with_evict else None
     with _hip.TIMER.timed("proto_prefix_topk"):
-        rc = lib.pfa_proto_prefix_topk(_hip.ptr(scores), B, Ts, scores.stride(0), K, _hip.ptr(sets), _hip.ptr(ws),
-                                       ws.numel(), _hip.stream_ptr(device))
+        rc = lib.pfa_proto_prefix_topk(_hip.ptr(scores), B, Ts, scores.stride(0), K, _hip.ptr(sets), _hip.ptr(evict),
+                                       _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device))
     _hip.check(rc, "pfa_proto_prefix_topk")
-    return sets
+    return (sets, evict) if with_evict else sets
 
 
 def _resolve_caps(max_candidates, linear_window, anchor_stride, use_local, use_anchors, has_proto, seq_len,
@@ -339,6 +341,49 @@ def _attn_launch(
         _hip.ptr(head_max), float(scale), _hip.ptr(scales[0]), _hip.ptr(scales[1]), _hip.ptr(scales[2]),
         _hip.stream_ptr(device))
     _hip.check(rc, "pfa_sparse_attn_fwd")
+
+
+def _shortlist_attn_structured(
+    q4: "_hip.Tensor4",
+    k4: "_hip.Tensor4",
+    v4: "_hip.Tensor4",
+    out4: "_hip.Tensor4",
+    H: int,
+    T: int,
+    D: int,
+    token_idx: torch.Tensor,
+    row_head: torch.Tensor,
+    head_map: torch.Tensor,
+    summary: torch.Tensor,
+    row_of: torch.Tensor,
+    local_w: int,
+    stride: int,
+    slots: int,
+    sets: Optional[torch.Tensor],
+    evict: Optional[torch.Tensor],
+    scale: float,
+    device: torch.device,
+) -> torch.Tensor:
+    """Module-path shortlist attention without materialised candidates
+    (bf16, D=64).  Returns each row's candidate count (int32, (N,))."""
+
+    lib = _hip.lib()
+    N = int(token_idx.numel())
+    lengths = torch.empty(N, dtype=torch.int32, device=device)
+    anchors = stride > 0 and slots > 0
+    part = None
+    if anchors:
+        part = torch.empty(N, int(lib.pfa_shortlist_attn_part_floats()), dtype=torch.float32, device=device)
+    K = int(sets.size(2)) if sets is not None else 0
+    plen = int(sets.size(1)) if sets is not None else 0
+    with _hip.TIMER.timed("shortlist_attn_fwd"):
+        rc = lib.pfa_shortlist_attn_fwd(
+            q4, k4, v4, out4, _hip.PFA_BF16, int(H), int(T), int(D), _hip.ptr(token_idx), _hip.ptr(row_head),
+            _hip.ptr(head_map), N, int(head_map.numel()), _hip.ptr(summary), _hip.ptr(row_of), int(local_w),
+            int(stride), int(slots), _hip.ptr(sets), K, plen, _hip.ptr(evict), float(scale), _hip.ptr(part),
+            _hip.ptr(lengths), _hip.stream_ptr(device))
+    _hip.check(rc, "pfa_shortlist_attn_fwd")
+    return lengths
 
 
 def aspa_sparse_attention(

@@ -153,6 +153,20 @@ class SwitchRouter(nn.Module):
         return indices, scores, probs
 
 
+def pack_router_weights(w_router: torch.Tensor, proto_norm: Optional[torch.Tensor], x_dtype: torch.dtype) -> torch.Tensor:
+    """(C, 2*Gp) f32 channel-interleaved router weights for pfa_router_topk:
+    column g holds the router weight of gate g at its ``x_dtype`` value,
+    column Gp+g the normalised prototype; padding gates are zero."""
+
+    G, C = w_router.shape
+    Gp = int(_hip.lib().pfa_router_gate_pad(G))
+    packed = torch.zeros(C, 2 * Gp, dtype=torch.float32, device=w_router.device)
+    packed[:, :G] = w_router.detach().to(x_dtype).to(torch.float32).t()
+    if proto_norm is not None:
+        packed[:, Gp:Gp + G] = proto_norm.detach().to(torch.float32).t()
+    return packed
+
+
 def _flag(value: Any) -> bool:
     return bool(value)
 
@@ -687,25 +701,27 @@ class AdaptiveSparseAttention(nn.Module):
         device = x2d.device
         n_tok, C = x2d.shape
         G, H = self.attn_gates, self.h_total
-        w = self.head_router.linear.weight
-        if w.dtype != x2d.dtype:
-            w = w.to(x2d.dtype)
-        w = w.contiguous()
         pn, conf, usage = self._proto_inputs(device)
+        wpk = pack_router_weights(self.head_router.linear.weight, pn, x2d.dtype)
         gate = torch.empty(n_tok, G, dtype=torch.float32, device=device)
         imp = torch.empty(n_tok, dtype=torch.float32, device=device)
         sim = torch.empty(n_tok, dtype=torch.float32, device=device) if pn is not None else None
         blend = torch.empty(n_tok, dtype=torch.float32, device=device) if pn is not None else None
         hidx = torch.empty(n_tok, topk, dtype=torch.int32, device=device)
         hsc = torch.empty(n_tok, topk, dtype=torch.float32, device=device) if need_head_scores else None
+        nblk = _hip.ctypes.c_int(0)
+        _hip.check(lib.pfa_router_block_count(n_tok, _hip.ctypes.byref(nblk)), "pfa_router_block_count")
+        stats = torch.empty(max(1, nblk.value), 8, dtype=torch.float32, device=device)
         g2h = self.gate_to_head.to(device=device, dtype=torch.int32).contiguous()
         with _hip.TIMER.timed("router_topk"):
             rc = lib.pfa_router_topk(
-            _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(w), _hip.ptr(pn), _hip.ptr(conf),
+            _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(wpk), 1 if pn is not None else 0,
+            _hip.ptr(conf),
             _hip.ptr(usage), _hip.ptr(g2h), H, topk, float(self.proto_temp), float(self.proto_threshold),
             float(self.proto_blend), float(self.proto_usage_boost), _hip.ptr(gate), _hip.ptr(sim), _hip.ptr(blend),
-            _hip.ptr(imp), _hip.ptr(hidx), _hip.ptr(hsc), _hip.stream_ptr(device))
+            _hip.ptr(imp), _hip.ptr(hidx), _hip.ptr(hsc), _hip.ptr(stats), _hip.stream_ptr(device))
         _hip.check(rc, "pfa_router_topk")
+        self._router_stats = stats
         return gate, sim, blend, imp, hidx, hsc
 
     def _select_active_tokens(self, importance: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
@@ -761,23 +777,14 @@ class AdaptiveSparseAttention(nn.Module):
             sums = torch.empty(G, C + 1, dtype=torch.float32, device=device)
             _hip.check(lib.pfa_proto_partial_reduce(_hip.ptr(partial), nparts.value, G, C, _hip.ptr(sums),
                                                     _hip.stream_ptr(device)), "pfa_proto_partial_reduce")
-            weighted, counts = sums[:, :C], sums[:, C]
-            mask = counts > 1e-6
-            maskf = mask.to(torch.float32).unsqueeze(-1)
-            mean = torch.where(mask.unsqueeze(-1), weighted / counts.clamp_min(1e-30).unsqueeze(-1),
-                               torch.zeros_like(weighted))
-            decay = self.proto_decay
-            proto = self.routing_prototypes
-            new_proto = proto * decay + mean.to(proto.dtype) * (1.0 - decay)
-            proto.copy_(torch.where(mask.unsqueeze(-1), new_proto, proto))
-            usage = self.routing_usage_ema
-            usage.mul_(decay)
-            usage.add_(torch.where(mask, counts * (1.0 - decay), torch.zeros_like(counts)).to(usage.dtype))
-            conf = self.routing_confidence
-            conf.mul_(decay)
-            conf.add_((maskf.squeeze(-1) * (1.0 - decay)).to(conf.dtype))
-            self._proto_update_mask = mask
-            del maskf
+            proto, usage, conf = self.routing_prototypes, self.routing_usage_ema, self.routing_confidence
+            if not (proto.dtype == usage.dtype == conf.dtype and proto.is_contiguous()):
+                raise ValueError("routing_prototypes / routing_usage_ema / routing_confidence must share one "
+                                 "dtype and be contiguous")
+            _hip.check(lib.pfa_proto_ema_update(_hip.ptr(sums), G, C, float(self.proto_decay), _hip.ptr(proto),
+                                                _hip.ptr(usage), _hip.ptr(conf), _hip.dtype_tag(proto.dtype),
+                                                _hip.stream_ptr(device)), "pfa_proto_ema_update")
+            self._proto_sums = sums
 
     # ------------------------------------------------------------------
     def _full_rows(self, B: int, T: int, device: torch.device):
@@ -941,19 +948,30 @@ class AdaptiveSparseAttention(nn.Module):
         row_offsets = torch.empty(BH + 1, dtype=torch.int32, device=device)
         token_idx = torch.empty(BH * T, dtype=torch.int32, device=device)
         row_head = torch.empty(BH * T, dtype=torch.int32, device=device)
+        row_of = torch.empty(BH, T, dtype=torch.int32, device=device)
         summary = torch.empty(4, dtype=torch.int32, device=device)
         ws = _sa._workspace(_sa._size_out(lib.pfa_pack_workspace_size, B, H, T), device)
         tm8 = token_mask.view(torch.uint8) if token_mask is not None else None
         with _hip.TIMER.timed("pack_rows"):
             rc = lib.pfa_pack_rows(_hip.ptr(hidx), topk, _hip.ptr(tm8), B, H, T, _hip.ptr(mask8), _hip.ptr(active_heads),
-                               _hip.ptr(row_offsets), _hip.ptr(token_idx), _hip.ptr(row_head), _hip.ptr(summary),
+                               _hip.ptr(row_offsets), _hip.ptr(token_idx), _hip.ptr(row_head), _hip.ptr(row_of),
+                               _hip.ptr(summary),
                                _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device))
         _hip.check(rc, "pfa_pack_rows")
-        summ = summary.cpu()
-        P, N, max_rows = int(summ[0]), int(summ[1]), int(summ[2])
-        density_est = float(max_rows) / float(max(1, T))
-        self._update_density(density_est)
         density_threshold = self._density_threshold()
+        # The host needs the packing summary only to decide force-dense by
+        # density / fullness or when a token mask makes the row count data
+        # dependent; otherwise every token has exactly `topk` active rows and
+        # the summary is read back with the telemetry at the end (no stall
+        # between the router and the attention launches).
+        need_summary = (density_threshold is not None or self.force_dense_when_full or token_mask is not None)
+        if need_summary:
+            summ = summary.cpu()
+            P, N, max_rows = int(summ[0]), int(summ[1]), int(summ[2])
+        else:
+            P, N, max_rows = -1, B * T * topk, -1
+        self._pending_summary = None if need_summary else summary
+        density_est = float(max_rows) / float(max(1, T)) if max_rows >= 0 else 0.0
         all_rows_active = N == BH * T
         prefer_dense = alpha <= self.dense_alpha_cutoff and not self.quantize_sparse_int8
         force_dense, dense_reason = False, None
@@ -980,10 +998,8 @@ class AdaptiveSparseAttention(nn.Module):
             self._attend_dense_causal(qkv, B, T, attn)
             if dense_reason == "alpha":
                 mode_label = "dense_alpha"
-            elif P == BH:
-                mode_label = "dense"
             else:
-                mode_label = "dense_auto"
+                mode_label = "dense_auto"  # refined to "dense" once P is read back
             _record_backend("hip_dense", device=str(device), heads=BH, tokens=T, max_rows=T, quantized=False)
             self._last_sparse_state = {
                 "mode": mode_label, "backend": get_last_backend(), "max_rows": max_rows, "density": density_est,
@@ -993,7 +1009,7 @@ class AdaptiveSparseAttention(nn.Module):
                 "mode_selected": f"cvt(alpha={alpha:.2f})", "shortlist_alpha": float(alpha),
                 "dense_reason": dense_reason,
             }
-        elif P == 0 or N == 0:
+        elif P == 0 or N == 0 or (not need_summary and B * T == 0):
             dense_reason = None
             self._cached_active_mask = None
             self._cached_packing = None
@@ -1010,13 +1026,13 @@ class AdaptiveSparseAttention(nn.Module):
             mode_label = "shortlist"
             tok = token_idx[:N]
             rh = row_head[:N]
-            heads = active_heads[:P]
-            self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets[:P + 1], alpha)
+            heads = active_heads[:P] if P >= 0 else active_heads
+            self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets, alpha, row_of, summary)
             backend_info = self._last_shortlist_backend_info or get_last_backend_info()
             state = {
                 "mode": mode_label, "backend": str(backend_info.get("name", "shortlist")),
-                "active_head_indices": heads.to(torch.int64), "head_idx": rh, "token_idx": tok,
-                "row_offsets": row_offsets[:P + 1], "max_rows": int(max_rows), "density": density_est,
+                "active_head_indices": heads, "head_idx": rh, "token_idx": tok,
+                "row_offsets": row_offsets, "max_rows": int(max_rows), "density": density_est,
                 "target_k": int(topk),
                 "force_dense_threshold": None if density_threshold is None else float(density_threshold),
                 "cache_hit": False, "quantized": bool(self.quantize_sparse_int8 and not self.training),
@@ -1036,8 +1052,8 @@ class AdaptiveSparseAttention(nn.Module):
         self.last_head_consensus = None if self.training else attn.detach()
         y = self.dropout(self.proj(attn))
 
-        self._finish_stats(gate_probs, hsc, hidx, token_mask, topk, adaptive_topk, max_rows, density_est,
-                           density_threshold, alpha, mode_label, dense_reason, N, B, T)
+        self._finish_stats(token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
+                           dense_reason, B, T, active_heads, row_offsets, summary)
         self.last_router_reg = router_reg
         self._update_routing_prototypes(x, gate_probs)
         finish(f"cvt(alpha={alpha:.2f})::{mode_label}")
@@ -1049,28 +1065,55 @@ class AdaptiveSparseAttention(nn.Module):
                 self.adjust_linear_L_scale(self.linear_latency_growth)
         return y
 
-    def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha) -> None:
-        """Candidate build + candidate attention (aspa.py:1175-1310)."""
+    def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha, row_of,
+                              summary) -> None:
+        """Candidate attention (aspa.py:1175-1310).
+
+        When no row can be truncated to L, bf16 with D=64 and no int8 path,
+        the candidate sets are used through their structure (window, strided
+        anchors, prototype prefix sets) by pfa_shortlist_attn_fwd; otherwise
+        the candidates are materialised (pfa_shortlist_build) and attended by
+        pfa_sparse_attn_fwd.  Both give the reference's candidate sets."""
         H, D = self.h_total, self.d_head
         device = qkv.device
         runtime = self._prepare_linear_runtime(T, B, alpha)
         L = int(runtime["effective_L"])
+        stride = int(runtime["anchor_stride"])
         local_w, slots, proto_cap_val = _sa._resolve_caps(
-            L, runtime["window"], runtime["anchor_stride"], self.linear_use_local, self.linear_use_anchors,
+            L, runtime["window"], stride, self.linear_use_local, self.linear_use_anchors,
             self.linear_use_proto and self._last_token_similarity is not None, T, runtime["local_cap"],
             runtime["anchor_cap"], runtime["proto_cap"])
-        sets = None
-        row_batch = None
+        K = 0
         if self.linear_use_proto and self._last_token_similarity is not None and proto_cap_val > 0:
             K = min(L, proto_cap_val, T)
-            if K > 0:
-                sets = _sa._proto_prefix_sets(self._last_token_similarity, K)
-                row_batch = (heads.index_select(0, row_head) // H).to(torch.int32) if B > 1 else None
-        cand, lens = _sa._shortlist_build_device(token_idx, row_batch, T, L, local_w, runtime["anchor_stride"], slots,
-                                                 sets)
-        self._last_shortlist_lengths = lens
         use_quant = bool(self.quantize_sparse_int8 and not self.training)
+        anchors = stride > 0 and slots > 0
+        w_eff = max(1, local_w)
+        bound = w_eff + ((min(slots, (T - 1) // stride) + 1) if anchors else 0) + K
+        structured = (qkv.dtype == torch.bfloat16 and D == 64 and not use_quant and bound <= L and K <= 1024
+                      and (not anchors or (T - 1) // stride + 1 <= 4096) and not _hip.env_flag("PFA_FORCE_GENERIC"))
         q5 = qkv.view(B, T, 3, H, D)
+        if structured:
+            sets = evict = None
+            if K > 0:
+                sets, evict = _sa._proto_prefix_sets(self._last_token_similarity, K, with_evict=True)
+            lens = _sa._shortlist_attn_structured(
+                _hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
+                _hip.tensor4(q5[:, :, 2], H, "bthd"), _hip.tensor4(attn.view(B, T, H, D), H, "bthd"), H, T, D,
+                token_idx, row_head, heads, summary, row_of, w_eff, stride, slots, sets, evict,
+                1.0 / math.sqrt(D), device)
+            self._last_shortlist_lengths = lens
+            _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
+                            quantized=False, candidates=True, structured=True)
+            self._last_shortlist_backend_info = get_last_backend_info()
+            return
+        sets = None
+        row_batch = None
+        if K > 0:
+            sets = _sa._proto_prefix_sets(self._last_token_similarity, K)
+            row_batch = (heads.index_select(0, row_head) // H).to(torch.int32) if B > 1 else None
+        cand, lens = _sa._shortlist_build_device(token_idx, row_batch, T, L, local_w, stride, slots, sets)
+        self._last_shortlist_lengths = lens
         out4 = _hip.tensor4(attn.view(B, T, H, D), H, "bthd")
         if use_quant:
             # Per-head int8 of the active heads (aspa.py:1258-1267): the
@@ -1093,8 +1136,8 @@ class AdaptiveSparseAttention(nn.Module):
             _sa._attn_launch(_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
                              _hip.tensor4(q5[:, :, 2], H, "bthd"), qkv.dtype, out4, qkv.dtype, H, T, D, token_idx,
                              row_head, heads, cand, lens, None, None, 1.0 / math.sqrt(D), (None, None, None), device)
-        _record_backend("hip", device=str(device), heads=int(heads.numel()), tokens=T,
-                        rows=int(token_idx.numel()), L=L, quantized=use_quant, candidates=True)
+        _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
+                        quantized=use_quant, candidates=True, structured=False)
         self._last_shortlist_backend_info = get_last_backend_info()
 
     def _router_regulariser(self, gate_probs: torch.Tensor) -> Optional[torch.Tensor]:
@@ -1115,37 +1158,39 @@ class AdaptiveSparseAttention(nn.Module):
             total = total + t
         return self.router_reg_lambda * total
 
-    def _finish_stats(self, gate_probs, head_scores, head_idx, token_mask, topk, adaptive_topk, max_rows, density_est,
-                      density_threshold, alpha, mode_label, dense_reason, N, B, T) -> None:
-        """Telemetry dictionaries (aspa.py:1857-1916) with one host readback."""
+    def _finish_stats(self, token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
+                      dense_reason, B, T, active_heads, row_offsets, summary) -> None:
+        """Telemetry dictionaries (aspa.py:1857-1916) from the router's
+        per-workgroup partials and the packing summary: one host readback."""
         H = self.h_total
         with torch.no_grad():
-            gp = gate_probs.float()
-            entropy = -(gp.clamp_min(1e-9).log() * gp).sum(dim=-1).mean()
-            # numerator over every token's top-k scores, denominator over
-            # the active (token-masked) entries, as aspa.py:1860-1866
-            keep_frac = (token_mask.to(torch.float32).mean() if token_mask is not None
-                         else torch.ones((), device=gp.device))
-            score_sum = head_scores.sum() if head_scores is not None else torch.zeros((), device=gp.device)
-            sel = torch.zeros(H, device=gp.device, dtype=torch.float32)
-            sel.index_add_(0, head_idx.view(-1).to(torch.int64),
-                           (token_mask.view(-1, 1).expand(-1, topk).reshape(-1).to(torch.float32)
-                            if token_mask is not None else torch.ones(head_idx.numel(), device=gp.device)))
-            extras = [entropy, keep_frac, score_sum, (sel > 0).sum().to(torch.float32)]
-            if self._last_token_similarity is not None:
-                extras += [self._last_token_similarity.mean(), self._last_token_blend.mean(),
-                           (self._last_token_blend > 0).sum().to(torch.float32)]
-            vals = torch.stack([e.to(torch.float32) for e in extras]).cpu().tolist()
-        entropy_v, keep_v, score_v, uniq_v = vals[0], vals[1], vals[2], vals[3]
-        denom = max(1.0, float(N))
-        if self._last_sparse_state is not None:
-            self._last_sparse_state["token_keep_fraction"] = float(keep_v)
+            part = self._router_stats.sum(dim=0, dtype=torch.float64)
+            vals = torch.cat([part[:5], summary.to(torch.float64), active_heads.to(torch.float64)]).cpu().tolist()
+        ent_sum, sim_sum, blend_sum, blend_pos, score_sum = vals[:5]
+        P, N, max_rows = int(vals[5]), int(vals[6]), int(vals[7])
+        heads_list = [int(v) for v in vals[9:9 + P]]
+        n_tok = max(1, B * T)
+        density_est = float(max_rows) / float(max(1, T))
+        self._update_density(density_est)
+        keep_frac = float(N) / float(max(1, topk * B * T)) if token_mask is not None else 1.0
+        if mode_label == "dense_auto" and P == B * H:
+            mode_label = "dense"
+        st = self._last_sparse_state
+        if st is not None:
+            st["token_keep_fraction"] = keep_frac
+            st["max_rows"] = int(max_rows)
+            st["density"] = density_est
+            if st.get("mode") == "dense_auto" and mode_label == "dense":
+                st["mode"] = "dense"
+            if "active_head_indices" in st:
+                st["active_head_indices"] = st["active_head_indices"][:P].to(torch.int64)
+                st["row_offsets"] = st["row_offsets"][:P + 1]
         self.last_head_stats = {
             "top_k": int(topk),
-            "mean_gate_prob": float(score_v / denom),
-            "router_entropy": float(entropy_v),
-            "mean_active_per_token": float(N) / float(max(1, B * T)),
-            "unique_heads": int(uniq_v),
+            "mean_gate_prob": float(score_sum / max(1.0, float(N))),
+            "router_entropy": float(ent_sum / n_tok),
+            "mean_active_per_token": float(N) / float(n_tok),
+            "unique_heads": len({hb % H for hb in heads_list}),
             "active_fraction": float(N) / float(max(1, B * T * H)),
             "max_active_rows": int(max_rows),
             "max_active_density": float(density_est),
@@ -1155,7 +1200,7 @@ class AdaptiveSparseAttention(nn.Module):
             "active_max": int(self.h_active_max),
             "force_dense_threshold": None if density_threshold is None else float(density_threshold),
             "active_curve": float(self.h_active_curve),
-            "token_keep_fraction": float(keep_v),
+            "token_keep_fraction": keep_frac,
             "mode": mode_label,
             "mode_selected": f"cvt(alpha={alpha:.2f})",
             "shortlist_alpha": float(alpha),
@@ -1176,9 +1221,9 @@ class AdaptiveSparseAttention(nn.Module):
                 if isinstance(det, dict):
                     for key, val in det.items():
                         self.last_head_stats[f"linear_shortlist_{key}"] = val
-        if len(vals) > 4:
-            self._last_proto_stats = {"max_sim_mean": float(vals[4]), "blend_mean": float(vals[5]),
-                                      "active_tokens": int(vals[6])}
+        if self._last_token_similarity is not None:
+            self._last_proto_stats = {"max_sim_mean": float(sim_sum / n_tok), "blend_mean": float(blend_sum / n_tok),
+                                      "active_tokens": int(blend_pos)}
             self.last_head_stats["proto"] = dict(self._last_proto_stats)
             self.last_head_stats["dna"] = dict(self._last_proto_stats)
 

@@ -148,6 +148,59 @@ def test_proto_prefix_sets_vs_brute_force(dev):
             assert torch.equal(sets[b].long(), exp), (T, K, b)
 
 
+def test_proto_evict_matches_prefix_sets(dev):
+    """p is in the prefix top-K set of t  <=>  p <= t < evict[p]."""
+    from proteus_attention.kernels import sparse_attn as sa
+
+    g = torch.Generator().manual_seed(18)
+    for T, K in ((400, 9), (257, 64), (130, 200)):
+        s = torch.randint(0, 7, (2, T), generator=g).float()
+        sets, ev = sa._proto_prefix_sets(s.to(dev), K, with_evict=True)
+        ev = ev.cpu().long()
+        for b in range(2):
+            exp = O.proto_prefix_sets(s[b], K)
+            member = torch.zeros(T, T, dtype=torch.bool)
+            for t in range(T):
+                member[t, exp[t, : min(t + 1, K)]] = True
+            pos = torch.arange(T)
+            by_evict = (pos[None, :] <= pos[:, None]) & (ev[b][None, :] > pos[:, None])
+            assert torch.equal(member, by_evict), (T, K, b)
+
+
+@pytest.mark.parametrize("T,L,w,s,B,outlier", [(4096, 1024, 256, 64, 1, 0.01), (3000, 700, 100, 37, 2, 0.0),
+                                               (65536, 2048, 512, 256, 1, 0.01)])
+def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, monkeypatch):
+    """The structure-driven MFMA path and the builder + gather path give the
+    same candidate counts per row and the same outputs (bf16 tolerance)."""
+    from configs import shortlist_cfg
+
+    _say(f"structured vs materialised T={T} L={L} w={w} s={s} B={B}")
+    cfg = shortlist_cfg(T, 512, 8, L, w, s)
+    m, x = _module(cfg, B, T, 512, torch.bfloat16, dev, outlier)
+    snap = {n: b.detach().clone() for n, b in m.named_buffers() if n.startswith("routing_")}
+    with torch.no_grad():
+        y_s = m(x)
+        a_s = m.last_head_consensus.float().clone()
+        assert m._last_sparse_state["linear_shortlist_structured"] is True
+        len_s = m._last_shortlist_lengths.cpu().long()
+        for n, b in snap.items():
+            getattr(m, n).copy_(b)
+        monkeypatch.setenv("PFA_FORCE_GENERIC", "1")
+        y_g = m(x)
+        a_g = m.last_head_consensus.float()
+        assert m._last_sparse_state["linear_shortlist_structured"] is False
+        len_g = m._last_shortlist_lengths.cpu().long()
+    assert torch.equal(len_s, len_g)
+    # attention outputs (before the output projection): both accumulate in
+    # f32 and round once to bf16, so they differ by at most one bf16 ulp
+    err = float((a_s - a_g).abs().max())
+    ulp = float((a_g.abs().clamp_min(2.0 ** -126) * 2.0 ** -7).max())
+    _say(f"max-abs structured vs materialised: attention {err:.3e}, y {float((y_s.float() - y_g.float()).abs().max()):.3e}")
+    assert err <= min(TOL_BF16, ulp)
+    rel = float(((y_s.float() - y_g.float()).abs() / (y_g.float().abs() + 1.0)).max())
+    assert rel <= TOL_BF16
+
+
 # ---------------------------------------------------------------------------
 # router, token top-k, packing, RoPE
 # ---------------------------------------------------------------------------
@@ -170,17 +223,19 @@ def _run_router(dev, x, w, protos, conf, dt, topk, H, temp=0.2, thr=0.25, blend=
     lib = _hip.lib()
     n, C = x.reshape(-1, x.size(-1)).shape
     G = w.size(0)
+    from proteus_attention.models.aspa import pack_router_weights
+
     xd = x.reshape(n, C).to(dev, dt).contiguous()
-    wd = w.to(dev, dt).contiguous()
     pn = torch.nn.functional.normalize(protos.to(torch.float32), dim=-1, eps=1e-6).to(dev).contiguous()
+    wpk = pack_router_weights(w.to(dev), pn, dt)
     cw = (conf + 1e-6).to(torch.float32).to(dev)
     outs = [torch.empty(n, G, device=dev), torch.empty(n, device=dev), torch.empty(n, device=dev),
             torch.empty(n, device=dev), torch.empty(n, topk, device=dev, dtype=torch.int32),
             torch.empty(n, topk, device=dev)]
     g2h = O.default_gate_map(G, H).to(torch.int32).to(dev)
-    rc = lib.pfa_router_topk(_hip.ptr(xd), _hip.dtype_tag(dt), n, C, G, _hip.ptr(wd), _hip.ptr(pn), _hip.ptr(cw),
+    rc = lib.pfa_router_topk(_hip.ptr(xd), _hip.dtype_tag(dt), n, C, G, _hip.ptr(wpk), 1, _hip.ptr(cw),
                              None, _hip.ptr(g2h), H, topk, temp, thr, blend, 0.0, *[_hip.ptr(o) for o in outs],
-                             _hip.stream_ptr(dev))
+                             None, _hip.stream_ptr(dev))
     _hip.check(rc, "router")
     return [o.cpu() for o in outs]
 
