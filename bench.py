@@ -85,6 +85,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (5 times) and exit: the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the ASPA path shards by (batch, head) with no exchange, "
@@ -98,6 +101,15 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
+        return 0
     log("building config-3 module")
     m, x_cpu, weights = build_module(dev, dtype)
     x = x_cpu.to(dtype).to(dev)

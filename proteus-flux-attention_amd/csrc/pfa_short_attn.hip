@@ -158,22 +158,18 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 4; ++i) st.acc[db][i] *= alpha;
-  // P is split into bf16 hi + lo parts (two MFMAs per V block), so the P.V
-  // product keeps ~16 significant bits of each probability instead of 8.
+  // P is rounded to bf16 for the P.V MFMA (the reference's bf16 path rounds
+  // its probabilities to bf16 too); the accumulator stays f32.
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
-    uint16_t ph[8], pl[8];
+    uint16_t pb16[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float a0 = s[2 * kc][i], a1 = s[2 * kc + 1][i];
-      ph[i] = bf16_bits(a0);
-      ph[4 + i] = bf16_bits(a1);
-      pl[i] = bf16_bits(a0 - bf16_to_f32(ph[i]));
-      pl[4 + i] = bf16_bits(a1 - bf16_to_f32(ph[4 + i]));
+      pb16[i] = bf16_bits(s[2 * kc][i]);
+      pb16[4 + i] = bf16_bits(s[2 * kc + 1][i]);
     }
-    bf16x8_t pbh, pbl;
-    __builtin_memcpy(&pbh, ph, 16);
-    __builtin_memcpy(&pbl, pl, 16);
+    bf16x8_t pb;
+    __builtin_memcpy(&pb, pb16, 16);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       const uint16_t* vr = Vt + (16 * db + r16) * kLd + 32 * kc + 4 * g;
@@ -182,8 +178,7 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
       uint32_t w4[4] = {lo8.x, lo8.y, hi8.x, hi8.y};
       bf16x8_t va;
       __builtin_memcpy(&va, w4, 16);
-      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pbh, st.acc[db], 0, 0, 0);
-      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pbl, st.acc[db], 0, 0, 0);
+      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, st.acc[db], 0, 0, 0);
     }
   }
 }

@@ -191,12 +191,20 @@ def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, 
         assert m._last_sparse_state["linear_shortlist_structured"] is False
         len_g = m._last_shortlist_lengths.cpu().long()
     assert torch.equal(len_s, len_g)
-    # attention outputs (before the output projection): both accumulate in
-    # f32 and round once to bf16, so they differ by at most one bf16 ulp
-    err = float((a_s - a_g).abs().max())
-    ulp = float((a_g.abs().clamp_min(2.0 ** -126) * 2.0 ** -7).max())
-    _say(f"max-abs structured vs materialised: attention {err:.3e}, y {float((y_s.float() - y_g.float()).abs().max()):.3e}")
-    assert err <= min(TOL_BF16, ulp)
+    # attention outputs (before the output projection).  The gather path keeps
+    # probabilities in f32; the MFMA path rounds them to bf16 (relative error
+    # <= 2^-9 each, as the reference's bf16 softmax does), so per element
+    # |a_s - a_g| <= 2^-9 * max|v| + one bf16 ulp of the output.
+    with torch.no_grad():
+        C = x.shape[-1]
+        vmax = float(m.qkv(x)[..., 2 * C:].float().abs().max())
+    diff = (a_s - a_g).abs()
+    mag = torch.maximum(a_s.abs(), a_g.abs()).clamp_min(2.0 ** -126)
+    ulp = torch.ldexp(torch.ones_like(mag), torch.frexp(mag).exponent - 8)
+    _say(f"max-abs structured vs materialised: attention {float(diff.max()):.3e}, "
+         f"y {float((y_s.float() - y_g.float()).abs().max()):.3e}")
+    bound = ulp + 2.0 ** -9 * vmax
+    assert bool((diff <= bound).all()), float((diff - bound).max())
     rel = float(((y_s.float() - y_g.float()).abs() / (y_g.float().abs() + 1.0)).max())
     assert rel <= TOL_BF16
 
