@@ -30,6 +30,20 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 CFG3 = dict(B=1, T=65536, C=512, H=8, L=2048, window=512, stride=256, outlier=0.01)
 
 
+def recorded_traffic() -> dict:
+    """HBM bytes per launch of each entry point, from the rocprofv3
+    FETCH_SIZE/WRITE_SIZE passes recorded in profiles/cfg3_hbm_traffic.md
+    (counter readings scaled by a copy of known size)."""
+    out = {}
+    path = ROOT / "profiles" / "cfg3_hbm_traffic.md"
+    if path.exists():
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes "):
+                name, val = line[len("traffic_bytes "):].split(":")
+                out[name.strip()] = int(float(val))
+    return out
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -177,19 +191,20 @@ def main() -> int:
         "proto_prefix_topk": ("hbm", tokens * 205 * 4.0 + tokens * 4.0, HBM_PEAK_GBS, "GB/s", 1e9),
     }
     per_stage.update(per_stage_extra)
+    traffic = recorded_traffic()
     kernels = {}
     for name, ms in per_stage.items():
         if name in alg:
             bound, work, peak, unit, scale = alg[name]
             ach = work / (ms * 1e-3) / scale
             kernels[name] = {"ms": round(ms, 4), "bound": bound, "achieved": round(ach, 3), "peak": peak,
-                             "unit": unit, "frac": round(ach / peak, 5)}
+                             "unit": unit, "frac": round(ach / peak, 5), "traffic": traffic.get(name)}
         else:
             kernels[name] = {"ms": round(ms, 4)}
     dominant = max((k for k in module_stages if k in alg), key=lambda k: per_stage[k])
     dk = kernels[dominant]
     roofline = {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
-                "unit": dk["unit"], "frac": dk["frac"], "traffic": None}
+                "unit": dk["unit"], "frac": dk["frac"], "traffic": dk["traffic"]}
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle pipeline on host cores)")
