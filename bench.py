@@ -143,14 +143,17 @@ def main() -> int:
         _hip.TIMER.enabled = True
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        host = 0.0
         for i in range(args.steps):
             restore()
+            h0 = time.perf_counter()
             m(x)
+            host += time.perf_counter() - h0
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
         _hip.TIMER.enabled = False
     stages = _hip.TIMER.summary_ms()
-    log(f"timed {args.steps} steps in {elapsed:.3f}s")
+    log(f"timed {args.steps} steps in {elapsed:.3f}s (host time inside forward calls {1e3 * host / args.steps:.3f} ms/step)")
     c = CFG3
     tokens = c["B"] * c["T"]
     value = tokens * args.steps / elapsed

@@ -90,13 +90,14 @@ int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G,
  * partial sums  sum_t gate[t,g]*x[t,c]  (columns 0..C-1) and
  * sum_t gate[t,g]  (column C), laid out (n_parts, G, C+1) f32, then summed
  * in a fixed order into (G, C+1).  Replaces the (G,BT)@(BT,C) product of
- * aspa.py:703-707 without materialising x in f32.
+ * aspa.py:703-707 without materialising x in f32.  The reduction works in
+ * place: `partial` is scratch and holds no useful values afterwards.
  * ==================================================================== */
 int pfa_proto_partial_count(int64_t n_tok, int* n_parts);
 int pfa_proto_accumulate(const void* x, int x_dtype, int64_t n_tok, int C,
                          int G, const float* gate_probs, float* partial,
                          int n_parts, void* stream);
-int pfa_proto_partial_reduce(const float* partial, int n_parts, int G, int C,
+int pfa_proto_partial_reduce(float* partial, int n_parts, int G, int C,
                              float* out, void* stream);
 
 /* EMA step of aspa.py:700-716 from the reduced (G, C+1) sums: for gates with

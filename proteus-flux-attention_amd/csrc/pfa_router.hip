@@ -240,15 +240,17 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
   }
 }
 
-// Prototype EMA partial sums: part p accumulates, for a slice of 64 tokens,
-// sum_t gate[t,g]*x[t,c] (columns 0..C-1) and sum_t gate[t,g] (column C).
-// A thread owns a pair of channels (one 4-byte load per token, coalesced
-// across the workgroup); the gate row of the current token is wave-uniform
-// (scalar loads); eight tokens are in flight per step, and thousands of
-// 4-wave workgroups keep the CUs busy.
+// Prototype EMA partial sums: part p accumulates, for a slice of at most
+// kEmaTok tokens, sum_t gate[t,g]*x[t,c] (columns 0..C-1) and sum_t gate[t,g]
+// (column C).  The slice's gate rows are staged in LDS (zero-padded to GMAX
+// gates) and read back as broadcast float4s; a thread owns a pair of
+// channels (one 4-byte load per token, coalesced across the workgroup), with
+// eight tokens in flight per step.  Every sum runs in token order, so the
+// result does not depend on scheduling.
 constexpr int kEmaThreads = 256;
 constexpr int kEmaTok = 64;
 constexpr int kEmaMaxParts = 4096;
+constexpr int kEmaGroup = 32;  // parts summed per thread in the first reduce level
 
 template <int DT>
 __device__ __forceinline__ void load2(const typename Elem<DT>::T* p, bool two, float& a, float& b) {
@@ -271,83 +273,128 @@ template <int DT, int GMAX>
 __global__ void __launch_bounds__(kEmaThreads)
 proto_accum_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, int G,
                    const float* __restrict__ gate_probs, int64_t tok_per_part, float* __restrict__ partial) {
+  __shared__ float4 g_lds[kEmaTok * (GMAX / 4)];
   const int part = blockIdx.x;
-  const int64_t t0 = (int64_t)part * tok_per_part;
-  const int64_t t1 = min(n_tok, t0 + tok_per_part);
+  const int64_t tb = (int64_t)part * tok_per_part;
+  const int64_t te = min(n_tok, tb + tok_per_part);
   float* out = partial + (int64_t)part * G * (C + 1);
   const int npair = (C + 1) / 2;
-  for (int cp = threadIdx.x; cp < npair; cp += blockDim.x) {
-    const int c0 = 2 * cp;
-    const bool two = c0 + 1 < C;
-    float a0[GMAX], a1[GMAX];
+  float* gl = reinterpret_cast<float*>(g_lds);
+  float a0[GMAX], a1[GMAX];
+  float csum = 0.f;
+  const int cp = threadIdx.x;
+  for (int64_t t0 = tb; t0 < te; t0 += kEmaTok) {
+    const int nt = (int)min<int64_t>(kEmaTok, te - t0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kEmaTok * GMAX; i += blockDim.x) {
+      const int u = i / GMAX, g = i % GMAX;
+      gl[i] = (u < nt && g < G) ? gate_probs[(t0 + u) * G + g] : 0.f;
+    }
+    __syncthreads();
+    if (threadIdx.x < GMAX) {
+      // column C: lane g sums gate g over the slice, in token order
+      for (int u = 0; u < nt; ++u) csum += gl[u * GMAX + threadIdx.x];
+    }
+    for (int c2 = cp; c2 < npair; c2 += blockDim.x) {
+      const int c0 = 2 * c2;
+      const bool two = c0 + 1 < C;
+      if (t0 == tb || C > 2 * (int)blockDim.x) {
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) { a0[g] = 0.f; a1[g] = 0.f; }
-    int64_t t = t0;
-    for (; t + 8 <= t1; t += 8) {
-      float x0[8], x1[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) load2<DT>(x + (t + u) * C + c0, two, x0[u], x1[u]);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float* pr = gate_probs + (t + u) * G;
+        for (int g = 0; g < GMAX; ++g) { a0[g] = 0.f; a1[g] = 0.f; }
+      }
+      if (C > 2 * (int)blockDim.x && t0 != tb) {
+        // wide rows: reload the running sums of this channel pair
 #pragma unroll
         for (int g = 0; g < GMAX; ++g)
           if (g < G) {
-            a0[g] = __builtin_fmaf(pr[g], x0[u], a0[g]);
-            a1[g] = __builtin_fmaf(pr[g], x1[u], a1[g]);
+            a0[g] = out[(int64_t)g * (C + 1) + c0];
+            if (two) a1[g] = out[(int64_t)g * (C + 1) + c0 + 1];
           }
       }
-    }
-    for (; t < t1; ++t) {
-      float x0, x1;
-      load2<DT>(x + t * C + c0, two, x0, x1);
-      const float* pr = gate_probs + t * G;
+      int u = 0;
+      for (; u + 8 <= nt; u += 8) {
+        float x0[8], x1[8];
 #pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) {
-          a0[g] = __builtin_fmaf(pr[g], x0, a0[g]);
-          a1[g] = __builtin_fmaf(pr[g], x1, a1[g]);
+        for (int k = 0; k < 8; ++k) load2<DT>(x + (t0 + u + k) * C + c0, two, x0[k], x1[k]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+#pragma unroll
+          for (int q = 0; q < GMAX / 4; ++q) {
+            const float4 pr = g_lds[(u + k) * (GMAX / 4) + q];
+            a0[4 * q + 0] = __builtin_fmaf(pr.x, x0[k], a0[4 * q + 0]);
+            a0[4 * q + 1] = __builtin_fmaf(pr.y, x0[k], a0[4 * q + 1]);
+            a0[4 * q + 2] = __builtin_fmaf(pr.z, x0[k], a0[4 * q + 2]);
+            a0[4 * q + 3] = __builtin_fmaf(pr.w, x0[k], a0[4 * q + 3]);
+            a1[4 * q + 0] = __builtin_fmaf(pr.x, x1[k], a1[4 * q + 0]);
+            a1[4 * q + 1] = __builtin_fmaf(pr.y, x1[k], a1[4 * q + 1]);
+            a1[4 * q + 2] = __builtin_fmaf(pr.z, x1[k], a1[4 * q + 2]);
+            a1[4 * q + 3] = __builtin_fmaf(pr.w, x1[k], a1[4 * q + 3]);
+          }
         }
-    }
+      }
+      for (; u < nt; ++u) {
+        float x0, x1;
+        load2<DT>(x + (t0 + u) * C + c0, two, x0, x1);
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-      if (g < G) {
-        out[(int64_t)g * (C + 1) + c0] = a0[g];
-        if (two) out[(int64_t)g * (C + 1) + c0 + 1] = a1[g];
+        for (int q = 0; q < GMAX / 4; ++q) {
+          const float4 pr = g_lds[u * (GMAX / 4) + q];
+          a0[4 * q + 0] = __builtin_fmaf(pr.x, x0, a0[4 * q + 0]);
+          a0[4 * q + 1] = __builtin_fmaf(pr.y, x0, a0[4 * q + 1]);
+          a0[4 * q + 2] = __builtin_fmaf(pr.z, x0, a0[4 * q + 2]);
+          a0[4 * q + 3] = __builtin_fmaf(pr.w, x0, a0[4 * q + 3]);
+          a1[4 * q + 0] = __builtin_fmaf(pr.x, x1, a1[4 * q + 0]);
+          a1[4 * q + 1] = __builtin_fmaf(pr.y, x1, a1[4 * q + 1]);
+          a1[4 * q + 2] = __builtin_fmaf(pr.z, x1, a1[4 * q + 2]);
+          a1[4 * q + 3] = __builtin_fmaf(pr.w, x1, a1[4 * q + 3]);
+        }
+      }
+      const bool last = t0 + kEmaTok >= te;
+      if (last || C > 2 * (int)blockDim.x) {
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+          if (g < G) {
+            out[(int64_t)g * (C + 1) + c0] = a0[g];
+            if (two) out[(int64_t)g * (C + 1) + c0 + 1] = a1[g];
+          }
+        }
       }
     }
   }
-  // column C (sum of gate probabilities) by wave 0
-  if (threadIdx.x < 64) {
-    float cs[GMAX];
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) cs[g] = 0.f;
-    for (int64_t t = t0 + threadIdx.x; t < t1; t += 64)
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) cs[g] += gate_probs[t * G + g];
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-      for (int off = 32; off > 0; off >>= 1) cs[g] += __shfl_xor(cs[g], off, 64);
-      if (g < G && threadIdx.x == 0) out[(int64_t)g * (C + 1) + C] = cs[g];
-    }
-  }
+  if (threadIdx.x < G) out[(int64_t)threadIdx.x * (C + 1) + C] = csum;
 }
 
-__global__ void partial_reduce_kernel(const float* __restrict__ partial, int n_parts, int64_t width,
-                                      float* __restrict__ out) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Sum of the partial rows, in two fixed-order levels (in place): level 0
+// sums rows [k*kEmaGroup, (k+1)*kEmaGroup) into row k*kEmaGroup; level 1 sums
+// rows 0, kEmaGroup, 2*kEmaGroup, ... into out.  Each thread owns one column.
+__global__ void __launch_bounds__(256) partial_reduce_group(float* __restrict__ partial, int n_parts, int64_t width) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= width) return;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  int p = 0;
-  for (; p + 4 <= n_parts; p += 4) {
-    s0 = s0 + partial[(int64_t)p * width + i];
-    s1 = s1 + partial[(int64_t)(p + 1) * width + i];
-    s2 = s2 + partial[(int64_t)(p + 2) * width + i];
-    s3 = s3 + partial[(int64_t)(p + 3) * width + i];
+  const int p0 = blockIdx.y * kEmaGroup;
+  const int p1 = min(n_parts, p0 + kEmaGroup);
+  float v[kEmaGroup];
+#pragma unroll
+  for (int k = 0; k < kEmaGroup; ++k) v[k] = (p0 + k < p1) ? partial[(int64_t)(p0 + k) * width + i] : 0.f;
+  float s = v[0];
+#pragma unroll
+  for (int k = 1; k < kEmaGroup; ++k) s = s + v[k];
+  partial[(int64_t)p0 * width + i] = s;
+}
+
+__global__ void __launch_bounds__(256) partial_reduce_final(const float* __restrict__ partial, int n_groups,
+                                                            int64_t width, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= width) return;
+  float s = 0.f;
+  int k = 0;
+  for (; k + 8 <= n_groups; k += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = partial[(int64_t)(k + j) * kEmaGroup * width + i];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s = s + v[j];
   }
-  for (; p < n_parts; ++p) s0 = s0 + partial[(int64_t)p * width + i];
-  out[i] = (s0 + s1) + (s2 + s3);
+  for (; k < n_groups; ++k) s = s + partial[(int64_t)k * kEmaGroup * width + i];
+  out[i] = s;
 }
 
 // EMA update of prototypes / usage / confidence from the reduced sums
@@ -506,11 +553,16 @@ extern "C" int pfa_proto_accumulate(const void* x, int x_dtype, int64_t n_tok, i
   return PFA_OK;
 }
 
-extern "C" int pfa_proto_partial_reduce(const float* partial, int n_parts, int G, int C, float* out, void* stream) {
+extern "C" int pfa_proto_partial_reduce(float* partial, int n_parts, int G, int C, float* out, void* stream) {
   clear_error();
   PFA_CHECK_ARG(partial && out && n_parts > 0 && G > 0 && C > 0, "pfa_proto_partial_reduce: bad arguments");
   int64_t width = (int64_t)G * (C + 1);
-  partial_reduce_kernel<<<(unsigned)((width + 255) / 256), 256, 0, as_stream(stream)>>>(partial, n_parts, width, out);
+  hipStream_t s = as_stream(stream);
+  const unsigned cols = (unsigned)((width + 255) / 256);
+  const int groups = (n_parts + kEmaGroup - 1) / kEmaGroup;
+  partial_reduce_group<<<dim3(cols, (unsigned)groups), 256, 0, s>>>(partial, n_parts, width);
+  PFA_CHECK_LAUNCH("pfa_proto_partial_reduce");
+  partial_reduce_final<<<cols, 256, 0, s>>>(partial, groups, width, out);
   PFA_CHECK_LAUNCH("pfa_proto_partial_reduce");
   return PFA_OK;
 }

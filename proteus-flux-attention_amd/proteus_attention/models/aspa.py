@@ -177,8 +177,31 @@ def _policy_tokens(raw: str) -> set:
     return toks or {"local", "anchors"}
 
 
+def _lazy_stat(name: str) -> property:
+    """Telemetry attribute whose value may still be in flight from the GPU:
+    reading it first completes the pending readbacks of earlier forwards, so
+    a forward itself never waits on the device for its statistics."""
+    key = "_lazy_" + name
+
+    def get(self):
+        self._resolve_stats()
+        return self.__dict__.get(key)
+
+    def put(self, value):
+        self.__dict__[key] = value
+
+    return property(get, put)
+
+
 class AdaptiveSparseAttention(nn.Module):
     """ASPA layer (reference aspa.py:170-1932) on MI355X kernels."""
+
+    last_head_stats = _lazy_stat("last_head_stats")
+    _last_sparse_state = _lazy_stat("_last_sparse_state")
+    _last_proto_stats = _lazy_stat("_last_proto_stats")
+    _density_ema = _lazy_stat("_density_ema")
+    _last_density = _lazy_stat("_last_density")
+    _latency_ema = _lazy_stat("_latency_ema")
 
     def __init__(self, config: ModelConfig):
         super().__init__()
@@ -487,6 +510,19 @@ class AdaptiveSparseAttention(nn.Module):
         if keep < mean.numel():
             keep += 1
         return min(max_cap, max(1, keep))
+
+    def _defer(self, fn) -> None:
+        """Queue a telemetry step that needs device results; it runs at the
+        next _resolve_stats (a telemetry read or the next forward)."""
+        self.__dict__.setdefault("_pending_stats", []).append(fn)
+
+    def _resolve_stats(self) -> None:
+        pend = self.__dict__.get("_pending_stats")
+        if not pend:
+            return
+        self.__dict__["_pending_stats"] = []
+        for fn in pend:
+            fn()
 
     def _update_density(self, value: float) -> None:
         value = float(max(0.0, value))
@@ -823,6 +859,7 @@ class AdaptiveSparseAttention(nn.Module):
     def _forward_dense_fastpath(self, x: torch.Tensor) -> torch.Tensor:
         """Dense causal attention for short sequences (aspa.py:1365-1440)."""
         B, T, C = x.shape
+        self._resolve_stats()
         qkv = self._project_qkv(x)
         attn = torch.empty(B, T, C, dtype=qkv.dtype, device=x.device)
         self._attend_dense_causal(qkv, B, T, attn)
@@ -869,20 +906,34 @@ class AdaptiveSparseAttention(nn.Module):
         self._last_batch_size = B
 
         def finish(label: str) -> None:
+            # latency and labels land in the statistics of this forward; the
+            # latency needs the end event, so both are deferred with them
+            st_now = self.__dict__.get("_lazy__last_sparse_state")
             if self.track_latency and ev0 is not None:
                 ev1.record()
-                ev1.synchronize()
-                ms = float(ev0.elapsed_time(ev1))
-                self._latency_ema = ms if self._latency_ema is None else 0.8 * self._latency_ema + 0.2 * ms
-                if self.last_head_stats is not None:
-                    self.last_head_stats["latency_ms"] = ms
-                if self._last_sparse_state is not None:
-                    self._last_sparse_state["latency_ms"] = ms
-            if self.last_head_stats is not None:
-                self.last_head_stats["mode_setting"] = self.mode_setting
-                self.last_head_stats["mode_selected"] = label
-            if self._last_sparse_state is not None:
-                self._last_sparse_state["mode_selected"] = label
+
+                def latency(st=st_now):
+                    ev1.synchronize()
+                    ms = float(ev0.elapsed_time(ev1))
+                    prev = self.__dict__.get("_lazy__latency_ema")
+                    self._latency_ema = ms if prev is None else 0.8 * prev + 0.2 * ms
+                    hs = self.__dict__.get("_lazy_last_head_stats")
+                    if hs is not None:
+                        hs["latency_ms"] = ms
+                    if st is not None:
+                        st["latency_ms"] = ms
+
+                self._defer(latency)
+
+            def labels(st=st_now):
+                hs = self.__dict__.get("_lazy_last_head_stats")
+                if hs is not None:
+                    hs["mode_setting"] = self.mode_setting
+                    hs["mode_selected"] = label
+                if st is not None:
+                    st["mode_selected"] = label
+
+            self._defer(labels)
 
         if self.small_seq_dense and T <= self.small_seq_dense:
             y = self._forward_dense_fastpath(x)
@@ -1161,71 +1212,94 @@ class AdaptiveSparseAttention(nn.Module):
     def _finish_stats(self, token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
                       dense_reason, B, T, active_heads, row_offsets, summary) -> None:
         """Telemetry dictionaries (aspa.py:1857-1916) from the router's
-        per-workgroup partials and the packing summary: one host readback."""
+        per-workgroup partials and the packing summary.  The three small
+        device buffers are copied into pinned host memory without waiting;
+        the dictionaries are built when first read (or at the next forward),
+        so the forward never stalls the device queue for them."""
+        self._resolve_stats()
         H = self.h_total
         with torch.no_grad():
-            part = self._router_stats.sum(dim=0, dtype=torch.float64)
-            vals = torch.cat([part[:5], summary.to(torch.float64), active_heads.to(torch.float64)]).cpu().tolist()
-        ent_sum, sim_sum, blend_sum, blend_pos, score_sum = vals[:5]
-        P, N, max_rows = int(vals[5]), int(vals[6]), int(vals[7])
-        heads_list = [int(v) for v in vals[9:9 + P]]
-        n_tok = max(1, B * T)
-        density_est = float(max_rows) / float(max(1, T))
-        self._update_density(density_est)
-        keep_frac = float(N) / float(max(1, topk * B * T)) if token_mask is not None else 1.0
-        if mode_label == "dense_auto" and P == B * H:
-            mode_label = "dense"
-        st = self._last_sparse_state
-        if st is not None:
-            st["token_keep_fraction"] = keep_frac
-            st["max_rows"] = int(max_rows)
-            st["density"] = density_est
-            if st.get("mode") == "dense_auto" and mode_label == "dense":
-                st["mode"] = "dense"
-            if "active_head_indices" in st:
-                st["active_head_indices"] = st["active_head_indices"][:P].to(torch.int64)
-                st["row_offsets"] = st["row_offsets"][:P + 1]
-        self.last_head_stats = {
-            "top_k": int(topk),
-            "mean_gate_prob": float(score_sum / max(1.0, float(N))),
-            "router_entropy": float(ent_sum / n_tok),
-            "mean_active_per_token": float(N) / float(n_tok),
-            "unique_heads": len({hb % H for hb in heads_list}),
-            "active_fraction": float(N) / float(max(1, B * T * H)),
-            "max_active_rows": int(max_rows),
-            "max_active_density": float(density_est),
-            "target_k": int(self._last_target_k or topk),
-            "seq_len": int(T),
-            "active_min": int(self.h_active_min),
-            "active_max": int(self.h_active_max),
-            "force_dense_threshold": None if density_threshold is None else float(density_threshold),
-            "active_curve": float(self.h_active_curve),
-            "token_keep_fraction": keep_frac,
-            "mode": mode_label,
-            "mode_selected": f"cvt(alpha={alpha:.2f})",
-            "shortlist_alpha": float(alpha),
-            "router_top_p": float(self.router_top_p),
-            "nucleus_k": int(adaptive_topk),
-            "top_a_consensus": True,
-        }
-        if dense_reason is not None:
-            self.last_head_stats["dense_reason"] = dense_reason
-        if alpha > 0.0:
-            self.last_head_stats["linear_L"] = int(self.linear_L)
-            self.last_head_stats["linear_window"] = int(self.linear_window)
-            self.last_head_stats["linear_anchor_stride"] = int(self.linear_anchor_stride)
-            info = self._last_shortlist_backend_info or get_last_backend_info()
-            if info.get("name") is not None:
-                self.last_head_stats["linear_shortlist_backend"] = info.get("name")
-                det = info.get("details")
-                if isinstance(det, dict):
-                    for key, val in det.items():
-                        self.last_head_stats[f"linear_shortlist_{key}"] = val
-        if self._last_token_similarity is not None:
-            self._last_proto_stats = {"max_sim_mean": float(sim_sum / n_tok), "blend_mean": float(blend_sum / n_tok),
-                                      "active_tokens": int(blend_pos)}
-            self.last_head_stats["proto"] = dict(self._last_proto_stats)
-            self.last_head_stats["dna"] = dict(self._last_proto_stats)
+            host = []
+            for t in (self._router_stats, summary, active_heads):
+                h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+                h.copy_(t, non_blocking=True)
+                host.append(h)
+            done = torch.cuda.Event()
+            done.record()
+        # everything the dictionaries need from the host side, as of now
+        st = self.__dict__.get("_lazy__last_sparse_state")
+        info = self._last_shortlist_backend_info or get_last_backend_info()
+        ctx = dict(
+            target_k=int(self._last_target_k or topk), linear=(int(self.linear_L), int(self.linear_window),
+                                                           int(self.linear_anchor_stride)),
+            proto=self._last_token_similarity is not None, mode_setting=self.mode_setting)
+
+        def build() -> None:
+            nonlocal mode_label
+            done.synchronize()
+            part = host[0].to(torch.float64).sum(dim=0).tolist()
+            summ = host[1].tolist()
+            ent_sum, sim_sum, blend_sum, blend_pos, score_sum = part[:5]
+            P_, N_, max_rows_ = int(summ[0]), int(summ[1]), int(summ[2])
+            heads_list = host[2][:P_].tolist()
+            n_tok = max(1, B * T)
+            density_est = float(max_rows_) / float(max(1, T))
+            self._update_density(density_est)
+            keep_frac = float(N_) / float(max(1, topk * B * T)) if token_mask is not None else 1.0
+            if mode_label == "dense_auto" and P_ == B * H:
+                mode_label = "dense"
+            if st is not None:
+                st["token_keep_fraction"] = keep_frac
+                st["max_rows"] = int(max_rows_)
+                st["density"] = density_est
+                if st.get("mode") == "dense_auto" and mode_label == "dense":
+                    st["mode"] = "dense"
+                if "active_head_indices" in st:
+                    st["active_head_indices"] = st["active_head_indices"][:P_].to(torch.int64)
+                    st["row_offsets"] = st["row_offsets"][:P_ + 1]
+            hs = {
+                "top_k": int(topk),
+                "mean_gate_prob": float(score_sum / max(1.0, float(N_))),
+                "router_entropy": float(ent_sum / n_tok),
+                "mean_active_per_token": float(N_) / float(n_tok),
+                "unique_heads": len({int(hb) % H for hb in heads_list}),
+                "active_fraction": float(N_) / float(max(1, B * T * H)),
+                "max_active_rows": int(max_rows_),
+                "max_active_density": float(density_est),
+                "target_k": ctx["target_k"],
+                "seq_len": int(T),
+                "active_min": int(self.h_active_min),
+                "active_max": int(self.h_active_max),
+                "force_dense_threshold": None if density_threshold is None else float(density_threshold),
+                "active_curve": float(self.h_active_curve),
+                "token_keep_fraction": keep_frac,
+                "mode": mode_label,
+                "mode_selected": f"cvt(alpha={alpha:.2f})",
+                "shortlist_alpha": float(alpha),
+                "router_top_p": float(self.router_top_p),
+                "nucleus_k": int(adaptive_topk),
+                "top_a_consensus": True,
+            }
+            if dense_reason is not None:
+                hs["dense_reason"] = dense_reason
+            if alpha > 0.0:
+                hs["linear_L"], hs["linear_window"], hs["linear_anchor_stride"] = ctx["linear"]
+                if info.get("name") is not None:
+                    hs["linear_shortlist_backend"] = info.get("name")
+                    det = info.get("details")
+                    if isinstance(det, dict):
+                        for key, val in det.items():
+                            hs[f"linear_shortlist_{key}"] = val
+            proto_stats = None
+            if ctx["proto"]:
+                proto_stats = {"max_sim_mean": float(sim_sum / n_tok), "blend_mean": float(blend_sum / n_tok),
+                               "active_tokens": int(blend_pos)}
+                hs["proto"] = dict(proto_stats)
+                hs["dna"] = dict(proto_stats)
+            self._last_proto_stats = proto_stats
+            self.last_head_stats = hs
+
+        self._defer(build)
 
 
 class AdaptiveSparseProtoAttention(AdaptiveSparseAttention):
@@ -1256,8 +1330,6 @@ class AdaptiveSparseAttentionBlock(nn.Module):
         self.last_aux_loss = None
         self.last_moe_stats = None
         self.last_router_reg = None
-        self.last_head_stats = None
-        self.last_sparse_state = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x = x + self.attn(self.ln1(x))
@@ -1265,6 +1337,12 @@ class AdaptiveSparseAttentionBlock(nn.Module):
         self.last_aux_loss = getattr(self.mlp, "last_aux_loss", None)
         self.last_router_reg = getattr(self.attn, "last_router_reg", None)
         self.last_moe_stats = None
-        self.last_head_stats = getattr(self.attn, "last_head_stats", None)
-        self.last_sparse_state = getattr(self.attn, "_last_sparse_state", None)
         return x
+
+    @property
+    def last_head_stats(self) -> Optional[dict]:
+        return getattr(self.attn, "last_head_stats", None)
+
+    @property
+    def last_sparse_state(self) -> Optional[dict]:
+        return getattr(self.attn, "_last_sparse_state", None)

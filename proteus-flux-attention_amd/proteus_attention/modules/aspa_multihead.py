@@ -137,9 +137,11 @@ class CausalASPAMultiheadAttention(nn.Module):
         if need_weights:
             shape = (batch, seq_len, seq_len) if average_attn_weights else (batch * self.num_heads, seq_len, seq_len)
             weights = out.new_zeros(*shape)
-        head_stats = getattr(self.attention, "last_head_stats", None)
+        # the statistics are read back from the device only when consumed
+        want = self._want_stats(return_stats)
+        head_stats = getattr(self.attention, "last_head_stats", None) if (want or self._sparse_ctl) else None
         snap: Optional[SparseCtlSnapshot] = self._sparse_ctl.observe(head_stats) if self._sparse_ctl else None
-        if self._want_stats(return_stats):
+        if want:
             stats = {"head_stats": head_stats,
                      "sparse_state": getattr(self.attention, "_last_sparse_state", None),
                      "shortlist_backend": get_last_backend_info()}

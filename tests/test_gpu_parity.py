@@ -283,6 +283,38 @@ def test_router_vs_golden_and_oracle(dev, golden, name, B, T, C, dt, outlier):
     assert int((~agree).sum()) <= (0 if dt == torch.float32 else max(4, n // 500))
 
 
+@pytest.mark.parametrize("n_tok,C,G,dt", [(300_000, 512, 8, torch.bfloat16), (5000, 1025, 12, torch.float32),
+                                          (37, 64, 3, torch.float16)])
+def test_proto_ema_sums_vs_f64(dev, n_tok, C, G, dt):
+    """Gate-weighted token sums of the prototype EMA (aspa.py:703-707):
+    sum_t gate[t,g]*x[t,c] and sum_t gate[t,g], against a float64 product on
+    the CPU.  Covers slices longer than one LDS stage (300k tokens), rows
+    wider than one channel pair per thread (C=1025, odd) and a tiny input."""
+    from proteus_attention import _hip
+
+    _say(f"proto EMA sums n_tok={n_tok} C={C} G={G} {dt}")
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(n_tok, C, generator=g).to(dt)
+    gp = torch.softmax(torch.randn(n_tok, G, generator=g), dim=-1)
+    lib = _hip.lib()
+    n = _hip.ctypes.c_int(0)
+    _hip.check(lib.pfa_proto_partial_count(n_tok, _hip.ctypes.byref(n)), "count")
+    xd, gd = x.to(dev), gp.to(dev)
+    part = torch.empty(n.value, G, C + 1, dtype=torch.float32, device=dev)
+    sums = torch.empty(G, C + 1, dtype=torch.float32, device=dev)
+    s = _hip.stream_ptr(dev)
+    _hip.check(lib.pfa_proto_accumulate(_hip.ptr(xd), _hip.dtype_tag(dt), n_tok, C, G, _hip.ptr(gd), _hip.ptr(part),
+                                        n.value, s), "accumulate")
+    _hip.check(lib.pfa_proto_partial_reduce(_hip.ptr(part), n.value, G, C, _hip.ptr(sums), s), "reduce")
+    got = sums.cpu().double()
+    ref = torch.cat([gp.double().t() @ x.double(), gp.double().sum(0).unsqueeze(1)], dim=1)
+    scale = (gp.double().t() @ x.double().abs()).clamp_min(1.0)
+    scale = torch.cat([scale, gp.double().sum(0).unsqueeze(1).clamp_min(1.0)], dim=1)
+    err = float(((got - ref).abs() / scale).max())
+    _say(f"max scaled error {err:.2e}")
+    assert err < 1e-5
+
+
 def test_token_topk_vs_oracle(dev):
     from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
 
@@ -486,6 +518,33 @@ def test_module_forward_vs_golden(dev, golden, name, maker, B, T, C, dt, outlier
                           rtol=1e-4 if dt == torch.float32 else 1e-2)
     assert torch.allclose(m.routing_usage_ema.float().cpu(), torch.from_numpy(z["usage_after"]), rtol=1e-4,
                           atol=1e-4 if dt == torch.float32 else 1e-1)
+
+
+def test_module_telemetry_deferred(dev):
+    """Statistics (aspa.py:1857-1916) are read back after the forward without
+    a device wait; reading them gives the values of the latest forward, and
+    they agree with closed forms over the forward's own router outputs."""
+    from configs import shortlist_cfg
+
+    _say("telemetry after two forwards of different length")
+    cfg = shortlist_cfg(4096, 512, 8, 1024, 256, 64)
+    m, x = _module(cfg, 1, 4096, 512, torch.bfloat16, dev, 0.01)
+    with torch.no_grad():
+        m(x)
+        m(x[:, :2048].contiguous())
+        gate = m._last_gate_probs.double().cpu()
+        sim = m._last_token_similarity.double().cpu()
+    hs = m.last_head_stats
+    assert hs["seq_len"] == 2048 and hs["mode"] == "shortlist"
+    assert hs["mean_active_per_token"] == pytest.approx(2.0)
+    assert hs["latency_ms"] > 0.0 and hs["mode_selected"].startswith("cvt(")
+    ent = float(-(gate.clamp_min(1e-9).log() * gate).sum(-1).mean())
+    assert hs["router_entropy"] == pytest.approx(ent, rel=1e-4, abs=1e-6)
+    assert hs["proto"]["max_sim_mean"] == pytest.approx(float(sim.mean()), rel=1e-4, abs=1e-6)
+    st = m._last_sparse_state
+    assert st["max_rows"] == hs["max_active_rows"] and st["latency_ms"] == hs["latency_ms"]
+    assert st["active_head_indices"].numel() == 8 and st["row_offsets"].numel() == 9
+    assert m._density_ema is not None and m._latency_ema is not None
 
 
 def test_module_dense_paths_vs_oracle(dev):
