@@ -7,12 +7,16 @@ dominant kernel and the CPU oracle pipeline timed on the host beside it.
 
 Prints exactly one JSON line on stdout.  A "step" is one module forward of
 config 3 (router, head top-k, packing, QKV projection + RoPE, prototype
-prefix sets, candidate builder, candidate attention, output projection,
-prototype EMA) over one synthetic batch already resident in HBM.
+prefix sets, candidate attention, output projection, prototype EMA) over one
+synthetic batch already resident in HBM.  The timed steps run the module's
+HIP-graph mode (every launch of the forward replayed from one captured
+graph); per-kernel durations come from the same number of eager forwards
+timed with HIP events, whose ms/step is reported as eager_ms_per_step.
 """
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -99,6 +103,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time the forward without HIP graph replay")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times) and exit: the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
@@ -133,27 +138,46 @@ def main() -> int:
         for n, b in snap.items():
             getattr(m, n).copy_(b)
 
+    # the forward replays as one HIP graph (the module's own graph mode);
+    # --eager times the launch-by-launch forward instead.  Objects that exist
+    # before the loop are frozen out of the cyclic GC, as serving loops do.
+    m.enable_hip_graph(not args.eager)
+    gc.collect()
+    gc.freeze()
     with torch.no_grad():
         for i in range(args.warmup):
             restore()
             m(x)
         torch.cuda.synchronize()
-        log(f"warmup done ({args.warmup} steps)")
-        _hip.TIMER.reset()
-        _hip.TIMER.enabled = True
+        log(f"warmup done ({args.warmup} steps, {'eager' if args.eager else 'graph replay'})")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        host = 0.0
+        host = []
         for i in range(args.steps):
             restore()
             h0 = time.perf_counter()
             m(x)
-            host += time.perf_counter() - h0
+            host.append(time.perf_counter() - h0)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
+        # per-kernel durations: the same forwards launched one by one, with
+        # HIP events around each entry point on the launch stream
+        m.enable_hip_graph(False)
+        restore()
+        m(x)
+        _hip.TIMER.reset()
+        _hip.TIMER.enabled = True
+        torch.cuda.synchronize()
+        e0 = time.perf_counter()
+        for i in range(args.steps):
+            restore()
+            m(x)
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - e0) * 1000.0 / args.steps
         _hip.TIMER.enabled = False
     stages = _hip.TIMER.summary_ms()
-    log(f"timed {args.steps} steps in {elapsed:.3f}s (host time inside forward calls {1e3 * host / args.steps:.3f} ms/step)")
+    log(f"timed {args.steps} steps in {elapsed:.3f}s (host ms inside each forward call: "
+        f"{' '.join(f'{1e3 * h:.2f}' for h in host)}); eager forward {eager_ms:.3f} ms/step")
     c = CFG3
     tokens = c["B"] * c["T"]
     value = tokens * args.steps / elapsed
@@ -220,6 +244,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "eager_ms_per_step": round(eager_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

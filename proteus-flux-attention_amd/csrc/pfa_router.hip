@@ -278,6 +278,12 @@ proto_accum_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, in
   const int64_t tb = (int64_t)part * tok_per_part;
   const int64_t te = min(n_tok, tb + tok_per_part);
   float* out = partial + (int64_t)part * G * (C + 1);
+  if (tb >= te) {
+    // trailing parts past the last token (the part count is capped and
+    // rounded): their rows still take part in the reduction
+    for (int64_t i = threadIdx.x; i < (int64_t)G * (C + 1); i += blockDim.x) out[i] = 0.f;
+    return;
+  }
   const int npair = (C + 1) / 2;
   float* gl = reinterpret_cast<float*>(g_lds);
   float a0[GMAX], a1[GMAX];

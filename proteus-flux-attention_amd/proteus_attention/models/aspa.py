@@ -400,6 +400,9 @@ class AdaptiveSparseAttention(nn.Module):
         # --- telemetry / caches (aspa.py:497-567) ---
         self.last_head_stats: Optional[dict] = None
         self._last_sparse_state: Optional[dict] = None
+        self._hip_graph_enabled = _flag(g("attn_hip_graph", False))
+        self._hip_graphs: Dict[Any, dict] = {}
+        self._hip_graph_pool = None
         self._cached_active_mask: Optional[torch.Tensor] = None
         self._cached_packing = None
         self.last_aux_loss: Optional[torch.Tensor] = None
@@ -887,11 +890,147 @@ class AdaptiveSparseAttention(nn.Module):
 
     # ------------------------------------------------------------------
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        B, T, C = x.shape
-        device = x.device
         _hip.require_device(x, what="AdaptiveSparseAttention.forward")
         if self.training and float(self.dropout.p) > 0.0:
             raise NotImplementedError("training-mode attention dropout is not provided by the HIP forward path")
+        if self._hip_graph_enabled and self._graph_eligible(x):
+            return self._forward_graph(x)
+        return self._forward_impl(x)
+
+    # ------------------------------------------------------------------
+    # HIP graph replay of the forward
+    def enable_hip_graph(self, enabled: bool = True) -> None:
+        """Replay the forward from a captured HIP graph.
+
+        The first call for an input shape/dtype (and the schedule state that
+        fixes the launch sequence) captures every launch of the forward up to
+        the attention output, plus the prototype EMA, into one graph; later
+        calls copy the input into the graph's static buffer (skipped when the
+        caller passes that buffer back), replay it and run the output
+        projection eagerly, so the returned tensor is fresh.  Telemetry is
+        read back as in the eager forward.  Applies in eval / no-grad mode
+        when no host decision depends on device results (no token sparsity,
+        density threshold, nucleus head count, memory or latency budget);
+        otherwise the eager forward runs.  Tensors the module keeps from the
+        last forward (last_head_consensus, _last_gate_probs, ...) are the
+        graph's static buffers and change with the next replay."""
+        self._hip_graph_enabled = bool(enabled)
+        if not enabled:
+            self.reset_hip_graphs()
+
+    def reset_hip_graphs(self) -> None:
+        self._resolve_stats()
+        self._hip_graphs = {}
+
+    def _graph_eligible(self, x: torch.Tensor) -> bool:
+        return (x.dim() == 3 and not self.training and not torch.is_grad_enabled()
+                and self._dense_threshold is None and not self.force_dense_when_full and not self.token_sparse
+                and self.router_top_p <= 0.0 and not self.linear_mem_budget_mb
+                and self.linear_latency_budget_ms is None and not self.quantize_sparse_int8
+                and not (self.small_seq_dense and x.shape[1] <= self.small_seq_dense)
+                and x.dtype in (torch.float32, torch.bfloat16, torch.float16))
+
+    _GRAPH_STATE = ("_last_batch_size", "_current_alpha", "_token_keep_ratio_runtime", "_last_target_k",
+                    "_last_gate_probs", "_last_token_similarity", "_last_token_blend", "_last_token_importance",
+                    "_last_token_mask", "_router_stats", "_proto_sums", "_last_shortlist_lengths",
+                    "_last_shortlist_backend_info", "_cached_active_mask", "_cached_packing", "_pending_summary",
+                    "last_head_consensus", "last_router_reg", "last_aux_loss")
+
+    def _graph_key(self, x: torch.Tensor):
+        T = int(x.shape[1])
+        return (tuple(x.shape), tuple(x.stride()), x.dtype, x.device, float(self._compute_cvt_alpha(T)),
+                int(self.linear_L), float(self._linear_L_scale_runtime), self._shortlist_alpha_override,
+                str(self.mode_setting))
+
+    def _capture_graph(self, x: torch.Tensor, key) -> dict:
+        self._resolve_stats()
+        device = x.device
+        bufs = {n: b.detach().clone() for n, b in self.named_buffers()}
+        xs = x.detach().clone()
+        timer_on = _hip.TIMER.enabled
+        _hip.TIMER.enabled = False
+        try:
+            side = torch.cuda.Stream(device=device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):
+                self._forward_impl(xs, capture=True)  # warm-up: library handles, lazy allocations
+            torch.cuda.current_stream(device).wait_stream(side)
+            with torch.no_grad():
+                for n, b in self.named_buffers():
+                    b.copy_(bufs[n])
+            if getattr(self, "_hip_graph_pool", None) is None:
+                self._hip_graph_pool = torch.cuda.graph_pool_handle()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool=self._hip_graph_pool):
+                attn, stats_args, label = self._forward_impl(xs, capture=True)
+        finally:
+            _hip.TIMER.enabled = timer_on
+        ent = {"graph": graph, "x": xs, "attn": attn, "stats_args": stats_args, "label": label,
+               "state": {k: self.__dict__.get(k) for k in self._GRAPH_STATE},
+               "sparse_state": self.__dict__.get("_lazy__last_sparse_state")}
+        self._hip_graphs[key] = ent
+        return ent
+
+    def _forward_graph(self, x: torch.Tensor) -> torch.Tensor:
+        key = self._graph_key(x)
+        ent = self._hip_graphs.get(key)
+        if ent is None:
+            ent = self._capture_graph(x, key)
+        ev0 = ev1 = None
+        if self.track_latency:
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
+        xs = ent["x"]
+        if x.data_ptr() != xs.data_ptr():
+            xs.copy_(x)
+        ent["graph"].replay()
+        y = self.dropout(self.proj(ent["attn"]))
+        for k, v in ent["state"].items():
+            self.__dict__[k] = v
+        st = ent["sparse_state"]
+        self._last_sparse_state = dict(st) if st is not None else None
+        self._finish_stats(*ent["stats_args"])
+        self._finish_forward(ent["label"], ev0, ev1)
+        return y
+
+    # ------------------------------------------------------------------
+    def _finish_forward(self, label: str, ev0, ev1) -> None:
+        """Latency and mode labels of this forward, deferred with its other
+        statistics (the latency needs the end event)."""
+        st_now = self.__dict__.get("_lazy__last_sparse_state")
+        if self.track_latency and ev0 is not None:
+            ev1.record()
+
+            def latency(st=st_now):
+                ev1.synchronize()
+                ms = float(ev0.elapsed_time(ev1))
+                prev = self.__dict__.get("_lazy__latency_ema")
+                self._latency_ema = ms if prev is None else 0.8 * prev + 0.2 * ms
+                hs = self.__dict__.get("_lazy_last_head_stats")
+                if hs is not None:
+                    hs["latency_ms"] = ms
+                if st is not None:
+                    st["latency_ms"] = ms
+
+            self._defer(latency)
+
+        def labels(st=st_now):
+            hs = self.__dict__.get("_lazy_last_head_stats")
+            if hs is not None:
+                hs["mode_setting"] = self.mode_setting
+                hs["mode_selected"] = label
+            if st is not None:
+                st["mode_selected"] = label
+
+        self._defer(labels)
+
+    def _forward_impl(self, x: torch.Tensor, capture: bool = False):
+        """The forward (aspa.py:1442-1932).  With capture=True nothing waits
+        on the host and the output projection, statistics and latency are
+        left to the caller: returns (attn, stats_args, label)."""
+        B, T, C = x.shape
+        device = x.device
         self.last_aux_loss = None
         self._last_token_importance = None
         self._last_token_mask = None
@@ -899,41 +1038,14 @@ class AdaptiveSparseAttention(nn.Module):
         if not self.proto_enabled:
             self._last_token_similarity = None
         ev0 = ev1 = None
-        if self.track_latency:
+        if self.track_latency and not capture:
             ev0 = torch.cuda.Event(enable_timing=True)
             ev1 = torch.cuda.Event(enable_timing=True)
             ev0.record()
         self._last_batch_size = B
 
         def finish(label: str) -> None:
-            # latency and labels land in the statistics of this forward; the
-            # latency needs the end event, so both are deferred with them
-            st_now = self.__dict__.get("_lazy__last_sparse_state")
-            if self.track_latency and ev0 is not None:
-                ev1.record()
-
-                def latency(st=st_now):
-                    ev1.synchronize()
-                    ms = float(ev0.elapsed_time(ev1))
-                    prev = self.__dict__.get("_lazy__latency_ema")
-                    self._latency_ema = ms if prev is None else 0.8 * prev + 0.2 * ms
-                    hs = self.__dict__.get("_lazy_last_head_stats")
-                    if hs is not None:
-                        hs["latency_ms"] = ms
-                    if st is not None:
-                        st["latency_ms"] = ms
-
-                self._defer(latency)
-
-            def labels(st=st_now):
-                hs = self.__dict__.get("_lazy_last_head_stats")
-                if hs is not None:
-                    hs["mode_setting"] = self.mode_setting
-                    hs["mode_selected"] = label
-                if st is not None:
-                    st["mode_selected"] = label
-
-            self._defer(labels)
+            self._finish_forward(label, ev0, ev1)
 
         if self.small_seq_dense and T <= self.small_seq_dense:
             y = self._forward_dense_fastpath(x)
@@ -1101,13 +1213,18 @@ class AdaptiveSparseAttention(nn.Module):
         if force_dense and token_mask is not None:
             attn.view(B, T, H, D).mul_(token_mask.view(B, T, 1, 1).to(attn.dtype))
         self.last_head_consensus = None if self.training else attn.detach()
+        self.last_router_reg = router_reg
+        stats_args = (token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
+                      dense_reason, B, T, active_heads, row_offsets, summary)
+        label = f"cvt(alpha={alpha:.2f})::{mode_label}"
+        if capture:
+            self._update_routing_prototypes(x, gate_probs)
+            return attn, stats_args, label
         y = self.dropout(self.proj(attn))
 
-        self._finish_stats(token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
-                           dense_reason, B, T, active_heads, row_offsets, summary)
-        self.last_router_reg = router_reg
+        self._finish_stats(*stats_args)
         self._update_routing_prototypes(x, gate_probs)
-        finish(f"cvt(alpha={alpha:.2f})::{mode_label}")
+        finish(label)
         if self.linear_mem_budget_mb and device.type == "cuda":
             allocated = torch.cuda.memory_allocated(device) / (1024 * 1024)
             if allocated > self.linear_mem_budget_mb * 1.1:
@@ -1219,12 +1336,21 @@ class AdaptiveSparseAttention(nn.Module):
         self._resolve_stats()
         H = self.h_total
         with torch.no_grad():
+            # one pinned staging tensor per source, kept across forwards: the
+            # previous forward's values were consumed by _resolve_stats above
+            bufs = self.__dict__.setdefault("_stats_host", {})
             host = []
-            for t in (self._router_stats, summary, active_heads):
-                h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+            for i, t in enumerate((self._router_stats, summary, active_heads)):
+                h = bufs.get(i)
+                if h is None or h.shape != t.shape or h.dtype != t.dtype:
+                    h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+                    bufs[i] = h
                 h.copy_(t, non_blocking=True)
                 host.append(h)
-            done = torch.cuda.Event()
+            done = self.__dict__.get("_stats_event")
+            if done is None:
+                done = torch.cuda.Event()
+                self.__dict__["_stats_event"] = done
             done.record()
         # everything the dictionaries need from the host side, as of now
         st = self.__dict__.get("_lazy__last_sparse_state")

@@ -547,6 +547,47 @@ def test_module_telemetry_deferred(dev):
     assert m._density_ema is not None and m._latency_ema is not None
 
 
+def test_module_hip_graph_replay_matches_eager(dev):
+    """Graph mode: every replay equals the eager forward on the same inputs
+    and state (the prototype EMA carries over between forwards), with eager
+    device work and synchronisations between replays; a second input shape
+    captures its own graph without disturbing the first."""
+    from configs import shortlist_cfg
+
+    _say("hip graph replay vs eager, T=4096 and T=2048")
+    cfg = shortlist_cfg(4096, 512, 8, 1024, 256, 64)
+    m, x = _module(cfg, 1, 4096, 512, torch.bfloat16, dev, 0.01)
+    init = {n: b.detach().clone() for n, b in m.named_buffers()}
+    xs = [x, (x * 0.5).contiguous(), torch.roll(x, 7, dims=1).contiguous(), x[:, :2048].contiguous(), x]
+
+    def run(graph: bool):
+        for n, b in m.named_buffers():
+            b.copy_(init[n])
+        m.enable_hip_graph(graph)
+        outs = []
+        with torch.no_grad():
+            for i, xi in enumerate(xs):
+                y = m(xi)
+                a = m.last_head_consensus.clone()
+                ent = m.last_head_stats["router_entropy"]
+                junk = torch.randn(1 << 20, device=dev).sum()  # eager work between replays
+                torch.cuda.synchronize()
+                outs.append((y.float().cpu(), a.float().cpu(), ent, m.routing_prototypes.float().cpu().clone(),
+                             float(junk)))
+        return outs
+
+    eager = run(False)
+    graph = run(True)
+    assert len(m._hip_graphs) == 2
+    for i, (e, g) in enumerate(zip(eager, graph)):
+        assert torch.equal(e[1], g[1]), f"forward {i}: attention output differs"
+        assert torch.equal(e[3], g[3]), f"forward {i}: prototype EMA differs"
+        assert (e[0] - g[0]).abs().max() <= TOL_BF16 * (1.0 + e[0].abs().max())
+        assert g[2] == pytest.approx(e[2], rel=1e-6)
+    m.enable_hip_graph(False)
+    assert not m._hip_graphs
+
+
 def test_module_dense_paths_vs_oracle(dev):
     """subquad mode (force-dense) and the small-sequence dense fast path
     equal dense causal attention of the projected q/k/v."""
