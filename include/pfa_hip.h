@@ -158,15 +158,28 @@ int pfa_pack_mask(const uint8_t* mask, int P, int64_t T, int32_t* row_offsets_ou
 /* ====================================================================
  * Prototype candidates: for every token t of every batch row b, the
  * indices of the min(t+1, K) largest proto_scores[b, 0..t] (ties -> lowest
- * index), written sorted by index into (B, T, K) int32 (entries past
- * min(t+1, K) hold t).  Optionally evict_out (B, T) int32: the first token
- * at which position p is no longer among the prefix top-K (INT32_MAX if
- * never, p if it never enters), so that p is in the set of token t exactly
- * when p <= t < evict[p].
- * Replaces the (rows, T) masked topk of _shortlist_prepare_proto_candidates
- * (sparse_attn.py:260-300) by a blocked prefix top-k.
+ * index).  Replaces the (rows, T) masked topk of
+ * _shortlist_prepare_proto_candidates (sparse_attn.py:260-300) by a
+ * superblock scan plus a rank-based parallel resolution of each 64-token
+ * block.  1 <= K <= 2048.
+ *
+ * pfa_proto_prefix_blocks writes the compact form:
+ *   blocks_out (B, ceil(T/64), K) int32: row j = the set of token 64j-1
+ *     (the prefix before block j) sorted by index, padded with INT32_MAX;
+ *   evict_out (B, T) int32: the first token at which position p is no
+ *     longer in the set (p if it never enters, INT32_MAX if it stays), so
+ *     that p is in the set of token t exactly when p <= t < evict[p], and
+ *     set(t) = { p in blocks[t/64] U {64*(t/64) .. t} : evict[p] > t }.
+ * pfa_proto_prefix_topk writes every token's set, sorted by index, into
+ * sets_out (B, T, K) int32 (entries past min(t+1, K) hold t); evict_out is
+ * optional there.  Both take the workspace sized by
+ * pfa_proto_prefix_workspace_size.
  * ==================================================================== */
 int pfa_proto_prefix_workspace_size(int B, int64_t T, int K, size_t* bytes);
+int pfa_proto_prefix_blocks(const float* proto_scores, int B, int64_t T,
+                            int64_t score_stride, int K, int32_t* blocks_out,
+                            int32_t* evict_out, void* workspace,
+                            size_t ws_bytes, void* stream);
 int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T,
                           int64_t score_stride, int K, int32_t* sets_out,
                           int32_t* evict_out, void* workspace, size_t ws_bytes,
@@ -245,8 +258,10 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
  * module's packed rows when no row is truncated (local_w + anchors below the
  * window + proto_k + 1 <= L, checked by the caller): each row attends to its
  * window [t - min(t+1, local_w) + 1, t], its strided anchors below the window
- * and its prototype prefix set below the window (proto_sets/proto_evict from
- * pfa_proto_prefix_topk), with the zero anchor, all on bf16 MFMA.
+ * and its prototype prefix set below the window (proto_blocks (B,
+ * ceil(T/64), proto_k) and proto_evict (B, T) from pfa_proto_prefix_blocks
+ * over the T tokens; proto_k <= 1024), with the zero anchor, all on bf16
+ * MFMA.
  * Replaces sparse_attn.py:457-596 + 597-921 on the module path
  * (aspa.py:1269-1302).
  *   row_of (B*H, T) from pfa_pack_rows; summary from pfa_pack_rows ({P,...});
@@ -261,10 +276,9 @@ int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                            const int32_t* head_map, int64_t N, int P_cap,
                            const int32_t* summary, const int32_t* row_of,
                            int local_w, int anchor_stride, int anchor_slots,
-                           const int32_t* proto_sets, int proto_k,
-                           int64_t proto_len, const int32_t* proto_evict,
-                           float scale, float* partials, int32_t* lengths,
-                           void* stream);
+                           const int32_t* proto_blocks, int proto_k,
+                           const int32_t* proto_evict, float scale,
+                           float* partials, int32_t* lengths, void* stream);
 
 /* Per compact head, the largest token among its packed rows (needed by the
  * explicit-mask branch: sparse_attn.py:1010-1015). */

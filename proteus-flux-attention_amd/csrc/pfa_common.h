@@ -151,9 +151,10 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // Order used by every top-k in this library: larger value first, equal
-// values -> smaller index first.  NaN compares as smaller than anything.
+// values -> smaller index first.  NaN compares as smaller than anything
+// else (two NaNs: smaller index first), so the order is strict and total.
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
-  return (va > vb) || (va == vb && ia < ib) || (vb != vb && va == va);
+  return (va > vb) || (va == vb && ia < ib) || (vb != vb && (va == va || ia < ib));
 }
 
 }  // namespace pfa

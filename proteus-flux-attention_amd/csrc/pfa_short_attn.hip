@@ -9,7 +9,8 @@
 //          clamped anchor 0 when max(t - s*slots, 0) == 0 is not itself a
 //          strided anchor ("zero anchor")
 // and a position p belongs to the prototype prefix set of t exactly when
-// p <= t < evict[p] (evict from pfa_proto_prefix_topk).
+// p <= t < evict[p]; the set of t is drawn from the set table row of t's
+// 64-token block plus the block's own tokens (pfa_proto_prefix_blocks).
 //
 // Pass 1, short_anchor_kernel: one workgroup per (compact head, residue class
 // c = t mod s).  The anchors of every row of the class lie on the strided
@@ -53,10 +54,10 @@ struct ShortArgs {
   const int32_t* head_map;
   int64_t N;
   int local_w, stride, slots;
-  const int32_t* sets;   // (B, plen, K) or null
+  const int32_t* blk;    // (B, nblk, K) prefix set table rows, or null
   int K;
-  int64_t plen;
-  const int32_t* evict;  // (B, plen) or null
+  int64_t nblk;
+  const int32_t* evict;  // (B, T) or null
   const int32_t* row_of; // (B*H, T)
   const int32_t* summary;
   float* part;           // (N, kPartW)
@@ -309,8 +310,8 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
   __shared__ int32_t r_p[kRows];
   __shared__ int32_t seg_begin[kRows + 1];
   __shared__ int s_nseg;
-  __shared__ int32_t plist[kMaxProto + 1];
-  __shared__ int32_t pev[kMaxProto + 1];
+  __shared__ int32_t plist[kMaxProto + 64 + 1];
+  __shared__ int32_t pev[kMaxProto + 64 + 1];
   __shared__ int s_plen;
 
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
@@ -353,24 +354,46 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
     const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
     const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
 
-    // prototype key list: prefix set of t_first below lo_last, then key 0
+    // prototype key list: the prefix set of t_first below lo_last (set table
+    // row of t_first's block, then the block's tokens up to t_first, both
+    // ascending, keeping p with evict[p] > t_first), then key 0
     if (tid < 64) {
       int n = 0;
-      if (a.sets != nullptr) {
-        const int64_t prow = t_first < a.plen - 1 ? t_first : a.plen - 1;
-        const int32_t* S = a.sets + (bb * a.plen + prow) * a.K;
+      if (a.blk != nullptr) {
+        const uint64_t lt = (1ull << lane) - 1;
+        const int64_t jb = t_first >> 6;
+        const int32_t* P = a.blk + (bb * a.nblk + jb) * a.K;
+        const int32_t* ev = a.evict + bb * a.T;
         for (int base = 0; base < a.K; base += 64) {
           const int j = base + lane;
-          const int32_t v = j < a.K ? S[j] : INT32_MAX;
-          const bool below = j < a.K && v < lo_last;
-          const uint64_t bal = __ballot(below);
-          if (below) {
-            plist[n + j - base] = v;
-            pev[n + j - base] = a.evict[bb * a.plen + v];
+          const int32_t v = j < a.K ? P[j] : INT32_MAX;
+          bool keep = false;
+          int32_t e = 0;
+          if (v < lo_last) {
+            e = ev[v];
+            keep = (int64_t)e > t_first;
+          }
+          const uint64_t bal = __ballot(keep);
+          if (keep) {
+            plist[n + __popcll(bal & lt)] = v;
+            pev[n + __popcll(bal & lt)] = e;
           }
           n += __popcll(bal);
-          if (bal != ~0ull) break;
+          if (__ballot(v >= lo_last)) break;  // ascending: nothing further lies below lo_last
         }
+        const int64_t q = (jb << 6) + lane;
+        bool keep = false;
+        int32_t e = 0;
+        if (q <= t_first && q < lo_last) {
+          e = ev[q];
+          keep = (int64_t)e > t_first;
+        }
+        const uint64_t bal = __ballot(keep);
+        if (keep) {
+          plist[n + __popcll(bal & lt)] = (int32_t)q;
+          pev[n + __popcll(bal & lt)] = e;
+        }
+        n += __popcll(bal);
       }
       if (lo_last > 0 && a.stride > 0 && a.slots > 0) {
         // append key 0 for the zero-anchor rule unless the (ascending) list
@@ -489,8 +512,8 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
                                       int64_t T, int D, const int32_t* token_idx, const int32_t* row_head,
                                       const int32_t* head_map, int64_t N, int P_cap, const int32_t* summary,
                                       const int32_t* row_of, int local_w, int anchor_stride, int anchor_slots,
-                                      const int32_t* proto_sets, int proto_k, int64_t proto_len,
-                                      const int32_t* proto_evict, float scale, float* partials, int32_t* lengths,
+                                      const int32_t* proto_blocks, int proto_k, const int32_t* proto_evict,
+                                      float scale, float* partials, int32_t* lengths,
                                       void* stream) {
   clear_error();
   PFA_CHECK_ARG(dtype == PFA_BF16 && D == 64, "pfa_shortlist_attn_fwd: bf16 and D=64 only (got dtype %d D %d)", dtype,
@@ -499,7 +522,7 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   if (N == 0) return PFA_OK;
   PFA_CHECK_ARG(q.ptr && k.ptr && v.ptr && out.ptr && token_idx && row_head && summary,
                 "pfa_shortlist_attn_fwd: null pointer");
-  PFA_CHECK_ARG(proto_sets == nullptr || (proto_k > 0 && proto_k <= kMaxProto && proto_evict && proto_len > 0),
+  PFA_CHECK_ARG(proto_blocks == nullptr || (proto_k > 0 && proto_k <= kMaxProto && proto_evict),
                 "pfa_shortlist_attn_fwd: prototype table (K <= %d with evict) required", kMaxProto);
   const bool anchors = anchor_stride > 0 && anchor_slots > 0;
   PFA_CHECK_ARG(!anchors || (row_of && partials), "pfa_shortlist_attn_fwd: anchors need row_of and partials");
@@ -513,7 +536,7 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   a.q = q; a.k = k; a.v = v; a.out = out;
   a.H = H; a.T = T; a.token_idx = token_idx; a.row_head = row_head; a.head_map = head_map; a.N = N;
   a.local_w = local_w; a.stride = anchor_stride; a.slots = anchor_slots;
-  a.sets = proto_sets; a.K = proto_k; a.plen = proto_len; a.evict = proto_evict;
+  a.blk = proto_blocks; a.K = proto_k; a.nblk = (T + 63) / 64; a.evict = proto_evict;
   a.row_of = row_of; a.summary = summary; a.part = partials; a.lengths = lengths;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = as_stream(stream);

@@ -1,17 +1,34 @@
 // Shortlist candidates: prototype prefix top-k and the packed builder.
 //
 // Prototype prefix top-k (replaces the O(rows*T) masked torch.topk of
-// sparse_attn.py:260-300).  For batch b and token t the set is the
-// min(t+1, K) largest scores among positions 0..t, ties to the lowest
-// index.  Tokens are cut into blocks of 64:
-//   1. block_sort : each block's scores sorted (value desc, index asc) by a
-//                   wave-wide bitonic network in registers, truncated to K;
-//   2. scan_level : Hillis-Steele inclusive scan over blocks whose operator
-//                   is "top-K of the union of two sorted lists" (merge path);
-//   3. block_walk : one wave per block starts from the exclusive prefix
-//                   (re-sorted by index in LDS) and walks its 64 tokens in
-//                   order, replacing the current minimum whenever a better
-//                   score arrives, writing each token's set sorted by index.
+// sparse_attn.py:260-300).  For batch b and token t the set S(t) is the
+// min(t+1, K) largest scores among positions 0..t under the order "larger
+// value first, equal values -> smaller index first".  Tokens are cut into
+// blocks of 64 and blocks into superblocks of `sbs` blocks:
+//   1. block_sort : each block's scores sorted best first (wave bitonic);
+//   2. sb_local   : per superblock, one workgroup folds its blocks in order:
+//                   Q[j] = top-K of the superblock's tokens up to block j;
+//   3. sb_scan    : one workgroup folds the superblock totals:
+//                   R[s] = top-K of all tokens before superblock s;
+//   4. block_walk : per block j, P = top-K(R[s] U Q[j-1]) = S(64j - 1) is
+//                   written sorted by index (the block's set table row), and
+//                   the block's tokens are resolved in parallel from exact
+//                   rank counts (below);
+//   5. expand     : (optional) S(t) for every token, sorted by index.
+//
+// Block walk without a sequential loop.  Let P be the set entering block j
+// (sorted best first, n = |P| <= K) and B the block's tokens.  A token t
+// enters iff fewer than K elements of P U {q in B, q < t} are better than
+// t.  The set after the block is F = top-K(P U B).  Every element of
+// P U entered that is not in F leaves during the block; since the K-th best
+// element only rises, they leave in increasing key order, and the i-th
+// insertion that finds the set full evicts the i-th of them.  With ranks in
+// P U B (F occupies ranks < K), the leaver at rank r is evicted by entered
+// token number max(0, K - n) + #(leavers with rank >= r) - 1.  Hence
+//   evict[p] = first token at which p is no longer in the set, p if it never
+//   enters, INT32_MAX if it is still in the set at the end,
+// and p is in S(t) exactly when p <= t < evict[p]; so
+//   S(t) = { p in P(block of t) U {64j .. t} : evict[p] > t }.
 //
 // Builder (replaces sparse_attn.py:376-596).  Per row, everything below the
 // local window start `lo` (strided anchors in closed form, the prototype set
@@ -24,31 +41,44 @@ namespace pfa {
 
 constexpr int kBlk = 64;  // tokens per prefix block (one wave)
 
-struct PrefixWs {
-  float* val[2];
-  int32_t* idx[2];
-  int32_t* len[2];
-};
-
-static size_t prefix_ws_bytes(int64_t B, int64_t nb, int64_t K) {
-  size_t lists = (size_t)B * nb * K;
-  size_t one = ((lists * 4 + 255) & ~(size_t)255);
-  size_t lens = (((size_t)B * nb * 4 + 255) & ~(size_t)255);
-  return 2 * (2 * one + lens);
+static int64_t prefix_sbs(int64_t nb) {
+  int64_t s = 1;
+  while (s * s < 2 * nb) s <<= 1;
+  return s;
 }
 
-static PrefixWs carve_prefix(void* ws, int64_t B, int64_t nb, int64_t K) {
-  size_t lists = (size_t)B * nb * K;
-  size_t one = ((lists * 4 + 255) & ~(size_t)255);
-  size_t lens = (((size_t)B * nb * 4 + 255) & ~(size_t)255);
-  char* p = (char*)ws;
-  PrefixWs w;
-  for (int i = 0; i < 2; ++i) {
-    w.val[i] = (float*)p; p += one;
-    w.idx[i] = (int32_t*)p; p += one;
-    w.len[i] = (int32_t*)p; p += lens;
-  }
-  return w;
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct PrefixWs {
+  float* bval;
+  int32_t* bidx;
+  int32_t* blen;
+  float* qval;
+  int32_t* qidx;
+  int32_t* qlen;
+  float* rval;
+  int32_t* ridx;
+  int32_t* rlen;
+  int32_t* blk;    // (B, nb, K) set table (used by pfa_proto_prefix_topk)
+  int32_t* evict;  // (B, T) (used when the caller passes no evict array)
+};
+
+static size_t prefix_ws_bytes(int64_t B, int64_t T, int64_t nb, int64_t nsb, int64_t K, PrefixWs* w, char* base) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return base ? base + o : nullptr; };
+  char* p;
+  p = take((size_t)B * nb * kBlk * 4); if (w) w->bval = (float*)p;
+  p = take((size_t)B * nb * kBlk * 4); if (w) w->bidx = (int32_t*)p;
+  p = take((size_t)B * nb * 4);        if (w) w->blen = (int32_t*)p;
+  p = take((size_t)B * nb * K * 4);    if (w) w->qval = (float*)p;
+  p = take((size_t)B * nb * K * 4);    if (w) w->qidx = (int32_t*)p;
+  p = take((size_t)B * nb * 4);        if (w) w->qlen = (int32_t*)p;
+  p = take((size_t)B * nsb * K * 4);   if (w) w->rval = (float*)p;
+  p = take((size_t)B * nsb * K * 4);   if (w) w->ridx = (int32_t*)p;
+  p = take((size_t)B * nsb * 4);       if (w) w->rlen = (int32_t*)p;
+  p = take((size_t)B * nb * K * 4);    if (w) w->blk = (int32_t*)p;
+  p = take((size_t)B * T * 4);         if (w) w->evict = (int32_t*)p;
+  return off;
 }
 
 // Sort (v, i) across the 64 lanes of a wave: best first.
@@ -75,7 +105,7 @@ prefix_block_sort(const float* __restrict__ scores, int64_t T, int64_t stride, i
                   int32_t* __restrict__ evict) {
   const int j = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   int64_t t = (int64_t)j * kBlk + lane;
-  if (evict != nullptr && t < T) evict[(int64_t)b * T + t] = INT32_MAX;
+  if (t < T) evict[(int64_t)b * T + t] = INT32_MAX;
   float v = -INFINITY;
   int i = INT32_MAX;
   if (t < T) { v = scores[(int64_t)b * stride + t]; i = (int)t; }
@@ -83,147 +113,271 @@ prefix_block_sort(const float* __restrict__ scores, int64_t T, int64_t stride, i
   int64_t n = T - (int64_t)j * kBlk;
   if (n > kBlk) n = kBlk;
   if (n > K) n = K;
-  int64_t base = ((int64_t)b * nb + j) * K;
+  int64_t base = ((int64_t)b * nb + j) * kBlk;
   if (lane < n) { oval[base + lane] = v; oidx[base + lane] = i; }
   if (lane == 0) olen[(int64_t)b * nb + j] = (int)n;
 }
 
-// out[j] = topK(in[j-d] U in[j]) for j >= d, else copy.  Both inputs are
-// staged in LDS (2 x K x 8 bytes) so the co-rank searches stay on chip.
-__global__ void __launch_bounds__(64)
-prefix_scan_level(int nb, int K, int d, const float* __restrict__ ival, const int32_t* __restrict__ iidx,
-                  const int32_t* __restrict__ ilen, float* __restrict__ oval, int32_t* __restrict__ oidx,
-                  int32_t* __restrict__ olen) {
+// Element p of top-K(a U c) for best-first lists a (na) and c (nc), by a
+// merge-path co-rank.  Either list may live in LDS or global memory.
+__device__ __forceinline__ void merge_at(int p, const float* av, const int32_t* ai, int na, const float* cv,
+                                         const int32_t* ci, int nc, float& ov, int32_t& oi) {
+  int lo = max(0, p - nc), hi = min(p, na);
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if (better(av[mid], ai[mid], cv[p - 1 - mid], ci[p - 1 - mid])) lo = mid + 1;
+    else hi = mid;
+  }
+  const int ia = lo, ic = p - lo;
+  const bool take_a = ia < na && (ic >= nc || better(av[ia], ai[ia], cv[ic], ci[ic]));
+  ov = take_a ? av[ia] : cv[ic];
+  oi = take_a ? ai[ia] : ci[ic];
+}
+
+// Q[j] = top-K(Q[j-1] U block j) within each superblock (one workgroup).
+__global__ void __launch_bounds__(256)
+prefix_sb_local(int nb, int sbs, int K, const float* __restrict__ bval, const int32_t* __restrict__ bidx,
+                const int32_t* __restrict__ blen, float* __restrict__ qval, int32_t* __restrict__ qidx,
+                int32_t* __restrict__ qlen) {
   extern __shared__ char smem[];
-  float* av = (float*)smem;
-  int32_t* ai = (int32_t*)(av + K);
-  float* bv = (float*)(ai + K);
-  int32_t* bi = (int32_t*)(bv + K);
-  const int j = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const int64_t rowj = (int64_t)b * nb + j;
-  const int nbl = ilen[rowj];
-  if (j < d) {
-    for (int p = lane; p < nbl; p += 64) { oval[rowj * K + p] = ival[rowj * K + p]; oidx[rowj * K + p] = iidx[rowj * K + p]; }
-    if (lane == 0) olen[rowj] = nbl;
-    return;
-  }
-  const int64_t rowa = rowj - d;
-  const int na = ilen[rowa];
-  for (int p = lane; p < na; p += 64) { av[p] = ival[rowa * K + p]; ai[p] = iidx[rowa * K + p]; }
-  for (int p = lane; p < nbl; p += 64) { bv[p] = ival[rowj * K + p]; bi[p] = iidx[rowj * K + p]; }
-  __syncthreads();
-  const int m = min(K, na + nbl);
-  for (int p = lane; p < m; p += 64) {
-    int lo = max(0, p - nbl), hi = min(p, na);
-    while (lo < hi) {
-      int mid = (lo + hi) >> 1;
-      if (better(av[mid], ai[mid], bv[p - 1 - mid], bi[p - 1 - mid])) lo = mid + 1;
-      else hi = mid;
+  float* cv0 = (float*)smem;
+  int32_t* ci0 = (int32_t*)(cv0 + K);
+  float* cv1 = (float*)(ci0 + K);
+  int32_t* ci1 = (int32_t*)(cv1 + K);
+  float* kv = (float*)(ci1 + K);
+  int32_t* ki = (int32_t*)(kv + kBlk);
+  const int sb = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int j0 = sb * sbs, j1 = min(nb, j0 + sbs);
+  int n = 0, cur = 0;
+  for (int j = j0; j < j1; ++j) {
+    const int64_t row = (int64_t)b * nb + j;
+    const int nbl = blen[row];
+    if (tid < nbl) { kv[tid] = bval[row * kBlk + tid]; ki[tid] = bidx[row * kBlk + tid]; }
+    __syncthreads();
+    const int m = min(K, n + nbl);
+    const float* av = cur ? cv1 : cv0;
+    const int32_t* ai = cur ? ci1 : ci0;
+    float* ov = cur ? cv0 : cv1;
+    int32_t* oi = cur ? ci0 : ci1;
+    for (int p = tid; p < m; p += 256) {
+      float vv;
+      int32_t ii;
+      merge_at(p, av, ai, n, kv, ki, nbl, vv, ii);
+      ov[p] = vv;
+      oi[p] = ii;
+      qval[row * K + p] = vv;
+      qidx[row * K + p] = ii;
     }
-    int ia = lo, ib = p - lo;
-    bool take_a = ia < na && (ib >= nbl || better(av[ia], ai[ia], bv[ib], bi[ib]));
-    oval[rowj * K + p] = take_a ? av[ia] : bv[ib];
-    oidx[rowj * K + p] = take_a ? ai[ia] : bi[ib];
-  }
-  if (lane == 0) olen[rowj] = m;
-}
-
-// LDS bitonic sort by index ascending of n (<= cap, power of two) entries.
-__device__ void lds_sort_by_index(float* v, int32_t* ix, int cap) {
-  const int lane = threadIdx.x & 63;
-  for (int k = 2; k <= cap; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int e = lane; e < cap; e += 64) {
-        int p = e ^ j;
-        if (p > e) {
-          bool up = (e & k) == 0;
-          int a = ix[e], c = ix[p];
-          bool swap = up ? (a > c) : (a < c);
-          if (swap) {
-            ix[e] = c; ix[p] = a;
-            float tv = v[e]; v[e] = v[p]; v[p] = tv;
-          }
-        }
-      }
-      __syncthreads();
-    }
+    if (tid == 0) qlen[row] = m;
+    __syncthreads();
+    cur ^= 1;
+    n = m;
   }
 }
 
-// One wave per (batch, block).  LDS: value + index arrays of `cap` entries
-// (cap = next power of two >= K).
-__global__ void __launch_bounds__(64)
-prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int K, int cap,
-                  const float* __restrict__ pval, const int32_t* __restrict__ pidx, const int32_t* __restrict__ plen,
-                  int32_t* __restrict__ sets, int32_t* __restrict__ evict) {
+// R[s] = top-K of every token before superblock s (one workgroup per batch).
+__global__ void __launch_bounds__(256)
+prefix_sb_scan(int nb, int sbs, int nsb, int K, const float* __restrict__ qval, const int32_t* __restrict__ qidx,
+               const int32_t* __restrict__ qlen, float* __restrict__ rval, int32_t* __restrict__ ridx,
+               int32_t* __restrict__ rlen) {
+  extern __shared__ char smem[];
+  float* cv0 = (float*)smem;
+  int32_t* ci0 = (int32_t*)(cv0 + K);
+  float* cv1 = (float*)(ci0 + K);
+  int32_t* ci1 = (int32_t*)(cv1 + K);
+  const int b = blockIdx.x, tid = threadIdx.x;
+  if (tid == 0) rlen[(int64_t)b * nsb] = 0;
+  int n = 0, cur = 0;
+  for (int s = 1; s < nsb; ++s) {
+    const int64_t qrow = (int64_t)b * nb + (int64_t)s * sbs - 1;  // last block of superblock s-1
+    const int nt = qlen[qrow];
+    const float* tv = qval + qrow * K;
+    const int32_t* ti = qidx + qrow * K;
+    const int m = min(K, n + nt);
+    const float* av = cur ? cv1 : cv0;
+    const int32_t* ai = cur ? ci1 : ci0;
+    float* ov = cur ? cv0 : cv1;
+    int32_t* oi = cur ? ci0 : ci1;
+    const int64_t rrow = (int64_t)b * nsb + s;
+    for (int p = tid; p < m; p += 256) {
+      float vv;
+      int32_t ii;
+      merge_at(p, av, ai, n, tv, ti, nt, vv, ii);
+      ov[p] = vv;
+      oi[p] = ii;
+      rval[rrow * K + p] = vv;
+      ridx[rrow * K + p] = ii;
+    }
+    if (tid == 0) rlen[rrow] = m;
+    __syncthreads();
+    cur ^= 1;
+    n = m;
+  }
+}
+
+// One workgroup (256 threads) per (block j, batch b).  LDS: the entering set
+// P best first (cap entries, cap = power of two >= K), an index-sorted copy,
+// the rank of each element of P, and the block's 64 tokens.
+__global__ void __launch_bounds__(256)
+prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int sbs, int nsb, int K,
+                  int cap, const float* __restrict__ qval, const int32_t* __restrict__ qidx,
+                  const int32_t* __restrict__ qlen, const float* __restrict__ rval, const int32_t* __restrict__ ridx,
+                  const int32_t* __restrict__ rlen, int32_t* __restrict__ blk_out, int32_t* __restrict__ evict) {
   extern __shared__ char smem[];
   float* v = (float*)smem;
   int32_t* ix = (int32_t*)(v + cap);
-  const int j = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  int n = 0;
-  if (j > 0) {
-    const int64_t row = (int64_t)b * nb + (j - 1);
-    n = plen[row];
-    for (int p = lane; p < cap; p += 64) {
-      if (p < n) { v[p] = pval[row * K + p]; ix[p] = pidx[row * K + p]; }
-      else { v[p] = -INFINITY; ix[p] = INT32_MAX; }
+  int32_t* srt = ix + cap;
+  int32_t* rk = srt + cap;
+  __shared__ float bv[kBlk];
+  __shared__ int32_t bi[kBlk];
+  __shared__ int32_t flag[kBlk];
+  __shared__ int32_t ent[kBlk];
+  __shared__ uint64_t s_fl;
+  __shared__ int s_nent;
+  const int j = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int s = j / sbs, k = j % sbs;
+  const int64_t rrow = (int64_t)b * nsb + s;
+  const int na = rlen[rrow];
+  const float* av = rval + rrow * K;
+  const int32_t* ai = ridx + rrow * K;
+  int nq = 0;
+  const float* cq = qval;
+  const int32_t* ciq = qidx;
+  if (k > 0) {
+    const int64_t qrow = (int64_t)b * nb + j - 1;
+    nq = qlen[qrow];
+    cq = qval + qrow * K;
+    ciq = qidx + qrow * K;
+  }
+  const int n = min(K, na + nq);
+  for (int p = tid; p < cap; p += 256) {
+    if (p < n) {
+      float vv;
+      int32_t ii;
+      merge_at(p, av, ai, na, cq, ciq, nq, vv, ii);
+      v[p] = vv;
+      ix[p] = ii;
+      srt[p] = ii;
+    } else {
+      srt[p] = INT32_MAX;
     }
-  } else {
-    for (int p = lane; p < cap; p += 64) { v[p] = -INFINITY; ix[p] = INT32_MAX; }
+  }
+  const int64_t t0 = (int64_t)j * kBlk;
+  const int nB = (int)min<int64_t>(kBlk, T - t0);
+  float sv = -INFINITY;
+  int32_t st = INT32_MAX;
+  if (tid < kBlk) {
+    if (tid < nB) { sv = scores[(int64_t)b * stride + t0 + tid]; st = (int32_t)(t0 + tid); }
+    bv[tid] = sv;
+    bi[tid] = st;
+    flag[tid] = 0;
   }
   __syncthreads();
-  if (n > 1) lds_sort_by_index(v, ix, cap);
-  const int64_t t0 = (int64_t)j * kBlk;
-  const int64_t t1 = min(T, t0 + kBlk);
-  for (int64_t t = t0; t < t1; ++t) {
-    float s = scores[(int64_t)b * stride + t];
-    if (n < K) {
-      if (lane == 0) { v[n] = s; ix[n] = (int)t; }
-      ++n;
-      __syncthreads();
-    } else {
-      // worst element of the current set
-      float wv = INFINITY;
-      int wi = -1, wp = -1;
-      for (int p = lane; p < n; p += 64) {
-        if (wp < 0 || better(wv, wi, v[p], ix[p])) { wv = v[p]; wi = ix[p]; wp = p; }
-      }
-      for (int off = 32; off > 0; off >>= 1) {
-        float ov = __shfl_xor(wv, off, 64);
-        int oi = __shfl_xor(wi, off, 64), op = __shfl_xor(wp, off, 64);
-        bool take;
-        if (op < 0) take = false;
-        else if (wp < 0) take = true;
-        else take = better(wv, wi, ov, oi);
-        if (take) { wv = ov; wi = oi; wp = op; }
-      }
-      if (!better(s, (int)t, wv, wi)) {
-        if (evict != nullptr && lane == 0) evict[(int64_t)b * T + t] = (int32_t)t;  // never enters
-      } else {
-        if (evict != nullptr && lane == 0) evict[(int64_t)b * T + wi] = (int32_t)t;  // wi leaves at t
-        float tv[4];
-        int ti[4];
-        int cnt = 0;
-        for (int p = wp + 1 + lane; p < n && cnt < 4; p += 64, ++cnt) { tv[cnt] = v[p]; ti[cnt] = ix[p]; }
-        // n - wp - 1 may exceed 256: loop in rounds
-        int p0 = wp + 1;
-        while (true) {
-          __syncthreads();
-          int c = 0;
-          for (int p = p0 + lane; p < n && c < 4; p += 64, ++c) { v[p - 1] = tv[c]; ix[p - 1] = ti[c]; }
-          p0 += 256;
-          __syncthreads();
-          if (p0 >= n) break;
-          c = 0;
-          for (int p = p0 + lane; p < n && c < 4; p += 64, ++c) { tv[c] = v[p]; ti[c] = ix[p]; }
+  // the block's set table row: P sorted by index (bitonic over cap entries)
+  for (int kk = 2; kk <= cap; kk <<= 1) {
+    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+      for (int e = tid; e < cap; e += 256) {
+        const int q = e ^ jj;
+        if (q > e) {
+          const int x = srt[e], y = srt[q];
+          if (((e & kk) == 0) ? (x > y) : (x < y)) { srt[e] = y; srt[q] = x; }
         }
-        if (lane == 0) { v[n - 1] = s; ix[n - 1] = (int)t; }
-        __syncthreads();
+      }
+      __syncthreads();
+    }
+  }
+  int32_t* orow = blk_out + ((int64_t)b * nb + j) * K;
+  for (int p = tid; p < K; p += 256) orow[p] = srt[p];
+  // ranks of P's elements in P U B (P is sorted best first)
+  for (int p = tid; p < n; p += 256) {
+    int c = 0;
+    for (int q = 0; q < nB; ++q) c += better(bv[q], bi[q], v[p], ix[p]) ? 1 : 0;
+    const int r = p + c;
+    rk[p] = r;
+    if (r >= K) flag[r - K] = 1;
+  }
+  // the block's tokens (wave 0)
+  bool enters = false;
+  int rt = 0;
+  if (tid < kBlk && tid < nB) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (better(v[mid], ix[mid], sv, st)) lo = mid + 1;
+      else hi = mid;
+    }
+    int ra = 0, rb = 0;
+    for (int q = 0; q < nB; ++q) {
+      if (better(bv[q], bi[q], sv, st)) {
+        ++ra;
+        if (q < tid) ++rb;
       }
     }
-    int32_t* out = sets + ((int64_t)b * T + t) * K;
-    for (int p = lane; p < K; p += 64) out[p] = (p < n) ? ix[p] : (int32_t)t;
+    enters = lo + rb < K;
+    rt = lo + ra;
+    if (enters && rt >= K) flag[rt - K] = 1;
   }
+  __syncthreads();
+  if (tid < kBlk) {
+    const uint64_t fl = __ballot(flag[tid] != 0);
+    const uint64_t em = __ballot(enters);
+    if (enters) ent[__popcll(em & ((1ull << tid) - 1))] = st;
+    if (tid == 0) { s_fl = fl; s_nent = __popcll(em); }
+  }
+  __syncthreads();
+  const uint64_t fl = s_fl;
+  const int nent = s_nent;
+  const int free_ins = max(0, K - n);
+  int32_t* ev = evict + (int64_t)b * T;
+  for (int p = tid; p < n; p += 256) {
+    const int r = rk[p];
+    if (r >= K) {
+      const int e = free_ins + __popcll(fl >> (r - K)) - 1;
+      if (e >= 0 && e < nent) ev[ix[p]] = ent[e];
+    }
+  }
+  if (tid < kBlk && tid < nB) {
+    if (!enters) {
+      ev[st] = st;
+    } else if (rt >= K) {
+      const int e = free_ins + __popcll(fl >> (rt - K)) - 1;
+      if (e >= 0 && e < nent) ev[st] = ent[e];
+    }
+  }
+}
+
+// S(t) for every token, sorted by index, entries past min(t+1, K) = t.
+// One wave per token.
+__global__ void __launch_bounds__(256)
+prefix_expand(int64_t T, int nb, int K, const int32_t* __restrict__ blk, const int32_t* __restrict__ evict,
+              int32_t* __restrict__ sets) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int b = blockIdx.y;
+  if (t >= T) return;
+  const int64_t j = t / kBlk;
+  const int32_t* P = blk + ((int64_t)b * nb + j) * K;
+  const int32_t* ev = evict + (int64_t)b * T;
+  int32_t* out = sets + ((int64_t)b * T + t) * K;
+  const uint64_t lt = (1ull << lane) - 1;
+  int n = 0;
+  for (int base = 0; base < K; base += 64) {
+    const int p = base + lane;
+    const int32_t x = p < K ? P[p] : INT32_MAX;
+    const bool keep = x != INT32_MAX && ev[x] > t;
+    const uint64_t m = __ballot(keep);
+    if (keep) out[n + __popcll(m & lt)] = x;
+    n += __popcll(m);
+    if (__ballot(x == INT32_MAX)) break;
+  }
+  {
+    const int64_t q = j * kBlk + lane;
+    const bool keep = q <= t && ev[q] > t;
+    const uint64_t m = __ballot(keep);
+    if (keep) out[n + __popcll(m & lt)] = (int32_t)q;
+    n += __popcll(m);
+  }
+  for (int p = n + lane; p < K; p += 64) out[p] = (int32_t)t;
 }
 
 // ------------------------------------------------------------------
@@ -417,48 +571,81 @@ shortlist_build_kernel(const int32_t* __restrict__ rows, const int32_t* __restri
 
 using namespace pfa;
 
+static constexpr int kPrefixMaxK = 2048;
+
+static int prefix_cap(int K) {
+  int cap = 64;
+  while (cap < K) cap <<= 1;
+  return cap;
+}
+
 extern "C" int pfa_proto_prefix_workspace_size(int B, int64_t T, int K, size_t* bytes) {
   clear_error();
   PFA_CHECK_ARG(bytes && B >= 0 && T >= 0 && K > 0, "pfa_proto_prefix_workspace_size: bad arguments");
   int64_t nb = (T + kBlk - 1) / kBlk;
   if (nb < 1) nb = 1;
-  *bytes = prefix_ws_bytes(B, nb, K);
+  const int64_t sbs = prefix_sbs(nb);
+  const int64_t nsb = (nb + sbs - 1) / sbs;
+  *bytes = prefix_ws_bytes(B, T, nb, nsb, K, nullptr, nullptr);
   return PFA_OK;
+}
+
+// Steps 1-4: set table rows (B, nb, K) and evict (B, T).
+static int prefix_blocks(const float* scores, int B, int64_t T, int64_t stride, int K, int32_t* blk,
+                         int32_t* evict, const PrefixWs& w, int64_t nb, hipStream_t s) {
+  const int64_t sbs = prefix_sbs(nb);
+  const int64_t nsb = (nb + sbs - 1) / sbs;
+  const int cap = prefix_cap(K);
+  dim3 grid((unsigned)nb, (unsigned)B);
+  prefix_block_sort<<<grid, 64, 0, s>>>(scores, T, stride, (int)nb, K, w.bval, w.bidx, w.blen, evict);
+  PFA_CHECK_LAUNCH("pfa_proto_prefix/sort");
+  prefix_sb_local<<<dim3((unsigned)nsb, (unsigned)B), 256, (size_t)K * 16 + kBlk * 8, s>>>(
+      (int)nb, (int)sbs, K, w.bval, w.bidx, w.blen, w.qval, w.qidx, w.qlen);
+  PFA_CHECK_LAUNCH("pfa_proto_prefix/local");
+  prefix_sb_scan<<<(unsigned)B, 256, (size_t)K * 16, s>>>((int)nb, (int)sbs, (int)nsb, K, w.qval, w.qidx, w.qlen,
+                                                          w.rval, w.ridx, w.rlen);
+  PFA_CHECK_LAUNCH("pfa_proto_prefix/scan");
+  prefix_block_walk<<<grid, 256, (size_t)cap * 16, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K, cap,
+                                                         w.qval, w.qidx, w.qlen, w.rval, w.ridx, w.rlen, blk, evict);
+  PFA_CHECK_LAUNCH("pfa_proto_prefix/walk");
+  return PFA_OK;
+}
+
+#define PFA_PREFIX_SETUP(NAME)                                                                              \
+  clear_error();                                                                                            \
+  PFA_CHECK_ARG(proto_scores && workspace && B > 0 && T > 0 && K > 0 && K <= kPrefixMaxK,                   \
+                NAME ": bad arguments (B=%d T=%lld K=%d, K <= %d)", B, (long long)T, K, kPrefixMaxK);       \
+  PFA_CHECK_ARG(T < ((int64_t)1 << 31), NAME ": T too large");                                              \
+  const int64_t nb = (T + kBlk - 1) / kBlk;                                                                 \
+  const int64_t sbs = prefix_sbs(nb);                                                                       \
+  const int64_t nsb = (nb + sbs - 1) / sbs;                                                                 \
+  const size_t need = prefix_ws_bytes(B, T, nb, nsb, K, nullptr, nullptr);                                  \
+  if (ws_bytes < need) {                                                                                    \
+    set_error(NAME ": workspace %zu < %zu", ws_bytes, need);                                               \
+    return PFA_E_WORKSPACE;                                                                                 \
+  }                                                                                                         \
+  PrefixWs w;                                                                                               \
+  prefix_ws_bytes(B, T, nb, nsb, K, &w, (char*)workspace);                                                  \
+  hipStream_t s = as_stream(stream)
+
+extern "C" int pfa_proto_prefix_blocks(const float* proto_scores, int B, int64_t T, int64_t score_stride, int K,
+                                       int32_t* blocks_out, int32_t* evict_out, void* workspace, size_t ws_bytes,
+                                       void* stream) {
+  PFA_PREFIX_SETUP("pfa_proto_prefix_blocks");
+  PFA_CHECK_ARG(blocks_out && evict_out, "pfa_proto_prefix_blocks: null output");
+  return prefix_blocks(proto_scores, B, T, score_stride, K, blocks_out, evict_out, w, nb, s);
 }
 
 extern "C" int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T, int64_t score_stride, int K,
                                      int32_t* sets_out, int32_t* evict_out, void* workspace, size_t ws_bytes,
                                      void* stream) {
-  clear_error();
-  PFA_CHECK_ARG(proto_scores && sets_out && workspace && B > 0 && T > 0 && K > 0 && K <= 4096,
-                "pfa_proto_prefix_topk: bad arguments (B=%d T=%lld K=%d)", B, (long long)T, K);
-  int64_t nb = (T + kBlk - 1) / kBlk;
-  PFA_CHECK_ARG(nb < 65536 * 64, "pfa_proto_prefix_topk: T too large");
-  size_t need = prefix_ws_bytes(B, nb, K);
-  if (ws_bytes < need) {
-    set_error("pfa_proto_prefix_topk: workspace %zu < %zu", ws_bytes, need);
-    return PFA_E_WORKSPACE;
-  }
-  PrefixWs w = carve_prefix(workspace, B, nb, K);
-  hipStream_t s = as_stream(stream);
-  dim3 grid((unsigned)nb, (unsigned)B);
-  prefix_block_sort<<<grid, 64, 0, s>>>(proto_scores, T, score_stride, (int)nb, K, w.val[0], w.idx[0], w.len[0],
-                                             evict_out);
-  PFA_CHECK_LAUNCH("pfa_proto_prefix_topk/sort");
-  int cur = 0;
-  for (int64_t d = 1; d < nb; d <<= 1) {
-    prefix_scan_level<<<grid, 64, (size_t)K * 16, s>>>((int)nb, K, (int)d, w.val[cur], w.idx[cur], w.len[cur], w.val[cur ^ 1],
-                                          w.idx[cur ^ 1], w.len[cur ^ 1]);
-    PFA_CHECK_LAUNCH("pfa_proto_prefix_topk/scan");
-    cur ^= 1;
-  }
-  int cap = 1;
-  while (cap < K) cap <<= 1;
-  size_t lds = (size_t)cap * 8;
-  PFA_CHECK_ARG(lds <= 160 * 1024, "pfa_proto_prefix_topk: K=%d too large for LDS", K);
-  prefix_block_walk<<<grid, 64, lds, s>>>(proto_scores, T, score_stride, (int)nb, K, cap, w.val[cur], w.idx[cur],
-                                          w.len[cur], sets_out, evict_out);
-  PFA_CHECK_LAUNCH("pfa_proto_prefix_topk/walk");
+  PFA_PREFIX_SETUP("pfa_proto_prefix_topk");
+  PFA_CHECK_ARG(sets_out != nullptr, "pfa_proto_prefix_topk: null output");
+  int32_t* ev = evict_out ? evict_out : w.evict;
+  int rc = prefix_blocks(proto_scores, B, T, score_stride, K, w.blk, ev, w, nb, s);
+  if (rc != PFA_OK) return rc;
+  prefix_expand<<<dim3((unsigned)((T + 3) / 4), (unsigned)B), 256, 0, s>>>(T, (int)nb, K, w.blk, ev, sets_out);
+  PFA_CHECK_LAUNCH("pfa_proto_prefix/expand");
   return PFA_OK;
 }
 

@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "pfa_pack_mask",
     "pfa_proto_prefix_workspace_size",
     "pfa_proto_prefix_topk",
+    "pfa_proto_prefix_blocks",
     "pfa_shortlist_build",
     "pfa_sparse_attn_fwd",
     "pfa_shortlist_attn_part_floats",
@@ -90,13 +91,14 @@ _SIGNATURES = {
     "pfa_pack_mask": ([_vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_proto_prefix_workspace_size": ([_i32, _i64, _i32, ctypes.POINTER(_sz)], _i32),
     "pfa_proto_prefix_topk": ([_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp], _i32),
+    "pfa_proto_prefix_blocks": ([_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_shortlist_build": ([_vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i64, _vp, _vp, _i32,
                              _vp, _i32, _vp, _i32, _vp], _i32),
     "pfa_sparse_attn_fwd": ([Tensor4, Tensor4, Tensor4, _i32, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp,
                              _i64, _vp, _i64, _vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp], _i32),
     "pfa_shortlist_attn_part_floats": ([], _i32),
     "pfa_shortlist_attn_fwd": ([Tensor4, Tensor4, Tensor4, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp, _i64,
-                                _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _i64, _vp, _f32, _vp, _vp, _vp], _i32),
+                                _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp], _i32),
     "pfa_head_max_token": ([_vp, _vp, _i32, _vp, _vp], _i32),
     "pfa_rope_qk_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
     "pfa_zero_fill": ([_vp, _sz, _vp], _i32),

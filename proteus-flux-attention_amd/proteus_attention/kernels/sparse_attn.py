@@ -138,6 +138,26 @@ def _proto_prefix_sets(scores: torch.Tensor, K: int, with_evict: bool = False):
     return (sets, evict) if with_evict else sets
 
 
+def _proto_prefix_blocks(scores: torch.Tensor, K: int):
+    """Compact form of the prototype prefix sets: per (batch, 64-token block
+    j) the set of token 64j-1 sorted by index (INT32_MAX-padded), and per
+    token the eviction token evict[p] (p is in the set of t exactly when
+    p <= t < evict[p]).  Returns ((B, ceil(T/64), K), (B, T)) int32."""
+
+    lib = _hip.lib()
+    device = scores.device
+    scores = scores.to(torch.float32).contiguous()
+    B, Ts = scores.shape
+    ws = _workspace(_size_out(lib.pfa_proto_prefix_workspace_size, B, Ts, K), device)
+    blocks = torch.empty(B, (Ts + 63) // 64, K, dtype=torch.int32, device=device)
+    evict = torch.empty(B, Ts, dtype=torch.int32, device=device)
+    with _hip.TIMER.timed("proto_prefix_topk"):
+        rc = lib.pfa_proto_prefix_blocks(_hip.ptr(scores), B, Ts, scores.stride(0), K, _hip.ptr(blocks),
+                                         _hip.ptr(evict), _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device))
+    _hip.check(rc, "pfa_proto_prefix_blocks")
+    return blocks, evict
+
+
 def _resolve_caps(max_candidates, linear_window, anchor_stride, use_local, use_anchors, has_proto, seq_len,
                   local_cap, anchor_cap, proto_cap):
     """Cap resolution of sparse_attn.py:395-397 / 476-490 and the piece
@@ -359,13 +379,14 @@ def _shortlist_attn_structured(
     local_w: int,
     stride: int,
     slots: int,
-    sets: Optional[torch.Tensor],
+    blocks: Optional[torch.Tensor],
     evict: Optional[torch.Tensor],
     scale: float,
     device: torch.device,
 ) -> torch.Tensor:
     """Module-path shortlist attention without materialised candidates
-    (bf16, D=64).  Returns each row's candidate count (int32, (N,))."""
+    (bf16, D=64); the prototype sets come as _proto_prefix_blocks tables of
+    the T-token scores.  Returns each row's candidate count (int32, (N,))."""
 
     lib = _hip.lib()
     N = int(token_idx.numel())
@@ -374,13 +395,16 @@ def _shortlist_attn_structured(
     part = None
     if anchors:
         part = torch.empty(N, int(lib.pfa_shortlist_attn_part_floats()), dtype=torch.float32, device=device)
-    K = int(sets.size(2)) if sets is not None else 0
-    plen = int(sets.size(1)) if sets is not None else 0
+    K = 0
+    if blocks is not None:
+        K = int(blocks.size(2))
+        if evict is None or int(evict.size(1)) != int(T) or int(blocks.size(1)) != (int(T) + 63) // 64:
+            raise ValueError("prototype block tables must cover the T tokens of the sequence")
     with _hip.TIMER.timed("shortlist_attn_fwd"):
         rc = lib.pfa_shortlist_attn_fwd(
             q4, k4, v4, out4, _hip.PFA_BF16, int(H), int(T), int(D), _hip.ptr(token_idx), _hip.ptr(row_head),
             _hip.ptr(head_map), N, int(head_map.numel()), _hip.ptr(summary), _hip.ptr(row_of), int(local_w),
-            int(stride), int(slots), _hip.ptr(sets), K, plen, _hip.ptr(evict), float(scale), _hip.ptr(part),
+            int(stride), int(slots), _hip.ptr(blocks), K, _hip.ptr(evict), float(scale), _hip.ptr(part),
             _hip.ptr(lengths), _hip.stream_ptr(device))
     _hip.check(rc, "pfa_shortlist_attn_fwd")
     return lengths

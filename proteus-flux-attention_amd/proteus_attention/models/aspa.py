@@ -1262,13 +1262,13 @@ class AdaptiveSparseAttention(nn.Module):
                       and (not anchors or (T - 1) // stride + 1 <= 4096) and not _hip.env_flag("PFA_FORCE_GENERIC"))
         q5 = qkv.view(B, T, 3, H, D)
         if structured:
-            sets = evict = None
+            blocks = evict = None
             if K > 0:
-                sets, evict = _sa._proto_prefix_sets(self._last_token_similarity, K, with_evict=True)
+                blocks, evict = _sa._proto_prefix_blocks(self._last_token_similarity, K)
             lens = _sa._shortlist_attn_structured(
                 _hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
                 _hip.tensor4(q5[:, :, 2], H, "bthd"), _hip.tensor4(attn.view(B, T, H, D), H, "bthd"), H, T, D,
-                token_idx, row_head, heads, summary, row_of, w_eff, stride, slots, sets, evict,
+                token_idx, row_head, heads, summary, row_of, w_eff, stride, slots, blocks, evict,
                 1.0 / math.sqrt(D), device)
             self._last_shortlist_lengths = lens
             _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,

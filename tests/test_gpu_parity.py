@@ -167,6 +167,60 @@ def test_proto_evict_matches_prefix_sets(dev):
             assert torch.equal(member, by_evict), (T, K, b)
 
 
+def test_proto_prefix_blocks_match_sets(dev):
+    """Block tables: row j is the set of token 64j-1 sorted by index, and
+    set(t) = {p in row t/64 U [64(t/64), t] : evict[p] > t}; evict agrees with
+    the per-token form.  Sizes span one to many superblocks, with heavy ties,
+    K above and below the 64-token block."""
+    from proteus_attention.kernels import sparse_attn as sa
+
+    g = torch.Generator().manual_seed(23)
+    for T, K, B, tied in ((64, 5, 1, False), (1000, 70, 2, True), (20000, 205, 1, False), (9000, 900, 1, True)):
+        _say(f"prefix blocks T={T} K={K} B={B} tied={tied}")
+        s = (torch.randint(0, 9, (B, T), generator=g).float() if tied else torch.rand(B, T, generator=g))
+        sd = s.to(dev)
+        sets, ev1 = sa._proto_prefix_sets(sd, K, with_evict=True)
+        blk, ev2 = sa._proto_prefix_blocks(sd, K)
+        assert torch.equal(ev1.cpu(), ev2.cpu())
+        sets, blk, ev = sets.cpu().long(), blk.cpu().long(), ev2.cpu().long()
+        nb = (T + 63) // 64
+        for b in range(B):
+            for j in range(nb):
+                t = 64 * j - 1
+                want = sets[b, t, : min(t + 1, K)].tolist() if t >= 0 else []
+                row = [v for v in blk[b, j].tolist() if v != 2 ** 31 - 1]
+                assert row == want, (T, K, b, j)
+            # per-token expansion of the compact form, spot rows
+            for t in list(range(0, T, max(1, T // 97))) + [T - 1]:
+                j = t // 64
+                cand = [p for p in blk[b, j].tolist() if p != 2 ** 31 - 1] + list(range(64 * j, t + 1))
+                got = [p for p in cand if ev[b, p] > t]
+                assert got == sets[b, t, : min(t + 1, K)].tolist(), (T, K, b, t)
+
+
+def test_proto_prefix_sets_large_vs_c_oracle(dev):
+    """Prefix sets at config-4 scale (T = 524,288, K = 409: 8192 blocks, 64
+    superblocks) against the C restatement."""
+    from proteus_attention.kernels import sparse_attn as sa
+
+    T, K = 524_288, 409
+    _say(f"prefix sets T={T} K={K} vs C oracle")
+    g = torch.Generator().manual_seed(29)
+    s = torch.rand(1, T, generator=g)
+    s[0, ::1000] = 0.5  # a few exact ties
+    sets = sa._proto_prefix_sets(s.to(dev), K)
+    rows = np.arange(0, T, 997, dtype=np.int32)
+    # the C builder with only the prototype piece and L = K + 1 returns
+    # sorted(set(t) U {t}) padded with t
+    exp, _ = c_oracle.shortlist_build(rows, None, T, K + 1, 0, 0, 0, s.numpy(), K)
+    got = sets[0][torch.from_numpy(rows).long().to(dev)].cpu().numpy()
+    del sets
+    for r, t in enumerate(rows.tolist()):
+        u = sorted(set(got[r, : min(t + 1, K)].tolist()) | {t})
+        u = u + [t] * (K + 1 - len(u))
+        assert u == exp[r].tolist(), t
+
+
 @pytest.mark.parametrize("T,L,w,s,B,outlier", [(4096, 1024, 256, 64, 1, 0.01), (3000, 700, 100, 37, 2, 0.0),
                                                (65536, 2048, 512, 256, 1, 0.01)])
 def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, monkeypatch):
