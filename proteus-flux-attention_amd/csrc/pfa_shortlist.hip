@@ -43,7 +43,7 @@ constexpr int kBlk = 64;  // tokens per prefix block (one wave)
 
 static int64_t prefix_sbs(int64_t nb) {
   int64_t s = 1;
-  while (s * s < 2 * nb) s <<= 1;
+  while (s * s < nb) s <<= 1;
   return s;
 }
 
@@ -135,6 +135,8 @@ __device__ __forceinline__ void merge_at(int p, const float* av, const int32_t* 
 }
 
 // Q[j] = top-K(Q[j-1] U block j) within each superblock (one workgroup).
+// The next block's sorted list is fetched into registers while the current
+// merge runs, so the sequential chain never waits on global memory.
 __global__ void __launch_bounds__(256)
 prefix_sb_local(int nb, int sbs, int K, const float* __restrict__ bval, const int32_t* __restrict__ bidx,
                 const int32_t* __restrict__ blen, float* __restrict__ qval, int32_t* __restrict__ qidx,
@@ -144,16 +146,36 @@ prefix_sb_local(int nb, int sbs, int K, const float* __restrict__ bval, const in
   int32_t* ci0 = (int32_t*)(cv0 + K);
   float* cv1 = (float*)(ci0 + K);
   int32_t* ci1 = (int32_t*)(cv1 + K);
-  float* kv = (float*)(ci1 + K);
-  int32_t* ki = (int32_t*)(kv + kBlk);
+  float* kv = (float*)(ci1 + K);        // 2 x kBlk (double buffer)
+  int32_t* ki = (int32_t*)(kv + 2 * kBlk);
+  __shared__ int s_nbl[2];
   const int sb = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int j0 = sb * sbs, j1 = min(nb, j0 + sbs);
-  int n = 0, cur = 0;
-  for (int j = j0; j < j1; ++j) {
-    const int64_t row = (int64_t)b * nb + j;
+  if (j0 >= j1) return;
+  // stage the first block
+  {
+    const int64_t row = (int64_t)b * nb + j0;
     const int nbl = blen[row];
     if (tid < nbl) { kv[tid] = bval[row * kBlk + tid]; ki[tid] = bidx[row * kBlk + tid]; }
-    __syncthreads();
+    if (tid == 0) s_nbl[0] = nbl;
+  }
+  __syncthreads();
+  int n = 0, cur = 0;
+  for (int j = j0; j < j1; ++j) {
+    const int kb = (j - j0) & 1;
+    // prefetch block j+1 into registers
+    float pv = 0.f;
+    int32_t pi = 0;
+    int pn = 0;
+    if (j + 1 < j1) {
+      const int64_t nrow = (int64_t)b * nb + j + 1;
+      pn = blen[nrow];
+      if (tid < pn) { pv = bval[nrow * kBlk + tid]; pi = bidx[nrow * kBlk + tid]; }
+    }
+    const int64_t row = (int64_t)b * nb + j;
+    const int nbl = s_nbl[kb];
+    const float* bv = kv + kb * kBlk;
+    const int32_t* bi = ki + kb * kBlk;
     const int m = min(K, n + nbl);
     const float* av = cur ? cv1 : cv0;
     const int32_t* ai = cur ? ci1 : ci0;
@@ -162,13 +184,17 @@ prefix_sb_local(int nb, int sbs, int K, const float* __restrict__ bval, const in
     for (int p = tid; p < m; p += 256) {
       float vv;
       int32_t ii;
-      merge_at(p, av, ai, n, kv, ki, nbl, vv, ii);
+      merge_at(p, av, ai, n, bv, bi, nbl, vv, ii);
       ov[p] = vv;
       oi[p] = ii;
       qval[row * K + p] = vv;
       qidx[row * K + p] = ii;
     }
     if (tid == 0) qlen[row] = m;
+    if (j + 1 < j1) {
+      if (tid < pn) { kv[(kb ^ 1) * kBlk + tid] = pv; ki[(kb ^ 1) * kBlk + tid] = pi; }
+      if (tid == 0) s_nbl[kb ^ 1] = pn;
+    }
     __syncthreads();
     cur ^= 1;
     n = m;
@@ -176,23 +202,39 @@ prefix_sb_local(int nb, int sbs, int K, const float* __restrict__ bval, const in
 }
 
 // R[s] = top-K of every token before superblock s (one workgroup per batch).
+// Superblock totals are staged in LDS one step ahead.
 __global__ void __launch_bounds__(256)
-prefix_sb_scan(int nb, int sbs, int nsb, int K, const float* __restrict__ qval, const int32_t* __restrict__ qidx,
-               const int32_t* __restrict__ qlen, float* __restrict__ rval, int32_t* __restrict__ ridx,
-               int32_t* __restrict__ rlen) {
+prefix_sb_scan(int nb, int sbs, int nsb, int K, int dbl, const float* __restrict__ qval,
+               const int32_t* __restrict__ qidx, const int32_t* __restrict__ qlen, float* __restrict__ rval,
+               int32_t* __restrict__ ridx, int32_t* __restrict__ rlen) {
   extern __shared__ char smem[];
   float* cv0 = (float*)smem;
   int32_t* ci0 = (int32_t*)(cv0 + K);
   float* cv1 = (float*)(ci0 + K);
   int32_t* ci1 = (int32_t*)(cv1 + K);
+  float* tv0 = (float*)(ci1 + K);
+  int32_t* ti0 = (int32_t*)(tv0 + K);
+  float* tv1 = dbl ? (float*)(ti0 + K) : tv0;  // second staging slot only when LDS allows
+  int32_t* ti1 = dbl ? (int32_t*)(tv1 + K) : ti0;
+  __shared__ int s_nt[2];
   const int b = blockIdx.x, tid = threadIdx.x;
   if (tid == 0) rlen[(int64_t)b * nsb] = 0;
-  int n = 0, cur = 0;
-  for (int s = 1; s < nsb; ++s) {
+  if (nsb <= 1) return;
+  auto stage = [&](int s, float* tv, int32_t* ti, int slot) {
     const int64_t qrow = (int64_t)b * nb + (int64_t)s * sbs - 1;  // last block of superblock s-1
     const int nt = qlen[qrow];
-    const float* tv = qval + qrow * K;
-    const int32_t* ti = qidx + qrow * K;
+    for (int p = tid; p < nt; p += 256) { tv[p] = qval[qrow * K + p]; ti[p] = qidx[qrow * K + p]; }
+    if (tid == 0) s_nt[slot] = nt;
+  };
+  stage(1, tv0, ti0, 0);
+  __syncthreads();
+  int n = 0, cur = 0;
+  for (int s = 1; s < nsb; ++s) {
+    const int slot = dbl ? ((s - 1) & 1) : 0;
+    const float* tv = slot ? tv1 : tv0;
+    const int32_t* ti = slot ? ti1 : ti0;
+    const int nt = s_nt[slot];
+    if (dbl && s + 1 < nsb) stage(s + 1, slot ? tv0 : tv1, slot ? ti0 : ti1, slot ^ 1);
     const int m = min(K, n + nt);
     const float* av = cur ? cv1 : cv0;
     const int32_t* ai = cur ? ci1 : ci0;
@@ -210,14 +252,19 @@ prefix_sb_scan(int nb, int sbs, int nsb, int K, const float* __restrict__ qval, 
     }
     if (tid == 0) rlen[rrow] = m;
     __syncthreads();
+    if (!dbl && s + 1 < nsb) {
+      stage(s + 1, tv0, ti0, 0);
+      __syncthreads();
+    }
     cur ^= 1;
     n = m;
   }
 }
 
 // One workgroup (256 threads) per (block j, batch b).  LDS: the entering set
-// P best first (cap entries, cap = power of two >= K), an index-sorted copy,
-// the rank of each element of P, and the block's 64 tokens.
+// P best first (v, ix: cap entries each, cap = power of two >= K) and a
+// staging area of 2*cap floats + 2*cap ints that first holds R[s] and
+// Q[j-1] for the merge, then the index-sorted copy and the ranks of P.
 __global__ void __launch_bounds__(256)
 prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int sbs, int nsb, int K,
                   int cap, const float* __restrict__ qval, const int32_t* __restrict__ qidx,
@@ -226,8 +273,12 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
   extern __shared__ char smem[];
   float* v = (float*)smem;
   int32_t* ix = (int32_t*)(v + cap);
-  int32_t* srt = ix + cap;
-  int32_t* rk = srt + cap;
+  float* sav = (float*)(ix + cap);        // staging: R values   (cap)
+  int32_t* sai = (int32_t*)(sav + cap);   //          R indices  (cap)
+  float* sqv = (float*)(sai + cap);       //          Q values   (cap)
+  int32_t* sqi = (int32_t*)(sqv + cap);   //          Q indices  (cap)
+  int32_t* srt = sai;                     // after the merge: index-sorted copy
+  int32_t* rk = sqi;                      //                  ranks of P
   __shared__ float bv[kBlk];
   __shared__ int32_t bi[kBlk];
   __shared__ int32_t flag[kBlk];
@@ -238,29 +289,12 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
   const int s = j / sbs, k = j % sbs;
   const int64_t rrow = (int64_t)b * nsb + s;
   const int na = rlen[rrow];
-  const float* av = rval + rrow * K;
-  const int32_t* ai = ridx + rrow * K;
+  for (int p = tid; p < na; p += 256) { sav[p] = rval[rrow * K + p]; sai[p] = ridx[rrow * K + p]; }
   int nq = 0;
-  const float* cq = qval;
-  const int32_t* ciq = qidx;
   if (k > 0) {
     const int64_t qrow = (int64_t)b * nb + j - 1;
     nq = qlen[qrow];
-    cq = qval + qrow * K;
-    ciq = qidx + qrow * K;
-  }
-  const int n = min(K, na + nq);
-  for (int p = tid; p < cap; p += 256) {
-    if (p < n) {
-      float vv;
-      int32_t ii;
-      merge_at(p, av, ai, na, cq, ciq, nq, vv, ii);
-      v[p] = vv;
-      ix[p] = ii;
-      srt[p] = ii;
-    } else {
-      srt[p] = INT32_MAX;
-    }
+    for (int p = tid; p < nq; p += 256) { sqv[p] = qval[qrow * K + p]; sqi[p] = qidx[qrow * K + p]; }
   }
   const int64_t t0 = (int64_t)j * kBlk;
   const int nB = (int)min<int64_t>(kBlk, T - t0);
@@ -272,6 +306,17 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
     bi[tid] = st;
     flag[tid] = 0;
   }
+  __syncthreads();
+  const int n = min(K, na + nq);
+  for (int p = tid; p < n; p += 256) {
+    float vv;
+    int32_t ii;
+    merge_at(p, sav, sai, na, sqv, sqi, nq, vv, ii);
+    v[p] = vv;
+    ix[p] = ii;
+  }
+  __syncthreads();
+  for (int p = tid; p < cap; p += 256) srt[p] = p < n ? ix[p] : INT32_MAX;
   __syncthreads();
   // the block's set table row: P sorted by index (bitonic over cap entries)
   for (int kk = 2; kk <= cap; kk <<= 1) {
@@ -366,7 +411,8 @@ prefix_expand(int64_t T, int nb, int K, const int32_t* __restrict__ blk, const i
     const int32_t x = p < K ? P[p] : INT32_MAX;
     const bool keep = x != INT32_MAX && ev[x] > t;
     const uint64_t m = __ballot(keep);
-    if (keep) out[n + __popcll(m & lt)] = x;
+    const int pos = n + __popcll(m & lt);
+    if (keep && pos < K) out[pos] = x;  // |set| = min(t+1, K): the guard never binds
     n += __popcll(m);
     if (__ballot(x == INT32_MAX)) break;
   }
@@ -374,7 +420,8 @@ prefix_expand(int64_t T, int nb, int K, const int32_t* __restrict__ blk, const i
     const int64_t q = j * kBlk + lane;
     const bool keep = q <= t && ev[q] > t;
     const uint64_t m = __ballot(keep);
-    if (keep) out[n + __popcll(m & lt)] = (int32_t)q;
+    const int pos = n + __popcll(m & lt);
+    if (keep && pos < K) out[pos] = (int32_t)q;
     n += __popcll(m);
   }
   for (int p = n + lane; p < K; p += 64) out[p] = (int32_t)t;
@@ -572,6 +619,7 @@ shortlist_build_kernel(const int32_t* __restrict__ rows, const int32_t* __restri
 using namespace pfa;
 
 static constexpr int kPrefixMaxK = 2048;
+static constexpr size_t kPrefixLds = 60 * 1024;  // dynamic LDS budget per workgroup
 
 static int prefix_cap(int K) {
   int cap = 64;
@@ -599,13 +647,14 @@ static int prefix_blocks(const float* scores, int B, int64_t T, int64_t stride, 
   dim3 grid((unsigned)nb, (unsigned)B);
   prefix_block_sort<<<grid, 64, 0, s>>>(scores, T, stride, (int)nb, K, w.bval, w.bidx, w.blen, evict);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/sort");
-  prefix_sb_local<<<dim3((unsigned)nsb, (unsigned)B), 256, (size_t)K * 16 + kBlk * 8, s>>>(
+  prefix_sb_local<<<dim3((unsigned)nsb, (unsigned)B), 256, (size_t)K * 16 + kBlk * 16, s>>>(
       (int)nb, (int)sbs, K, w.bval, w.bidx, w.blen, w.qval, w.qidx, w.qlen);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/local");
-  prefix_sb_scan<<<(unsigned)B, 256, (size_t)K * 16, s>>>((int)nb, (int)sbs, (int)nsb, K, w.qval, w.qidx, w.qlen,
-                                                          w.rval, w.ridx, w.rlen);
+  const int dbl = (size_t)K * 32 <= kPrefixLds ? 1 : 0;
+  prefix_sb_scan<<<(unsigned)B, 256, (size_t)K * (dbl ? 32 : 24), s>>>((int)nb, (int)sbs, (int)nsb, K, dbl, w.qval,
+                                                                      w.qidx, w.qlen, w.rval, w.ridx, w.rlen);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/scan");
-  prefix_block_walk<<<grid, 256, (size_t)cap * 16, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K, cap,
+  prefix_block_walk<<<grid, 256, (size_t)cap * 24, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K, cap,
                                                          w.qval, w.qidx, w.qlen, w.rval, w.ridx, w.rlen, blk, evict);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/walk");
   return PFA_OK;

@@ -175,7 +175,8 @@ def test_proto_prefix_blocks_match_sets(dev):
     from proteus_attention.kernels import sparse_attn as sa
 
     g = torch.Generator().manual_seed(23)
-    for T, K, B, tied in ((64, 5, 1, False), (1000, 70, 2, True), (20000, 205, 1, False), (9000, 900, 1, True)):
+    for T, K, B, tied in ((64, 5, 1, False), (1000, 70, 2, True), (20000, 205, 1, False), (9000, 900, 1, True),
+                          (6000, 1700, 1, True)):
         _say(f"prefix blocks T={T} K={K} B={B} tied={tied}")
         s = (torch.randint(0, 9, (B, T), generator=g).float() if tied else torch.rand(B, T, generator=g))
         sd = s.to(dev)
