@@ -165,7 +165,7 @@ int pfa_pack_mask(const uint8_t* mask, int P, int64_t T, int32_t* row_offsets_ou
  *
  * pfa_proto_prefix_blocks writes the compact form:
  *   blocks_out (B, ceil(T/64), K) int32: row j = the set of token 64j-1
- *     (the prefix before block j) sorted by index, padded with INT32_MAX;
+ *     (the prefix before block j), best score first, padded with INT32_MAX;
  *   evict_out (B, T) int32: the first token at which position p is no
  *     longer in the set (p if it never enters, INT32_MAX if it stays), so
  *     that p is in the set of token t exactly when p <= t < evict[p], and

@@ -355,10 +355,12 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
     const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
 
     // prototype key list: the prefix set of t_first below lo_last (set table
-    // row of t_first's block, then the block's tokens up to t_first, both
-    // ascending, keeping p with evict[p] > t_first), then key 0
+    // row of t_first's block -- any order, INT32_MAX-padded -- then the
+    // block's tokens up to t_first, keeping p with evict[p] > t_first), then
+    // key 0 for the zero-anchor rule
     if (tid < 64) {
       int n = 0;
+      bool has0 = false;
       if (a.blk != nullptr) {
         const uint64_t lt = (1ull << lane) - 1;
         const int64_t jb = t_first >> 6;
@@ -379,7 +381,8 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
             pev[n + __popcll(bal & lt)] = e;
           }
           n += __popcll(bal);
-          if (__ballot(v >= lo_last)) break;  // ascending: nothing further lies below lo_last
+          has0 = has0 || __ballot(keep && v == 0) != 0;
+          if (__ballot(v == INT32_MAX)) break;  // padding: the row holds no more entries
         }
         const int64_t q = (jb << 6) + lane;
         bool keep = false;
@@ -394,19 +397,15 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
           pev[n + __popcll(bal & lt)] = e;
         }
         n += __popcll(bal);
+        has0 = has0 || __ballot(keep && q == 0) != 0;
       }
-      if (lo_last > 0 && a.stride > 0 && a.slots > 0) {
-        // append key 0 for the zero-anchor rule unless the (ascending) list
-        // already starts with it; order inside the list does not matter
-        wave_sync();
-        const int32_t first = n > 0 ? plist[0] : -1;
-        if (first != 0) {
-          if (lane == 0) {
-            plist[n] = 0;
-            pev[n] = -1;  // not in the prototype set: only the zero-anchor rule applies
-          }
-          ++n;
+      if (lo_last > 0 && a.stride > 0 && a.slots > 0 && !has0) {
+        // order inside the list does not matter
+        if (lane == 0) {
+          plist[n] = 0;
+          pev[n] = -1;  // not in the prototype set: only the zero-anchor rule applies
         }
+        ++n;
       }
       if (lane == 0) s_plen = n;
     }

@@ -11,7 +11,8 @@
 //   3. sb_scan    : one workgroup folds the superblock totals:
 //                   R[s] = top-K of all tokens before superblock s;
 //   4. block_walk : per block j, P = top-K(R[s] U Q[j-1]) = S(64j - 1) is
-//                   written sorted by index (the block's set table row), and
+//                   written as the block's set table row (best first, or
+//                   sorted by index when the per-token sets are wanted), and
 //                   the block's tokens are resolved in parallel from exact
 //                   rank counts (below);
 //   5. expand     : (optional) S(t) for every token, sorted by index.
@@ -135,47 +136,51 @@ __device__ __forceinline__ void merge_at(int p, const float* av, const int32_t* 
 }
 
 // Q[j] = top-K(Q[j-1] U block j) within each superblock (one workgroup).
-// The next block's sorted list is fetched into registers while the current
-// merge runs, so the sequential chain never waits on global memory.
+// With `preload` every block list of the superblock is staged in LDS up
+// front (one burst of loads); otherwise the next block is fetched one step
+// ahead.  The sequential chain then runs on LDS only.
 __global__ void __launch_bounds__(256)
-prefix_sb_local(int nb, int sbs, int K, const float* __restrict__ bval, const int32_t* __restrict__ bidx,
-                const int32_t* __restrict__ blen, float* __restrict__ qval, int32_t* __restrict__ qidx,
-                int32_t* __restrict__ qlen) {
+prefix_sb_local(int nb, int sbs, int K, int preload, const float* __restrict__ bval,
+                const int32_t* __restrict__ bidx, const int32_t* __restrict__ blen, float* __restrict__ qval,
+                int32_t* __restrict__ qidx, int32_t* __restrict__ qlen) {
   extern __shared__ char smem[];
   float* cv0 = (float*)smem;
   int32_t* ci0 = (int32_t*)(cv0 + K);
   float* cv1 = (float*)(ci0 + K);
   int32_t* ci1 = (int32_t*)(cv1 + K);
-  float* kv = (float*)(ci1 + K);        // 2 x kBlk (double buffer)
-  int32_t* ki = (int32_t*)(kv + 2 * kBlk);
-  __shared__ int s_nbl[2];
+  const int nslot = preload ? sbs : 2;
+  float* kv = (float*)(ci1 + K);  // nslot x kBlk
+  int32_t* ki = (int32_t*)(kv + nslot * kBlk);
+  int32_t* kn = ki + nslot * kBlk;  // nslot lengths
   const int sb = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int j0 = sb * sbs, j1 = min(nb, j0 + sbs);
   if (j0 >= j1) return;
-  // stage the first block
-  {
-    const int64_t row = (int64_t)b * nb + j0;
+  const int cnt = j1 - j0;
+  const int nfirst = preload ? cnt : 1;
+  for (int e = tid; e < nfirst * kBlk; e += 256) {
+    const int jj = e / kBlk, l = e % kBlk;
+    const int64_t row = (int64_t)b * nb + j0 + jj;
     const int nbl = blen[row];
-    if (tid < nbl) { kv[tid] = bval[row * kBlk + tid]; ki[tid] = bidx[row * kBlk + tid]; }
-    if (tid == 0) s_nbl[0] = nbl;
+    if (l < nbl) { kv[jj * kBlk + l] = bval[row * kBlk + l]; ki[jj * kBlk + l] = bidx[row * kBlk + l]; }
+    if (l == 0) kn[jj] = nbl;
   }
   __syncthreads();
   int n = 0, cur = 0;
-  for (int j = j0; j < j1; ++j) {
-    const int kb = (j - j0) & 1;
-    // prefetch block j+1 into registers
+  for (int i = 0; i < cnt; ++i) {
+    const int j = j0 + i;
+    const int slot = preload ? i : (i & 1);
     float pv = 0.f;
     int32_t pi = 0;
     int pn = 0;
-    if (j + 1 < j1) {
+    if (!preload && i + 1 < cnt) {
       const int64_t nrow = (int64_t)b * nb + j + 1;
       pn = blen[nrow];
       if (tid < pn) { pv = bval[nrow * kBlk + tid]; pi = bidx[nrow * kBlk + tid]; }
     }
     const int64_t row = (int64_t)b * nb + j;
-    const int nbl = s_nbl[kb];
-    const float* bv = kv + kb * kBlk;
-    const int32_t* bi = ki + kb * kBlk;
+    const int nbl = kn[slot];
+    const float* bv = kv + slot * kBlk;
+    const int32_t* bi = ki + slot * kBlk;
     const int m = min(K, n + nbl);
     const float* av = cur ? cv1 : cv0;
     const int32_t* ai = cur ? ci1 : ci0;
@@ -191,9 +196,10 @@ prefix_sb_local(int nb, int sbs, int K, const float* __restrict__ bval, const in
       qidx[row * K + p] = ii;
     }
     if (tid == 0) qlen[row] = m;
-    if (j + 1 < j1) {
-      if (tid < pn) { kv[(kb ^ 1) * kBlk + tid] = pv; ki[(kb ^ 1) * kBlk + tid] = pi; }
-      if (tid == 0) s_nbl[kb ^ 1] = pn;
+    if (!preload && i + 1 < cnt) {
+      const int ns = (i + 1) & 1;
+      if (tid < pn) { kv[ns * kBlk + tid] = pv; ki[ns * kBlk + tid] = pi; }
+      if (tid == 0) kn[ns] = pn;
     }
     __syncthreads();
     cur ^= 1;
@@ -202,9 +208,10 @@ prefix_sb_local(int nb, int sbs, int K, const float* __restrict__ bval, const in
 }
 
 // R[s] = top-K of every token before superblock s (one workgroup per batch).
-// Superblock totals are staged in LDS one step ahead.
+// Superblock totals are staged in LDS: all of them up front when they fit
+// (mode 2), else one step ahead (mode 1) or one at a time (mode 0).
 __global__ void __launch_bounds__(256)
-prefix_sb_scan(int nb, int sbs, int nsb, int K, int dbl, const float* __restrict__ qval,
+prefix_sb_scan(int nb, int sbs, int nsb, int K, int mode, const float* __restrict__ qval,
                const int32_t* __restrict__ qidx, const int32_t* __restrict__ qlen, float* __restrict__ rval,
                int32_t* __restrict__ ridx, int32_t* __restrict__ rlen) {
   extern __shared__ char smem[];
@@ -212,29 +219,45 @@ prefix_sb_scan(int nb, int sbs, int nsb, int K, int dbl, const float* __restrict
   int32_t* ci0 = (int32_t*)(cv0 + K);
   float* cv1 = (float*)(ci0 + K);
   int32_t* ci1 = (int32_t*)(cv1 + K);
-  float* tv0 = (float*)(ci1 + K);
-  int32_t* ti0 = (int32_t*)(tv0 + K);
-  float* tv1 = dbl ? (float*)(ti0 + K) : tv0;  // second staging slot only when LDS allows
-  int32_t* ti1 = dbl ? (int32_t*)(tv1 + K) : ti0;
+  const int nslot = mode == 2 ? max(1, nsb - 1) : (mode == 1 ? 2 : 1);
+  float* tvs = (float*)(ci1 + K);           // nslot x K
+  int32_t* tis = (int32_t*)(tvs + (size_t)nslot * K);
   __shared__ int s_nt[2];
+  int32_t* tn = (int32_t*)(tis + (size_t)nslot * K);  // nslot lengths (mode 2)
   const int b = blockIdx.x, tid = threadIdx.x;
   if (tid == 0) rlen[(int64_t)b * nsb] = 0;
   if (nsb <= 1) return;
-  auto stage = [&](int s, float* tv, int32_t* ti, int slot) {
-    const int64_t qrow = (int64_t)b * nb + (int64_t)s * sbs - 1;  // last block of superblock s-1
+  auto qrow_of = [&](int s) { return (int64_t)b * nb + (int64_t)s * sbs - 1; };  // last block of superblock s-1
+  if (mode == 2) {
+    for (int s = 1; s < nsb; ++s) {
+      const int64_t qrow = qrow_of(s);
+      const int nt = qlen[qrow];
+      float* tv = tvs + (size_t)(s - 1) * K;
+      int32_t* ti = tis + (size_t)(s - 1) * K;
+      for (int p = tid; p < nt; p += 256) { tv[p] = qval[qrow * K + p]; ti[p] = qidx[qrow * K + p]; }
+      if (tid == 0) tn[s - 1] = nt;
+    }
+  } else {
+    const int64_t qrow = qrow_of(1);
     const int nt = qlen[qrow];
-    for (int p = tid; p < nt; p += 256) { tv[p] = qval[qrow * K + p]; ti[p] = qidx[qrow * K + p]; }
-    if (tid == 0) s_nt[slot] = nt;
-  };
-  stage(1, tv0, ti0, 0);
+    for (int p = tid; p < nt; p += 256) { tvs[p] = qval[qrow * K + p]; tis[p] = qidx[qrow * K + p]; }
+    if (tid == 0) s_nt[0] = nt;
+  }
   __syncthreads();
   int n = 0, cur = 0;
   for (int s = 1; s < nsb; ++s) {
-    const int slot = dbl ? ((s - 1) & 1) : 0;
-    const float* tv = slot ? tv1 : tv0;
-    const int32_t* ti = slot ? ti1 : ti0;
-    const int nt = s_nt[slot];
-    if (dbl && s + 1 < nsb) stage(s + 1, slot ? tv0 : tv1, slot ? ti0 : ti1, slot ^ 1);
+    const int slot = mode == 2 ? s - 1 : (mode == 1 ? ((s - 1) & 1) : 0);
+    const float* tv = tvs + (size_t)slot * K;
+    const int32_t* ti = tis + (size_t)slot * K;
+    const int nt = mode == 2 ? tn[slot] : s_nt[slot & 1];
+    if (mode == 1 && s + 1 < nsb) {
+      const int64_t qrow = qrow_of(s + 1);
+      const int nn = qlen[qrow];
+      float* dv = tvs + (size_t)(slot ^ 1) * K;
+      int32_t* di = tis + (size_t)(slot ^ 1) * K;
+      for (int p = tid; p < nn; p += 256) { dv[p] = qval[qrow * K + p]; di[p] = qidx[qrow * K + p]; }
+      if (tid == 0) s_nt[slot ^ 1] = nn;
+    }
     const int m = min(K, n + nt);
     const float* av = cur ? cv1 : cv0;
     const int32_t* ai = cur ? ci1 : ci0;
@@ -252,8 +275,11 @@ prefix_sb_scan(int nb, int sbs, int nsb, int K, int dbl, const float* __restrict
     }
     if (tid == 0) rlen[rrow] = m;
     __syncthreads();
-    if (!dbl && s + 1 < nsb) {
-      stage(s + 1, tv0, ti0, 0);
+    if (mode == 0 && s + 1 < nsb) {
+      const int64_t qrow = qrow_of(s + 1);
+      const int nn = qlen[qrow];
+      for (int p = tid; p < nn; p += 256) { tvs[p] = qval[qrow * K + p]; tis[p] = qidx[qrow * K + p]; }
+      if (tid == 0) s_nt[0] = nn;
       __syncthreads();
     }
     cur ^= 1;
@@ -265,6 +291,7 @@ prefix_sb_scan(int nb, int sbs, int nsb, int K, int dbl, const float* __restrict
 // P best first (v, ix: cap entries each, cap = power of two >= K) and a
 // staging area of 2*cap floats + 2*cap ints that first holds R[s] and
 // Q[j-1] for the merge, then the index-sorted copy and the ranks of P.
+template <bool SORT>
 __global__ void __launch_bounds__(256)
 prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int sbs, int nsb, int K,
                   int cap, const float* __restrict__ qval, const int32_t* __restrict__ qidx,
@@ -316,23 +343,28 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
     ix[p] = ii;
   }
   __syncthreads();
-  for (int p = tid; p < cap; p += 256) srt[p] = p < n ? ix[p] : INT32_MAX;
-  __syncthreads();
-  // the block's set table row: P sorted by index (bitonic over cap entries)
-  for (int kk = 2; kk <= cap; kk <<= 1) {
-    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-      for (int e = tid; e < cap; e += 256) {
-        const int q = e ^ jj;
-        if (q > e) {
-          const int x = srt[e], y = srt[q];
-          if (((e & kk) == 0) ? (x > y) : (x < y)) { srt[e] = y; srt[q] = x; }
-        }
-      }
-      __syncthreads();
-    }
-  }
   int32_t* orow = blk_out + ((int64_t)b * nb + j) * K;
-  for (int p = tid; p < K; p += 256) orow[p] = srt[p];
+  if constexpr (SORT) {
+    // the block's set table row sorted by index (bitonic over cap entries)
+    for (int p = tid; p < cap; p += 256) srt[p] = p < n ? ix[p] : INT32_MAX;
+    __syncthreads();
+    for (int kk = 2; kk <= cap; kk <<= 1) {
+      for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+        for (int e = tid; e < cap; e += 256) {
+          const int q = e ^ jj;
+          if (q > e) {
+            const int x = srt[e], y = srt[q];
+            if (((e & kk) == 0) ? (x > y) : (x < y)) { srt[e] = y; srt[q] = x; }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int p = tid; p < K; p += 256) orow[p] = srt[p];
+  } else {
+    // best first, as merged
+    for (int p = tid; p < K; p += 256) orow[p] = p < n ? ix[p] : INT32_MAX;
+  }
   // ranks of P's elements in P U B (P is sorted best first)
   for (int p = tid; p < n; p += 256) {
     int c = 0;
@@ -640,22 +672,34 @@ extern "C" int pfa_proto_prefix_workspace_size(int B, int64_t T, int K, size_t* 
 
 // Steps 1-4: set table rows (B, nb, K) and evict (B, T).
 static int prefix_blocks(const float* scores, int B, int64_t T, int64_t stride, int K, int32_t* blk,
-                         int32_t* evict, const PrefixWs& w, int64_t nb, hipStream_t s) {
+                         int32_t* evict, const PrefixWs& w, int64_t nb, bool sorted_rows, hipStream_t s) {
   const int64_t sbs = prefix_sbs(nb);
   const int64_t nsb = (nb + sbs - 1) / sbs;
   const int cap = prefix_cap(K);
   dim3 grid((unsigned)nb, (unsigned)B);
   prefix_block_sort<<<grid, 64, 0, s>>>(scores, T, stride, (int)nb, K, w.bval, w.bidx, w.blen, evict);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/sort");
-  prefix_sb_local<<<dim3((unsigned)nsb, (unsigned)B), 256, (size_t)K * 16 + kBlk * 16, s>>>(
-      (int)nb, (int)sbs, K, w.bval, w.bidx, w.blen, w.qval, w.qidx, w.qlen);
+  const int preload = (size_t)K * 16 + (size_t)sbs * (kBlk * 8 + 4) <= kPrefixLds ? 1 : 0;
+  const size_t lds_local = (size_t)K * 16 + (size_t)(preload ? sbs : 2) * (kBlk * 8 + 4);
+  prefix_sb_local<<<dim3((unsigned)nsb, (unsigned)B), 256, lds_local, s>>>(
+      (int)nb, (int)sbs, K, preload, w.bval, w.bidx, w.blen, w.qval, w.qidx, w.qlen);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/local");
-  const int dbl = (size_t)K * 32 <= kPrefixLds ? 1 : 0;
-  prefix_sb_scan<<<(unsigned)B, 256, (size_t)K * (dbl ? 32 : 24), s>>>((int)nb, (int)sbs, (int)nsb, K, dbl, w.qval,
-                                                                      w.qidx, w.qlen, w.rval, w.ridx, w.rlen);
+  const size_t per_slot = (size_t)K * 8 + 4;
+  int mode = 0;
+  if ((size_t)K * 16 + (size_t)(nsb > 1 ? nsb - 1 : 1) * per_slot <= kPrefixLds) mode = 2;
+  else if ((size_t)K * 16 + 2 * per_slot <= kPrefixLds) mode = 1;
+  const size_t lds_scan = (size_t)K * 16 + (size_t)(mode == 2 ? (nsb > 1 ? nsb - 1 : 1) : (mode == 1 ? 2 : 1)) * per_slot;
+  prefix_sb_scan<<<(unsigned)B, 256, lds_scan, s>>>((int)nb, (int)sbs, (int)nsb, K, mode, w.qval, w.qidx, w.qlen,
+                                                    w.rval, w.ridx, w.rlen);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/scan");
-  prefix_block_walk<<<grid, 256, (size_t)cap * 24, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K, cap,
-                                                         w.qval, w.qidx, w.qlen, w.rval, w.ridx, w.rlen, blk, evict);
+  if (sorted_rows)
+    prefix_block_walk<true><<<grid, 256, (size_t)cap * 24, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K,
+                                                                cap, w.qval, w.qidx, w.qlen, w.rval, w.ridx, w.rlen,
+                                                                blk, evict);
+  else
+    prefix_block_walk<false><<<grid, 256, (size_t)cap * 24, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K,
+                                                                 cap, w.qval, w.qidx, w.qlen, w.rval, w.ridx, w.rlen,
+                                                                 blk, evict);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/walk");
   return PFA_OK;
 }
@@ -682,7 +726,7 @@ extern "C" int pfa_proto_prefix_blocks(const float* proto_scores, int B, int64_t
                                        void* stream) {
   PFA_PREFIX_SETUP("pfa_proto_prefix_blocks");
   PFA_CHECK_ARG(blocks_out && evict_out, "pfa_proto_prefix_blocks: null output");
-  return prefix_blocks(proto_scores, B, T, score_stride, K, blocks_out, evict_out, w, nb, s);
+  return prefix_blocks(proto_scores, B, T, score_stride, K, blocks_out, evict_out, w, nb, false, s);
 }
 
 extern "C" int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T, int64_t score_stride, int K,
@@ -691,7 +735,7 @@ extern "C" int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T
   PFA_PREFIX_SETUP("pfa_proto_prefix_topk");
   PFA_CHECK_ARG(sets_out != nullptr, "pfa_proto_prefix_topk: null output");
   int32_t* ev = evict_out ? evict_out : w.evict;
-  int rc = prefix_blocks(proto_scores, B, T, score_stride, K, w.blk, ev, w, nb, s);
+  int rc = prefix_blocks(proto_scores, B, T, score_stride, K, w.blk, ev, w, nb, true, s);
   if (rc != PFA_OK) return rc;
   prefix_expand<<<dim3((unsigned)((T + 3) / 4), (unsigned)B), 256, 0, s>>>(T, (int)nb, K, w.blk, ev, sets_out);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/expand");

@@ -168,7 +168,7 @@ def test_proto_evict_matches_prefix_sets(dev):
 
 
 def test_proto_prefix_blocks_match_sets(dev):
-    """Block tables: row j is the set of token 64j-1 sorted by index, and
+    """Block tables: row j is the set of token 64j-1 (best first), and
     set(t) = {p in row t/64 U [64(t/64), t] : evict[p] > t}; evict agrees with
     the per-token form.  Sizes span one to many superblocks, with heavy ties,
     K above and below the 64-token block."""
@@ -190,11 +190,14 @@ def test_proto_prefix_blocks_match_sets(dev):
                 t = 64 * j - 1
                 want = sets[b, t, : min(t + 1, K)].tolist() if t >= 0 else []
                 row = [v for v in blk[b, j].tolist() if v != 2 ** 31 - 1]
-                assert row == want, (T, K, b, j)
+                assert sorted(row) == want, (T, K, b, j)
+                # best first: scores non-increasing, equal scores by ascending index
+                keys = [(-float(s[b, v]), v) for v in row]
+                assert keys == sorted(keys), (T, K, b, j)
             # per-token expansion of the compact form, spot rows
             for t in list(range(0, T, max(1, T // 97))) + [T - 1]:
                 j = t // 64
-                cand = [p for p in blk[b, j].tolist() if p != 2 ** 31 - 1] + list(range(64 * j, t + 1))
+                cand = sorted(p for p in blk[b, j].tolist() if p != 2 ** 31 - 1) + list(range(64 * j, t + 1))
                 got = [p for p in cand if ev[b, p] > t]
                 assert got == sets[b, t, : min(t + 1, K)].tolist(), (T, K, b, t)
 
