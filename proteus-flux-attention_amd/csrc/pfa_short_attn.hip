@@ -90,23 +90,44 @@ __device__ __forceinline__ bool zero_anchor(int64_t t, int s, int slots) {
 
 __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); }
 
-// Stage keys kpos[0..63] (valid positions) of one head into Ks / Vt.
-__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
-                                          int64_t ks_t, int64_t vs_t, int64_t key, uint16_t* Ks, uint16_t* Vt) {
-  const int tid = threadIdx.x;
-  const int j = tid >> 2, qd = tid & 3;
+// A 64-key tile is staged by 256 threads: thread tid fetches a quarter of
+// key row tid/4 (16 elements of K and of V) into registers; storing writes K
+// row-major and V transposed into LDS.  Fetch and store are split so the
+// next tile's loads are in flight while the current tile is computed.
+struct TileRegs {
+  uint4 k0, k1, v0, v1;
+};
+
+__device__ __forceinline__ TileRegs fetch_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
+                                               int64_t ks_t, int64_t vs_t, int64_t key) {
+  const int qd = threadIdx.x & 3;
   const uint4* ksrc = reinterpret_cast<const uint4*>(kb + key * ks_t + 16 * qd);
   const uint4* vsrc = reinterpret_cast<const uint4*>(vb + key * vs_t + 16 * qd);
-  uint4 k0 = ksrc[0], k1 = ksrc[1], v0 = vsrc[0], v1 = vsrc[1];
+  TileRegs r;
+  r.k0 = ksrc[0];
+  r.k1 = ksrc[1];
+  r.v0 = vsrc[0];
+  r.v1 = vsrc[1];
+  return r;
+}
+
+__device__ __forceinline__ void store_tile(const TileRegs& r, uint16_t* Ks, uint16_t* Vt) {
+  const int tid = threadIdx.x;
+  const int j = tid >> 2, qd = tid & 3;
   uint4* kd = reinterpret_cast<uint4*>(Ks + j * kLd + 16 * qd);
-  kd[0] = k0;
-  kd[1] = k1;
-  const uint32_t vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+  kd[0] = r.k0;
+  kd[1] = r.k1;
+  const uint32_t vw[8] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     Vt[(16 * qd + 2 * e) * kLd + j] = (uint16_t)(vw[e] & 0xffffu);
     Vt[(16 * qd + 2 * e + 1) * kLd + j] = (uint16_t)(vw[e] >> 16);
   }
+}
+
+__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
+                                          int64_t ks_t, int64_t vs_t, int64_t key, uint16_t* Ks, uint16_t* Vt) {
+  store_tile(fetch_tile(kb, vb, ks_t, vs_t, key), Ks, Vt);
 }
 
 // One 64-key tile for the 16 query rows of this wave.  mask(kl) decides
@@ -210,9 +231,9 @@ __device__ __forceinline__ int64_t xcd_block(int64_t P, int64_t nblk) {
 // Pass 1: anchors per (residue class, compact head)
 // ---------------------------------------------------------------------
 __global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
-  __shared__ __align__(16) uint16_t Ks[kTile * kLd];
-  __shared__ __align__(16) uint16_t Vt[64 * kLd];
-  __shared__ int32_t cls_m[kMaxClassRows];
+  __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
+  __shared__ __align__(16) uint16_t Vt[2][64 * kLd];
+  __shared__ uint16_t cls_m[kMaxClassRows];  // M < kMaxClassRows <= 65536
   __shared__ int32_t cls_r[kMaxClassRows];
   __shared__ int s_count;
   __shared__ int wave_cnt[4];
@@ -243,7 +264,7 @@ __global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
     for (int w = 0; w < wid; ++w) before += wave_cnt[w];
     if (act) {
       const int pos = before + __popcll(bal & ((1ull << lane) - 1ull));
-      cls_m[pos] = (int32_t)M;
+      cls_m[pos] = (uint16_t)M;
       cls_r[pos] = r;
     }
     __syncthreads();
@@ -274,16 +295,27 @@ __global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
     load_q(qb + tq * a.q.s_t, qf);
     QState st;
     init_state(st);
-    for (int64_t m0 = mlo; m0 <= mhi; m0 += kTile) {
-      const int64_t mk = min(m0 + (tid >> 2), mhi);
-      load_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * mk, Ks, Vt);
-      __syncthreads();
-      tile_step(qf, Ks, Vt, a.scale_log2,
+    // pipelined over the class's key tiles: tile i+1 is fetched while tile i
+    // is computed
+    const int ntile = mhi >= mlo ? (int)((mhi - mlo) / kTile + 1) : 0;
+    const int64_t jrow = tid >> 2;
+    if (ntile > 0) {
+      store_tile(fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min(mlo + jrow, mhi)), Ks[0], Vt[0]);
+    }
+    __syncthreads();
+    for (int i = 0; i < ntile; ++i) {
+      const int cur = i & 1;
+      const int64_t m0 = mlo + (int64_t)kTile * i;
+      TileRegs nxt;
+      const bool more = i + 1 < ntile;
+      if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min(m0 + kTile + jrow, mhi));
+      tile_step(qf, Ks[cur], Vt[cur], a.scale_log2,
                 [&](int kl) {
                   const int64_t m = m0 + kl;
                   return m <= mhi && m >= lo_q && m <= hi_q;
                 },
                 st);
+      if (more) store_tile(nxt, Ks[cur ^ 1], Vt[cur ^ 1]);
       __syncthreads();
     }
     float lt = st.l;
@@ -303,25 +335,29 @@ __global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
 // ---------------------------------------------------------------------
 // Pass 2: window + prototype keys per segment of consecutive rows
 // ---------------------------------------------------------------------
-__global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_part) {
-  __shared__ __align__(16) uint16_t Ks[kTile * kLd];
-  __shared__ __align__(16) uint16_t Vt[64 * kLd];
-  __shared__ int64_t r_t[kRows];
+__global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_part, int pcap) {
+  __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
+  __shared__ __align__(16) uint16_t Vt[2][64 * kLd];
+  __shared__ int32_t r_t[kRows];
   __shared__ int32_t r_p[kRows];
   __shared__ int32_t seg_begin[kRows + 1];
   __shared__ int s_nseg;
-  __shared__ int32_t plist[kMaxProto + 64 + 1];
-  __shared__ int32_t pev[kMaxProto + 64 + 1];
   __shared__ int s_plen;
+  // prototype key list of the current segment: position, evict, position mod stride
+  extern __shared__ int32_t pdyn[];
+  int32_t* pk = pdyn;
+  int32_t* pe = pk + pcap;
+  int32_t* pm = pe + pcap;
 
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   const int64_t r0 = lb * kRows;
   if (r0 >= a.N) return;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int w = a.local_w;
+  const int sa = a.stride, sl = a.slots;
   if (tid < kRows) {
     const int64_t r = r0 + tid;
-    r_t[tid] = r < a.N ? (int64_t)a.token_idx[r] : -1;
+    r_t[tid] = r < a.N ? a.token_idx[r] : -1;
     r_p[tid] = r < a.N ? a.row_head[r] : -1;
   }
   __syncthreads();
@@ -330,7 +366,7 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
     int i = 0;
     while (i < kRows && r_t[i] >= 0) {
       seg_begin[n++] = i;
-      const int64_t t0 = r_t[i];
+      const int t0 = r_t[i];
       const int p0 = r_p[i];
       ++i;
       while (i < kRows && r_t[i] >= 0 && r_p[i] == p0 && r_t[i] - t0 < w) ++i;
@@ -348,8 +384,8 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
     const int p = r_p[s0];
     const int bh = a.head_map ? a.head_map[p] : p;
     const int64_t bb = bh / a.H, hh = bh % a.H;
-    const int64_t t_first = r_t[s0], t_last = r_t[s1 - 1];
-    const int64_t lo_first = win_lo(t_first, w), lo_last = win_lo(t_last, w);
+    const int t_first = r_t[s0], t_last = r_t[s1 - 1];
+    const int lo_first = (int)win_lo(t_first, w), lo_last = (int)win_lo(t_last, w);
     const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
     const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
     const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
@@ -373,37 +409,42 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
           int32_t e = 0;
           if (v < lo_last) {
             e = ev[v];
-            keep = (int64_t)e > t_first;
+            keep = e > t_first;
           }
           const uint64_t bal = __ballot(keep);
           if (keep) {
-            plist[n + __popcll(bal & lt)] = v;
-            pev[n + __popcll(bal & lt)] = e;
+            const int pos = n + __popcll(bal & lt);
+            pk[pos] = v;
+            pe[pos] = e;
+            pm[pos] = sa > 0 ? v % sa : 0;
           }
           n += __popcll(bal);
           has0 = has0 || __ballot(keep && v == 0) != 0;
           if (__ballot(v == INT32_MAX)) break;  // padding: the row holds no more entries
         }
-        const int64_t q = (jb << 6) + lane;
+        const int q = (int)(jb << 6) + lane;
         bool keep = false;
         int32_t e = 0;
         if (q <= t_first && q < lo_last) {
           e = ev[q];
-          keep = (int64_t)e > t_first;
+          keep = e > t_first;
         }
         const uint64_t bal = __ballot(keep);
         if (keep) {
-          plist[n + __popcll(bal & lt)] = (int32_t)q;
-          pev[n + __popcll(bal & lt)] = e;
+          const int pos = n + __popcll(bal & lt);
+          pk[pos] = q;
+          pe[pos] = e;
+          pm[pos] = sa > 0 ? q % sa : 0;
         }
         n += __popcll(bal);
         has0 = has0 || __ballot(keep && q == 0) != 0;
       }
-      if (lo_last > 0 && a.stride > 0 && a.slots > 0 && !has0) {
+      if (lo_last > 0 && sa > 0 && sl > 0 && !has0) {
         // order inside the list does not matter
         if (lane == 0) {
-          plist[n] = 0;
-          pev[n] = -1;  // not in the prototype set: only the zero-anchor rule applies
+          pk[n] = 0;
+          pe[n] = -1;  // not in the prototype set: only the zero-anchor rule applies
+          pm[n] = 0;
         }
         ++n;
       }
@@ -414,42 +455,56 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
 
     // this lane's query row
     const bool qv = qs >= s0 && qs < s1;
-    const int64_t tq = qv ? r_t[qs] : t_first;
-    const int64_t loq = win_lo(tq, w);
-    const bool zf = qv && zero_anchor(tq, a.stride, a.slots) && loq > 0;
+    const int tq = qv ? r_t[qs] : t_first;
+    const int loq = (int)win_lo(tq, w);
+    const bool zf = qv && zero_anchor(tq, sa, sl) && loq > 0;
+    const bool anch_on = sa > 0 && sl > 0;
+    const int tmod = sa > 0 ? tq % sa : 0;
+    const int64_t alo = (int64_t)tq - (int64_t)sa * sl;  // strided anchors lie in [alo, tq)
     bf16x8_t qf[2];
-    load_q(qb + tq * a.q.s_t, qf);
+    load_q(qb + (int64_t)tq * a.q.s_t, qf);
     QState st;
     init_state(st);
 
-    // window tiles [lo_first, t_last]
-    for (int64_t k0 = lo_first; k0 <= t_last; k0 += kTile) {
-      const int64_t key = min(k0 + (tid >> 2), t_last);
-      load_tile(kb, vb, a.k.s_t, a.v.s_t, key, Ks, Vt);
-      __syncthreads();
-      tile_step(qf, Ks, Vt, a.scale_log2,
-                [&](int kl) {
-                  const int64_t kp = k0 + kl;
-                  return qv && kp <= tq && kp >= loq;
-                },
-                st);
-      __syncthreads();
-    }
-    // prototype (and zero-anchor) tiles
-    for (int j0 = 0; j0 < plen; j0 += kTile) {
-      const int jj = min(j0 + (tid >> 2), plen - 1);
-      load_tile(kb, vb, a.k.s_t, a.v.s_t, (int64_t)plist[jj], Ks, Vt);
-      __syncthreads();
-      tile_step(qf, Ks, Vt, a.scale_log2,
-                [&](int kl) {
-                  const int j = j0 + kl;
-                  if (!qv || j >= plen) return false;
-                  const int64_t kp = plist[j];
-                  if (kp >= loq) return false;
-                  const bool in_proto = (int64_t)pev[j] > tq && !strided_anchor(tq, kp, a.stride, a.slots);
-                  return in_proto || (kp == 0 && zf);
-                },
-                st);
+    // one pipelined pass over the window tiles [lo_first, t_last] and the
+    // prototype tiles: tile i+1 is fetched while tile i is computed
+    const int nw = (t_last - lo_first) / kTile + 1;
+    const int ntile = nw + (plen + kTile - 1) / kTile;
+    const int jrow = tid >> 2;
+    auto key_of = [&](int i) -> int64_t {
+      if (i < nw) return min(lo_first + kTile * i + jrow, t_last);
+      return pk[min((i - nw) * kTile + jrow, plen - 1)];
+    };
+    store_tile(fetch_tile(kb, vb, a.k.s_t, a.v.s_t, key_of(0)), Ks[0], Vt[0]);
+    __syncthreads();
+    for (int i = 0; i < ntile; ++i) {
+      const int cur = i & 1;
+      TileRegs nxt;
+      const bool more = i + 1 < ntile;
+      if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, key_of(i + 1));
+      if (i < nw) {
+        const int k0 = lo_first + kTile * i;
+        tile_step(qf, Ks[cur], Vt[cur], a.scale_log2,
+                  [&](int kl) {
+                    const int kp = k0 + kl;
+                    return qv && kp <= tq && kp >= loq;
+                  },
+                  st);
+      } else {
+        const int j0 = (i - nw) * kTile;
+        tile_step(qf, Ks[cur], Vt[cur], a.scale_log2,
+                  [&](int kl) {
+                    const int j = j0 + kl;
+                    if (!qv || j >= plen) return false;
+                    const int kp = pk[j];
+                    if (kp >= loq) return false;
+                    const bool anchor = anch_on && pm[j] == tmod && kp >= alo;
+                    const bool in_proto = pe[j] > tq && !anchor;
+                    return in_proto || (kp == 0 && zf);
+                  },
+                  st);
+      }
+      if (more) store_tile(nxt, Ks[cur ^ 1], Vt[cur ^ 1]);
       __syncthreads();
     }
 
@@ -477,7 +532,7 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
       }
       const float den = lt * fa + lp * fb;
       const float inv = 1.f / den;
-      uint16_t* op = (uint16_t*)a.out.ptr + bb * a.out.s_b + hh * a.out.s_h + tq * a.out.s_t;
+      uint16_t* op = (uint16_t*)a.out.ptr + bb * a.out.s_b + hh * a.out.s_h + (int64_t)tq * a.out.s_t;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         uint16_t o4[4];
@@ -517,7 +572,8 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   clear_error();
   PFA_CHECK_ARG(dtype == PFA_BF16 && D == 64, "pfa_shortlist_attn_fwd: bf16 and D=64 only (got dtype %d D %d)", dtype,
                 D);
-  PFA_CHECK_ARG(H > 0 && T > 0 && N >= 0 && P_cap > 0 && local_w >= 1, "pfa_shortlist_attn_fwd: bad sizes");
+  PFA_CHECK_ARG(H > 0 && T > 0 && T < INT32_MAX && N >= 0 && P_cap > 0 && local_w >= 1,
+                "pfa_shortlist_attn_fwd: bad sizes");
   if (N == 0) return PFA_OK;
   PFA_CHECK_ARG(q.ptr && k.ptr && v.ptr && out.ptr && token_idx && row_head && summary,
                 "pfa_shortlist_attn_fwd: null pointer");
@@ -547,7 +603,8 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   int64_t blocks = (N + kRows - 1) / kRows;
   blocks = (blocks + 7) / 8 * 8;
   PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_shortlist_attn_fwd: too many rows");
-  short_main_kernel<<<(unsigned)blocks, 256, 0, s>>>(a, anchors ? 1 : 0);
+  const int pcap = (proto_blocks ? proto_k : 0) + 64 + 1;
+  short_main_kernel<<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
   PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/main");
   return PFA_OK;
 }
