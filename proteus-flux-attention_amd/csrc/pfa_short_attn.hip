@@ -130,9 +130,13 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ kb, const
   store_tile(fetch_tile(kb, vb, ks_t, vs_t, key), Ks, Vt);
 }
 
-// One 64-key tile for the 16 query rows of this wave.  mask(kl) decides
-// whether tile key kl (0..63) is a candidate of this lane's query row.
-template <class MaskF>
+// One 64-key tile for the 16 query rows of this wave.  With MASKED,
+// mask(kl) decides whether tile key kl (0..63) is a candidate of this lane's
+// query row; without, every key of the tile is (the caller has checked that
+// the tile lies inside every row's key range).  exp2 runs on v_exp_f32
+// directly (arguments are <= 0; -inf gives 0), P is rounded to bf16 with
+// v_cvt_pk_bf16_f32 (round to nearest even).
+template <bool MASKED, class MaskF>
 __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_t* Ks, const uint16_t* Vt,
                                           float scale_log2, MaskF mask, QState& st) {
   const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
@@ -148,24 +152,29 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool ok = mask(16 * kb + 4 * g + i);
-      s[kb][i] = ok ? c[i] * scale_log2 : -INFINITY;
-      st.cnt += ok ? 1 : 0;
+      if constexpr (MASKED) {
+        const bool ok = mask(16 * kb + 4 * g + i);
+        s[kb][i] = ok ? c[i] * scale_log2 : -INFINITY;
+        st.cnt += ok ? 1 : 0;
+      } else {
+        s[kb][i] = c[i] * scale_log2;
+      }
       tmax = fmaxf(tmax, s[kb][i]);
     }
   }
+  if constexpr (!MASKED) st.cnt += 16;
   tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
   tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
   const float mn = fmaxf(st.m, tmax);
   float alpha = 1.f;
   float psum = 0.f;
   if (mn != -INFINITY) {
-    alpha = exp2f(st.m - mn);  // st.m == -inf -> 0
+    alpha = __builtin_amdgcn_exp2f(st.m - mn);  // st.m == -inf -> 0
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[kb][i] = exp2f(s[kb][i] - mn);  // -inf -> 0
+        s[kb][i] = __builtin_amdgcn_exp2f(s[kb][i] - mn);  // -inf -> 0
         psum += s[kb][i];
       }
   } else {
@@ -184,14 +193,14 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
   // its probabilities to bf16 too); the accumulator stays f32.
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
-    uint16_t pb16[8];
+    __bf16 pv[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pb16[i] = bf16_bits(s[2 * kc][i]);
-      pb16[4 + i] = bf16_bits(s[2 * kc + 1][i]);
+      pv[i] = (__bf16)s[2 * kc][i];
+      pv[4 + i] = (__bf16)s[2 * kc + 1][i];
     }
     bf16x8_t pb;
-    __builtin_memcpy(&pb, pb16, 16);
+    __builtin_memcpy(&pb, pv, 16);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       const uint16_t* vr = Vt + (16 * db + r16) * kLd + 32 * kc + 4 * g;
@@ -279,12 +288,25 @@ __global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
   for (int c0 = 0; c0 < nrows; c0 += kRows) {
     const int qs = 16 * wid + (lane & 15);
     const bool qv = c0 + qs < nrows;
-    const int64_t Mq = qv ? cls_m[c0 + qs] : 0;
+    const int Mq = qv ? cls_m[c0 + qs] : 0;
     const int rq = qv ? cls_r[c0 + qs] : 0;
     const int64_t tq = c + (int64_t)s * Mq;
-    const int64_t j0 = (tq - win_lo(tq, a.local_w)) / s + 1;
-    const int64_t hi_q = qv ? Mq - j0 : -1;
-    const int64_t lo_q = Mq - a.slots > 0 ? Mq - a.slots : 0;
+    const int j0 = (int)((tq - win_lo(tq, a.local_w)) / s) + 1;
+    const int hi_q = qv ? Mq - j0 : -1;
+    const int lo_q = Mq - a.slots > 0 ? Mq - a.slots : 0;
+    // wave rows ascending in M: lo_q and hi_q are non-decreasing
+    const int fr = 16 * wid, lr = min(nrows - c0, 16 * wid + 16) - 1;
+    const bool wave_rows = fr <= lr;
+    const bool wave_full = lr == 16 * wid + 15;
+    int w_lolo = 0, w_lohi = 0, w_hilo = -1, w_hihi = -1;
+    if (wave_rows) {
+      const int Ma = cls_m[c0 + fr], Mb = cls_m[c0 + lr];
+      const int64_t ta = c + (int64_t)s * Ma, tb = c + (int64_t)s * Mb;
+      w_lolo = Ma - a.slots > 0 ? Ma - a.slots : 0;
+      w_lohi = Mb - a.slots > 0 ? Mb - a.slots : 0;
+      w_hilo = Ma - ((int)((ta - win_lo(ta, a.local_w)) / s) + 1);
+      w_hihi = Mb - ((int)((tb - win_lo(tb, a.local_w)) / s) + 1);
+    }
     // key range of the chunk (lo/hi are non-decreasing in M)
     const int last = min(nrows, c0 + kRows) - 1;
     const int64_t Mf = cls_m[c0], Ml = cls_m[last];
@@ -305,16 +327,18 @@ __global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
     __syncthreads();
     for (int i = 0; i < ntile; ++i) {
       const int cur = i & 1;
-      const int64_t m0 = mlo + (int64_t)kTile * i;
+      const int m0 = (int)mlo + kTile * i;
       TileRegs nxt;
       const bool more = i + 1 < ntile;
-      if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min(m0 + kTile + jrow, mhi));
-      tile_step(qf, Ks[cur], Vt[cur], a.scale_log2,
-                [&](int kl) {
-                  const int64_t m = m0 + kl;
-                  return m <= mhi && m >= lo_q && m <= hi_q;
-                },
-                st);
+      if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min((int64_t)m0 + kTile + jrow, mhi));
+      const bool empty = !wave_rows || m0 > w_hihi || m0 + kTile - 1 < w_lolo;
+      const bool full = wave_full && m0 >= w_lohi && m0 + kTile - 1 <= w_hilo && m0 + kTile - 1 <= mhi;
+      auto cls_mask = [&](int kl) {
+        const int m = m0 + kl;
+        return m <= (int)mhi && m >= lo_q && m <= hi_q;
+      };
+      if (full) tile_step<false>(qf, Ks[cur], Vt[cur], a.scale_log2, cls_mask, st);
+      else if (!empty) tile_step<true>(qf, Ks[cur], Vt[cur], a.scale_log2, cls_mask, st);
       if (more) store_tile(nxt, Ks[cur ^ 1], Vt[cur ^ 1]);
       __syncthreads();
     }
@@ -466,6 +490,14 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
     QState st;
     init_state(st);
 
+    // the rows of this wave are ascending in token: their key ranges lie in
+    // [win_lo(first), last] and all contain [win_lo(last), first]
+    const int fr = max(s0, 16 * wid), lr = min(s1, 16 * wid + 16) - 1;
+    const bool wave_rows = fr <= lr;
+    const bool wave_full = fr == 16 * wid && lr == 16 * wid + 15;
+    const int w_tlo = wave_rows ? r_t[fr] : 0, w_thi = wave_rows ? r_t[lr] : -1;
+    const int w_llo = (int)win_lo(w_tlo, w), w_lhi = (int)win_lo(w_thi < 0 ? 0 : w_thi, w);
+
     // one pipelined pass over the window tiles [lo_first, t_last] and the
     // prototype tiles: tile i+1 is fetched while tile i is computed
     const int nw = (t_last - lo_first) / kTile + 1;
@@ -484,15 +516,17 @@ __global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_pa
       if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, key_of(i + 1));
       if (i < nw) {
         const int k0 = lo_first + kTile * i;
-        tile_step(qf, Ks[cur], Vt[cur], a.scale_log2,
-                  [&](int kl) {
-                    const int kp = k0 + kl;
-                    return qv && kp <= tq && kp >= loq;
-                  },
-                  st);
-      } else {
+        const bool empty = !wave_rows || k0 > w_thi || k0 + kTile - 1 < w_llo;
+        const bool full = wave_full && k0 >= w_lhi && k0 + kTile - 1 <= w_tlo;
+        auto win_mask = [&](int kl) {
+          const int kp = k0 + kl;
+          return qv && kp <= tq && kp >= loq;
+        };
+        if (full) tile_step<false>(qf, Ks[cur], Vt[cur], a.scale_log2, win_mask, st);
+        else if (!empty) tile_step<true>(qf, Ks[cur], Vt[cur], a.scale_log2, win_mask, st);
+      } else if (wave_rows) {
         const int j0 = (i - nw) * kTile;
-        tile_step(qf, Ks[cur], Vt[cur], a.scale_log2,
+        tile_step<true>(qf, Ks[cur], Vt[cur], a.scale_log2,
                   [&](int kl) {
                     const int j = j0 + kl;
                     if (!qv || j >= plen) return false;
