@@ -301,6 +301,87 @@ int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D,
  * ==================================================================== */
 int pfa_zero_fill(void* ptr, size_t bytes, void* stream);
 
+/* ====================================================================
+ * Chunk salience top-k.  Replaces _select_top_tokens + _nucleus_select
+ * (src/proteus_attention/tools/chunked_shortlist.py:140-208): scores
+ * (n) f32 with positions whose keep_mask byte is 0 (keep_mask may be NULL)
+ * set to -inf; non-finite scores rank as -1e9; the first
+ * keep = min(budget, n) positions in the order (score desc, position asc)
+ * are taken, or with top_p < 1 the nucleus count
+ * #(cumulative softmax mass < top_p) + 1 (clamped to [1, min(budget, n)]);
+ * with drop_nonfinite, entries whose (masked) score is not finite are then
+ * dropped (the filter of _select_top_tokens).  Writes, in
+ * selection order, values_out (budget) f32 and indices_out (budget) int64
+ * (position + index_offset), and count_out (1) int32 (0 when no score is
+ * finite: the reference's "None").  Ties: lowest position first.
+ * ==================================================================== */
+int pfa_chunk_topk_workspace_size(int64_t n, int budget, size_t* bytes);
+int pfa_chunk_topk(const float* scores, const uint8_t* keep_mask, int64_t n,
+                   int budget, float top_p, int64_t index_offset,
+                   int drop_nonfinite, float* values_out, int64_t* indices_out,
+                   int32_t* count_out, void* workspace, size_t ws_bytes,
+                   void* stream);
+
+/* ====================================================================
+ * Global shortlist merge.  Replaces _finalise_indices
+ * (chunked_shortlist.py:211-254): the n candidates (scores f32, indices
+ * int64 in [-2^31, 2^31)) ordered by score descending (ties: lower
+ * candidate position first), one survivor per index -- its last entry in
+ * that order -- then the first max_tokens survivors, returned sorted by
+ * index: keep_indices_out (max_tokens) int64, keep_scores_out (max_tokens)
+ * f32, count_out (1) int32 = number written.
+ * ==================================================================== */
+int pfa_shortlist_finalise_workspace_size(int64_t n, size_t* bytes);
+int pfa_shortlist_finalise(const float* scores, const int64_t* indices, int64_t n,
+                           int64_t max_tokens, int64_t* keep_indices_out,
+                           float* keep_scores_out, int32_t* count_out,
+                           void* workspace, size_t ws_bytes, void* stream);
+
+/* ====================================================================
+ * Per-(head, row) symmetric int8 quantisation of the shortlisted K or V
+ * rows of the chunked pipeline's final pass.  The per-head scheme of
+ * AdaptiveSparseAttention._quantize_per_head_int8 (aspa.py:1312-1363,
+ * "max" mode) applied to each (head, row) of D elements:
+ * scale = max(absmax / 127, 1e-6), q = clamp(round_half_even(x / scale),
+ * -127, 127).  src row r, head h at src + r*row_stride + h*D (dtype
+ * PFA_F32 / PFA_BF16 / PFA_F16); dst (H, n_rows, D) int8, scales
+ * (H, n_rows) f32.
+ * ==================================================================== */
+int pfa_quantize_rows_int8(const void* src, int dtype, int64_t n_rows,
+                           int64_t row_stride, int H, int D, int8_t* dst,
+                           float* scales, void* stream);
+
+/* ====================================================================
+ * RoPE in place on arbitrary rows: H heads of D elements at
+ * x + r*row_stride, rotated with table row positions[r] (positions NULL:
+ * pos_offset + r).  Same arithmetic and rounding as pfa_rope_qk_inplace
+ * (_apply_rope_embedding, aspa.py:606-618); used for query slices of a
+ * streamed chunk and for shortlisted keys at their original positions.
+ * ==================================================================== */
+int pfa_rope_rows_inplace(void* x, int dtype, int64_t n_rows, int64_t row_stride,
+                          int H, int D, const void* cos_tab, const void* sin_tab,
+                          const int32_t* positions, int64_t pos_offset,
+                          void* stream);
+
+/* ====================================================================
+ * All-query attention over an int8 shortlist (bf16, D = 64): the chunked
+ * pipeline's final pass in its all-query form.  The reference attends the
+ * reduced sequence to itself (chunked_shortlist.py:710-739); this entry
+ * point lets every one of T query tokens attend to the S shortlisted keys,
+ * causal by original position when `causal` (key j visible to query t iff
+ * key_pos[j] <= t; key_pos ascending).  K/V are int8 (H, S, D) with
+ * per-(head, row) scales (H, S) from pfa_quantize_rows_int8, dequantised
+ * to bf16 inside each LDS tile.  q/out are bf16 [h][t][d] through
+ * pfa_tensor4 strides (s_b unused: one sequence).  A query with no
+ * visible key gets a zero row.  S >= 1.
+ * ==================================================================== */
+int pfa_int8_kv_attn_workspace_size(int64_t T, size_t* bytes);
+int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, int H, int D,
+                         const int8_t* k8, const int8_t* v8, const float* k_scale,
+                         const float* v_scale, const int32_t* key_pos, int S,
+                         int causal, float scale, void* workspace,
+                         size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -390,3 +390,106 @@ def causal_attention_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> t
     s = (q.float() @ k.float().transpose(1, 2)) / math.sqrt(q.size(-1))
     s = s.masked_fill(torch.triu(torch.ones(T, T, dtype=torch.bool), 1), float("-inf"))
     return torch.softmax(s, -1) @ v.float()
+
+
+# ---------------------------------------------------------------------------
+# chunked shortlist selection (tools/chunked_shortlist.py:140-254)
+# ---------------------------------------------------------------------------
+
+def nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float, keep_mask: Optional[torch.Tensor] = None,
+                   index_offset: int = 0, drop_nonfinite: bool = False):
+    """_nucleus_select (chunked_shortlist.py:175-208) with the masking and
+    finite filter of _select_top_tokens (:140-172).  The order is (score
+    desc, position asc) -- a stable descending sort; the reference's
+    argsort leaves ties open.  Returns (values, positions + offset) or None."""
+
+    s = scores.to(torch.float32).clone()
+    if keep_mask is not None:
+        s = torch.where(keep_mask.to(torch.bool), s, torch.full_like(s, float("-inf")))
+    n = s.numel()
+    limit = min(int(max_tokens), n)
+    if limit <= 0:
+        return None
+    finite = torch.isfinite(s)
+    if not bool(finite.any()):
+        return None
+    safe = torch.where(finite, s, torch.full_like(s, -1e9))
+    order = torch.sort(safe, descending=True, stable=True).indices
+    if top_p >= 1.0:
+        keep = limit
+    else:
+        probs = torch.softmax(safe, dim=-1)[order]
+        mass = torch.cumsum(probs, dim=-1)
+        keep = int((mass < float(top_p)).sum())
+        if keep < n:
+            keep += 1
+        keep = min(limit, max(1, keep))
+    sel = order[:keep]
+    vals = s[sel]
+    if drop_nonfinite:
+        ok = torch.isfinite(vals)
+        sel, vals = sel[ok], vals[ok]
+        if sel.numel() == 0:
+            return None
+    return vals, sel + int(index_offset)
+
+
+def finalise_indices(scores: torch.Tensor, indices: torch.Tensor, max_tokens: int):
+    """_finalise_indices (chunked_shortlist.py:211-254): score-descending
+    order (stable), one survivor per index -- its last entry in that order
+    (the composite key index*(n+1)-position of :233-243) -- the first
+    max_tokens survivors, sorted by index.  Returns (indices int64, scores)."""
+
+    sc = scores.to(torch.float32)
+    order = torch.sort(sc, descending=True, stable=True).indices
+    s_ord, i_ord = sc[order], indices[order].to(torch.long)
+    n = i_ord.numel()
+    pos = torch.arange(n, dtype=torch.long)
+    by_idx = torch.sort(i_ord * (n + 1) - pos, stable=True).indices
+    grouped = i_ord[by_idx]
+    first = torch.ones(n, dtype=torch.bool)
+    first[1:] = grouped[1:] != grouped[:-1]
+    keep = torch.sort(by_idx[first]).values[:max_tokens]
+    ki, ks = i_ord[keep], s_ord[keep]
+    back = torch.sort(ki).indices
+    return ki[back], ks[back]
+
+
+# ---------------------------------------------------------------------------
+# all-query final pass over an int8 shortlist (no reference counterpart:
+# the reference attends the reduced sequence to itself,
+# chunked_shortlist.py:710-739)
+# ---------------------------------------------------------------------------
+
+def quantize_rows_int8(x: torch.Tensor, heads: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """x (S, H*D) -> int8 (H, S, D), scales (H, S): quantize_per_head_int8
+    applied to every (head, row) slice of D elements."""
+
+    S, C = x.shape
+    D = C // heads
+    slices = x.reshape(S, heads, D).permute(1, 0, 2).reshape(heads * S, 1, D)
+    q, s = quantize_per_head_int8(slices)
+    return q.view(heads, S, D), s.view(heads, S)
+
+
+def int8_kv_attention(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor, k_scale: torch.Tensor,
+                      v_scale: torch.Tensor, key_pos: torch.Tensor, causal: bool = True,
+                      scale: Optional[float] = None) -> torch.Tensor:
+    """q (T, H, D); k8/v8 (H, S, D) int8 with scales (H, S); key_pos (S,).
+    Dequantise in f32, softmax(q k^T * scale + mask) v in f32 with key j
+    visible to query t iff key_pos[j] <= t (causal); rows with no visible
+    key are zero.  Returns (T, H, D) f32."""
+
+    T, H, D = q.shape
+    sc = (1.0 / math.sqrt(D)) if scale is None else float(scale)
+    k = k8.to(torch.float32) * k_scale.to(torch.float32).unsqueeze(-1)
+    v = v8.to(torch.float32) * v_scale.to(torch.float32).unsqueeze(-1)
+    qh = q.to(torch.float32).permute(1, 0, 2)  # (H, T, D)
+    s = (qh @ k.transpose(1, 2)) * sc  # (H, T, S)
+    vis = torch.ones(T, k.size(1), dtype=torch.bool)
+    if causal:
+        vis = key_pos.view(1, -1).to(torch.long) <= torch.arange(T).view(-1, 1)
+    s = s.masked_fill(~vis.unsqueeze(0), float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    p = torch.nan_to_num(p, nan=0.0)  # all-masked rows -> zero output
+    return (p @ v).permute(1, 0, 2).contiguous()

@@ -1,0 +1,338 @@
+// All-query attention over an int8 shortlist: the final pass of the chunked
+// shortlist pipeline (config 5).  Every query token t of one sequence
+// attends to the S shortlisted keys; with `causal`, only to keys whose
+// original position key_pos[j] <= t.  K and V of the shortlist are int8 with
+// one symmetric scale per (head, key row); they are dequantised inside the
+// tile: each staged 64-key tile is converted k8 * k_scale -> bf16 (and
+// likewise V) in LDS, then S = Q K^T and O += P V run on
+// v_mfma_f32_16x16x32_bf16 with an online softmax in f32 registers.
+//
+// Workgroup: 8 waves, 256 consecutive query tokens of one head (32 per wave
+// in two 16-query MFMA column groups).  The shortlist is sorted by
+// position, so a query tile's keys are a prefix of it: keys below
+// rng.x (position < first token of the tile) are visible to every query and
+// run unmasked; the at most few keys in [rng.x, rng.y) are masked per
+// (query, key).  Block b handles head b % H, so on 8 XCDs each XCD's L2
+// holds one head's int8 K/V; tiles run heaviest first.
+#include "pfa_common.h"
+
+namespace pfa {
+namespace fin {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kQ = 32 * kWaves;  // queries per workgroup
+constexpr int kTile = 64;        // keys per tile
+constexpr int kLd = 72;          // padded LDS row (bf16 elements)
+constexpr int kD = 64;
+
+struct Args {
+  const uint16_t* q;
+  int64_t q_sh, q_st;
+  uint16_t* out;
+  int64_t o_sh, o_st;
+  const int8_t* k8;
+  const int8_t* v8;
+  const float* ks;
+  const float* vs;
+  const int32_t* kpos;
+  const int2* rng;
+  int H, S, causal, nqt;
+  int64_t T;
+  float scale_log2;
+};
+
+struct St {
+  float m, l;
+  f32x4_t acc[4];
+};
+
+// one 64-key tile staged by 512 threads: thread -> key tid/8, elements
+// 8*(tid%8) .. +7 of that key's K and V rows
+struct Fetch {
+  uint2 k, v;
+  float kscale, vscale;
+  int pos;
+};
+
+__device__ __forceinline__ Fetch fetch(const int8_t* kb, const int8_t* vb, const float* ksb, const float* vsb,
+                                       const int32_t* kpos, int key) {
+  const int oct = threadIdx.x & 7;
+  Fetch f;
+  f.k = *reinterpret_cast<const uint2*>(kb + (int64_t)key * kD + 8 * oct);
+  f.v = *reinterpret_cast<const uint2*>(vb + (int64_t)key * kD + 8 * oct);
+  f.kscale = ksb[key];
+  f.vscale = vsb[key];
+  f.pos = kpos[key];
+  return f;
+}
+
+__device__ __forceinline__ float i8f(uint32_t w, int e) { return (float)(int)(int8_t)((w >> (8 * e)) & 0xffu); }
+
+__device__ __forceinline__ void store(const Fetch& f, uint16_t* Ks, uint16_t* Vt, int32_t* kp) {
+  const int j = threadIdx.x >> 3, oct = threadIdx.x & 7;
+  __bf16 kd[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) kd[e] = (__bf16)(i8f(e < 4 ? f.k.x : f.k.y, e & 3) * f.kscale);
+  uint4 kw;
+  __builtin_memcpy(&kw, kd, 16);
+  *reinterpret_cast<uint4*>(Ks + j * kLd + 8 * oct) = kw;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 v = (__bf16)(i8f(e < 4 ? f.v.x : f.v.y, e & 3) * f.vscale);
+    uint16_t bits;
+    __builtin_memcpy(&bits, &v, 2);
+    Vt[(8 * oct + e) * kLd + j] = bits;
+  }
+  if (oct == 0) kp[j] = f.pos;
+}
+
+template <bool MASKED>
+__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const uint16_t* Ks, const uint16_t* Vt,
+                                     const int32_t* kp, int key0, int S, int causal, const int (&tq)[2],
+                                     float sl2, St (&st)[2]) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
+  float s[2][16];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(Ks + (16 * kb + r16) * kLd + 8 * g);
+    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(Ks + (16 * kb + r16) * kLd + 32 + 8 * g);
+#pragma unroll
+    for (int gr = 0; gr < 2; ++gr) {
+      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[gr][0], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[gr][1], c, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (MASKED) {
+          const int kl = 16 * kb + 4 * g + i;
+          const bool ok = key0 + kl < S && (!causal || kp[kl] <= tq[gr]);
+          s[gr][4 * kb + i] = ok ? c[i] : -INFINITY;
+        } else {
+          s[gr][4 * kb + i] = c[i];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int gr = 0; gr < 2; ++gr) {
+    float tmax = s[gr][0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[gr][i]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mn = fmaxf(st[gr].m, tmax);
+    if (mn == -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[gr][i] = 0.f;
+      continue;
+    }
+    const float off = mn * sl2;
+    const float alpha = __builtin_amdgcn_exp2f(st[gr].m * sl2 - off);  // m == -inf -> 0
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[gr][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[gr][i], sl2, -off));  // -inf -> 0
+      psum += s[gr][i];
+    }
+    st[gr].l = st[gr].l * alpha + psum;
+    st[gr].m = mn;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st[gr].acc[db][i] *= alpha;
+  }
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    bf16x8_t pb[2];
+#pragma unroll
+    for (int gr = 0; gr < 2; ++gr) {
+      __bf16 pv[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pv[i] = (__bf16)s[gr][8 * kc + i];
+        pv[4 + i] = (__bf16)s[gr][8 * kc + 4 + i];
+      }
+      __builtin_memcpy(&pb[gr], pv, 16);
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint16_t* vr = Vt + (16 * db + r16) * kLd + 32 * kc + 4 * g;
+      const uint2 lo8 = *reinterpret_cast<const uint2*>(vr);
+      const uint2 hi8 = *reinterpret_cast<const uint2*>(vr + 16);
+      const uint32_t w4[4] = {lo8.x, lo8.y, hi8.x, hi8.y};
+      bf16x8_t va;
+      __builtin_memcpy(&va, w4, 16);
+#pragma unroll
+      for (int gr = 0; gr < 2; ++gr)
+        st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gr], st[gr].acc[db], 0, 0, 0);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restrict__ kpos, int S, int64_t T,
+                                                         int nqt, int causal, int2* __restrict__ rng) {
+  const int qt = blockIdx.x * blockDim.x + threadIdx.x;
+  if (qt >= nqt) return;
+  if (!causal) {
+    rng[qt] = make_int2(S, S);
+    return;
+  }
+  const int64_t t0 = (int64_t)qt * kQ;
+  const int64_t t1 = (t0 + kQ < T ? t0 + kQ : T) - 1;
+  int lo = 0, hi = S;  // first j with kpos[j] >= t0
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if ((int64_t)kpos[mid] < t0) lo = mid + 1;
+    else hi = mid;
+  }
+  const int below = lo;
+  hi = S;  // first j with kpos[j] > t1
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if ((int64_t)kpos[mid] <= t1) lo = mid + 1;
+    else hi = mid;
+  }
+  rng[qt] = make_int2(below, lo);
+}
+
+__global__ void __launch_bounds__(kThreads) final_attn_kernel(Args a) {
+  __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
+  __shared__ __align__(16) uint16_t Vt[2][kD * kLd];
+  __shared__ int32_t kp[2][kTile];
+
+  const int bid = blockIdx.x;
+  const int h = bid % a.H;
+  const int qt = a.nqt - 1 - bid / a.H;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int2 rg = a.rng[qt];
+  const int64_t t_base = (int64_t)qt * kQ;
+  int tq[2];
+  bool qv[2];
+#pragma unroll
+  for (int gr = 0; gr < 2; ++gr) {
+    const int64_t t = t_base + 32 * wid + 16 * gr + r16;
+    qv[gr] = t < a.T;
+    tq[gr] = (int)(qv[gr] ? t : a.T - 1);
+  }
+  const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
+  bf16x8_t qf[2][2];
+#pragma unroll
+  for (int gr = 0; gr < 2; ++gr)
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc) {
+      const uint4 w = *reinterpret_cast<const uint4*>(qh + (int64_t)tq[gr] * a.q_st + 32 * dc + 8 * g);
+      __builtin_memcpy(&qf[gr][dc], &w, 16);
+    }
+  St st[2];
+#pragma unroll
+  for (int gr = 0; gr < 2; ++gr) {
+    st[gr].m = -INFINITY;
+    st[gr].l = 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) st[gr].acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const int8_t* kb = a.k8 + (int64_t)h * a.S * kD;
+  const int8_t* vb = a.v8 + (int64_t)h * a.S * kD;
+  const float* ksb = a.ks + (int64_t)h * a.S;
+  const float* vsb = a.vs + (int64_t)h * a.S;
+  const int ntile = (rg.y + kTile - 1) / kTile;
+  const int jrow = tid >> 3;
+  if (ntile > 0) store(fetch(kb, vb, ksb, vsb, a.kpos, min(jrow, a.S - 1)), Ks[0], Vt[0], kp[0]);
+  __syncthreads();
+  for (int i = 0; i < ntile; ++i) {
+    const int cur = i & 1;
+    const bool more = i + 1 < ntile;
+    Fetch nxt;
+    if (more) nxt = fetch(kb, vb, ksb, vsb, a.kpos, min(kTile * (i + 1) + jrow, a.S - 1));
+    const int key0 = kTile * i;
+    if (key0 + kTile <= rg.x) tile<false>(qf, Ks[cur], Vt[cur], kp[cur], key0, a.S, a.causal, tq, a.scale_log2, st);
+    else tile<true>(qf, Ks[cur], Vt[cur], kp[cur], key0, a.S, a.causal, tq, a.scale_log2, st);
+    if (more) store(nxt, Ks[cur ^ 1], Vt[cur ^ 1], kp[cur ^ 1]);
+    __syncthreads();
+  }
+  uint16_t* oh = a.out + (int64_t)h * a.o_sh;
+#pragma unroll
+  for (int gr = 0; gr < 2; ++gr) {
+    float l = st[gr].l;
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (!qv[gr]) continue;
+    const float inv = l > 0.f ? 1.f / l : 0.f;  // a query with no visible key writes zeros
+    uint16_t* op = oh + (int64_t)tq[gr] * a.o_st;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      uint16_t o4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o4[i] = f32_to_bf16(st[gr].acc[db][i] * inv);
+      *reinterpret_cast<uint2*>(op + 16 * db + 4 * g) =
+          make_uint2((uint32_t)o4[0] | ((uint32_t)o4[1] << 16), (uint32_t)o4[2] | ((uint32_t)o4[3] << 16));
+    }
+  }
+}
+
+}  // namespace fin
+}  // namespace pfa
+
+using namespace pfa;
+
+extern "C" int pfa_int8_kv_attn_workspace_size(int64_t T, size_t* bytes) {
+  clear_error();
+  PFA_CHECK_ARG(bytes && T >= 0, "pfa_int8_kv_attn_workspace_size: bad arguments");
+  const int64_t nqt = (T + fin::kQ - 1) / fin::kQ;
+  *bytes = (size_t)(nqt > 0 ? nqt : 1) * sizeof(int2);
+  return PFA_OK;
+}
+
+extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, int H, int D, const int8_t* k8,
+                                    const int8_t* v8, const float* k_scale, const float* v_scale,
+                                    const int32_t* key_pos, int S, int causal, float scale, void* workspace,
+                                    size_t ws_bytes, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(D == fin::kD, "pfa_int8_kv_attn_fwd: D must be 64 (got %d)", D);
+  PFA_CHECK_ARG(T >= 0 && T < INT32_MAX && H > 0 && S >= 0, "pfa_int8_kv_attn_fwd: bad sizes T=%lld H=%d S=%d",
+                (long long)T, H, S);
+  if (T == 0) return PFA_OK;
+  PFA_CHECK_ARG(q.ptr && out.ptr, "pfa_int8_kv_attn_fwd: null q/out");
+  auto al = [](const pfa_tensor4& x) { return ((uintptr_t)x.ptr % 16) == 0 && x.s_h % 8 == 0 && x.s_t % 8 == 0; };
+  PFA_CHECK_ARG(al(q) && al(out), "pfa_int8_kv_attn_fwd: q/out must be 16-byte aligned with strides of 8 elements");
+  hipStream_t s = as_stream(stream);
+  PFA_CHECK_ARG(S > 0, "pfa_int8_kv_attn_fwd: empty shortlist (S must be >= 1)");
+  PFA_CHECK_ARG(k8 && v8 && k_scale && v_scale && key_pos, "pfa_int8_kv_attn_fwd: null shortlist pointer");
+  PFA_CHECK_ARG(((uintptr_t)k8 % 8) == 0 && ((uintptr_t)v8 % 8) == 0, "pfa_int8_kv_attn_fwd: k8/v8 must be 8-byte aligned");
+  size_t need = 0;
+  pfa_int8_kv_attn_workspace_size(T, &need);
+  PFA_CHECK_ARG(workspace && ws_bytes >= need, "pfa_int8_kv_attn_fwd: workspace of %zu bytes required", need);
+  const int nqt = (int)((T + fin::kQ - 1) / fin::kQ);
+  int2* rng = (int2*)workspace;
+  fin::key_ranges_kernel<<<(unsigned)((nqt + 255) / 256), 256, 0, s>>>(key_pos, S, T, nqt, causal ? 1 : 0, rng);
+  PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/ranges");
+  fin::Args a;
+  a.q = (const uint16_t*)q.ptr;
+  a.q_sh = q.s_h;
+  a.q_st = q.s_t;
+  a.out = (uint16_t*)out.ptr;
+  a.o_sh = out.s_h;
+  a.o_st = out.s_t;
+  a.k8 = k8;
+  a.v8 = v8;
+  a.ks = k_scale;
+  a.vs = v_scale;
+  a.kpos = key_pos;
+  a.rng = rng;
+  a.H = H;
+  a.S = S;
+  a.causal = causal ? 1 : 0;
+  a.nqt = nqt;
+  a.T = T;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int64_t blocks = (int64_t)nqt * H;
+  PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_int8_kv_attn_fwd: too many query tiles");
+  fin::final_attn_kernel<<<(unsigned)blocks, fin::kThreads, 0, s>>>(a);
+  PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd");
+  return PFA_OK;
+}

@@ -48,6 +48,14 @@ EXPORTED_SYMBOLS = (
     "pfa_head_max_token",
     "pfa_rope_qk_inplace",
     "pfa_zero_fill",
+    "pfa_chunk_topk_workspace_size",
+    "pfa_chunk_topk",
+    "pfa_shortlist_finalise_workspace_size",
+    "pfa_shortlist_finalise",
+    "pfa_quantize_rows_int8",
+    "pfa_rope_rows_inplace",
+    "pfa_int8_kv_attn_workspace_size",
+    "pfa_int8_kv_attn_fwd",
 )
 
 
@@ -102,6 +110,15 @@ _SIGNATURES = {
     "pfa_head_max_token": ([_vp, _vp, _i32, _vp, _vp], _i32),
     "pfa_rope_qk_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
     "pfa_zero_fill": ([_vp, _sz, _vp], _i32),
+    "pfa_chunk_topk_workspace_size": ([_i64, _i32, ctypes.POINTER(_sz)], _i32),
+    "pfa_chunk_topk": ([_vp, _vp, _i64, _i32, _f32, _i64, _i32, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
+    "pfa_shortlist_finalise_workspace_size": ([_i64, ctypes.POINTER(_sz)], _i32),
+    "pfa_shortlist_finalise": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
+    "pfa_quantize_rows_int8": ([_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
+    "pfa_rope_rows_inplace": ([_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _vp], _i32),
+    "pfa_int8_kv_attn_workspace_size": ([_i64, ctypes.POINTER(_sz)], _i32),
+    "pfa_int8_kv_attn_fwd": ([Tensor4, Tensor4, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp,
+                              _sz, _vp], _i32),
 }
 
 

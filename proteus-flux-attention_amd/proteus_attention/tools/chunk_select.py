@@ -1,12 +1,14 @@
 """Chunk salience selection and global shortlist merge on the device.
 
-nucleus_select  -- reference chunked_shortlist.py:175-208
+nucleus_select  -- reference chunked_shortlist.py:175-208 (and the masking
+                   and finite filter of _select_top_tokens, :140-172)
 finalise        -- reference chunked_shortlist.py:211-254
 
-Both keep the reference's semantics with the tie rule made explicit: equal
-scores are ordered by ascending position (the reference's unstable argsort
-leaves it open).  Inputs are device tensors; the work is a handful of
-device sorts over at most a few thousand (value, index) pairs per call.
+Both run as HIP kernels of libpfa_hip.so (``pfa_chunk_topk``: radix select
+plus an LDS bitonic sort of the selected keys; ``pfa_shortlist_finalise``:
+two u64 key sorts and a single-workgroup emit).  The tie rule is made
+explicit: equal scores are ordered by ascending position (the reference's
+unstable argsort leaves it open).  Inputs are device tensors.
 """
 from __future__ import annotations
 
@@ -14,44 +16,48 @@ from typing import Optional, Tuple
 
 import torch
 
-
-def _order_desc(values: torch.Tensor) -> torch.Tensor:
-    # stable descending sort: ties keep ascending position
-    return torch.sort(values, descending=True, stable=True).indices
+from .. import _hip
+from ..kernels.sparse_attn import _size_out, _workspace
 
 
 def nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float,
-                   keep_mask: Optional[torch.Tensor] = None) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+                   keep_mask: Optional[torch.Tensor] = None, index_offset: int = 0,
+                   drop_nonfinite: bool = False) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
     """Top tokens of one chunk by score with nucleus (top-p) truncation.
 
-    Returns ``(selected_scores, selected_positions)`` in selection order, or
-    None when nothing is finite.
-    """
+    Positions where ``keep_mask`` is False score -inf.  Returns
+    ``(selected_scores, selected_positions + index_offset)`` in selection
+    order (int64 positions), or None when nothing is finite or nothing is
+    selected.  ``drop_nonfinite`` removes selected entries whose score is
+    not finite (the filter _select_top_tokens applies)."""
 
     if scores.ndim != 1:
         raise ValueError("scores tensor must be 1-D for nucleus selection.")
-    scores = scores.to(torch.float32)
-    if keep_mask is not None:
-        scores = torch.where(keep_mask.to(torch.bool), scores, torch.full_like(scores, float("-inf")))
-    limit = min(int(max_tokens), int(scores.numel()))
+    if not (float(top_p) > 0.0):
+        raise ValueError("top_p must be positive")
+    device = _hip.require_device(scores, keep_mask, what="nucleus_select")
+    n = int(scores.numel())
+    limit = min(int(max_tokens), n)
     if limit <= 0:
         return None
-    finite = torch.isfinite(scores)
-    if not bool(finite.any()):
+    sc = scores.to(torch.float32).contiguous()
+    mk = None
+    if keep_mask is not None:
+        if keep_mask.shape != scores.shape:
+            raise ValueError("keep_mask must match scores")
+        mk = keep_mask.to(torch.bool).contiguous().view(torch.uint8)
+    lib = _hip.lib()
+    vals = torch.empty(limit, dtype=torch.float32, device=device)
+    idx = torch.empty(limit, dtype=torch.int64, device=device)
+    cnt = torch.empty(1, dtype=torch.int32, device=device)
+    ws = _workspace(_size_out(lib.pfa_chunk_topk_workspace_size, n, limit), device)
+    _hip.check(lib.pfa_chunk_topk(_hip.ptr(sc), _hip.ptr(mk), n, limit, float(top_p), int(index_offset),
+                                  1 if drop_nonfinite else 0, _hip.ptr(vals), _hip.ptr(idx), _hip.ptr(cnt),
+                                  _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device)), "pfa_chunk_topk")
+    c = int(cnt.item())
+    if c == 0:
         return None
-    safe = torch.where(finite, scores, torch.full_like(scores, -1e9))
-    order = _order_desc(safe)
-    if top_p >= 1.0:
-        keep = limit
-    else:
-        probs = torch.softmax(safe, dim=-1)[order]
-        mass = torch.cumsum(probs, dim=-1)
-        keep = int((mass < float(top_p)).sum())
-        if keep < order.numel():
-            keep += 1
-        keep = min(limit, max(1, keep))
-    sel = order[:keep]
-    return scores[sel], sel
+    return vals[:c], idx[:c]
 
 
 def finalise(scores: torch.Tensor, indices: torch.Tensor, max_tokens: int) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -65,17 +71,22 @@ def finalise(scores: torch.Tensor, indices: torch.Tensor, max_tokens: int) -> Tu
     group (chunked_shortlist.py:233-243), which is the latest one.  Chunks
     are disjoint, so in the pipeline itself positions never repeat."""
 
-    order = _order_desc(scores.to(torch.float32))
-    s_ord = scores[order]
-    i_ord = indices[order].to(torch.long)
-    n = i_ord.numel()
-    pos = torch.arange(n, device=i_ord.device, dtype=torch.long)
-    by_idx = torch.sort(i_ord * (n + 1) - pos).indices
-    sorted_idx = i_ord[by_idx]
-    first = torch.ones_like(sorted_idx, dtype=torch.bool)
-    first[1:] = sorted_idx[1:] != sorted_idx[:-1]
-    firsts = torch.sort(by_idx[first]).values[:max_tokens]
-    sel_i = i_ord[firsts]
-    sel_s = s_ord[firsts]
-    back = torch.sort(sel_i).indices
-    return sel_i[back], sel_s[back]
+    if scores.ndim != 1 or indices.ndim != 1 or scores.numel() != indices.numel():
+        raise ValueError("scores and indices must be 1-D tensors of equal length")
+    device = _hip.require_device(scores, indices, what="finalise")
+    n = int(scores.numel())
+    if n == 0:
+        raise RuntimeError("No candidate tokens captured during chunking.")
+    sc = scores.to(torch.float32).contiguous()
+    ix = indices.to(torch.int64).contiguous()
+    m = max(0, min(int(max_tokens), n))
+    lib = _hip.lib()
+    keep_i = torch.empty(max(m, 1), dtype=torch.int64, device=device)
+    keep_s = torch.empty(max(m, 1), dtype=torch.float32, device=device)
+    cnt = torch.empty(1, dtype=torch.int32, device=device)
+    ws = _workspace(_size_out(lib.pfa_shortlist_finalise_workspace_size, n), device)
+    _hip.check(lib.pfa_shortlist_finalise(_hip.ptr(sc), _hip.ptr(ix), n, m, _hip.ptr(keep_i), _hip.ptr(keep_s),
+                                          _hip.ptr(cnt), _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device)),
+               "pfa_shortlist_finalise")
+    c = int(cnt.item())
+    return keep_i[:c], keep_s[:c]

@@ -26,9 +26,10 @@ from typing import Any, Dict, Iterable, List, Literal, Optional, Sequence, Tuple
 import numpy as np
 import torch
 
-from ..kernels.sparse_attn import get_last_backend_info
+from ..kernels.sparse_attn import _record_backend, get_last_backend_info
 from ..models.aspa import AdaptiveSparseAttention, ModelConfig
 from . import chunk_select
+from .final_pass import AllQueryFinalPass
 
 LOGGER = logging.getLogger(__name__)
 
@@ -93,15 +94,11 @@ def _select_top_tokens(model: AdaptiveSparseAttention, global_offset: int, *, pe
         return None
     scores = importance.squeeze(0).to(torch.float32)
     mask = getattr(model, "_last_token_mask", None)
-    sel = chunk_select.nucleus_select(scores, per_chunk_budget, nucleus_top_p,
-                                      keep_mask=mask.squeeze(0) if mask is not None else None)
-    if sel is None:
-        return None
-    values, indices = sel
-    finite = torch.isfinite(values)
-    if not bool(finite.any()):
-        return None
-    return values[finite], indices[finite] + int(global_offset)
+    # masking, nucleus selection and the finite filter run in one kernel
+    # (pfa_chunk_topk); None when nothing finite is selected
+    return chunk_select.nucleus_select(scores, per_chunk_budget, nucleus_top_p,
+                                       keep_mask=mask.squeeze(0) if mask is not None else None,
+                                       index_offset=int(global_offset), drop_nonfinite=True)
 
 
 def _nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float):
@@ -189,6 +186,12 @@ class ChunkedShortlistConfig:
     storage: Literal["cpu", "disk", "auto"] = "auto"
     temp_dir: Optional[Path] = None
     ram_limit_bytes: Optional[int] = None
+    # "reduced": the reference's final pass (final model over the reduced
+    # sequence).  "all_queries": every token of the sequence attends to the
+    # int8 (per head and row) shortlist, causal by original position when
+    # final_causal (tools/final_pass.py).
+    final_mode: Literal["reduced", "all_queries"] = "reduced"
+    final_causal: bool = True
 
     def validate(self) -> None:
         """Reference chunked_shortlist.py:337-366."""
@@ -217,6 +220,8 @@ class ChunkedShortlistConfig:
             raise ValueError("storage must be 'cpu', 'disk', or 'auto'.")
         if self.ram_limit_bytes is not None and self.ram_limit_bytes <= 0:
             raise ValueError("ram_limit_bytes must be positive when provided.")
+        if self.final_mode not in {"reduced", "all_queries"}:
+            raise ValueError("final_mode must be 'reduced' or 'all_queries'.")
 
 
 class ChunkedShortlistRunner:
@@ -226,6 +231,17 @@ class ChunkedShortlistRunner:
         self.config = config
         self.config.validate()
         self.logger = logger or LOGGER
+
+    def _final_model(self, seq_len: int, dtype: torch.dtype) -> AdaptiveSparseAttention:
+        """Final-pass model recipe (reference chunked_shortlist.py:712-727)."""
+        cfg = self.config
+        model = AdaptiveSparseAttention(_build_model_config(
+            seq_len, cfg.d_model, heads=cfg.heads, sparse_ratio=cfg.final_sparse_ratio,
+            shortlist_alpha=cfg.shortlist_alpha, router_top_p=cfg.nucleus_top_p)).to(
+                device=cfg.device, dtype=dtype).eval()
+        model.use_sdpa = False
+        model.set_shortlist_alpha(float(cfg.shortlist_alpha))
+        return model
 
     def _stage(self, sequence: Optional[torch.Tensor]):
         """Host staging (reference chunked_shortlist.py:417-560)."""
@@ -241,6 +257,17 @@ class ChunkedShortlistRunner:
                 raise ValueError("Chunked Shortlist runner currently expects batch size of 1.")
             source = sequence[:, :cfg.seq_len].detach()
             base_dtype = source.dtype
+            if source.device.type == "cuda":
+                # already resident in HBM: chunks are views, the shortlist a
+                # device gather (no host staging, no copies)
+                if source.device != cfg.device:
+                    raise ValueError(f"sequence on {source.device} but the runner targets {cfg.device}")
+                src = source.contiguous()
+                size = int(src.numel() * src.element_size())
+                return {"mode": "device", "reason": "sequence resident in device memory", "required": size,
+                        "limit": None, "dtype": base_dtype, "memmap": None, "path": None, "pinned": False,
+                        "allocated": 0, "dataset": size, "fetch": lambda s, e: src[:, s:e],
+                        "gather": lambda idx: src.index_select(1, idx.to(device=src.device, dtype=torch.long))}
         else:
             source = None
             base_dtype = torch.get_default_dtype()
@@ -318,7 +345,15 @@ class ChunkedShortlistRunner:
                                                                                          dtype=base_dtype).eval()
             chunk_model.use_sdpa = False
             chunk_model.set_shortlist_alpha(float(cfg.shortlist_alpha))
-            chunk_buf = torch.empty(1, cfg.chunk_len, cfg.d_model, device=device, dtype=base_dtype)
+            direct = st["mode"] == "device"
+            chunk_buf = None if direct else torch.empty(1, cfg.chunk_len, cfg.d_model, device=device,
+                                                        dtype=base_dtype)
+            final_model = None
+            all_q = None
+            if cfg.run_final_pass and cfg.final_mode == "all_queries":
+                final_model = self._final_model(cfg.buffer_tokens, base_dtype)
+                all_q = AllQueryFinalPass(final_model, cfg.seq_len, device, base_dtype, causal=cfg.final_causal)
+            self.last_final_pass = all_q
             with torch.inference_mode():
                 chunk_model(torch.randn(1, cfg.chunk_len, cfg.d_model, device=device, dtype=base_dtype))
             if device.type == "cuda":
@@ -335,15 +370,21 @@ class ChunkedShortlistRunner:
             t_chunks = t_start
             for ci, (s, e) in enumerate(_chunk_iter(cfg.seq_len, cfg.chunk_len)):
                 n = e - s
-                chunk_buf[:, :n].copy_(st["fetch"](s, e), non_blocking=st["pinned"])
-                if n < cfg.chunk_len:
-                    chunk_buf[:, n:].zero_()
+                if direct:
+                    xc = st["fetch"](s, e)
+                else:
+                    chunk_buf[:, :n].copy_(st["fetch"](s, e), non_blocking=st["pinned"])
+                    if n < cfg.chunk_len:
+                        chunk_buf[:, n:].zero_()
+                    xc = chunk_buf[:, :n]
                 with torch.inference_mode():
-                    chunk_model(chunk_buf[:, :n])
+                    chunk_model(xc)
+                    if all_q is not None:
+                        all_q.add_chunk(xc, s)
                 promoted = _select_top_tokens(chunk_model, s, per_chunk_budget=cfg.per_chunk_budget,
                                               nucleus_top_p=cfg.nucleus_top_p)
                 if promoted is None:
-                    sel = _nucleus_select(chunk_buf[0, :n].detach().norm(dim=-1).to(torch.float32),
+                    sel = _nucleus_select(xc[0].detach().norm(dim=-1).to(torch.float32),
                                           cfg.per_chunk_budget, cfg.nucleus_top_p)
                     if sel is None:
                         continue
@@ -376,12 +417,8 @@ class ChunkedShortlistRunner:
             t_final_end = t_chunks
             if cfg.run_final_pass:
                 t_f0 = time.perf_counter()
-                final_model = AdaptiveSparseAttention(_build_model_config(
-                    reduced.size(1), cfg.d_model, heads=cfg.heads, sparse_ratio=cfg.final_sparse_ratio,
-                    shortlist_alpha=cfg.shortlist_alpha, router_top_p=cfg.nucleus_top_p)).to(
-                        device=device, dtype=base_dtype).eval()
-                final_model.use_sdpa = False
-                final_model.set_shortlist_alpha(float(cfg.shortlist_alpha))
+                if final_model is None:
+                    final_model = self._final_model(reduced.size(1), base_dtype)
                 ev_f0 = ev_f1 = None
                 if device.type == "cuda":
                     torch.cuda.reset_peak_memory_stats(device)
@@ -389,7 +426,13 @@ class ChunkedShortlistRunner:
                         ev_f0, ev_f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                         ev_f0.record()
                 with torch.inference_mode():
-                    final_out = final_model(reduced).detach()
+                    if all_q is not None:
+                        final_out = all_q.finish(reduced, keep_idx).detach()
+                        _record_backend("hip_int8_all_queries", device=str(device), tokens=cfg.seq_len,
+                                        shortlist=int(keep_idx.numel()), causal=bool(cfg.final_causal),
+                                        quantized=True)
+                    else:
+                        final_out = final_model(reduced).detach()
                 t_final_end = time.perf_counter()
                 backend_info = get_last_backend_info()
                 raw = getattr(final_model, "last_head_stats", {}) or {}
@@ -408,7 +451,8 @@ class ChunkedShortlistRunner:
                 if final_ms is None:
                     final_ms = float((t_final_end - t_f0) * 1000.0)
                 if final_ms and final_ms > 0:
-                    final_tps = float(keep_idx.numel() * 1000.0 / final_ms)
+                    final_tok = cfg.seq_len if all_q is not None else keep_idx.numel()
+                    final_tps = float(final_tok * 1000.0 / final_ms)
             total = t_final_end - t_start
             metrics = ChunkedShortlistMetrics(
                 original_tokens=cfg.seq_len, retained_tokens=int(keep_idx.numel()),

@@ -1,0 +1,168 @@
+"""GPU parity of the chunked shortlist pipeline's device stages: chunk
+salience top-k, global shortlist merge, per-row int8 quantisation, RoPE on
+rows and the all-query int8 attention, each against the CPU oracle (and the
+reference's golden vectors where they exist)."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import aspa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _same(got, ref):
+    if ref is None:
+        return got is None
+    assert got is not None
+    return torch.equal(got[0].cpu(), ref[0]) and torch.equal(got[1].cpu(), ref[1])
+
+
+def test_chunk_topk_golden(dev, golden):
+    from proteus_attention.tools import chunk_select
+
+    z = golden("chunk_select")
+    s = torch.from_numpy(z["scores"]).to(dev)
+    v, i = chunk_select.nucleus_select(s, 512, 1.0)
+    assert np.array_equal(i.cpu().numpy(), z["i_p1"]) and np.array_equal(v.cpu().numpy(), z["v_p1"])
+    v, i = chunk_select.nucleus_select(s * 4.0, 512, 0.9)
+    assert np.array_equal(i.cpu().numpy(), z["i_p09"]) and np.array_equal(v.cpu().numpy(), z["v_p09"])
+
+
+@pytest.mark.parametrize("n,budget,top_p,ties,masked", [
+    (4096, 512, 1.0, False, True), (65536, 512, 1.0, False, True), (65536, 512, 1.0, True, True),
+    (1000, 5000, 1.0, True, False), (70000, 9000, 1.0, True, True), (3000, 700, 0.5, False, True),
+    (1, 1, 1.0, False, False), (257, 3, 0.999, True, True)])
+def test_chunk_topk_vs_oracle(dev, n, budget, top_p, ties, masked):
+    from proteus_attention.tools import chunk_select
+
+    g = torch.Generator().manual_seed(n + budget)
+    s = torch.randint(-20, 20, (n,), generator=g).float() if ties else torch.randn(n, generator=g)
+    s[torch.rand(n, generator=g) < 0.05] = float("-inf")
+    mask = (torch.rand(n, generator=g) < 0.7) if masked else None
+    print(f"chunk_topk n={n} budget={budget} top_p={top_p}", flush=True)
+    for drop in (False, True):
+        got = chunk_select.nucleus_select(s.to(dev), budget, top_p, keep_mask=None if mask is None else mask.to(dev),
+                                          index_offset=12345, drop_nonfinite=drop)
+        ref = O.nucleus_select(s, budget, top_p, keep_mask=mask, index_offset=12345, drop_nonfinite=drop)
+        assert _same(got, ref)
+
+
+def test_chunk_topk_all_masked_is_none(dev):
+    from proteus_attention.tools import chunk_select
+
+    s = torch.randn(300, device=dev)
+    assert chunk_select.nucleus_select(s, 10, 1.0, keep_mask=torch.zeros(300, dtype=torch.bool, device=dev)) is None
+    assert chunk_select.nucleus_select(torch.full((50,), float("-inf"), device=dev), 10, 1.0) is None
+
+
+def test_finalise_golden(dev, golden):
+    from proteus_attention.tools import chunk_select
+
+    z = golden("chunk_select")
+    ki, ks = chunk_select.finalise(torch.from_numpy(z["all_scores"]).to(dev), torch.from_numpy(z["all_idx"]).to(dev),
+                                   4096)
+    assert np.array_equal(ki.cpu().numpy(), z["keep_idx"]) and np.array_equal(ks.cpu().numpy(), z["keep_scores"])
+
+
+@pytest.mark.parametrize("n,span,m", [(8192, 60000, 8192), (20000, 3000, 1500), (5, 3, 10), (40000, 10 ** 6, 8192)])
+def test_finalise_vs_oracle(dev, n, span, m):
+    from proteus_attention.tools import chunk_select
+
+    g = torch.Generator().manual_seed(n)
+    sc = torch.randint(-50, 50, (n,), generator=g).float() / 7.0
+    idx = torch.randint(0, span, (n,), generator=g)
+    print(f"finalise n={n} span={span} m={m}", flush=True)
+    ki, ks = chunk_select.finalise(sc.to(dev), idx.to(dev), m)
+    ri, rs = O.finalise_indices(sc, idx, m)
+    assert torch.equal(ki.cpu(), ri) and torch.equal(ks.cpu(), rs)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_quantize_rows_bitwise(dev, dt):
+    from proteus_attention.tools.final_pass import quantize_rows_int8
+
+    g = torch.Generator().manual_seed(3)
+    S, H, D = 777, 8, 64
+    full = (torch.randn(S, 2 * H * D, generator=g) * torch.rand(S, 1, generator=g) * 4).to(dt)
+    full[5, : H * D] = 0
+    x = full[:, : H * D]  # row stride 2*H*D, as the K half of a (S, 2C) projection
+    q, s = quantize_rows_int8(x.to(dev), H)
+    rq, rs = O.quantize_rows_int8(x.float(), H)
+    assert torch.equal(s.cpu(), rs) and torch.equal(q.cpu(), rq)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_rope_rows_bitwise(dev, dt):
+    from proteus_attention.tools.final_pass import rope_rows_
+
+    g = torch.Generator().manual_seed(4)
+    T, H, D, n = 5000, 4, 64, 300
+    cos, sin = O.rope_tables(T, D, 10000.0, dt)
+    x = torch.randn(n, 2 * H * D, generator=g).to(dt)
+    pos = torch.randint(0, T, (n,), generator=g)
+    xd = x.to(dev)
+    rope_rows_(xd[:, : H * D], H, cos.to(dev), sin.to(dev), positions=pos.to(dev))
+    ref = O.apply_rope(x[:, : H * D].reshape(1, n, H, D), cos[pos], sin[pos]).reshape(n, H * D)
+    assert torch.equal(xd[:, : H * D].cpu(), ref)
+    assert torch.equal(xd[:, H * D:].cpu(), x[:, H * D:])
+    # contiguous slice with an offset: rows start..start+n-1
+    y = torch.randn(n, H * D, generator=g).to(dt)
+    yd = y.to(dev)
+    rope_rows_(yd, H, cos.to(dev), sin.to(dev), offset=1234)
+    refy = O.apply_rope(y.view(1, n, H, D), cos[1234:1234 + n], sin[1234:1234 + n]).view(n, H * D)
+    assert torch.equal(yd.cpu(), refy)
+
+
+@pytest.mark.parametrize("T,H,S,causal,first", [(1000, 3, 77, True, 0), (4096, 8, 512, True, 300),
+                                                (3000, 2, 130, False, 0), (700, 1, 1, True, 10),
+                                                (513, 2, 513, True, 0)])
+def test_int8_attention_vs_oracle(dev, T, H, S, causal, first):
+    from proteus_attention.tools.final_pass import int8_shortlist_attention, quantize_rows_int8
+
+    g = torch.Generator().manual_seed(T + S)
+    D = 64
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(S, H * D, generator=g).to(torch.bfloat16)
+    v = torch.randn(S, H * D, generator=g).to(torch.bfloat16)
+    pos = torch.sort(torch.randperm(T - first, generator=g)[:S] + first).values
+    print(f"int8 attention T={T} H={H} S={S} causal={causal}", flush=True)
+    k8, ks = quantize_rows_int8(k.to(dev), H)
+    v8, vs = quantize_rows_int8(v.to(dev), H)
+    out = int8_shortlist_attention(q.to(dev), k8, v8, ks, vs, pos.to(dev), causal=causal)
+    ref = O.int8_kv_attention(q, k8.cpu(), v8.cpu(), ks.cpu(), vs.cpu(), pos, causal=causal)
+    err = float((out.float().cpu() - ref).abs().max())
+    assert err <= 2e-2, err
+    if causal and first > 0:
+        assert float(out[:first].float().abs().max()) == 0.0
+
+
+def test_chunked_runner_all_queries_gpu(dev):
+    from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
+
+    g = torch.Generator().manual_seed(21)
+    T, C = 8192, 512
+    x = torch.randn(1, T, C, generator=g).to(torch.bfloat16).to(dev)
+    cfg = ChunkedShortlistConfig(seq_len=T, d_model=C, chunk_len=2048, buffer_tokens=512, per_chunk_budget=128,
+                                 device=dev, heads=8, nucleus_top_p=1.0, final_mode="all_queries")
+    runner = ChunkedShortlistRunner(cfg)
+    res = runner.run(x)
+    k = res.keep_indices
+    # each chunk promotes min(budget, its token-kept count) tokens (the chunk
+    # model keeps ~5% of 2048 tokens); the buffer holds them all
+    promoted = sum(len(ch.promoted) for ch in res.chunks)
+    assert all(1 <= len(ch.promoted) <= 128 for ch in res.chunks)
+    assert k.numel() == min(512, promoted) and bool(torch.all(k[1:] > k[:-1]))
+    assert res.final_output.shape == (1, T, C) and bool(torch.isfinite(res.final_output.float()).all())
+    assert torch.equal(res.reduced_sequence.cpu(), x[:, k.to(dev)].cpu())
+    fp = runner.last_final_pass
+    k8, ks, v8, vs, pos = fp.last_shortlist
+    ref = O.int8_kv_attention(fp.q_all[0].view(T, 8, 64).cpu(), k8.cpu(), v8.cpu(), ks.cpu(), vs.cpu(), pos.cpu())
+    err = float((fp.last_attn.float().cpu() - ref).abs().max())
+    assert err <= 2e-2, err
+    for ch in res.chunks:
+        assert all(ch.start <= p < ch.end for p in ch.promoted)

@@ -249,3 +249,95 @@ def test_router_oracle_matches_reference(golden, name, B, T, C, dt, outlier):
     assert torch.allclose(gate, torch.from_numpy(z["gate_probs"]), atol=1e-6, rtol=0)
     assert torch.allclose(imp, torch.from_numpy(z["importance"]), atol=1e-6, rtol=0)
     assert torch.allclose(sim, torch.from_numpy(z["sim"]), atol=1e-6, rtol=0)
+
+
+# ---------------------------------------------------------------------------
+# chunked shortlist selection and the all-query int8 final pass
+# ---------------------------------------------------------------------------
+
+def test_chunk_selection_oracle_matches_reference(golden):
+    z = golden("chunk_select")
+    s = torch.from_numpy(z["scores"])
+    v, i = O.nucleus_select(s, 512, 1.0)
+    assert np.array_equal(i.numpy(), z["i_p1"]) and np.array_equal(v.numpy(), z["v_p1"])
+    v, i = O.nucleus_select(s * 4.0, 512, 0.9)
+    assert np.array_equal(i.numpy(), z["i_p09"]) and np.array_equal(v.numpy(), z["v_p09"])
+    ki, ks = O.finalise_indices(torch.from_numpy(z["all_scores"]), torch.from_numpy(z["all_idx"]), 4096)
+    assert np.array_equal(ki.numpy(), z["keep_idx"]) and np.array_equal(ks.numpy(), z["keep_scores"])
+
+
+def test_chunk_selection_oracle_brute_force_ties():
+    g = torch.Generator().manual_seed(5)
+    for trial in range(20):
+        n = int(torch.randint(1, 60, (1,), generator=g))
+        s = torch.randint(-3, 4, (n,), generator=g).float()
+        s[torch.rand(n, generator=g) < 0.15] = float("-inf")
+        mask = torch.rand(n, generator=g) < 0.8
+        budget = int(torch.randint(1, 70, (1,), generator=g))
+        got = O.nucleus_select(s, budget, 1.0, keep_mask=mask, index_offset=100, drop_nonfinite=True)
+        ms = torch.where(mask, s, torch.full_like(s, float("-inf")))
+        safe = [(v if math.isfinite(v) else -1e9) for v in ms.tolist()]
+        order = sorted(range(n), key=lambda j: (-safe[j], j))[:min(budget, n)]
+        keep = [j for j in order if math.isfinite(ms[j].item())]
+        if not keep:
+            assert got is None
+            continue
+        assert got[1].tolist() == [j + 100 for j in keep]
+        assert got[0].tolist() == [ms[j].item() for j in keep]
+        # finalise: one survivor per index (its last entry in score order)
+        idx = torch.randint(0, 15, (n,), generator=g)
+        sc = torch.randint(-2, 3, (n,), generator=g).float()
+        m = int(torch.randint(0, 20, (1,), generator=g))
+        ki, ks = O.finalise_indices(sc, idx, m)
+        order = sorted(range(n), key=lambda j: (-sc[j].item(), j))
+        last = {}
+        for rank, j in enumerate(order):
+            last[idx[j].item()] = rank
+        chosen = sorted(last.items(), key=lambda kv: kv[1])[:m]
+        expect = sorted((ix, sc[order[r]].item()) for ix, r in chosen)
+        assert ki.tolist() == [e[0] for e in expect] and ks.tolist() == [e[1] for e in expect]
+
+
+def test_quantize_rows_int8_invariants():
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(37, 4 * 16, generator=g) * torch.rand(37, 1, generator=g) * 5
+    x[3] = 0.0
+    q, s = O.quantize_rows_int8(x, 4)
+    xr = x.view(37, 4, 16).permute(1, 0, 2)
+    amax = xr.abs().amax(-1)
+    assert torch.equal(s, torch.clamp(amax / 127.0, min=1e-6))
+    # the absmax element maps to +-127, every element within half a step
+    assert bool((q.abs().amax(-1)[amax > 0] == 127).all())
+    assert float((q.float() * s.unsqueeze(-1) - xr).abs().max()) <= float(s.max()) * 0.5 + 1e-7
+    assert int(q[:, 3].abs().max()) == 0
+
+
+def test_int8_kv_attention_oracle_matches_sdpa_and_brute_force():
+    g = torch.Generator().manual_seed(11)
+    T, H, D, S = 40, 2, 8, 9
+    q = torch.randn(T, H, D, generator=g)
+    k8 = torch.randint(-127, 128, (H, S, D), generator=g).to(torch.int8)
+    v8 = torch.randint(-127, 128, (H, S, D), generator=g).to(torch.int8)
+    ks = torch.rand(H, S, generator=g) * 0.02
+    vs = torch.rand(H, S, generator=g) * 0.02
+    pos = torch.sort(torch.randperm(T, generator=g)[:S]).values
+    pos[0] = 5  # queries 0..4 see no key
+    pos = torch.sort(pos).values
+    out = O.int8_kv_attention(q, k8, v8, ks, vs, pos, causal=True)
+    k = k8.float() * ks.unsqueeze(-1)
+    v = v8.float() * vs.unsqueeze(-1)
+    vis = pos.view(1, -1) <= torch.arange(T).view(-1, 1)
+    ref = F.scaled_dot_product_attention(q.permute(1, 0, 2), k, v, attn_mask=vis)
+    rows = vis.any(-1)
+    assert torch.allclose(out.permute(1, 0, 2)[:, rows], ref[:, rows], atol=1e-6)
+    assert float(out[~rows].abs().max()) == 0.0
+    # brute force one query per head, including the last (sees every key)
+    for h in range(H):
+        for t in (7, T - 1):
+            sc = [(q[t, h] @ k[h, j]).item() / math.sqrt(D) for j in range(S) if pos[j] <= t]
+            w = torch.softmax(torch.tensor(sc), 0)
+            vv = v[h][pos <= t]
+            assert torch.allclose(out[t, h], (w.unsqueeze(-1) * vv).sum(0), atol=1e-6)
+    # non-causal: every key visible
+    nc = O.int8_kv_attention(q, k8, v8, ks, vs, pos, causal=False)
+    assert torch.allclose(nc.permute(1, 0, 2), F.scaled_dot_product_attention(q.permute(1, 0, 2), k, v), atol=1e-6)
