@@ -4,6 +4,7 @@
 dominant kernel and the CPU oracle pipeline timed on the host beside it.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+                    [--workload cfg3|cfg4|cfg5]
 
 Prints exactly one JSON line on stdout.  A "step" is one module forward of
 config 3 (router, head top-k, packing, QKV projection + RoPE, prototype
@@ -12,6 +13,11 @@ synthetic batch already resident in HBM.  The timed steps run the module's
 HIP-graph mode (every launch of the forward replayed from one captured
 graph); per-kernel durations come from the same number of eager forwards
 timed with HIP events, whose ms/step is reported as eager_ms_per_step.
+
+--workload cfg4 times the same forward at T=524,288 with L=4096 (single
+pass, no chunking); --workload cfg5 times one run of the chunked shortlist
+pipeline at T=1,048,576 (16 chunks of 65,536, top-512 per chunk, 8,192-token
+int8 shortlist, all-query final pass).  Neither is the headline line.
 """
 from __future__ import annotations
 
@@ -32,6 +38,8 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 CFG3 = dict(B=1, T=65536, C=512, H=8, L=2048, window=512, stride=256, outlier=0.01)
+CFG4 = dict(B=1, T=524288, C=512, H=8, L=4096, window=512, stride=256, outlier=0.0)
+CFG5 = dict(T=1 << 20, C=512, H=8, chunk=65536, budget=512, buffer=8192)
 
 
 def recorded_traffic() -> dict:
@@ -52,13 +60,12 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_module(dev, dtype):
+def build_module(dev, dtype, c):
     import torch
     from configs import init_weights, make_inputs, shortlist_cfg
 
     from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
 
-    c = CFG3
     torch.manual_seed(1234)
     m = AdaptiveSparseAttention(ModelConfig(**shortlist_cfg(c["T"], c["C"], c["H"], c["L"], c["window"], c["stride"])))
     x, g = make_inputs(c["B"], c["T"], c["C"], seed=0, outlier_frac=c["outlier"])
@@ -70,18 +77,30 @@ def build_module(dev, dtype):
     return m, x, weights_cpu
 
 
-def cpu_baseline(x, weights, dtype) -> dict:
+def shortlist_caps(m, c):
+    """(local window, anchor slots, prototype K) of the module's candidate
+    sets at this length (the caps of aspa.py:1075-1137)."""
+    from proteus_attention.kernels import sparse_attn as sa
+
+    rt = m._prepare_linear_runtime(c["T"], c["B"], 1.0)
+    L = int(rt["effective_L"])
+    local_w, slots, pcap = sa._resolve_caps(L, rt["window"], int(rt["anchor_stride"]), True, True, True, c["T"],
+                                            rt["local_cap"], rt["anchor_cap"], rt["proto_cap"])
+    return L, local_w, int(rt["anchor_stride"]), slots, min(L, pcap, c["T"])
+
+
+def cpu_baseline(x, weights, dtype, c, caps) -> dict:
     import torch
 
     from oracle import cpu_pipeline
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    c = CFG3
+    L, local_w, stride, slots, K = caps
     xs = x.to(dtype)
     t0 = time.perf_counter()
-    t = cpu_pipeline.shortlist_forward_seconds(xs, weights, H=c["H"], L=c["L"], local_w=c["window"],
-                                               stride=c["stride"], slots=614, K=205, sample_every=8)
+    t = cpu_pipeline.shortlist_forward_seconds(xs, weights, H=c["H"], L=L, local_w=local_w, stride=stride,
+                                               slots=slots, K=K, sample_every=8)
     wall = time.perf_counter() - t0
     tokens = c["B"] * c["T"]
     return {
@@ -97,41 +116,35 @@ def cpu_baseline(x, weights, dtype) -> dict:
     }
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--eager", action="store_true", help="time the forward without HIP graph replay")
-    ap.add_argument("--copy-probe-mib", type=int, default=0,
-                    help="only run a plain device copy of this many MiB (5 times) and exit: the "
-                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: the ASPA path shards by (batch, head) with no exchange, "
-              f"and this build runs and reports the single-GPU shard only (got --gpus {args.gpus}).",
-              file=sys.stderr)
-        return 2
+def kernel_table(per_stage: dict, alg: dict, traffic: dict) -> dict:
+    kernels = {}
+    for name, ms in per_stage.items():
+        if name in alg:
+            bound, work, peak, unit, scale = alg[name]
+            ach = work / (ms * 1e-3) / scale
+            kernels[name] = {"ms": round(ms, 4), "bound": bound, "achieved": round(ach, 3), "peak": peak,
+                             "unit": unit, "frac": round(ach / peak, 5), "traffic": traffic.get(name)}
+        else:
+            kernels[name] = {"ms": round(ms, 4)}
+    return kernels
 
+
+def bench_forward(args, workload: str) -> dict:
+    """Configs 3 and 4: the module forward (graph replay timed, eager
+    forwards for per-kernel events)."""
     import torch
 
     from proteus_attention import _hip
+    from proteus_attention.kernels import sparse_attn as sa
 
+    c = CFG3 if workload == "cfg3" else CFG4
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16
-    if args.copy_probe_mib > 0:
-        n = args.copy_probe_mib << 20
-        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
-        return 0
-    log("building config-3 module")
-    m, x_cpu, weights = build_module(dev, dtype)
+    log(f"building {workload} module (T={c['T']})")
+    m, x_cpu, weights = build_module(dev, dtype, c)
     x = x_cpu.to(dtype).to(dev)
+    caps = shortlist_caps(m, c)
+    L, local_w, stride, slots, K = caps
     snap = {n: b.detach().clone() for n, b in m.named_buffers() if n.startswith("routing_")}
 
     def restore():
@@ -178,7 +191,6 @@ def main() -> int:
     stages = _hip.TIMER.summary_ms()
     log(f"timed {args.steps} steps in {elapsed:.3f}s (host ms inside each forward call: "
         f"{' '.join(f'{1e3 * h:.2f}' for h in host)}); eager forward {eager_ms:.3f} ms/step")
-    c = CFG3
     tokens = c["B"] * c["T"]
     value = tokens * args.steps / elapsed
     ms_step = elapsed * 1000.0 / args.steps
@@ -194,50 +206,41 @@ def main() -> int:
     # the candidate builder of the operator API (build_packed_shortlist_
     # candidates) on the same rows, timed on its own: the module path does
     # not materialise candidates
-    from proteus_attention.kernels import sparse_attn as sa
-
     with torch.no_grad():
         st = m._last_sparse_state
         rows = st["token_idx"]
-        sets = sa._proto_prefix_sets(m._last_token_similarity, 205)
+        sets = sa._proto_prefix_sets(m._last_token_similarity, K)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        sa._shortlist_build_device(rows, None, c["T"], c["L"], c["window"], c["stride"], 614, sets)
+        sa._shortlist_build_device(rows, None, c["T"], L, local_w, stride, slots, sets)
         e0.record()
         reps = 5
         for _ in range(reps):
-            cand, _lens = sa._shortlist_build_device(rows, None, c["T"], c["L"], c["window"], c["stride"], 614, sets)
+            cand, _lens = sa._shortlist_build_device(rows, None, c["T"], L, local_w, stride, slots, sets)
         e1.record()
         torch.cuda.synchronize()
-        per_stage_extra = {"shortlist_build": e0.elapsed_time(e1) / reps}
-        del cand
+        per_stage["shortlist_build"] = e0.elapsed_time(e1) / reps
+        del cand, sets
     alg = {
         "sparse_attn_fwd": ("mfma", 4.0 * sum_len * D, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", 1e12),
         "shortlist_attn_fwd": ("mfma", 4.0 * sum_len * D, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", 1e12),
-        "shortlist_build": ("hbm", N * (4.0 * c["L"] + 12) + tokens * 4.0, HBM_PEAK_GBS, "GB/s", 1e9),
+        "shortlist_build": ("hbm", N * (4.0 * L + 12) + tokens * 4.0, HBM_PEAK_GBS, "GB/s", 1e9),
         "router_topk": ("hbm", tokens * (c["C"] * E + 8 * 2 + 12) + 8 * c["C"] * (E + 4), HBM_PEAK_GBS, "GB/s", 1e9),
-        "proto_prefix_topk": ("hbm", tokens * 205 * 4.0 + tokens * 4.0, HBM_PEAK_GBS, "GB/s", 1e9),
+        "proto_prefix_topk": ("hbm", tokens * K * 4.0 + tokens * 4.0, HBM_PEAK_GBS, "GB/s", 1e9),
     }
-    per_stage.update(per_stage_extra)
-    traffic = recorded_traffic()
-    kernels = {}
-    for name, ms in per_stage.items():
-        if name in alg:
-            bound, work, peak, unit, scale = alg[name]
-            ach = work / (ms * 1e-3) / scale
-            kernels[name] = {"ms": round(ms, 4), "bound": bound, "achieved": round(ach, 3), "peak": peak,
-                             "unit": unit, "frac": round(ach / peak, 5), "traffic": traffic.get(name)}
-        else:
-            kernels[name] = {"ms": round(ms, 4)}
+    traffic = recorded_traffic() if workload == "cfg3" else {}
+    kernels = kernel_table(per_stage, alg, traffic)
     dominant = max((k for k in module_stages if k in alg), key=lambda k: per_stage[k])
     dk = kernels[dominant]
     roofline = {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                 "unit": dk["unit"], "frac": dk["frac"], "traffic": dk["traffic"]}
     cpu = None
-    if not args.no_cpu_baseline:
+    if workload == "cfg3" and not args.no_cpu_baseline:
         log("cpu baseline (oracle pipeline on host cores)")
-        cpu = cpu_baseline(x_cpu, weights, dtype)
-    line = {
-        "metric": "shortlist fwd tokens/s @T=64K bf16 + % of HBM/MFMA roofline, 1 GPU",
+        cpu = cpu_baseline(x_cpu, weights, dtype, c, caps)
+    metric = ("shortlist fwd tokens/s @T=64K bf16 + % of HBM/MFMA roofline, 1 GPU" if workload == "cfg3" else
+              "shortlist fwd tokens/s @T=512K bf16 single pass, 1 GPU")
+    return {
+        "metric": metric,
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -249,15 +252,120 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: x~N(0,1) seed 0 with 1% rows x4, Xavier-normal weights from the same generator",
-        "config": {"workload": "config 3: ASPA shortlist forward, B=1 T=65536 d_model=512 H=8 D=64 L=2048 "
-                               "window=512 anchor_stride=256 policy=local+anchors+proto top-2 heads",
+        "data": (f"synthetic: x~N(0,1) seed 0{' with 1% rows x4' if c['outlier'] else ''}, Xavier-normal weights "
+                 "from the same generator"),
+        "config": {"workload": (f"config {workload[-1]}: ASPA shortlist forward, B=1 T={c['T']} d_model=512 H=8 D=64 "
+                                f"L={L} window={local_w} anchor_stride={stride} policy=local+anchors+proto top-2 "
+                                "heads"),
                    "rows": N, "sum_candidates": sum_len, "global_batch": 1, "seq_len": c["T"],
+                   "peak_mem_gib": round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 2),
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
+
+
+def bench_cfg5(args) -> dict:
+    """Config 5: one run of the chunked shortlist pipeline over a sequence
+    already resident in HBM; the last of warmup + steps runs is reported."""
+    import torch
+
+    from proteus_attention import _hip
+    from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
+
+    c = CFG5
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    log("building config-5 sequence (T=1,048,576)")
+    x = torch.randn(1, c["T"], c["C"], generator=g).to(torch.bfloat16).to(dev)
+    cfg = ChunkedShortlistConfig(seq_len=c["T"], d_model=c["C"], chunk_len=c["chunk"], buffer_tokens=c["buffer"],
+                                 per_chunk_budget=c["budget"], device=dev, heads=c["H"], nucleus_top_p=1.0,
+                                 final_mode="all_queries", report_latency=True)
+    runs = max(1, args.warmup) + max(1, args.steps)
+    walls = []
+    for i in range(runs):
+        last = i == runs - 1
+        _hip.TIMER.reset()
+        _hip.TIMER.enabled = last
+        torch.manual_seed(7)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        runner = ChunkedShortlistRunner(cfg)
+        res = runner.run(x)
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+    _hip.TIMER.enabled = False
+    stages = {k: sum(v) / len(v) for k, v in _hip.TIMER.summary_ms().items()}
+    mt = res.metrics
+    pipe_ms = mt.chunk_time_ms + mt.final_time_ms
+    keep = res.keep_indices.to(torch.int64)
+    D = c["C"] // c["H"]
+    vis = int((c["T"] - keep).sum())  # (query, key) pairs with key position <= query
+    alg = {"int8_kv_attn_fwd": ("mfma", 4.0 * D * c["H"] * vis, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", 1e12),
+           "router_topk": ("hbm", c["chunk"] * (c["C"] * 2 + 8 * c["H"] + 12), HBM_PEAK_GBS, "GB/s", 1e9)}
+    kernels = kernel_table(stages, alg, {})
+    dk = kernels["int8_kv_attn_fwd"]
+    log(f"runs wall ms: {' '.join(f'{1e3 * w:.1f}' for w in walls)}; chunk {mt.chunk_time_ms:.2f} ms, "
+        f"final {mt.final_time_ms:.2f} ms, kept {mt.retained_tokens}")
+    return {
+        "metric": "chunked shortlist pipeline tokens/s @T=1M bf16 (int8 shortlist, all-query final pass), 1 GPU",
+        "value": round(c["T"] / (pipe_ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": 1,
+        "warmup": runs - 1,
+        "ms_per_step": round(pipe_ms, 4),
+        "wall_ms_per_run": round(1e3 * walls[-1], 3),
+        "chunk_ms": round(mt.chunk_time_ms, 4),
+        "final_ms": round(mt.final_time_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: x~N(0,1) seed 0, resident in HBM; random-init chunk and final models",
+        "config": {"workload": "config 5: chunked shortlist, T=1048576 d_model=512 H=8 D=64, chunks of 65536, "
+                               "top-512 per chunk, 8192-token shortlist, int8 per-(head,row) K/V, all-query "
+                               "causal-by-position final pass", "retained": mt.retained_tokens,
+                   "visible_pairs_per_head": vis, "parallelism": "single GPU"},
+        "roofline": {"kernel": "int8_kv_attn_fwd", "bound": dk["bound"], "achieved": dk["achieved"],
+                     "peak": dk["peak"], "unit": dk["unit"], "frac": dk["frac"], "traffic": None},
+        "kernels": kernels,
+        "cpu_baseline": None,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=("cfg3", "cfg4", "cfg5"), default="cfg3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time the forward without HIP graph replay")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (5 times) and exit: the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the ASPA path shards by (batch, head) with no exchange, "
+              f"and this build runs and reports the single-GPU shard only (got --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
+        return 0
+    line = bench_cfg5(args) if args.workload == "cfg5" else bench_forward(args, args.workload)
     print(json.dumps(line), flush=True)
     return 0
 
