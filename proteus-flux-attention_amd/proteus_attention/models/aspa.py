@@ -721,18 +721,48 @@ class AdaptiveSparseAttention(nn.Module):
     # ------------------------------------------------------------------
     # device stages
     # ------------------------------------------------------------------
-    def _proto_inputs(self, device: torch.device):
-        """G-sized prototype tensors the router kernel consumes (aspa.py:636-663)."""
-        if not (self.proto_enabled and self.routing_prototypes is not None):
-            return None, None, None
-        pn = F.normalize(self.routing_prototypes.to(device=device, dtype=torch.float32), dim=-1, eps=1e-6).contiguous()
-        conf = None
-        if self.routing_confidence is not None:
-            conf = (self.routing_confidence.view(-1) + 1e-6).to(torch.float32).contiguous()
-        usage = None
-        if self.proto_usage_boost > 0.0 and self.routing_usage_ema is not None:
-            usage = torch.softmax(-(self.routing_usage_ema + 1e-6), dim=0).to(torch.float32).contiguous()
-        return pn, conf, usage
+    def _router_inputs(self, device: torch.device, x_dtype: torch.dtype):
+        """Router weight table, prototype prior inputs (aspa.py:636-663) in one
+        launch (pfa_router_prepare): (w_packed, conf_weight, usage_bias,
+        use_proto)."""
+        lib = _hip.lib()
+        G, C = self.attn_gates, self.d_model
+        w = self.head_router.linear.weight.detach()
+        if w.device != device:
+            w = w.to(device)
+        w = w.contiguous()
+        use_proto = bool(self.proto_enabled and self.routing_prototypes is not None)
+        protos = conf_b = usage_b = None
+        buf_dtype = w.dtype
+        if use_proto:
+            protos = self.routing_prototypes.detach().contiguous()
+            buf_dtype = protos.dtype
+            if self.routing_confidence is not None:
+                conf_b = self.routing_confidence.detach().view(-1).contiguous()
+            if self.proto_usage_boost > 0.0 and self.routing_usage_ema is not None:
+                usage_b = self.routing_usage_ema.detach().view(-1).contiguous()
+            for t in (conf_b, usage_b):
+                if t is not None and t.dtype != buf_dtype:
+                    raise ValueError("routing_prototypes / routing_confidence / routing_usage_ema must share one dtype")
+        Gp = int(lib.pfa_router_gate_pad(G))
+        wpk = torch.empty(C, 2 * Gp, dtype=torch.float32, device=device)
+        conf = torch.empty(G, dtype=torch.float32, device=device) if conf_b is not None else None
+        usage = torch.empty(G, dtype=torch.float32, device=device) if usage_b is not None else None
+        _hip.check(lib.pfa_router_prepare(_hip.ptr(w), _hip.dtype_tag(w.dtype), _hip.ptr(protos), _hip.ptr(conf_b),
+                                          _hip.ptr(usage_b), _hip.dtype_tag(buf_dtype), G, C, _hip.dtype_tag(x_dtype),
+                                          _hip.ptr(wpk), _hip.ptr(conf), _hip.ptr(usage), _hip.stream_ptr(device)),
+                   "pfa_router_prepare")
+        return wpk, conf, usage, use_proto
+
+    def _gate_to_head_i32(self, device: torch.device) -> torch.Tensor:
+        # int32 copy, rebuilt when the mapping buffer moves or is modified
+        src = self.gate_to_head
+        key = (device, src.data_ptr(), src._version)
+        cached = getattr(self, "_g2h_cache", None)
+        if cached is None or cached[0] != key:
+            cached = (key, src.to(device=device, dtype=torch.int32).contiguous())
+            self._g2h_cache = cached
+        return cached[1]
 
     def _route_device(self, x2d: torch.Tensor, topk: int, need_head_scores: bool = True):
         """Fused router: gate probs, sim, blend, importance, head top-k."""
@@ -740,25 +770,30 @@ class AdaptiveSparseAttention(nn.Module):
         device = x2d.device
         n_tok, C = x2d.shape
         G, H = self.attn_gates, self.h_total
-        pn, conf, usage = self._proto_inputs(device)
-        wpk = pack_router_weights(self.head_router.linear.weight, pn, x2d.dtype)
+        wpk, conf, usage, use_proto = self._router_inputs(device, x2d.dtype)
         gate = torch.empty(n_tok, G, dtype=torch.float32, device=device)
         imp = torch.empty(n_tok, dtype=torch.float32, device=device)
-        sim = torch.empty(n_tok, dtype=torch.float32, device=device) if pn is not None else None
-        blend = torch.empty(n_tok, dtype=torch.float32, device=device) if pn is not None else None
+        sim = torch.empty(n_tok, dtype=torch.float32, device=device) if use_proto else None
+        blend = torch.empty(n_tok, dtype=torch.float32, device=device) if use_proto else None
         hidx = torch.empty(n_tok, topk, dtype=torch.int32, device=device)
         hsc = torch.empty(n_tok, topk, dtype=torch.float32, device=device) if need_head_scores else None
         nblk = _hip.ctypes.c_int(0)
         _hip.check(lib.pfa_router_block_count(n_tok, _hip.ctypes.byref(nblk)), "pfa_router_block_count")
         stats = torch.empty(max(1, nblk.value), 8, dtype=torch.float32, device=device)
-        g2h = self.gate_to_head.to(device=device, dtype=torch.int32).contiguous()
+        # prototype EMA statistics accumulated in the same pass over x
+        # (consumed by _update_routing_prototypes at the end of the forward)
+        ema = None
+        if self._ema_active():
+            ema = torch.empty(max(1, nblk.value), G, C + 1, dtype=torch.float32, device=device)
+        self._ema_partial = (ema, x2d.data_ptr(), n_tok) if ema is not None else None
+        g2h = self._gate_to_head_i32(device)
         with _hip.TIMER.timed("router_topk"):
             rc = lib.pfa_router_topk(
-            _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(wpk), 1 if pn is not None else 0,
+            _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(wpk), 1 if use_proto else 0,
             _hip.ptr(conf),
             _hip.ptr(usage), _hip.ptr(g2h), H, topk, float(self.proto_temp), float(self.proto_threshold),
             float(self.proto_blend), float(self.proto_usage_boost), _hip.ptr(gate), _hip.ptr(sim), _hip.ptr(blend),
-            _hip.ptr(imp), _hip.ptr(hidx), _hip.ptr(hsc), _hip.ptr(stats), _hip.stream_ptr(device))
+            _hip.ptr(imp), _hip.ptr(hidx), _hip.ptr(hsc), _hip.ptr(stats), _hip.ptr(ema), _hip.stream_ptr(device))
         _hip.check(rc, "pfa_router_topk")
         self._router_stats = stats
         return gate, sim, blend, imp, hidx, hsc
@@ -793,10 +828,13 @@ class AdaptiveSparseAttention(nn.Module):
         self._last_token_mask = mask
         return mask
 
+    def _ema_active(self) -> bool:
+        return bool(self.proto_enabled and self.routing_prototypes is not None
+                    and self.routing_usage_ema is not None and self.routing_confidence is not None)
+
     def _update_routing_prototypes(self, token_feats: torch.Tensor, gate_probs: torch.Tensor) -> None:
         """Prototype / usage / confidence EMA (aspa.py:692-718)."""
-        if not (self.proto_enabled and self.routing_prototypes is not None
-                and self.routing_usage_ema is not None and self.routing_confidence is not None):
+        if not self._ema_active():
             return
         with torch.no_grad():
             lib = _hip.lib()
@@ -804,17 +842,25 @@ class AdaptiveSparseAttention(nn.Module):
             if x2d.dtype not in (torch.float32, torch.bfloat16, torch.float16):
                 x2d = x2d.to(torch.float32)
             x2d = x2d.contiguous()
-            probs = gate_probs.detach().to(torch.float32).reshape(-1, self.attn_gates).contiguous()
             device = x2d.device
             n_tok, C, G = x2d.size(0), self.d_model, self.attn_gates
-            nparts = _hip.ctypes.c_int(0)
-            _hip.check(lib.pfa_proto_partial_count(n_tok, _hip.ctypes.byref(nparts)), "pfa_proto_partial_count")
-            partial = torch.empty(nparts.value, G, C + 1, dtype=torch.float32, device=device)
-            _hip.check(lib.pfa_proto_accumulate(_hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G,
-                                                _hip.ptr(probs), _hip.ptr(partial), nparts.value,
-                                                _hip.stream_ptr(device)), "pfa_proto_accumulate")
+            fused = getattr(self, "_ema_partial", None)
+            self._ema_partial = None
+            if fused is not None and fused[1] == x2d.data_ptr() and fused[2] == n_tok:
+                # statistics already accumulated by this forward's router pass
+                partial = fused[0]
+                nparts = partial.size(0)
+            else:
+                probs = gate_probs.detach().to(torch.float32).reshape(-1, self.attn_gates).contiguous()
+                np_c = _hip.ctypes.c_int(0)
+                _hip.check(lib.pfa_proto_partial_count(n_tok, _hip.ctypes.byref(np_c)), "pfa_proto_partial_count")
+                nparts = np_c.value
+                partial = torch.empty(nparts, G, C + 1, dtype=torch.float32, device=device)
+                _hip.check(lib.pfa_proto_accumulate(_hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G,
+                                                    _hip.ptr(probs), _hip.ptr(partial), nparts,
+                                                    _hip.stream_ptr(device)), "pfa_proto_accumulate")
             sums = torch.empty(G, C + 1, dtype=torch.float32, device=device)
-            _hip.check(lib.pfa_proto_partial_reduce(_hip.ptr(partial), nparts.value, G, C, _hip.ptr(sums),
+            _hip.check(lib.pfa_proto_partial_reduce(_hip.ptr(partial), nparts, G, C, _hip.ptr(sums),
                                                     _hip.stream_ptr(device)), "pfa_proto_partial_reduce")
             proto, usage, conf = self.routing_prototypes, self.routing_usage_ema, self.routing_confidence
             if not (proto.dtype == usage.dtype == conf.dtype and proto.is_contiguous()):
@@ -921,6 +967,20 @@ class AdaptiveSparseAttention(nn.Module):
     def reset_hip_graphs(self) -> None:
         self._resolve_stats()
         self._hip_graphs = {}
+
+    def hip_graph_input(self, x: torch.Tensor) -> torch.Tensor:
+        """The static input buffer of the graph that serves inputs shaped like
+        x (capturing it first if needed), filled with x.  A caller that writes
+        its next input into this buffer and passes it to forward() skips the
+        per-call input copy."""
+        if not (self._hip_graph_enabled and self._graph_eligible(x)):
+            raise RuntimeError("hip_graph_input: graph mode is off or not applicable to this input")
+        key = self._graph_key(x)
+        ent = self._hip_graphs.get(key)
+        if ent is None:
+            ent = self._capture_graph(x, key)
+        ent["x"].copy_(x)
+        return ent["x"]
 
     def _graph_eligible(self, x: torch.Tensor) -> bool:
         return (x.dim() == 3 and not self.training and not torch.is_grad_enabled()

@@ -303,7 +303,7 @@ def _run_router(dev, x, w, protos, conf, dt, topk, H, temp=0.2, thr=0.25, blend=
     g2h = O.default_gate_map(G, H).to(torch.int32).to(dev)
     rc = lib.pfa_router_topk(_hip.ptr(xd), _hip.dtype_tag(dt), n, C, G, _hip.ptr(wpk), 1, _hip.ptr(cw),
                              None, _hip.ptr(g2h), H, topk, temp, thr, blend, 0.0, *[_hip.ptr(o) for o in outs],
-                             None, _hip.stream_ptr(dev))
+                             None, None, _hip.stream_ptr(dev))
     _hip.check(rc, "router")
     return [o.cpu() for o in outs]
 
@@ -373,6 +373,87 @@ def test_proto_ema_sums_vs_f64(dev, n_tok, C, G, dt):
     err = float(((got - ref).abs() / scale).max())
     _say(f"max scaled error {err:.2e}")
     assert err < 1e-5
+
+
+@pytest.mark.parametrize("n_tok,C,G,dt", [(300_000, 512, 8, torch.bfloat16), (5000, 1024, 12, torch.float32),
+                                          (37, 64, 3, torch.float16), (1000, 200, 20, torch.bfloat16)])
+def test_router_fused_ema_sums_vs_f64(dev, n_tok, C, G, dt):
+    """The EMA statistics the router accumulates in its own pass over x
+    (ema_partial of pfa_router_topk, reduced with pfa_proto_partial_reduce)
+    against a float64 product of the router's own gate probabilities."""
+    from proteus_attention import _hip
+    from proteus_attention.models.aspa import pack_router_weights
+
+    _say(f"router fused EMA sums n_tok={n_tok} C={C} G={G} {dt}")
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(n_tok, C, generator=g).to(dt)
+    w = (torch.randn(G, C, generator=g) * 0.05).to(dt)
+    protos = torch.randn(G, C, generator=g)
+    lib = _hip.lib()
+    nb = _hip.ctypes.c_int(0)
+    _hip.check(lib.pfa_router_block_count(n_tok, _hip.ctypes.byref(nb)), "count")
+    xd = x.to(dev)
+    pn = torch.nn.functional.normalize(protos, dim=-1, eps=1e-6).to(dev)
+    wpk = pack_router_weights(w.to(dev), pn, dt)
+    H = min(G, 8)
+    g2h = O.default_gate_map(G, H).to(torch.int32).to(dev)
+    gate = torch.empty(n_tok, G, device=dev)
+    imp = torch.empty(n_tok, device=dev)
+    hidx = torch.empty(n_tok, 2, dtype=torch.int32, device=dev)
+    part = torch.empty(nb.value, G, C + 1, device=dev)
+    sums = torch.empty(G, C + 1, device=dev)
+    s = _hip.stream_ptr(dev)
+    _hip.check(lib.pfa_router_topk(_hip.ptr(xd), _hip.dtype_tag(dt), n_tok, C, G, _hip.ptr(wpk), 1, None, None,
+                                   _hip.ptr(g2h), H, 2, 0.2, 0.25, 0.6, 0.0, _hip.ptr(gate), None, None, _hip.ptr(imp),
+                                   _hip.ptr(hidx), None, None, _hip.ptr(part), s), "router")
+    _hip.check(lib.pfa_proto_partial_reduce(_hip.ptr(part), nb.value, G, C, _hip.ptr(sums), s), "reduce")
+    gp = gate.cpu().double()
+    got = sums.cpu().double()
+    ref = torch.cat([gp.t() @ x.double(), gp.sum(0).unsqueeze(1)], dim=1)
+    scale = (gp.t() @ x.double().abs()).clamp_min(1.0)
+    scale = torch.cat([scale, gp.sum(0).unsqueeze(1).clamp_min(1.0)], dim=1)
+    err = float(((got - ref).abs() / scale).max())
+    _say(f"max scaled error {err:.2e}")
+    assert err < 1e-5
+
+
+@pytest.mark.parametrize("wdt,bdt,xdt,boost", [(torch.bfloat16, torch.bfloat16, torch.bfloat16, 0.0),
+                                               (torch.float32, torch.float32, torch.bfloat16, 0.3),
+                                               (torch.float32, torch.bfloat16, torch.float32, 0.5)])
+def test_router_prepare_matches_tensor_ops(dev, wdt, bdt, xdt, boost):
+    """pfa_router_prepare against the tensor ops it replaces, evaluated by
+    torch on the same device: weight table and confidence/usage weights
+    exactly, normalised prototypes to one f32 rounding (norm summation
+    order)."""
+    from proteus_attention import _hip
+    from proteus_attention.models.aspa import pack_router_weights
+
+    g = torch.Generator().manual_seed(8)
+    G, C = 8, 512
+    w = torch.randn(G, C, generator=g).to(wdt).to(dev)
+    protos = (torch.randn(G, C, generator=g) * 0.02).to(bdt).to(dev)
+    conf = torch.rand(G, generator=g).to(bdt).to(dev)
+    usage = (torch.rand(G, generator=g) * 3).to(bdt).to(dev)
+    lib = _hip.lib()
+    Gp = int(lib.pfa_router_gate_pad(G))
+    wpk = torch.empty(C, 2 * Gp, device=dev)
+    cw = torch.empty(G, device=dev)
+    ub = torch.empty(G, device=dev)
+    _hip.check(lib.pfa_router_prepare(_hip.ptr(w), _hip.dtype_tag(wdt), _hip.ptr(protos), _hip.ptr(conf),
+                                      _hip.ptr(usage) if boost > 0 else None, _hip.dtype_tag(bdt), G, C,
+                                      _hip.dtype_tag(xdt), _hip.ptr(wpk), _hip.ptr(cw), _hip.ptr(ub),
+                                      _hip.stream_ptr(dev)), "prepare")
+    pn = torch.nn.functional.normalize(protos.to(torch.float32), dim=-1, eps=1e-6)
+    ref = pack_router_weights(w, pn, xdt)
+    assert torch.equal(wpk[:, :Gp], ref[:, :Gp])
+    assert torch.allclose(wpk[:, Gp:], ref[:, Gp:], rtol=2.5e-7, atol=1e-12)
+    assert torch.equal(cw, (conf + 1e-6).to(torch.float32))
+    if boost > 0:
+        # softmax: exp and normalisation differ from torch's kernel in the
+        # last bits of f32; in bf16 they may straddle a rounding boundary
+        ref_u = torch.softmax(-(usage + 1e-6), dim=0).to(torch.float32)
+        ulp = 2.0 ** -7 if bdt == torch.bfloat16 else 2.0 ** -22
+        assert torch.allclose(ub, ref_u, rtol=ulp, atol=0.0)
 
 
 def test_token_topk_vs_oracle(dev):
