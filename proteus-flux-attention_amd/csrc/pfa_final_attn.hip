@@ -28,6 +28,7 @@ constexpr int kQ = 32 * kWaves;  // queries per workgroup
 constexpr int kTile = 64;        // keys per tile
 constexpr int kLd = 72;          // padded LDS row (bf16 elements)
 constexpr int kD = 64;
+constexpr float kRescaleLog2 = 0.0f;  // rescale only when some row's max rises
 
 struct Args {
   const uint16_t* q;
@@ -117,6 +118,8 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const uint16_t*
       }
     }
   }
+  // lazy rescaling: the accumulators are rescaled only on tiles where some
+  // row of the wave sees a new maximum; m stays the exact running max
 #pragma unroll
   for (int gr = 0; gr < 2; ++gr) {
     float tmax = s[gr][0];
@@ -124,26 +127,25 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const uint16_t*
     for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[gr][i]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mn = fmaxf(st[gr].m, tmax);
-    if (mn == -INFINITY) {
+    const float tm = tmax * sl2;
+    if (__ballot(tm > st[gr].m + kRescaleLog2) != 0) {
+      const float mn = fmaxf(st[gr].m, tm);
+      const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(st[gr].m - mn);  // m == -inf -> 0
+      st[gr].l *= alpha;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[gr][i] = 0.f;
-      continue;
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[gr].acc[db][i] *= alpha;
+      st[gr].m = mn;
     }
-    const float off = mn * sl2;
-    const float alpha = __builtin_amdgcn_exp2f(st[gr].m * sl2 - off);  // m == -inf -> 0
+    const float moff = st[gr].m == -INFINITY ? 0.f : st[gr].m;
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      s[gr][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[gr][i], sl2, -off));  // -inf -> 0
+      s[gr][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[gr][i], sl2, -moff));  // -inf -> 0
       psum += s[gr][i];
     }
-    st[gr].l = st[gr].l * alpha + psum;
-    st[gr].m = mn;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st[gr].acc[db][i] *= alpha;
+    st[gr].l += psum;
   }
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {

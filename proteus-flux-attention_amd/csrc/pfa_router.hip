@@ -103,7 +103,7 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
               float* __restrict__ importance, int32_t* __restrict__ head_idx, float* __restrict__ head_score,
               float* __restrict__ stats, float* __restrict__ ema_part) {
   constexpr int NV = 2 * GP + 1;  // logits, proto dots, sum of squares
-  constexpr int WS = PROTO ? 2 * GP : GP;
+  constexpr int WS = 2 * GP;  // row stride of the packed table (prototype columns unread without PROTO)
   __shared__ float red[(NW > 1) ? (NW - 1) * 64 * NV : 1];
   __shared__ float gl[64 * GP];  // final gate probabilities for the fused EMA statistics
   const int lane = threadIdx.x & 63;
@@ -513,46 +513,60 @@ static int gate_pad(int G) { return G <= 8 ? 8 : G <= 16 ? 16 : G <= 32 ? 32 : 6
 // buffer dtype (aspa.py:636-663).
 constexpr int kPrepThreads = 256;
 
-template <int WDT, int PDT, int XDT>
+template <int WDT, int PDT, int XDT, int GP>
 __global__ void __launch_bounds__(kPrepThreads)
 router_prepare_kernel(const typename Elem<WDT>::T* __restrict__ w, const typename Elem<PDT>::T* __restrict__ protos,
                       const typename Elem<PDT>::T* __restrict__ conf, const typename Elem<PDT>::T* __restrict__ usage,
-                      int G, int C, int GP, float* __restrict__ wpk, float* __restrict__ conf_w,
+                      int G, int C, float* __restrict__ wpk, float* __restrict__ conf_w,
                       float* __restrict__ usage_b) {
-  __shared__ float denom[64];
-  __shared__ float wsum[kPrepThreads / 64];
+  // one pass: each thread owns channels c = tid + k*kPrepThreads; the G
+  // prototype norms are reduced once for all gates, then each thread writes
+  // its channels' 2*GP-float rows
+  __shared__ float wsum[kPrepThreads / 64][GP];
+  __shared__ float denom[GP];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   if (protos != nullptr) {
-    for (int g = 0; g < G; ++g) {
-      float acc = 0.f;
-      for (int c = tid; c < C; c += kPrepThreads) {
-        const float v = load_f<PDT>(protos + (int64_t)g * C + c);
-        acc = __builtin_fmaf(v, v, acc);
-      }
-      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-      if (lane == 0) wsum[wv] = acc;
-      __syncthreads();
-      if (tid == 0) {
-        float s = 0.f;
-        for (int k = 0; k < kPrepThreads / 64; ++k) s += wsum[k];
-        denom[g] = fmaxf(sqrtf(s), 1e-6f);
-      }
-      __syncthreads();
+    float acc[GP];
+#pragma unroll
+    for (int g = 0; g < GP; ++g) acc[g] = 0.f;
+    for (int c = tid; c < C; c += kPrepThreads) {
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) {
+          const float v = load_f<PDT>(protos + (int64_t)g * C + c);
+          acc[g] = __builtin_fmaf(v, v, acc[g]);
+        }
     }
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+      float a = acc[g];
+      for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+      if (lane == 0) wsum[wv][g] = a;
+    }
+    __syncthreads();
+    if (tid < GP) {
+      float t = 0.f;
+      for (int k = 0; k < kPrepThreads / 64; ++k) t += wsum[k][tid];
+      denom[tid] = fmaxf(sqrtf(t), 1e-6f);
+    }
+    __syncthreads();
   }
-  const int W = 2 * GP;
-  for (int64_t i = tid; i < (int64_t)C * W; i += kPrepThreads) {
-    const int c = (int)(i / W), j = (int)(i % W);
-    float v = 0.f;
-    if (j < G) v = round_to<XDT>(load_f<WDT>(w + (int64_t)j * C + c));
-    else if (protos != nullptr && j >= GP && j < GP + G) v = load_f<PDT>(protos + (int64_t)(j - GP) * C + c) / denom[j - GP];
-    wpk[i] = v;
+  for (int c = tid; c < C; c += kPrepThreads) {
+    float row[2 * GP];
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+      row[g] = g < G ? round_to<XDT>(load_f<WDT>(w + (int64_t)g * C + c)) : 0.f;
+      row[GP + g] = (protos != nullptr && g < G) ? load_f<PDT>(protos + (int64_t)g * C + c) / denom[g] : 0.f;
+    }
+    float4* dst = reinterpret_cast<float4*>(wpk + (int64_t)c * 2 * GP);
+#pragma unroll
+    for (int k = 0; k < GP / 2; ++k) dst[k] = make_float4(row[4 * k], row[4 * k + 1], row[4 * k + 2], row[4 * k + 3]);
   }
   if (tid == 0) {
     if (conf != nullptr && conf_w != nullptr)
       for (int g = 0; g < G; ++g) conf_w[g] = round_to<PDT>(load_f<PDT>(conf + g) + 1e-6f);
     if (usage != nullptr && usage_b != nullptr) {
-      float v[64];
+      float v[GP];
       float m = -INFINITY;
       for (int g = 0; g < G; ++g) {
         v[g] = -round_to<PDT>(load_f<PDT>(usage + g) + 1e-6f);
@@ -631,13 +645,21 @@ extern "C" int pfa_router_prepare(const void* w_router, int w_dtype, const void*
                                   float* conf_weight, float* usage_bias, void* stream) {
   clear_error();
   PFA_CHECK_ARG(w_router && w_packed && G > 0 && G <= 64 && C > 0, "pfa_router_prepare: bad arguments");
+  PFA_CHECK_ARG(((uintptr_t)w_packed & 15) == 0, "pfa_router_prepare: w_packed must be 16-byte aligned");
   hipStream_t s = as_stream(stream);
   const int GP = gate_pad(G);
-#define PFA_PREP(WD, PD, XD)                                                                                  \
-  router_prepare_kernel<WD, PD, XD><<<1, kPrepThreads, 0, s>>>(                                              \
+#define PFA_PREP_G(WD, PD, XD, GPV)                                                                         \
+  router_prepare_kernel<WD, PD, XD, GPV><<<1, kPrepThreads, 0, s>>>(                                        \
       (const typename Elem<WD>::T*)w_router, (const typename Elem<PD>::T*)protos,                            \
-      (const typename Elem<PD>::T*)confidence, (const typename Elem<PD>::T*)usage, G, C, GP, w_packed,        \
+      (const typename Elem<PD>::T*)confidence, (const typename Elem<PD>::T*)usage, G, C, w_packed,            \
       conf_weight, usage_bias)
+#define PFA_PREP(WD, PD, XD)                              \
+  do {                                                    \
+    if (GP == 8) PFA_PREP_G(WD, PD, XD, 8);               \
+    else if (GP == 16) PFA_PREP_G(WD, PD, XD, 16);        \
+    else if (GP == 32) PFA_PREP_G(WD, PD, XD, 32);        \
+    else PFA_PREP_G(WD, PD, XD, 64);                      \
+  } while (0)
 #define PFA_PREP_X(WD, PD)                                                 \
   switch (x_dtype) {                                                       \
     case PFA_F32: PFA_PREP(WD, PD, PFA_F32); break;                        \
@@ -661,6 +683,7 @@ extern "C" int pfa_router_prepare(const void* w_router, int w_dtype, const void*
 #undef PFA_PREP_P
 #undef PFA_PREP_X
 #undef PFA_PREP
+#undef PFA_PREP_G
   PFA_CHECK_LAUNCH("pfa_router_prepare");
   return PFA_OK;
 }

@@ -44,6 +44,7 @@ constexpr int kLd = 72;     // padded LDS row, bf16 elements
 constexpr int kPartW = 68;  // floats per partial row: m, l, pad, pad, acc[64]
 constexpr int kMaxProto = 1024;
 constexpr int kMaxClassRows = 4096;
+constexpr float kRescaleLog2 = 0.0f;  // rescale only when some row's max rises
 
 struct ShortArgs {
   pfa_tensor4 q, k, v, out;
@@ -141,7 +142,7 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
                                           float scale_log2, MaskF mask, QState& st) {
   const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
   float s[4][4];
-  float tmax = -INFINITY;
+  float tmax = -INFINITY;  // raw scores (the scale is applied in the exp argument)
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     f32x4_t c = {0.f, 0.f, 0.f, 0.f};
@@ -154,10 +155,10 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
     for (int i = 0; i < 4; ++i) {
       if constexpr (MASKED) {
         const bool ok = mask(16 * kb + 4 * g + i);
-        s[kb][i] = ok ? c[i] * scale_log2 : -INFINITY;
+        s[kb][i] = ok ? c[i] : -INFINITY;
         st.cnt += ok ? 1 : 0;
       } else {
-        s[kb][i] = c[i] * scale_log2;
+        s[kb][i] = c[i];
       }
       tmax = fmaxf(tmax, s[kb][i]);
     }
@@ -165,30 +166,33 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
   if constexpr (!MASKED) st.cnt += 16;
   tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
   tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-  const float mn = fmaxf(st.m, tmax);
-  float alpha = 1.f;
-  float psum = 0.f;
-  if (mn != -INFINITY) {
-    alpha = __builtin_amdgcn_exp2f(st.m - mn);  // st.m == -inf -> 0
+  // Lazy rescaling: the accumulator is rescaled only on tiles where some row
+  // of the wave sees a new maximum (a wave-uniform branch); st.m stays the
+  // exact running max (log2 units), so every P <= 1 and the arithmetic is
+  // that of the plain online softmax.
+  const float tm = tmax * scale_log2;
+  if (__ballot(tm > st.m + kRescaleLog2) != 0) {
+    const float mn = fmaxf(st.m, tm);
+    const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(st.m - mn);  // st.m == -inf -> 0
+    st.l *= alpha;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[kb][i] = __builtin_amdgcn_exp2f(s[kb][i] - mn);  // -inf -> 0
-        psum += s[kb][i];
-      }
-  } else {
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[kb][i] = 0.f;
+      for (int i = 0; i < 4; ++i) st.acc[db][i] *= alpha;
+    st.m = mn;
   }
-  st.l = st.l * alpha + psum;
-  st.m = mn;
+  // a row whose reference is still -inf has seen only masked keys: its
+  // scores are -inf and its P is 0 with any finite offset
+  const float moff = st.m == -INFINITY ? 0.f : st.m;
+  float psum = 0.f;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st.acc[db][i] *= alpha;
+    for (int i = 0; i < 4; ++i) {
+      s[kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], scale_log2, -moff));  // -inf -> 0
+      psum += s[kb][i];
+    }
+  st.l += psum;
   // P is rounded to bf16 for the P.V MFMA (the reference's bf16 path rounds
   // its probabilities to bf16 too); the accumulator stays f32.
 #pragma unroll

@@ -797,3 +797,30 @@ def test_chunked_runner_small_gpu(dev):
     assert res.metrics.used_fallback is False
     assert res.final_output is not None and torch.isfinite(res.final_output).all()
     del seq
+
+
+def test_router_without_prototypes_vs_oracle(dev):
+    """use_proto == 0: gates are the router softmax alone; the packed table
+    keeps its (C, 2*Gp) layout and only the weight columns are read."""
+    from proteus_attention import _hip
+    from proteus_attention.models.aspa import pack_router_weights
+
+    g = torch.Generator().manual_seed(12)
+    n, C, G, H = 3000, 512, 8, 8
+    x = torch.randn(n, C, generator=g)
+    w = torch.randn(G, C, generator=g) * 0.05
+    lib = _hip.lib()
+    wpk = pack_router_weights(w.to(dev), None, torch.float32)
+    g2h = O.default_gate_map(G, H).to(torch.int32).to(dev)
+    gate = torch.empty(n, G, device=dev)
+    imp = torch.empty(n, device=dev)
+    hidx = torch.empty(n, 2, dtype=torch.int32, device=dev)
+    _hip.check(lib.pfa_router_topk(_hip.ptr(x.to(dev)), _hip.PFA_F32, n, C, G, _hip.ptr(wpk), 0, None, None,
+                                   _hip.ptr(g2h), H, 2, 0.2, 0.25, 0.6, 0.0, _hip.ptr(gate), None, None, _hip.ptr(imp),
+                                   _hip.ptr(hidx), None, None, None, _hip.stream_ptr(dev)), "router")
+    og, _, _, oimp = O.route_tokens(x, w, None, None, None, proto_temp=0.2, proto_threshold=0.25, proto_blend=0.6,
+                                    usage_boost=0.0)
+    assert torch.allclose(gate.cpu(), og, atol=2e-6, rtol=0)
+    assert torch.allclose(imp.cpu(), oimp, atol=2e-6, rtol=0)
+    _, oidx = O.topk_lowest(gate.cpu(), 2)
+    assert torch.equal(hidx.cpu().long(), oidx)
