@@ -7,7 +7,7 @@
 // likewise V) in LDS, then S = Q K^T and O += P V run on
 // v_mfma_f32_16x16x32_bf16 with an online softmax in f32 registers.
 //
-// Workgroup: 8 waves, 256 consecutive query tokens of one head (32 per wave
+// Workgroup: 4 waves, 128 consecutive query tokens of one head (32 per wave
 // in two 16-query MFMA column groups).  The shortlist is sorted by
 // position, so a query tile's keys are a prefix of it: keys below
 // rng.x (position < first token of the tile) are visible to every query and
@@ -22,7 +22,7 @@ namespace fin {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQ = 32 * kWaves;  // queries per workgroup
 constexpr int kTile = 64;        // keys per tile
@@ -51,20 +51,20 @@ struct St {
   f32x4_t acc[4];
 };
 
-// one 64-key tile staged by 512 threads: thread -> key tid/8, elements
-// 8*(tid%8) .. +7 of that key's K and V rows
+// one 64-key tile staged by 256 threads: thread -> key tid/4, elements
+// 16*(tid%4) .. +15 of that key's K and V rows
 struct Fetch {
-  uint2 k, v;
+  uint4 k, v;
   float kscale, vscale;
   int pos;
 };
 
 __device__ __forceinline__ Fetch fetch(const int8_t* kb, const int8_t* vb, const float* ksb, const float* vsb,
                                        const int32_t* kpos, int key) {
-  const int oct = threadIdx.x & 7;
+  const int qd = threadIdx.x & 3;
   Fetch f;
-  f.k = *reinterpret_cast<const uint2*>(kb + (int64_t)key * kD + 8 * oct);
-  f.v = *reinterpret_cast<const uint2*>(vb + (int64_t)key * kD + 8 * oct);
+  f.k = *reinterpret_cast<const uint4*>(kb + (int64_t)key * kD + 16 * qd);
+  f.v = *reinterpret_cast<const uint4*>(vb + (int64_t)key * kD + 16 * qd);
   f.kscale = ksb[key];
   f.vscale = vsb[key];
   f.pos = kpos[key];
@@ -74,21 +74,24 @@ __device__ __forceinline__ Fetch fetch(const int8_t* kb, const int8_t* vb, const
 __device__ __forceinline__ float i8f(uint32_t w, int e) { return (float)(int)(int8_t)((w >> (8 * e)) & 0xffu); }
 
 __device__ __forceinline__ void store(const Fetch& f, uint16_t* Ks, uint16_t* Vt, int32_t* kp) {
-  const int j = threadIdx.x >> 3, oct = threadIdx.x & 7;
-  __bf16 kd[8];
+  const int j = threadIdx.x >> 2, qd = threadIdx.x & 3;
+  const uint32_t kw4[4] = {f.k.x, f.k.y, f.k.z, f.k.w};
+  const uint32_t vw4[4] = {f.v.x, f.v.y, f.v.z, f.v.w};
+  __bf16 kd[16];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) kd[e] = (__bf16)(i8f(e < 4 ? f.k.x : f.k.y, e & 3) * f.kscale);
-  uint4 kw;
-  __builtin_memcpy(&kw, kd, 16);
-  *reinterpret_cast<uint4*>(Ks + j * kLd + 8 * oct) = kw;
+  for (int e = 0; e < 16; ++e) kd[e] = (__bf16)(i8f(kw4[e >> 2], e & 3) * f.kscale);
+  uint4 kw[2];
+  __builtin_memcpy(kw, kd, 32);
+  *reinterpret_cast<uint4*>(Ks + j * kLd + 16 * qd) = kw[0];
+  *reinterpret_cast<uint4*>(Ks + j * kLd + 16 * qd + 8) = kw[1];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const __bf16 v = (__bf16)(i8f(e < 4 ? f.v.x : f.v.y, e & 3) * f.vscale);
+  for (int e = 0; e < 16; ++e) {
+    const __bf16 v = (__bf16)(i8f(vw4[e >> 2], e & 3) * f.vscale);
     uint16_t bits;
     __builtin_memcpy(&bits, &v, 2);
-    Vt[(8 * oct + e) * kLd + j] = bits;
+    Vt[(16 * qd + e) * kLd + j] = bits;
   }
-  if (oct == 0) kp[j] = f.pos;
+  if (qd == 0) kp[j] = f.pos;
 }
 
 template <bool MASKED>
@@ -201,7 +204,8 @@ __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restri
   rng[qt] = make_int2(below, lo);
 }
 
-__global__ void __launch_bounds__(kThreads) final_attn_kernel(Args a) {
+// at most 168 VGPRs: three 4-wave workgroups per CU
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) final_attn_kernel(Args a) {
   __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
   __shared__ __align__(16) uint16_t Vt[2][kD * kLd];
   __shared__ int32_t kp[2][kTile];
@@ -243,7 +247,7 @@ __global__ void __launch_bounds__(kThreads) final_attn_kernel(Args a) {
   const float* ksb = a.ks + (int64_t)h * a.S;
   const float* vsb = a.vs + (int64_t)h * a.S;
   const int ntile = (rg.y + kTile - 1) / kTile;
-  const int jrow = tid >> 3;
+  const int jrow = tid >> 2;
   if (ntile > 0) store(fetch(kb, vb, ksb, vsb, a.kpos, min(jrow, a.S - 1)), Ks[0], Vt[0], kp[0]);
   __syncthreads();
   for (int i = 0; i < ntile; ++i) {

@@ -243,11 +243,16 @@ __device__ __forceinline__ int64_t xcd_block(int64_t P, int64_t nblk) {
 // ---------------------------------------------------------------------
 // Pass 1: anchors per (residue class, compact head)
 // ---------------------------------------------------------------------
-__global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
+// Occupancy: at most 168 VGPRs so that three 4-wave workgroups share a CU.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) short_anchor_kernel(ShortArgs a,
+                                                                                                     int ccap) {
   __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
   __shared__ __align__(16) uint16_t Vt[2][64 * kLd];
-  __shared__ uint16_t cls_m[kMaxClassRows];  // M < kMaxClassRows <= 65536
-  __shared__ int32_t cls_r[kMaxClassRows];
+  // active rows of the class: row index and class position M (M < ccap <=
+  // kMaxClassRows), sized to the class length (dynamic LDS)
+  extern __shared__ int32_t cls_dyn[];
+  int32_t* cls_r = cls_dyn;
+  uint16_t* cls_m = reinterpret_cast<uint16_t*>(cls_dyn + ccap);
   __shared__ int s_count;
   __shared__ int wave_cnt[4];
 
@@ -363,7 +368,8 @@ __global__ void __launch_bounds__(256) short_anchor_kernel(ShortArgs a) {
 // ---------------------------------------------------------------------
 // Pass 2: window + prototype keys per segment of consecutive rows
 // ---------------------------------------------------------------------
-__global__ void __launch_bounds__(256) short_main_kernel(ShortArgs a, int use_part, int pcap) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
+short_main_kernel(ShortArgs a, int use_part, int pcap) {
   __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
   __shared__ __align__(16) uint16_t Vt[2][64 * kLd];
   __shared__ int32_t r_t[kRows];
@@ -635,7 +641,8 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   hipStream_t s = as_stream(stream);
   if (anchors) {
     dim3 grid((unsigned)((int64_t)anchor_stride < T ? (int64_t)anchor_stride : T), (unsigned)P_cap);
-    short_anchor_kernel<<<grid, 256, 0, s>>>(a);
+    const int ccap = (int)((T - 1) / anchor_stride + 1);
+    short_anchor_kernel<<<grid, 256, (size_t)ccap * 6 + 16, s>>>(a, ccap);
     PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
   }
   int64_t blocks = (N + kRows - 1) / kRows;
