@@ -69,6 +69,37 @@ __global__ void __launch_bounds__(256) rope8_kernel(typename Elem<DT>::T* qkv, i
   store8<DT>(base, o);
 }
 
+// Token-row variant for D = 64: workgroup bt rotates the 2*H*8 groups of 8
+// elements of token row bt (q heads, then k heads), which share one table
+// row.  Index math is shifts and one compare per group (no 64-bit division
+// per element).
+template <int DT>
+__global__ void __launch_bounds__(256) rope64_row_kernel(typename Elem<DT>::T* qkv, int64_t T, int H,
+                                                         const typename Elem<DT>::T* cos_tab,
+                                                         const typename Elem<DT>::T* sin_tab) {
+  const int64_t bt = blockIdx.x;
+  const int64_t t = (int64_t)((uint32_t)bt % (uint32_t)T);  // rows < 2^31 (host check)
+  const int C = H * 64;
+  typename Elem<DT>::T* row = qkv + bt * (3 * (int64_t)C);
+  const int groups = 2 * H * 8;
+  for (int e = threadIdx.x; e < groups; e += blockDim.x) {
+    const int g8 = e & 7;   // 8-element group within the head
+    const int hw = e >> 3;  // q head hw, or k head hw - H
+    const int off = (hw >= H ? C + (hw - H) * 64 : hw * 64) + 8 * g8;
+    float xv[8], cv[8], sv[8], o[8];
+    load8<DT>(row + off, xv);
+    load8<DT>(cos_tab + t * 64 + 8 * g8, cv);
+    load8<DT>(sin_tab + t * 64 + 8 * g8, sv);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float xe = xv[2 * p], xo = xv[2 * p + 1];
+      o[2 * p] = round_to<DT>(round_to<DT>(xe * cv[2 * p]) + round_to<DT>(-xo * sv[2 * p]));
+      o[2 * p + 1] = round_to<DT>(round_to<DT>(xo * cv[2 * p + 1]) + round_to<DT>(xe * sv[2 * p + 1]));
+    }
+    store8<DT>(row + off, o);
+  }
+}
+
 // Per-pair variant for head dims that are not a multiple of 8.
 template <int DT>
 __global__ void __launch_bounds__(256) rope_kernel(typename Elem<DT>::T* qkv, int64_t n_pairs, int64_t T,
@@ -140,6 +171,31 @@ extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H
   hipStream_t s = as_stream(stream);
   const bool vec = (D % 8) == 0 && ((uintptr_t)qkv % 16) == 0 && ((uintptr_t)cos_tab % 16) == 0 &&
                    ((uintptr_t)sin_tab % 16) == 0;
+  if (vec && D == 64 && (int64_t)B * T < INT32_MAX && H <= 256) {
+    const int64_t rows = (int64_t)B * T;
+    if (rows == 0) return PFA_OK;
+    const unsigned threads = (unsigned)(2 * H * 8 < 256 ? 2 * H * 8 : 256);
+    const unsigned nblk = (unsigned)rows;
+    switch (dtype) {
+      case PFA_F32:
+        rope64_row_kernel<PFA_F32><<<nblk, threads, 0, s>>>((float*)qkv, T, H, (const float*)cos_tab,
+                                                                      (const float*)sin_tab);
+        break;
+      case PFA_BF16:
+        rope64_row_kernel<PFA_BF16><<<nblk, threads, 0, s>>>((uint16_t*)qkv, T, H, (const uint16_t*)cos_tab,
+                                                                       (const uint16_t*)sin_tab);
+        break;
+      case PFA_F16:
+        rope64_row_kernel<PFA_F16><<<nblk, threads, 0, s>>>((uint16_t*)qkv, T, H, (const uint16_t*)cos_tab,
+                                                                      (const uint16_t*)sin_tab);
+        break;
+      default:
+        set_error("pfa_rope_qk_inplace: unsupported dtype %d", dtype);
+        return PFA_E_UNSUPPORTED;
+    }
+    PFA_CHECK_LAUNCH("pfa_rope_qk_inplace");
+    return PFA_OK;
+  }
   if (vec) {
     int64_t n_groups = (int64_t)B * T * 2 * H * (D / 8);
     if (n_groups == 0) return PFA_OK;

@@ -505,11 +505,11 @@ def test_pack_vs_oracle(dev):
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_rope_kernel_bitwise(dev, dt):
+@pytest.mark.parametrize("B,T,H,D", [(2, 37, 4, 16), (2, 300, 8, 64), (1, 70, 3, 64)])
+def test_rope_kernel_bitwise(dev, dt, B, T, H, D):
     from proteus_attention import _hip
 
     g = torch.Generator().manual_seed(14)
-    B, T, H, D = 2, 37, 4, 16
     qkv = torch.randn(B, T, 3 * H * D, generator=g).to(dt)
     cos, sin = O.rope_tables(T, D, 10000.0, dt)
     d = qkv.to(dev).contiguous()
