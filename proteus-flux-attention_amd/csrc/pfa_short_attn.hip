@@ -137,7 +137,7 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ kb, const
 // the tile lies inside every row's key range).  exp2 runs on v_exp_f32
 // directly (arguments are <= 0; -inf gives 0), P is rounded to bf16 with
 // v_cvt_pk_bf16_f32 (round to nearest even).
-template <bool MASKED, class MaskF>
+template <bool MASKED, bool COUNT, class MaskF>
 __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_t* Ks, const uint16_t* Vt,
                                           float scale_log2, MaskF mask, QState& st) {
   const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
@@ -156,14 +156,14 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
       if constexpr (MASKED) {
         const bool ok = mask(16 * kb + 4 * g + i);
         s[kb][i] = ok ? c[i] : -INFINITY;
-        st.cnt += ok ? 1 : 0;
+        if constexpr (COUNT) st.cnt += ok ? 1 : 0;
       } else {
         s[kb][i] = c[i];
       }
       tmax = fmaxf(tmax, s[kb][i]);
     }
   }
-  if constexpr (!MASKED) st.cnt += 16;
+  if constexpr (!MASKED && COUNT) st.cnt += 16;
   tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
   tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
   // Lazy rescaling: the accumulator is rescaled only on tiles where some row
@@ -346,8 +346,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
         const int m = m0 + kl;
         return m <= (int)mhi && m >= lo_q && m <= hi_q;
       };
-      if (full) tile_step<false>(qf, Ks[cur], Vt[cur], a.scale_log2, cls_mask, st);
-      else if (!empty) tile_step<true>(qf, Ks[cur], Vt[cur], a.scale_log2, cls_mask, st);
+      if (full) tile_step<false, false>(qf, Ks[cur], Vt[cur], a.scale_log2, cls_mask, st);
+      else if (!empty) tile_step<true, false>(qf, Ks[cur], Vt[cur], a.scale_log2, cls_mask, st);
       if (more) store_tile(nxt, Ks[cur ^ 1], Vt[cur ^ 1]);
       __syncthreads();
     }
@@ -368,6 +368,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
 // ---------------------------------------------------------------------
 // Pass 2: window + prototype keys per segment of consecutive rows
 // ---------------------------------------------------------------------
+template <bool COUNT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
 short_main_kernel(ShortArgs a, int use_part, int pcap) {
   __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
@@ -377,6 +378,8 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
   __shared__ int32_t seg_begin[kRows + 1];
   __shared__ int s_nseg;
   __shared__ int s_plen;
+  __shared__ int s_wcnt[4];
+  __shared__ int s_has0;
   // prototype key list of the current segment: position, evict, position mod stride
   extern __shared__ int32_t pdyn[];
   int32_t* pk = pdyn;
@@ -427,62 +430,58 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     // prototype key list: the prefix set of t_first below lo_last (set table
     // row of t_first's block -- any order, INT32_MAX-padded -- then the
     // block's tokens up to t_first, keeping p with evict[p] > t_first), then
-    // key 0 for the zero-anchor rule
-    if (tid < 64) {
-      int n = 0;
-      bool has0 = false;
-      if (a.blk != nullptr) {
-        const uint64_t lt = (1ull << lane) - 1;
-        const int64_t jb = t_first >> 6;
-        const int32_t* P = a.blk + (bb * a.nblk + jb) * a.K;
-        const int32_t* ev = a.evict + bb * a.T;
-        for (int base = 0; base < a.K; base += 64) {
-          const int j = base + lane;
-          const int32_t v = j < a.K ? P[j] : INT32_MAX;
-          bool keep = false;
-          int32_t e = 0;
-          if (v < lo_last) {
-            e = ev[v];
-            keep = e > t_first;
-          }
-          const uint64_t bal = __ballot(keep);
-          if (keep) {
-            const int pos = n + __popcll(bal & lt);
-            pk[pos] = v;
-            pe[pos] = e;
-            pm[pos] = sa > 0 ? v % sa : 0;
-          }
-          n += __popcll(bal);
-          has0 = has0 || __ballot(keep && v == 0) != 0;
-          if (__ballot(v == INT32_MAX)) break;  // padding: the row holds no more entries
+    // key 0 for the zero-anchor rule.  All 256 threads take one candidate
+    // each (the evict lookups of a segment are one round of loads) and
+    // compact the kept ones through per-wave counts.
+    if (tid == 0) {
+      s_plen = 0;
+      s_has0 = 0;
+    }
+    __syncthreads();
+    if (a.blk != nullptr) {
+      const int64_t jb = t_first >> 6;
+      const int32_t* P = a.blk + (bb * a.nblk + jb) * a.K;
+      const int32_t* ev = a.evict + bb * a.T;
+      const int ncand = a.K + 64;
+      for (int base = 0; base < ncand; base += 256) {
+        const int e = base + tid;
+        int32_t v = INT32_MAX;
+        if (e < a.K) {
+          v = P[e];
+        } else if (e < ncand) {
+          const int q = (int)(jb << 6) + (e - a.K);
+          if (q <= t_first) v = q;
         }
-        const int q = (int)(jb << 6) + lane;
         bool keep = false;
-        int32_t e = 0;
-        if (q <= t_first && q < lo_last) {
-          e = ev[q];
-          keep = e > t_first;
+        int32_t evv = 0;
+        if (v < lo_last) {
+          evv = ev[v];
+          keep = evv > t_first;
         }
         const uint64_t bal = __ballot(keep);
+        if (lane == 0) s_wcnt[wid] = __popcll(bal);
+        if (keep && v == 0) s_has0 = 1;
+        __syncthreads();
+        int before = s_plen;
+        for (int w2 = 0; w2 < wid; ++w2) before += s_wcnt[w2];
         if (keep) {
-          const int pos = n + __popcll(bal & lt);
-          pk[pos] = q;
-          pe[pos] = e;
-          pm[pos] = sa > 0 ? q % sa : 0;
+          const int pos = before + __popcll(bal & ((1ull << lane) - 1ull));
+          pk[pos] = v;
+          pe[pos] = evv;
+          pm[pos] = sa > 0 ? v % sa : 0;
         }
-        n += __popcll(bal);
-        has0 = has0 || __ballot(keep && q == 0) != 0;
+        __syncthreads();
+        if (tid == 0) s_plen += s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
+        __syncthreads();
       }
-      if (lo_last > 0 && sa > 0 && sl > 0 && !has0) {
-        // order inside the list does not matter
-        if (lane == 0) {
-          pk[n] = 0;
-          pe[n] = -1;  // not in the prototype set: only the zero-anchor rule applies
-          pm[n] = 0;
-        }
-        ++n;
-      }
-      if (lane == 0) s_plen = n;
+    }
+    if (tid == 0 && lo_last > 0 && sa > 0 && sl > 0 && !s_has0) {
+      // order inside the list does not matter
+      const int n = s_plen;
+      pk[n] = 0;
+      pe[n] = -1;  // not in the prototype set: only the zero-anchor rule applies
+      pm[n] = 0;
+      s_plen = n + 1;
     }
     __syncthreads();
     const int plen = s_plen;
@@ -528,15 +527,15 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
         const int k0 = lo_first + kTile * i;
         const bool empty = !wave_rows || k0 > w_thi || k0 + kTile - 1 < w_llo;
         const bool full = wave_full && k0 >= w_lhi && k0 + kTile - 1 <= w_tlo;
-        auto win_mask = [&](int kl) {
-          const int kp = k0 + kl;
-          return qv && kp <= tq && kp >= loq;
-        };
-        if (full) tile_step<false>(qf, Ks[cur], Vt[cur], a.scale_log2, win_mask, st);
-        else if (!empty) tile_step<true>(qf, Ks[cur], Vt[cur], a.scale_log2, win_mask, st);
+        // this row's window keys in the tile are kl in [wa, wa + wn)
+        const int wa = max(loq - k0, 0);
+        const int wn = qv ? max(min(tq - k0, kTile - 1) - wa + 1, 0) : 0;
+        auto win_mask = [&](int kl) { return (unsigned)(kl - wa) < (unsigned)wn; };
+        if (full) tile_step<false, COUNT>(qf, Ks[cur], Vt[cur], a.scale_log2, win_mask, st);
+        else if (!empty) tile_step<true, COUNT>(qf, Ks[cur], Vt[cur], a.scale_log2, win_mask, st);
       } else if (wave_rows) {
         const int j0 = (i - nw) * kTile;
-        tile_step<true>(qf, Ks[cur], Vt[cur], a.scale_log2,
+        tile_step<true, COUNT>(qf, Ks[cur], Vt[cur], a.scale_log2,
                   [&](int kl) {
                     const int j = j0 + kl;
                     if (!qv || j >= plen) return false;
@@ -556,9 +555,11 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     float lt = st.l;
     lt += __shfl_xor(lt, 16, 64);
     lt += __shfl_xor(lt, 32, 64);
-    int ct = st.cnt;
-    ct += __shfl_xor(ct, 16, 64);
-    ct += __shfl_xor(ct, 32, 64);
+    int ct = COUNT ? st.cnt : 0;
+    if constexpr (COUNT) {
+      ct += __shfl_xor(ct, 16, 64);
+      ct += __shfl_xor(ct, 32, 64);
+    }
     if (qv) {
       const int64_t r = r0 + qs;
       float m = st.m;
@@ -585,7 +586,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
         *reinterpret_cast<uint2*>(op + 16 * db + 4 * g) =
             make_uint2((uint32_t)o4[0] | ((uint32_t)o4[1] << 16), (uint32_t)o4[2] | ((uint32_t)o4[3] << 16));
       }
-      if (a.lengths != nullptr && g == 0) {
+      if (COUNT && g == 0) {
         int64_t na = 0;
         if (a.stride > 0 && a.slots > 0) {
           const int64_t M = tq / a.stride;
@@ -649,7 +650,10 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   blocks = (blocks + 7) / 8 * 8;
   PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_shortlist_attn_fwd: too many rows");
   const int pcap = (proto_blocks ? proto_k : 0) + 64 + 1;
-  short_main_kernel<<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
+  if (lengths != nullptr)
+    short_main_kernel<true><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
+  else
+    short_main_kernel<false><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
   PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/main");
   return PFA_OK;
 }

@@ -383,14 +383,16 @@ def _shortlist_attn_structured(
     evict: Optional[torch.Tensor],
     scale: float,
     device: torch.device,
-) -> torch.Tensor:
+    want_lengths: bool = True,
+) -> Optional[torch.Tensor]:
     """Module-path shortlist attention without materialised candidates
     (bf16, D=64); the prototype sets come as _proto_prefix_blocks tables of
-    the T-token scores.  Returns each row's candidate count (int32, (N,))."""
+    the T-token scores.  Returns each row's candidate count (int32, (N,)),
+    or None when want_lengths is False (the kernel then skips the counting)."""
 
     lib = _hip.lib()
     N = int(token_idx.numel())
-    lengths = torch.empty(N, dtype=torch.int32, device=device)
+    lengths = torch.empty(N, dtype=torch.int32, device=device) if want_lengths else None
     anchors = stride > 0 and slots > 0
     part = None
     if anchors:

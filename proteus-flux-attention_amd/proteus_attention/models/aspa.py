@@ -449,6 +449,9 @@ class AdaptiveSparseAttention(nn.Module):
         self.last_head_consensus: Optional[torch.Tensor] = None
         self._last_gate_probs: Optional[torch.Tensor] = None
         self._last_shortlist_lengths: Optional[torch.Tensor] = None
+        # per-row candidate counts of the structured shortlist path are
+        # telemetry: computed (inside the attention kernel) only on request
+        self.record_shortlist_lengths = False
 
     # ------------------------------------------------------------------
     # RoPE tables (aspa.py:576-604)
@@ -1329,7 +1332,7 @@ class AdaptiveSparseAttention(nn.Module):
                 _hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
                 _hip.tensor4(q5[:, :, 2], H, "bthd"), _hip.tensor4(attn.view(B, T, H, D), H, "bthd"), H, T, D,
                 token_idx, row_head, heads, summary, row_of, w_eff, stride, slots, blocks, evict,
-                1.0 / math.sqrt(D), device)
+                1.0 / math.sqrt(D), device, want_lengths=bool(self.record_shortlist_lengths))
             self._last_shortlist_lengths = lens
             _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
                             quantized=False, candidates=True, structured=True)

@@ -237,6 +237,7 @@ def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, 
     _say(f"structured vs materialised T={T} L={L} w={w} s={s} B={B}")
     cfg = shortlist_cfg(T, 512, 8, L, w, s)
     m, x = _module(cfg, B, T, 512, torch.bfloat16, dev, outlier)
+    m.record_shortlist_lengths = True
     snap = {n: b.detach().clone() for n, b in m.named_buffers() if n.startswith("routing_")}
     with torch.no_grad():
         y_s = m(x)
