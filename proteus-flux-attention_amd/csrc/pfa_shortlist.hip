@@ -8,7 +8,8 @@
 //   1. block_sort : each block's scores sorted best first (wave bitonic);
 //   2. sb_local   : per superblock, one workgroup folds its blocks in order:
 //                   Q[j] = top-K of the superblock's tokens up to block j;
-//   3. sb_scan    : one workgroup folds the superblock totals:
+//   3. scan_round : a log-depth scan over the superblock totals (ceil(log2
+//                   nsb) rounds, every superblock in parallel):
 //                   R[s] = top-K of all tokens before superblock s;
 //   4. block_walk : per block j, P = top-K(R[s] U Q[j-1]) = S(64j - 1) is
 //                   written as the block's set table row (best first, or
@@ -57,9 +58,12 @@ struct PrefixWs {
   float* qval;
   int32_t* qidx;
   int32_t* qlen;
-  float* rval;
+  float* rval;  // (B, nsb+1, K): row s+1 = top-K of superblocks 0..s, row 0 empty
   int32_t* ridx;
   int32_t* rlen;
+  float* r2val;  // ping-pong partner of rval/ridx/rlen for the log-depth scan
+  int32_t* r2idx;
+  int32_t* r2len;
   int32_t* blk;    // (B, nb, K) set table (used by pfa_proto_prefix_topk)
   int32_t* evict;  // (B, T) (used when the caller passes no evict array)
 };
@@ -74,9 +78,12 @@ static size_t prefix_ws_bytes(int64_t B, int64_t T, int64_t nb, int64_t nsb, int
   p = take((size_t)B * nb * K * 4);    if (w) w->qval = (float*)p;
   p = take((size_t)B * nb * K * 4);    if (w) w->qidx = (int32_t*)p;
   p = take((size_t)B * nb * 4);        if (w) w->qlen = (int32_t*)p;
-  p = take((size_t)B * nsb * K * 4);   if (w) w->rval = (float*)p;
-  p = take((size_t)B * nsb * K * 4);   if (w) w->ridx = (int32_t*)p;
-  p = take((size_t)B * nsb * 4);       if (w) w->rlen = (int32_t*)p;
+  p = take((size_t)B * (nsb + 1) * K * 4);   if (w) w->rval = (float*)p;
+  p = take((size_t)B * (nsb + 1) * K * 4);   if (w) w->ridx = (int32_t*)p;
+  p = take((size_t)B * (nsb + 1) * 4);       if (w) w->rlen = (int32_t*)p;
+  p = take((size_t)B * (nsb + 1) * K * 4);   if (w) w->r2val = (float*)p;
+  p = take((size_t)B * (nsb + 1) * K * 4);   if (w) w->r2idx = (int32_t*)p;
+  p = take((size_t)B * (nsb + 1) * 4);       if (w) w->r2len = (int32_t*)p;
   p = take((size_t)B * nb * K * 4);    if (w) w->blk = (int32_t*)p;
   p = take((size_t)B * T * 4);         if (w) w->evict = (int32_t*)p;
   return off;
@@ -207,84 +214,65 @@ prefix_sb_local(int nb, int sbs, int K, int preload, const float* __restrict__ b
   }
 }
 
-// R[s] = top-K of every token before superblock s (one workgroup per batch).
-// Superblock totals are staged in LDS: all of them up front when they fit
-// (mode 2), else one step ahead (mode 1) or one at a time (mode 0).
+// One round of a log-depth (Hillis-Steele) inclusive scan over superblock
+// totals: out[s] = top-K(in[s] U in[s-d]) for s >= d, else in[s].  Rows are
+// (nsb+1)-strided with row s+1 holding superblock s (row 0 stays empty, so
+// that the walk reads row s as "everything before superblock s").  With
+// `from_q` the input is the superblock totals themselves: the local prefix
+// of each superblock's last block.  One workgroup per (superblock, batch);
+// both lists are staged in LDS and merged by co-rank.
 __global__ void __launch_bounds__(256)
-prefix_sb_scan(int nb, int sbs, int nsb, int K, int mode, const float* __restrict__ qval,
-               const int32_t* __restrict__ qidx, const int32_t* __restrict__ qlen, float* __restrict__ rval,
-               int32_t* __restrict__ ridx, int32_t* __restrict__ rlen) {
+prefix_scan_round(int nb, int sbs, int nsb, int K, int d, int from_q, const float* __restrict__ qval,
+                  const int32_t* __restrict__ qidx, const int32_t* __restrict__ qlen,
+                  const float* __restrict__ ival, const int32_t* __restrict__ iidx, const int32_t* __restrict__ ilen,
+                  float* __restrict__ oval, int32_t* __restrict__ oidx, int32_t* __restrict__ olen) {
   extern __shared__ char smem[];
-  float* cv0 = (float*)smem;
-  int32_t* ci0 = (int32_t*)(cv0 + K);
-  float* cv1 = (float*)(ci0 + K);
-  int32_t* ci1 = (int32_t*)(cv1 + K);
-  const int nslot = mode == 2 ? max(1, nsb - 1) : (mode == 1 ? 2 : 1);
-  float* tvs = (float*)(ci1 + K);           // nslot x K
-  int32_t* tis = (int32_t*)(tvs + (size_t)nslot * K);
-  __shared__ int s_nt[2];
-  int32_t* tn = (int32_t*)(tis + (size_t)nslot * K);  // nslot lengths (mode 2)
-  const int b = blockIdx.x, tid = threadIdx.x;
-  if (tid == 0) rlen[(int64_t)b * nsb] = 0;
-  if (nsb <= 1) return;
-  auto qrow_of = [&](int s) { return (int64_t)b * nb + (int64_t)s * sbs - 1; };  // last block of superblock s-1
-  if (mode == 2) {
-    for (int s = 1; s < nsb; ++s) {
-      const int64_t qrow = qrow_of(s);
-      const int nt = qlen[qrow];
-      float* tv = tvs + (size_t)(s - 1) * K;
-      int32_t* ti = tis + (size_t)(s - 1) * K;
-      for (int p = tid; p < nt; p += 256) { tv[p] = qval[qrow * K + p]; ti[p] = qidx[qrow * K + p]; }
-      if (tid == 0) tn[s - 1] = nt;
+  float* av = (float*)smem;
+  int32_t* ai = (int32_t*)(av + K);
+  float* cv = (float*)(ai + K);
+  int32_t* ci = (int32_t*)(cv + K);
+  const int s = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int64_t rb = (int64_t)b * (nsb + 1);
+  auto src = [&](int ss, const float*& v, const int32_t*& ix, int& n) {
+    if (from_q) {
+      const int64_t last = (int64_t)b * nb + min(nb, (ss + 1) * sbs) - 1;
+      v = qval + last * K;
+      ix = qidx + last * K;
+      n = qlen[last];
+    } else {
+      v = ival + (rb + ss + 1) * K;
+      ix = iidx + (rb + ss + 1) * K;
+      n = ilen[rb + ss + 1];
     }
-  } else {
-    const int64_t qrow = qrow_of(1);
-    const int nt = qlen[qrow];
-    for (int p = tid; p < nt; p += 256) { tvs[p] = qval[qrow * K + p]; tis[p] = qidx[qrow * K + p]; }
-    if (tid == 0) s_nt[0] = nt;
+  };
+  const float* v0;
+  const int32_t* i0;
+  int n0;
+  src(s, v0, i0, n0);
+  float* ov = oval + (rb + s + 1) * K;
+  int32_t* oi = oidx + (rb + s + 1) * K;
+  if (s == 0 && tid == 0) olen[rb] = 0;
+  if (s < d) {
+    for (int p = tid; p < n0; p += 256) { ov[p] = v0[p]; oi[p] = i0[p]; }
+    if (tid == 0) olen[rb + s + 1] = n0;
+    return;
   }
+  const float* v1;
+  const int32_t* i1;
+  int n1;
+  src(s - d, v1, i1, n1);
+  for (int p = tid; p < n0; p += 256) { av[p] = v0[p]; ai[p] = i0[p]; }
+  for (int p = tid; p < n1; p += 256) { cv[p] = v1[p]; ci[p] = i1[p]; }
   __syncthreads();
-  int n = 0, cur = 0;
-  for (int s = 1; s < nsb; ++s) {
-    const int slot = mode == 2 ? s - 1 : (mode == 1 ? ((s - 1) & 1) : 0);
-    const float* tv = tvs + (size_t)slot * K;
-    const int32_t* ti = tis + (size_t)slot * K;
-    const int nt = mode == 2 ? tn[slot] : s_nt[slot & 1];
-    if (mode == 1 && s + 1 < nsb) {
-      const int64_t qrow = qrow_of(s + 1);
-      const int nn = qlen[qrow];
-      float* dv = tvs + (size_t)(slot ^ 1) * K;
-      int32_t* di = tis + (size_t)(slot ^ 1) * K;
-      for (int p = tid; p < nn; p += 256) { dv[p] = qval[qrow * K + p]; di[p] = qidx[qrow * K + p]; }
-      if (tid == 0) s_nt[slot ^ 1] = nn;
-    }
-    const int m = min(K, n + nt);
-    const float* av = cur ? cv1 : cv0;
-    const int32_t* ai = cur ? ci1 : ci0;
-    float* ov = cur ? cv0 : cv1;
-    int32_t* oi = cur ? ci0 : ci1;
-    const int64_t rrow = (int64_t)b * nsb + s;
-    for (int p = tid; p < m; p += 256) {
-      float vv;
-      int32_t ii;
-      merge_at(p, av, ai, n, tv, ti, nt, vv, ii);
-      ov[p] = vv;
-      oi[p] = ii;
-      rval[rrow * K + p] = vv;
-      ridx[rrow * K + p] = ii;
-    }
-    if (tid == 0) rlen[rrow] = m;
-    __syncthreads();
-    if (mode == 0 && s + 1 < nsb) {
-      const int64_t qrow = qrow_of(s + 1);
-      const int nn = qlen[qrow];
-      for (int p = tid; p < nn; p += 256) { tvs[p] = qval[qrow * K + p]; tis[p] = qidx[qrow * K + p]; }
-      if (tid == 0) s_nt[0] = nn;
-      __syncthreads();
-    }
-    cur ^= 1;
-    n = m;
+  const int m = min(K, n0 + n1);
+  for (int p = tid; p < m; p += 256) {
+    float vv;
+    int32_t ii;
+    merge_at(p, av, ai, n0, cv, ci, n1, vv, ii);
+    ov[p] = vv;
+    oi[p] = ii;
   }
+  if (tid == 0) olen[rb + s + 1] = m;
 }
 
 // One workgroup (256 threads) per (block j, batch b).  LDS: the entering set
@@ -314,7 +302,7 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
   __shared__ int s_nent;
   const int j = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int s = j / sbs, k = j % sbs;
-  const int64_t rrow = (int64_t)b * nsb + s;
+  const int64_t rrow = (int64_t)b * (nsb + 1) + s;  // row s: top-K of superblocks 0..s-1
   const int na = rlen[rrow];
   for (int p = tid; p < na; p += 256) { sav[p] = rval[rrow * K + p]; sai[p] = ridx[rrow * K + p]; }
   int nq = 0;
@@ -758,21 +746,37 @@ static int prefix_blocks(const float* scores, int B, int64_t T, int64_t stride, 
   prefix_sb_local<<<dim3((unsigned)nsb, (unsigned)B), 256, lds_local, s>>>(
       (int)nb, (int)sbs, K, preload, w.bval, w.bidx, w.blen, w.qval, w.qidx, w.qlen);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/local");
-  const size_t per_slot = (size_t)K * 8 + 4;
-  int mode = 0;
-  if ((size_t)K * 16 + (size_t)(nsb > 1 ? nsb - 1 : 1) * per_slot <= kPrefixLds) mode = 2;
-  else if ((size_t)K * 16 + 2 * per_slot <= kPrefixLds) mode = 1;
-  const size_t lds_scan = (size_t)K * 16 + (size_t)(mode == 2 ? (nsb > 1 ? nsb - 1 : 1) : (mode == 1 ? 2 : 1)) * per_slot;
-  prefix_sb_scan<<<(unsigned)B, 256, lds_scan, s>>>((int)nb, (int)sbs, (int)nsb, K, mode, w.qval, w.qidx, w.qlen,
-                                                    w.rval, w.ridx, w.rlen);
-  PFA_CHECK_LAUNCH("pfa_proto_prefix/scan");
+  // log-depth inclusive scan of the superblock totals (ping-pong between
+  // the two R buffers; the last round lands in the buffer the walk reads)
+  int rounds = 0;
+  while ((1ll << rounds) < nsb) ++rounds;
+  if (rounds == 0) rounds = 1;
+  const size_t lds_round = (size_t)K * 16;
+  const float* fin_v = nullptr;
+  const int32_t* fin_i = nullptr;
+  const int32_t* fin_l = nullptr;
+  for (int r = 0; r < rounds; ++r) {
+    const bool to_primary = ((rounds - 1 - r) & 1) == 0;
+    float* ov = to_primary ? w.rval : w.r2val;
+    int32_t* oi = to_primary ? w.ridx : w.r2idx;
+    int32_t* ol = to_primary ? w.rlen : w.r2len;
+    const float* iv = to_primary ? w.r2val : w.rval;
+    const int32_t* ii = to_primary ? w.r2idx : w.ridx;
+    const int32_t* il = to_primary ? w.r2len : w.rlen;
+    prefix_scan_round<<<dim3((unsigned)nsb, (unsigned)B), 256, lds_round, s>>>(
+        (int)nb, (int)sbs, (int)nsb, K, 1 << r, r == 0 ? 1 : 0, w.qval, w.qidx, w.qlen, iv, ii, il, ov, oi, ol);
+    PFA_CHECK_LAUNCH("pfa_proto_prefix/scan");
+    fin_v = ov;
+    fin_i = oi;
+    fin_l = ol;
+  }
   if (sorted_rows)
     prefix_block_walk<true><<<grid, 256, (size_t)cap * 24, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K,
-                                                                cap, w.qval, w.qidx, w.qlen, w.rval, w.ridx, w.rlen,
+                                                                cap, w.qval, w.qidx, w.qlen, fin_v, fin_i, fin_l,
                                                                 blk, evict);
   else
     prefix_block_walk<false><<<grid, 256, (size_t)cap * 24, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K,
-                                                                 cap, w.qval, w.qidx, w.qlen, w.rval, w.ridx, w.rlen,
+                                                                 cap, w.qval, w.qidx, w.qlen, fin_v, fin_i, fin_l,
                                                                  blk, evict);
   PFA_CHECK_LAUNCH("pfa_proto_prefix/walk");
   return PFA_OK;
