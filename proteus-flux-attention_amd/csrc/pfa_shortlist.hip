@@ -43,10 +43,10 @@ namespace pfa {
 
 constexpr int kBlk = 64;  // tokens per prefix block (one wave)
 
+// Superblock size: the local fold is a sequential chain of sbs merges, the
+// superblock scan takes ceil(log2(nb / sbs)) parallel rounds.
 static int64_t prefix_sbs(int64_t nb) {
-  int64_t s = 1;
-  while (s * s < nb) s <<= 1;
-  return s;
+  return nb < 8 ? (nb > 0 ? nb : 1) : 8;
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
