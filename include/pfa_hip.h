@@ -287,6 +287,14 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
  *   head_map (P_cap) compact -> b*H+h; partials (N, pfa_shortlist_attn_part_
  *   floats()) f32 scratch for the anchor pass; lengths (N) int32 or NULL
  *   receives each row's candidate count (the builder's lengths).
+ *   q_rope_cos / q_rope_sin: NULL, or the bf16 (T, 64) RoPE tables of
+ *   pfa_rope_qk_inplace; q rows are then rotated as they are loaded (the
+ *   caller rotated only k, with pfa_rope_k_inplace), giving the same q bits
+ *   as rotating the q tensor first.
+ *   passes: 3 runs both launches; 1 only the anchor pass (writes partials),
+ *   2 only the main pass (reads them).  Splitting lets the anchor pass run
+ *   on another stream while the prototype tables are built; the caller
+ *   orders pass 1 before pass 2 and keeps partials alive between them.
  * ==================================================================== */
 int pfa_shortlist_attn_part_floats(void);
 int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
@@ -297,7 +305,9 @@ int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                            int local_w, int anchor_stride, int anchor_slots,
                            const int32_t* proto_blocks, int proto_k,
                            const int32_t* proto_evict, float scale,
-                           float* partials, int32_t* lengths, void* stream);
+                           float* partials, int32_t* lengths,
+                           const void* q_rope_cos, const void* q_rope_sin,
+                           int passes, void* stream);
 
 /* Per compact head, the largest token among its packed rows (needed by the
  * explicit-mask branch: sparse_attn.py:1010-1015). */
@@ -313,6 +323,11 @@ int pfa_head_max_token(const int32_t* token_idx, const int32_t* row_offsets,
  * ==================================================================== */
 int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D,
                         const void* cos_tab, const void* sin_tab, void* stream);
+
+/* The k third only (same arithmetic), for callers that rotate q elsewhere
+ * (pfa_shortlist_attn_fwd with q_rope_cos / q_rope_sin). */
+int pfa_rope_k_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D,
+                       const void* cos_tab, const void* sin_tab, void* stream);
 
 /* ====================================================================
  * Fill: write zeros into `bytes` of device memory with a vector-store

@@ -88,6 +88,43 @@ __device__ __forceinline__ void store_f(typename Elem<DT>::T* p, float f) {
   else if constexpr (DT == PFA_F16) *p = f32_to_f16(f);
 }
 
+// Maximum over the four lanes l, l^16, l^32, l^48 of a wave64 (the four
+// 16-lane rows), with the gfx950 row-swap permutes (VALU, no LDS round
+// trip): permlane32_swap pairs each lane with l^32 and permlane16_swap with
+// l^16.
+__device__ __forceinline__ float max_over_rows4(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// RoPE on 8 consecutive elements (4 interleaved (even, odd) pairs):
+//   o_e = r(r(x_e c_e) + r(-x_o s_e)),  o_o = r(r(x_o c_o) + r(x_e s_o))
+// where r() rounds to the tensor dtype, matching q*cos + rotate_half(q)*sin
+// evaluated as three elementwise ops in that dtype.  Shared by every kernel
+// that rotates rows, so all of them produce the same bits.
+// For bf16 the roundings use the hardware converter (v_cvt_pk_bf16_f32,
+// round to nearest even: the same bits as round_to<PFA_BF16> for every
+// non-NaN value; a NaN comes out as a NaN).
+template <int DT>
+__device__ __forceinline__ float rope_round(float f) {
+  if constexpr (DT == PFA_BF16) return (float)(__bf16)f;
+  else return round_to<DT>(f);
+}
+
+template <int DT>
+__device__ __forceinline__ void rope_rotate8(const float (&xv)[8], const float (&cv)[8], const float (&sv)[8],
+                                             float (&o)[8]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float xe = xv[2 * p], xo = xv[2 * p + 1];
+    o[2 * p] = rope_round<DT>(rope_round<DT>(xe * cv[2 * p]) + rope_round<DT>(-xo * sv[2 * p]));
+    o[2 * p + 1] = rope_round<DT>(rope_round<DT>(xo * cv[2 * p + 1]) + rope_round<DT>(xe * sv[2 * p + 1]));
+  }
+}
+
 // Load 8 consecutive elements (d .. d+7) as floats; the address must be
 // aligned to 8 elements.
 template <int DT>

@@ -43,7 +43,7 @@ __global__ void zero_fill_tail(uint8_t* p, size_t n) {
 template <int DT>
 __global__ void __launch_bounds__(256) rope8_kernel(typename Elem<DT>::T* qkv, int64_t n_groups, int64_t T, int H,
                                                     int D, const typename Elem<DT>::T* cos_tab,
-                                                    const typename Elem<DT>::T* sin_tab) {
+                                                    const typename Elem<DT>::T* sin_tab, int nparts) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n_groups) return;
   const int per_head = D / 8;
@@ -52,50 +52,49 @@ __global__ void __launch_bounds__(256) rope8_kernel(typename Elem<DT>::T* qkv, i
   int64_t rest = i / per_head;
   int h = (int)(rest % H);
   rest /= H;
-  int which = (int)(rest % 2);
-  int64_t bt = rest / 2;
+  int which = (int)(rest % nparts) + (2 - nparts);  // 0 = q, 1 = k (k only when nparts == 1)
+  int64_t bt = rest / nparts;
   int64_t t = bt % T;
   typename Elem<DT>::T* base = qkv + bt * (3 * (int64_t)C) + which * C + h * D + 8 * gidx;
   float xv[8], cv[8], sv[8], o[8];
   load8<DT>(base, xv);
   load8<DT>(cos_tab + t * D + 8 * gidx, cv);
   load8<DT>(sin_tab + t * D + 8 * gidx, sv);
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    float xe = xv[2 * p], xo = xv[2 * p + 1];
-    o[2 * p] = round_to<DT>(round_to<DT>(xe * cv[2 * p]) + round_to<DT>(-xo * sv[2 * p]));
-    o[2 * p + 1] = round_to<DT>(round_to<DT>(xo * cv[2 * p + 1]) + round_to<DT>(xe * sv[2 * p + 1]));
-  }
+  rope_rotate8<DT>(xv, cv, sv, o);
   store8<DT>(base, o);
 }
 
-// Token-row variant for D = 64: workgroup bt rotates the 2*H*8 groups of 8
-// elements of token row bt (q heads, then k heads), which share one table
-// row.  Index math is shifts and one compare per group (no 64-bit division
-// per element).
+// Token-row variant for D = 64: a token row has nparts*H*8 groups of 8
+// elements (q heads, then k heads; k heads only when nparts == 1), which
+// share one table row.  A 256-thread workgroup rotates 256 / groups whole
+// rows (one row, looping, when a row has more groups than threads).  Index
+// math is shifts and one compare per group (no 64-bit division per element).
 template <int DT>
-__global__ void __launch_bounds__(256) rope64_row_kernel(typename Elem<DT>::T* qkv, int64_t T, int H,
-                                                         const typename Elem<DT>::T* cos_tab,
-                                                         const typename Elem<DT>::T* sin_tab) {
-  const int64_t bt = blockIdx.x;
+__global__ void __launch_bounds__(256) rope64_row_kernel(typename Elem<DT>::T* qkv, int64_t rows, int64_t T,
+                                                         int H, const typename Elem<DT>::T* cos_tab,
+                                                         const typename Elem<DT>::T* sin_tab, int nparts) {
+  const int groups = nparts * H * 8;
+  const bool wide = groups >= 256;
+  const int rpw = wide ? 1 : 256 / groups;
+  const int sub = wide ? 0 : (int)threadIdx.x / groups;
+  if (sub >= rpw) return;
+  const int64_t bt = (int64_t)blockIdx.x * rpw + sub;
+  if (bt >= rows) return;
   const int64_t t = (int64_t)((uint32_t)bt % (uint32_t)T);  // rows < 2^31 (host check)
   const int C = H * 64;
   typename Elem<DT>::T* row = qkv + bt * (3 * (int64_t)C);
-  const int groups = 2 * H * 8;
-  for (int e = threadIdx.x; e < groups; e += blockDim.x) {
-    const int g8 = e & 7;   // 8-element group within the head
-    const int hw = e >> 3;  // q head hw, or k head hw - H
+  const int hw0 = (2 - nparts) * H;  // k heads only when nparts == 1
+  const int e0 = wide ? (int)threadIdx.x : (int)threadIdx.x - sub * groups;
+  const int step = wide ? (int)blockDim.x : groups;
+  for (int e = e0; e < groups; e += step) {
+    const int g8 = e & 7;           // 8-element group within the head
+    const int hw = hw0 + (e >> 3);  // q head hw, or k head hw - H
     const int off = (hw >= H ? C + (hw - H) * 64 : hw * 64) + 8 * g8;
     float xv[8], cv[8], sv[8], o[8];
     load8<DT>(row + off, xv);
     load8<DT>(cos_tab + t * 64 + 8 * g8, cv);
     load8<DT>(sin_tab + t * 64 + 8 * g8, sv);
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const float xe = xv[2 * p], xo = xv[2 * p + 1];
-      o[2 * p] = round_to<DT>(round_to<DT>(xe * cv[2 * p]) + round_to<DT>(-xo * sv[2 * p]));
-      o[2 * p + 1] = round_to<DT>(round_to<DT>(xo * cv[2 * p + 1]) + round_to<DT>(xe * sv[2 * p + 1]));
-    }
+    rope_rotate8<DT>(xv, cv, sv, o);
     store8<DT>(row + off, o);
   }
 }
@@ -104,7 +103,7 @@ __global__ void __launch_bounds__(256) rope64_row_kernel(typename Elem<DT>::T* q
 template <int DT>
 __global__ void __launch_bounds__(256) rope_kernel(typename Elem<DT>::T* qkv, int64_t n_pairs, int64_t T,
                                                    int H, int D, const typename Elem<DT>::T* cos_tab,
-                                                   const typename Elem<DT>::T* sin_tab) {
+                                                   const typename Elem<DT>::T* sin_tab, int nparts) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n_pairs) return;
   const int half = D / 2;
@@ -113,8 +112,8 @@ __global__ void __launch_bounds__(256) rope_kernel(typename Elem<DT>::T* qkv, in
   int64_t rest = i / half;
   int h = (int)(rest % H);
   rest /= H;
-  int which = (int)(rest % 2);  // 0 = q, 1 = k
-  int64_t bt = rest / 2;
+  int which = (int)(rest % nparts) + (2 - nparts);  // 0 = q, 1 = k (k only when nparts == 1)
+  int64_t bt = rest / nparts;
   int64_t t = bt % T;
   typename Elem<DT>::T* base = qkv + bt * (3 * (int64_t)C) + which * C + h * D + 2 * pair;
   float xe = load_f<DT>(base), xo = load_f<DT>(base + 1);
@@ -162,9 +161,8 @@ extern "C" int pfa_zero_fill(void* ptr, size_t bytes, void* stream) {
   return PFA_OK;
 }
 
-extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D,
-                                   const void* cos_tab, const void* sin_tab, void* stream) {
-  clear_error();
+static int rope_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D, const void* cos_tab,
+                        const void* sin_tab, int nparts, void* stream) {
   PFA_CHECK_ARG(qkv && cos_tab && sin_tab, "pfa_rope_qk_inplace: null pointer");
   PFA_CHECK_ARG(B >= 0 && T >= 0 && H > 0 && D > 0 && D % 2 == 0,
                 "pfa_rope_qk_inplace: bad shape B=%d T=%lld H=%d D=%d", B, (long long)T, H, D);
@@ -174,20 +172,22 @@ extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H
   if (vec && D == 64 && (int64_t)B * T < INT32_MAX && H <= 256) {
     const int64_t rows = (int64_t)B * T;
     if (rows == 0) return PFA_OK;
-    const unsigned threads = (unsigned)(2 * H * 8 < 256 ? 2 * H * 8 : 256);
-    const unsigned nblk = (unsigned)rows;
+    const int groups = nparts * H * 8;
+    const int64_t rpw = groups >= 256 ? 1 : 256 / groups;
+    const unsigned threads = 256;
+    const unsigned nblk = (unsigned)((rows + rpw - 1) / rpw);
     switch (dtype) {
       case PFA_F32:
-        rope64_row_kernel<PFA_F32><<<nblk, threads, 0, s>>>((float*)qkv, T, H, (const float*)cos_tab,
-                                                                      (const float*)sin_tab);
+        rope64_row_kernel<PFA_F32><<<nblk, threads, 0, s>>>((float*)qkv, rows, T, H, (const float*)cos_tab,
+                                                                      (const float*)sin_tab, nparts);
         break;
       case PFA_BF16:
-        rope64_row_kernel<PFA_BF16><<<nblk, threads, 0, s>>>((uint16_t*)qkv, T, H, (const uint16_t*)cos_tab,
-                                                                       (const uint16_t*)sin_tab);
+        rope64_row_kernel<PFA_BF16><<<nblk, threads, 0, s>>>((uint16_t*)qkv, rows, T, H, (const uint16_t*)cos_tab,
+                                                                       (const uint16_t*)sin_tab, nparts);
         break;
       case PFA_F16:
-        rope64_row_kernel<PFA_F16><<<nblk, threads, 0, s>>>((uint16_t*)qkv, T, H, (const uint16_t*)cos_tab,
-                                                                      (const uint16_t*)sin_tab);
+        rope64_row_kernel<PFA_F16><<<nblk, threads, 0, s>>>((uint16_t*)qkv, rows, T, H, (const uint16_t*)cos_tab,
+                                                                      (const uint16_t*)sin_tab, nparts);
         break;
       default:
         set_error("pfa_rope_qk_inplace: unsupported dtype %d", dtype);
@@ -197,21 +197,21 @@ extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H
     return PFA_OK;
   }
   if (vec) {
-    int64_t n_groups = (int64_t)B * T * 2 * H * (D / 8);
+    int64_t n_groups = (int64_t)B * T * nparts * H * (D / 8);
     if (n_groups == 0) return PFA_OK;
     unsigned blocks = (unsigned)((n_groups + 255) / 256);
     switch (dtype) {
       case PFA_F32:
         rope8_kernel<PFA_F32><<<blocks, 256, 0, s>>>((float*)qkv, n_groups, T, H, D, (const float*)cos_tab,
-                                                      (const float*)sin_tab);
+                                                      (const float*)sin_tab, nparts);
         break;
       case PFA_BF16:
         rope8_kernel<PFA_BF16><<<blocks, 256, 0, s>>>((uint16_t*)qkv, n_groups, T, H, D,
-                                                       (const uint16_t*)cos_tab, (const uint16_t*)sin_tab);
+                                                       (const uint16_t*)cos_tab, (const uint16_t*)sin_tab, nparts);
         break;
       case PFA_F16:
         rope8_kernel<PFA_F16><<<blocks, 256, 0, s>>>((uint16_t*)qkv, n_groups, T, H, D,
-                                                      (const uint16_t*)cos_tab, (const uint16_t*)sin_tab);
+                                                      (const uint16_t*)cos_tab, (const uint16_t*)sin_tab, nparts);
         break;
       default:
         set_error("pfa_rope_qk_inplace: unsupported dtype %d", dtype);
@@ -220,21 +220,21 @@ extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H
     PFA_CHECK_LAUNCH("pfa_rope_qk_inplace");
     return PFA_OK;
   }
-  int64_t n_pairs = (int64_t)B * T * 2 * H * (D / 2);
+  int64_t n_pairs = (int64_t)B * T * nparts * H * (D / 2);
   if (n_pairs == 0) return PFA_OK;
   unsigned blocks = (unsigned)((n_pairs + 255) / 256);
   switch (dtype) {
     case PFA_F32:
       rope_kernel<PFA_F32><<<blocks, 256, 0, s>>>((float*)qkv, n_pairs, T, H, D, (const float*)cos_tab,
-                                                   (const float*)sin_tab);
+                                                   (const float*)sin_tab, nparts);
       break;
     case PFA_BF16:
       rope_kernel<PFA_BF16><<<blocks, 256, 0, s>>>((uint16_t*)qkv, n_pairs, T, H, D,
-                                                    (const uint16_t*)cos_tab, (const uint16_t*)sin_tab);
+                                                    (const uint16_t*)cos_tab, (const uint16_t*)sin_tab, nparts);
       break;
     case PFA_F16:
       rope_kernel<PFA_F16><<<blocks, 256, 0, s>>>((uint16_t*)qkv, n_pairs, T, H, D,
-                                                   (const uint16_t*)cos_tab, (const uint16_t*)sin_tab);
+                                                   (const uint16_t*)cos_tab, (const uint16_t*)sin_tab, nparts);
       break;
     default:
       set_error("pfa_rope_qk_inplace: unsupported dtype %d", dtype);
@@ -242,4 +242,16 @@ extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H
   }
   PFA_CHECK_LAUNCH("pfa_rope_qk_inplace");
   return PFA_OK;
+}
+
+extern "C" int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D, const void* cos_tab,
+                                   const void* sin_tab, void* stream) {
+  clear_error();
+  return rope_inplace(qkv, dtype, B, T, H, D, cos_tab, sin_tab, 2, stream);
+}
+
+extern "C" int pfa_rope_k_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D, const void* cos_tab,
+                                  const void* sin_tab, void* stream) {
+  clear_error();
+  return rope_inplace(qkv, dtype, B, T, H, D, cos_tab, sin_tab, 1, stream);
 }

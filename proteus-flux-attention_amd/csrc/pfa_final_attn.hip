@@ -128,8 +128,7 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const uint16_t*
     float tmax = s[gr][0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[gr][i]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = max_over_rows4(tmax);
     const float tm = tmax * sl2;
     if (__ballot(tm > st[gr].m + kRescaleLog2) != 0) {
       const float mn = fmaxf(st[gr].m, tm);

@@ -85,6 +85,167 @@ __device__ __forceinline__ void router_ema_accum(const typename Elem<DT>::T* __r
   }
 }
 
+// Per-token epilogue shared by the router kernels (one lane per token):
+// acc holds the GP gate logits, the GP prototype dot products and the sum of
+// squares of the token row.  Writes the token's outputs and the workgroup's
+// telemetry partials (row `group` of stats) and returns the final gate
+// probabilities in gate.
+template <int DT, int GP, bool PROTO>
+__device__ __forceinline__ void router_epilogue(float (&acc)[2 * GP + 1], int64_t tok, bool live, int64_t group, int G,
+                                                const float* __restrict__ conf_weight,
+                                                const float* __restrict__ usage_bias,
+                                                const int32_t* __restrict__ gate_to_head, int H, int topk,
+                                                float proto_temp, float proto_threshold, float proto_blend,
+                                                float usage_boost, float* __restrict__ gate_probs,
+                                                float* __restrict__ sim_out, float* __restrict__ blend_out,
+                                                float* __restrict__ importance, int32_t* __restrict__ head_idx,
+                                                float* __restrict__ head_score, float* __restrict__ stats,
+                                                float (&gate)[GP]) {
+  constexpr int NV = 2 * GP + 1;
+  const int lane = threadIdx.x & 63;
+  // per-gate inputs loaded unconditionally (padding gates re-read gate G-1
+  // and are never used) so that the loads are issued together
+  float cwv[GP], ubv[GP];
+  int hgv[GP];
+#pragma unroll
+  for (int g = 0; g < GP; ++g) {
+    const int gc = g < G ? g : G - 1;
+    cwv[g] = conf_weight != nullptr ? conf_weight[gc] : 1.f;
+    ubv[g] = usage_bias != nullptr ? usage_bias[gc] : 0.f;
+    hgv[g] = gate_to_head[gc];
+  }
+  float* logit = acc;
+  float* dotp = acc + GP;
+  const float sq = acc[NV - 1];
+
+  // --- SwitchRouter: logits in x dtype, softmax in f32 rounded to x dtype.
+  float lmax = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < GP; ++g)
+    if (g < G) { logit[g] = round_to<DT>(logit[g]); lmax = fmaxf(lmax, logit[g]); }
+  float lsum = 0.f;
+#pragma unroll
+  for (int g = 0; g < GP; ++g) {
+    gate[g] = 0.f;
+    if (g < G) { gate[g] = expf(logit[g] - lmax); lsum = lsum + gate[g]; }
+  }
+#pragma unroll
+  for (int g = 0; g < GP; ++g)
+    if (g < G) gate[g] = round_to<DT>(gate[g] / lsum);
+
+  float sim_max = 0.f, blend_scalar = 0.f;
+  if constexpr (PROTO) {
+    float inv_den = fmaxf(sqrtf(sq), 1e-6f);
+    float sims[GP];
+    sim_max = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) { sims[g] = dotp[g] / inv_den; sim_max = fmaxf(sim_max, sims[g]); }
+    float pp[GP];
+    float smax = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) { pp[g] = sims[g] / proto_temp; smax = fmaxf(smax, pp[g]); }
+    float ssum = 0.f;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) { pp[g] = expf(pp[g] - smax); ssum = ssum + pp[g]; }
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) pp[g] = pp[g] / ssum;
+    float den = fmaxf(1e-6f, 1.0f - proto_threshold);
+    blend_scalar = fminf(fmaxf((sim_max - proto_threshold) / den, 0.f), 1.f);
+    if (conf_weight != nullptr) {
+      float cs = 0.f;
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) { pp[g] = pp[g] * cwv[g]; cs = cs + pp[g]; }
+      cs = fmaxf(cs, 1e-6f);
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) pp[g] = pp[g] / cs;
+    }
+    float blend = proto_blend * blend_scalar;
+    float one_m = 1.0f - blend;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) gate[g] = gate[g] * one_m + pp[g] * blend;
+    if (usage_bias != nullptr && usage_boost > 0.f) {
+      float scale_u = (1.0f - blend_scalar) * usage_boost;
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) gate[g] = gate[g] + ubv[g] * scale_u;
+    }
+    float gs = 0.f;
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) { gate[g] = fmaxf(gate[g], 0.f); gs = gs + gate[g]; }
+    gs = fmaxf(gs, 1e-6f);
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+      if (g < G) gate[g] = gate[g] / gs;
+  }
+
+  float gmax = -INFINITY, ent = 0.f;
+#pragma unroll
+  for (int g = 0; g < GP; ++g)
+    if (g < G) { gmax = fmaxf(gmax, gate[g]); ent = ent + logf(fmaxf(gate[g], 1e-9f)) * gate[g]; }
+  float imp = PROTO ? (gmax * (1.0f - blend_scalar) + sim_max * blend_scalar) : gmax;
+
+  float score_sum = 0.f;
+  if (live) {
+    if (gate_probs) {
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) gate_probs[tok * G + g] = gate[g];
+    }
+    if (sim_out) sim_out[tok] = sim_max;
+    if (blend_out) blend_out[tok] = blend_scalar;
+    importance[tok] = imp;
+
+    // head_probs = gate_probs @ onehot(gate_to_head); top-k (ties -> lower head).
+    float hp[GP];
+#pragma unroll
+    for (int h = 0; h < GP; ++h) hp[h] = 0.f;
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+      if (g < G) {
+        const int hg = hgv[g];
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+          if (h == hg) hp[h] = hp[h] + gate[g];
+      }
+    }
+    uint64_t taken = 0;
+    for (int j = 0; j < topk; ++j) {
+      float bv = 0.f;
+      int bi = -1;
+#pragma unroll
+      for (int h = 0; h < GP; ++h) {
+        if (h < H && !((taken >> h) & 1ull)) {
+          if (bi < 0 || better(hp[h], h, bv, bi)) { bv = hp[h]; bi = h; }
+        }
+      }
+      taken |= 1ull << bi;
+      head_idx[tok * topk + j] = bi;
+      if (head_score) head_score[tok * topk + j] = bv;
+      score_sum += bv;
+    }
+  }
+  if (stats) {
+    // per-workgroup telemetry partials: entropy, sim, blend, #blend>0, top-k score sum
+    float v[5] = {live ? -ent : 0.f, live ? sim_max : 0.f, live ? blend_scalar : 0.f,
+                  (live && blend_scalar > 0.f) ? 1.f : 0.f, score_sum};
+#pragma unroll
+    for (int i = 0; i < 5; ++i)
+      for (int off = 32; off > 0; off >>= 1) v[i] += __shfl_xor(v[i], off, 64);
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 5; ++i) stats[group * 8 + i] = v[i];
+    }
+  }
+}
+
 // Router weights come pre-packed per channel as f32, wpk[c][0..GP) = W[:, c]
 // and wpk[c][GP..2GP) = P[:, c] (GP = gates padded to 8/16/32/64, padding
 // zero).  All lanes of a wave walk the channels in lock step, so the weight
@@ -183,137 +344,10 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
 #pragma unroll
       for (int i = 0; i < NV; ++i) acc[i] = acc[i] + red[((w - 1) * NV + i) * 64 + lane];
   }
-  float* logit = acc;
-  float* dotp = acc + GP;
-  const float sq = acc[NV - 1];
-
-  // --- SwitchRouter: logits in x dtype, softmax in f32 rounded to x dtype.
   float gate[GP];
-  float lmax = -INFINITY;
-#pragma unroll
-  for (int g = 0; g < GP; ++g)
-    if (g < G) { logit[g] = round_to<DT>(logit[g]); lmax = fmaxf(lmax, logit[g]); }
-  float lsum = 0.f;
-#pragma unroll
-  for (int g = 0; g < GP; ++g) {
-    gate[g] = 0.f;
-    if (g < G) { gate[g] = expf(logit[g] - lmax); lsum = lsum + gate[g]; }
-  }
-#pragma unroll
-  for (int g = 0; g < GP; ++g)
-    if (g < G) gate[g] = round_to<DT>(gate[g] / lsum);
-
-  float sim_max = 0.f, blend_scalar = 0.f;
-  if constexpr (PROTO) {
-    float inv_den = fmaxf(sqrtf(sq), 1e-6f);
-    float sims[GP];
-    sim_max = -INFINITY;
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-      if (g < G) { sims[g] = dotp[g] / inv_den; sim_max = fmaxf(sim_max, sims[g]); }
-    float pp[GP];
-    float smax = -INFINITY;
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-      if (g < G) { pp[g] = sims[g] / proto_temp; smax = fmaxf(smax, pp[g]); }
-    float ssum = 0.f;
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-      if (g < G) { pp[g] = expf(pp[g] - smax); ssum = ssum + pp[g]; }
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-      if (g < G) pp[g] = pp[g] / ssum;
-    float den = fmaxf(1e-6f, 1.0f - proto_threshold);
-    blend_scalar = fminf(fmaxf((sim_max - proto_threshold) / den, 0.f), 1.f);
-    if (conf_weight != nullptr) {
-      float cs = 0.f;
-#pragma unroll
-      for (int g = 0; g < GP; ++g)
-        if (g < G) { pp[g] = pp[g] * conf_weight[g]; cs = cs + pp[g]; }
-      cs = fmaxf(cs, 1e-6f);
-#pragma unroll
-      for (int g = 0; g < GP; ++g)
-        if (g < G) pp[g] = pp[g] / cs;
-    }
-    float blend = proto_blend * blend_scalar;
-    float one_m = 1.0f - blend;
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-      if (g < G) gate[g] = gate[g] * one_m + pp[g] * blend;
-    if (usage_bias != nullptr && usage_boost > 0.f) {
-      float scale_u = (1.0f - blend_scalar) * usage_boost;
-#pragma unroll
-      for (int g = 0; g < GP; ++g)
-        if (g < G) gate[g] = gate[g] + usage_bias[g] * scale_u;
-    }
-    float gs = 0.f;
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-      if (g < G) { gate[g] = fmaxf(gate[g], 0.f); gs = gs + gate[g]; }
-    gs = fmaxf(gs, 1e-6f);
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-      if (g < G) gate[g] = gate[g] / gs;
-  }
-
-  float gmax = -INFINITY, ent = 0.f;
-#pragma unroll
-  for (int g = 0; g < GP; ++g)
-    if (g < G) { gmax = fmaxf(gmax, gate[g]); ent = ent + logf(fmaxf(gate[g], 1e-9f)) * gate[g]; }
-  float imp = PROTO ? (gmax * (1.0f - blend_scalar) + sim_max * blend_scalar) : gmax;
-
-  float score_sum = 0.f;
-  if (live) {
-    if (gate_probs) {
-#pragma unroll
-      for (int g = 0; g < GP; ++g)
-        if (g < G) gate_probs[tok * G + g] = gate[g];
-    }
-    if (sim_out) sim_out[tok] = sim_max;
-    if (blend_out) blend_out[tok] = blend_scalar;
-    importance[tok] = imp;
-
-    // head_probs = gate_probs @ onehot(gate_to_head); top-k (ties -> lower head).
-    float hp[GP];
-#pragma unroll
-    for (int h = 0; h < GP; ++h) hp[h] = 0.f;
-#pragma unroll
-    for (int g = 0; g < GP; ++g) {
-      if (g < G) {
-        int hg = gate_to_head[g];
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-          if (h == hg) hp[h] = hp[h] + gate[g];
-      }
-    }
-    uint64_t taken = 0;
-    for (int j = 0; j < topk; ++j) {
-      float bv = 0.f;
-      int bi = -1;
-#pragma unroll
-      for (int h = 0; h < GP; ++h) {
-        if (h < H && !((taken >> h) & 1ull)) {
-          if (bi < 0 || better(hp[h], h, bv, bi)) { bv = hp[h]; bi = h; }
-        }
-      }
-      taken |= 1ull << bi;
-      head_idx[tok * topk + j] = bi;
-      if (head_score) head_score[tok * topk + j] = bv;
-      score_sum += bv;
-    }
-  }
-  if (stats) {
-    // per-workgroup telemetry partials: entropy, sim, blend, #blend>0, top-k score sum
-    float v[5] = {live ? -ent : 0.f, live ? sim_max : 0.f, live ? blend_scalar : 0.f,
-                  (live && blend_scalar > 0.f) ? 1.f : 0.f, score_sum};
-#pragma unroll
-    for (int i = 0; i < 5; ++i)
-      for (int off = 32; off > 0; off >>= 1) v[i] += __shfl_xor(v[i], off, 64);
-    if (lane == 0) {
-#pragma unroll
-      for (int i = 0; i < 5; ++i) stats[(int64_t)blockIdx.x * 8 + i] = v[i];
-    }
-  }
+  router_epilogue<DT, GP, PROTO>(acc, tok, live, blockIdx.x, G, conf_weight, usage_bias, gate_to_head, H, topk,
+                                 proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim_out,
+                                 blend_out, importance, head_idx, head_score, stats, gate);
   if (ema_part != nullptr) {
 #pragma unroll
     for (int g = 0; g < GP; ++g) gl[lane * GP + g] = (live && g < G) ? gate[g] : 0.f;
@@ -325,6 +359,243 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
       part[(int64_t)lane * (C + 1) + C] = cs;
     }
     router_ema_accum<DT, GP>(x, (int64_t)blockIdx.x * kRouterTok, n_tok, C, G, cbeg, cw, gl, part);
+  }
+}
+
+// ---------------------------------------------------------------------
+// bf16 router on MFMA (8 gates)
+// ---------------------------------------------------------------------
+// Each wave owns one group of 64 tokens (4 tiles of 16) and computes, with
+// v_mfma_f32_16x16x32_bf16, the 16 x 64 product of an operand table with the
+// tokens' rows: table rows 0-7 are the gate weights (already rounded to
+// bf16) and rows 8-15 the normalised prototypes.  An f32 prototype entry is
+// split into three bf16 parts, p = hi + mid + lo (hi = bf16(p), mid =
+// bf16(p - hi), lo = bf16(p - hi - mid); every difference is exact in f32 and
+// the three parts carry p's 24-bit significand), so with bf16 token values
+// every product is exact in f32 and the prototype dots are f32 dots
+// accumulated in a different order.  Table A0 = [W | hi], table A1 =
+// [mid | lo], each multiplied into its own accumulator.
+//
+// Channel order: lane (c16, g) of tile n holds the 32 consecutive channels
+// 128q + 32g .. +31 of token 16n + c16 (four 16-byte loads, a whole 128-byte
+// line per four lanes); half h of them feeds k-step s = 4q + h, so the table
+// fragment of lane (r, g) for k-step s holds channels
+// ch(s, g, j) = 128*(s/4) + 32g + 8*(s%4) + j.  The sum over channels does
+// not depend on the order, only the two operands must agree.
+constexpr int kRmWaves = 4;
+constexpr int kRmEpW = 33;  // staged floats per token: 8 logits, 8 hi, 8 mid, 8 lo, sum of squares
+
+__host__ __device__ constexpr int rm_region0(int C) {
+  return (64 * C > kRmWaves * 64 * kRmEpW * 4) ? 64 * C : kRmWaves * 64 * kRmEpW * 4;
+}
+
+// Prototype EMA statistics of one 64-token group, one wave: lane owns the
+// eight channels cb + 8*lane .. +7 (one 16-byte load per token), gate rows
+// from LDS; every sum runs in token order.
+template <int GP>
+__device__ __forceinline__ void ema_accum_rows_bf16(const uint16_t* __restrict__ x, int64_t tok0, int nt, int C,
+                                                    int G, const float* gl, float* __restrict__ part) {
+  const int lane = threadIdx.x & 63;
+  for (int cb = 0; cb < C; cb += 512) {
+    const int c = cb + 8 * lane;
+    const bool has = c < C;
+    float a[8][GP];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int g = 0; g < GP; ++g) a[j][g] = 0.f;
+    for (int u0 = 0; u0 < nt; u0 += 16) {
+      uint4 xv[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        xv[k] = (has && u0 + k < nt) ? *reinterpret_cast<const uint4*>(x + (tok0 + u0 + k) * C + c)
+                                     : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float4* gr = reinterpret_cast<const float4*>(gl + (u0 + k) * GP);
+        float gv[GP];
+#pragma unroll
+        for (int q = 0; q < GP / 4; ++q) {
+          const float4 t = gr[q];
+          gv[4 * q] = t.x; gv[4 * q + 1] = t.y; gv[4 * q + 2] = t.z; gv[4 * q + 3] = t.w;
+        }
+        const uint32_t w[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x0 = __uint_as_float(w[i] << 16), x1 = __uint_as_float(w[i] & 0xffff0000u);
+#pragma unroll
+          for (int g = 0; g < GP; ++g) {
+            a[2 * i][g] = __builtin_fmaf(gv[g], x0, a[2 * i][g]);
+            a[2 * i + 1][g] = __builtin_fmaf(gv[g], x1, a[2 * i + 1][g]);
+          }
+        }
+      }
+    }
+    if (has) {
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) part[(int64_t)g * (C + 1) + c + j] = a[j][g];
+        }
+    }
+  }
+}
+
+template <bool PROTO>
+__global__ void __launch_bounds__(64 * kRmWaves)
+router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, const float* __restrict__ wpk,
+                   const float* __restrict__ conf_weight, const float* __restrict__ usage_bias,
+                   const int32_t* __restrict__ gate_to_head, int H, int topk, float proto_temp,
+                   float proto_threshold, float proto_blend, float usage_boost, float* __restrict__ gate_probs,
+                   float* __restrict__ sim_out, float* __restrict__ blend_out, float* __restrict__ importance,
+                   int32_t* __restrict__ head_idx, float* __restrict__ head_score, float* __restrict__ stats,
+                   float* __restrict__ ema_part) {
+  constexpr int GP = 8;
+  typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+  typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+  extern __shared__ __align__(16) unsigned char rm_lds[];
+  uint16_t* tab = reinterpret_cast<uint16_t*>(rm_lds);  // [C/32][2][64 lanes][8]
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int c16 = lane & 15, g4 = lane >> 4;
+
+  // operand table from the packed f32 rows (wpk[c][0..8) = W, wpk[c][8..16) = P)
+  for (int ch = tid; ch < C; ch += 64 * kRmWaves) {
+    const float4* src = reinterpret_cast<const float4*>(wpk + (int64_t)ch * 2 * GP);
+    const float4 w0 = src[0], w1 = src[1];
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float pv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if constexpr (PROTO) {
+      const float4 p0 = src[2], p1 = src[3];
+      pv[0] = p0.x; pv[1] = p0.y; pv[2] = p0.z; pv[3] = p0.w;
+      pv[4] = p1.x; pv[5] = p1.y; pv[6] = p1.z; pv[7] = p1.w;
+    }
+    const int st = 4 * (ch >> 7) + ((ch >> 3) & 3), g = (ch >> 5) & 3, j = ch & 7;
+    uint16_t* t0 = tab + ((int64_t)(2 * st) * 64 + 16 * g) * 8 + j;
+    uint16_t* t1 = t0 + 64 * 8;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const uint16_t hi = f32_to_bf16(pv[r]);
+      const float r1 = pv[r] - bf16_to_f32(hi);
+      const uint16_t mid = f32_to_bf16(r1);
+      const uint16_t lo = f32_to_bf16(r1 - bf16_to_f32(mid));
+      t0[r * 8] = f32_to_bf16(wv[r]);
+      t0[(8 + r) * 8] = hi;
+      t1[r * 8] = mid;
+      t1[(8 + r) * 8] = lo;
+    }
+  }
+  __syncthreads();
+
+  const int64_t group = (int64_t)blockIdx.x * kRmWaves + wid;
+  const int64_t n_groups = (n_tok + kRouterTok - 1) / kRouterTok;
+  const int64_t tok0 = group * kRouterTok;
+  const uint16_t* xr[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    int64_t t = tok0 + 16 * n + c16;
+    t = t < n_tok ? t : n_tok - 1;
+    xr[n] = x + t * C + 32 * g4;
+  }
+  f32x4 acc0[4], acc1[4];
+  float ss[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    acc0[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc1[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    ss[n] = 0.f;
+  }
+  const int nq = C / 128;
+  uint4 cur[4][4], nxt[4][4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n)
+#pragma unroll
+    for (int h = 0; h < 4; ++h) cur[n][h] = reinterpret_cast<const uint4*>(xr[n])[h];
+  for (int q = 0; q < nq; ++q) {
+    const bool more = q + 1 < nq;
+    if (more) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) nxt[n][h] = reinterpret_cast<const uint4*>(xr[n] + 128 * (q + 1))[h];
+    }
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const uint16_t* tf = tab + ((int64_t)(2 * (4 * q + h)) * 64 + lane) * 8;
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(tf);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(tf + 64 * 8);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        bf16x8 b;
+        __builtin_memcpy(&b, &cur[n][h], 16);
+        acc0[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, acc0[n], 0, 0, 0);
+        if constexpr (PROTO) acc1[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, acc1[n], 0, 0, 0);
+        const uint32_t w[4] = {cur[n][h].x, cur[n][h].y, cur[n][h].z, cur[n][h].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x0 = __uint_as_float(w[i] << 16), x1 = __uint_as_float(w[i] & 0xffff0000u);
+          ss[n] = __builtin_fmaf(x0, x0, ss[n]);
+          ss[n] = __builtin_fmaf(x1, x1, ss[n]);
+        }
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) cur[n][h] = nxt[n][h];
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    ss[n] += __shfl_xor(ss[n], 16, 64);
+    ss[n] += __shfl_xor(ss[n], 32, 64);
+  }
+  // token-per-lane staging (reuses the table space once every wave is done)
+  __syncthreads();
+  float* ep = reinterpret_cast<float*>(rm_lds) + wid * 64 * kRmEpW;
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    float* e = ep + (16 * n + c16) * kRmEpW;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      e[4 * g4 + i] = acc0[n][i];
+      e[16 + 4 * g4 + i] = PROTO ? acc1[n][i] : 0.f;
+    }
+    if (g4 == 0) e[32] = ss[n];
+  }
+  __syncthreads();
+  float acc[2 * GP + 1];
+  {
+    const float* e = ep + lane * kRmEpW;
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+      acc[g] = e[g];
+      acc[GP + g] = (e[24 + g] + e[16 + g]) + e[8 + g];
+    }
+    acc[2 * GP] = e[32];
+  }
+  const int64_t tok = tok0 + lane;
+  const bool live = tok < n_tok;
+  float gate[GP];
+  router_epilogue<PFA_BF16, GP, PROTO>(acc, tok, live, group, G, conf_weight, usage_bias, gate_to_head, H, topk,
+                                       proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim_out,
+                                       blend_out, importance, head_idx, head_score,
+                                       group < n_groups ? stats : nullptr, gate);
+  if (ema_part != nullptr) {
+    float* gl = reinterpret_cast<float*>(rm_lds + rm_region0(C)) + wid * 64 * GP;
+#pragma unroll
+    for (int g = 0; g < GP; ++g) gl[lane * GP + g] = (live && g < G) ? gate[g] : 0.f;
+    __syncthreads();
+    if (group < n_groups) {
+      float* part = ema_part + group * G * (C + 1);
+      if (lane < G) {
+        float cs = 0.f;  // column C: sum of gate g over the group's tokens, in token order
+        for (int u = 0; u < 64; ++u) cs += gl[u * GP + lane];
+        part[(int64_t)lane * (C + 1) + C] = cs;
+      }
+      ema_accum_rows_bf16<GP>(x, tok0, (int)min<int64_t>(64, n_tok - tok0), C, G, gl, part);
+    }
   }
 }
 
@@ -525,17 +796,35 @@ router_prepare_kernel(const typename Elem<WDT>::T* __restrict__ w, const typenam
   __shared__ float wsum[kPrepThreads / 64][GP];
   __shared__ float denom[GP];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (wv == kPrepThreads / 64 - 1) {
+    // confidence weights and usage softmax, one gate per lane of the last
+    // wave (independent loads issued together, wave reductions); the other
+    // waves start on the prototype norms meanwhile
+    const bool has = lane < G;
+    if (conf != nullptr && conf_w != nullptr && has)
+      conf_w[lane] = round_to<PDT>(load_f<PDT>(conf + lane) + 1e-6f);
+    if (usage != nullptr && usage_b != nullptr) {
+      const float v = has ? -round_to<PDT>(load_f<PDT>(usage + lane) + 1e-6f) : -INFINITY;
+      float m = v;
+      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      const float e = has ? expf(v - m) : 0.f;
+      float sum = e;
+      for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+      if (has) usage_b[lane] = round_to<PDT>(e / sum);
+    }
+  }
   if (protos != nullptr) {
     float acc[GP];
 #pragma unroll
     for (int g = 0; g < GP; ++g) acc[g] = 0.f;
     for (int c = tid; c < C; c += kPrepThreads) {
+      // unconditional loads (padding gates re-read gate G-1 and are masked
+      // afterwards) so that all GP loads are in flight together
+      float v[GP];
 #pragma unroll
-      for (int g = 0; g < GP; ++g)
-        if (g < G) {
-          const float v = load_f<PDT>(protos + (int64_t)g * C + c);
-          acc[g] = __builtin_fmaf(v, v, acc[g]);
-        }
+      for (int g = 0; g < GP; ++g) v[g] = load_f<PDT>(protos + (int64_t)(g < G ? g : G - 1) * C + c);
+#pragma unroll
+      for (int g = 0; g < GP; ++g) acc[g] = g < G ? __builtin_fmaf(v[g], v[g], acc[g]) : 0.f;
     }
 #pragma unroll
     for (int g = 0; g < GP; ++g) {
@@ -554,31 +843,19 @@ router_prepare_kernel(const typename Elem<WDT>::T* __restrict__ w, const typenam
   for (int c = tid; c < C; c += kPrepThreads) {
     float row[2 * GP];
 #pragma unroll
+    for (int g = 0; g < GP; ++g) row[g] = load_f<WDT>(w + (int64_t)(g < G ? g : G - 1) * C + c);
+    if (protos != nullptr) {
+#pragma unroll
+      for (int g = 0; g < GP; ++g) row[GP + g] = load_f<PDT>(protos + (int64_t)(g < G ? g : G - 1) * C + c);
+    }
+#pragma unroll
     for (int g = 0; g < GP; ++g) {
-      row[g] = g < G ? round_to<XDT>(load_f<WDT>(w + (int64_t)g * C + c)) : 0.f;
-      row[GP + g] = (protos != nullptr && g < G) ? load_f<PDT>(protos + (int64_t)g * C + c) / denom[g] : 0.f;
+      row[g] = g < G ? round_to<XDT>(row[g]) : 0.f;
+      row[GP + g] = (protos != nullptr && g < G) ? row[GP + g] / denom[g] : 0.f;
     }
     float4* dst = reinterpret_cast<float4*>(wpk + (int64_t)c * 2 * GP);
 #pragma unroll
     for (int k = 0; k < GP / 2; ++k) dst[k] = make_float4(row[4 * k], row[4 * k + 1], row[4 * k + 2], row[4 * k + 3]);
-  }
-  if (tid == 0) {
-    if (conf != nullptr && conf_w != nullptr)
-      for (int g = 0; g < G; ++g) conf_w[g] = round_to<PDT>(load_f<PDT>(conf + g) + 1e-6f);
-    if (usage != nullptr && usage_b != nullptr) {
-      float v[GP];
-      float m = -INFINITY;
-      for (int g = 0; g < G; ++g) {
-        v[g] = -round_to<PDT>(load_f<PDT>(usage + g) + 1e-6f);
-        m = fmaxf(m, v[g]);
-      }
-      float s = 0.f;
-      for (int g = 0; g < G; ++g) {
-        v[g] = expf(v[g] - m);
-        s += v[g];
-      }
-      for (int g = 0; g < G; ++g) usage_b[g] = round_to<PDT>(v[g] / s);
-    }
   }
 }
 
@@ -589,6 +866,16 @@ static void launch_router_gp(const void* x, int64_t n_tok, int C, int G, const f
                              float* stats, float* ema, hipStream_t s) {
   using ET = typename Elem<DT>::T;
   unsigned blocks = (unsigned)((n_tok + kRouterTok - 1) / kRouterTok);
+  if constexpr (DT == PFA_BF16 && GP == 8) {
+    if (C % 128 == 0 && C <= 768) {
+      const unsigned mb = (blocks + kRmWaves - 1) / kRmWaves;
+      const size_t lds = (size_t)rm_region0(C) + (size_t)kRmWaves * 64 * GP * sizeof(float);
+      router_mfma_kernel<PROTO><<<mb, 64 * kRmWaves, lds, s>>>((const uint16_t*)x, n_tok, C, G, wpk, cw, ub, g2h, H,
+                                                               topk, temp, thr, pb, boost, gp, sim, bl, imp, hi, hs,
+                                                               stats, ema);
+      return;
+    }
+  }
   if (GP <= 16 && C % 128 == 0)
     router_kernel<DT, GP, PROTO, 4><<<blocks, 256, 0, s>>>((const ET*)x, n_tok, C, G, wpk, cw, ub, g2h, H, topk,
                                                            temp, thr, pb, boost, gp, sim, bl, imp, hi, hs, stats,

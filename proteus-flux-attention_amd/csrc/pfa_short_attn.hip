@@ -26,11 +26,12 @@
 // "segment" of rows streams those keys once, masks per (row, key), merges the
 // anchor partial and writes the normalised bf16 row into [b][h][t][:].
 //
-// Tiles: 4 waves x 16 query rows, 64 keys per tile staged in LDS (K row-
-// major, V transposed, rows padded to 72 elements: conflict-free 16-lane
-// reads).  Each wave computes S^T = K Q^T and O^T += V^T P^T with
-// v_mfma_f32_16x16x32_bf16, so a lane owns one query row throughout: the
-// softmax max/sum need only two cross-lane shuffles.
+// Tiles: 4 waves x 16 query rows, 64 keys per tile staged in LDS (K and V
+// row-major, rows padded to 72 elements: conflict-free 16-lane K reads; the
+// V^T operand comes from the LDS transpose read).  Each wave computes
+// S^T = K Q^T and O^T += V^T P^T with v_mfma_f32_16x16x32_bf16, so a lane
+// owns one query row throughout: the softmax max needs two cross-lane
+// permutes per tile.
 #include "pfa_common.h"
 
 namespace pfa {
@@ -63,6 +64,8 @@ struct ShortArgs {
   const int32_t* summary;
   float* part;           // (N, kPartW)
   int32_t* lengths;      // (N) or null
+  const uint16_t* rcos;  // (T, 64) RoPE tables applied to q rows on load, or null
+  const uint16_t* rsin;
   float scale_log2;
 };
 
@@ -92,8 +95,8 @@ __device__ __forceinline__ bool zero_anchor(int64_t t, int s, int slots) {
 __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); }
 
 // A 64-key tile is staged by 256 threads: thread tid fetches a quarter of
-// key row tid/4 (16 elements of K and of V) into registers; storing writes K
-// row-major and V transposed into LDS.  Fetch and store are split so the
+// key row tid/4 (16 elements of K and of V) into registers; storing writes
+// both row-major into LDS.  Fetch and store are split so the
 // next tile's loads are in flight while the current tile is computed.
 struct TileRegs {
   uint4 k0, k1, v0, v1;
@@ -112,24 +115,29 @@ __device__ __forceinline__ TileRegs fetch_tile(const uint16_t* __restrict__ kb, 
   return r;
 }
 
-__device__ __forceinline__ void store_tile(const TileRegs& r, uint16_t* Ks, uint16_t* Vt) {
+__device__ __forceinline__ void store_tile(const TileRegs& r, uint16_t* Ks, uint16_t* Vs) {
   const int tid = threadIdx.x;
   const int j = tid >> 2, qd = tid & 3;
   uint4* kd = reinterpret_cast<uint4*>(Ks + j * kLd + 16 * qd);
   kd[0] = r.k0;
   kd[1] = r.k1;
-  const uint32_t vw[8] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    Vt[(16 * qd + 2 * e) * kLd + j] = (uint16_t)(vw[e] & 0xffffu);
-    Vt[(16 * qd + 2 * e + 1) * kLd + j] = (uint16_t)(vw[e] >> 16);
-  }
+  uint4* vd = reinterpret_cast<uint4*>(Vs + j * kLd + 16 * qd);
+  vd[0] = r.v0;
+  vd[1] = r.v1;
 }
 
-__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
-                                          int64_t ks_t, int64_t vs_t, int64_t key, uint16_t* Ks, uint16_t* Vt) {
-  store_tile(fetch_tile(kb, vb, ks_t, vs_t, key), Ks, Vt);
+// Four bf16 of one head dim from four consecutive key rows of the row-major
+// V tile, by the gfx950 LDS transpose read: within each 16-lane row of the
+// wave, lane 4a+b receives element b of the 8-byte chunks addressed by lanes
+// a, a+4, a+8, a+12.  Lane m of the row addresses key row0 + m/4, dims
+// d0 + 4*(m%4) .. +3, so lane i = 4a+b gets V[row0 + k][d0 + i], k = 0..3.
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4_t;
+__device__ __forceinline__ i16x4_t v_tr4(const uint16_t* Vs, int row0, int d0) {
+  const int m = threadIdx.x & 15;
+  const uint16_t* p = Vs + (row0 + (m >> 2)) * kLd + d0 + 4 * (m & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p));
 }
+
 
 // One 64-key tile for the 16 query rows of this wave.  With MASKED,
 // mask(kl) decides whether tile key kl (0..63) is a candidate of this lane's
@@ -138,7 +146,7 @@ __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ kb, const
 // directly (arguments are <= 0; -inf gives 0), P is rounded to bf16 with
 // v_cvt_pk_bf16_f32 (round to nearest even).
 template <bool MASKED, bool COUNT, class MaskF>
-__device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_t* Ks, const uint16_t* Vt,
+__device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_t* Ks, const uint16_t* Vs,
                                           float scale_log2, MaskF mask, QState& st) {
   const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
   float s[4][4];
@@ -164,8 +172,7 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
     }
   }
   if constexpr (!MASKED && COUNT) st.cnt += 16;
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  tmax = max_over_rows4(tmax);
   // Lazy rescaling: the accumulator is rescaled only on tiles where some row
   // of the wave sees a new maximum (a wave-uniform branch); st.m stays the
   // exact running max (log2 units), so every P <= 1 and the arithmetic is
@@ -207,12 +214,13 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
     __builtin_memcpy(&pb, pv, 16);
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const uint16_t* vr = Vt + (16 * db + r16) * kLd + 32 * kc + 4 * g;
-      uint2 lo8 = *reinterpret_cast<const uint2*>(vr);
-      uint2 hi8 = *reinterpret_cast<const uint2*>(vr + 16);
-      uint32_t w4[4] = {lo8.x, lo8.y, hi8.x, hi8.y};
+      // A operand V^T: lane (dim 16db + r16, g) holds the keys of pb's
+      // slots, 32kc + 4g + (0..3) and 32kc + 16 + 4g + (0..3)
+      const i16x4_t lo = v_tr4(Vs, 32 * kc + 4 * g, 16 * db);
+      const i16x4_t hi = v_tr4(Vs, 32 * kc + 16 + 4 * g, 16 * db);
       bf16x8_t va;
-      __builtin_memcpy(&va, w4, 16);
+      __builtin_memcpy(&va, &lo, 8);
+      __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
       st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, st.acc[db], 0, 0, 0);
     }
   }
@@ -225,6 +233,35 @@ __device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[2]) 
     uint4 w = *reinterpret_cast<const uint4*>(qrow + 32 * dc + 8 * g);
     __builtin_memcpy(&qf[dc], &w, 16);
   }
+}
+
+// q row with RoPE applied on load: the lane's two 8-dim chunks are whole
+// (even, odd) pairs, rotated with the same arithmetic as the RoPE kernels
+// (rope_rotate8), so the fragments hold exactly the bits a rotated q tensor
+// would hold.
+__device__ __forceinline__ void load_q_rope(const uint16_t* qrow, const uint16_t* crow, const uint16_t* srow,
+                                            bf16x8_t (&qf)[2]) {
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int dc = 0; dc < 2; ++dc) {
+    const int d0 = 32 * dc + 8 * g;
+    float xv[8], cv[8], sv[8], o[8];
+    load8<PFA_BF16>(qrow + d0, xv);
+    load8<PFA_BF16>(crow + d0, cv);
+    load8<PFA_BF16>(srow + d0, sv);
+    rope_rotate8<PFA_BF16>(xv, cv, sv, o);
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f32_to_bf16(o[2 * i]) | ((uint32_t)f32_to_bf16(o[2 * i + 1]) << 16);
+    __builtin_memcpy(&qf[dc], w, 16);
+  }
+}
+
+__device__ __forceinline__ void load_q_row(const ShortArgs& a, const uint16_t* qb, int64_t t, bf16x8_t (&qf)[2]) {
+  if (a.rcos != nullptr)
+    load_q_rope(qb + t * a.q.s_t, a.rcos + t * 64, a.rsin + t * 64, qf);
+  else
+    load_q(qb + t * a.q.s_t, qf);
 }
 
 __device__ __forceinline__ void init_state(QState& st) {
@@ -247,7 +284,7 @@ __device__ __forceinline__ int64_t xcd_block(int64_t P, int64_t nblk) {
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) short_anchor_kernel(ShortArgs a,
                                                                                                      int ccap) {
   __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
-  __shared__ __align__(16) uint16_t Vt[2][64 * kLd];
+  __shared__ __align__(16) uint16_t Vs[2][kTile * kLd];
   // active rows of the class: row index and class position M (M < ccap <=
   // kMaxClassRows), sized to the class length (dynamic LDS)
   extern __shared__ int32_t cls_dyn[];
@@ -322,17 +359,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
     const int64_t mlo = Mf - a.slots > 0 ? Mf - a.slots : 0;
     const int64_t tl = c + (int64_t)s * Ml;
     const int64_t mhi = Ml - ((tl - win_lo(tl, a.local_w)) / s + 1);
-    bf16x8_t qf[2];
-    load_q(qb + tq * a.q.s_t, qf);
-    QState st;
-    init_state(st);
     // pipelined over the class's key tiles: tile i+1 is fetched while tile i
-    // is computed
+    // is computed; the first tile's loads are issued before the q row's
     const int ntile = mhi >= mlo ? (int)((mhi - mlo) / kTile + 1) : 0;
     const int64_t jrow = tid >> 2;
-    if (ntile > 0) {
-      store_tile(fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min(mlo + jrow, mhi)), Ks[0], Vt[0]);
-    }
+    TileRegs first;
+    if (ntile > 0) first = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min(mlo + jrow, mhi));
+    bf16x8_t qf[2];
+    load_q_row(a, qb, tq, qf);
+    QState st;
+    init_state(st);
+    if (ntile > 0) store_tile(first, Ks[0], Vs[0]);
     __syncthreads();
     for (int i = 0; i < ntile; ++i) {
       const int cur = i & 1;
@@ -346,9 +383,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
         const int m = m0 + kl;
         return m <= (int)mhi && m >= lo_q && m <= hi_q;
       };
-      if (full) tile_step<false, false>(qf, Ks[cur], Vt[cur], a.scale_log2, cls_mask, st);
-      else if (!empty) tile_step<true, false>(qf, Ks[cur], Vt[cur], a.scale_log2, cls_mask, st);
-      if (more) store_tile(nxt, Ks[cur ^ 1], Vt[cur ^ 1]);
+      if (full) tile_step<false, false>(qf, Ks[cur], Vs[cur], a.scale_log2, cls_mask, st);
+      else if (!empty) tile_step<true, false>(qf, Ks[cur], Vs[cur], a.scale_log2, cls_mask, st);
+      if (more) store_tile(nxt, Ks[cur ^ 1], Vs[cur ^ 1]);
       __syncthreads();
     }
     float lt = st.l;
@@ -372,7 +409,7 @@ template <bool COUNT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
 short_main_kernel(ShortArgs a, int use_part, int pcap) {
   __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
-  __shared__ __align__(16) uint16_t Vt[2][64 * kLd];
+  __shared__ __align__(16) uint16_t Vs[2][kTile * kLd];
   __shared__ int32_t r_t[kRows];
   __shared__ int32_t r_p[kRows];
   __shared__ int32_t seg_begin[kRows + 1];
@@ -426,6 +463,9 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
     const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
     const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
+    // the segment's first key tile (window keys from lo_first) is fetched
+    // now, so its loads overlap the prototype list and the q row
+    const TileRegs first = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, min(lo_first + (tid >> 2), t_last));
 
     // prototype key list: the prefix set of t_first below lo_last (set table
     // row of t_first's block -- any order, INT32_MAX-padded -- then the
@@ -494,8 +534,17 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const bool anch_on = sa > 0 && sl > 0;
     const int tmod = sa > 0 ? tq % sa : 0;
     const int64_t alo = (int64_t)tq - (int64_t)sa * sl;  // strided anchors lie in [alo, tq)
+    // one pipelined pass over the window tiles [lo_first, t_last] and the
+    // prototype tiles: tile i+1 is fetched while tile i is computed
+    const int nw = (t_last - lo_first) / kTile + 1;
+    const int ntile = nw + (plen + kTile - 1) / kTile;
+    const int jrow = tid >> 2;
+    auto key_of = [&](int i) -> int64_t {
+      if (i < nw) return min(lo_first + kTile * i + jrow, t_last);
+      return pk[min((i - nw) * kTile + jrow, plen - 1)];
+    };
     bf16x8_t qf[2];
-    load_q(qb + (int64_t)tq * a.q.s_t, qf);
+    load_q_row(a, qb, tq, qf);
     QState st;
     init_state(st);
 
@@ -507,16 +556,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const int w_tlo = wave_rows ? r_t[fr] : 0, w_thi = wave_rows ? r_t[lr] : -1;
     const int w_llo = (int)win_lo(w_tlo, w), w_lhi = (int)win_lo(w_thi < 0 ? 0 : w_thi, w);
 
-    // one pipelined pass over the window tiles [lo_first, t_last] and the
-    // prototype tiles: tile i+1 is fetched while tile i is computed
-    const int nw = (t_last - lo_first) / kTile + 1;
-    const int ntile = nw + (plen + kTile - 1) / kTile;
-    const int jrow = tid >> 2;
-    auto key_of = [&](int i) -> int64_t {
-      if (i < nw) return min(lo_first + kTile * i + jrow, t_last);
-      return pk[min((i - nw) * kTile + jrow, plen - 1)];
-    };
-    store_tile(fetch_tile(kb, vb, a.k.s_t, a.v.s_t, key_of(0)), Ks[0], Vt[0]);
+    store_tile(first, Ks[0], Vs[0]);
     __syncthreads();
     for (int i = 0; i < ntile; ++i) {
       const int cur = i & 1;
@@ -531,11 +571,11 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
         const int wa = max(loq - k0, 0);
         const int wn = qv ? max(min(tq - k0, kTile - 1) - wa + 1, 0) : 0;
         auto win_mask = [&](int kl) { return (unsigned)(kl - wa) < (unsigned)wn; };
-        if (full) tile_step<false, COUNT>(qf, Ks[cur], Vt[cur], a.scale_log2, win_mask, st);
-        else if (!empty) tile_step<true, COUNT>(qf, Ks[cur], Vt[cur], a.scale_log2, win_mask, st);
+        if (full) tile_step<false, COUNT>(qf, Ks[cur], Vs[cur], a.scale_log2, win_mask, st);
+        else if (!empty) tile_step<true, COUNT>(qf, Ks[cur], Vs[cur], a.scale_log2, win_mask, st);
       } else if (wave_rows) {
         const int j0 = (i - nw) * kTile;
-        tile_step<true, COUNT>(qf, Ks[cur], Vt[cur], a.scale_log2,
+        tile_step<true, COUNT>(qf, Ks[cur], Vs[cur], a.scale_log2,
                   [&](int kl) {
                     const int j = j0 + kl;
                     if (!qv || j >= plen) return false;
@@ -547,7 +587,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
                   },
                   st);
       }
-      if (more) store_tile(nxt, Ks[cur ^ 1], Vt[cur ^ 1]);
+      if (more) store_tile(nxt, Ks[cur ^ 1], Vs[cur ^ 1]);
       __syncthreads();
     }
 
@@ -612,13 +652,14 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
                                       const int32_t* head_map, int64_t N, int P_cap, const int32_t* summary,
                                       const int32_t* row_of, int local_w, int anchor_stride, int anchor_slots,
                                       const int32_t* proto_blocks, int proto_k, const int32_t* proto_evict,
-                                      float scale, float* partials, int32_t* lengths,
-                                      void* stream) {
+                                      float scale, float* partials, int32_t* lengths, const void* q_rope_cos,
+                                      const void* q_rope_sin, int passes, void* stream) {
   clear_error();
   PFA_CHECK_ARG(dtype == PFA_BF16 && D == 64, "pfa_shortlist_attn_fwd: bf16 and D=64 only (got dtype %d D %d)", dtype,
                 D);
   PFA_CHECK_ARG(H > 0 && T > 0 && T < INT32_MAX && N >= 0 && P_cap > 0 && local_w >= 1,
                 "pfa_shortlist_attn_fwd: bad sizes");
+  PFA_CHECK_ARG(passes >= 1 && passes <= 3, "pfa_shortlist_attn_fwd: passes must be 1, 2 or 3 (got %d)", passes);
   if (N == 0) return PFA_OK;
   PFA_CHECK_ARG(q.ptr && k.ptr && v.ptr && out.ptr && token_idx && row_head && summary,
                 "pfa_shortlist_attn_fwd: null pointer");
@@ -632,20 +673,26 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
     return ((uintptr_t)x.ptr % 16) == 0 && x.s_b % 8 == 0 && x.s_h % 8 == 0 && x.s_t % 8 == 0;
   };
   PFA_CHECK_ARG(al(q) && al(k) && al(v) && al(out), "pfa_shortlist_attn_fwd: tensors must be 16-byte aligned");
+  PFA_CHECK_ARG((q_rope_cos == nullptr) == (q_rope_sin == nullptr),
+                "pfa_shortlist_attn_fwd: q_rope_cos and q_rope_sin go together");
+  PFA_CHECK_ARG(q_rope_cos == nullptr || (((uintptr_t)q_rope_cos | (uintptr_t)q_rope_sin) & 15) == 0,
+                "pfa_shortlist_attn_fwd: RoPE tables must be 16-byte aligned");
   ShortArgs a;
   a.q = q; a.k = k; a.v = v; a.out = out;
   a.H = H; a.T = T; a.token_idx = token_idx; a.row_head = row_head; a.head_map = head_map; a.N = N;
   a.local_w = local_w; a.stride = anchor_stride; a.slots = anchor_slots;
   a.blk = proto_blocks; a.K = proto_k; a.nblk = (T + 63) / 64; a.evict = proto_evict;
   a.row_of = row_of; a.summary = summary; a.part = partials; a.lengths = lengths;
+  a.rcos = (const uint16_t*)q_rope_cos; a.rsin = (const uint16_t*)q_rope_sin;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = as_stream(stream);
-  if (anchors) {
+  if (anchors && (passes & 1)) {
     dim3 grid((unsigned)((int64_t)anchor_stride < T ? (int64_t)anchor_stride : T), (unsigned)P_cap);
     const int ccap = (int)((T - 1) / anchor_stride + 1);
     short_anchor_kernel<<<grid, 256, (size_t)ccap * 6 + 16, s>>>(a, ccap);
     PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
   }
+  if (!(passes & 2)) return PFA_OK;
   int64_t blocks = (N + kRows - 1) / kRows;
   blocks = (blocks + 7) / 8 * 8;
   PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_shortlist_attn_fwd: too many rows");

@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "pfa_shortlist_attn_fwd",
     "pfa_head_max_token",
     "pfa_rope_qk_inplace",
+    "pfa_rope_k_inplace",
     "pfa_zero_fill",
     "pfa_chunk_topk_workspace_size",
     "pfa_chunk_topk",
@@ -108,9 +109,11 @@ _SIGNATURES = {
                              _i64, _vp, _i64, _vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp], _i32),
     "pfa_shortlist_attn_part_floats": ([], _i32),
     "pfa_shortlist_attn_fwd": ([Tensor4, Tensor4, Tensor4, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp, _i64,
-                                _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp], _i32),
+                                _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp, _i32,
+                                _vp], _i32),
     "pfa_head_max_token": ([_vp, _vp, _i32, _vp, _vp], _i32),
     "pfa_rope_qk_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
+    "pfa_rope_k_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
     "pfa_zero_fill": ([_vp, _sz, _vp], _i32),
     "pfa_chunk_topk_workspace_size": ([_i64, _i32, ctypes.POINTER(_sz)], _i32),
     "pfa_chunk_topk": ([_vp, _vp, _i64, _i32, _f32, _i64, _i32, _vp, _vp, _vp, _vp, _sz, _vp], _i32),

@@ -363,6 +363,11 @@ def _attn_launch(
     _hip.check(rc, "pfa_sparse_attn_fwd")
 
 
+def shortlist_partials(N: int, device: torch.device) -> torch.Tensor:
+    """f32 (N, pfa_shortlist_attn_part_floats()) anchor-pass partials."""
+    return torch.empty(N, int(_hip.lib().pfa_shortlist_attn_part_floats()), dtype=torch.float32, device=device)
+
+
 def _shortlist_attn_structured(
     q4: "_hip.Tensor4",
     k4: "_hip.Tensor4",
@@ -384,30 +389,44 @@ def _shortlist_attn_structured(
     scale: float,
     device: torch.device,
     want_lengths: bool = True,
+    q_rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+    passes: int = 3,
+    part: Optional[torch.Tensor] = None,
 ) -> Optional[torch.Tensor]:
     """Module-path shortlist attention without materialised candidates
     (bf16, D=64); the prototype sets come as _proto_prefix_blocks tables of
     the T-token scores.  Returns each row's candidate count (int32, (N,)),
-    or None when want_lengths is False (the kernel then skips the counting)."""
+    or None when want_lengths is False (the kernel then skips the counting).
+    q_rope = (cos, sin) bf16 (T, 64) tables: q is still unrotated and its
+    rows are rotated as the kernel loads them.  passes = 1 runs only the
+    anchor pass and 2 only the main pass (the caller orders them and passes
+    the same `part`, from shortlist_partials, to both); 3 runs both."""
 
     lib = _hip.lib()
     N = int(token_idx.numel())
-    lengths = torch.empty(N, dtype=torch.int32, device=device) if want_lengths else None
+    lengths = torch.empty(N, dtype=torch.int32, device=device) if (want_lengths and passes & 2) else None
     anchors = stride > 0 and slots > 0
-    part = None
-    if anchors:
-        part = torch.empty(N, int(lib.pfa_shortlist_attn_part_floats()), dtype=torch.float32, device=device)
+    if anchors and part is None:
+        if passes != 3:
+            raise ValueError("split anchor/main passes need a shared partials buffer")
+        part = shortlist_partials(N, device)
     K = 0
     if blocks is not None:
         K = int(blocks.size(2))
         if evict is None or int(evict.size(1)) != int(T) or int(blocks.size(1)) != (int(T) + 63) // 64:
             raise ValueError("prototype block tables must cover the T tokens of the sequence")
+    rc_cos = rc_sin = None
+    if q_rope is not None:
+        rc_cos, rc_sin = q_rope
+        if (rc_cos.dtype != torch.bfloat16 or rc_sin.dtype != torch.bfloat16 or tuple(rc_cos.shape) != (int(T), 64)
+                or tuple(rc_sin.shape) != (int(T), 64) or not rc_cos.is_contiguous() or not rc_sin.is_contiguous()):
+            raise ValueError("q_rope tables must be contiguous bf16 (T, 64)")
     with _hip.TIMER.timed("shortlist_attn_fwd"):
         rc = lib.pfa_shortlist_attn_fwd(
             q4, k4, v4, out4, _hip.PFA_BF16, int(H), int(T), int(D), _hip.ptr(token_idx), _hip.ptr(row_head),
             _hip.ptr(head_map), N, int(head_map.numel()), _hip.ptr(summary), _hip.ptr(row_of), int(local_w),
             int(stride), int(slots), _hip.ptr(blocks), K, _hip.ptr(evict), float(scale), _hip.ptr(part),
-            _hip.ptr(lengths), _hip.stream_ptr(device))
+            _hip.ptr(lengths), _hip.ptr(rc_cos), _hip.ptr(rc_sin), int(passes), _hip.stream_ptr(device))
     _hip.check(rc, "pfa_shortlist_attn_fwd")
     return lengths
 

@@ -452,6 +452,9 @@ class AdaptiveSparseAttention(nn.Module):
         # per-row candidate counts of the structured shortlist path are
         # telemetry: computed (inside the attention kernel) only on request
         self.record_shortlist_lengths = False
+        # structured shortlist path: rotate q rows inside the attention kernel
+        # (only k is rotated in the QKV buffer); False rotates q in the buffer
+        self.fuse_q_rope = True
 
     # ------------------------------------------------------------------
     # RoPE tables (aspa.py:576-604)
@@ -896,17 +899,25 @@ class AdaptiveSparseAttention(nn.Module):
                          (None, None, None), qkv.device)
 
     def _project_qkv(self, x: torch.Tensor) -> torch.Tensor:
-        B, T, C = x.shape
         qkv = self.qkv(x).contiguous()  # (B, T, 3C) = (B, T, 3, H, D)
-        if self.use_rope:
-            cos, sin = self._rope_factors(T, x.device, qkv.dtype)
-            cos, sin = cos.contiguous(), sin.contiguous()
-            with _hip.TIMER.timed("rope_qk"):
-                rc = _hip.lib().pfa_rope_qk_inplace(_hip.ptr(qkv), _hip.dtype_tag(qkv.dtype), B, T, self.h_total,
-                                                 self.d_head, _hip.ptr(cos), _hip.ptr(sin),
-                                                 _hip.stream_ptr(x.device))
-            _hip.check(rc, "pfa_rope_qk_inplace")
+        self._rope_inplace(qkv, rotate_q=True)
         return qkv
+
+    def _rope_inplace(self, qkv: torch.Tensor, rotate_q: bool):
+        """RoPE of the QKV buffer (aspa.py:606-618).  With rotate_q=False only
+        k is rotated and the (cos, sin) tables are returned for a kernel that
+        rotates q rows as it loads them (pfa_shortlist_attn_fwd)."""
+        if not self.use_rope:
+            return None
+        B, T = qkv.shape[0], qkv.shape[1]
+        cos, sin = self._rope_factors(T, qkv.device, qkv.dtype)
+        cos, sin = cos.contiguous(), sin.contiguous()
+        fn = _hip.lib().pfa_rope_qk_inplace if rotate_q else _hip.lib().pfa_rope_k_inplace
+        with _hip.TIMER.timed("rope_qk"):
+            rc = fn(_hip.ptr(qkv), _hip.dtype_tag(qkv.dtype), B, T, self.h_total, self.d_head, _hip.ptr(cos),
+                    _hip.ptr(sin), _hip.stream_ptr(qkv.device))
+        _hip.check(rc, "pfa_rope_qk_inplace" if rotate_q else "pfa_rope_k_inplace")
+        return None if rotate_q else (cos, sin)
 
     def _forward_dense_fastpath(self, x: torch.Tensor) -> torch.Tensor:
         """Dense causal attention for short sequences (aspa.py:1365-1440)."""
@@ -1115,6 +1126,16 @@ class AdaptiveSparseAttention(nn.Module):
             finish("dense_fastpath")
             return y
 
+        # Two streams: the QKV projection, RoPE, the output zero fill and the
+        # anchor pass run on a forked stream while the router, packing, the
+        # prototype EMA and the prototype prefix tables run on the calling
+        # stream; the main attention pass joins them.
+        main_s = torch.cuda.current_stream(device)
+        fork_s = self._fork_stream(device)
+        fork_s.wait_stream(main_s)
+        with torch.cuda.stream(fork_s):
+            qkv = self.qkv(x).contiguous()  # (B, T, 3C) = (B, T, 3, H, D)
+
         alpha = self._compute_cvt_alpha(T)
         self._current_alpha = alpha
         if self.token_sparse:
@@ -1151,6 +1172,10 @@ class AdaptiveSparseAttention(nn.Module):
             hsc = hsc_all[:, :topk].contiguous()
         gate_probs = gate.view(B, T, self.attn_gates)
         self._last_gate_probs = gate_probs
+        # the prototype EMA (aspa.py:692-718) reads only this forward's router
+        # outputs and is read only by the next forward's router: it runs here,
+        # overlapping the projection on the forked stream
+        self._update_routing_prototypes(x, gate_probs)
         if sim is not None:
             self._last_token_similarity = sim.view(B, T)
             self._last_token_blend = blend.view(B, T)
@@ -1214,8 +1239,20 @@ class AdaptiveSparseAttention(nn.Module):
                 dense_reason = None
             force_dense = False
 
-        qkv = self._project_qkv(x)
-        attn = torch.zeros(B, T, C, dtype=qkv.dtype, device=device)
+        shortlist_path = not force_dense and not (P == 0 or N == 0 or (not need_summary and B * T == 0))
+        plan = self._shortlist_plan(B, T, alpha, qkv.dtype) if shortlist_path else None
+        structured = plan is not None and plan["structured"]
+        with torch.cuda.stream(fork_s):
+            # the structured kernel rotates q rows as it loads them: only k is
+            # rotated here
+            q_rope = self._rope_inplace(qkv, rotate_q=not (structured and self.fuse_q_rope))
+            attn = torch.zeros(B, T, C, dtype=qkv.dtype, device=device)
+        if not capture:
+            # the forked stream's tensors are used (and freed) on this stream
+            qkv.record_stream(main_s)
+            attn.record_stream(main_s)
+        if not structured:
+            main_s.wait_stream(fork_s)
         D = self.d_head
         mode_label = "sparse"
         if force_dense:
@@ -1253,7 +1290,8 @@ class AdaptiveSparseAttention(nn.Module):
             tok = token_idx[:N]
             rh = row_head[:N]
             heads = active_heads[:P] if P >= 0 else active_heads
-            self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets, alpha, row_of, summary)
+            self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets, alpha, row_of, summary,
+                                       plan=plan, q_rope=q_rope, streams=(main_s, fork_s))
             backend_info = self._last_shortlist_backend_info or get_last_backend_info()
             state = {
                 "mode": mode_label, "backend": str(backend_info.get("name", "shortlist")),
@@ -1281,12 +1319,10 @@ class AdaptiveSparseAttention(nn.Module):
                       dense_reason, B, T, active_heads, row_offsets, summary)
         label = f"cvt(alpha={alpha:.2f})::{mode_label}"
         if capture:
-            self._update_routing_prototypes(x, gate_probs)
             return attn, stats_args, label
         y = self.dropout(self.proj(attn))
 
         self._finish_stats(*stats_args)
-        self._update_routing_prototypes(x, gate_probs)
         finish(label)
         if self.linear_mem_budget_mb and device.type == "cuda":
             allocated = torch.cuda.memory_allocated(device) / (1024 * 1024)
@@ -1296,17 +1332,10 @@ class AdaptiveSparseAttention(nn.Module):
                 self.adjust_linear_L_scale(self.linear_latency_growth)
         return y
 
-    def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha, row_of,
-                              summary) -> None:
-        """Candidate attention (aspa.py:1175-1310).
-
-        When no row can be truncated to L, bf16 with D=64 and no int8 path,
-        the candidate sets are used through their structure (window, strided
-        anchors, prototype prefix sets) by pfa_shortlist_attn_fwd; otherwise
-        the candidates are materialised (pfa_shortlist_build) and attended by
-        pfa_sparse_attn_fwd.  Both give the reference's candidate sets."""
-        H, D = self.h_total, self.d_head
-        device = qkv.device
+    def _shortlist_plan(self, B: int, T: int, alpha: float, dtype: torch.dtype) -> Dict[str, Any]:
+        """Shortlist sizes of this forward (aspa.py:1175-1210) and whether the
+        structured kernel serves it (bf16, D=64, no int8, no row truncated)."""
+        D = self.d_head
         runtime = self._prepare_linear_runtime(T, B, alpha)
         L = int(runtime["effective_L"])
         stride = int(runtime["anchor_stride"])
@@ -1321,18 +1350,70 @@ class AdaptiveSparseAttention(nn.Module):
         anchors = stride > 0 and slots > 0
         w_eff = max(1, local_w)
         bound = w_eff + ((min(slots, (T - 1) // stride) + 1) if anchors else 0) + K
-        structured = (qkv.dtype == torch.bfloat16 and D == 64 and not use_quant and bound <= L and K <= 1024
+        structured = (dtype == torch.bfloat16 and D == 64 and not use_quant and bound <= L and K <= 1024
                       and (not anchors or (T - 1) // stride + 1 <= 4096) and not _hip.env_flag("PFA_FORCE_GENERIC"))
+        return {"L": L, "stride": stride, "local_w": local_w, "slots": slots, "K": K, "use_quant": use_quant,
+                "w_eff": w_eff, "structured": structured}
+
+    def _fork_stream(self, device: torch.device) -> torch.cuda.Stream:
+        """The forward's second stream on `device` (default priority), created
+        once per device."""
+        streams = self.__dict__.setdefault("_fork_streams", {})
+        key = (device.type, device.index)
+        st = streams.get(key)
+        if st is None:
+            st = torch.cuda.Stream(device=device)
+            streams[key] = st
+        return st
+
+    def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha, row_of,
+                              summary, plan: Optional[Dict[str, Any]] = None, q_rope=None, streams=None) -> None:
+        """Candidate attention (aspa.py:1175-1310).
+
+        When no row can be truncated to L, bf16 with D=64 and no int8 path,
+        the candidate sets are used through their structure (window, strided
+        anchors, prototype prefix sets) by pfa_shortlist_attn_fwd; otherwise
+        the candidates are materialised (pfa_shortlist_build) and attended by
+        pfa_sparse_attn_fwd.  Both give the reference's candidate sets.
+
+        streams = (main, fork): qkv and attn come from work queued on the
+        fork stream; the structured path queues its anchor pass there too
+        (after the packing on main) while main builds the prototype tables,
+        then main waits for the fork stream before the main pass.  The other
+        paths are entered with the fork stream already joined."""
+        H, D = self.h_total, self.d_head
+        device = qkv.device
+        if plan is None:
+            plan = self._shortlist_plan(B, T, alpha, qkv.dtype)
+        L, stride, local_w, slots, K = plan["L"], plan["stride"], plan["local_w"], plan["slots"], plan["K"]
+        use_quant, w_eff, structured = plan["use_quant"], plan["w_eff"], plan["structured"]
+        if q_rope is not None and not structured:
+            raise RuntimeError("q rows left unrotated for a path that does not rotate them")
         q5 = qkv.view(B, T, 3, H, D)
         if structured:
+            t4 = (_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
+                  _hip.tensor4(q5[:, :, 2], H, "bthd"), _hip.tensor4(attn.view(B, T, H, D), H, "bthd"))
+            args = (H, T, D, token_idx, row_head, heads, summary, row_of, w_eff, stride, slots)
+            scale = 1.0 / math.sqrt(D)
+            part = None
+            if stride > 0 and slots > 0:
+                part = _sa.shortlist_partials(int(token_idx.numel()), device)
+                if streams is not None:
+                    main_s, fork_s = streams
+                    # anchor pass on the fork stream, after the packing
+                    fork_s.wait_stream(main_s)
+                    with torch.cuda.stream(fork_s):
+                        _sa._shortlist_attn_structured(*t4, *args, None, None, scale, device, want_lengths=False,
+                                                       q_rope=q_rope, passes=1, part=part)
             blocks = evict = None
             if K > 0:
                 blocks, evict = _sa._proto_prefix_blocks(self._last_token_similarity, K)
+            if streams is not None:
+                streams[0].wait_stream(streams[1])
+            passes = 2 if (part is not None and streams is not None) else 3
             lens = _sa._shortlist_attn_structured(
-                _hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
-                _hip.tensor4(q5[:, :, 2], H, "bthd"), _hip.tensor4(attn.view(B, T, H, D), H, "bthd"), H, T, D,
-                token_idx, row_head, heads, summary, row_of, w_eff, stride, slots, blocks, evict,
-                1.0 / math.sqrt(D), device, want_lengths=bool(self.record_shortlist_lengths))
+                *t4, *args, blocks, evict, scale, device, want_lengths=bool(self.record_shortlist_lengths),
+                q_rope=q_rope, passes=passes, part=part)
             self._last_shortlist_lengths = lens
             _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
                             quantized=False, candidates=True, structured=True)
