@@ -88,6 +88,13 @@ __device__ __forceinline__ void store_f(typename Elem<DT>::T* p, float f) {
   else if constexpr (DT == PFA_F16) *p = f32_to_f16(f);
 }
 
+// Kernels on the forward's critical chain (router, packing, prototype
+// tables) run beside the projection GEMM and the anchor pass, which are
+// queued on another stream and fill the CUs; they raise their waves' issue
+// priority (s_setprio: instruction arbitration within a SIMD only, no effect
+// on dispatch order, memory or results).
+#define PFA_CRITICAL_CHAIN_PRIORITY() __builtin_amdgcn_s_setprio(2)
+
 // Maximum over the four lanes l, l^16, l^32, l^48 of a wave64 (the four
 // 16-lane rows), with the gfx950 row-swap permutes (VALU, no LDS round
 // trip): permlane32_swap pairs each lane with l^32 and permlane16_swap with

@@ -263,6 +263,7 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
               float* __restrict__ gate_probs, float* __restrict__ sim_out, float* __restrict__ blend_out,
               float* __restrict__ importance, int32_t* __restrict__ head_idx, float* __restrict__ head_score,
               float* __restrict__ stats, float* __restrict__ ema_part) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   constexpr int NV = 2 * GP + 1;  // logits, proto dots, sum of squares
   constexpr int WS = 2 * GP;  // row stride of the packed table (prototype columns unread without PROTO)
   __shared__ float red[(NW > 1) ? (NW - 1) * 64 * NV : 1];
@@ -451,6 +452,7 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
                    float* __restrict__ sim_out, float* __restrict__ blend_out, float* __restrict__ importance,
                    int32_t* __restrict__ head_idx, float* __restrict__ head_score, float* __restrict__ stats,
                    float* __restrict__ ema_part) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   constexpr int GP = 8;
   typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
   typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
@@ -790,6 +792,7 @@ router_prepare_kernel(const typename Elem<WDT>::T* __restrict__ w, const typenam
                       const typename Elem<PDT>::T* __restrict__ conf, const typename Elem<PDT>::T* __restrict__ usage,
                       int G, int C, float* __restrict__ wpk, float* __restrict__ conf_w,
                       float* __restrict__ usage_b) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   // one pass: each thread owns channels c = tid + k*kPrepThreads; the G
   // prototype norms are reduced once for all gates, then each thread writes
   // its channels' 2*GP-float rows

@@ -127,6 +127,7 @@ __global__ void __launch_bounds__(kPackThreads)
 pack_count_routed(const int32_t* __restrict__ head_idx, int topk, const uint8_t* __restrict__ token_mask, int H,
                   int64_t T, int nblk, uint8_t* __restrict__ mask_out, int32_t* __restrict__ blockcounts,
                   int32_t* __restrict__ row_of) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   __shared__ int red[16];
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh % H;
@@ -167,16 +168,23 @@ __global__ void __launch_bounds__(1024)
 pack_scan_kernel(int32_t* __restrict__ blockcounts, int BH, int nblk, int compact, int32_t* __restrict__ totals,
                  int32_t* __restrict__ compact_id, int32_t* __restrict__ active_heads,
                  int32_t* __restrict__ row_offsets, int32_t* __restrict__ summary) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   __shared__ int wave_tot[16];
   __shared__ int s_carry_p, s_carry_n, s_max;
   if (threadIdx.x == 0) { s_carry_p = 0; s_carry_n = 0; s_max = 0; }
-  for (int bh = threadIdx.x; bh < BH; bh += blockDim.x) {
-    int64_t tot = 0;
-    for (int j = 0; j < nblk; ++j) tot += blockcounts[(int64_t)bh * nblk + j];
-    totals[bh] = (int32_t)tot;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // per-row totals: one wave per row, 64 tile counts per step
+  for (int bh = wid; bh < BH; bh += nw) {
+    int tot = 0;
+    for (int j0 = 0; j0 < nblk; j0 += 64) {
+      const int j = j0 + lane;
+      int c = j < nblk ? blockcounts[(int64_t)bh * nblk + j] : 0;
+      for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+      tot += c;
+    }
+    if (lane == 0) totals[bh] = tot;
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
   for (int base = 0; base < BH; base += blockDim.x) {
     int bh = base + threadIdx.x;
     int tot = (bh < BH) ? totals[bh] : 0;
@@ -221,15 +229,22 @@ pack_scan_kernel(int32_t* __restrict__ blockcounts, int BH, int nblk, int compac
     summary[3] = 0;
   }
   __syncthreads();
-  // per-tile bases
-  for (int bh = threadIdx.x; bh < BH; bh += blockDim.x) {
-    int id = compact_id[bh];
+  // per-tile bases: one wave per row, an exclusive scan of 64 tile counts
+  // per step
+  for (int bh = wid; bh < BH; bh += nw) {
+    const int id = compact_id[bh];
     if (id < 0) continue;
     int run = row_offsets[id];
-    for (int j = 0; j < nblk; ++j) {
-      int c = blockcounts[(int64_t)bh * nblk + j];
-      blockcounts[(int64_t)bh * nblk + j] = run;
-      run += c;
+    for (int j0 = 0; j0 < nblk; j0 += 64) {
+      const int j = j0 + lane;
+      const int c = j < nblk ? blockcounts[(int64_t)bh * nblk + j] : 0;
+      int v = c;
+      for (int off = 1; off < 64; off <<= 1) {
+        const int n = __shfl_up(v, off, 64);
+        if (lane >= off) v += n;
+      }
+      if (j < nblk) blockcounts[(int64_t)bh * nblk + j] = run + v - c;
+      run += __shfl(v, 63, 64);
     }
   }
 }
@@ -238,6 +253,7 @@ __global__ void __launch_bounds__(kPackThreads)
 pack_fill_kernel(const uint8_t* __restrict__ mask, int64_t T, int nblk, const int32_t* __restrict__ bases,
                  const int32_t* __restrict__ compact_id, int32_t* __restrict__ token_idx,
                  int32_t* __restrict__ row_head, int32_t* __restrict__ row_of) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   __shared__ int wave_tot[4];
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int id = compact_id[bh];

@@ -111,6 +111,7 @@ __global__ void __launch_bounds__(64)
 prefix_block_sort(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int K,
                   float* __restrict__ oval, int32_t* __restrict__ oidx, int32_t* __restrict__ olen,
                   int32_t* __restrict__ evict) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   const int j = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   int64_t t = (int64_t)j * kBlk + lane;
   if (t < T) evict[(int64_t)b * T + t] = INT32_MAX;
@@ -150,6 +151,7 @@ __global__ void __launch_bounds__(256)
 prefix_sb_local(int nb, int sbs, int K, int preload, const float* __restrict__ bval,
                 const int32_t* __restrict__ bidx, const int32_t* __restrict__ blen, float* __restrict__ qval,
                 int32_t* __restrict__ qidx, int32_t* __restrict__ qlen) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   extern __shared__ char smem[];
   float* cv0 = (float*)smem;
   int32_t* ci0 = (int32_t*)(cv0 + K);
@@ -214,65 +216,122 @@ prefix_sb_local(int nb, int sbs, int K, int preload, const float* __restrict__ b
   }
 }
 
-// One round of a log-depth (Hillis-Steele) inclusive scan over superblock
-// totals: out[s] = top-K(in[s] U in[s-d]) for s >= d, else in[s].  Rows are
-// (nsb+1)-strided with row s+1 holding superblock s (row 0 stays empty, so
-// that the walk reads row s as "everything before superblock s").  With
-// `from_q` the input is the superblock totals themselves: the local prefix
-// of each superblock's last block.  One workgroup per (superblock, batch);
-// both lists are staged in LDS and merged by co-rank.
+// One round of a log-depth radix-R (Hillis-Steele) inclusive scan over
+// superblock totals: out[s] = top-K(in[s] U in[s-d] U ... U in[s-(R-1)d])
+// over the terms with a non-negative index (d = R^round, so after round r
+// row s covers superblocks s-R^(r+1)+1 .. s).  Rows are (nsb+1)-strided with
+// row s+1 holding superblock s (row 0 stays empty, so that the walk reads
+// row s as "everything before superblock s").  With `from_q` the input is
+// the superblock totals themselves: the local prefix of each superblock's
+// last block.  One workgroup per (superblock, batch): the (up to R <= 8)
+// lists are staged in LDS together and reduced by a tree of pairwise
+// co-rank merges (log2 R levels, the pairs of a level merged side by side,
+// the last level written straight to the output row).  Top-K under the
+// strict order `better` of distinct positions does not depend on the merge
+// order.
 __global__ void __launch_bounds__(256)
-prefix_scan_round(int nb, int sbs, int nsb, int K, int d, int from_q, const float* __restrict__ qval,
+prefix_scan_round(int nb, int sbs, int nsb, int K, int d, int radix, int from_q, const float* __restrict__ qval,
                   const int32_t* __restrict__ qidx, const int32_t* __restrict__ qlen,
                   const float* __restrict__ ival, const int32_t* __restrict__ iidx, const int32_t* __restrict__ ilen,
                   float* __restrict__ oval, int32_t* __restrict__ oidx, int32_t* __restrict__ olen) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   extern __shared__ char smem[];
-  float* av = (float*)smem;
-  int32_t* ai = (int32_t*)(av + K);
-  float* cv = (float*)(ai + K);
-  int32_t* ci = (int32_t*)(cv + K);
+  // entry arrays: radix input lists, then level-1 outputs (radix/2 lists),
+  // then level-2 outputs (radix/4 lists); list i of a region at i*K
+  float* ev = (float*)smem;
+  const int cap_e = (radix + (radix > 2 ? radix / 2 : 0) + (radix > 4 ? radix / 4 : 0)) * K;
+  int32_t* ei = (int32_t*)(ev + cap_e);
+  __shared__ int s_off[8], s_len[8];
   const int s = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int64_t rb = (int64_t)b * (nsb + 1);
-  auto src = [&](int ss, const float*& v, const int32_t*& ix, int& n) {
-    if (from_q) {
-      const int64_t last = (int64_t)b * nb + min(nb, (ss + 1) * sbs) - 1;
-      v = qval + last * K;
-      ix = qidx + last * K;
-      n = qlen[last];
-    } else {
-      v = ival + (rb + ss + 1) * K;
-      ix = iidx + (rb + ss + 1) * K;
-      n = ilen[rb + ss + 1];
-    }
+  // input row of superblock ss (entries at row * K) and its length
+  auto row_of_sb = [&](int ss) -> int64_t {
+    return from_q ? (int64_t)b * nb + min(nb, (ss + 1) * sbs) - 1 : rb + ss + 1;
   };
-  const float* v0;
-  const int32_t* i0;
-  int n0;
-  src(s, v0, i0, n0);
+  const float* inv = from_q ? qval : ival;
+  const int32_t* ini = from_q ? qidx : iidx;
+  const int32_t* inl = from_q ? qlen : ilen;
   float* ov = oval + (rb + s + 1) * K;
   int32_t* oi = oidx + (rb + s + 1) * K;
   if (s == 0 && tid == 0) olen[rb] = 0;
-  if (s < d) {
-    for (int p = tid; p < n0; p += 256) { ov[p] = v0[p]; oi[p] = i0[p]; }
+  const int nl = min(radix, s / d + 1);  // terms s, s-d, ... that exist
+  // all lengths in one round of loads, then every entry in one flat loop
+  if (tid < nl) {
+    s_off[tid] = tid * K;
+    s_len[tid] = inl[row_of_sb(s - tid * d)];
+  }
+  __syncthreads();
+  if (nl == 1) {
+    const int64_t r0 = row_of_sb(s);
+    const int n0 = s_len[0];
+    for (int p = tid; p < n0; p += 256) { ov[p] = inv[r0 * K + p]; oi[p] = ini[r0 * K + p]; }
     if (tid == 0) olen[rb + s + 1] = n0;
     return;
   }
-  const float* v1;
-  const int32_t* i1;
-  int n1;
-  src(s - d, v1, i1, n1);
-  for (int p = tid; p < n0; p += 256) { av[p] = v0[p]; ai[p] = i0[p]; }
-  for (int p = tid; p < n1; p += 256) { cv[p] = v1[p]; ci[p] = i1[p]; }
-  __syncthreads();
-  const int m = min(K, n0 + n1);
-  for (int p = tid; p < m; p += 256) {
-    float vv;
-    int32_t ii;
-    merge_at(p, av, ai, n0, cv, ci, n1, vv, ii);
-    ov[p] = vv;
-    oi[p] = ii;
+  for (int e = tid; e < nl * K; e += 256) {
+    const int k = e / K, p = e - k * K;
+    if (p < s_len[k]) {
+      const int64_t r = row_of_sb(s - k * d);
+      ev[e] = inv[r * K + p];
+      ei[e] = ini[r * K + p];
+    }
   }
-  if (tid == 0) olen[rb + s + 1] = m;
+  __syncthreads();
+  int n = nl;
+  int region = radix * K;  // where level 1 writes
+  for (int level = 0; n > 1; ++level) {
+    const int np = n >> 1;
+    const bool last = n == 2;
+    const int tpp = 256 / np;  // threads per pair (np <= 4)
+    const int pr = tid / tpp, pt = tid % tpp;
+    int m = 0;
+    if (pr < np) {
+      const int oa = s_off[2 * pr], na = s_len[2 * pr];
+      const int oc = s_off[2 * pr + 1], nc = s_len[2 * pr + 1];
+      m = min(K, na + nc);
+      const int od = region + pr * K;
+      for (int p = pt; p < m; p += tpp) {
+        float vv;
+        int32_t ii;
+        merge_at(p, ev + oa, ei + oa, na, ev + oc, ei + oc, nc, vv, ii);
+        if (last) {
+          ov[p] = vv;
+          oi[p] = ii;
+        } else {
+          ev[od + p] = vv;
+          ei[od + p] = ii;
+        }
+      }
+    }
+    __syncthreads();
+    if (last) {
+      if (tid == 0) olen[rb + s + 1] = m;
+      break;
+    }
+    // pair pr becomes list pr; an odd last list is carried as it is (the
+    // descriptors are read before any is rewritten)
+    int new_off = 0, new_len = 0, carry_off = 0, carry_len = 0;
+    if (tid < np) {
+      new_off = region + tid * K;
+      new_len = min(K, s_len[2 * tid] + s_len[2 * tid + 1]);
+    }
+    if (tid == 0 && (n & 1)) {
+      carry_off = s_off[n - 1];
+      carry_len = s_len[n - 1];
+    }
+    __syncthreads();
+    if (tid < np) {
+      s_off[tid] = new_off;
+      s_len[tid] = new_len;
+    }
+    if (tid == 0 && (n & 1)) {
+      s_off[np] = carry_off;
+      s_len[np] = carry_len;
+    }
+    __syncthreads();
+    region += np * K;
+    n = np + (n & 1);
+  }
 }
 
 // One workgroup (256 threads) per (block j, batch b).  LDS: the entering set
@@ -285,6 +344,7 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
                   int cap, const float* __restrict__ qval, const int32_t* __restrict__ qidx,
                   const int32_t* __restrict__ qlen, const float* __restrict__ rval, const int32_t* __restrict__ ridx,
                   const int32_t* __restrict__ rlen, int32_t* __restrict__ blk_out, int32_t* __restrict__ evict) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
   extern __shared__ char smem[];
   float* v = (float*)smem;
   int32_t* ix = (int32_t*)(v + cap);
@@ -303,13 +363,13 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
   const int j = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int s = j / sbs, k = j % sbs;
   const int64_t rrow = (int64_t)b * (nsb + 1) + s;  // row s: top-K of superblocks 0..s-1
+  const int64_t qrow = (int64_t)b * nb + j - 1;      // block j-1's local prefix (k > 0)
+  // both lengths in one round of loads, then the entries of both rows
   const int na = rlen[rrow];
-  for (int p = tid; p < na; p += 256) { sav[p] = rval[rrow * K + p]; sai[p] = ridx[rrow * K + p]; }
-  int nq = 0;
-  if (k > 0) {
-    const int64_t qrow = (int64_t)b * nb + j - 1;
-    nq = qlen[qrow];
-    for (int p = tid; p < nq; p += 256) { sqv[p] = qval[qrow * K + p]; sqi[p] = qidx[qrow * K + p]; }
+  const int nq = k > 0 ? qlen[qrow] : 0;
+  for (int p = tid; p < K; p += 256) {
+    if (p < na) { sav[p] = rval[rrow * K + p]; sai[p] = ridx[rrow * K + p]; }
+    if (p < nq) { sqv[p] = qval[qrow * K + p]; sqi[p] = qidx[qrow * K + p]; }
   }
   const int64_t t0 = (int64_t)j * kBlk;
   const int nB = (int)min<int64_t>(kBlk, T - t0);
@@ -715,6 +775,15 @@ using namespace pfa;
 static constexpr int kPrefixMaxK = 2048;
 static constexpr size_t kPrefixLds = 60 * 1024;  // dynamic LDS budget per workgroup
 
+// Radix of the superblock scan: as many lists as fit the LDS budget (R
+// inputs plus the tree's intermediate lists, 8 bytes per entry), at most 8.
+static int prefix_round_entries(int radix) { return radix + (radix > 2 ? radix / 2 : 0) + (radix > 4 ? radix / 4 : 0); }
+static int prefix_radix(int K) {
+  for (int r = 8; r > 2; r >>= 1)
+    if ((size_t)prefix_round_entries(r) * K * 8 <= kPrefixLds) return r;
+  return 2;
+}
+
 static int prefix_cap(int K) {
   int cap = 64;
   while (cap < K) cap <<= 1;
@@ -748,10 +817,11 @@ static int prefix_blocks(const float* scores, int B, int64_t T, int64_t stride, 
   PFA_CHECK_LAUNCH("pfa_proto_prefix/local");
   // log-depth inclusive scan of the superblock totals (ping-pong between
   // the two R buffers; the last round lands in the buffer the walk reads)
+  const int radix = prefix_radix(K);
   int rounds = 0;
-  while ((1ll << rounds) < nsb) ++rounds;
+  for (int64_t span = 1; span < nsb; span *= radix) ++rounds;
   if (rounds == 0) rounds = 1;
-  const size_t lds_round = (size_t)K * 16;
+  const size_t lds_round = (size_t)prefix_round_entries(radix) * K * 8;
   const float* fin_v = nullptr;
   const int32_t* fin_i = nullptr;
   const int32_t* fin_l = nullptr;
@@ -763,8 +833,10 @@ static int prefix_blocks(const float* scores, int B, int64_t T, int64_t stride, 
     const float* iv = to_primary ? w.r2val : w.rval;
     const int32_t* ii = to_primary ? w.r2idx : w.ridx;
     const int32_t* il = to_primary ? w.r2len : w.rlen;
+    int d = 1;
+    for (int q = 0; q < r; ++q) d *= radix;
     prefix_scan_round<<<dim3((unsigned)nsb, (unsigned)B), 256, lds_round, s>>>(
-        (int)nb, (int)sbs, (int)nsb, K, 1 << r, r == 0 ? 1 : 0, w.qval, w.qidx, w.qlen, iv, ii, il, ov, oi, ol);
+        (int)nb, (int)sbs, (int)nsb, K, d, radix, r == 0 ? 1 : 0, w.qval, w.qidx, w.qlen, iv, ii, il, ov, oi, ol);
     PFA_CHECK_LAUNCH("pfa_proto_prefix/scan");
     fin_v = ov;
     fin_i = oi;

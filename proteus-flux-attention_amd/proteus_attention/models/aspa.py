@@ -768,6 +768,9 @@ class AdaptiveSparseAttention(nn.Module):
         if cached is None or cached[0] != key:
             cached = (key, src.to(device=device, dtype=torch.int32).contiguous())
             self._g2h_cache = cached
+        keep = self.__dict__.get("_capture_keep")
+        if keep is not None:
+            keep.append(cached[1])
         return cached[1]
 
     def _route_device(self, x2d: torch.Tensor, topk: int, need_head_scores: bool = True):
@@ -912,6 +915,9 @@ class AdaptiveSparseAttention(nn.Module):
         B, T = qkv.shape[0], qkv.shape[1]
         cos, sin = self._rope_factors(T, qkv.device, qkv.dtype)
         cos, sin = cos.contiguous(), sin.contiguous()
+        keep = self.__dict__.get("_capture_keep")
+        if keep is not None:
+            keep.extend((cos, sin))
         fn = _hip.lib().pfa_rope_qk_inplace if rotate_q else _hip.lib().pfa_rope_k_inplace
         with _hip.TIMER.timed("rope_qk"):
             rc = fn(_hip.ptr(qkv), _hip.dtype_tag(qkv.dtype), B, T, self.h_total, self.d_head, _hip.ptr(cos),
@@ -1032,16 +1038,25 @@ class AdaptiveSparseAttention(nn.Module):
             with torch.no_grad():
                 for n, b in self.named_buffers():
                     b.copy_(bufs[n])
+            # the restore bumped the buffers' versions: refresh the int32 gate
+            # map now, so that the capture does not record its rebuild
+            self._gate_to_head_i32(device)
             if getattr(self, "_hip_graph_pool", None) is None:
                 self._hip_graph_pool = torch.cuda.graph_pool_handle()
             graph = torch.cuda.CUDAGraph()
+            # cached tensors the captured kernels read (gate map, RoPE tables)
+            # are held by the graph: a later rebuild of a cache must not free
+            # memory a replay still reads
+            self._capture_keep = []
             with torch.cuda.graph(graph, pool=self._hip_graph_pool):
                 attn, stats_args, label = self._forward_impl(xs, capture=True)
+            keep = self._capture_keep
         finally:
             _hip.TIMER.enabled = timer_on
+            self._capture_keep = None
         ent = {"graph": graph, "x": xs, "attn": attn, "stats_args": stats_args, "label": label,
                "state": {k: self.__dict__.get(k) for k in self._GRAPH_STATE},
-               "sparse_state": self.__dict__.get("_lazy__last_sparse_state")}
+               "sparse_state": self.__dict__.get("_lazy__last_sparse_state"), "keep": keep}
         self._hip_graphs[key] = ent
         return ent
 
@@ -1173,9 +1188,14 @@ class AdaptiveSparseAttention(nn.Module):
         gate_probs = gate.view(B, T, self.attn_gates)
         self._last_gate_probs = gate_probs
         # the prototype EMA (aspa.py:692-718) reads only this forward's router
-        # outputs and is read only by the next forward's router: it runs here,
-        # overlapping the projection on the forked stream
-        self._update_routing_prototypes(x, gate_probs)
+        # outputs and is read only by the next forward's router: on the
+        # structured path it is queued behind the anchor pass on the forked
+        # stream, elsewhere before the streams join
+
+        ema_keep = self.__dict__.get("_ema_partial")  # may be consumed on the fork stream: held to the join
+
+        def ema() -> None:
+            self._update_routing_prototypes(x, gate_probs)
         if sim is not None:
             self._last_token_similarity = sim.view(B, T)
             self._last_token_blend = blend.view(B, T)
@@ -1252,6 +1272,7 @@ class AdaptiveSparseAttention(nn.Module):
             qkv.record_stream(main_s)
             attn.record_stream(main_s)
         if not structured:
+            ema()
             main_s.wait_stream(fork_s)
         D = self.d_head
         mode_label = "sparse"
@@ -1291,7 +1312,8 @@ class AdaptiveSparseAttention(nn.Module):
             rh = row_head[:N]
             heads = active_heads[:P] if P >= 0 else active_heads
             self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets, alpha, row_of, summary,
-                                       plan=plan, q_rope=q_rope, streams=(main_s, fork_s))
+                                       plan=plan, q_rope=q_rope, streams=(main_s, fork_s),
+                                       before_join=ema if structured else None)
             backend_info = self._last_shortlist_backend_info or get_last_backend_info()
             state = {
                 "mode": mode_label, "backend": str(backend_info.get("name", "shortlist")),
@@ -1318,6 +1340,7 @@ class AdaptiveSparseAttention(nn.Module):
         stats_args = (token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
                       dense_reason, B, T, active_heads, row_offsets, summary)
         label = f"cvt(alpha={alpha:.2f})::{mode_label}"
+        del ema_keep  # the streams have joined
         if capture:
             return attn, stats_args, label
         y = self.dropout(self.proj(attn))
@@ -1367,7 +1390,8 @@ class AdaptiveSparseAttention(nn.Module):
         return st
 
     def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha, row_of,
-                              summary, plan: Optional[Dict[str, Any]] = None, q_rope=None, streams=None) -> None:
+                              summary, plan: Optional[Dict[str, Any]] = None, q_rope=None, streams=None,
+                              before_join=None) -> None:
         """Candidate attention (aspa.py:1175-1310).
 
         When no row can be truncated to L, bf16 with D=64 and no int8 path,
@@ -1378,9 +1402,10 @@ class AdaptiveSparseAttention(nn.Module):
 
         streams = (main, fork): qkv and attn come from work queued on the
         fork stream; the structured path queues its anchor pass there too
-        (after the packing on main) while main builds the prototype tables,
-        then main waits for the fork stream before the main pass.  The other
-        paths are entered with the fork stream already joined."""
+        (after the packing on main), followed by `before_join`, while main
+        builds the prototype tables; main then waits for the fork stream
+        before the main pass.  The other paths are entered with the fork
+        stream already joined."""
         H, D = self.h_total, self.d_head
         device = qkv.device
         if plan is None:
@@ -1400,14 +1425,20 @@ class AdaptiveSparseAttention(nn.Module):
                 part = _sa.shortlist_partials(int(token_idx.numel()), device)
                 if streams is not None:
                     main_s, fork_s = streams
-                    # anchor pass on the fork stream, after the packing
+                    # anchor pass on the fork stream, after the packing, then
+                    # `before_join` behind it
                     fork_s.wait_stream(main_s)
                     with torch.cuda.stream(fork_s):
                         _sa._shortlist_attn_structured(*t4, *args, None, None, scale, device, want_lengths=False,
                                                        q_rope=q_rope, passes=1, part=part)
+                        if before_join is not None:
+                            before_join()
+                            before_join = None
             blocks = evict = None
             if K > 0:
                 blocks, evict = _sa._proto_prefix_blocks(self._last_token_similarity, K)
+            if before_join is not None:
+                before_join()
             if streams is not None:
                 streams[0].wait_stream(streams[1])
             passes = 2 if (part is not None and streams is not None) else 3
