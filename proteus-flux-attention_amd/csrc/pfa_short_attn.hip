@@ -139,18 +139,16 @@ __device__ __forceinline__ i16x4_t v_tr4(const uint16_t* Vs, int row0, int d0) {
 }
 
 
-// One 64-key tile for the 16 query rows of this wave.  With MASKED,
-// mask(kl) decides whether tile key kl (0..63) is a candidate of this lane's
-// query row; without, every key of the tile is (the caller has checked that
-// the tile lies inside every row's key range).  exp2 runs on v_exp_f32
-// directly (arguments are <= 0; -inf gives 0), P is rounded to bf16 with
-// v_cvt_pk_bf16_f32 (round to nearest even).
-template <bool MASKED, bool COUNT, class MaskF>
-__device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_t* Ks, const uint16_t* Vs,
-                                          float scale_log2, MaskF mask, QState& st) {
+// One 64-key tile for the 16 query rows of this wave, in three stages that
+// every tile kind shares: qk_tile (the scores), a mask (keys of the tile
+// that are not candidates of the lane's row get -inf), softmax_pv (online
+// softmax and the P.V product).  One accumulation path for all tile kinds
+// keeps the running state in the same registers across tiles.
+//
+// S^T = K Q^T: s[kb][i] is the raw score of tile key 16kb + 4g + i against
+// the lane's query row (the scale is applied in the exp argument).
+__device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[2], const uint16_t* Ks, float (&s)[4][4]) {
   const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
-  float s[4][4];
-  float tmax = -INFINITY;  // raw scores (the scale is applied in the exp argument)
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     f32x4_t c = {0.f, 0.f, 0.f, 0.f};
@@ -160,18 +158,54 @@ __device__ __forceinline__ void tile_step(const bf16x8_t (&qf)[2], const uint16_
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[dc], c, 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (MASKED) {
-        const bool ok = mask(16 * kb + 4 * g + i);
-        s[kb][i] = ok ? c[i] : -INFINITY;
-        if constexpr (COUNT) st.cnt += ok ? 1 : 0;
-      } else {
-        s[kb][i] = c[i];
-      }
-      tmax = fmaxf(tmax, s[kb][i]);
-    }
+    for (int i = 0; i < 4; ++i) s[kb][i] = c[i];
   }
-  if constexpr (!MASKED && COUNT) st.cnt += 16;
+}
+
+// Range mask: the lane's candidates in the tile are the keys kl in
+// [lo, hi]; lo4 = lo - 4g and hi4 = hi - 4g, so each element is one compare
+// against a constant (16kb + i) and a select.  LO / HI pick which bounds can
+// cut this tile (a wave-uniform choice).
+template <bool LO, bool HI, bool COUNT>
+__device__ __forceinline__ void mask_range(float (&s)[4][4], int lo4, int hi4, int& cnt) {
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 16 * kb + i;
+      bool ok = true;
+      if constexpr (LO) ok = ok && c >= lo4;
+      if constexpr (HI) ok = ok && c <= hi4;
+      s[kb][i] = ok ? s[kb][i] : -INFINITY;
+      if constexpr (COUNT) cnt += ok ? 1 : 0;
+    }
+}
+
+// The lane's candidates in the tile are [lo, hi] (tile-local, lo > hi for
+// none); need_lo / need_hi (wave-uniform) say whether some row of the wave
+// is cut by that bound in this tile.
+template <bool COUNT>
+__device__ __forceinline__ void mask_window(float (&s)[4][4], bool need_lo, bool need_hi, int lo, int hi, int& cnt) {
+  const int g4 = 4 * ((threadIdx.x & 63) >> 4);
+  // the conditions are wave-uniform: scalar branches
+  need_lo = __builtin_amdgcn_readfirstlane(need_lo ? 1 : 0) != 0;
+  need_hi = __builtin_amdgcn_readfirstlane(need_hi ? 1 : 0) != 0;
+  if (need_lo && need_hi) mask_range<true, true, COUNT>(s, lo - g4, hi - g4, cnt);
+  else if (need_lo) mask_range<true, false, COUNT>(s, lo - g4, 0, cnt);
+  else if (need_hi) mask_range<false, true, COUNT>(s, 0, hi - g4, cnt);
+  else if (COUNT) cnt += 16;
+}
+
+// Online softmax (exp2 on v_exp_f32 directly: arguments are <= 0, -inf
+// gives 0) and O^T += V^T P^T with P rounded to bf16 (v_cvt_pk_bf16_f32,
+// round to nearest even).
+__device__ __forceinline__ void softmax_pv(float (&s)[4][4], const uint16_t* Vs, float scale_log2, QState& st) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[kb][i]);
   tmax = max_over_rows4(tmax);
   // Lazy rescaling: the accumulator is rescaled only on tiles where some row
   // of the wave sees a new maximum (a wave-uniform branch); st.m stays the
@@ -378,13 +412,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
       const bool more = i + 1 < ntile;
       if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min((int64_t)m0 + kTile + jrow, mhi));
       const bool empty = !wave_rows || m0 > w_hihi || m0 + kTile - 1 < w_lolo;
-      const bool full = wave_full && m0 >= w_lohi && m0 + kTile - 1 <= w_hilo && m0 + kTile - 1 <= mhi;
-      auto cls_mask = [&](int kl) {
-        const int m = m0 + kl;
-        return m <= (int)mhi && m >= lo_q && m <= hi_q;
-      };
-      if (full) tile_step<false, false>(qf, Ks[cur], Vs[cur], a.scale_log2, cls_mask, st);
-      else if (!empty) tile_step<true, false>(qf, Ks[cur], Vs[cur], a.scale_log2, cls_mask, st);
+      if (!empty) {
+        // the row's keys m in [lo_q, min(hi_q, mhi)], tile-local
+        const bool need_lo = !wave_full || m0 < w_lohi;
+        const bool need_hi = !wave_full || m0 + kTile - 1 > min(w_hilo, (int)mhi);
+        const int lo = qv ? lo_q - m0 : kTile;
+        const int hi = min(hi_q, (int)mhi) - m0;
+        float sc[4][4];
+        int unused = 0;
+        qk_tile(qf, Ks[cur], sc);
+        mask_window<false>(sc, need_lo, need_hi, lo, hi, unused);
+        softmax_pv(sc, Vs[cur], a.scale_log2, st);
+      }
       if (more) store_tile(nxt, Ks[cur ^ 1], Vs[cur ^ 1]);
       __syncthreads();
     }
@@ -563,29 +602,36 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
       TileRegs nxt;
       const bool more = i + 1 < ntile;
       if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, key_of(i + 1));
-      if (i < nw) {
-        const int k0 = lo_first + kTile * i;
-        const bool empty = !wave_rows || k0 > w_thi || k0 + kTile - 1 < w_llo;
-        const bool full = wave_full && k0 >= w_lhi && k0 + kTile - 1 <= w_tlo;
-        // this row's window keys in the tile are kl in [wa, wa + wn)
-        const int wa = max(loq - k0, 0);
-        const int wn = qv ? max(min(tq - k0, kTile - 1) - wa + 1, 0) : 0;
-        auto win_mask = [&](int kl) { return (unsigned)(kl - wa) < (unsigned)wn; };
-        if (full) tile_step<false, COUNT>(qf, Ks[cur], Vs[cur], a.scale_log2, win_mask, st);
-        else if (!empty) tile_step<true, COUNT>(qf, Ks[cur], Vs[cur], a.scale_log2, win_mask, st);
-      } else if (wave_rows) {
-        const int j0 = (i - nw) * kTile;
-        tile_step<true, COUNT>(qf, Ks[cur], Vs[cur], a.scale_log2,
-                  [&](int kl) {
-                    const int j = j0 + kl;
-                    if (!qv || j >= plen) return false;
-                    const int kp = pk[j];
-                    if (kp >= loq) return false;
-                    const bool anchor = anch_on && pm[j] == tmod && kp >= alo;
-                    const bool in_proto = pe[j] > tq && !anchor;
-                    return in_proto || (kp == 0 && zf);
-                  },
-                  st);
+      const bool is_win = i < nw;
+      const int k0 = lo_first + kTile * i;
+      const bool active = is_win ? (wave_rows && k0 <= w_thi && k0 + kTile - 1 >= w_llo) : wave_rows;
+      if (active) {
+        float sc[4][4];
+        qk_tile(qf, Ks[cur], sc);
+        if (is_win) {
+          // the row's window keys in the tile: [loq - k0, tq - k0]
+          const bool need_lo = !wave_full || k0 < w_lhi;
+          const bool need_hi = !wave_full || k0 + kTile - 1 > w_tlo;
+          mask_window<COUNT>(sc, need_lo, need_hi, qv ? loq - k0 : kTile, tq - k0, st.cnt);
+        } else {
+          const int j0 = (i - nw) * kTile;
+          const int g4 = 4 * g;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int j = j0 + 16 * kb + g4 + e;
+              bool ok = false;
+              if (qv && j < plen) {
+                const int kp = pk[j];
+                const bool anchor = anch_on && pm[j] == tmod && kp >= alo;
+                ok = kp < loq && ((pe[j] > tq && !anchor) || (kp == 0 && zf));
+              }
+              sc[kb][e] = ok ? sc[kb][e] : -INFINITY;
+              if constexpr (COUNT) st.cnt += ok ? 1 : 0;
+            }
+        }
+        softmax_pv(sc, Vs[cur], a.scale_log2, st);
       }
       if (more) store_tile(nxt, Ks[cur ^ 1], Vs[cur ^ 1]);
       __syncthreads();
