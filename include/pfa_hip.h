@@ -80,6 +80,13 @@ const char* pfa_last_error_string(void);
  *     them with pfa_proto_partial_reduce(ema_partial, n_blocks, ...).
  * ==================================================================== */
 int pfa_router_gate_pad(int G);
+/* Sum of the router's per-workgroup telemetry partials (stats_partial
+ * (n_blocks, 8) of pfa_router_topk) column by column in float64, into out[8]
+ * (fixed summation order).  No counterpart in the reference, which reduces
+ * these statistics with tensor ops; a single 64-byte result keeps the
+ * device-to-host telemetry copy small. */
+int pfa_router_stats_reduce(const float* stats_partial, int n_blocks, double* out, void* stream);
+
 int pfa_router_block_count(int64_t n_tok, int* n_blocks);
 
 /* Per-forward router inputs in one launch (replaces the tensor ops of

@@ -924,6 +924,34 @@ static void launch_accum(const void* x, int64_t n_tok, int C, int G, const float
   else proto_accum_kernel<DT, 64><<<n_parts, kEmaThreads, 0, s>>>((const ET*)x, n_tok, C, G, gp, per, partial);
 }
 
+// Telemetry partials (n_blocks, 8) summed column-wise in f64 into out[8]:
+// thread t owns column t % 8 and the blocks t/8 + 128k; each pass issues
+// eight independent loads before adding them, and the 128 per-column
+// partials are then added in a fixed tree order (deterministic).
+__global__ void __launch_bounds__(1024) router_stats_reduce_kernel(const float* __restrict__ stats, int n_blocks,
+                                                                   double* __restrict__ out) {
+  __shared__ double part[1024];
+  const int t = threadIdx.x, c = t & 7, b0 = t >> 3;
+  double acc = 0.0;
+  for (int base = 0; base < n_blocks; base += 1024) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int b = base + b0 + 128 * k;
+      v[k] = b < n_blocks ? stats[(int64_t)b * 8 + c] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc += (double)v[k];
+  }
+  part[t] = acc;
+  __syncthreads();
+  for (int w = 512; w >= 8; w >>= 1) {
+    if (t < w) part[t] += part[t + w];
+    __syncthreads();
+  }
+  if (t < 8) out[t] = part[t];
+}
+
 }  // namespace pfa
 
 using namespace pfa;
@@ -1008,6 +1036,14 @@ extern "C" int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C,
       set_error("pfa_router_topk: unsupported dtype %d", x_dtype);
       return PFA_E_UNSUPPORTED;
   }
+}
+
+extern "C" int pfa_router_stats_reduce(const float* stats_partial, int n_blocks, double* out, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(stats_partial && out && n_blocks > 0, "pfa_router_stats_reduce: bad arguments");
+  router_stats_reduce_kernel<<<1, 1024, 0, as_stream(stream)>>>(stats_partial, n_blocks, out);
+  PFA_CHECK_LAUNCH("pfa_router_stats_reduce");
+  return PFA_OK;
 }
 
 extern "C" int pfa_router_block_count(int64_t n_tok, int* n_blocks) {

@@ -315,6 +315,8 @@ __device__ __forceinline__ int64_t xcd_block(int64_t P, int64_t nblk) {
 // Pass 1: anchors per (residue class, compact head)
 // ---------------------------------------------------------------------
 // Occupancy: at most 168 VGPRs so that three 4-wave workgroups share a CU.
+// The pass runs beside the prototype-table kernels on another stream; three
+// workgroups (about 115 KB of LDS) leave LDS and wave slots for them.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) short_anchor_kernel(ShortArgs a,
                                                                                                      int ccap) {
   __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
@@ -444,8 +446,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
 // ---------------------------------------------------------------------
 // Pass 2: window + prototype keys per segment of consecutive rows
 // ---------------------------------------------------------------------
+// Occupancy: at most 128 VGPRs so that four 4-wave workgroups (about 150 KB
+// of LDS) share a CU; the few registers the compiler spills at that limit
+// cost less than the latency the fourth workgroup hides.
 template <bool COUNT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
 short_main_kernel(ShortArgs a, int use_part, int pcap) {
   __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
   __shared__ __align__(16) uint16_t Vs[2][kTile * kLd];

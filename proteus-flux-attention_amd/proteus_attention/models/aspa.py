@@ -1195,7 +1195,11 @@ class AdaptiveSparseAttention(nn.Module):
         ema_keep = self.__dict__.get("_ema_partial")  # may be consumed on the fork stream: held to the join
 
         def ema() -> None:
+            # the router's tail: the prototype EMA and the telemetry reduction
+            # (both read only router outputs; neither is read in this forward)
             self._update_routing_prototypes(x, gate_probs)
+            _hip.check(lib.pfa_router_stats_reduce(_hip.ptr(router_stats), int(router_stats.size(0)), _hip.ptr(comb),
+                                                   _hip.stream_ptr(device)), "pfa_router_stats_reduce")
         if sim is not None:
             self._last_token_similarity = sim.view(B, T)
             self._last_token_blend = blend.view(B, T)
@@ -1215,12 +1219,17 @@ class AdaptiveSparseAttention(nn.Module):
         H = self.h_total
         BH = B * H
         mask8 = torch.empty(BH, T, dtype=torch.uint8, device=device)
-        active_heads = torch.empty(BH, dtype=torch.int32, device=device)
+        # telemetry for the host in one small buffer (one device-to-host copy):
+        # [0:16) the router statistics as 8 float64, [16:20) the packing
+        # summary, [20:20+BH) the active heads
+        comb = torch.empty(20 + BH, dtype=torch.int32, device=device)
+        active_heads = comb[20:]
+        router_stats = self._router_stats
         row_offsets = torch.empty(BH + 1, dtype=torch.int32, device=device)
         token_idx = torch.empty(BH * T, dtype=torch.int32, device=device)
         row_head = torch.empty(BH * T, dtype=torch.int32, device=device)
         row_of = torch.empty(BH, T, dtype=torch.int32, device=device)
-        summary = torch.empty(4, dtype=torch.int32, device=device)
+        summary = comb[16:20]
         ws = _sa._workspace(_sa._size_out(lib.pfa_pack_workspace_size, B, H, T), device)
         tm8 = token_mask.view(torch.uint8) if token_mask is not None else None
         with _hip.TIMER.timed("pack_rows"):
@@ -1338,7 +1347,7 @@ class AdaptiveSparseAttention(nn.Module):
         self.last_head_consensus = None if self.training else attn.detach()
         self.last_router_reg = router_reg
         stats_args = (token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
-                      dense_reason, B, T, active_heads, row_offsets, summary)
+                      dense_reason, B, T, active_heads, row_offsets, summary, comb)
         label = f"cvt(alpha={alpha:.2f})::{mode_label}"
         del ema_keep  # the streams have joined
         if capture:
@@ -1502,26 +1511,25 @@ class AdaptiveSparseAttention(nn.Module):
         return self.router_reg_lambda * total
 
     def _finish_stats(self, token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
-                      dense_reason, B, T, active_heads, row_offsets, summary) -> None:
+                      dense_reason, B, T, active_heads, row_offsets, summary, comb) -> None:
         """Telemetry dictionaries (aspa.py:1857-1916) from the router's
-        per-workgroup partials and the packing summary.  The three small
-        device buffers are copied into pinned host memory without waiting;
-        the dictionaries are built when first read (or at the next forward),
-        so the forward never stalls the device queue for them."""
+        statistics and the packing summary.  `comb` (the reduced router
+        statistics, the summary and the active heads, under a hundred bytes
+        for the usual head counts) is copied into pinned host memory without
+        waiting -- a large device-to-host copy would make the host wait for
+        the device -- and the dictionaries are built when first read (or at
+        the next forward), so the forward never stalls the device queue."""
         self._resolve_stats()
         H = self.h_total
         with torch.no_grad():
-            # one pinned staging tensor per source, kept across forwards: the
-            # previous forward's values were consumed by _resolve_stats above
-            bufs = self.__dict__.setdefault("_stats_host", {})
-            host = []
-            for i, t in enumerate((self._router_stats, summary, active_heads)):
-                h = bufs.get(i)
-                if h is None or h.shape != t.shape or h.dtype != t.dtype:
-                    h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
-                    bufs[i] = h
-                h.copy_(t, non_blocking=True)
-                host.append(h)
+            # one pinned staging tensor, kept across forwards: the previous
+            # forward's values were consumed by _resolve_stats above
+            h = self.__dict__.get("_stats_host")
+            if h is None or h.shape != comb.shape:
+                h = torch.empty(comb.shape, dtype=torch.int32, pin_memory=True)
+                self.__dict__["_stats_host"] = h
+            h.copy_(comb, non_blocking=True)
+            host = (h[:16].view(torch.float64), h[16:20], h[20:])
             done = self.__dict__.get("_stats_event")
             if done is None:
                 done = torch.cuda.Event()
@@ -1538,7 +1546,7 @@ class AdaptiveSparseAttention(nn.Module):
         def build() -> None:
             nonlocal mode_label
             done.synchronize()
-            part = host[0].to(torch.float64).sum(dim=0).tolist()
+            part = host[0].tolist()
             summ = host[1].tolist()
             ent_sum, sim_sum, blend_sum, blend_pos, score_sum = part[:5]
             P_, N_, max_rows_ = int(summ[0]), int(summ[1]), int(summ[2])
