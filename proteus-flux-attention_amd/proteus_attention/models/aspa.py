@@ -1414,7 +1414,9 @@ class AdaptiveSparseAttention(nn.Module):
         (after the packing on main), followed by `before_join`, while main
         builds the prototype tables; main then waits for the fork stream
         before the main pass.  The other paths are entered with the fork
-        stream already joined."""
+        stream already joined.  The prototype tables are queued before the
+        anchor pass so that, in a captured graph, they follow the packing on
+        its queue instead of starting on another one."""
         H, D = self.h_total, self.d_head
         device = qkv.device
         if plan is None:
@@ -1430,22 +1432,28 @@ class AdaptiveSparseAttention(nn.Module):
             args = (H, T, D, token_idx, row_head, heads, summary, row_of, w_eff, stride, slots)
             scale = 1.0 / math.sqrt(D)
             part = None
-            if stride > 0 and slots > 0:
+            anchors = stride > 0 and slots > 0
+            if anchors:
                 part = _sa.shortlist_partials(int(token_idx.numel()), device)
-                if streams is not None:
-                    main_s, fork_s = streams
-                    # anchor pass on the fork stream, after the packing, then
-                    # `before_join` behind it
-                    fork_s.wait_stream(main_s)
-                    with torch.cuda.stream(fork_s):
-                        _sa._shortlist_attn_structured(*t4, *args, None, None, scale, device, want_lengths=False,
-                                                       q_rope=q_rope, passes=1, part=part)
-                        if before_join is not None:
-                            before_join()
-                            before_join = None
+            packed = None
+            if anchors and streams is not None:
+                packed = torch.cuda.Event()
+                packed.record(streams[0])  # the packing is done
+            # prototype tables on this stream, queued before the anchor pass
+            # (which waits only for the packing, not for them)
             blocks = evict = None
             if K > 0:
                 blocks, evict = _sa._proto_prefix_blocks(self._last_token_similarity, K)
+            if packed is not None:
+                fork_s = streams[1]
+                fork_s.wait_event(packed)
+                # anchor pass on the fork stream, then `before_join` behind it
+                with torch.cuda.stream(fork_s):
+                    _sa._shortlist_attn_structured(*t4, *args, None, None, scale, device, want_lengths=False,
+                                                   q_rope=q_rope, passes=1, part=part)
+                    if before_join is not None:
+                        before_join()
+                        before_join = None
             if before_join is not None:
                 before_join()
             if streams is not None:
