@@ -1188,11 +1188,10 @@ class AdaptiveSparseAttention(nn.Module):
         gate_probs = gate.view(B, T, self.attn_gates)
         self._last_gate_probs = gate_probs
         # the prototype EMA (aspa.py:692-718) reads only this forward's router
-        # outputs and is read only by the next forward's router: on the
-        # structured path it is queued behind the anchor pass on the forked
-        # stream, elsewhere before the streams join
+        # outputs and is read only by the next forward's router: it is queued
+        # last before the streams join (on the structured path, after the
+        # prototype tables)
 
-        ema_keep = self.__dict__.get("_ema_partial")  # may be consumed on the fork stream: held to the join
 
         def ema() -> None:
             # the router's tail: the prototype EMA and the telemetry reduction
@@ -1349,7 +1348,6 @@ class AdaptiveSparseAttention(nn.Module):
         stats_args = (token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
                       dense_reason, B, T, active_heads, row_offsets, summary, comb)
         label = f"cvt(alpha={alpha:.2f})::{mode_label}"
-        del ema_keep  # the streams have joined
         if capture:
             return attn, stats_args, label
         y = self.dropout(self.proj(attn))
@@ -1411,9 +1409,9 @@ class AdaptiveSparseAttention(nn.Module):
 
         streams = (main, fork): qkv and attn come from work queued on the
         fork stream; the structured path queues its anchor pass there too
-        (after the packing on main), followed by `before_join`, while main
-        builds the prototype tables; main then waits for the fork stream
-        before the main pass.  The other paths are entered with the fork
+        (after the packing on main) while main builds the prototype tables
+        and runs `before_join`; main then waits for the fork stream before
+        the main pass.  The other paths are entered with the fork
         stream already joined.  The prototype tables are queued before the
         anchor pass so that, in a captured graph, they follow the packing on
         its queue instead of starting on another one."""
@@ -1447,13 +1445,10 @@ class AdaptiveSparseAttention(nn.Module):
             if packed is not None:
                 fork_s = streams[1]
                 fork_s.wait_event(packed)
-                # anchor pass on the fork stream, then `before_join` behind it
+                # anchor pass on the fork stream
                 with torch.cuda.stream(fork_s):
                     _sa._shortlist_attn_structured(*t4, *args, None, None, scale, device, want_lengths=False,
                                                    q_rope=q_rope, passes=1, part=part)
-                    if before_join is not None:
-                        before_join()
-                        before_join = None
             if before_join is not None:
                 before_join()
             if streams is not None:
