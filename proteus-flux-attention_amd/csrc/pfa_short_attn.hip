@@ -26,9 +26,11 @@
 // "segment" of rows streams those keys once, masks per (row, key), merges the
 // anchor partial and writes the normalised bf16 row into [b][h][t][:].
 //
-// Tiles: 4 waves x 16 query rows, 64 keys per tile staged in LDS (K and V
-// row-major, rows padded to 72 elements: conflict-free 16-lane K reads; the
-// V^T operand comes from the LDS transpose read).  Each wave computes
+// Tiles: 4 waves x 16 query rows, 64 keys per tile.  Key tiles reach LDS by
+// DMA (global_load_lds, no register staging) into a ring of stages, so the
+// next tiles are in flight while one is computed; rows are 128 bytes with
+// XOR-swizzled 16-byte chunks (conflict-free K fragment reads; the V^T
+// operand comes from the LDS transpose read).  Each wave computes
 // S^T = K Q^T and O^T += V^T P^T with v_mfma_f32_16x16x32_bf16, so a lane
 // owns one query row throughout: the softmax max needs two cross-lane
 // permutes per tile.
@@ -41,7 +43,6 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
 constexpr int kRows = 64;   // query rows per workgroup
 constexpr int kTile = 64;   // keys per tile
-constexpr int kLd = 72;     // padded LDS row, bf16 elements
 constexpr int kPartW = 68;  // floats per partial row: m, l, pad, pad, acc[64]
 constexpr int kMaxProto = 1024;
 constexpr int kMaxClassRows = 4096;
@@ -94,50 +95,97 @@ __device__ __forceinline__ bool zero_anchor(int64_t t, int s, int slots) {
 
 __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); }
 
-// A 64-key tile is staged by 256 threads: thread tid fetches a quarter of
-// key row tid/4 (16 elements of K and of V) into registers; storing writes
-// both row-major into LDS.  Fetch and store are split so the
-// next tile's loads are in flight while the current tile is computed.
-struct TileRegs {
-  uint4 k0, k1, v0, v1;
-};
-
-__device__ __forceinline__ TileRegs fetch_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
-                                               int64_t ks_t, int64_t vs_t, int64_t key) {
-  const int qd = threadIdx.x & 3;
-  const uint4* ksrc = reinterpret_cast<const uint4*>(kb + key * ks_t + 16 * qd);
-  const uint4* vsrc = reinterpret_cast<const uint4*>(vb + key * vs_t + 16 * qd);
-  TileRegs r;
-  r.k0 = ksrc[0];
-  r.k1 = ksrc[1];
-  r.v0 = vsrc[0];
-  r.v1 = vsrc[1];
-  return r;
-}
-
-__device__ __forceinline__ void store_tile(const TileRegs& r, uint16_t* Ks, uint16_t* Vs) {
-  const int tid = threadIdx.x;
-  const int j = tid >> 2, qd = tid & 3;
-  uint4* kd = reinterpret_cast<uint4*>(Ks + j * kLd + 16 * qd);
-  kd[0] = r.k0;
-  kd[1] = r.k1;
-  uint4* vd = reinterpret_cast<uint4*>(Vs + j * kLd + 16 * qd);
-  vd[0] = r.v0;
-  vd[1] = r.v1;
-}
-
-// Four bf16 of one head dim from four consecutive key rows of the row-major
-// V tile, by the gfx950 LDS transpose read: within each 16-lane row of the
-// wave, lane 4a+b receives element b of the 8-byte chunks addressed by lanes
-// a, a+4, a+8, a+12.  Lane m of the row addresses key row0 + m/4, dims
+// Four bf16 of one head dim from four consecutive key rows of a V tile, by
+// the gfx950 LDS transpose read: within each 16-lane row of the wave, lane
+// 4a+b receives element b of the 8-byte chunks addressed by lanes a, a+4,
+// a+8, a+12.  Lane m of the row addresses key row0 + m/4, dims
 // d0 + 4*(m%4) .. +3, so lane i = 4a+b gets V[row0 + k][d0 + i], k = 0..3.
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4_t;
-__device__ __forceinline__ i16x4_t v_tr4(const uint16_t* Vs, int row0, int d0) {
-  const int m = threadIdx.x & 15;
-  const uint16_t* p = Vs + (row0 + (m >> 2)) * kLd + d0 + 4 * (m & 3);
+__device__ __forceinline__ i16x4_t ds_tr4(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p));
 }
 
+// A 64-key tile (K and V, 64 x 64 bf16 each) in LDS gives the MFMA
+// fragments through two calls: kfrag(kb, dc) is the lane's 8 K elements
+// (key 16kb + lane%16, dims 32dc + 8*(lane/16) ..+7) and vtr(kc, h, db) the
+// address the lane passes to the transpose read for keys
+// 32kc + 16h + 4*(lane/16) .. +3, dims 16db ..+15.
+//
+// SwzTile: unpadded 128-byte rows filled by LDS DMA (global_load_lds, 16
+// bytes per lane at consecutive LDS addresses).  The 16-byte chunk c of key
+// row r (dims 8c..8c+7) sits in chunk slot 8r + (c ^ tile_swz(r)): eight
+// consecutive rows read at one chunk (the K fragments) fall in eight
+// different bank groups, and so do the four rows x 32 bytes of each
+// transpose read.
+constexpr int kTileElems = kTile * 64;  // one unpadded K or V tile, bf16 elements
+__device__ __forceinline__ int tile_swz(int r) {
+  return (((r & 3) << 1) | ((r >> 2) & 1)) ^ (((r >> 3) & 1) << 1);
+}
+// per-lane element offsets into a SwzTile, fixed for the kernel
+struct SwzLane {
+  int ko[2];  // K fragment, dc = 0, 1 (plus 1024 * kb)
+  int vo[4];  // transpose read, db = 0..3 (plus 64 * (32kc + 16h))
+  __device__ __forceinline__ void init() {
+    const int lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
+    const int c0 = g ^ tile_swz(r16);
+    ko[0] = r16 * 64 + 8 * c0;
+    ko[1] = r16 * 64 + 8 * (c0 ^ 4);
+    const int m = r16, row = 4 * g + (m >> 2);
+    const int cv = ((m & 3) >> 1) ^ tile_swz(row);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) vo[db] = row * 64 + 8 * ((2 * db) ^ cv) + 4 * (m & 1);
+  }
+};
+struct SwzTile {
+  const uint16_t* base;  // K tile, V tile at base + kTileElems
+  const SwzLane& L;
+  __device__ __forceinline__ const uint16_t* kfrag(int kb, int dc) const { return base + 1024 * kb + L.ko[dc]; }
+  __device__ __forceinline__ const uint16_t* vtr(int kc, int h, int db) const {
+    return base + kTileElems + 64 * (32 * kc + 16 * h) + L.vo[db];
+  }
+};
+
+// LDS DMA of 16 bytes per lane: lane l's bytes from g land at LDS byte
+// address lds_wave + 16*l (lds_wave is the same for the whole wave).
+// Written as assembly so that the compiler does not wait for the transfer
+// before every LDS read: completion is waited for explicitly
+// (dma_wait_barrier).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// M0 is named as clobbered; nothing else in this file uses M0 (no LDS DMA
+// builtins, GWS, message or relative-indexing instructions), so no value of
+// the compiler's lives in it across the statement.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_wave) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_wave) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// Wait until at most N of this wave's vector memory operations are
+// outstanding and its LDS reads are done, then meet the other waves.
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+// One 64-key tile by DMA into a SwzTile: thread tid moves chunk slot tid%8
+// of key rows tid/8 and tid/8 + 32 (keys key0, key1) of K and of V: four
+// 16-byte transfers, each wave filling 1 KB runs of chunk slots.  lds_w is
+// the tile's LDS byte address plus 1 KB per wave index (wave-uniform).
+constexpr int kDmaPerTile = 4;
+__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
+                                         uint32_t ks_t, uint32_t vs_t, int key0, int key1, uint32_t lds_w) {
+  const int tid = threadIdx.x;
+  const int c = 8 * ((tid & 7) ^ tile_swz(tid >> 3));  // rows tid/8 and tid/8 + 32 share the swizzle
+  // element offsets: one 32 x 32 -> 64-bit multiply each (keys and row
+  // strides are below 2^31)
+  const uint64_t k0 = (uint64_t)(uint32_t)key0 * ks_t, k1 = (uint64_t)(uint32_t)key1 * ks_t;
+  const uint64_t v0 = (uint64_t)(uint32_t)key0 * vs_t, v1 = (uint64_t)(uint32_t)key1 * vs_t;
+  lds_dma16(kb + c + k0, lds_w);
+  lds_dma16(kb + c + k1, lds_w + 4096);
+  lds_dma16(vb + c + v0, lds_w + 2 * kTileElems);
+  lds_dma16(vb + c + v1, lds_w + 2 * kTileElems + 4096);
+}
 
 // One 64-key tile for the 16 query rows of this wave, in three stages that
 // every tile kind shares: qk_tile (the scores), a mask (keys of the tile
@@ -147,19 +195,24 @@ __device__ __forceinline__ i16x4_t v_tr4(const uint16_t* Vs, int row0, int d0) {
 //
 // S^T = K Q^T: s[kb][i] is the raw score of tile key 16kb + 4g + i against
 // the lane's query row (the scale is applied in the exp argument).
-__device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[2], const uint16_t* Ks, float (&s)[4][4]) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
+template <typename Tile>
+__device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[2], const Tile& t, float (&s)[4][4]) {
+  // all eight fragment reads first, then four independent MFMA chains
+  bf16x8_t a[2][4];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+  for (int dc = 0; dc < 2; ++dc)
 #pragma unroll
-    for (int dc = 0; dc < 2; ++dc) {
-      bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(Ks + (16 * kb + r16) * kLd + 32 * dc + 8 * g);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[dc], c, 0, 0, 0);
-    }
+    for (int kb = 0; kb < 4; ++kb) a[dc][kb] = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, dc));
+  f32x4_t c[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[kb][i] = c[i];
-  }
+  for (int kb = 0; kb < 4; ++kb)
+    c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0][kb], qf[0], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1][kb], qf[1], c[kb], 0, 0, 0);
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[kb][i] = c[kb][i];
 }
 
 // Range mask: the lane's candidates in the tile are the keys kl in
@@ -199,8 +252,8 @@ __device__ __forceinline__ void mask_window(float (&s)[4][4], bool need_lo, bool
 // Online softmax (exp2 on v_exp_f32 directly: arguments are <= 0, -inf
 // gives 0) and O^T += V^T P^T with P rounded to bf16 (v_cvt_pk_bf16_f32,
 // round to nearest even).
-__device__ __forceinline__ void softmax_pv(float (&s)[4][4], const uint16_t* Vs, float scale_log2, QState& st) {
-  const int lane = threadIdx.x & 63, g = lane >> 4;
+template <typename Tile>
+__device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, float scale_log2, QState& st) {
   float tmax = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
@@ -250,8 +303,8 @@ __device__ __forceinline__ void softmax_pv(float (&s)[4][4], const uint16_t* Vs,
     for (int db = 0; db < 4; ++db) {
       // A operand V^T: lane (dim 16db + r16, g) holds the keys of pb's
       // slots, 32kc + 4g + (0..3) and 32kc + 16 + 4g + (0..3)
-      const i16x4_t lo = v_tr4(Vs, 32 * kc + 4 * g, 16 * db);
-      const i16x4_t hi = v_tr4(Vs, 32 * kc + 16 + 4 * g, 16 * db);
+      const i16x4_t lo = ds_tr4(t.vtr(kc, 0, db));
+      const i16x4_t hi = ds_tr4(t.vtr(kc, 1, db));
       bf16x8_t va;
       __builtin_memcpy(&va, &lo, 8);
       __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
@@ -316,11 +369,13 @@ __device__ __forceinline__ int64_t xcd_block(int64_t P, int64_t nblk) {
 // ---------------------------------------------------------------------
 // Occupancy: at most 168 VGPRs so that three 4-wave workgroups share a CU.
 // The pass runs beside the prototype-table kernels on another stream; three
-// workgroups (about 115 KB of LDS) leave LDS and wave slots for them.
+// workgroups (about 100 KB of LDS with a two-stage ring) leave LDS and wave
+// slots for them.
+constexpr int kAnchorStages = 2;
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) short_anchor_kernel(ShortArgs a,
                                                                                                      int ccap) {
-  __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
-  __shared__ __align__(16) uint16_t Vs[2][kTile * kLd];
+  constexpr int S = kAnchorStages;
+  __shared__ __align__(16) uint16_t ring[S][2 * kTileElems];
   // active rows of the class: row index and class position M (M < ccap <=
   // kMaxClassRows), sized to the class length (dynamic LDS)
   extern __shared__ int32_t cls_dyn[];
@@ -339,6 +394,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   const int64_t bb = bh / a.H, hh = bh % a.H;
   const int64_t Mmax = (a.T - 1 - c) / s;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  SwzLane L;
+  L.init();
+  const int drow = tid >> 3;  // this thread's DMA rows: drow and drow + 32
+  const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + 1024u * (uint32_t)wid);
+  constexpr uint32_t kStageBytes = 2 * kTileElems * 2;
 
   // compact the active rows of this class (ascending M)
   if (tid == 0) s_count = 0;
@@ -395,24 +455,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
     const int64_t mlo = Mf - a.slots > 0 ? Mf - a.slots : 0;
     const int64_t tl = c + (int64_t)s * Ml;
     const int64_t mhi = Ml - ((tl - win_lo(tl, a.local_w)) / s + 1);
-    // pipelined over the class's key tiles: tile i+1 is fetched while tile i
-    // is computed; the first tile's loads are issued before the q row's
+    // pipelined over the class's key tiles (strided keys c + s*m) through
+    // the LDS ring; the first tile is requested before the q row's loads
     const int ntile = mhi >= mlo ? (int)((mhi - mlo) / kTile + 1) : 0;
-    const int64_t jrow = tid >> 2;
-    TileRegs first;
-    if (ntile > 0) first = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min(mlo + jrow, mhi));
+    auto request = [&](int i) {
+      const int m0 = (int)mlo + kTile * i;
+      dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, c + s * min(m0 + drow, (int)mhi),
+               c + s * min(m0 + drow + 32, (int)mhi), ring_w + kStageBytes * (uint32_t)(i % S));
+    };
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i)
+      if (i < ntile) request(i);
     bf16x8_t qf[2];
     load_q_row(a, qb, tq, qf);
+    asm volatile("" : "+v"(qf[0]), "+v"(qf[1]));  // no load left for the tile loop to wait on
     QState st;
     init_state(st);
-    if (ntile > 0) store_tile(first, Ks[0], Vs[0]);
-    __syncthreads();
     for (int i = 0; i < ntile; ++i) {
-      const int cur = i & 1;
+      if (S == 3 && i + 1 < ntile)
+        dma_wait_barrier<kDmaPerTile>();
+      else
+        dma_wait_barrier<0>();
+      if (i + S - 1 < ntile) request(i + S - 1);
       const int m0 = (int)mlo + kTile * i;
-      TileRegs nxt;
-      const bool more = i + 1 < ntile;
-      if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, c + (int64_t)s * min((int64_t)m0 + kTile + jrow, mhi));
       const bool empty = !wave_rows || m0 > w_hihi || m0 + kTile - 1 < w_lolo;
       if (!empty) {
         // the row's keys m in [lo_q, min(hi_q, mhi)], tile-local
@@ -422,12 +487,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
         const int hi = min(hi_q, (int)mhi) - m0;
         float sc[4][4];
         int unused = 0;
-        qk_tile(qf, Ks[cur], sc);
+        const SwzTile tl{ring[i % S], L};
+        qk_tile(qf, tl, sc);
         mask_window<false>(sc, need_lo, need_hi, lo, hi, unused);
-        softmax_pv(sc, Vs[cur], a.scale_log2, st);
+        softmax_pv(sc, tl, a.scale_log2, st);
       }
-      if (more) store_tile(nxt, Ks[cur ^ 1], Vs[cur ^ 1]);
-      __syncthreads();
     }
     float lt = st.l;
     lt += __shfl_xor(lt, 16, 64);
@@ -440,29 +504,49 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
       for (int db = 0; db < 4; ++db)
         *reinterpret_cast<f32x4_t*>(pr + 4 + 16 * db + 4 * g) = st.acc[db];
     }
+    // every wave is done with the ring before the next chunk's requests
+    __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------------
 // Pass 2: window + prototype keys per segment of consecutive rows
 // ---------------------------------------------------------------------
-// Occupancy: at most 128 VGPRs so that four 4-wave workgroups (about 150 KB
-// of LDS) share a CU; the few registers the compiler spills at that limit
-// cost less than the latency the fourth workgroup hides.
-template <bool COUNT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
+// Key tiles reach LDS by DMA into a ring of S stages: tile i + S - 1 is
+// requested when tile i starts, so S - 1 tiles are in flight while one is
+// computed, and no registers hold tiles in transit.
+// Occupancy: S = 2 stages (32 KB) allow four workgroups per CU and 128
+// VGPRs; S = 3 (48 KB) three workgroups and 168 VGPRs.  Measured at
+// config 3, four workgroups of two stages beat three of three: the pass is
+// bound by instruction latency more than by the tile transfers.
+#ifndef PFA_MAIN_STAGES
+#define PFA_MAIN_STAGES 2
+#endif
+constexpr int kMainStages = PFA_MAIN_STAGES;
+template <int S>
+struct MainOcc;
+template <>
+struct MainOcc<2> {
+  static constexpr int kWaves = 4;
+};
+template <>
+struct MainOcc<3> {
+  static constexpr int kWaves = 3;
+};
+
+template <bool COUNT, int S>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MainOcc<S>::kWaves, 8)))
 short_main_kernel(ShortArgs a, int use_part, int pcap) {
-  __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
-  __shared__ __align__(16) uint16_t Vs[2][kTile * kLd];
+  __shared__ __align__(16) uint16_t ring[S][2 * kTileElems];
   __shared__ int32_t r_t[kRows];
   __shared__ int32_t r_p[kRows];
   __shared__ int32_t seg_begin[kRows + 1];
   __shared__ int s_nseg;
-  __shared__ int s_plen;
-  __shared__ int s_wcnt[4];
-  __shared__ int s_has0;
-  // prototype key list of the current segment: position, evict, position mod stride
-  extern __shared__ int32_t pdyn[];
+  __shared__ int s_cnt[2][4];
+  __shared__ int s_pe0;
+  // prototype key list of the current segment: position, evict, position mod
+  // stride (-1 without anchors); pcap is a multiple of the tile size
+  extern __shared__ __align__(16) int32_t pdyn[];
   int32_t* pk = pdyn;
   int32_t* pe = pk + pcap;
   int32_t* pm = pe + pcap;
@@ -473,29 +557,50 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int w = a.local_w;
   const int sa = a.stride, sl = a.slots;
-  if (tid < kRows) {
-    const int64_t r = r0 + tid;
-    r_t[tid] = r < a.N ? a.token_idx[r] : -1;
-    r_p[tid] = r < a.N ? a.row_head[r] : -1;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int n = 0;
-    int i = 0;
-    while (i < kRows && r_t[i] >= 0) {
-      seg_begin[n++] = i;
-      const int t0 = r_t[i];
-      const int p0 = r_p[i];
-      ++i;
-      while (i < kRows && r_t[i] >= 0 && r_p[i] == p0 && r_t[i] - t0 < w) ++i;
+  SwzLane L;
+  L.init();
+  // segments, found by the first wave: rows are ordered by (head, token)
+  // with absent rows last, so "row j ends the segment begun at row i"
+  // (absent, another head, or t_j - t_i >= w) is monotone in j > i; each
+  // lane binary-searches its successor and lane 0 follows the chain from
+  // row 0.
+  if (wid == 0) {
+    const int64_t r = r0 + lane;
+    const int t = r < a.N ? a.token_idx[r] : -1;
+    const int pp = r < a.N ? a.row_head[r] : -1;
+    r_t[lane] = t;
+    r_p[lane] = pp;
+    int lo = lane + 1, hi = kRows;
+#pragma unroll
+    for (int step = 0; step < 6; ++step) {
+      const int mid = (lo + hi) >> 1;
+      const int tj = __shfl(t, mid & 63, 64), pj = __shfl(pp, mid & 63, 64);
+      const bool ends = mid >= kRows || tj < 0 || pj != pp || tj - t >= w;
+      if (lo < hi) {
+        if (ends) hi = mid;
+        else lo = mid + 1;
+      }
     }
-    seg_begin[n] = i;
-    s_nseg = n;
+    int n = 0, i = 0;
+    while (i < kRows && __shfl(t, i, 64) >= 0) {
+      if (lane == 0) seg_begin[n] = i;
+      ++n;
+      i = __shfl(lo, i, 64);
+    }
+    if (lane == 0) {
+      seg_begin[n] = i;
+      s_nseg = n;
+      s_pe0 = -1;
+    }
   }
   __syncthreads();
   const int nseg = s_nseg;
   const int qs = 16 * wid + (lane & 15);
   const int g = lane >> 4;
+  const int drow = tid >> 3;  // this thread's DMA rows: drow and drow + 32
+  // LDS byte address of stage 0 plus this wave's 1 KB run (wave-uniform)
+  const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + 1024u * (uint32_t)wid);
+  constexpr uint32_t kStageBytes = 2 * kTileElems * 2;
 
   for (int sg = 0; sg < nseg; ++sg) {
     const int s0 = seg_begin[sg], s1 = seg_begin[sg + 1];
@@ -507,88 +612,129 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
     const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
     const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
-    // the segment's first key tile (window keys from lo_first) is fetched
-    // now, so its loads overlap the prototype list and the q row
-    const TileRegs first = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, min(lo_first + (tid >> 2), t_last));
+    // the segment's first key tile (window keys from lo_first) is requested
+    // now, so its transfer overlaps the prototype list
+    const int nw = (t_last - lo_first) / kTile + 1;
+    dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, min(lo_first + drow, t_last), min(lo_first + drow + 32, t_last),
+             ring_w);
+    const bool qv = qs >= s0 && qs < s1;
+    const int tq = qv ? r_t[qs] : t_first;
 
     // prototype key list: the prefix set of t_first below lo_last (set table
     // row of t_first's block -- any order, INT32_MAX-padded -- then the
-    // block's tokens up to t_first, keeping p with evict[p] > t_first), then
-    // key 0 for the zero-anchor rule.  All 256 threads take one candidate
-    // each (the evict lookups of a segment are one round of loads) and
-    // compact the kept ones through per-wave counts.
-    if (tid == 0) {
-      s_plen = 0;
-      s_has0 = 0;
-    }
-    __syncthreads();
+    // block's tokens up to t_first, keeping p with evict[p] > t_first).
+    // Each thread takes two candidates per pass (their set-table and evict
+    // loads are one round each); kept keys are compacted in a fixed order
+    // (candidate half, then wave, then lane) from per-wave counts, so the
+    // list, and the summation order, is the same on every run.  Slot 0 is
+    // kept for key 0 (the zero-anchor rule may need it whether or not it is
+    // in the set; pe = -1 when it is not), so the mask tests the
+    // zero-anchor rule on that one slot only.
+    const bool anch_on = sa > 0 && sl > 0;
+    const bool rsv = a.blk != nullptr || (lo_last > 0 && anch_on);
+    int plen = rsv ? 1 : 0;
     if (a.blk != nullptr) {
       const int64_t jb = t_first >> 6;
       const int32_t* P = a.blk + (bb * a.nblk + jb) * a.K;
       const int32_t* ev = a.evict + bb * a.T;
       const int ncand = a.K + 64;
-      for (int base = 0; base < ncand; base += 256) {
-        const int e = base + tid;
-        int32_t v = INT32_MAX;
-        if (e < a.K) {
-          v = P[e];
-        } else if (e < ncand) {
-          const int q = (int)(jb << 6) + (e - a.K);
-          if (q <= t_first) v = q;
+      const uint64_t below = (1ull << lane) - 1ull;
+      for (int base = 0; base < ncand; base += 512) {
+        int32_t v[2], evv[2];
+        bool keep[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int e = base + 256 * h + tid;
+          v[h] = INT32_MAX;
+          if (e < a.K) {
+            v[h] = P[e];
+          } else if (e < ncand) {
+            const int q = (int)(jb << 6) + (e - a.K);
+            if (q <= t_first) v[h] = q;
+          }
         }
-        bool keep = false;
-        int32_t evv = 0;
-        if (v < lo_last) {
-          evv = ev[v];
-          keep = evv > t_first;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) evv[h] = v[h] < lo_last ? ev[v[h]] : 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          keep[h] = v[h] < lo_last && evv[h] > t_first;
+          if (keep[h] && v[h] == 0) {
+            s_pe0 = evv[h];  // key 0 is in the set: its slot carries the evict
+            keep[h] = false;
+          }
         }
-        const uint64_t bal = __ballot(keep);
-        if (lane == 0) s_wcnt[wid] = __popcll(bal);
-        if (keep && v == 0) s_has0 = 1;
+        const uint64_t b0 = __ballot(keep[0]), b1 = __ballot(keep[1]);
+        if (lane == 0) {
+          s_cnt[0][wid] = __popcll(b0);
+          s_cnt[1][wid] = __popcll(b1);
+        }
         __syncthreads();
-        int before = s_plen;
-        for (int w2 = 0; w2 < wid; ++w2) before += s_wcnt[w2];
-        if (keep) {
-          const int pos = before + __popcll(bal & ((1ull << lane) - 1ull));
-          pk[pos] = v;
-          pe[pos] = evv;
-          pm[pos] = sa > 0 ? v % sa : 0;
+        int off[2] = {plen, plen};
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2) {
+          off[0] += w2 < wid ? s_cnt[0][w2] : 0;
+          off[1] += s_cnt[0][w2] + (w2 < wid ? s_cnt[1][w2] : 0);
+          plen += s_cnt[0][w2] + s_cnt[1][w2];
         }
-        __syncthreads();
-        if (tid == 0) s_plen += s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (keep[h]) {
+            const int pos = off[h] + __popcll((h ? b1 : b0) & below);
+            pk[pos] = v[h];
+            pe[pos] = evv[h];
+            pm[pos] = anch_on ? v[h] % sa : -1;
+          }
+        if (tid == 0 && rsv && base + 512 >= ncand) {
+          pk[0] = 0;
+          pe[0] = s_pe0;
+          pm[0] = anch_on ? 0 : -1;
+          s_pe0 = -1;
+        }
         __syncthreads();
       }
+    } else if (rsv) {
+      if (tid == 0) {
+        pk[0] = 0;
+        pe[0] = -1;
+        pm[0] = anch_on ? 0 : -1;
+      }
+      __syncthreads();
     }
-    if (tid == 0 && lo_last > 0 && sa > 0 && sl > 0 && !s_has0) {
-      // order inside the list does not matter
-      const int n = s_plen;
-      pk[n] = 0;
-      pe[n] = -1;  // not in the prototype set: only the zero-anchor rule applies
-      pm[n] = 0;
-      s_plen = n + 1;
+    // pad the last prototype tile: pk = INT32_MAX fails every row's test
+    // (the tile loop's first barrier orders these writes before any read)
+    {
+      const int pend = (plen + kTile - 1) / kTile * kTile;
+      if (plen + tid < pend) pk[plen + tid] = INT32_MAX;
     }
-    __syncthreads();
-    const int plen = s_plen;
 
     // this lane's query row
-    const bool qv = qs >= s0 && qs < s1;
-    const int tq = qv ? r_t[qs] : t_first;
     const int loq = (int)win_lo(tq, w);
-    const bool zf = qv && zero_anchor(tq, sa, sl) && loq > 0;
-    const bool anch_on = sa > 0 && sl > 0;
-    const int tmod = sa > 0 ? tq % sa : 0;
-    const int64_t alo = (int64_t)tq - (int64_t)sa * sl;  // strided anchors lie in [alo, tq)
+    // prototype test of key p for this row (t = tq): p < win_lo(t), i.e.
+    // p <= t - w; evict[p] > t; not a strided anchor of t (p = t mod s and
+    // p >= t - s*slots); or key 0 under the zero-anchor rule (slot 0)
+    const int p_tw = qv ? tq - w : -1 - w;  // a row that is not there takes no key
+    const int p_tmod = sa > 0 ? tq % sa : 0;
+    const int p_ts = anch_on ? (int)max((int64_t)tq - (int64_t)sa * sl, (int64_t)INT32_MIN + 1) : INT32_MAX;
+    const bool p_zero = qv && zero_anchor(tq, sa, sl);
     // one pipelined pass over the window tiles [lo_first, t_last] and the
-    // prototype tiles: tile i+1 is fetched while tile i is computed
-    const int nw = (t_last - lo_first) / kTile + 1;
+    // prototype tiles
     const int ntile = nw + (plen + kTile - 1) / kTile;
-    const int jrow = tid >> 2;
-    auto key_of = [&](int i) -> int64_t {
-      if (i < nw) return min(lo_first + kTile * i + jrow, t_last);
-      return pk[min((i - nw) * kTile + jrow, plen - 1)];
+    auto key_of = [&](int i, int r) -> int {
+      if (i < nw) return min(lo_first + kTile * i + r, t_last);
+      return pk[min((i - nw) * kTile + r, plen - 1)];
     };
+    auto request = [&](int i) {
+      dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, key_of(i, drow), key_of(i, drow + 32),
+               ring_w + kStageBytes * (uint32_t)(i % S));
+    };
+#pragma unroll
+    for (int i = 1; i < S - 1; ++i)
+      if (i < ntile) request(i);
     bf16x8_t qf[2];
     load_q_row(a, qb, tq, qf);
+    // settle the q fragments here: the tile loop then holds no load the
+    // compiler would wait for (its wait would also drain the tile requests)
+    asm volatile("" : "+v"(qf[0]), "+v"(qf[1]));
     QState st;
     init_state(st);
 
@@ -600,46 +746,46 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const int w_tlo = wave_rows ? r_t[fr] : 0, w_thi = wave_rows ? r_t[lr] : -1;
     const int w_llo = (int)win_lo(w_tlo, w), w_lhi = (int)win_lo(w_thi < 0 ? 0 : w_thi, w);
 
-    store_tile(first, Ks[0], Vs[0]);
-    __syncthreads();
     for (int i = 0; i < ntile; ++i) {
-      const int cur = i & 1;
-      TileRegs nxt;
-      const bool more = i + 1 < ntile;
-      if (more) nxt = fetch_tile(kb, vb, a.k.s_t, a.v.s_t, key_of(i + 1));
+      // tile i has landed (tiles i+1 .. i+S-2 may still be in flight) and
+      // every wave is done with tile i-1, whose stage takes tile i+S-1
+      if (S == 3 && i + 1 < ntile)
+        dma_wait_barrier<kDmaPerTile>();
+      else
+        dma_wait_barrier<0>();
+      if (i + S - 1 < ntile) request(i + S - 1);
+      const SwzTile tl{ring[i % S], L};
       const bool is_win = i < nw;
       const int k0 = lo_first + kTile * i;
       const bool active = is_win ? (wave_rows && k0 <= w_thi && k0 + kTile - 1 >= w_llo) : wave_rows;
       if (active) {
         float sc[4][4];
-        qk_tile(qf, Ks[cur], sc);
+        qk_tile(qf, tl, sc);
         if (is_win) {
           // the row's window keys in the tile: [loq - k0, tq - k0]
           const bool need_lo = !wave_full || k0 < w_lhi;
           const bool need_hi = !wave_full || k0 + kTile - 1 > w_tlo;
           mask_window<COUNT>(sc, need_lo, need_hi, qv ? loq - k0 : kTile, tq - k0, st.cnt);
         } else {
-          const int j0 = (i - nw) * kTile;
-          const int g4 = 4 * g;
+          const int j0 = (i - nw) * kTile + 4 * g;
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
+          for (int kb = 0; kb < 4; ++kb) {
+            const int4 kp = *reinterpret_cast<const int4*>(pk + j0 + 16 * kb);
+            const int4 ke = *reinterpret_cast<const int4*>(pe + j0 + 16 * kb);
+            const int4 km = *reinterpret_cast<const int4*>(pm + j0 + 16 * kb);
+            const int kpv[4] = {kp.x, kp.y, kp.z, kp.w}, kev[4] = {ke.x, ke.y, ke.z, ke.w},
+                      kmv[4] = {km.x, km.y, km.z, km.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const int j = j0 + 16 * kb + g4 + e;
-              bool ok = false;
-              if (qv && j < plen) {
-                const int kp = pk[j];
-                const bool anchor = anch_on && pm[j] == tmod && kp >= alo;
-                ok = kp < loq && ((pe[j] > tq && !anchor) || (kp == 0 && zf));
-              }
+              bool ok = kpv[e] <= p_tw && kev[e] > tq && !(kmv[e] == p_tmod && kpv[e] >= p_ts);
+              if (kb == 0 && e == 0) ok = ok || (p_zero && j0 == 0 && p_tw >= 0);
               sc[kb][e] = ok ? sc[kb][e] : -INFINITY;
               if constexpr (COUNT) st.cnt += ok ? 1 : 0;
             }
+          }
         }
-        softmax_pv(sc, Vs[cur], a.scale_log2, st);
+        softmax_pv(sc, tl, a.scale_log2, st);
       }
-      if (more) store_tile(nxt, Ks[cur ^ 1], Vs[cur ^ 1]);
-      __syncthreads();
     }
 
     // merge the anchor partial, normalise, write
@@ -724,6 +870,8 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
     return ((uintptr_t)x.ptr % 16) == 0 && x.s_b % 8 == 0 && x.s_h % 8 == 0 && x.s_t % 8 == 0;
   };
   PFA_CHECK_ARG(al(q) && al(k) && al(v) && al(out), "pfa_shortlist_attn_fwd: tensors must be 16-byte aligned");
+  PFA_CHECK_ARG(k.s_t > 0 && v.s_t > 0 && k.s_t < INT32_MAX && v.s_t < INT32_MAX,
+                "pfa_shortlist_attn_fwd: k/v token strides must be positive and below 2^31");
   PFA_CHECK_ARG((q_rope_cos == nullptr) == (q_rope_sin == nullptr),
                 "pfa_shortlist_attn_fwd: q_rope_cos and q_rope_sin go together");
   PFA_CHECK_ARG(q_rope_cos == nullptr || (((uintptr_t)q_rope_cos | (uintptr_t)q_rope_sin) & 15) == 0,
@@ -747,11 +895,14 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   int64_t blocks = (N + kRows - 1) / kRows;
   blocks = (blocks + 7) / 8 * 8;
   PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_shortlist_attn_fwd: too many rows");
-  const int pcap = (proto_blocks ? proto_k : 0) + 64 + 1;
+  // prototype slots: key 0's slot, the set table row, the block's 64 tokens;
+  // rounded up to whole tiles
+  const int pcap = ((proto_blocks ? proto_k : 0) + 64 + 1 + kTile - 1) / kTile * kTile;
+  constexpr int S = kMainStages;
   if (lengths != nullptr)
-    short_main_kernel<true><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
+    short_main_kernel<true, S><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
   else
-    short_main_kernel<false><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
+    short_main_kernel<false, S><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
   PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/main");
   return PFA_OK;
 }
