@@ -250,10 +250,11 @@ __device__ __forceinline__ void mask_window(float (&s)[4][4], bool need_lo, bool
 }
 
 // Online softmax (exp2 on v_exp_f32 directly: arguments are <= 0, -inf
-// gives 0) and O^T += V^T P^T with P rounded to bf16 (v_cvt_pk_bf16_f32,
-// round to nearest even).
-template <typename Tile>
-__device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, float scale_log2, QState& st) {
+// gives 0): updates the running max / sum (rescaling the accumulator when
+// the max rises) and returns P rounded to bf16 (v_cvt_pk_bf16_f32, round to
+// nearest even) as the two B operands of the P.V product, pb[kc] holding
+// keys 32kc + 4g + (0..3) and 32kc + 16 + 4g + (0..3).
+__device__ __forceinline__ void softmax_p(float (&s)[4][4], float scale_log2, QState& st, bf16x8_t (&pb)[2]) {
   float tmax = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
@@ -297,20 +298,32 @@ __device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, floa
       pv[i] = (__bf16)s[2 * kc][i];
       pv[4 + i] = (__bf16)s[2 * kc + 1][i];
     }
-    bf16x8_t pb;
-    __builtin_memcpy(&pb, pv, 16);
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      // A operand V^T: lane (dim 16db + r16, g) holds the keys of pb's
-      // slots, 32kc + 4g + (0..3) and 32kc + 16 + 4g + (0..3)
-      const i16x4_t lo = ds_tr4(t.vtr(kc, 0, db));
-      const i16x4_t hi = ds_tr4(t.vtr(kc, 1, db));
-      bf16x8_t va;
-      __builtin_memcpy(&va, &lo, 8);
-      __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
-      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, st.acc[db], 0, 0, 0);
-    }
+    __builtin_memcpy(&pb[kc], pv, 16);
   }
+}
+
+// A operand V^T of the P.V product: lane (dim 16db + r16, g) holds keys
+// 32kc + 4g + (0..3) and 32kc + 16 + 4g + (0..3), matching pb[kc].
+template <typename Tile>
+__device__ __forceinline__ bf16x8_t v_frag(const Tile& t, int kc, int db) {
+  const i16x4_t lo = ds_tr4(t.vtr(kc, 0, db));
+  const i16x4_t hi = ds_tr4(t.vtr(kc, 1, db));
+  bf16x8_t va;
+  __builtin_memcpy(&va, &lo, 8);
+  __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
+  return va;
+}
+
+// Softmax and O^T += V^T P^T for one 16-row group.
+template <typename Tile>
+__device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, float scale_log2, QState& st) {
+  bf16x8_t pb[2];
+  softmax_p(s, scale_log2, st, pb);
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_frag(t, kc, db), pb[kc], st.acc[db], 0, 0, 0);
 }
 
 __device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[2]) {
@@ -892,12 +905,12 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
     PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
   }
   if (!(passes & 2)) return PFA_OK;
-  int64_t blocks = (N + kRows - 1) / kRows;
-  blocks = (blocks + 7) / 8 * 8;
-  PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_shortlist_attn_fwd: too many rows");
   // prototype slots: key 0's slot, the set table row, the block's 64 tokens;
   // rounded up to whole tiles
   const int pcap = ((proto_blocks ? proto_k : 0) + 64 + 1 + kTile - 1) / kTile * kTile;
+  int64_t blocks = (N + kRows - 1) / kRows;
+  blocks = (blocks + 7) / 8 * 8;
+  PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_shortlist_attn_fwd: too many rows");
   constexpr int S = kMainStages;
   if (lengths != nullptr)
     short_main_kernel<true, S><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);

@@ -1189,13 +1189,20 @@ class AdaptiveSparseAttention(nn.Module):
         self._last_gate_probs = gate_probs
         # the prototype EMA (aspa.py:692-718) reads only this forward's router
         # outputs and is read only by the next forward's router: it is queued
-        # last before the streams join (on the structured path, after the
-        # prototype tables)
+        # last before the streams join (on the structured path, on the forked
+        # stream after the anchor pass, beside the main pass)
 
 
-        def ema() -> None:
+        def ema(stream: Optional[torch.cuda.Stream] = None) -> None:
             # the router's tail: the prototype EMA and the telemetry reduction
-            # (both read only router outputs; neither is read in this forward)
+            # (both read only router outputs; neither is read in this forward).
+            # `stream`: queued on that (forked) stream, which then also uses
+            # tensors allocated on this one
+            if stream is not None and not capture:
+                fused = getattr(self, "_ema_partial", None)
+                if fused is not None:
+                    fused[0].record_stream(stream)
+                comb.record_stream(stream)
             self._update_routing_prototypes(x, gate_probs)
             _hip.check(lib.pfa_router_stats_reduce(_hip.ptr(router_stats), int(router_stats.size(0)), _hip.ptr(comb),
                                                    _hip.stream_ptr(device)), "pfa_router_stats_reduce")
@@ -1409,12 +1416,13 @@ class AdaptiveSparseAttention(nn.Module):
 
         streams = (main, fork): qkv and attn come from work queued on the
         fork stream; the structured path queues its anchor pass there too
-        (after the packing on main) while main builds the prototype tables
-        and runs `before_join`; main then waits for the fork stream before
-        the main pass.  The other paths are entered with the fork
-        stream already joined.  The prototype tables are queued before the
-        anchor pass so that, in a captured graph, they follow the packing on
-        its queue instead of starting on another one."""
+        (after the packing on main) followed by `before_join(fork)`, while
+        main builds the prototype tables; main waits for the anchor pass
+        before the main pass and joins the fork stream after it.  The other
+        paths are entered with the fork stream already joined.  The
+        prototype tables are queued before the anchor pass so that, in a
+        captured graph, they follow the packing on its queue instead of
+        starting on another one."""
         H, D = self.h_total, self.d_head
         device = qkv.device
         if plan is None:
@@ -1442,21 +1450,34 @@ class AdaptiveSparseAttention(nn.Module):
             blocks = evict = None
             if K > 0:
                 blocks, evict = _sa._proto_prefix_blocks(self._last_token_similarity, K)
+            tail_on_fork = False
             if packed is not None:
                 fork_s = streams[1]
                 fork_s.wait_event(packed)
-                # anchor pass on the fork stream
+                # anchor pass on the fork stream, then `before_join` there:
+                # the main pass waits for the anchor pass only, and the tail
+                # runs beside it
                 with torch.cuda.stream(fork_s):
                     _sa._shortlist_attn_structured(*t4, *args, None, None, scale, device, want_lengths=False,
                                                    q_rope=q_rope, passes=1, part=part)
-            if before_join is not None:
-                before_join()
-            if streams is not None:
-                streams[0].wait_stream(streams[1])
+                    anchored = torch.cuda.Event()
+                    anchored.record(fork_s)
+                    if before_join is not None:
+                        before_join(fork_s)
+                        tail_on_fork = True
+                streams[0].wait_event(anchored)
+            else:
+                if before_join is not None:
+                    before_join()
+                if streams is not None:
+                    streams[0].wait_stream(streams[1])
             passes = 2 if (part is not None and streams is not None) else 3
             lens = _sa._shortlist_attn_structured(
                 *t4, *args, blocks, evict, scale, device, want_lengths=bool(self.record_shortlist_lengths),
                 q_rope=q_rope, passes=passes, part=part)
+            if tail_on_fork:
+                # join: the forward ends after the tail
+                streams[0].wait_stream(streams[1])
             self._last_shortlist_lengths = lens
             _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
                             quantized=False, candidates=True, structured=True)
