@@ -1193,6 +1193,8 @@ class AdaptiveSparseAttention(nn.Module):
         # stream after the anchor pass, beside the main pass)
 
 
+        heads64 = [None]
+
         def ema(stream: Optional[torch.cuda.Stream] = None) -> None:
             # the router's tail: the prototype EMA and the telemetry reduction
             # (both read only router outputs; neither is read in this forward).
@@ -1204,6 +1206,9 @@ class AdaptiveSparseAttention(nn.Module):
                     fused[0].record_stream(stream)
                 comb.record_stream(stream)
             self._update_routing_prototypes(x, gate_probs)
+            # the int64 active-head list of the sparse state, made here (off the
+            # critical path) rather than when the telemetry is read
+            heads64[0] = active_heads.to(torch.int64)
             _hip.check(lib.pfa_router_stats_reduce(_hip.ptr(router_stats), int(router_stats.size(0)), _hip.ptr(comb),
                                                    _hip.stream_ptr(device)), "pfa_router_stats_reduce")
         if sim is not None:
@@ -1332,7 +1337,8 @@ class AdaptiveSparseAttention(nn.Module):
             backend_info = self._last_shortlist_backend_info or get_last_backend_info()
             state = {
                 "mode": mode_label, "backend": str(backend_info.get("name", "shortlist")),
-                "active_head_indices": heads, "head_idx": rh, "token_idx": tok,
+                "active_head_indices": heads if heads64[0] is None else heads64[0], "head_idx": rh,
+                "token_idx": tok,
                 "row_offsets": row_offsets, "max_rows": int(max_rows), "density": density_est,
                 "target_k": int(topk),
                 "force_dense_threshold": None if density_threshold is None else float(density_threshold),
