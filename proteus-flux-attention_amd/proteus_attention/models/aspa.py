@@ -455,6 +455,13 @@ class AdaptiveSparseAttention(nn.Module):
         # structured shortlist path: rotate q rows inside the attention kernel
         # (only k is rotated in the QKV buffer); False rotates q in the buffer
         self.fuse_q_rope = True
+        # The prototype EMA statistics (sum_t gate * x) are accumulated inside
+        # the router pass (x is read from HBM once); False accumulates them by
+        # a separate pass over x in the router's tail instead.  Both give the
+        # same sums (same 64-token parts, same token order).  Measured at
+        # config 3 the separate pass shortens the router by ~20 us but, beside
+        # the main attention pass, slows it by more.
+        self.fuse_ema_stats = True
 
     # ------------------------------------------------------------------
     # RoPE tables (aspa.py:576-604)
@@ -789,10 +796,11 @@ class AdaptiveSparseAttention(nn.Module):
         nblk = _hip.ctypes.c_int(0)
         _hip.check(lib.pfa_router_block_count(n_tok, _hip.ctypes.byref(nblk)), "pfa_router_block_count")
         stats = torch.empty(max(1, nblk.value), 8, dtype=torch.float32, device=device)
-        # prototype EMA statistics accumulated in the same pass over x
-        # (consumed by _update_routing_prototypes at the end of the forward)
+        # prototype EMA statistics accumulated in the same pass over x when
+        # fuse_ema_stats is set (consumed by _update_routing_prototypes at the
+        # end of the forward; otherwise that step accumulates them itself)
         ema = None
-        if self._ema_active():
+        if self._ema_active() and self.fuse_ema_stats:
             ema = torch.empty(max(1, nblk.value), G, C + 1, dtype=torch.float32, device=device)
         self._ema_partial = (ema, x2d.data_ptr(), n_tok) if ema is not None else None
         g2h = self._gate_to_head_i32(device)
@@ -1205,6 +1213,8 @@ class AdaptiveSparseAttention(nn.Module):
                 if fused is not None:
                     fused[0].record_stream(stream)
                 comb.record_stream(stream)
+                x.record_stream(stream)
+                gate_probs.record_stream(stream)
             self._update_routing_prototypes(x, gate_probs)
             # the int64 active-head list of the sparse state, made here (off the
             # critical path) rather than when the telemetry is read

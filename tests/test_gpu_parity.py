@@ -535,6 +535,32 @@ def test_rope_kernel_bitwise(dev, dt, B, T, H, D, k_only):
     assert torch.equal(got[:, :, 2], ref[:, :, 2])
 
 
+@pytest.mark.parametrize("T,B", [(4096, 1), (3000, 2)])
+def test_ema_stats_fused_or_separate_bitwise(dev, T, B):
+    """The prototype EMA statistics accumulated inside the router pass or by
+    the separate pass in the router's tail give bit-identical prototypes,
+    usage and confidence (same 64-token parts, same token order)."""
+    from configs import shortlist_cfg
+
+    _say(f"EMA stats fused vs separate T={T} B={B}")
+    cfg = shortlist_cfg(T, 512, 8, 1024, 256, 64)
+    m, x = _module(cfg, B, T, 512, torch.bfloat16, dev, 0.01)
+    snap = {n: b.detach().clone() for n, b in m.named_buffers() if n.startswith("routing_")}
+    got = []
+    with torch.no_grad():
+        for fused in (True, False):
+            for n, b in snap.items():
+                getattr(m, n).copy_(b)
+            m.fuse_ema_stats = fused
+            for _ in range(2):
+                y = m(x)
+            got.append(({n: getattr(m, n).clone() for n in snap}, y.clone()))
+    for n in snap:
+        assert not torch.equal(got[0][0][n], snap[n]) or n != "routing_prototypes"
+        assert torch.equal(got[0][0][n], got[1][0][n]), n
+    assert torch.equal(got[0][1], got[1][1])
+
+
 @pytest.mark.parametrize("T,L,w,s,B", [(4096, 1024, 256, 64, 1), (3000, 700, 100, 37, 2)])
 def test_structured_fused_q_rope_bitwise(dev, T, L, w, s, B):
     """q rows rotated as the structured kernel loads them give exactly the
