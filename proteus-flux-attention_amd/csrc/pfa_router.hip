@@ -390,55 +390,93 @@ __host__ __device__ constexpr int rm_region0(int C) {
   return (64 * C > kRmWaves * 64 * kRmEpW * 4) ? 64 * C : kRmWaves * 64 * kRmEpW * 4;
 }
 
-// Prototype EMA statistics of one 64-token group, one wave: lane owns the
-// eight channels cb + 8*lane .. +7 (one 16-byte load per token), gate rows
-// from LDS; every sum runs in token order.
-template <int GP>
-__device__ __forceinline__ void ema_accum_rows_bf16(const uint16_t* __restrict__ x, int64_t tok0, int nt, int C,
-                                                    int G, const float* gl, float* __restrict__ part) {
-  const int lane = threadIdx.x & 63;
-  for (int cb = 0; cb < C; cb += 512) {
-    const int c = cb + 8 * lane;
-    const bool has = c < C;
-    float a[8][GP];
+// Prototype EMA statistics of one 64-token group, one wave, on MFMA:
+// part[g][c] = sum_t gate[t][g] * x[t][c].  D = A.B with v_mfma_f32_16x16x32_bf16,
+// A = gates (rows) x tokens (k), B = tokens (k) x 16 channels.  A gate
+// g = hi + mid + lo is split into three bf16 parts (as the router's
+// prototype table: every difference exact, the parts carry g's whole
+// significand), so every product with a bf16 x is exact in f32; A1 holds hi
+// in rows 0-7 and mid in rows 8-15, A2 lo in rows 0-7.  The x rows are
+// staged in LDS 64 channels at a time (rows padded to kXsLd elements: the
+// four rows of a transpose read fall in disjoint banks) and read as B by the
+// LDS transpose read; gl holds the wave's gates [token][GP].
+constexpr int kXsLd = 80;                          // staged x row, bf16 elements
+constexpr int kXsWave = 64 * kXsLd * 2;            // bytes per wave
+__host__ __device__ constexpr int rm_region_a(int C) {
+  return rm_region0(C) > kRmWaves * kXsWave ? rm_region0(C) : kRmWaves * kXsWave;
+}
+__device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, int64_t tok0, int nt, int C, int G,
+                                               const float* gl, float* __restrict__ part, uint16_t* xs) {
+  typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+  typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+  typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+  constexpr int GP = 8;
+  const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
+  // A operands for the two 32-token k-steps
+  bf16x8 a1[2], a2[2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+  for (int ks = 0; ks < 2; ++ks) {
+    uint16_t h1[8], h2[8];
 #pragma unroll
-      for (int g = 0; g < GP; ++g) a[j][g] = 0.f;
-    for (int u0 = 0; u0 < nt; u0 += 16) {
-      uint4 xv[16];
+    for (int j = 0; j < 8; ++j) {
+      const float gv = gl[(32 * ks + 8 * kg + j) * GP + (m & 7)];
+      const uint16_t hi = f32_to_bf16(gv);
+      const float r1 = gv - bf16_to_f32(hi);
+      const uint16_t mid = f32_to_bf16(r1);
+      const uint16_t lo = f32_to_bf16(r1 - bf16_to_f32(mid));
+      h1[j] = m < 8 ? hi : mid;
+      h2[j] = m < 8 ? lo : (uint16_t)0;
+    }
+    __builtin_memcpy(&a1[ks], h1, 16);
+    __builtin_memcpy(&a2[ks], h2, 16);
+  }
+  // staging: lane l moves 16 bytes (channels 8*(l%8) ..+7) of tokens 8i + l/8
+  const int srow = lane >> 3, scol = 8 * (lane & 7);
+  auto fetch = [&](int cc, uint4 (&r)[8]) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k)
-        xv[k] = (has && u0 + k < nt) ? *reinterpret_cast<const uint4*>(x + (tok0 + u0 + k) * C + c)
-                                     : make_uint4(0u, 0u, 0u, 0u);
+    for (int i = 0; i < 8; ++i) {
+      const int t = 8 * i + srow;
+      r[i] = t < nt ? *reinterpret_cast<const uint4*>(x + (tok0 + t) * C + 64 * cc + scol) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  uint4 cur[8], nxt[8];
+  fetch(0, cur);
+  const int nc = C / 64;
+  for (int cc = 0; cc < nc; ++cc) {
+    wave_sync();  // the previous chunk's transpose reads are done
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const float4* gr = reinterpret_cast<const float4*>(gl + (u0 + k) * GP);
-        float gv[GP];
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(xs + (8 * i + srow) * kXsLd + scol) = cur[i];
+    if (cc + 1 < nc) fetch(cc + 1, nxt);
+    wave_sync();
 #pragma unroll
-        for (int q = 0; q < GP / 4; ++q) {
-          const float4 t = gr[q];
-          gv[4 * q] = t.x; gv[4 * q + 1] = t.y; gv[4 * q + 2] = t.z; gv[4 * q + 3] = t.w;
-        }
-        const uint32_t w[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+    for (int ct = 0; ct < 4; ++ct) {
+      f32x4 d1 = {0.f, 0.f, 0.f, 0.f}, d2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float x0 = __uint_as_float(w[i] << 16), x1 = __uint_as_float(w[i] & 0xffff0000u);
+      for (int ks = 0; ks < 2; ++ks) {
+        // lane (n, kg) gets x[32ks + 8kg + 0..7][16ct + n]
+        const uint16_t* p0 = xs + (32 * ks + 8 * kg + (m >> 2)) * kXsLd + 16 * ct + 4 * (m & 3);
+        const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p0));
+        const s16x4 hi4 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p0 + 4 * kXsLd));
+        bf16x8 b;
+        __builtin_memcpy(&b, &lo4, 8);
+        __builtin_memcpy(reinterpret_cast<char*>(&b) + 8, &hi4, 8);
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[ks], b, d1, 0, 0, 0);
+        d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[ks], b, d2, 0, 0, 0);
+      }
+      // lanes 0-31 hold rows 4*(lane/16) + i: hi (d1) and lo (d2) of gates
+      // 0-7; the mid of the same gates is in d1 of lane + 32
+      const int c = 64 * cc + 16 * ct + m;
 #pragma unroll
-          for (int g = 0; g < GP; ++g) {
-            a[2 * i][g] = __builtin_fmaf(gv[g], x0, a[2 * i][g]);
-            a[2 * i + 1][g] = __builtin_fmaf(gv[g], x1, a[2 * i + 1][g]);
-          }
-        }
+      for (int i = 0; i < 4; ++i) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d1[i]), __float_as_uint(d1[i]), false, false);
+        const int g = 4 * kg + i;
+        if (lane < 32 && g < G) part[(int64_t)g * (C + 1) + c] = (d1[i] + __uint_as_float(sw[1])) + d2[i];
       }
     }
-    if (has) {
+    if (cc + 1 < nc) {
 #pragma unroll
-      for (int g = 0; g < GP; ++g)
-        if (g < G) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) part[(int64_t)g * (C + 1) + c + j] = a[j][g];
-        }
+      for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
     }
   }
 }
@@ -585,7 +623,7 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
                                        blend_out, importance, head_idx, head_score,
                                        group < n_groups ? stats : nullptr, gate);
   if (ema_part != nullptr) {
-    float* gl = reinterpret_cast<float*>(rm_lds + rm_region0(C)) + wid * 64 * GP;
+    float* gl = reinterpret_cast<float*>(rm_lds + rm_region_a(C)) + wid * 64 * GP;
 #pragma unroll
     for (int g = 0; g < GP; ++g) gl[lane * GP + g] = (live && g < G) ? gate[g] : 0.f;
     __syncthreads();
@@ -596,7 +634,9 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
         for (int u = 0; u < 64; ++u) cs += gl[u * GP + lane];
         part[(int64_t)lane * (C + 1) + C] = cs;
       }
-      ema_accum_rows_bf16<GP>(x, tok0, (int)min<int64_t>(64, n_tok - tok0), C, G, gl, part);
+      // the table / staging region is free again: each wave stages its x rows there
+      ema_accum_mfma(x, tok0, (int)min<int64_t>(64, n_tok - tok0), C, G, gl, part,
+                     reinterpret_cast<uint16_t*>(rm_lds + wid * kXsWave));
     }
   }
 }
@@ -872,7 +912,7 @@ static void launch_router_gp(const void* x, int64_t n_tok, int C, int G, const f
   if constexpr (DT == PFA_BF16 && GP == 8) {
     if (C % 128 == 0 && C <= 768) {
       const unsigned mb = (blocks + kRmWaves - 1) / kRmWaves;
-      const size_t lds = (size_t)rm_region0(C) + (size_t)kRmWaves * 64 * GP * sizeof(float);
+      const size_t lds = (size_t)rm_region_a(C) + (size_t)kRmWaves * 64 * GP * sizeof(float);
       router_mfma_kernel<PROTO><<<mb, 64 * kRmWaves, lds, s>>>((const uint16_t*)x, n_tok, C, G, wpk, cw, ub, g2h, H,
                                                                topk, temp, thr, pb, boost, gp, sim, bl, imp, hi, hs,
                                                                stats, ema);

@@ -456,11 +456,10 @@ class AdaptiveSparseAttention(nn.Module):
         # (only k is rotated in the QKV buffer); False rotates q in the buffer
         self.fuse_q_rope = True
         # The prototype EMA statistics (sum_t gate * x) are accumulated inside
-        # the router pass (x is read from HBM once); False accumulates them by
-        # a separate pass over x in the router's tail instead.  Both give the
-        # same sums (same 64-token parts, same token order).  Measured at
-        # config 3 the separate pass shortens the router by ~20 us but, beside
-        # the main attention pass, slows it by more.
+        # the router pass (x is read from HBM once; MFMA with exact products);
+        # False accumulates them by a separate pass over x in the router's
+        # tail instead (token-order f32 sums).  Both give the same sums up to
+        # f32 rounding, in the same 64-token parts.
         self.fuse_ema_stats = True
 
     # ------------------------------------------------------------------

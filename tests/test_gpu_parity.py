@@ -536,10 +536,11 @@ def test_rope_kernel_bitwise(dev, dt, B, T, H, D, k_only):
 
 
 @pytest.mark.parametrize("T,B", [(4096, 1), (3000, 2)])
-def test_ema_stats_fused_or_separate_bitwise(dev, T, B):
-    """The prototype EMA statistics accumulated inside the router pass or by
-    the separate pass in the router's tail give bit-identical prototypes,
-    usage and confidence (same 64-token parts, same token order)."""
+def test_ema_stats_fused_or_separate(dev, T, B):
+    """The prototype EMA statistics accumulated inside the router pass (on
+    MFMA, exact products) or by the separate pass in the router's tail
+    (token-order f32 sums) give the same prototypes, usage and confidence to
+    f32 rounding, and the same routing."""
     from configs import shortlist_cfg
 
     _say(f"EMA stats fused vs separate T={T} B={B}")
@@ -552,13 +553,15 @@ def test_ema_stats_fused_or_separate_bitwise(dev, T, B):
             for n, b in snap.items():
                 getattr(m, n).copy_(b)
             m.fuse_ema_stats = fused
-            for _ in range(2):
-                y = m(x)
-            got.append(({n: getattr(m, n).clone() for n in snap}, y.clone()))
+            y = m(x)
+            got.append(({n: getattr(m, n).float().clone() for n in snap}, y.clone(),
+                        m.last_head_consensus.clone()))
+    assert not torch.equal(got[0][0]["routing_prototypes"], snap["routing_prototypes"].float())
     for n in snap:
-        assert not torch.equal(got[0][0][n], snap[n]) or n != "routing_prototypes"
-        assert torch.equal(got[0][0][n], got[1][0][n]), n
+        torch.testing.assert_close(got[0][0][n], got[1][0][n], rtol=1e-5, atol=1e-6, msg=n)
+    # this forward's routing does not depend on the statistics (they feed the next one)
     assert torch.equal(got[0][1], got[1][1])
+    assert torch.equal(got[0][2], got[1][2])
 
 
 @pytest.mark.parametrize("T,L,w,s,B", [(4096, 1024, 256, 64, 1), (3000, 700, 100, 37, 2)])
