@@ -164,6 +164,9 @@ pack_count_mask(const uint8_t* __restrict__ mask, int64_t T, int nblk, int32_t* 
 
 // Single workgroup: per-row totals, optional compaction of empty rows,
 // row_offsets, and per-(row, tile) base offsets written over blockcounts.
+// Launched with kScanThreads (four waves): a 16-wave workgroup has to wait
+// for a nearly empty CU while the concurrent GEMM fills them.
+constexpr int kScanThreads = 256;
 __global__ void __launch_bounds__(1024)
 pack_scan_kernel(int32_t* __restrict__ blockcounts, int BH, int nblk, int compact, int32_t* __restrict__ totals,
                  int32_t* __restrict__ compact_id, int32_t* __restrict__ active_heads,
@@ -370,7 +373,7 @@ extern "C" int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* t
   pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts,
                                                   row_of_out);
   PFA_CHECK_LAUNCH("pfa_pack_rows/count");
-  pack_scan_kernel<<<1, 1024, 0, s>>>(w.blockcounts, (int)BH, nblk, 1, w.totals, w.compact_id, active_heads_out,
+  pack_scan_kernel<<<1, kScanThreads, 0, s>>>(w.blockcounts, (int)BH, nblk, 1, w.totals, w.compact_id, active_heads_out,
                                       row_offsets_out, summary_out);
   PFA_CHECK_LAUNCH("pfa_pack_rows/scan");
   pack_fill_kernel<<<grid, kPackThreads, 0, s>>>(mask_out, T, nblk, w.blockcounts, w.compact_id, token_idx_out,
@@ -398,7 +401,7 @@ extern "C" int pfa_pack_mask(const uint8_t* mask, int P, int64_t T, int32_t* row
   dim3 grid(nblk, (unsigned)P);
   pack_count_mask<<<grid, kPackThreads, 0, s>>>(mask, T, nblk, w.blockcounts);
   PFA_CHECK_LAUNCH("pfa_pack_mask/count");
-  pack_scan_kernel<<<1, 1024, 0, s>>>(w.blockcounts, P, nblk, 0, w.totals, w.compact_id, nullptr, row_offsets_out,
+  pack_scan_kernel<<<1, kScanThreads, 0, s>>>(w.blockcounts, P, nblk, 0, w.totals, w.compact_id, nullptr, row_offsets_out,
                                       summary_out);
   PFA_CHECK_LAUNCH("pfa_pack_mask/scan");
   pack_fill_kernel<<<grid, kPackThreads, 0, s>>>(mask, T, nblk, w.blockcounts, w.compact_id, token_idx_out,
