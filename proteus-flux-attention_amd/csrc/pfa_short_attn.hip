@@ -550,6 +550,7 @@ struct MainOcc<3> {
 template <bool COUNT, int S>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MainOcc<S>::kWaves, 8)))
 short_main_kernel(ShortArgs a, int use_part, int pcap) {
+  constexpr int kSlots = 16;  // tile slots of the shared window-tile schedule
   __shared__ __align__(16) uint16_t ring[S][2 * kTileElems];
   __shared__ int32_t r_t[kRows];
   __shared__ int32_t r_p[kRows];
@@ -563,6 +564,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
   int32_t* pk = pdyn;
   int32_t* pe = pk + pcap;
   int32_t* pm = pe + pcap;
+  int32_t* ord = pm + pcap;  // tile order of the segment (ordcap entries)
 
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   const int64_t r0 = lb * kRows;
@@ -625,11 +627,21 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
     const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
     const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
-    // the segment's first key tile (window keys from lo_first) is requested
-    // now, so its transfer overlaps the prototype list
-    const int nw = (t_last - lo_first) / kTile + 1;
-    dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, min(lo_first + drow, t_last), min(lo_first + drow + 32, t_last),
-             ring_w);
+    // Window tiles lie on the global 64-key grid (tile k: keys 64k .. 64k+63,
+    // the keys outside [lo_first, t_last] masked).  Every workgroup takes
+    // window tile k in slot k mod kSlots of its tile sequence and fills the
+    // free slots with its prototype tiles: neighbouring workgroups of one
+    // head share most of their window tiles, and taking a shared tile in the
+    // same slot, at about the same time, the later requests find it in L2.
+    const int wA = lo_first >> 6, wB = t_last >> 6;
+    const int nw = wB - wA + 1;
+    // the tile of slot 0, requested now (its transfer overlaps the prototype
+    // list) when it is a window tile
+    const int k_slot0 = wA + ((0 - wA) & (kSlots - 1));
+    const bool early = k_slot0 <= wB;
+    if (early)
+      dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, min(kTile * k_slot0 + drow, t_last),
+               min(kTile * k_slot0 + drow + 32, t_last), ring_w);
     const bool qv = qs >= s0 && qs < s1;
     const int tq = qv ? r_t[qs] : t_first;
 
@@ -729,17 +741,33 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const int p_tmod = sa > 0 ? tq % sa : 0;
     const int p_ts = anch_on ? (int)max((int64_t)tq - (int64_t)sa * sl, (int64_t)INT32_MIN + 1) : INT32_MAX;
     const bool p_zero = qv && zero_anchor(tq, sa, sl);
-    // one pipelined pass over the window tiles [lo_first, t_last] and the
-    // prototype tiles
-    const int ntile = nw + (plen + kTile - 1) / kTile;
+    // one pipelined pass over the tiles in slot order: ord[i] >= 0 is window
+    // tile ord[i], ord[i] < 0 prototype tile -1 - ord[i]
+    const int np = (plen + kTile - 1) / kTile;
+    const int ntile = nw + np;
+    if (tid == 0) {
+      int pos = 0, pj = 0;
+      for (int sl2 = 0; sl2 < kSlots; ++sl2) {
+        int k = wA + ((sl2 - wA) & (kSlots - 1));
+        if (k <= wB) {
+          for (; k <= wB; k += kSlots) ord[pos++] = k;
+        } else if (pj < np) {
+          ord[pos++] = -1 - pj++;
+        }
+      }
+      while (pj < np) ord[pos++] = -1 - pj++;
+    }
+    __syncthreads();
     auto key_of = [&](int i, int r) -> int {
-      if (i < nw) return min(lo_first + kTile * i + r, t_last);
-      return pk[min((i - nw) * kTile + r, plen - 1)];
+      const int d = ord[i];
+      if (d >= 0) return min(kTile * d + r, t_last);
+      return pk[min((-1 - d) * kTile + r, plen - 1)];
     };
     auto request = [&](int i) {
       dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, key_of(i, drow), key_of(i, drow + 32),
                ring_w + kStageBytes * (uint32_t)(i % S));
     };
+    if (!early) request(0);
 #pragma unroll
     for (int i = 1; i < S - 1; ++i)
       if (i < ntile) request(i);
@@ -768,8 +796,9 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
         dma_wait_barrier<0>();
       if (i + S - 1 < ntile) request(i + S - 1);
       const SwzTile tl{ring[i % S], L};
-      const bool is_win = i < nw;
-      const int k0 = lo_first + kTile * i;
+      const int d = ord[i];
+      const bool is_win = d >= 0;
+      const int k0 = kTile * d;
       const bool active = is_win ? (wave_rows && k0 <= w_thi && k0 + kTile - 1 >= w_llo) : wave_rows;
       if (active) {
         float sc[4][4];
@@ -780,7 +809,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
           const bool need_hi = !wave_full || k0 + kTile - 1 > w_tlo;
           mask_window<COUNT>(sc, need_lo, need_hi, qv ? loq - k0 : kTile, tq - k0, st.cnt);
         } else {
-          const int j0 = (i - nw) * kTile + 4 * g;
+          const int j0 = (-1 - d) * kTile + 4 * g;
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb) {
             const int4 kp = *reinterpret_cast<const int4*>(pk + j0 + 16 * kb);
@@ -912,10 +941,14 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   blocks = (blocks + 7) / 8 * 8;
   PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_shortlist_attn_fwd: too many rows");
   constexpr int S = kMainStages;
+  // tile order: the window tiles of a segment (its rows span less than w)
+  // plus the prototype tiles
+  const int ordcap = (2 * local_w + kTile - 1) / kTile + 2 + pcap / kTile;
+  const size_t dyn = (size_t)pcap * 12 + (size_t)ordcap * 4;
   if (lengths != nullptr)
-    short_main_kernel<true, S><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
+    short_main_kernel<true, S><<<(unsigned)blocks, 256, dyn, s>>>(a, anchors ? 1 : 0, pcap);
   else
-    short_main_kernel<false, S><<<(unsigned)blocks, 256, (size_t)pcap * 12, s>>>(a, anchors ? 1 : 0, pcap);
+    short_main_kernel<false, S><<<(unsigned)blocks, 256, dyn, s>>>(a, anchors ? 1 : 0, pcap);
   PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/main");
   return PFA_OK;
 }
