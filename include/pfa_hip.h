@@ -302,6 +302,9 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
  *   2 only the main pass (reads them).  Splitting lets the anchor pass run
  *   on another stream while the prototype tables are built; the caller
  *   orders pass 1 before pass 2 and keeps partials alive between them.
+ *   q, k, v, out: 16-byte aligned with strides multiple of 8 elements; the
+ *   k and v token strides positive and below 2^31 (PFA_E_INVALID otherwise).
+ *   Results are deterministic: the same inputs give the same bits.
  * ==================================================================== */
 int pfa_shortlist_attn_part_floats(void);
 int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
