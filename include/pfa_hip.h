@@ -76,8 +76,12 @@ const char* pfa_last_error_string(void);
  *   ema_partial (n_blocks, G, C+1) f32 or NULL: the prototype EMA statistics
  *     of aspa.py:703-707 fused into the same pass -- per workgroup of 64
  *     tokens, sum_t gate[t,g]*x[t,c] (columns 0..C-1) and sum_t gate[t,g]
- *     (column C) over the final gate probabilities, in token order; reduce
- *     them with pfa_proto_partial_reduce(ema_partial, n_blocks, ...).
+ *     (column C) over the final gate probabilities; reduce them with
+ *     pfa_proto_partial_reduce(ema_partial, n_blocks, ...).  Column C and
+ *     the other shapes sum in token order; bf16 x with G <= 8 sums the
+ *     columns 0..C-1 on MFMA from exact products (each gate split into
+ *     three bf16 parts), in a fixed order.  Deterministic either way; equal
+ *     to pfa_proto_accumulate's sums up to f32 rounding.
  * ==================================================================== */
 int pfa_router_gate_pad(int G);
 /* Sum of the router's per-workgroup telemetry partials (stats_partial
