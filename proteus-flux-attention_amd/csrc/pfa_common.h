@@ -201,4 +201,37 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
   return (va > vb) || (va == vb && ia < ib) || (vb != vb && (va == va || ia < ib));
 }
 
+// ---- LDS DMA tiles (shared by the attention passes and the linear kernel) --
+// Swizzle of unpadded 128-byte LDS rows: the 16-byte chunk c of row r sits in
+// chunk slot 8r + (c ^ tile_swz(r)).  Eight consecutive rows read at one chunk
+// fall in eight bank groups, and so do four rows x 32 bytes of a transpose
+// read.
+__device__ __forceinline__ int tile_swz(int r) {
+  return (((r & 3) << 1) | ((r >> 2) & 1)) ^ (((r >> 3) & 1) << 1);
+}
+
+// LDS DMA of 16 bytes per lane: lane l's bytes from g land at LDS byte
+// address lds_wave + 16*l (lds_wave is the same for the whole wave).
+// Written as assembly so that the compiler does not wait for the transfer
+// before every LDS read: completion is waited for explicitly
+// (dma_wait_barrier).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// M0 is named as clobbered; no kernel of this library uses M0 otherwise (no
+// LDS DMA builtins, GWS, message or relative-indexing instructions), so no
+// value of the compiler's lives in it across the statement.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_wave) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_wave) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// Wait until at most N of this wave's vector memory operations are
+// outstanding and its LDS reads are done, then meet the other waves.
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 }  // namespace pfa

@@ -118,9 +118,6 @@ __device__ __forceinline__ i16x4_t ds_tr4(const uint16_t* p) {
 // different bank groups, and so do the four rows x 32 bytes of each
 // transpose read.
 constexpr int kTileElems = kTile * 64;  // one unpadded K or V tile, bf16 elements
-__device__ __forceinline__ int tile_swz(int r) {
-  return (((r & 3) << 1) | ((r >> 2) & 1)) ^ (((r >> 3) & 1) << 1);
-}
 // per-lane element offsets into a SwzTile, fixed for the kernel
 struct SwzLane {
   int ko[2];  // K fragment, dc = 0, 1 (plus 1024 * kb)
@@ -145,29 +142,6 @@ struct SwzTile {
   }
 };
 
-// LDS DMA of 16 bytes per lane: lane l's bytes from g land at LDS byte
-// address lds_wave + 16*l (lds_wave is the same for the whole wave).
-// Written as assembly so that the compiler does not wait for the transfer
-// before every LDS read: completion is waited for explicitly
-// (dma_wait_barrier).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-// M0 is named as clobbered; nothing else in this file uses M0 (no LDS DMA
-// builtins, GWS, message or relative-indexing instructions), so no value of
-// the compiler's lives in it across the statement.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_wave) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_wave) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-// Wait until at most N of this wave's vector memory operations are
-// outstanding and its LDS reads are done, then meet the other waves.
-template <int N>
-__device__ __forceinline__ void dma_wait_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
 // One 64-key tile by DMA into a SwzTile: thread tid moves chunk slot tid%8
 // of key rows tid/8 and tid/8 + 32 (keys key0, key1) of K and of V: four
 // 16-byte transfers, each wave filling 1 KB runs of chunk slots.  lds_w is
