@@ -149,6 +149,60 @@ pack_count_routed(const int32_t* __restrict__ head_idx, int topk, const uint8_t*
   if (threadIdx.x == 0) blockcounts[(int64_t)bh * nblk + blk] = s;
 }
 
+// Token-parallel form for H <= kPackHeads: one workgroup per (tile, batch)
+// reads each token's head list once and writes the mask, row_of = -1 and the
+// tile counts of all H head rows (the per-row form above re-reads the head
+// lists once per head row).  The counts are integer sums: the same in any
+// order.
+constexpr int kPackHeads = 16;
+__global__ void __launch_bounds__(kPackThreads)
+pack_count_routed_tok(const int32_t* __restrict__ head_idx, int topk, const uint8_t* __restrict__ token_mask, int H,
+                      int64_t T, int nblk, uint8_t* __restrict__ mask_out, int32_t* __restrict__ blockcounts,
+                      int32_t* __restrict__ row_of) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
+  __shared__ int cnt_s[kPackHeads];
+  const int blk = blockIdx.x, b = blockIdx.y;
+  if (threadIdx.x < kPackHeads) cnt_s[threadIdx.x] = 0;
+  __syncthreads();
+  int cnt[kPackHeads];
+#pragma unroll
+  for (int h = 0; h < kPackHeads; ++h) cnt[h] = 0;
+  for (int j = 0; j < kPackTile / kPackThreads; ++j) {
+    const int64_t t = (int64_t)blk * kPackTile + j * kPackThreads + threadIdx.x;
+    if (t < T) {
+      const int64_t bt = (int64_t)b * T + t;
+      uint32_t sel = 0;
+      if (token_mask == nullptr || token_mask[bt] != 0)
+        for (int kk = 0; kk < topk; ++kk) {
+          const int hv = head_idx[bt * topk + kk];
+          if ((unsigned)hv < (unsigned)H) sel |= 1u << hv;  // other values select no row, as above
+        }
+#pragma unroll
+      for (int h = 0; h < kPackHeads; ++h) {
+        if (h < H) {
+          const int a = (sel >> h) & 1u;
+          const int64_t o = ((int64_t)b * H + h) * T + t;
+          mask_out[o] = (uint8_t)a;
+          if (row_of != nullptr) row_of[o] = -1;
+          cnt[h] += a;
+        }
+      }
+    }
+  }
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int h = 0; h < kPackHeads; ++h) {
+    if (h < H) {
+      int v = cnt[h];
+      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+      if (lane == 0) atomicAdd(&cnt_s[h], v);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < H && threadIdx.x < kPackHeads)
+    blockcounts[((int64_t)b * H + threadIdx.x) * nblk + blk] = cnt_s[threadIdx.x];
+}
+
 __global__ void __launch_bounds__(kPackThreads)
 pack_count_mask(const uint8_t* __restrict__ mask, int64_t T, int nblk, int32_t* __restrict__ blockcounts) {
   __shared__ int red[16];
@@ -370,8 +424,12 @@ extern "C" int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* t
   PackWs w = carve(workspace, BH, nblk);
   hipStream_t s = as_stream(stream);
   dim3 grid(nblk, (unsigned)BH);
-  pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts,
-                                                  row_of_out);
+  if (H <= kPackHeads)
+    pack_count_routed_tok<<<dim3(nblk, (unsigned)B), kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk,
+                                                                          mask_out, w.blockcounts, row_of_out);
+  else
+    pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts,
+                                                    row_of_out);
   PFA_CHECK_LAUNCH("pfa_pack_rows/count");
   pack_scan_kernel<<<1, kScanThreads, 0, s>>>(w.blockcounts, (int)BH, nblk, 1, w.totals, w.compact_id, active_heads_out,
                                       row_offsets_out, summary_out);

@@ -506,6 +506,61 @@ def test_pack_vs_oracle(dev):
         assert torch.equal(got[2].cpu(), exp[2]) and got[3] == exp[3]
 
 
+@pytest.mark.parametrize("B,T,H,topk,masked", [(1, 5000, 8, 2, False), (2, 3001, 8, 3, True), (2, 1500, 20, 4, False),
+                                                 (1, 700, 16, 1, True), (3, 64, 5, 5, False)])
+def test_pack_rows_routed_vs_oracle(dev, B, T, H, topk, masked):
+    """pfa_pack_rows from per-token head lists (the module's packing; H <= 16
+    and H > 16 take different count kernels): the row mask, the active heads,
+    the compacted rows and row_of against the oracle's packing of the same
+    mask restricted to its non-empty rows."""
+    from proteus_attention import _hip
+    from proteus_attention.kernels import sparse_attn as sa
+
+    g = torch.Generator().manual_seed(B * 1000 + T + H)
+    scores = torch.rand(B * T, H, generator=g)
+    if H > 6:
+        scores[:, 3] -= 2.0  # a head nobody picks (a compacted-away row)
+    hidx = torch.topk(scores, topk, dim=1).indices.to(torch.int32)
+    tmask = (torch.rand(B, T, generator=g) < 0.7) if masked else None
+    BH = B * H
+    sel = torch.zeros(B, T, H, dtype=torch.bool)
+    sel.scatter_(2, hidx.long().view(B, T, topk), True)
+    if tmask is not None:
+        sel &= tmask[:, :, None]
+    mask = sel.permute(0, 2, 1).reshape(BH, T)
+    lib = _hip.lib()
+    mask8 = torch.empty(BH, T, dtype=torch.uint8, device=dev)
+    heads = torch.empty(BH, dtype=torch.int32, device=dev)
+    offs = torch.empty(BH + 1, dtype=torch.int32, device=dev)
+    tok = torch.empty(BH * T, dtype=torch.int32, device=dev)
+    rh = torch.empty(BH * T, dtype=torch.int32, device=dev)
+    row_of = torch.empty(BH, T, dtype=torch.int32, device=dev)
+    summ = torch.empty(4, dtype=torch.int32, device=dev)
+    ws = sa._workspace(sa._size_out(lib.pfa_pack_workspace_size, B, H, T), dev)
+    hd = hidx.to(dev)
+    tm = tmask.to(torch.uint8).to(dev) if tmask is not None else None
+    rc = lib.pfa_pack_rows(_hip.ptr(hd), topk, _hip.ptr(tm), B, H, T, _hip.ptr(mask8), _hip.ptr(heads), _hip.ptr(offs),
+                           _hip.ptr(tok), _hip.ptr(rh), _hip.ptr(row_of), _hip.ptr(summ), _hip.ptr(ws), ws.numel(),
+                           _hip.stream_ptr(dev))
+    _hip.check(rc, "pfa_pack_rows")
+    assert torch.equal(mask8.cpu().bool(), mask)
+    active = mask.any(dim=1).nonzero().flatten()
+    P = int(active.numel())
+    s_ = summ.cpu().tolist()
+    assert s_[0] == P and s_[1] == int(mask.sum())
+    assert torch.equal(heads.cpu()[:P].long(), active)
+    exp = O.pack_active_rows(mask[active])
+    row_head, tok_e, offs_e, max_rows = exp
+    N = int(tok_e.numel())
+    assert s_[2] == max_rows
+    assert torch.equal(offs.cpu()[:P + 1], offs_e)
+    assert torch.equal(tok.cpu()[:N].long(), tok_e)
+    assert torch.equal(rh.cpu()[:N].long(), row_head)
+    ro = torch.full((BH, T), -1, dtype=torch.long)
+    ro[active[row_head], tok_e] = torch.arange(N)
+    assert torch.equal(row_of.cpu().long(), ro)
+
+
 @pytest.mark.parametrize("k_only", [False, True])
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,T,H,D", [(2, 37, 4, 16), (2, 300, 8, 64), (1, 70, 3, 64), (1, 50, 2, 12),
