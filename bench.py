@@ -100,7 +100,7 @@ def cpu_baseline(x, weights, dtype, c, caps) -> dict:
     xs = x.to(dtype)
     t0 = time.perf_counter()
     t = cpu_pipeline.shortlist_forward_seconds(xs, weights, H=c["H"], L=L, local_w=local_w, stride=stride,
-                                               slots=slots, K=K, sample_every=8)
+                                               slots=slots, K=K, sample_every=1)
     wall = time.perf_counter() - t0
     tokens = c["B"] * c["T"]
     return {
@@ -110,7 +110,7 @@ def cpu_baseline(x, weights, dtype, c, caps) -> dict:
         "kind": "port",
         "sample": (f"config-3 forward, oracle CPU pipeline (torch CPU {str(dtype).replace('torch.', '')} with "
                    f"{cores} threads; single-threaded C builder); router/pack/QKV/proj on all {tokens} tokens, "
-                   f"builder+attention on every 8th packed row ({t['sample_fraction']:.4f} of rows), scaled; "
+                   f"builder+attention on all packed rows ({t['sample_fraction']:.4f} of rows); "
                    f"{wall:.1f}s wall; stage s: " +
                    ", ".join(f"{k}={v:.2f}" for k, v in t.items() if k not in ("total", "sample_fraction"))),
     }

@@ -25,7 +25,8 @@ from . import c_oracle
 
 
 def shortlist_forward_seconds(x: torch.Tensor, w: Dict[str, torch.Tensor], *, H: int, L: int, local_w: int,
-                              stride: int, slots: int, K: int, sample_every: int = 16) -> Dict[str, float]:
+                              stride: int, slots: int, K: int, sample_every: int = 16,
+                              row_chunk: int = 2048) -> Dict[str, float]:
     """x: (1, T, C) in the compute dtype.  Returns per-stage and total
     seconds (sampled stages already extrapolated)."""
 
@@ -69,15 +70,18 @@ def shortlist_forward_seconds(x: torch.Tensor, w: Dict[str, torch.Tensor], *, H:
     ct = torch.from_numpy(cand).long()
     lt = torch.from_numpy(lens).long()
     for h in torch.unique(hsel).tolist():
-        m = (hsel == h).nonzero(as_tuple=True)[0]
-        toks = token_idx[sel][m]
-        qs = qh[h][toks]
-        cr, lr = ct[m], lt[m]
-        ks, vs = kh[h][cr], vh[h][cr]
-        inval = torch.arange(L)[None, :] >= lr[:, None]
-        sc = torch.einsum("rd,rld->rl", qs, ks.masked_fill(inval[..., None], 0.0)) * (1.0 / math.sqrt(D))
-        p = torch.softmax(sc.masked_fill(inval, float("-inf")), -1)
-        torch.bmm(p.unsqueeze(1), vs.masked_fill(inval[..., None], 0.0))
+        mh = (hsel == h).nonzero(as_tuple=True)[0]
+        # rows in chunks: the gathered K/V of a chunk is chunk * L * D each
+        for c0 in range(0, mh.numel(), row_chunk):
+            m = mh[c0:c0 + row_chunk]
+            toks = token_idx[sel][m]
+            qs = qh[h][toks]
+            cr, lr = ct[m], lt[m]
+            ks, vs = kh[h][cr], vh[h][cr]
+            inval = torch.arange(L)[None, :] >= lr[:, None]
+            sc = torch.einsum("rd,rld->rl", qs, ks.masked_fill(inval[..., None], 0.0)) * (1.0 / math.sqrt(D))
+            p = torch.softmax(sc.masked_fill(inval, float("-inf")), -1)
+            torch.bmm(p.unsqueeze(1), vs.masked_fill(inval[..., None], 0.0))
     t["attention"] = (time.perf_counter() - s0) / frac
 
     s0 = time.perf_counter()
