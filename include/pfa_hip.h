@@ -177,6 +177,23 @@ int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* token_mask,
                   int32_t* row_of_out, int32_t* summary_out, void* workspace,
                   size_t ws_bytes, void* stream);
 
+/* pfa_pack_rows without a workspace: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * results as pfa_pack_rows; the per-(head, block) counts live in a static
+ * device array of PFA_PACK_STATIC_SCRATCH_BYTES per GPU instead of a
+ * workspace, so B*H*ceil(T/1024) is limited to about 2^18 (PFA_E_INVALID
+ * beyond that).  It calls no allocator.  The array is looked up on the first
+ * call on each device, which must then be the current device.  All calls on
+ * one GPU share that array: calls that overlap on one GPU (two streams, two
+ * threads) race and must be serialised by the caller. */
+#define PFA_PACK_STATIC_SCRATCH_BYTES ((size_t)1 << 20)
+int pfa_pack_rows_static(const int32_t* head_idx, int topk, const uint8_t* token_mask,
+                         int B, int H, int64_t T, uint8_t* mask_out,
+                         int32_t* active_heads_out, int32_t* row_offsets_out,
+                         int32_t* token_idx_out, int32_t* row_head_out,
+                         int32_t* row_of_out, int32_t* summary_out, void* stream);
+
 /* Same packing from an arbitrary (P, T) uint8 mask (the operator-level
  * entry point aspa_sparse_attention packs its own active_mask). Heads are
  * NOT compacted: compact id == mask row. */

@@ -1,6 +1,8 @@
 // Token top-k (radix select) and row packing.
 #include "pfa_common.h"
 
+#include <mutex>
+
 namespace pfa {
 
 // ---------------------------------------------------------------------
@@ -405,6 +407,73 @@ extern "C" int pfa_pack_workspace_size(int B, int H, int64_t T, size_t* bytes) {
   return PFA_OK;
 }
 
+namespace pfa {
+
+// The three launches of pfa_pack_rows over a carved workspace.
+static int pack_rows_launch(const int32_t* head_idx, int topk, const uint8_t* token_mask, int B, int H, int64_t T,
+                            int nblk, uint8_t* mask_out, int32_t* active_heads_out, int32_t* row_offsets_out,
+                            int32_t* token_idx_out, int32_t* row_head_out, int32_t* row_of_out,
+                            int32_t* summary_out, PackWs w, hipStream_t s) {
+  const int64_t BH = (int64_t)B * H;
+  dim3 grid(nblk, (unsigned)BH);
+  if (H <= kPackHeads)
+    pack_count_routed_tok<<<dim3(nblk, (unsigned)B), kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk,
+                                                                          mask_out, w.blockcounts, row_of_out);
+  else
+    pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts,
+                                                    row_of_out);
+  PFA_CHECK_LAUNCH("pfa_pack_rows/count");
+  pack_scan_kernel<<<1, kScanThreads, 0, s>>>(w.blockcounts, (int)BH, nblk, 1, w.totals, w.compact_id, active_heads_out,
+                                      row_offsets_out, summary_out);
+  PFA_CHECK_LAUNCH("pfa_pack_rows/scan");
+  pack_fill_kernel<<<grid, kPackThreads, 0, s>>>(mask_out, T, nblk, w.blockcounts, w.compact_id, token_idx_out,
+                                                 row_head_out, row_of_out);
+  PFA_CHECK_LAUNCH("pfa_pack_rows/fill");
+  return PFA_OK;
+}
+
+// Scratch of pfa_pack_rows_static: per-(head, block) counts, per-head totals
+// and compact ids (the pfa_pack_rows workspace layout), at most
+// kPackStaticBytes.  Every entry is written before it is read, so nothing is
+// cleared between calls.
+constexpr size_t kPackStaticBytes = PFA_PACK_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kPackStaticBytes];
+
+// Device address of `scratch` per device, looked up once per device with
+// that device current (host code never passes the symbol itself).
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("pfa_pack_rows_static: hipGetDevice failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("pfa_pack_rows_static: device %d beyond the %d supported", dev, kMaxDevices);
+    return PFA_E_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("pfa_pack_rows_static: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : PFA_E_UNSUPPORTED;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return PFA_OK;
+}
+
+}  // namespace pfa
+
+using namespace pfa;
+
 extern "C" int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* token_mask, int B, int H, int64_t T,
                              uint8_t* mask_out, int32_t* active_heads_out, int32_t* row_offsets_out,
                              int32_t* token_idx_out, int32_t* row_head_out, int32_t* row_of_out,
@@ -421,23 +490,33 @@ extern "C" int pfa_pack_rows(const int32_t* head_idx, int topk, const uint8_t* t
     set_error("pfa_pack_rows: workspace %zu < %zu", ws_bytes, need);
     return PFA_E_WORKSPACE;
   }
-  PackWs w = carve(workspace, BH, nblk);
-  hipStream_t s = as_stream(stream);
-  dim3 grid(nblk, (unsigned)BH);
-  if (H <= kPackHeads)
-    pack_count_routed_tok<<<dim3(nblk, (unsigned)B), kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk,
-                                                                          mask_out, w.blockcounts, row_of_out);
-  else
-    pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts,
-                                                    row_of_out);
-  PFA_CHECK_LAUNCH("pfa_pack_rows/count");
-  pack_scan_kernel<<<1, kScanThreads, 0, s>>>(w.blockcounts, (int)BH, nblk, 1, w.totals, w.compact_id, active_heads_out,
-                                      row_offsets_out, summary_out);
-  PFA_CHECK_LAUNCH("pfa_pack_rows/scan");
-  pack_fill_kernel<<<grid, kPackThreads, 0, s>>>(mask_out, T, nblk, w.blockcounts, w.compact_id, token_idx_out,
-                                                 row_head_out, row_of_out);
-  PFA_CHECK_LAUNCH("pfa_pack_rows/fill");
-  return PFA_OK;
+  return pack_rows_launch(head_idx, topk, token_mask, B, H, T, nblk, mask_out, active_heads_out, row_offsets_out,
+                          token_idx_out, row_head_out, row_of_out, summary_out, carve(workspace, BH, nblk),
+                          as_stream(stream));
+}
+
+extern "C" int pfa_pack_rows_static(const int32_t* head_idx, int topk, const uint8_t* token_mask, int B, int H,
+                                    int64_t T, uint8_t* mask_out, int32_t* active_heads_out,
+                                    int32_t* row_offsets_out, int32_t* token_idx_out, int32_t* row_head_out,
+                                    int32_t* row_of_out, int32_t* summary_out, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(head_idx && mask_out && row_offsets_out && token_idx_out && row_head_out && summary_out,
+                "pfa_pack_rows_static: null pointer");
+  PFA_CHECK_ARG(B > 0 && H > 0 && T > 0 && topk >= 1 && topk <= H, "pfa_pack_rows_static: bad sizes");
+  PFA_CHECK_ARG((int64_t)B * H * T < (int64_t)INT32_MAX, "pfa_pack_rows_static: B*H*T exceeds int32 row indexing");
+  int nblk;
+  const int64_t BH = (int64_t)B * H;
+  const size_t need = pack_ws_bytes(BH, T, &nblk);
+  PFA_CHECK_ARG(need <= kPackStaticBytes,
+                "pfa_pack_rows_static: B*H=%lld heads x %d token blocks need %zu bytes of scratch, above the "
+                "static maximum of %zu (use pfa_pack_rows with a workspace)",
+                (long long)BH, nblk, need, kPackStaticBytes);
+  void* ptr = nullptr;
+  const int rc = scratch_address(&ptr);
+  if (rc != PFA_OK) return rc;
+  return pack_rows_launch(head_idx, topk, token_mask, B, H, T, nblk, mask_out, active_heads_out, row_offsets_out,
+                          token_idx_out, row_head_out, row_of_out, summary_out, carve(ptr, BH, nblk),
+                          as_stream(stream));
 }
 
 extern "C" int pfa_pack_mask(const uint8_t* mask, int P, int64_t T, int32_t* row_offsets_out, int32_t* token_idx_out,

@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "pfa_token_topk",
     "pfa_pack_workspace_size",
     "pfa_pack_rows",
+    "pfa_pack_rows_static",
     "pfa_pack_mask",
     "pfa_proto_prefix_workspace_size",
     "pfa_proto_prefix_topk",
@@ -100,6 +101,7 @@ _SIGNATURES = {
     "pfa_token_topk": ([_vp, _i32, _i64, _i64, _i32, _f32, _vp, _vp], _i32),
     "pfa_pack_workspace_size": ([_i32, _i32, _i64, ctypes.POINTER(_sz)], _i32),
     "pfa_pack_rows": ([_vp, _i32, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
+    "pfa_pack_rows_static": ([_vp, _i32, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "pfa_pack_mask": ([_vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_proto_prefix_workspace_size": ([_i32, _i64, _i32, ctypes.POINTER(_sz)], _i32),
     "pfa_proto_prefix_topk": ([_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp], _i32),
