@@ -326,6 +326,13 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
  *   q, k, v, out: 16-byte aligned with strides multiple of 8 elements; the
  *   k and v token strides positive and below 2^31 (PFA_E_INVALID otherwise).
  *   Results are deterministic: the same inputs give the same bits.
+ *   q_scale / k_scale / v_scale: NULL, or per global head (b*H + h) f32
+ *   scales of the per-head int8 quantisation (aspa.py:1258-1267,
+ *   1312-1363; pfa_quantize_heads_int8 with bf16 output): q, k, v then
+ *   hold the int8 values as exact bf16 integers, the scores are
+ *   scale*q_scale*k_scale*(q8.k8) (exact integer dots on MFMA) and the
+ *   outputs v_scale*(P.v8)/l -- the dequantisation of sparse_attn.py:
+ *   1538-1541 applied inside the tile.  All three or none.
  * ==================================================================== */
 int pfa_shortlist_attn_part_floats(void);
 int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
@@ -338,7 +345,38 @@ int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                            const int32_t* proto_evict, float scale,
                            float* partials, int32_t* lengths,
                            const void* q_rope_cos, const void* q_rope_sin,
-                           int passes, void* stream);
+                           const float* q_scale, const float* k_scale,
+                           const float* v_scale, int passes, void* stream);
+
+/* ====================================================================
+ * Per-head symmetric int8 quantisation of the active heads of q, k or v.
+ * Replaces AdaptiveSparseAttention._quantize_per_head_int8
+ * (aspa.py:1312-1363) and its call sites (aspa.py:1258-1267): per compact
+ * head p < P (P = summary[0], or P_cap when summary is NULL) of global head
+ * bh = head_map[p] (identity when NULL), over its T x D elements of x
+ * ([b][h][t][d] through pfa_tensor4 strides, dtype PFA_F32/BF16/F16):
+ *   base  = max |x|                                      mode 0 ("max")
+ *         = torch.quantile(|x|, percentile) (linear interpolation; the
+ *           absmax when that is 0, or when percentile == 0)  mode 1
+ *         = as mode 1, then ema[p] = decay*e + (1-decay)*base with e =
+ *           ema[p] (ema_valid) or the absmax; base = ema[p]   mode 2
+ *   scales[bh] = max(base / 127, 1e-6)
+ *   dst[bh][t][d] = clamp(round_half_even(x / scale), -127, 127)
+ * each step an f32 operation rounded as the reference's tensor ops round.
+ * dst_dtype PFA_I8 writes int8; PFA_BF16 writes the same integers as bf16
+ * (exact), and dst may then be x itself (in place) -- the input of
+ * pfa_shortlist_attn_fwd's int8 mode.  ema: (P) f32, read and written in
+ * mode 2 only.  The workspace is sized by pfa_quantize_heads_workspace_size
+ * for the same P_cap, T, D and mode.
+ * ==================================================================== */
+int pfa_quantize_heads_workspace_size(int P_cap, int64_t T, int D, int mode,
+                                      size_t* bytes);
+int pfa_quantize_heads_int8(pfa_tensor4 x, int dtype, int H, int64_t T, int D,
+                            const int32_t* head_map, int P_cap,
+                            const int32_t* summary, int mode, float percentile,
+                            double ema_decay, float* ema, int ema_valid,
+                            pfa_tensor4 dst, int dst_dtype, float* scales,
+                            void* workspace, size_t ws_bytes, void* stream);
 
 /* Per compact head, the largest token among its packed rows (needed by the
  * explicit-mask branch: sparse_attn.py:1010-1015). */

@@ -22,7 +22,10 @@ Pinning (what checks each function beyond re-reading the formula):
                                semantics (local/anchor closed forms), C oracle
   sparse_attention             closed form softmax(QK^T/sqrt(D)+mask)V per row,
                                SDPA equality, golden vectors
-  quantize_per_head_int8       closed form (absmax/127, round, clamp)
+  quantize_per_head_int8       closed form (absmax/127, round, clamp); the
+                               percentile rule by hand-interpolated order
+                               statistics and the EMA recurrence; golden
+                               module vectors of the reference's int8 mode
   effective linear params      known answers from the reference tests
 """
 from __future__ import annotations
@@ -355,13 +358,31 @@ def sparse_attention(
     return result.to(out_dtype)
 
 
-def quantize_per_head_int8(t: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Per-head symmetric int8, "max" mode (aspa.py:1312-1363)."""
+def quantize_per_head_int8(t: torch.Tensor, mode: str = "max", percentile: float = 1.0, ema: Optional[torch.Tensor] = None,
+                           ema_decay: float = 0.9) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Per-head symmetric int8 (aspa.py:1312-1363): base = absmax ("max"),
+    torch.quantile of |x| with its absmax when that is 0 ("percentile",
+    percentile > 0), and for "ema_percentile" ema = decay*ema + (1-decay)*base
+    with ema starting at the absmax (aspa.py:1339-1355); scale =
+    clamp(base/127, min=1e-6); q = clamp(round(x/scale), +-127).  Returns
+    (q, scales, updated ema or None)."""
 
     flat = t.to(torch.float32).reshape(t.size(0), -1)
-    s = torch.clamp(flat.abs().amax(dim=1, keepdim=True) / 127.0, min=1e-6)
+    absf = flat.abs()
+    amax = absf.amax(dim=1, keepdim=True)
+    if mode == "max" or percentile <= 0.0:
+        base = amax
+    else:
+        base = torch.quantile(absf, percentile, dim=1, keepdim=True)
+        base = torch.where(base > 0.0, base, amax)
+    new_ema = None
+    if mode == "ema_percentile":
+        prev = amax.squeeze(1) if ema is None else ema.to(torch.float32)
+        new_ema = ema_decay * prev + (1.0 - ema_decay) * base.squeeze(1)
+        base = new_ema.unsqueeze(1)
+    s = torch.clamp(base / 127.0, min=1e-6)
     qv = torch.clamp((flat / s).round(), -127.0, 127.0).to(torch.int8).view_as(t)
-    return qv, s.squeeze(1)
+    return qv, s.squeeze(1), new_ema
 
 
 # ---------------------------------------------------------------------------
@@ -468,7 +489,7 @@ def quantize_rows_int8(x: torch.Tensor, heads: int) -> Tuple[torch.Tensor, torch
     S, C = x.shape
     D = C // heads
     slices = x.reshape(S, heads, D).permute(1, 0, 2).reshape(heads * S, 1, D)
-    q, s = quantize_per_head_int8(slices)
+    q, s, _ = quantize_per_head_int8(slices)
     return q.view(heads, S, D), s.view(heads, S)
 
 

@@ -68,6 +68,16 @@ struct ShortArgs {
   const uint16_t* rcos;  // (T, 64) RoPE tables applied to q rows on load, or null
   const uint16_t* rsin;
   float scale_log2;
+  // per global head (b*H + h) int8 scales of q, k, v, or null: q, k, v then
+  // hold the integer values (exact in bf16) of the per-head int8
+  // quantisation, scores are scaled by q_scale*k_scale and outputs by v_scale
+  const float* qsc;
+  const float* ksc;
+  const float* vsc;
+  __device__ __forceinline__ float head_scale_log2(int bh) const {
+    return qsc ? scale_log2 * (qsc[bh] * ksc[bh]) : scale_log2;
+  }
+  __device__ __forceinline__ float head_out_scale(int bh) const { return vsc ? vsc[bh] : 1.f; }
 };
 
 struct QState {
@@ -379,6 +389,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   if (c >= s || (int64_t)c >= a.T) return;
   const int bh = a.head_map ? a.head_map[p] : p;
   const int64_t bb = bh / a.H, hh = bh % a.H;
+  const float sl2 = a.head_scale_log2(bh);
   const int64_t Mmax = (a.T - 1 - c) / s;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   SwzLane L;
@@ -477,7 +488,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
         const SwzTile tl{ring[i % S], L};
         qk_tile(qf, tl, sc);
         mask_window<false>(sc, need_lo, need_hi, lo, hi, unused);
-        softmax_pv(sc, tl, a.scale_log2, st);
+        softmax_pv(sc, tl, sl2, st);
       }
     }
     float lt = st.l;
@@ -596,6 +607,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const int p = r_p[s0];
     const int bh = a.head_map ? a.head_map[p] : p;
     const int64_t bb = bh / a.H, hh = bh % a.H;
+    const float sl2 = a.head_scale_log2(bh);
     const int t_first = r_t[s0], t_last = r_t[s1 - 1];
     const int lo_first = (int)win_lo(t_first, w), lo_last = (int)win_lo(t_last, w);
     const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
@@ -800,7 +812,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
             }
           }
         }
-        softmax_pv(sc, tl, a.scale_log2, st);
+        softmax_pv(sc, tl, sl2, st);
       }
     }
 
@@ -829,7 +841,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
         fb = (ma == -INFINITY) ? 0.f : exp2f(ma - mm);
       }
       const float den = lt * fa + lp * fb;
-      const float inv = 1.f / den;
+      const float inv = a.head_out_scale(bh) / den;
       uint16_t* op = (uint16_t*)a.out.ptr + bb * a.out.s_b + hh * a.out.s_h + (int64_t)tq * a.out.s_t;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -866,7 +878,8 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
                                       const int32_t* row_of, int local_w, int anchor_stride, int anchor_slots,
                                       const int32_t* proto_blocks, int proto_k, const int32_t* proto_evict,
                                       float scale, float* partials, int32_t* lengths, const void* q_rope_cos,
-                                      const void* q_rope_sin, int passes, void* stream) {
+                                      const void* q_rope_sin, const float* q_scale, const float* k_scale,
+                                      const float* v_scale, int passes, void* stream) {
   clear_error();
   PFA_CHECK_ARG(dtype == PFA_BF16 && D == 64, "pfa_shortlist_attn_fwd: bf16 and D=64 only (got dtype %d D %d)", dtype,
                 D);
@@ -892,6 +905,8 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
                 "pfa_shortlist_attn_fwd: q_rope_cos and q_rope_sin go together");
   PFA_CHECK_ARG(q_rope_cos == nullptr || (((uintptr_t)q_rope_cos | (uintptr_t)q_rope_sin) & 15) == 0,
                 "pfa_shortlist_attn_fwd: RoPE tables must be 16-byte aligned");
+  PFA_CHECK_ARG((q_scale == nullptr) == (k_scale == nullptr) && (q_scale == nullptr) == (v_scale == nullptr),
+                "pfa_shortlist_attn_fwd: q_scale, k_scale and v_scale go together");
   ShortArgs a;
   a.q = q; a.k = k; a.v = v; a.out = out;
   a.H = H; a.T = T; a.token_idx = token_idx; a.row_head = row_head; a.head_map = head_map; a.N = N;
@@ -900,6 +915,7 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   a.row_of = row_of; a.summary = summary; a.part = partials; a.lengths = lengths;
   a.rcos = (const uint16_t*)q_rope_cos; a.rsin = (const uint16_t*)q_rope_sin;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.qsc = q_scale; a.ksc = k_scale; a.vsc = v_scale;
   hipStream_t s = as_stream(stream);
   if (anchors && (passes & 1)) {
     dim3 grid((unsigned)((int64_t)anchor_stride < T ? (int64_t)anchor_stride : T), (unsigned)P_cap);

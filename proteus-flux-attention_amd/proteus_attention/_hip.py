@@ -48,6 +48,8 @@ EXPORTED_SYMBOLS = (
     "pfa_shortlist_attn_part_floats",
     "pfa_shortlist_attn_fwd",
     "pfa_head_max_token",
+    "pfa_quantize_heads_workspace_size",
+    "pfa_quantize_heads_int8",
     "pfa_rope_qk_inplace",
     "pfa_rope_k_inplace",
     "pfa_router_stats_reduce",
@@ -112,9 +114,12 @@ _SIGNATURES = {
                              _i64, _vp, _i64, _vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp], _i32),
     "pfa_shortlist_attn_part_floats": ([], _i32),
     "pfa_shortlist_attn_fwd": ([Tensor4, Tensor4, Tensor4, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp, _i64,
-                                _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp, _i32,
-                                _vp], _i32),
+                                _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp, _vp,
+                                _vp, _vp, _i32, _vp], _i32),
     "pfa_head_max_token": ([_vp, _vp, _i32, _vp, _vp], _i32),
+    "pfa_quantize_heads_workspace_size": ([_i32, _i64, _i32, _i32, ctypes.POINTER(_sz)], _i32),
+    "pfa_quantize_heads_int8": ([Tensor4, _i32, _i32, _i64, _i32, _vp, _i32, _vp, _i32, _f32, ctypes.c_double, _vp,
+                                 _i32, Tensor4, _i32, _vp, _vp, _sz, _vp], _i32),
     "pfa_rope_qk_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
     "pfa_rope_k_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
     "pfa_router_stats_reduce": ([_vp, _i32, _vp, _vp], _i32),

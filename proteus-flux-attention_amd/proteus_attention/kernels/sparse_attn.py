@@ -392,6 +392,7 @@ def _shortlist_attn_structured(
     q_rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
     passes: int = 3,
     part: Optional[torch.Tensor] = None,
+    qkv_scales: Optional[torch.Tensor] = None,
 ) -> Optional[torch.Tensor]:
     """Module-path shortlist attention without materialised candidates
     (bf16, D=64); the prototype sets come as _proto_prefix_blocks tables of
@@ -400,7 +401,9 @@ def _shortlist_attn_structured(
     q_rope = (cos, sin) bf16 (T, 64) tables: q is still unrotated and its
     rows are rotated as the kernel loads them.  passes = 1 runs only the
     anchor pass and 2 only the main pass (the caller orders them and passes
-    the same `part`, from shortlist_partials, to both); 3 runs both."""
+    the same `part`, from shortlist_partials, to both); 3 runs both.
+    qkv_scales: (3, B*H) f32 per-head int8 scales of q, k, v (the tensors
+    then hold the int8 values as bf16, from quantize_heads_int8), or None."""
 
     lib = _hip.lib()
     N = int(token_idx.numel())
@@ -426,9 +429,51 @@ def _shortlist_attn_structured(
             q4, k4, v4, out4, _hip.PFA_BF16, int(H), int(T), int(D), _hip.ptr(token_idx), _hip.ptr(row_head),
             _hip.ptr(head_map), N, int(head_map.numel()), _hip.ptr(summary), _hip.ptr(row_of), int(local_w),
             int(stride), int(slots), _hip.ptr(blocks), K, _hip.ptr(evict), float(scale), _hip.ptr(part),
-            _hip.ptr(lengths), _hip.ptr(rc_cos), _hip.ptr(rc_sin), int(passes), _hip.stream_ptr(device))
+            _hip.ptr(lengths), _hip.ptr(rc_cos), _hip.ptr(rc_sin),
+            *((None, None, None) if qkv_scales is None else (_hip.ptr(qkv_scales[0]), _hip.ptr(qkv_scales[1]),
+                                                             _hip.ptr(qkv_scales[2]))),
+            int(passes), _hip.stream_ptr(device))
     _hip.check(rc, "pfa_shortlist_attn_fwd")
     return lengths
+
+
+_QUANT_MODES = {"max": 0, "percentile": 1, "ema_percentile": 2}
+
+
+def quantize_heads_int8(
+    x4: "_hip.Tensor4",
+    dtype: torch.dtype,
+    H: int,
+    T: int,
+    D: int,
+    head_map: Optional[torch.Tensor],
+    P_cap: int,
+    summary: Optional[torch.Tensor],
+    mode: str,
+    percentile: float,
+    ema_decay: float,
+    ema: Optional[torch.Tensor],
+    ema_valid: bool,
+    dst4: "_hip.Tensor4",
+    dst_dtype: torch.dtype,
+    scales: torch.Tensor,
+    device: torch.device,
+) -> None:
+    """Per-head symmetric int8 of the active heads (reference aspa.py:1312-1363)
+    on the device: scales[b*H+h] and the int8 values in dst4 (int8, or the
+    same integers as bf16 for the structured attention's int8 mode; dst4 may
+    be x4 itself then).  mode is "max", "percentile" or "ema_percentile"
+    (ema: (P,) f32, updated in place)."""
+
+    lib = _hip.lib()
+    m = _QUANT_MODES[mode]
+    ws = _workspace(_size_out(lib.pfa_quantize_heads_workspace_size, int(P_cap), int(T), int(D), m), device)
+    with _hip.TIMER.timed("quantize_heads_int8"):
+        rc = lib.pfa_quantize_heads_int8(x4, _hip.dtype_tag(dtype), int(H), int(T), int(D), _hip.ptr(head_map),
+                                         int(P_cap), _hip.ptr(summary), m, float(percentile), float(ema_decay),
+                                         _hip.ptr(ema), 1 if ema_valid else 0, dst4, _hip.dtype_tag(dst_dtype),
+                                         _hip.ptr(scales), _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device))
+    _hip.check(rc, "pfa_quantize_heads_int8")
 
 
 def aspa_sparse_attention(

@@ -705,30 +705,38 @@ class AdaptiveSparseAttention(nn.Module):
     # int8 per-head quantisation (aspa.py:1312-1363)
     # ------------------------------------------------------------------
     def _quantize_per_head_int8(self, tensor: torch.Tensor, ema_buffer: str) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(P, T, D) -> int8 (P, T, D) and per-head f32 scales (P,), on the
+        device (pfa_quantize_heads_int8)."""
         if tensor.dim() != 3:
             raise ValueError("Expected a rank-3 tensor for per-head quantization")
-        flat = tensor.to(torch.float32).reshape(tensor.size(0), -1)
-        absf = flat.abs()
+        device = _hip.require_device(tensor, what="_quantize_per_head_int8")
+        x = tensor if tensor.stride(-1) == 1 else tensor.contiguous()
+        P, T, D = x.shape
+        quant = torch.empty(P, T, D, dtype=torch.int8, device=device)
+        scales = torch.empty(P, dtype=torch.float32, device=device)
+        self._quantize_heads(_hip.tensor4(x, P), x.dtype, P, T, D, None, P, None, _hip.tensor4(quant, P), torch.int8,
+                             scales, ema_buffer)
+        return quant, scales
+
+    def _quantize_heads(self, x4, dtype, H, T, D, head_map, P, summary, dst4, dst_dtype, scales, ema_buffer):
+        """The reference's quantisation rule (aspa.py:1312-1363) for the P
+        active heads of one of q/k/v, with this module's mode and its
+        per-head EMA buffer (re-initialised when P changes, as the
+        reference's is)."""
         mode = self.quantize_sparse_int8_mode
-        if mode == "max" or self.quantize_sparse_int8_percentile <= 0.0:
-            base = absf.amax(dim=1, keepdim=True)
-        else:
-            base = torch.quantile(absf, self.quantize_sparse_int8_percentile, dim=1, keepdim=True)
-            base = torch.where(base > 0.0, base, absf.amax(dim=1, keepdim=True))
+        ema, valid = None, False
         if mode == "ema_percentile":
-            decay = self.quantize_sparse_int8_ema_decay
             ema = getattr(self, ema_buffer)
-            if ema is None or ema.numel() != flat.size(0) or not self._quant_ema_flags.get(ema_buffer, False):
-                ema = absf.amax(dim=1)
-            else:
-                ema = ema.to(tensor.device, dtype=torch.float32)
-            updated = decay * ema + (1.0 - decay) * base.squeeze(1)
-            setattr(self, ema_buffer, updated.detach())
+            valid = bool(ema is not None and ema.numel() == P and self._quant_ema_flags.get(ema_buffer, False)
+                         and ema.device == scales.device and ema.dtype == torch.float32)
+            if not valid:
+                ema = torch.empty(P, dtype=torch.float32, device=scales.device)
+        _sa.quantize_heads_int8(x4, dtype, H, T, D, head_map, P, summary, mode,
+                                float(self.quantize_sparse_int8_percentile), float(self.quantize_sparse_int8_ema_decay),
+                                ema, valid, dst4, dst_dtype, scales, scales.device)
+        if ema is not None:
+            setattr(self, ema_buffer, ema)
             self._quant_ema_flags[ema_buffer] = True
-            base = updated.unsqueeze(1)
-        scales = torch.clamp(base / 127.0, min=1e-6)
-        quant = torch.clamp((flat / scales).round(), -127.0, 127.0).to(torch.int8).view_as(tensor)
-        return quant.contiguous(), scales.squeeze(1).to(torch.float32).contiguous()
 
     # ------------------------------------------------------------------
     # device stages
@@ -1264,7 +1272,11 @@ class AdaptiveSparseAttention(nn.Module):
         # dependent; otherwise every token has exactly `topk` active rows and
         # the summary is read back with the telemetry at the end (no stall
         # between the router and the attention launches).
-        need_summary = (density_threshold is not None or self.force_dense_when_full or token_mask is not None)
+        # The int8 mode needs P on the host as well: its per-head EMA buffers
+        # have one entry per active head (aspa.py:1347-1357).
+        use_quant = bool(self.quantize_sparse_int8 and not self.training)
+        need_summary = (density_threshold is not None or self.force_dense_when_full or token_mask is not None
+                        or use_quant)
         if need_summary:
             summ = summary.cpu()
             P, N, max_rows = int(summ[0]), int(summ[1]), int(summ[2])
@@ -1294,13 +1306,16 @@ class AdaptiveSparseAttention(nn.Module):
         with torch.cuda.stream(fork_s):
             # the structured kernel rotates q rows as it loads them: only k is
             # rotated here
-            q_rope = self._rope_inplace(qkv, rotate_q=not (structured and self.fuse_q_rope))
+            q_rope = self._rope_inplace(qkv, rotate_q=not (structured and self.fuse_q_rope and not use_quant))
             attn = torch.zeros(B, T, C, dtype=qkv.dtype, device=device)
         if not capture:
             # the forked stream's tensors are used (and freed) on this stream
             qkv.record_stream(main_s)
             attn.record_stream(main_s)
-        if not structured:
+        # The structured path keeps the two streams apart up to the main pass;
+        # the others (and the int8 mode, which quantises q/k/v first) join here.
+        join_early = not structured or use_quant
+        if join_early:
             ema()
             main_s.wait_stream(fork_s)
         D = self.d_head
@@ -1341,8 +1356,8 @@ class AdaptiveSparseAttention(nn.Module):
             rh = row_head[:N]
             heads = active_heads[:P] if P >= 0 else active_heads
             self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets, alpha, row_of, summary,
-                                       plan=plan, q_rope=q_rope, streams=(main_s, fork_s),
-                                       before_join=ema if structured else None)
+                                       plan=plan, q_rope=q_rope, streams=None if join_early else (main_s, fork_s),
+                                       before_join=None if join_early else ema)
             backend_info = self._last_shortlist_backend_info or get_last_backend_info()
             state = {
                 "mode": mode_label, "backend": str(backend_info.get("name", "shortlist")),
@@ -1386,7 +1401,7 @@ class AdaptiveSparseAttention(nn.Module):
 
     def _shortlist_plan(self, B: int, T: int, alpha: float, dtype: torch.dtype) -> Dict[str, Any]:
         """Shortlist sizes of this forward (aspa.py:1175-1210) and whether the
-        structured kernel serves it (bf16, D=64, no int8, no row truncated)."""
+        structured kernel serves it (bf16, D=64, no row truncated)."""
         D = self.d_head
         runtime = self._prepare_linear_runtime(T, B, alpha)
         L = int(runtime["effective_L"])
@@ -1402,7 +1417,7 @@ class AdaptiveSparseAttention(nn.Module):
         anchors = stride > 0 and slots > 0
         w_eff = max(1, local_w)
         bound = w_eff + ((min(slots, (T - 1) // stride) + 1) if anchors else 0) + K
-        structured = (dtype == torch.bfloat16 and D == 64 and not use_quant and bound <= L and K <= 1024
+        structured = (dtype == torch.bfloat16 and D == 64 and bound <= L and K <= 1024
                       and (not anchors or (T - 1) // stride + 1 <= 4096) and not _hip.env_flag("PFA_FORCE_GENERIC"))
         return {"L": L, "stride": stride, "local_w": local_w, "slots": slots, "K": K, "use_quant": use_quant,
                 "w_eff": w_eff, "structured": structured}
@@ -1448,6 +1463,11 @@ class AdaptiveSparseAttention(nn.Module):
             raise RuntimeError("q rows left unrotated for a path that does not rotate them")
         q5 = qkv.view(B, T, 3, H, D)
         if structured:
+            qkv_scales = None
+            if use_quant:
+                # int8 values in place, as exact bf16 integers; the kernel
+                # applies the scales in its tiles
+                qkv_scales = self._quantize_qkv(q5, B, T, heads, q5)
             t4 = (_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
                   _hip.tensor4(q5[:, :, 2], H, "bthd"), _hip.tensor4(attn.view(B, T, H, D), H, "bthd"))
             args = (H, T, D, token_idx, row_head, heads, summary, row_of, w_eff, stride, slots)
@@ -1489,13 +1509,13 @@ class AdaptiveSparseAttention(nn.Module):
             passes = 2 if (part is not None and streams is not None) else 3
             lens = _sa._shortlist_attn_structured(
                 *t4, *args, blocks, evict, scale, device, want_lengths=bool(self.record_shortlist_lengths),
-                q_rope=q_rope, passes=passes, part=part)
+                q_rope=q_rope, passes=passes, part=part, qkv_scales=qkv_scales)
             if tail_on_fork:
                 # join: the forward ends after the tail
                 streams[0].wait_stream(streams[1])
             self._last_shortlist_lengths = lens
             _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
-                            quantized=False, candidates=True, structured=True)
+                            quantized=use_quant, candidates=True, structured=True)
             self._last_shortlist_backend_info = get_last_backend_info()
             return
         sets = None
@@ -1507,22 +1527,15 @@ class AdaptiveSparseAttention(nn.Module):
         self._last_shortlist_lengths = lens
         out4 = _hip.tensor4(attn.view(B, T, H, D), H, "bthd")
         if use_quant:
-            # Per-head int8 of the active heads (aspa.py:1258-1267): the
-            # compact (P, T, D) tensors are quantised, attended, and the
-            # (P, T, D) result is scattered into the (B, T, H, D) output.
-            P = heads.numel()
-            hsel = heads.to(torch.int64)
-            comp = [q5[:, :, i].permute(0, 2, 1, 3).reshape(B * H, T, D).index_select(0, hsel) for i in range(3)]
-            qi, qs = self._quantize_per_head_int8(comp[0], "_quant_ema_q")
-            ki, ks = self._quantize_per_head_int8(comp[1], "_quant_ema_k")
-            vi, vs = self._quantize_per_head_int8(comp[2], "_quant_ema_v")
-            outc = torch.zeros(P, T, D, dtype=qkv.dtype, device=device)
-            _sa._attn_launch(_hip.tensor4(qi, P), _hip.tensor4(ki, P), _hip.tensor4(vi, P), torch.int8,
-                             _hip.tensor4(outc, P), qkv.dtype, P, T, D, token_idx, row_head, None, cand, lens, None,
-                             None, 1.0 / math.sqrt(D), (qs, ks, vs), device)
-            full = torch.zeros(B * H, T, D, dtype=qkv.dtype, device=device)
-            full.index_copy_(0, hsel, outc)
-            attn.copy_(full.view(B, H, T, D).permute(0, 2, 1, 3).reshape(B, T, H * D))
+            # Per-head int8 of the active heads (aspa.py:1258-1267) into an
+            # int8 copy of the QKV layout (only the active heads are written
+            # or read), attended with the per-global-head scales.
+            q8 = torch.empty(B, T, 3, H, D, dtype=torch.int8, device=device)
+            scales = self._quantize_qkv(q5, B, T, heads, q8)
+            _sa._attn_launch(_hip.tensor4(q8[:, :, 0], H, "bthd"), _hip.tensor4(q8[:, :, 1], H, "bthd"),
+                             _hip.tensor4(q8[:, :, 2], H, "bthd"), torch.int8, out4, qkv.dtype, H, T, D, token_idx,
+                             row_head, heads, cand, lens, None, None, 1.0 / math.sqrt(D),
+                             (scales[0], scales[1], scales[2]), device)
         else:
             _sa._attn_launch(_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
                              _hip.tensor4(q5[:, :, 2], H, "bthd"), qkv.dtype, out4, qkv.dtype, H, T, D, token_idx,
@@ -1530,6 +1543,19 @@ class AdaptiveSparseAttention(nn.Module):
         _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
                         quantized=use_quant, candidates=True, structured=False)
         self._last_shortlist_backend_info = get_last_backend_info()
+
+    def _quantize_qkv(self, q5: torch.Tensor, B: int, T: int, heads: torch.Tensor, dst5: torch.Tensor) -> torch.Tensor:
+        """Per-head int8 of the P = heads.numel() active heads of q, k and v
+        (the (B, T, 3, H, D) view of the projection) into dst5 (int8, or bf16
+        integers -- possibly q5 itself); returns the (3, B*H) f32 scales,
+        indexed by global head (b*H + h)."""
+        H, D = self.h_total, self.d_head
+        P = int(heads.numel())
+        scales = torch.empty(3, B * H, dtype=torch.float32, device=q5.device)
+        for i, name in enumerate(("_quant_ema_q", "_quant_ema_k", "_quant_ema_v")):
+            self._quantize_heads(_hip.tensor4(q5[:, :, i], H, "bthd"), q5.dtype, H, T, D, heads, P, None,
+                                 _hip.tensor4(dst5[:, :, i], H, "bthd"), dst5.dtype, scales[i], name)
+        return scales
 
     def _router_regulariser(self, gate_probs: torch.Tensor) -> Optional[torch.Tensor]:
         """Router regularisation terms (aspa.py:1543-1573, 1608-1614)."""

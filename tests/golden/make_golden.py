@@ -49,7 +49,7 @@ def _save(name: str, **arrays) -> None:
 
 
 def module_case(ref, name: str, cfg: dict, B: int, T: int, C: int, dtype: torch.dtype, outlier: float = 0.0,
-                token_stride: int = 1) -> None:
+                token_stride: int = 1, n_forward: int = 1) -> None:
     ModelConfig = ref.models.aspa.ModelConfig
     ASPA = ref.models.aspa.AdaptiveSparseAttention
     torch.manual_seed(1234)
@@ -69,8 +69,17 @@ def module_case(ref, name: str, cfg: dict, B: int, T: int, C: int, dtype: torch.
         return out
 
     m._route_tokens = spy
+    extra = {}
     with torch.no_grad():
         y = m(xd)
+        for i in range(1, n_forward):
+            # later forwards see the EMA state the earlier ones left
+            extra[f"y_first{i}"] = y[:, ::token_stride].float()
+            y = m(xd)
+    for nm in ("_quant_ema_q", "_quant_ema_k", "_quant_ema_v"):
+        t = getattr(m, nm, None)
+        if isinstance(t, torch.Tensor):
+            extra[nm.lstrip("_")] = t.detach().float()
     st = m._last_sparse_state or {}
     # x and the weights are regenerated from the seed by the tests; their
     # digests pin the regeneration.
@@ -82,7 +91,7 @@ def module_case(ref, name: str, cfg: dict, B: int, T: int, C: int, dtype: torch.
         protos_after=m.routing_prototypes.detach().float(), usage_after=m.routing_usage_ema.detach().float(),
         conf_after=m.routing_confidence.detach().float(),
         linear_L=np.int64(m.linear_L), linear_window=np.int64(m.linear_window),
-        mode=np.array(str(m.last_head_stats.get("mode"))),
+        mode=np.array(str(m.last_head_stats.get("mode"))), n_forward=np.int64(n_forward), **extra,
     )
     if m._last_token_mask is not None:
         arrays["token_mask"] = m._last_token_mask.to(torch.uint8)
@@ -177,18 +186,60 @@ def main() -> None:
     import proteus_attention as ref
 
     torch.set_num_threads(8)
+    cases = module_cases()
+    only = [a for a in sys.argv[2:]]
+    if only:
+        # the named cases only (every other fixture left as it is)
+        for name in only:
+            cases[name](ref)
+        return
     builder_cases(ref)
     attention_cases(ref)
     chunk_cases(ref)
-    # config 1 exactly (f32), token-sparse causal
-    module_case(ref, "module_cfg1", sparse_cfg(1024, 256, 8), 1, 1024, 256, torch.float32)
-    # config 2 shape reduced in T (bf16), token-sparse causal; every 4th token stored
-    module_case(ref, "module_cfg2_T2048", sparse_cfg(2048, 512, 8), 2, 2048, 512, torch.bfloat16, token_stride=4)
-    # shortlist mode (config 3 recipe at T=4096, L=1024, window 256, stride 64), f32 and bf16
-    module_case(ref, "module_short_T4096_f32", shortlist_cfg(4096, 512, 8, 1024, 256, 64), 1, 4096, 512,
-                torch.float32, outlier=0.01, token_stride=4)
-    module_case(ref, "module_short_T4096_bf16", shortlist_cfg(4096, 512, 8, 1024, 256, 64), 1, 4096, 512,
-                torch.bfloat16, outlier=0.01, token_stride=4)
+    for name, fn in cases.items():
+        if name not in FULL_SIZE_CASES:
+            fn(ref)
+
+
+# Cases at a BASELINE config's full size take minutes of CPU time in the
+# reference; they are written only when named on the command line.
+FULL_SIZE_CASES = ("module_cfg2_full",)
+
+
+def module_cases():
+    short = shortlist_cfg(2048, 512, 8, 512, 128, 32)
+    return {
+        # config 1 exactly (f32), token-sparse causal
+        "module_cfg1": lambda ref: module_case(ref, "module_cfg1", sparse_cfg(1024, 256, 8), 1, 1024, 256,
+                                               torch.float32),
+        # config 2 shape reduced in T (bf16), token-sparse causal; every 4th token stored
+        "module_cfg2_T2048": lambda ref: module_case(ref, "module_cfg2_T2048", sparse_cfg(2048, 512, 8), 2, 2048, 512,
+                                                     torch.bfloat16, token_stride=4),
+        # config 2 at its BASELINE size (B=2, T=8192), every 16th token stored
+        "module_cfg2_full": lambda ref: module_case(ref, "module_cfg2_full", sparse_cfg(8192, 512, 8), 2, 8192, 512,
+                                                    torch.bfloat16, token_stride=16),
+        # shortlist mode (config 3 recipe at T=4096, L=1024, window 256, stride 64), f32 and bf16
+        "module_short_T4096_f32": lambda ref: module_case(ref, "module_short_T4096_f32",
+                                                          shortlist_cfg(4096, 512, 8, 1024, 256, 64), 1, 4096, 512,
+                                                          torch.float32, outlier=0.01, token_stride=4),
+        "module_short_T4096_bf16": lambda ref: module_case(ref, "module_short_T4096_bf16",
+                                                           shortlist_cfg(4096, 512, 8, 1024, 256, 64), 1, 4096, 512,
+                                                           torch.bfloat16, outlier=0.01, token_stride=4),
+        # per-head int8 mode (aspa.py:1258-1267, 1312-1363) in its three base
+        # rules: absmax and percentile in bf16, EMA of the percentile in f32
+        # over two forwards (the second reads the EMA the first left)
+        "module_int8_max_bf16": lambda ref: module_case(ref, "module_int8_max_bf16",
+                                                        dict(short, attn_quantize_int8=True), 1, 2048, 512,
+                                                        torch.bfloat16, outlier=0.01, token_stride=8),
+        "module_int8_pct_bf16": lambda ref: module_case(
+            ref, "module_int8_pct_bf16", dict(short, attn_quantize_int8=True, attn_quantize_int8_mode="percentile",
+                                              attn_quantize_int8_percentile=0.995), 1, 2048, 512, torch.bfloat16,
+            outlier=0.01, token_stride=8),
+        "module_int8_ema_f32": lambda ref: module_case(
+            ref, "module_int8_ema_f32", dict(short, attn_quantize_int8=True, attn_quantize_int8_mode="ema_percentile",
+                                             attn_quantize_int8_percentile=0.99, attn_quantize_int8_ema_decay=0.8),
+            1, 2048, 512, torch.float32, outlier=0.01, token_stride=8, n_forward=2),
+    }
 
 
 if __name__ == "__main__":

@@ -1,0 +1,175 @@
+"""GPU: the per-head int8 mode (reference aspa.py:1258-1267, 1312-1363) on
+the device -- pfa_quantize_heads_int8 against the oracle, and module
+forwards with attn_quantize_int8 against golden vectors written by the
+reference (structured MFMA path in bf16, materialised row path in f32)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import aspa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+# int8 outputs: the quantised values move by one step wherever a projected
+# element sits within rounding distance of a .5 boundary of x/scale (the
+# GPU and CPU projections round differently), so the int8 path is held to
+# the bf16 bound in both dtypes.
+TOL_INT8 = 2e-2
+
+
+def _say(msg: str) -> None:
+    print(f"[int8] {msg}", flush=True)
+
+
+def _quantize(dev, x5, heads, mode, pct, ema, ema_valid, out_dtype, decay=0.8):
+    """Run pfa_quantize_heads_int8 on the q third of a (B, T, 3, H, D) tensor
+    for the given global heads."""
+    from proteus_attention import _hip
+    from proteus_attention.kernels import sparse_attn as sa
+
+    B, T, _, H, D = x5.shape
+    xd = x5.to(dev)
+    dst = torch.zeros(B, T, 3, H, D, dtype=out_dtype, device=dev)
+    scales = torch.full((B * H,), -1.0, device=dev)
+    hm = torch.tensor(heads, dtype=torch.int32, device=dev)
+    sa.quantize_heads_int8(_hip.tensor4(xd[:, :, 0], H, "bthd"), xd.dtype, H, T, D, hm, len(heads), None, mode, pct,
+                           decay, ema, ema_valid, _hip.tensor4(dst[:, :, 0], H, "bthd"), out_dtype, scales, dev)
+    torch.cuda.synchronize()
+    return dst[:, :, 0].cpu(), scales.cpu()
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("mode,pct", [("max", 1.0), ("percentile", 0.995), ("percentile", 0.5), ("percentile", 1.0),
+                                      ("ema_percentile", 0.99), ("ema_percentile", 0.0)])
+def test_quantize_heads_vs_oracle(dev, dt, mode, pct):
+    """Scales bit for bit and every int8 value, per active head of a strided
+    (B, T, 3, H, D) view, for each base rule.  The tensor holds heavy ties
+    (values on a coarse grid) and a head that is mostly zeros, so the
+    quantile lands inside runs of equal values and on 0 (-> absmax)."""
+    _say(f"quantize {mode} p={pct} {dt}")
+    g = torch.Generator().manual_seed(3)
+    B, T, H, D = 2, 777, 4, 64
+    x = torch.randn(B, T, 3, H, D, generator=g)
+    x[0, :, 0, 1] = torch.round(x[0, :, 0, 1] * 4) / 4  # ties
+    x[1, :, 0, 2] = 0.0
+    x[1, :5, 0, 2] = torch.randn(5, 64, generator=g)  # mostly zeros
+    x = x.to(dt)
+    heads = [1, 6, 2, 4]  # global b*H + h, compact order
+    ema0 = torch.tensor([3.0, 0.5, 2.0, 7.0])
+    for ema_valid in ((False, True) if mode == "ema_percentile" else (False,)):
+        ema = ema0.clone().to(dev) if mode == "ema_percentile" else None
+        for out_dtype in (torch.int8, torch.bfloat16):
+            e = ema.clone() if ema is not None else None
+            got, sc = _quantize(dev, x, heads, mode, pct, e, ema_valid, out_dtype)
+            for p, bh in enumerate(heads):
+                b, h = divmod(bh, H)
+                t = x[b, :, 0, h].unsqueeze(0)
+                prev = ema0[p:p + 1] if ema_valid else None
+                qv, s, new_ema = O.quantize_per_head_int8(t, mode, pct, prev, 0.8)
+                assert sc[bh].item() == s.item(), (mode, pct, bh, sc[bh].item(), s.item())
+                assert torch.equal(got[b, :, h].to(torch.int8 if out_dtype == torch.int8 else torch.float32),
+                                   qv[0].to(torch.int8 if out_dtype == torch.int8 else torch.float32))
+                if new_ema is not None:
+                    assert e.cpu()[p].item() == new_ema.item()
+            inactive = [i for i in range(B * H) if i not in heads]
+            assert torch.all(sc[inactive] == -1.0)
+
+
+def test_quantize_heads_device_summary_limits_heads(dev):
+    """With summary = {P, ...} on the device only the first P compact heads
+    are quantised (the module's packing gives P on the device)."""
+    from proteus_attention import _hip
+    from proteus_attention.kernels import sparse_attn as sa
+
+    B, T, H, D = 1, 300, 8, 64
+    x = torch.randn(B, T, H, D).to(torch.bfloat16).to(dev)
+    scales = torch.full((H,), -1.0, device=dev)
+    dst = torch.zeros(B, T, H, D, dtype=torch.int8, device=dev)
+    hm = torch.tensor([5, 0, 3, 7], dtype=torch.int32, device=dev)
+    summ = torch.tensor([2, 0, 0, 0], dtype=torch.int32, device=dev)
+    sa.quantize_heads_int8(_hip.tensor4(x, H, "bthd"), x.dtype, H, T, D, hm, 4, summ, "max", 1.0, 0.9, None, False,
+                           _hip.tensor4(dst, H, "bthd"), torch.int8, scales, dev)
+    sc = scales.cpu()
+    assert sc[5] > 0 and sc[0] > 0 and sc[3] == -1.0 and sc[7] == -1.0
+    assert torch.count_nonzero(dst[:, :, 3]) == 0
+
+
+def _module(cfg, B, T, C, dt, dev, outlier):
+    from configs import init_weights, make_inputs
+
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    torch.manual_seed(1234)
+    m = AdaptiveSparseAttention(ModelConfig(**cfg))
+    x, g = make_inputs(B, T, C, seed=0, outlier_frac=outlier)
+    init_weights(m, g)
+    m = m.to(device=dev, dtype=dt).eval()
+    return m, x.to(dt).to(dev)
+
+
+def _heads_per_token(token_idx, row_offsets, heads, B, H, T):
+    act = torch.zeros(B * H, T, dtype=torch.bool)
+    offs = row_offsets.tolist()
+    for p, bh in enumerate(heads.tolist()):
+        act[bh, token_idx[offs[p]:offs[p + 1]]] = True
+    return act.view(B, H, T).permute(0, 2, 1)
+
+
+@pytest.mark.parametrize("name,dt,extra,structured", [
+    ("module_int8_max_bf16", torch.bfloat16, {}, True),
+    ("module_int8_pct_bf16", torch.bfloat16, dict(attn_quantize_int8_mode="percentile",
+                                                  attn_quantize_int8_percentile=0.995), True),
+    ("module_int8_ema_f32", torch.float32, dict(attn_quantize_int8_mode="ema_percentile",
+                                                attn_quantize_int8_percentile=0.99, attn_quantize_int8_ema_decay=0.8),
+     False),
+])
+def test_module_int8_vs_golden(dev, golden, name, dt, extra, structured):
+    """Module forwards with attn_quantize_int8 against the reference's own
+    outputs (its CPU fallback dequantises and attends in f32).  bf16 runs
+    the structured MFMA kernel on the int8 values (scores from exact integer
+    dots, scales applied in the tile); f32 runs the materialised row kernel
+    on int8 tensors.  The EMA case runs two forwards and checks the per-head
+    EMA buffers the reference leaves."""
+    from configs import shortlist_cfg
+
+    from proteus_attention.kernels.sparse_attn import get_last_backend_info
+
+    _say(f"module {name}")
+    z = golden(name)
+    B, T, C, H = 1, 2048, 512, 8
+    cfg = dict(shortlist_cfg(T, C, H, 512, 128, 32), attn_quantize_int8=True, **extra)
+    m, x = _module(cfg, B, T, C, dt, dev, 0.01)
+    n_fwd = int(z["n_forward"])
+    stride = int(z["token_stride"])
+    ys = []
+    with torch.no_grad():
+        for _ in range(n_fwd):
+            ys.append(m(x).float().cpu()[:, ::stride])
+    info = get_last_backend_info()
+    assert info["name"] == "hip" and info["details"]["quantized"] is True
+    assert info["details"]["structured"] is structured
+    st = m._last_sparse_state
+    assert st["quantized"] is True
+    ours = _heads_per_token(st["token_idx"].cpu().long(), st["row_offsets"].cpu().long(),
+                            st["active_head_indices"].cpu(), B, H, T)
+    ref = _heads_per_token(torch.from_numpy(z["packed_token_idx"]), torch.from_numpy(z["packed_row_offsets"]),
+                           torch.from_numpy(z["active_head_indices"]), B, H, T)
+    same = (ours == ref).all(-1)
+    n_flip = int((~same).sum())
+    _say(f"{name}: tokens routed differently: {n_flip}")
+    if dt == torch.float32:
+        assert n_flip == 0
+    sel = same[:, ::stride]
+    refs = ([torch.from_numpy(z["y_first1"])] if n_fwd == 2 else []) + [torch.from_numpy(z["y"])]
+    for i, (yo, yr) in enumerate(zip(ys, refs)):
+        err = float((yo - yr).abs().amax(-1)[sel].max())
+        _say(f"{name}: forward {i} max-abs err {err:.3e}")
+        assert err <= TOL_INT8
+    if "quant_ema_q" in z and dt == torch.float32:
+        for nm in ("quant_ema_q", "quant_ema_k", "quant_ema_v"):
+            got = getattr(m, "_" + nm).float().cpu()
+            exp = torch.from_numpy(z[nm])
+            assert got.shape == exp.shape
+            assert torch.allclose(got, exp, rtol=1e-5, atol=1e-6), nm

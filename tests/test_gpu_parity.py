@@ -694,7 +694,7 @@ def test_attention_int8_vs_oracle(dev):
     q, k, v = (torch.randn(4, 33, 16, generator=g) for _ in range(3))
     m = torch.rand(4, 33, generator=g) > 0.4
     causal = torch.triu(torch.full((33, 33), float("-inf")), diagonal=1)
-    (qi, qs), (ki, ks), (vi, vs) = (O.quantize_per_head_int8(t) for t in (q, k, v))
+    (qi, qs, _), (ki, ks, _), (vi, vs, _) = (O.quantize_per_head_int8(t) for t in (q, k, v))
     out = aspa_sparse_attention(qi.to(dev), ki.to(dev), vi.to(dev), active_mask=m.to(dev),
                                 causal_mask=causal.to(dev), q_scale=qs.to(dev), k_scale=ks.to(dev),
                                 v_scale=vs.to(dev), out_dtype=torch.float32)

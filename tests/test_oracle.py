@@ -201,10 +201,36 @@ def test_candidates_covering_prefix_equal_causal():
 def test_quantize_per_head_closed_form():
     g = torch.Generator().manual_seed(4)
     t = torch.randn(3, 10, 4, generator=g)
-    qv, s = O.quantize_per_head_int8(t)
+    qv, s, _ = O.quantize_per_head_int8(t)
     assert torch.allclose(s, t.reshape(3, -1).abs().amax(1) / 127.0)
     assert int(qv.abs().max()) == 127
     assert torch.allclose(qv.float() * s.view(-1, 1, 1), t, atol=float(s.max()) / 2 + 1e-7)
+
+
+def test_quantize_per_head_percentile_and_ema_closed_forms():
+    """Percentile base = the linear interpolation between the two order
+    statistics around rank p*(n-1) of |x| (by hand on a small sorted list),
+    the absmax when that is 0; ema_percentile = decay*ema + (1-decay)*base,
+    seeded with the absmax (aspa.py:1325-1355)."""
+    t = torch.tensor([[[0.0, -4.0], [1.0, 2.0], [-3.0, 0.5]], [[0.0, 0.0], [0.0, 0.0], [0.0, 9.0]]])
+    # head 0: |x| sorted = 0, .5, 1, 2, 3, 4; p = .5 -> rank 2.5 -> 1 + .5*(2 - 1) = 1.5
+    _, s, _ = O.quantize_per_head_int8(t, "percentile", 0.5)
+    assert s[0].item() == pytest.approx(1.5 / 127.0, rel=1e-7)
+    # head 1: the median of |x| is 0 -> the absmax 9
+    assert s[1].item() == pytest.approx(9.0 / 127.0, rel=1e-7)
+    # p = 1 is the absmax; p = 0 means "max" (percentile <= 0)
+    _, s1, _ = O.quantize_per_head_int8(t, "percentile", 1.0)
+    _, s0, _ = O.quantize_per_head_int8(t, "percentile", 0.0)
+    assert torch.equal(s1, torch.tensor([4.0, 9.0]) / 127.0) and torch.equal(s0, s1)
+    # EMA: first call seeds with the absmax, the second reads the first
+    _, s_a, e1 = O.quantize_per_head_int8(t, "ema_percentile", 0.5, None, 0.75)
+    assert e1[0].item() == pytest.approx(0.75 * 4.0 + 0.25 * 1.5, rel=1e-7)
+    _, s_b, e2 = O.quantize_per_head_int8(t, "ema_percentile", 0.5, e1, 0.75)
+    assert e2[0].item() == pytest.approx(0.75 * e1[0].item() + 0.25 * 1.5, rel=1e-7)
+    assert s_b[0].item() == pytest.approx(e2[0].item() / 127.0, rel=1e-7)
+    # the planted mistake: seeding the EMA with the quantile instead of the
+    # absmax gives another value
+    assert e1[0].item() != pytest.approx(1.5, rel=1e-3)
 
 
 # ---------------------------------------------------------------------------
