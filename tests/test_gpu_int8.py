@@ -157,10 +157,15 @@ def test_module_int8_vs_golden(dev, golden, name, dt, extra, structured):
     ref = _heads_per_token(torch.from_numpy(z["packed_token_idx"]), torch.from_numpy(z["packed_row_offsets"]),
                            torch.from_numpy(z["active_head_indices"]), B, H, T)
     same = (ours == ref).all(-1)
-    n_flip = int((~same).sum())
-    _say(f"{name}: tokens routed differently: {n_flip}")
     if dt == torch.float32:
-        assert n_flip == 0
+        assert bool(same.all())
+    else:
+        from routing_parity import check_routing
+
+        rep = check_routing(ours.reshape(T, H), ref.reshape(T, H), m._last_gate_probs.float().cpu().reshape(T, H),
+                            torch.from_numpy(z["gate_probs"]).reshape(T, H), x.cpu().reshape(T, C),
+                            m.head_router.linear.weight.detach().cpu(), 2)
+        _say(f"{name}: {rep}")
     sel = same[:, ::stride]
     refs = ([torch.from_numpy(z["y_first1"])] if n_fwd == 2 else []) + [torch.from_numpy(z["y"])]
     for i, (yo, yr) in enumerate(zip(ys, refs)):
