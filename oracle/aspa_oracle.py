@@ -495,11 +495,12 @@ def quantize_rows_int8(x: torch.Tensor, heads: int) -> Tuple[torch.Tensor, torch
 
 def int8_kv_attention(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor, k_scale: torch.Tensor,
                       v_scale: torch.Tensor, key_pos: torch.Tensor, causal: bool = True,
-                      scale: Optional[float] = None) -> torch.Tensor:
+                      scale: Optional[float] = None, q_pos: Optional[torch.Tensor] = None) -> torch.Tensor:
     """q (T, H, D); k8/v8 (H, S, D) int8 with scales (H, S); key_pos (S,).
     Dequantise in f32, softmax(q k^T * scale + mask) v in f32 with key j
     visible to query t iff key_pos[j] <= t (causal); rows with no visible
-    key are zero.  Returns (T, H, D) f32."""
+    key are zero.  q_pos (T,): the positions of the query rows when q holds
+    a subset of the sequence (default 0..T-1).  Returns (T, H, D) f32."""
 
     T, H, D = q.shape
     sc = (1.0 / math.sqrt(D)) if scale is None else float(scale)
@@ -509,7 +510,8 @@ def int8_kv_attention(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor, k_sca
     s = (qh @ k.transpose(1, 2)) * sc  # (H, T, S)
     vis = torch.ones(T, k.size(1), dtype=torch.bool)
     if causal:
-        vis = key_pos.view(1, -1).to(torch.long) <= torch.arange(T).view(-1, 1)
+        qp = torch.arange(T) if q_pos is None else q_pos.to(torch.long)
+        vis = key_pos.view(1, -1).to(torch.long) <= qp.view(-1, 1)
     s = s.masked_fill(~vis.unsqueeze(0), float("-inf"))
     p = torch.softmax(s, dim=-1)
     p = torch.nan_to_num(p, nan=0.0)  # all-masked rows -> zero output
