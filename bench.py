@@ -283,8 +283,12 @@ def bench_forward(args, workload: str) -> dict:
 
 
 def bench_cfg5(args) -> dict:
-    """Config 5: one run of the chunked shortlist pipeline over a sequence
-    already resident in HBM; the last of warmup + steps runs is reported."""
+    """Config 5: one run of the chunked shortlist pipeline; the last of
+    warmup + steps runs is reported.  --cfg5-source device: the sequence is
+    resident in HBM; pinned: it stays in pinned host memory and every chunk
+    is copied in by the runner's double-buffered stager (the copy of chunk
+    i+1 under the compute of chunk i); disk: staged in a disk memmap and
+    read into pinned buffers by a worker thread."""
     import torch
 
     from proteus_attention import _hip
@@ -293,11 +297,14 @@ def bench_cfg5(args) -> dict:
     c = CFG5
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(0)
-    log("building config-5 sequence (T=1,048,576)")
-    x = torch.randn(1, c["T"], c["C"], generator=g).to(torch.bfloat16).to(dev)
+    log(f"building config-5 sequence (T=1,048,576, source {args.cfg5_source})")
+    x = torch.randn(1, c["T"], c["C"], generator=g).to(torch.bfloat16)
+    if args.cfg5_source == "device":
+        x = x.to(dev)
     cfg = ChunkedShortlistConfig(seq_len=c["T"], d_model=c["C"], chunk_len=c["chunk"], buffer_tokens=c["buffer"],
                                  per_chunk_budget=c["budget"], device=dev, heads=c["H"], nucleus_top_p=1.0,
-                                 final_mode="all_queries", report_latency=True)
+                                 final_mode="all_queries", report_latency=True,
+                                 storage="disk" if args.cfg5_source == "disk" else "cpu")
     runs = max(1, args.warmup) + max(1, args.steps)
     walls = []
     for i in range(runs):
@@ -323,7 +330,10 @@ def bench_cfg5(args) -> dict:
     kernels = kernel_table(stages, alg, {})
     dk = kernels["int8_kv_attn_fwd"]
     log(f"runs wall ms: {' '.join(f'{1e3 * w:.1f}' for w in walls)}; chunk {mt.chunk_time_ms:.2f} ms, "
-        f"final {mt.final_time_ms:.2f} ms, kept {mt.retained_tokens}")
+        f"final {mt.final_time_ms:.2f} ms, kept {mt.retained_tokens}, staging {mt.storage_mode}, "
+        f"h2d {mt.h2d_time_ms} ms (compute stream waited {mt.h2d_stall_ms} ms)")
+    source = {"device": "resident in HBM", "pinned": "in pinned host memory, streamed chunk by chunk",
+              "disk": "staged in a disk memmap, streamed chunk by chunk"}[args.cfg5_source]
     return {
         "metric": "chunked shortlist pipeline tokens/s @T=1M bf16 (int8 shortlist, all-query final pass), 1 GPU",
         "value": round(c["T"] / (pipe_ms * 1e-3), 1),
@@ -335,11 +345,13 @@ def bench_cfg5(args) -> dict:
         "wall_ms_per_run": round(1e3 * walls[-1], 3),
         "chunk_ms": round(mt.chunk_time_ms, 4),
         "final_ms": round(mt.final_time_ms, 4),
+        "h2d_ms": None if mt.h2d_time_ms is None else round(mt.h2d_time_ms, 4),
+        "h2d_stall_ms": None if mt.h2d_stall_ms is None else round(mt.h2d_stall_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: x~N(0,1) seed 0, resident in HBM; random-init chunk and final models",
+        "data": f"synthetic: x~N(0,1) seed 0, {source}; random-init chunk and final models",
         "config": {"workload": "config 5: chunked shortlist, T=1048576 d_model=512 H=8 D=64, chunks of 65536, "
                                "top-512 per chunk, 8192-token shortlist, int8 per-(head,row) K/V, all-query "
                                "causal-by-position final pass", "retained": mt.retained_tokens,
@@ -358,6 +370,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=("cfg3", "cfg4", "cfg5"), default="cfg3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cfg5-source", choices=("device", "pinned", "disk"), default="device",
+                    help="where config 5's sequence lives (--workload cfg5)")
     ap.add_argument("--eager", action="store_true", help="time the forward without HIP graph replay")
     ap.add_argument("--default-gemms", action="store_true",
                     help="use torch's default GEMM heuristic instead of the shipped MI355X table")

@@ -6,13 +6,17 @@ are merged into a global shortlist (sorted by position), and a final ASPA
 pass runs over the reduced sequence.
 
 Same configuration, result and metric types as the reference.  Host staging
-(pinned RAM or a disk memmap) follows the reference; chunk copies go through
-a reused device buffer.  Chunk salience is the router importance of the chunk
-model (device tensors); the reference's norm-score fallback only applies when
-no importance is available.
+(pinned RAM or a disk memmap) follows the reference.  Chunks reach the device
+through two device buffers filled on a copy stream (_ChunkStager): the copy
+of chunk i+1 runs while chunk i is computed, and with disk staging a worker
+thread reads chunk i+2 from the memmap into one of two pinned buffers
+meanwhile.  Chunk salience is the router importance of the chunk model
+(device tensors); the reference's norm-score fallback only applies when no
+importance is available.
 """
 from __future__ import annotations
 
+import concurrent.futures as cf
 import contextlib
 import logging
 import math
@@ -152,6 +156,11 @@ class ChunkedShortlistMetrics:
     host_allocated_mb: Optional[float] = None
     host_limit_mb: Optional[float] = None
     storage_reason: Optional[str] = None
+    # host-staged runs: total host-to-device copy time (on the copy stream)
+    # and the part of it the compute stream waited for (not hidden behind
+    # the previous chunk's compute)
+    h2d_time_ms: Optional[float] = None
+    h2d_stall_ms: Optional[float] = None
 
 
 @dataclass
@@ -222,6 +231,104 @@ class ChunkedShortlistConfig:
             raise ValueError("ram_limit_bytes must be positive when provided.")
         if self.final_mode not in {"reduced", "all_queries"}:
             raise ValueError("final_mode must be 'reduced' or 'all_queries'.")
+
+
+class _ChunkStager:
+    """Double-buffered host-to-device chunk streaming (reference
+    chunked_shortlist.py:617-625, 688-689 copy each chunk with a blocking
+    .to(device)).
+
+    Two device buffers take alternate chunks.  start(i) queues chunk i's copy
+    on a copy stream (default priority) after the compute stream has
+    released that buffer (chunk i-2); take(i) makes the compute stream wait
+    for it; release(i) marks the compute stream's use of the buffer done.
+    Pinned staging ("cpu" mode) copies straight from the pinned sequence;
+    disk staging reads chunk rows from the memmap into one of two pinned
+    buffers on a worker thread (chunk i+1 is read while chunk i is copied
+    and computed), each buffer reused only after its previous copy is done.
+    Copy time and the compute stream's waits are measured with events."""
+
+    def __init__(self, st: Dict[str, Any], chunks: List[Tuple[int, int]], chunk_len: int, d_model: int,
+                 device: torch.device, dtype: torch.dtype) -> None:
+        self.st, self.chunks, self.device = st, chunks, device
+        self.bufs = [torch.empty(1, chunk_len, d_model, device=device, dtype=dtype) for _ in range(2)]
+        self.copy_s = torch.cuda.Stream(device=device)
+        self.ready = [torch.cuda.Event() for _ in range(2)]
+        self.freed = [None, None]
+        self.copy_ev = []
+        self.wait_ev = []
+        self.disk = st.get("memmap") is not None
+        self.pool = None
+        if self.disk:
+            self.host = [torch.empty(1, chunk_len, d_model, dtype=dtype).pin_memory() for _ in range(2)]
+            self.h2d_done = [None, None]
+            self.pool = cf.ThreadPoolExecutor(max_workers=1)
+            self.fills: Dict[int, cf.Future] = {}
+            self._fill(0)
+
+    def _fill(self, i: int) -> None:
+        if i >= len(self.chunks) or i in self.fills:
+            return
+        s, e = self.chunks[i]
+        slot = i % 2
+        done = self.h2d_done[slot]
+
+        def work() -> None:
+            if done is not None:
+                done.synchronize()  # the previous copy out of this pinned buffer
+            self.host[slot][:, :e - s].copy_(torch.from_numpy(np.asarray(self.st["memmap"][s:e])).unsqueeze(0))
+
+        self.fills[i] = self.pool.submit(work)
+
+    def start(self, i: int) -> None:
+        s, e = self.chunks[i]
+        slot = i % 2
+        if self.disk:
+            self._fill(i)
+            self.fills.pop(i).result()
+            src = self.host[slot][:, :e - s]
+        else:
+            src = self.st["fetch"](s, e)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(self.copy_s):
+            if self.freed[slot] is not None:
+                self.copy_s.wait_event(self.freed[slot])
+            e0.record(self.copy_s)
+            self.bufs[slot][:, :e - s].copy_(src, non_blocking=True)
+            e1.record(self.copy_s)
+            self.ready[slot].record(self.copy_s)
+        self.copy_ev.append((e0, e1))
+        if self.disk:
+            ev = torch.cuda.Event()
+            ev.record(self.copy_s)
+            self.h2d_done[slot] = ev
+            self._fill(i + 1)
+
+    def take(self, i: int) -> torch.Tensor:
+        s, e = self.chunks[i]
+        slot = i % 2
+        cur = torch.cuda.current_stream(self.device)
+        w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0.record(cur)
+        cur.wait_event(self.ready[slot])
+        w1.record(cur)
+        self.wait_ev.append((w0, w1))
+        return self.bufs[slot][:, :e - s]
+
+    def release(self, i: int) -> None:
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self.freed[i % 2] = ev
+
+    def timings_ms(self) -> Tuple[float, float]:
+        torch.cuda.synchronize(self.device)
+        copy = sum(a.elapsed_time(b) for a, b in self.copy_ev)
+        stall = sum(a.elapsed_time(b) for a, b in self.wait_ev)
+        return float(copy), float(stall)
+
+    def close(self) -> None:
+        if self.pool is not None:
+            self.pool.shutdown(wait=True)
 
 
 class ChunkedShortlistRunner:
@@ -346,8 +453,7 @@ class ChunkedShortlistRunner:
             chunk_model.use_sdpa = False
             chunk_model.set_shortlist_alpha(float(cfg.shortlist_alpha))
             direct = st["mode"] == "device"
-            chunk_buf = None if direct else torch.empty(1, cfg.chunk_len, cfg.d_model, device=device,
-                                                        dtype=base_dtype)
+            chunks = list(_chunk_iter(cfg.seq_len, cfg.chunk_len))
             final_model = None
             all_q = None
             if cfg.run_final_pass and cfg.final_mode == "all_queries":
@@ -368,15 +474,20 @@ class ChunkedShortlistRunner:
                 ev_c0.record()
             t_start = time.perf_counter()
             t_chunks = t_start
-            for ci, (s, e) in enumerate(_chunk_iter(cfg.seq_len, cfg.chunk_len)):
-                n = e - s
+            stager = None
+            if not direct:
+                if device.type != "cuda":
+                    raise RuntimeError("host-staged chunks need a ROCm device")
+                stager = _ChunkStager(st, chunks, cfg.chunk_len, cfg.d_model, device, base_dtype)
+                st["stager"] = stager
+                stager.start(0)
+            for ci, (s, e) in enumerate(chunks):
                 if direct:
                     xc = st["fetch"](s, e)
                 else:
-                    chunk_buf[:, :n].copy_(st["fetch"](s, e), non_blocking=st["pinned"])
-                    if n < cfg.chunk_len:
-                        chunk_buf[:, n:].zero_()
-                    xc = chunk_buf[:, :n]
+                    if ci + 1 < len(chunks):
+                        stager.start(ci + 1)  # its copy overlaps this chunk's compute
+                    xc = stager.take(ci)
                 with torch.inference_mode():
                     chunk_model(xc)
                     if all_q is not None:
@@ -387,12 +498,16 @@ class ChunkedShortlistRunner:
                     sel = _nucleus_select(xc[0].detach().norm(dim=-1).to(torch.float32),
                                           cfg.per_chunk_budget, cfg.nucleus_top_p)
                     if sel is None:
+                        if stager is not None:
+                            stager.release(ci)
                         continue
                     vals, rel = sel
                     sc, ix = vals, rel.to(torch.long) + s
                     used_fallback = True
                 else:
                     sc, ix = promoted
+                if stager is not None:
+                    stager.release(ci)
                 scores_all.append(sc)
                 idx_all.append(ix)
                 summaries.append(ChunkSummary(index=ci, start=s, end=e, promoted=ix.tolist(),
@@ -454,6 +569,9 @@ class ChunkedShortlistRunner:
                     final_tok = cfg.seq_len if all_q is not None else keep_idx.numel()
                     final_tps = float(final_tok * 1000.0 / final_ms)
             total = t_final_end - t_start
+            h2d_ms = h2d_stall = None
+            if stager is not None:
+                h2d_ms, h2d_stall = stager.timings_ms()
             metrics = ChunkedShortlistMetrics(
                 original_tokens=cfg.seq_len, retained_tokens=int(keep_idx.numel()),
                 retention_ratio=float(keep_idx.numel() / max(cfg.seq_len, 1)), chunk_count=len(summaries),
@@ -463,7 +581,7 @@ class ChunkedShortlistRunner:
                 storage_mode=st["mode"], host_required_mb=st["dataset"] / BYTES_PER_MB,
                 host_allocated_mb=st["allocated"] / BYTES_PER_MB if st.get("allocated") is not None else None,
                 host_limit_mb=st["limit"] / BYTES_PER_MB if st["limit"] is not None else None,
-                storage_reason=st["reason"])
+                storage_reason=st["reason"], h2d_time_ms=h2d_ms, h2d_stall_ms=h2d_stall)
             self.logger.info("Chunked Shortlist retained %s/%s tokens (%.3f) across %s chunks",
                              metrics.retained_tokens, metrics.original_tokens, metrics.retention_ratio,
                              metrics.chunk_count)
@@ -471,6 +589,8 @@ class ChunkedShortlistRunner:
                                           metrics=metrics, chunks=summaries, final_output=final_out,
                                           final_stats=final_stats, backend_info=backend_info)
         finally:
+            if st.get("stager") is not None:
+                st["stager"].close()
             if st.get("memmap") is not None:
                 st["memmap"].flush()
             if st.get("path") is not None:

@@ -166,3 +166,37 @@ def test_chunked_runner_all_queries_gpu(dev):
     assert err <= 2e-2, err
     for ch in res.chunks:
         assert all(ch.start <= p < ch.end for p in ch.promoted)
+
+
+@pytest.mark.parametrize("source", ["cpu_tensor", "disk_tensor", "generated_cpu"])
+def test_chunked_runner_host_staging_matches_device(dev, source):
+    """Host-staged runs (a CPU tensor staged in pinned RAM, the same tensor
+    staged in a disk memmap, and the runner's own seeded sequence) stream
+    their chunks through the double-buffered stager and select exactly what
+    the device-resident run over the same values selects."""
+    from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
+
+    T, C = 8192, 512
+    print(f"chunked runner staging {source}", flush=True)
+    kw = dict(seq_len=T, d_model=C, chunk_len=2048, buffer_tokens=512, per_chunk_budget=128, device=dev, heads=8,
+              nucleus_top_p=1.0, run_final_pass=False, seed=7)
+    if source == "generated_cpu":
+        gen = torch.Generator(device="cpu").manual_seed(7)
+        x = torch.randn(1, T, C, generator=gen)  # the runner's own sequence (default dtype)
+        torch.manual_seed(5)  # the chunk model's initial weights
+        res = ChunkedShortlistRunner(ChunkedShortlistConfig(storage="cpu", **kw)).run(None)
+    else:
+        x = torch.randn(1, T, C, generator=torch.Generator().manual_seed(21)).to(torch.bfloat16)
+        storage = "disk" if source == "disk_tensor" else "cpu"
+        torch.manual_seed(5)
+        res = ChunkedShortlistRunner(ChunkedShortlistConfig(storage=storage, **kw)).run(x)
+        assert res.metrics.storage_mode == storage
+    torch.manual_seed(5)
+    ref = ChunkedShortlistRunner(ChunkedShortlistConfig(storage="cpu", **kw)).run(x.to(dev))
+    assert ref.metrics.storage_mode == "device" and ref.metrics.h2d_time_ms is None
+    assert torch.equal(res.keep_indices, ref.keep_indices)
+    assert torch.equal(res.keep_scores, ref.keep_scores)
+    assert torch.equal(res.reduced_sequence.cpu(), ref.reduced_sequence.cpu())
+    assert [c.promoted for c in res.chunks] == [c.promoted for c in ref.chunks]
+    assert res.metrics.h2d_time_ms is not None and res.metrics.h2d_time_ms > 0.0
+    assert res.metrics.h2d_stall_ms is not None and res.metrics.h2d_stall_ms >= 0.0
