@@ -933,7 +933,9 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   constexpr int S = kMainStages;
   // tile order: the window tiles of a segment (its rows span less than w)
   // plus the prototype tiles
-  const int ordcap = (2 * local_w + kTile - 1) / kTile + 2 + pcap / kTile;
+  // (a segment's window tiles lie in [0, T): at most T/64 + 1 of them)
+  const int64_t wspan = (int64_t)2 * local_w < T ? (int64_t)2 * local_w : T;
+  const int ordcap = (int)((wspan + kTile - 1) / kTile) + 2 + pcap / kTile;
   const size_t dyn = (size_t)pcap * 12 + (size_t)ordcap * 4;
   if (lengths != nullptr)
     short_main_kernel<true, S><<<(unsigned)blocks, 256, dyn, s>>>(a, anchors ? 1 : 0, pcap);

@@ -437,6 +437,38 @@ def _shortlist_attn_structured(
     return lengths
 
 
+def _mfma_causal_ok(dtype: torch.dtype, D: int, *t4s: "_hip.Tensor4") -> bool:
+    """The structured MFMA kernel serves bf16, D = 64, 16-byte aligned rows."""
+    if dtype != torch.bfloat16 or D != 64:
+        return False
+    for t in t4s:
+        if int(t.ptr or 0) % 16 or t.s_b % 8 or t.s_h % 8 or t.s_t % 8 or t.s_t <= 0 or t.s_t >= 2 ** 31:
+            return False
+    return True
+
+
+def _causal_attn_mfma(q4, k4, v4, out4, H: int, T: int, D: int, token_idx: torch.Tensor, row_head: torch.Tensor,
+                      head_map: Optional[torch.Tensor], device: torch.device) -> None:
+    """Implicit-causal attention (row r attends to keys 0..token_idx[r] of its
+    head) on the structured MFMA kernel: a window that covers the whole
+    sequence, no anchors and no prototype keys.  Rows must be ordered by
+    (head, token), as the packing writes them; 64 consecutive rows of a head
+    form one flash-attention tile of queries that streams its key tiles
+    0..t_last once (reference: the causal SDPA of sparse_attn.py:1016-1043
+    and the dense paths of aspa.py:1365-1440, 1664-1701)."""
+
+    lib = _hip.lib()
+    N = int(token_idx.numel())
+    summary = torch.zeros(4, dtype=torch.int32, device=device)  # read only by the anchor pass (off here)
+    with _hip.TIMER.timed("causal_attn_mfma"):
+        rc = lib.pfa_shortlist_attn_fwd(
+            q4, k4, v4, out4, _hip.PFA_BF16, int(H), int(T), int(D), _hip.ptr(token_idx), _hip.ptr(row_head),
+            _hip.ptr(head_map), N, 1 if head_map is None else int(head_map.numel()), _hip.ptr(summary), None,
+            int(T), 0, 0, None, 0, None, float(1.0 / math.sqrt(D)), None, None, None, None, None, None, None, 2,
+            _hip.stream_ptr(device))
+    _hip.check(rc, "pfa_shortlist_attn_fwd (causal)")
+
+
 _QUANT_MODES = {"max": 0, "percentile": 1, "ema_percentile": 2}
 
 
@@ -589,6 +621,14 @@ def aspa_sparse_attention(
     out = torch.zeros(q.shape, device=device, dtype=out_dtype)
     H = batch_heads
     scale = 1.0 / math.sqrt(head_dim)
+    t4 = (_hip.tensor4(qc, H), _hip.tensor4(kc, H), _hip.tensor4(vc, H), _hip.tensor4(out, H))
+    if (cand is None and causal_mask is None and not is_quantized and out_dtype == q.dtype
+            and _mfma_causal_ok(q.dtype, head_dim, *t4)):
+        # implicit causal branch on MFMA tiles (rows are packed by (head, token))
+        _causal_attn_mfma(*t4, H, tokens, head_dim, token_idx, row_head, None, device)
+        _record_backend("hip", device=str(device), heads=batch_heads, tokens=tokens, max_rows=int(max_rows),
+                        quantized=False, candidates=False, mfma=True)
+        return out
     _attn_launch(_hip.tensor4(qc, H), _hip.tensor4(kc, H), _hip.tensor4(vc, H), q.dtype, _hip.tensor4(out, H),
                  out_dtype, H, tokens, head_dim, token_idx, row_head, None, cand, lens, causal_mask, head_max, scale,
                  scales, device)

@@ -911,6 +911,12 @@ class AdaptiveSparseAttention(nn.Module):
         token_idx, row_head = self._full_rows(B, T, qkv.device)
         q5 = qkv.view(B, T, 3, H, D)
         out4 = out.view(B, T, H, D)
+        t4 = (_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
+              _hip.tensor4(q5[:, :, 2], H, "bthd"), _hip.tensor4(out4, H, "bthd"))
+        if out.dtype == qkv.dtype and _sa._mfma_causal_ok(qkv.dtype, D, *t4):
+            # flash-style causal tiles on MFMA (64 queries x 64 keys)
+            _sa._causal_attn_mfma(*t4, H, T, D, token_idx, row_head, None, qkv.device)
+            return
         _sa._attn_launch(_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
                          _hip.tensor4(q5[:, :, 2], H, "bthd"), qkv.dtype, _hip.tensor4(out4, H, "bthd"), out.dtype,
                          H, T, D, token_idx, row_head, None, None, None, None, None, 1.0 / math.sqrt(D),

@@ -102,6 +102,49 @@ def module_case(ref, name: str, cfg: dict, B: int, T: int, C: int, dtype: torch.
     _save(name, **arrays)
 
 
+def dropin_case(ref, name: str, T: int, pad_from: int, **kw) -> None:
+    """CausalASPAMultiheadAttention (reference modules/aspa_multihead.py) in
+    eval mode on a seeded input with a key padding mask: its state dict, its
+    output and the head statistics of its attention layer (the default
+    router_top_p = 0.9 takes every forward through the nucleus head count,
+    aspa.py:749-780, 1574-1589)."""
+    MHA = ref.modules.CausalASPAMultiheadAttention
+    torch.manual_seed(4321)
+    mha = MHA(embed_dim=64, num_heads=4, batch_first=True, **kw).eval()
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, T, 64, generator=g)
+    pad = torch.zeros(2, T, dtype=torch.bool)
+    pad[1, pad_from:] = True
+    # the state before the forward (the forward moves the prototype EMA)
+    arrays = {f"sd::{k}": v.detach().clone() for k, v in mha.state_dict().items()}
+    with torch.no_grad():
+        out, w = mha(x, key_padding_mask=pad, need_weights=True)
+    hs = mha.attention.last_head_stats or {}
+    arrays.update(x=x, pad=pad.to(torch.uint8), out=out, weights_shape=np.array(w.shape),
+                  top_k=np.int64(hs.get("top_k", -1)), nucleus_k=np.int64(hs.get("nucleus_k", -1)),
+                  mode=np.array(str(hs.get("mode"))), kw=np.array(repr(sorted(kw.items()))))
+    _save(name, **arrays)
+
+
+def nucleus_case(ref) -> None:
+    """_nucleus_head_count (aspa.py:749-780) on seeded head probabilities:
+    softmax rows with a temperature sweep (mass spread from one head to all),
+    a target_p sweep and a cap sweep."""
+    ASPA = ref.models.aspa.AdaptiveSparseAttention
+    m = ASPA(ref.models.aspa.ModelConfig(d_model=64, n_head=8, attn_h_total=8, attn_gates=8))
+    g = torch.Generator().manual_seed(13)
+    probs, ks = [], []
+    for temp in (0.05, 0.3, 1.0, 4.0):
+        # a per-head bias so the mean mass is uneven across heads
+        bias = torch.linspace(3.0, -3.0, 8)[torch.randperm(8, generator=g)]
+        p = torch.softmax((torch.randn(2, 50, 8, generator=g) + bias) / temp, dim=-1)
+        probs.append(p)
+        row = [m._nucleus_head_count(p, tp, cap) for tp in (0.0, 0.5, 0.9, 0.99, 1.0) for cap in (1, 3, 8)]
+        ks.append(row)
+    _save("nucleus_head_count", probs=torch.stack(probs), k=torch.tensor(ks), target_p=np.array([0.0, 0.5, 0.9, 0.99, 1.0]),
+          caps=np.array([1, 3, 8]))
+
+
 def builder_cases(ref) -> None:
     sa = ref.kernels.sparse_attn
     g = torch.Generator().manual_seed(11)
@@ -183,6 +226,7 @@ def main() -> None:
     import proteus_attention.kernels.sparse_attn  # noqa: F401
     import proteus_attention.models.aspa  # noqa: F401
     import proteus_attention.tools.chunked_shortlist  # noqa: F401
+    import proteus_attention.modules  # noqa: F401
     import proteus_attention as ref
 
     torch.set_num_threads(8)
@@ -235,6 +279,11 @@ def module_cases():
             ref, "module_int8_pct_bf16", dict(short, attn_quantize_int8=True, attn_quantize_int8_mode="percentile",
                                               attn_quantize_int8_percentile=0.995), 1, 2048, 512, torch.bfloat16,
             outlier=0.01, token_stride=8),
+        # the drop-in module with its defaults, and in linear (shortlist) mode
+        "nucleus_head_count": nucleus_case,
+        "dropin_mha_auto": lambda ref: dropin_case(ref, "dropin_mha_auto", 96, 70),
+        "dropin_mha_linear": lambda ref: dropin_case(ref, "dropin_mha_linear", 300, 250, attn_mode="linear",
+                                                     attn_linear_L=64, attn_linear_window=32),
         "module_int8_ema_f32": lambda ref: module_case(
             ref, "module_int8_ema_f32", dict(short, attn_quantize_int8=True, attn_quantize_int8_mode="ema_percentile",
                                              attn_quantize_int8_percentile=0.99, attn_quantize_int8_ema_decay=0.8),

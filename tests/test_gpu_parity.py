@@ -970,3 +970,134 @@ def test_router_without_prototypes_vs_oracle(dev, dt):
         assert int((bad & ~torch.from_numpy(_at_boundary(x, w))).sum()) == 0
     _, oidx = O.topk_lowest(gate.cpu(), 2)
     assert torch.equal(hidx.cpu().long(), oidx)
+
+
+# ---------------------------------------------------------------------------
+# drop-in nn.MultiheadAttention replacement (reference tests/test_dropin_attention.py)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name,T,kw", [("dropin_mha_auto", 96, {}),
+                                       ("dropin_mha_linear", 300, dict(attn_mode="linear", attn_linear_L=64,
+                                                                       attn_linear_window=32))])
+def test_dropin_mha_matches_reference(dev, golden, name, T, kw):
+    """CausalASPAMultiheadAttention with the reference's state dict on the
+    reference's input and key padding mask: the output values, the zero
+    attention weights of the reference's shape, zero rows where padded, and
+    the head count its nucleus rule (router_top_p 0.9) chose."""
+    from proteus_attention import CausalASPAMultiheadAttention
+
+    z = golden(name)
+    torch.manual_seed(0)
+    mha = CausalASPAMultiheadAttention(embed_dim=64, num_heads=4, batch_first=True, **kw)
+    sd = {k[4:]: torch.from_numpy(v) for k, v in z.items() if k.startswith("sd::")}
+    missing, unexpected = mha.load_state_dict(sd, strict=False)
+    assert not unexpected, unexpected
+    assert all(k.startswith("attention._") or "rope" in k for k in missing), missing
+    mha = mha.to(dev).eval()
+    x = torch.from_numpy(z["x"]).to(dev)
+    pad = torch.from_numpy(z["pad"]).bool().to(dev)
+    with torch.no_grad():
+        out, w = mha(x, key_padding_mask=pad, need_weights=True)
+    hs = mha.attention.last_head_stats
+    assert hs["top_k"] == int(z["top_k"]) and hs["nucleus_k"] == int(z["nucleus_k"])
+    assert hs["mode"] == str(z["mode"])
+    assert tuple(w.shape) == tuple(z["weights_shape"]) and torch.count_nonzero(w) == 0
+    err = float((out.cpu() - torch.from_numpy(z["out"])).abs().max())
+    _say(f"{name}: mode {hs['mode']} top_k {hs['top_k']} max-abs err {err:.3e}")
+    assert err <= TOL_F32
+    assert torch.count_nonzero(out[pad]) == 0
+
+
+def test_dropin_mha_fallbacks_match_torch(dev):
+    """Cross attention and a custom (non-causal) mask go to the wrapped
+    nn.MultiheadAttention, equal to a torch module with the same weights
+    (reference tests/test_dropin_attention.py:55-113); the standard causal
+    mask stays on the ASPA path; an entirely padded batch row gives zeros."""
+    import torch.nn as nn
+
+    from proteus_attention import CausalASPAMultiheadAttention
+
+    torch.manual_seed(1)
+    mha = CausalASPAMultiheadAttention(embed_dim=16, num_heads=4, batch_first=True, dropout=0.0,
+                                       return_stats_default=True).to(dev)
+    ref = nn.MultiheadAttention(embed_dim=16, num_heads=4, batch_first=True, dropout=0.0).to(dev)
+    ref.load_state_dict(mha.fallback_attention.state_dict())
+    q, k = torch.randn(2, 5, 16, device=dev), torch.randn(2, 7, 16, device=dev)
+    out, w = mha(q, key=k, value=k, need_weights=True)
+    eo, ew = ref(q, k, k, need_weights=True)
+    assert torch.allclose(out, eo, atol=1e-6) and torch.allclose(w, ew, atol=1e-6)
+    assert mha.last_runtime_stats["shortlist_backend"]["name"] == "torch.nn.MultiheadAttention"
+    x = torch.randn(3, 6, 16, device=dev)
+    custom = torch.full((6, 6), float("-inf"), device=dev).triu_(1)
+    custom[0, 3] = 0.0
+    out, w = mha(x, attn_mask=custom, need_weights=True, average_attn_weights=False, is_causal=False)
+    eo, ew = ref(x, x, x, attn_mask=custom, need_weights=True, average_attn_weights=False, is_causal=False)
+    assert torch.allclose(out, eo, atol=1e-6) and torch.allclose(w, ew, atol=1e-6)
+    causal = torch.triu(torch.ones(6, 6, dtype=torch.bool, device=dev), diagonal=1)
+    out, _ = mha(x, attn_mask=causal, need_weights=False)
+    assert mha.last_runtime_stats["shortlist_backend"]["name"] != "torch.nn.MultiheadAttention"
+    pad = torch.zeros(3, 6, dtype=torch.bool, device=dev)
+    pad[2] = True
+    out, _ = mha(x, key_padding_mask=pad, need_weights=False)
+    assert torch.count_nonzero(out[2]) == 0 and torch.isfinite(out).all()
+    # batch_first=False: (T, B, C) in and out, weights (B, T, T)
+    mha_t = CausalASPAMultiheadAttention(embed_dim=16, num_heads=4, batch_first=False).to(dev)
+    out, w = mha_t(x.transpose(0, 1), need_weights=True)
+    assert out.shape == (6, 3, 16) and w.shape == (3, 6, 6)
+
+
+# ---------------------------------------------------------------------------
+# dense causal attention on MFMA tiles (force-dense / dense fast path /
+# the operator's implicit-causal branch)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("BH,T,p", [(8, 8192, 1.0), (6, 3001, 0.35), (3, 65, 1.0)])
+def test_operator_causal_branch_mfma_vs_oracle(dev, BH, T, p):
+    """aspa_sparse_attention without candidates or mask (each active row
+    attends to keys 0..t, sparse_attn.py:1016-1043) in bf16, D = 64, runs
+    the MFMA causal tiles; every active row against f32 causal attention,
+    inactive rows zero."""
+    from proteus_attention.kernels.sparse_attn import aspa_sparse_attention, get_last_backend_info
+
+    _say(f"operator causal mfma BH={BH} T={T} p={p}")
+    g = torch.Generator().manual_seed(T + BH)
+    q, k, v = (torch.randn(BH, T, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+    mask = torch.rand(BH, T, generator=g) < p
+    out = aspa_sparse_attention(q.to(dev), k.to(dev), v.to(dev), active_mask=mask.to(dev))
+    info = get_last_backend_info()
+    assert info["name"] == "hip" and info["details"].get("mfma") is True
+    ref = O.causal_attention_f32(q, k, v)
+    o = out.float().cpu()
+    err = float((o - ref)[mask].abs().max())
+    _say(f"max-abs err {err:.3e}")
+    assert err <= TOL_BF16
+    assert torch.count_nonzero(o[~mask]) == 0
+
+
+def test_module_force_dense_mfma_vs_oracle(dev):
+    """subquad mode (force-dense, aspa.py:1624-1677) at T = 8,192 in bf16:
+    the attention output equals causal attention of the module's own
+    projected and rotated q/k/v."""
+    from configs import COMMON
+
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    B, T, C, H = 1, 8192, 512, 8
+    _say(f"module force-dense T={T}")
+    torch.manual_seed(0)
+    m = AdaptiveSparseAttention(ModelConfig(**dict(COMMON, d_model=C, n_head=H, attn_h_total=H, attn_gates=H,
+                                                   attn_mode="subquad", attn_token_sparse=False)))
+    m = m.to(dev, torch.bfloat16).eval()
+    x = torch.randn(B, T, C, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        m(x)
+        qkv = m.qkv(x).view(B, T, 3, H, 64).cpu()
+    assert m._last_sparse_state["mode"].startswith("dense")
+    cos, sin = (t.cpu() for t in m._rope_factors(T, dev, torch.bfloat16))
+    q = O.apply_rope(qkv[:, :, 0], cos, sin)
+    k = O.apply_rope(qkv[:, :, 1], cos, sin)
+    qh, kh, vh = (a.permute(0, 2, 1, 3).reshape(B * H, T, 64) for a in (q, k, qkv[:, :, 2]))
+    ref = O.causal_attention_f32(qh, kh, vh).view(B, H, T, 64).permute(0, 2, 1, 3).reshape(B, T, C)
+    err = float((m.last_head_consensus.float().cpu() - ref).abs().max())
+    _say(f"max-abs err {err:.3e}")
+    assert err <= TOL_BF16

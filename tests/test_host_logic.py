@@ -149,3 +149,15 @@ def test_chunked_config_validation():
     with pytest.raises(ValueError):
         ChunkedShortlistConfig(seq_len=8, d_model=8, chunk_len=70000, buffer_tokens=2, per_chunk_budget=1,
                                device=torch.device("cpu")).validate()
+
+
+def test_nucleus_head_count_matches_reference(golden):
+    """_nucleus_head_count (reference aspa.py:749-780) against the
+    reference's own answers on seeded head probabilities, over target_p in
+    {0, .5, .9, .99, 1} and caps {1, 3, 8}."""
+    z = golden("nucleus_head_count")
+    m = AdaptiveSparseAttention(ModelConfig(d_model=64, n_head=8, attn_h_total=8, attn_gates=8))
+    probs = torch.from_numpy(z["probs"])
+    got = [[m._nucleus_head_count(p, float(tp), int(cap)) for tp in z["target_p"] for cap in z["caps"]]
+           for p in probs]
+    assert got == z["k"].tolist()
