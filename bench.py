@@ -89,6 +89,17 @@ def shortlist_caps(m, c):
     return L, local_w, int(rt["anchor_stride"]), slots, min(L, pcap, c["T"])
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(x, weights, dtype, c, caps) -> dict:
     import torch
 
@@ -108,8 +119,11 @@ def cpu_baseline(x, weights, dtype, c, caps) -> dict:
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"config-3 forward, oracle CPU pipeline (torch CPU {str(dtype).replace('torch.', '')} with "
-                   f"{cores} threads; single-threaded C builder); router/pack/QKV/proj on all {tokens} tokens, "
+        "cpu_model": cpu_model(),
+        "sample": (f"config-3 forward on {cpu_model()}, oracle CPU pipeline (torch CPU "
+                   f"{str(dtype).replace('torch.', '')} with {cores} threads; the candidate builder is the "
+                   f"single-threaded C oracle, an O(N log K) prefix walk in place of the reference's O(N*T) torch "
+                   f"builder); router/pack/QKV/proj on all {tokens} tokens, "
                    f"builder+attention on all packed rows ({t['sample_fraction']:.4f} of rows); "
                    f"{wall:.1f}s wall; stage s: " +
                    ", ".join(f"{k}={v:.2f}" for k, v in t.items() if k not in ("total", "sample_fraction"))),
@@ -154,7 +168,10 @@ def bench_forward(args, workload: str) -> dict:
     # the forward replays as one HIP graph (the module's own graph mode);
     # --eager times the launch-by-launch forward instead.  Objects that exist
     # before the loop are frozen out of the cyclic GC, as serving loops do.
-    m.enable_hip_graph(not args.eager)
+    # --static-output also captures the output projection (the returned
+    # tensor is then the graph's output buffer, consumed before the next
+    # step); by default it runs after each replay and returns a fresh tensor
+    m.enable_hip_graph(not args.eager, static_output=args.static_output)
     gc.collect()
     gc.freeze()
     with torch.no_grad():
@@ -241,14 +258,21 @@ def bench_forward(args, workload: str) -> dict:
         "shortlist_attn_fwd": ("mfma", 4.0 * sum_len * D, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", 1e12),
         "shortlist_build": ("hbm", N * (4.0 * L + 12) + tokens * 4.0, HBM_PEAK_GBS, "GB/s", 1e9),
         "router_topk": ("hbm", tokens * (c["C"] * E + 8 * 2 + 12) + 8 * c["C"] * (E + 4), HBM_PEAK_GBS, "GB/s", 1e9),
-        "proto_prefix_topk": ("hbm", tokens * K * 4.0 + tokens * 4.0, HBM_PEAK_GBS, "GB/s", 1e9),
+        # the module path builds the compact tables: scores in, per-64-token
+        # block set rows and per-token evict entries out
+        "proto_prefix_blocks": ("hbm", tokens * 8.0 + ((c["T"] + 63) // 64) * c["B"] * K * 4.0, HBM_PEAK_GBS,
+                                "GB/s", 1e9),
     }
     traffic = recorded_traffic() if workload == "cfg3" else {}
     kernels = kernel_table(per_stage, alg, traffic)
     dominant = max((k for k in module_stages if k in alg), key=lambda k: per_stage[k])
     dk = kernels[dominant]
     roofline = {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
-                "unit": dk["unit"], "frac": dk["frac"], "traffic": dk["traffic"]}
+                "unit": dk["unit"], "frac": dk["frac"], "traffic": dk["traffic"],
+                # traffic: not measured in this run -- HBM bytes per forward
+                # from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded
+                # in the profiles file named here
+                "traffic_source": "profiles/cfg3_hbm_traffic.md" if dk["traffic"] is not None else None}
     cpu = None
     if workload == "cfg3" and not args.no_cpu_baseline:
         log("cpu baseline (oracle pipeline on host cores)")
@@ -373,6 +397,8 @@ def main() -> int:
     ap.add_argument("--cfg5-source", choices=("device", "pinned", "disk"), default="device",
                     help="where config 5's sequence lives (--workload cfg5)")
     ap.add_argument("--eager", action="store_true", help="time the forward without HIP graph replay")
+    ap.add_argument("--static-output", action="store_true",
+                    help="graph mode: capture the output projection too (returns the graph's output buffer)")
     ap.add_argument("--default-gemms", action="store_true",
                     help="use torch's default GEMM heuristic instead of the shipped MI355X table")
     ap.add_argument("--copy-probe-mib", type=int, default=0,

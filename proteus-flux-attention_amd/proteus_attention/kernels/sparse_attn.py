@@ -117,6 +117,17 @@ def _pack_active_rows(
 # shortlist candidates
 # ---------------------------------------------------------------------------
 
+# Largest prototype set the prefix kernels keep (their sorted lists live in
+# LDS); the reference accepts any proto_cap (sparse_attn.py:260-300).
+MAX_PROTO_CANDIDATES = 2048
+
+
+def _check_proto_k(K: int) -> None:
+    if K > MAX_PROTO_CANDIDATES:
+        raise ValueError(f"prototype candidates per row: min(max_candidates, proto_cap, seq_len) = {K} exceeds "
+                         f"the {MAX_PROTO_CANDIDATES} this build supports")
+
+
 def _proto_prefix_sets(scores: torch.Tensor, K: int, with_evict: bool = False):
     """Per (batch, token) the top-min(t+1, K) score positions <= t, sorted.
 
@@ -124,6 +135,7 @@ def _proto_prefix_sets(scores: torch.Tensor, K: int, with_evict: bool = False):
     ``with_evict`` also the (B, T_s) int32 eviction tokens.
     """
 
+    _check_proto_k(K)
     lib = _hip.lib()
     device = scores.device
     scores = scores.to(torch.float32).contiguous()
@@ -144,6 +156,7 @@ def _proto_prefix_blocks(scores: torch.Tensor, K: int):
     token the eviction token evict[p] (p is in the set of t exactly when
     p <= t < evict[p]).  Returns ((B, ceil(T/64), K), (B, T)) int32."""
 
+    _check_proto_k(K)
     lib = _hip.lib()
     device = scores.device
     scores = scores.to(torch.float32).contiguous()
@@ -151,7 +164,7 @@ def _proto_prefix_blocks(scores: torch.Tensor, K: int):
     ws = _workspace(_size_out(lib.pfa_proto_prefix_workspace_size, B, Ts, K), device)
     blocks = torch.empty(B, (Ts + 63) // 64, K, dtype=torch.int32, device=device)
     evict = torch.empty(B, Ts, dtype=torch.int32, device=device)
-    with _hip.TIMER.timed("proto_prefix_topk"):
+    with _hip.TIMER.timed("proto_prefix_blocks"):
         rc = lib.pfa_proto_prefix_blocks(_hip.ptr(scores), B, Ts, scores.stride(0), K, _hip.ptr(blocks),
                                          _hip.ptr(evict), _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device))
     _hip.check(rc, "pfa_proto_prefix_blocks")
@@ -582,10 +595,17 @@ def aspa_sparse_attention(
 
     if prepacked is not None:
         head_idx_p, token_idx_p, row_offsets, max_rows = prepacked
+        if head_idx_p.numel() != token_idx_p.numel():
+            raise ValueError("prepacked head_idx and token_idx must have the same length")
         token_idx = token_idx_p.to(device=device, dtype=torch.int32).contiguous()
         row_head = head_idx_p.to(device=device, dtype=torch.int32).contiguous()
         row_offsets = row_offsets.to(device=device, dtype=torch.int32).contiguous()
         n_rows = int(token_idx.numel())
+        if n_rows > 0:
+            # the kernels index q/k/v/out with these: out-of-range rows are
+            # rejected here (the reference's index_copy_ raises IndexError)
+            _check_rows(token_idx, tokens, "aspa_sparse_attention: prepacked token_idx")
+            _check_rows(row_head, batch_heads, "aspa_sparse_attention: prepacked head_idx")
     else:
         token_idx, row_head, row_offsets, n_rows, max_rows = _pack_mask_i32(mask_bool)
     if n_rows == 0:

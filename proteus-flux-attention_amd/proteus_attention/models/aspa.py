@@ -401,6 +401,7 @@ class AdaptiveSparseAttention(nn.Module):
         self.last_head_stats: Optional[dict] = None
         self._last_sparse_state: Optional[dict] = None
         self._hip_graph_enabled = _flag(g("attn_hip_graph", False))
+        self._hip_graph_static_output = False
         self._hip_graphs: Dict[Any, dict] = {}
         self._hip_graph_pool = None
         self._cached_active_mask: Optional[torch.Tensor] = None
@@ -986,7 +987,7 @@ class AdaptiveSparseAttention(nn.Module):
 
     # ------------------------------------------------------------------
     # HIP graph replay of the forward
-    def enable_hip_graph(self, enabled: bool = True) -> None:
+    def enable_hip_graph(self, enabled: bool = True, static_output: bool = False) -> None:
         """Replay the forward from a captured HIP graph.
 
         The first call for an input shape/dtype (and the schedule state that
@@ -1000,8 +1001,17 @@ class AdaptiveSparseAttention(nn.Module):
         density threshold, nucleus head count, memory or latency budget);
         otherwise the eager forward runs.  Tensors the module keeps from the
         last forward (last_head_consensus, _last_gate_probs, ...) are the
-        graph's static buffers and change with the next replay."""
+        graph's static buffers and change with the next replay.
+
+        static_output=True captures the output projection too: forward()
+        then returns the graph's own output buffer, with no launch after the
+        replay, and that tensor is overwritten by the next forward of the
+        same shape (the usual contract of a captured graph's outputs; clone
+        it to keep it)."""
+        if bool(static_output) != self._hip_graph_static_output:
+            self.reset_hip_graphs()
         self._hip_graph_enabled = bool(enabled)
+        self._hip_graph_static_output = bool(static_output) and bool(enabled)
         if not enabled:
             self.reset_hip_graphs()
 
@@ -1071,11 +1081,12 @@ class AdaptiveSparseAttention(nn.Module):
             self._capture_keep = []
             with torch.cuda.graph(graph, pool=self._hip_graph_pool):
                 attn, stats_args, label = self._forward_impl(xs, capture=True)
+                y_static = self.dropout(self.proj(attn)) if self._hip_graph_static_output else None
             keep = self._capture_keep
         finally:
             _hip.TIMER.enabled = timer_on
             self._capture_keep = None
-        ent = {"graph": graph, "x": xs, "attn": attn, "stats_args": stats_args, "label": label,
+        ent = {"graph": graph, "x": xs, "attn": attn, "y": y_static, "stats_args": stats_args, "label": label,
                "state": {k: self.__dict__.get(k) for k in self._GRAPH_STATE},
                "sparse_state": self.__dict__.get("_lazy__last_sparse_state"), "keep": keep}
         self._hip_graphs[key] = ent
@@ -1095,7 +1106,7 @@ class AdaptiveSparseAttention(nn.Module):
         if x.data_ptr() != xs.data_ptr():
             xs.copy_(x)
         ent["graph"].replay()
-        y = self.dropout(self.proj(ent["attn"]))
+        y = ent["y"] if ent["y"] is not None else self.dropout(self.proj(ent["attn"]))
         for k, v in ent["state"].items():
             self.__dict__[k] = v
         st = ent["sparse_state"]

@@ -864,6 +864,38 @@ def test_module_hip_graph_replay_matches_eager(dev):
     assert not m._hip_graphs
 
 
+def test_module_hip_graph_static_output_matches_eager(dev):
+    """Graph mode with the output projection captured (static_output): every
+    replay's returned buffer equals the eager forward's output on the same
+    inputs and state, with eager device work between the replays."""
+    from configs import shortlist_cfg
+
+    _say("hip graph static output vs eager")
+    cfg = shortlist_cfg(4096, 512, 8, 1024, 256, 64)
+    m, x = _module(cfg, 1, 4096, 512, torch.bfloat16, dev, 0.01)
+    init = {n: b.detach().clone() for n, b in m.named_buffers()}
+    xs = [x, (x * 0.5).contiguous(), torch.roll(x, 3, dims=1).contiguous(), x]
+
+    def run(graph: bool):
+        for n, b in m.named_buffers():
+            b.copy_(init[n])
+        m.enable_hip_graph(graph, static_output=graph)
+        outs = []
+        with torch.no_grad():
+            for xi in xs:
+                y = m(xi).float().cpu()
+                junk = torch.randn(1 << 20, device=dev).sum()
+                torch.cuda.synchronize()
+                outs.append((y, float(junk)))
+        return outs
+
+    eager = run(False)
+    graph = run(True)
+    for i, (e, g) in enumerate(zip(eager, graph)):
+        assert torch.equal(e[0], g[0]), f"forward {i}: output differs"
+    m.enable_hip_graph(False)
+
+
 def test_module_dense_paths_vs_oracle(dev):
     """subquad mode (force-dense) and the small-sequence dense fast path
     equal dense causal attention of the projected q/k/v."""
@@ -1101,3 +1133,34 @@ def test_module_force_dense_mfma_vs_oracle(dev):
     err = float((m.last_head_consensus.float().cpu() - ref).abs().max())
     _say(f"max-abs err {err:.3e}")
     assert err <= TOL_BF16
+
+
+def test_operator_rejects_out_of_range_prepacked_rows(dev):
+    """Caller-supplied prepacked rows outside [0, T) / [0, B*H) raise
+    ValueError before any kernel runs."""
+    from proteus_attention.kernels.sparse_attn import aspa_sparse_attention
+
+    q = torch.randn(2, 16, 64, device=dev, dtype=torch.bfloat16)
+    offs = torch.tensor([0, 2, 3], dtype=torch.int32, device=dev)
+    for heads, toks in (([0, 0, 1], [3, 16, 2]), ([0, 0, 2], [3, 4, 2]), ([0, 0, -1], [3, 4, 2])):
+        pre = (torch.tensor(heads, device=dev), torch.tensor(toks, device=dev), offs, 2)
+        with pytest.raises(ValueError, match="prepacked"):
+            aspa_sparse_attention(q, q, q, prepacked=pre)
+
+
+def test_builder_rejects_prototype_sets_beyond_the_limit(dev):
+    """min(max_candidates, proto_cap, seq_len) above MAX_PROTO_CANDIDATES
+    (2048) is rejected with ValueError; 2048 itself is served."""
+    from proteus_attention.kernels.sparse_attn import MAX_PROTO_CANDIDATES, build_shortlist_candidates
+
+    T = 4096
+    rows = torch.arange(0, T, 97, device=dev)
+    sims = torch.rand(T, device=dev)
+    kw = dict(linear_window=16, anchor_stride=0, use_local=True, use_anchors=False, proto_scores=sims)
+    with pytest.raises(ValueError, match="exceeds"):
+        build_shortlist_candidates(rows, T, max_candidates=3000, proto_cap=MAX_PROTO_CANDIDATES + 1, **kw)
+    cand, lens = build_shortlist_candidates(rows, T, max_candidates=3000, proto_cap=MAX_PROTO_CANDIDATES, **kw)
+    oc, ol = O.build_shortlist(rows.cpu(), T, max_candidates=3000, proto_cap=MAX_PROTO_CANDIDATES,
+                               linear_window=16, anchor_stride=0, use_local=True, use_anchors=False,
+                               proto_scores=sims.cpu())
+    assert torch.equal(cand.cpu(), oc) and torch.equal(lens.cpu(), ol)
