@@ -345,6 +345,151 @@ pack_fill_kernel(const uint8_t* __restrict__ mask, int64_t T, int nblk, const in
   }
 }
 
+// Fill with the scan folded in, for BH * nblk <= kFusedScanMax: every
+// workgroup reads the whole (BH, nblk) count table (a few KB, from L2) and
+// derives its own base -- the totals of the heads before its head, the
+// compaction of empty heads, the counts of its head's earlier blocks -- so
+// no single-workgroup scan launch sits between the count and the fill.
+// Workgroup (0, 0) also writes the per-head outputs (active heads, row
+// offsets, summary) as pack_scan_kernel does.
+constexpr int kFusedScanMax = 4096;
+
+// Workgroup sums of a and b (every thread gets both).
+__device__ __forceinline__ void block_sum2(int& a, int& b, int* red) {
+  for (int off = 32; off > 0; off >>= 1) {
+    a += __shfl_xor(a, off, 64);
+    b += __shfl_xor(b, off, 64);
+  }
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) {
+    red[2 * wid] = a;
+    red[2 * wid + 1] = b;
+  }
+  __syncthreads();
+  a = 0;
+  b = 0;
+  for (int w = 0; w < nw; ++w) {
+    a += red[2 * w];
+    b += red[2 * w + 1];
+  }
+}
+
+__global__ void __launch_bounds__(kPackThreads)
+pack_fill_scan_kernel(const uint8_t* __restrict__ mask, int BH, int64_t T, int nblk,
+                      const int32_t* __restrict__ blockcounts, int compact, int32_t* __restrict__ active_heads,
+                      int32_t* __restrict__ row_offsets, int32_t* __restrict__ summary,
+                      int32_t* __restrict__ token_idx, int32_t* __restrict__ row_head, int32_t* __restrict__ row_of) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
+  extern __shared__ int s_tot[];  // per-head totals (BH)
+  __shared__ int red[2 * (kPackThreads / 64)];
+  __shared__ int wave_tot[kPackThreads / 64];
+  const int blk = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  for (int h = tid; h < BH; h += kPackThreads) s_tot[h] = 0;
+  __syncthreads();
+  // totals per head (LDS atomics: integer sums, any order) and this head's
+  // counts of the blocks before this one
+  int before_blk = 0;
+  const int n = BH * nblk;
+  for (int i = tid; i < n; i += kPackThreads) {
+    const int c = blockcounts[i];
+    const int h = i / nblk;
+    if (c != 0) atomicAdd(&s_tot[h], c);
+    if (h == bh && i - h * nblk < blk) before_blk += c;
+  }
+  __syncthreads();
+  // rows of the heads before this one, and how many of them are active
+  int rows_before = 0, heads_before = 0;
+  for (int h = tid; h < bh; h += kPackThreads) {
+    const int t = s_tot[h];
+    rows_before += t;
+    heads_before += (!compact || t > 0) ? 1 : 0;
+  }
+  block_sum2(rows_before, heads_before, red);
+  int unused = 0;
+  block_sum2(before_blk, unused, red);
+  if (blk == 0 && bh == 0) {
+    // per-head outputs: a scan over the BH totals, kPackThreads heads a step
+    int carry_p = 0, carry_n = 0, mx = 0;
+    for (int base = 0; base < BH; base += kPackThreads) {
+      const int h = base + tid;
+      const int tot = h < BH ? s_tot[h] : 0;
+      const int act = (h < BH) && (!compact || tot > 0);
+      int va = act, vn = act ? tot : 0;
+      for (int off = 1; off < 64; off <<= 1) {
+        const int na = __shfl_up(va, off, 64), nn = __shfl_up(vn, off, 64);
+        if (lane >= off) {
+          va += na;
+          vn += nn;
+        }
+      }
+      __syncthreads();
+      if (lane == 63) {
+        red[2 * wid] = va;
+        red[2 * wid + 1] = vn;
+      }
+      __syncthreads();
+      int ba = 0, bn = 0, ta = 0, tn = 0;
+      for (int w = 0; w < kPackThreads / 64; ++w) {
+        if (w < wid) {
+          ba += red[2 * w];
+          bn += red[2 * w + 1];
+        }
+        ta += red[2 * w];
+        tn += red[2 * w + 1];
+      }
+      if (act) {
+        const int id = carry_p + ba + va - 1;
+        if (active_heads) active_heads[id] = h;
+        row_offsets[id] = carry_n + bn + vn - tot;
+        mx = max(mx, tot);
+      }
+      carry_p += ta;
+      carry_n += tn;
+    }
+    for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off, 64));
+    __syncthreads();
+    if (lane == 0) red[wid] = mx;
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 0; w < kPackThreads / 64; ++w) mx = max(mx, red[w]);
+      row_offsets[carry_p] = carry_n;
+      summary[0] = carry_p;
+      summary[1] = carry_n;
+      summary[2] = mx;
+      summary[3] = 0;
+    }
+  }
+  if (compact && s_tot[bh] == 0) return;
+  const int id = heads_before;
+  int run = rows_before + before_blk;
+  for (int j = 0; j < kPackTile / kPackThreads; ++j) {
+    const int64_t t = (int64_t)blk * kPackTile + j * kPackThreads + tid;
+    const int act = (t < T && mask[(int64_t)bh * T + t]) ? 1 : 0;
+    int v = act;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int nn = __shfl_up(v, off, 64);
+      if (lane >= off) v += nn;
+    }
+    if (lane == 63) wave_tot[wid] = v;
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < kPackThreads / 64; ++w) {
+      if (w < wid) before += wave_tot[w];
+      total += wave_tot[w];
+    }
+    if (act) {
+      const int pos = run + before + v - 1;
+      token_idx[pos] = (int32_t)t;
+      row_head[pos] = id;
+      if (row_of != nullptr) row_of[(int64_t)bh * T + t] = pos;
+    }
+    run += total;
+    __syncthreads();
+  }
+}
+
 __global__ void head_max_token_kernel(const int32_t* __restrict__ token_idx, const int32_t* __restrict__ row_offsets,
                                       int P, int32_t* __restrict__ out) {
   __shared__ int red;
@@ -423,6 +568,13 @@ static int pack_rows_launch(const int32_t* head_idx, int topk, const uint8_t* to
     pack_count_routed<<<grid, kPackThreads, 0, s>>>(head_idx, topk, token_mask, H, T, nblk, mask_out, w.blockcounts,
                                                     row_of_out);
   PFA_CHECK_LAUNCH("pfa_pack_rows/count");
+  if (BH * nblk <= kFusedScanMax) {
+    pack_fill_scan_kernel<<<grid, kPackThreads, (size_t)BH * sizeof(int), s>>>(
+        mask_out, (int)BH, T, nblk, w.blockcounts, 1, active_heads_out, row_offsets_out, summary_out, token_idx_out,
+        row_head_out, row_of_out);
+    PFA_CHECK_LAUNCH("pfa_pack_rows/fill");
+    return PFA_OK;
+  }
   pack_scan_kernel<<<1, kScanThreads, 0, s>>>(w.blockcounts, (int)BH, nblk, 1, w.totals, w.compact_id, active_heads_out,
                                       row_offsets_out, summary_out);
   PFA_CHECK_LAUNCH("pfa_pack_rows/scan");
