@@ -4,8 +4,10 @@
 // original position key_pos[j] <= t.  K and V of the shortlist are int8 with
 // one symmetric scale per (head, key row); they are dequantised inside the
 // tile: each staged 64-key tile is converted k8 * k_scale -> bf16 (and
-// likewise V) in LDS, then S = Q K^T and O += P V run on
-// v_mfma_f32_16x16x32_bf16 with an online softmax in f32 registers.
+// likewise V) into the swizzled 128-byte-row layout of the bf16 attention
+// kernels (each thread writes two 16-byte chunks of K and two of V; the V^T
+// operand comes from the LDS transpose read), then S = Q K^T and O += P V run
+// on v_mfma_f32_16x16x32_bf16 with an online softmax in f32 registers.
 //
 // Workgroup: 4 waves, 128 consecutive query tokens of one head (32 per wave
 // in two 16-query MFMA column groups).  The shortlist is sorted by
@@ -19,14 +21,10 @@
 namespace pfa {
 namespace fin {
 
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
-
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQ = 32 * kWaves;  // queries per workgroup
-constexpr int kTile = 64;        // keys per tile
-constexpr int kLd = 72;          // padded LDS row (bf16 elements)
+constexpr int kTile = kSwzKeys;  // keys per tile
 constexpr int kD = 64;
 constexpr float kRescaleLog2 = 0.0f;  // rescale only when some row's max rises
 
@@ -73,37 +71,40 @@ __device__ __forceinline__ Fetch fetch(const int8_t* kb, const int8_t* vb, const
 
 __device__ __forceinline__ float i8f(uint32_t w, int e) { return (float)(int)(int8_t)((w >> (8 * e)) & 0xffu); }
 
-__device__ __forceinline__ void store(const Fetch& f, uint16_t* Ks, uint16_t* Vt, int32_t* kp) {
+// the thread's 16 K and 16 V elements (key tid/4, dims 16*(tid%4) ..+15) are
+// chunks 2*(tid%4) and 2*(tid%4)+1 of the key's row
+__device__ __forceinline__ void store(const Fetch& f, uint16_t* tile_base, int32_t* kp) {
   const int j = threadIdx.x >> 2, qd = threadIdx.x & 3;
+  const int sw = tile_swz(j);
   const uint32_t kw4[4] = {f.k.x, f.k.y, f.k.z, f.k.w};
   const uint32_t vw4[4] = {f.v.x, f.v.y, f.v.z, f.v.w};
-  __bf16 kd[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) kd[e] = (__bf16)(i8f(kw4[e >> 2], e & 3) * f.kscale);
-  uint4 kw[2];
-  __builtin_memcpy(kw, kd, 32);
-  *reinterpret_cast<uint4*>(Ks + j * kLd + 16 * qd) = kw[0];
-  *reinterpret_cast<uint4*>(Ks + j * kLd + 16 * qd + 8) = kw[1];
+  __bf16 kd[16], vd[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    const __bf16 v = (__bf16)(i8f(vw4[e >> 2], e & 3) * f.vscale);
-    uint16_t bits;
-    __builtin_memcpy(&bits, &v, 2);
-    Vt[(16 * qd + e) * kLd + j] = bits;
+    kd[e] = (__bf16)(i8f(kw4[e >> 2], e & 3) * f.kscale);
+    vd[e] = (__bf16)(i8f(vw4[e >> 2], e & 3) * f.vscale);
+  }
+  uint4 kw[2], vw[2];
+  __builtin_memcpy(kw, kd, 32);
+  __builtin_memcpy(vw, vd, 32);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int slot = 8 * j + ((2 * qd + h) ^ sw);
+    *reinterpret_cast<uint4*>(tile_base + 8 * slot) = kw[h];
+    *reinterpret_cast<uint4*>(tile_base + kSwzTileElems + 8 * slot) = vw[h];
   }
   if (qd == 0) kp[j] = f.pos;
 }
 
 template <bool MASKED>
-__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const uint16_t* Ks, const uint16_t* Vt,
-                                     const int32_t* kp, int key0, int S, int causal, const int (&tq)[2],
-                                     float sl2, St (&st)[2]) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
+__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& tl, const int32_t* kp, int key0,
+                                     int S, int causal, const int (&tq)[2], float sl2, St (&st)[2]) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
   float s[2][16];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(Ks + (16 * kb + r16) * kLd + 8 * g);
-    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(Ks + (16 * kb + r16) * kLd + 32 + 8 * g);
+    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 0));
+    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 1));
 #pragma unroll
     for (int gr = 0; gr < 2; ++gr) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
@@ -164,12 +165,13 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const uint16_t*
     }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const uint16_t* vr = Vt + (16 * db + r16) * kLd + 32 * kc + 4 * g;
-      const uint2 lo8 = *reinterpret_cast<const uint2*>(vr);
-      const uint2 hi8 = *reinterpret_cast<const uint2*>(vr + 16);
-      const uint32_t w4[4] = {lo8.x, lo8.y, hi8.x, hi8.y};
+      // V^T: lane (dim 16db + lane%16, g) holds keys 32kc + 4g + (0..3) and
+      // 32kc + 16 + 4g + (0..3), matching pb
+      const i16x4_t lo = ds_tr4(tl.vtr(kc, 0, db));
+      const i16x4_t hi = ds_tr4(tl.vtr(kc, 1, db));
       bf16x8_t va;
-      __builtin_memcpy(&va, w4, 16);
+      __builtin_memcpy(&va, &lo, 8);
+      __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
 #pragma unroll
       for (int gr = 0; gr < 2; ++gr)
         st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gr], st[gr].acc[db], 0, 0, 0);
@@ -205,8 +207,7 @@ __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restri
 
 // at most 168 VGPRs: three 4-wave workgroups per CU
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) final_attn_kernel(Args a) {
-  __shared__ __align__(16) uint16_t Ks[2][kTile * kLd];
-  __shared__ __align__(16) uint16_t Vt[2][kD * kLd];
+  __shared__ __align__(16) uint16_t ring[2][2 * kSwzTileElems];
   __shared__ int32_t kp[2][kTile];
 
   const int bid = blockIdx.x;
@@ -214,6 +215,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
   const int qt = a.nqt - 1 - bid / a.H;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
+  SwzLane L;
+  L.init();
   const int2 rg = a.rng[qt];
   const int64_t t_base = (int64_t)qt * kQ;
   int tq[2];
@@ -247,7 +250,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
   const float* vsb = a.vs + (int64_t)h * a.S;
   const int ntile = (rg.y + kTile - 1) / kTile;
   const int jrow = tid >> 2;
-  if (ntile > 0) store(fetch(kb, vb, ksb, vsb, a.kpos, min(jrow, a.S - 1)), Ks[0], Vt[0], kp[0]);
+  if (ntile > 0) store(fetch(kb, vb, ksb, vsb, a.kpos, min(jrow, a.S - 1)), ring[0], kp[0]);
   __syncthreads();
   for (int i = 0; i < ntile; ++i) {
     const int cur = i & 1;
@@ -255,9 +258,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
     Fetch nxt;
     if (more) nxt = fetch(kb, vb, ksb, vsb, a.kpos, min(kTile * (i + 1) + jrow, a.S - 1));
     const int key0 = kTile * i;
-    if (key0 + kTile <= rg.x) tile<false>(qf, Ks[cur], Vt[cur], kp[cur], key0, a.S, a.causal, tq, a.scale_log2, st);
-    else tile<true>(qf, Ks[cur], Vt[cur], kp[cur], key0, a.S, a.causal, tq, a.scale_log2, st);
-    if (more) store(nxt, Ks[cur ^ 1], Vt[cur ^ 1], kp[cur ^ 1]);
+    const SwzTile tl{ring[cur], L};
+    if (key0 + kTile <= rg.x) tile<false>(qf, tl, kp[cur], key0, a.S, a.causal, tq, a.scale_log2, st);
+    else tile<true>(qf, tl, kp[cur], key0, a.S, a.causal, tq, a.scale_log2, st);
+    if (more) store(nxt, ring[cur ^ 1], kp[cur ^ 1]);
     __syncthreads();
   }
   uint16_t* oh = a.out + (int64_t)h * a.o_sh;

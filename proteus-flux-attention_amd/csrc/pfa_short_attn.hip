@@ -38,8 +38,6 @@
 
 namespace pfa {
 
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
 constexpr int kRows = 64;   // query rows per workgroup
 constexpr int kTile = 64;   // keys per tile
@@ -105,52 +103,7 @@ __device__ __forceinline__ bool zero_anchor(int64_t t, int s, int slots) {
 
 __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); }
 
-// Four bf16 of one head dim from four consecutive key rows of a V tile, by
-// the gfx950 LDS transpose read: within each 16-lane row of the wave, lane
-// 4a+b receives element b of the 8-byte chunks addressed by lanes a, a+4,
-// a+8, a+12.  Lane m of the row addresses key row0 + m/4, dims
-// d0 + 4*(m%4) .. +3, so lane i = 4a+b gets V[row0 + k][d0 + i], k = 0..3.
-typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4_t;
-__device__ __forceinline__ i16x4_t ds_tr4(const uint16_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p));
-}
-
-// A 64-key tile (K and V, 64 x 64 bf16 each) in LDS gives the MFMA
-// fragments through two calls: kfrag(kb, dc) is the lane's 8 K elements
-// (key 16kb + lane%16, dims 32dc + 8*(lane/16) ..+7) and vtr(kc, h, db) the
-// address the lane passes to the transpose read for keys
-// 32kc + 16h + 4*(lane/16) .. +3, dims 16db ..+15.
-//
-// SwzTile: unpadded 128-byte rows filled by LDS DMA (global_load_lds, 16
-// bytes per lane at consecutive LDS addresses).  The 16-byte chunk c of key
-// row r (dims 8c..8c+7) sits in chunk slot 8r + (c ^ tile_swz(r)): eight
-// consecutive rows read at one chunk (the K fragments) fall in eight
-// different bank groups, and so do the four rows x 32 bytes of each
-// transpose read.
-constexpr int kTileElems = kTile * 64;  // one unpadded K or V tile, bf16 elements
-// per-lane element offsets into a SwzTile, fixed for the kernel
-struct SwzLane {
-  int ko[2];  // K fragment, dc = 0, 1 (plus 1024 * kb)
-  int vo[4];  // transpose read, db = 0..3 (plus 64 * (32kc + 16h))
-  __device__ __forceinline__ void init() {
-    const int lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
-    const int c0 = g ^ tile_swz(r16);
-    ko[0] = r16 * 64 + 8 * c0;
-    ko[1] = r16 * 64 + 8 * (c0 ^ 4);
-    const int m = r16, row = 4 * g + (m >> 2);
-    const int cv = ((m & 3) >> 1) ^ tile_swz(row);
-#pragma unroll
-    for (int db = 0; db < 4; ++db) vo[db] = row * 64 + 8 * ((2 * db) ^ cv) + 4 * (m & 1);
-  }
-};
-struct SwzTile {
-  const uint16_t* base;  // K tile, V tile at base + kTileElems
-  const SwzLane& L;
-  __device__ __forceinline__ const uint16_t* kfrag(int kb, int dc) const { return base + 1024 * kb + L.ko[dc]; }
-  __device__ __forceinline__ const uint16_t* vtr(int kc, int h, int db) const {
-    return base + kTileElems + 64 * (32 * kc + 16 * h) + L.vo[db];
-  }
-};
+constexpr int kTileElems = kSwzTileElems;  // one unpadded K or V tile, bf16 elements
 
 // One 64-key tile by DMA into a SwzTile: thread tid moves chunk slot tid%8
 // of key rows tid/8 and tid/8 + 32 (keys key0, key1) of K and of V: four

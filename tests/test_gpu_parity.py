@@ -510,10 +510,12 @@ def test_pack_vs_oracle(dev):
 
 
 @pytest.mark.parametrize("B,T,H,topk,masked", [(1, 5000, 8, 2, False), (2, 3001, 8, 3, True), (2, 1500, 20, 4, False),
-                                                 (1, 700, 16, 1, True), (3, 64, 5, 5, False)])
+                                                 (1, 700, 16, 1, True), (3, 64, 5, 5, False),
+                                                 (2, 70000, 32, 2, True)])
 def test_pack_rows_routed_vs_oracle(dev, B, T, H, topk, masked):
     """pfa_pack_rows from per-token head lists (the module's packing; H <= 16
-    and H > 16 take different count kernels): the row mask, the active heads,
+    and H > 16 take different count kernels, and B*H*ceil(T/1024) above 4096
+    -- the last case -- takes the separate scan launch): the row mask, the active heads,
     the compacted rows and row_of against the oracle's packing of the same
     mask restricted to its non-empty rows."""
     from proteus_attention import _hip
