@@ -144,9 +144,13 @@ int pfa_proto_ema_update(const float* sums, int G, int C, float decay,
  * guard), 1, T); the first `guard` tokens are always kept.
  * Replaces AdaptiveSparseAttention._select_active_tokens
  * (aspa.py:790-842).  importance (B, T) f32 -> mask (B, T) uint8.
+ * A radix select over the whole GPU (about 5 launches); workspace from
+ * pfa_token_topk_workspace_size (about 4*B*T bytes + 10 KB per row).
  * ==================================================================== */
+int pfa_token_topk_workspace_size(int B, int64_t T, size_t* bytes);
 int pfa_token_topk(const float* importance, int B, int64_t T, int64_t keep_count,
-                   int guard, float threshold, uint8_t* mask_out, void* stream);
+                   int guard, float threshold, uint8_t* mask_out,
+                   void* workspace, size_t ws_bytes, void* stream);
 
 /* ====================================================================
  * Row packing.  Builds the (B*H, T) activity mask from the head top-k

@@ -16,6 +16,7 @@
 // global compare-exchange passes for the strides >= kSortTile.  The whole
 // array lives in the caller's workspace.
 #include "pfa_common.h"
+#include "pfa_radix.h"
 
 // RoPE and quantisation round every elementwise product on its own, as the
 // reference's separate tensor ops do: no fused multiply-add contraction.
@@ -37,12 +38,9 @@ __device__ __forceinline__ bool finite_f(float f) { return (__float_as_uint(f) &
 // ---------------------------------------------------------------------
 // bitonic sort of u64 keys (ascending); n is a power of two
 // ---------------------------------------------------------------------
-__global__ void __launch_bounds__(1024) bitonic_tile_sort(uint64_t* keys, int64_t n, int kmax) {
-  __shared__ uint64_t s[kSortTile];
-  const int64_t base = (int64_t)blockIdx.x * kSortTile;
-  const int m = (int)(n - base < kSortTile ? n - base : kSortTile);
-  for (int i = threadIdx.x; i < m; i += blockDim.x) s[i] = keys[base + i];
-  __syncthreads();
+// Bitonic stages k = 2 .. kmax over s[0, m) in LDS; element i of the tile is
+// element base + i of the whole array (which fixes each pair's direction).
+__device__ __forceinline__ void lds_bitonic(uint64_t* s, int m, int kmax, int64_t base) {
   for (int k = 2; k <= kmax; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = threadIdx.x; i < m; i += blockDim.x) {
@@ -59,6 +57,15 @@ __global__ void __launch_bounds__(1024) bitonic_tile_sort(uint64_t* keys, int64_
       __syncthreads();
     }
   }
+}
+
+__global__ void __launch_bounds__(1024) bitonic_tile_sort(uint64_t* keys, int64_t n, int kmax) {
+  __shared__ uint64_t s[kSortTile];
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  const int m = (int)(n - base < kSortTile ? n - base : kSortTile);
+  for (int i = threadIdx.x; i < m; i += blockDim.x) s[i] = keys[base + i];
+  __syncthreads();
+  lds_bitonic(s, m, kmax, base);
   for (int i = threadIdx.x; i < m; i += blockDim.x) keys[base + i] = s[i];
 }
 
@@ -132,17 +139,6 @@ struct BlockScratch {
   int total;
 };
 
-__device__ __forceinline__ float block_max(float v, BlockScratch& sc) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sc.f[w] = v;
-  __syncthreads();
-  float r = sc.f[0];
-  for (int k = 1; k < kSelWaves; ++k) r = fmaxf(r, sc.f[k]);
-  return r;
-}
-
 __device__ __forceinline__ float block_sum(float v, BlockScratch& sc) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   const int w = threadIdx.x >> 6;
@@ -191,106 +187,179 @@ __device__ __forceinline__ float masked_score(const float* sc, const uint8_t* mk
 }
 __device__ __forceinline__ float safe_score(float v) { return finite_f(v) ? v : -1e9f; }
 
-// stats: [0] max safe score, [1] softmax denominator, [2] finite count (as float)
-__global__ void __launch_bounds__(kSelThreads) chunk_collect_kernel(const float* __restrict__ scores,
-                                                                  const uint8_t* __restrict__ mask, int64_t n,
-                                                                  int limit, int64_t limit_pow2, int need_z,
-                                                                  uint64_t* __restrict__ keys, float* stats) {
-  __shared__ BlockScratch sc;
-  __shared__ int hist[256];
-  __shared__ uint32_t s_prefix;
-  __shared__ int s_remaining;
-  __shared__ int s_gt;
-  const int tid = threadIdx.x;
-  // max of the safe scores and the number of finite masked scores
-  float mx = -INFINITY;
-  int nfin = 0;
-  for (int64_t i = tid; i < n; i += kSelThreads) {
-    const float v = masked_score(scores, mask, i);
-    mx = fmaxf(mx, safe_score(v));
-    nfin += finite_f(v) ? 1 : 0;
+struct ChunkKeys {
+  const float* scores;
+  const uint8_t* mask;
+  __device__ __forceinline__ uint32_t key(int, int64_t i) const {
+    return ord_key(safe_score(masked_score(scores, mask, i)));
   }
-  mx = block_max(mx, sc);
-  float fin = block_sum((float)nfin, sc);
-  float z = 0.f;
-  if (need_z) {
-    float acc = 0.f;
-    for (int64_t i = tid; i < n; i += kSelThreads) acc += expf(safe_score(masked_score(scores, mask, i)) - mx);
-    z = block_sum(acc, sc);
-  }
-  if (tid == 0) {
-    stats[0] = mx;
-    stats[1] = z;
-    stats[2] = fin;
-  }
-  // radix select: the limit-th largest key ord(safe)
-  uint32_t prefix = 0, pmask = 0;
-  int remaining = limit;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = tid; b < 256; b += kSelThreads) hist[b] = 0;
-    __syncthreads();
-    for (int64_t i = tid; i < n; i += kSelThreads) {
-      const uint32_t k = ord_key(safe_score(masked_score(scores, mask, i)));
-      if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int cum = 0;
-      int b = 255;
-      for (; b > 0; --b) {
-        if (cum + hist[b] >= remaining) break;
-        cum += hist[b];
-      }
-      s_prefix = prefix | ((uint32_t)b << shift);
-      s_remaining = remaining - cum;
-    }
-    __syncthreads();
-    prefix = s_prefix;
-    remaining = s_remaining;
-    pmask |= 255u << shift;
-  }
-  // keys above the threshold (any slot order), then `remaining` ties by
-  // ascending position
-  const uint32_t thr = prefix;
-  if (tid == 0) s_gt = 0;
-  __syncthreads();
-  const int n_gt = limit - remaining;
-  int tie_base = 0;
-  for (int64_t base = 0; base < n; base += kSelThreads) {
-    const int64_t i = base + tid;
-    uint32_t k = 0;
-    if (i < n) k = ord_key(safe_score(masked_score(scores, mask, i)));
-    const bool gt = i < n && k > thr;
-    const bool eq = i < n && k == thr;
-    if (gt) {
-      const int slot = atomicAdd(&s_gt, 1);
-      keys[slot] = ((uint64_t)(~k) << 32) | (uint64_t)(uint32_t)i;
-    }
-    int tot = 0;
-    const int r = block_rank(eq, sc, tot);
-    if (eq && tie_base + r < remaining) keys[n_gt + tie_base + r] = ((uint64_t)(~k) << 32) | (uint64_t)(uint32_t)i;
-    tie_base += tot;
-  }
-  for (int64_t i = limit + tid; i < limit_pow2; i += kSelThreads) keys[i] = ~0ull;
+};
+
+__device__ __forceinline__ float ord_to_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+// After the radix passes: writes the selected keys (~ord(score) << 32 |
+// position) into keys[0, limit) -- keys above the cut in any slot order,
+// then the `remaining` lowest-position ties -- pads keys[limit, limit_pow2)
+// with ~0, and gathers the emit statistics (largest safe score, finite
+// count).  grid = groups_of(n).
+__global__ void __launch_bounds__(rsel::kThreads) chunk_keys_kernel(ChunkKeys src, int64_t n, int64_t limit_pow2,
+                                                                    unsigned char* ws, uint64_t* __restrict__ keys) {
+  __shared__ uint32_t sm[rsel::kThreads / 64];
+  __shared__ uint32_t s_base;
+  const int w = blockIdx.x, tid = threadIdx.x;
+  rsel::State* st = reinterpret_cast<rsel::State*>(ws);
+  const int32_t* tiebase = reinterpret_cast<const int32_t*>(ws + rsel::layout(gridDim.x).tiebase);
+  const int64_t i0 = (int64_t)w * rsel::kSpan + (int64_t)tid * rsel::kPer;
+  uint32_t kv[rsel::kPer];
+  int nfin = 0;
+#pragma unroll
+  for (int e = 0; e < rsel::kPer; ++e) {
+    kv[e] = 0u;
+    if (i0 + e < n) {
+      const float v = masked_score(src.scores, src.mask, i0 + e);
+      nfin += finite_f(v) ? 1 : 0;
+      kv[e] = ord_key(safe_score(v));
+    }
+  }
+  // statistics of this workgroup (reduced by the emit kernel)
+  uint32_t mx = 0u;
+#pragma unroll
+  for (int e = 0; e < rsel::kPer; ++e) mx = i0 + e < n && kv[e] > mx ? kv[e] : mx;
+  for (int o = 32; o > 0; o >>= 1) {
+    mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+    nfin += __shfl_xor(nfin, o, 64);
+  }
+  __shared__ uint32_t s_mx[rsel::kThreads / 64];
+  __shared__ int s_fin[rsel::kThreads / 64];
+  if ((tid & 63) == 0) {
+    s_mx[tid >> 6] = mx;
+    s_fin[tid >> 6] = nfin;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t m2 = 0u;
+    int f2 = 0;
+    for (int k = 0; k < rsel::kThreads / 64; ++k) {
+      m2 = max(m2, s_mx[k]);
+      f2 += s_fin[k];
+    }
+    uint32_t* ws2 = reinterpret_cast<uint32_t*>(ws + rsel::layout(gridDim.x).wstat) + 2 * w;
+    ws2[0] = m2;
+    ws2[1] = (uint32_t)f2;
+  }
+  const int limit = st->need;
+  if ((int64_t)limit >= n) {
+    // everything is selected: key i in slot i
+#pragma unroll
+    for (int e = 0; e < rsel::kPer; ++e)
+      if (i0 + e < n) keys[i0 + e] = ((uint64_t)(~kv[e]) << 32) | (uint64_t)(uint32_t)(i0 + e);
+  } else {
+    bool sel[rsel::kPer], above[rsel::kPer];
+    uint32_t rank[rsel::kPer];
+    const int remaining = st->remaining;
+    rsel::select_keys(kv, i0, n, st->prefix, remaining, tiebase[w], sm, sel, above, rank);
+    uint32_t na = 0u;
+#pragma unroll
+    for (int e = 0; e < rsel::kPer; ++e) na += above[e] ? 1u : 0u;
+    uint32_t tot = 0u;
+    uint32_t pos = rsel::block_excl_scan(na, sm, tot);
+    if (tid == 0) s_base = tot != 0u ? atomicAdd(&st->slot, tot) : 0u;
+    __syncthreads();
+    pos += s_base;
+    const uint32_t n_above = (uint32_t)(limit - remaining);
+#pragma unroll
+    for (int e = 0; e < rsel::kPer; ++e) {
+      const uint64_t key = ((uint64_t)(~kv[e]) << 32) | (uint64_t)(uint32_t)(i0 + e);
+      if (above[e]) {
+        if (pos < n_above) keys[pos] = key;  // exactly n_above keys lie above the cut
+        ++pos;
+      } else if (sel[e]) {
+        keys[n_above + rank[e]] = key;
+      }
+    }
+  }
+  if (w == 0)
+    for (int64_t j = (limit < n ? limit : n) + tid; j < limit_pow2; j += rsel::kThreads) keys[j] = ~0ull;
+}
+
+// The selected keys in order, the nucleus cut and the outputs.  `keys` holds
+// limit_pow2 keys; sort_here: they are not sorted yet (limit_pow2 <= kSortTile)
+// and are sorted in LDS first.  wstat: the keys kernel's per-workgroup
+// statistics (largest order key, finite count) of `groups` workgroups.
 __global__ void __launch_bounds__(kSelThreads) chunk_emit_kernel(const float* __restrict__ scores,
                                                                const uint8_t* __restrict__ mask, int64_t n,
                                                                const uint64_t* __restrict__ keys, int limit,
-                                                               float top_p, const float* __restrict__ stats,
+                                                               int limit_pow2, int sort_here, float top_p,
+                                                               const uint32_t* __restrict__ wstat, int groups,
                                                                int64_t offset, int drop_nonfinite,
                                                                float* __restrict__ vals_out,
                                                                int64_t* __restrict__ idx_out, int32_t* count_out) {
   __shared__ BlockScratch sc;
   __shared__ int s_keep;
+  __shared__ uint64_t s_keys[kSortTile];
   const int tid = threadIdx.x;
-  if (limit <= 0 || !(stats[2] > 0.5f)) {  // nothing selectable, or no finite score
+  if (limit <= 0) {  // nothing selectable
     if (tid == 0) *count_out = 0;
     return;
   }
-  const float mx = stats[0], z = stats[1];
+  // statistics over the workgroups of the keys kernel
+  uint32_t mo = 0u;
+  int fin = 0;
+  for (int g = tid; g < groups; g += kSelThreads) {
+    mo = max(mo, wstat[2 * g]);
+    fin += (int)wstat[2 * g + 1];
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    mo = max(mo, (uint32_t)__shfl_xor((int)mo, o, 64));
+    fin += __shfl_xor(fin, o, 64);
+  }
+  if ((tid & 63) == 0) {
+    sc.i[tid >> 6] = fin;
+    sc.f[tid >> 6] = __uint_as_float(mo);
+  }
+  __syncthreads();
+  fin = 0;
+  mo = 0u;
+  for (int k = 0; k < kSelWaves; ++k) {
+    fin += sc.i[k];
+    mo = max(mo, __float_as_uint(sc.f[k]));
+  }
+  if (fin <= 0) {  // no finite score
+    if (tid == 0) *count_out = 0;
+    return;
+  }
+  const uint64_t* K = keys;
+  if (sort_here && limit <= kSelThreads) {
+    // rank sort: the keys are distinct (they carry the position), so key t
+    // goes to slot #(keys below it); one key per thread, kSortTile/2 slots
+    // of LDS for the input
+    uint64_t* in = s_keys + kSortTile / 2;
+    if (tid < limit) in[tid] = keys[tid];
+    __syncthreads();
+    if (tid < limit) {
+      const uint64_t k = in[tid];
+      int r = 0;
+      for (int j = 0; j < limit; ++j) r += in[j] < k ? 1 : 0;
+      s_keys[r] = k;
+    }
+    __syncthreads();
+    K = s_keys;
+  } else if (sort_here) {
+    for (int i = tid; i < limit_pow2; i += kSelThreads) s_keys[i] = keys[i];
+    __syncthreads();
+    lds_bitonic(s_keys, limit_pow2, limit_pow2, 0);
+    K = s_keys;
+  }
+  const float mx = ord_to_float(mo);
   int keep = limit;
   if (top_p < 1.0f) {
+    // softmax denominator over the chunk (each thread sums its strided
+    // scores, then the fixed-order block sum)
+    float acc = 0.f;
+    for (int64_t i = tid; i < n; i += kSelThreads) acc += expf(safe_score(masked_score(scores, mask, i)) - mx);
+    const float z = block_sum(acc, sc);
     // mass_r = cumulative softmax probability in selection order; keep =
     // #(mass < top_p) (+1 when that is not every token), clamped
     float carry = 0.f;
@@ -299,7 +368,7 @@ __global__ void __launch_bounds__(kSelThreads) chunk_emit_kernel(const float* __
       const int r = base + tid;
       float p = 0.f;
       if (r < limit) {
-        const int64_t i = (int64_t)(uint32_t)(keys[r] & 0xffffffffu);
+        const int64_t i = (int64_t)(uint32_t)(K[r] & 0xffffffffu);
         p = expf(safe_score(masked_score(scores, mask, i)) - mx) / z;
       }
       // inclusive scan of p over the step (wave scan, then wave totals)
@@ -335,7 +404,7 @@ __global__ void __launch_bounds__(kSelThreads) chunk_emit_kernel(const float* __
     float v = 0.f;
     int64_t i = 0;
     if (r < keep) {
-      i = (int64_t)(uint32_t)(keys[r] & 0xffffffffu);
+      i = (int64_t)(uint32_t)(K[r] & 0xffffffffu);
       v = masked_score(scores, mask, i);
     }
     const bool ok = r < keep && (!drop_nonfinite || finite_f(v));
@@ -480,12 +549,15 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(typename Elem<DT>::T* x,
 
 using namespace pfa;
 
-// workspace of pfa_chunk_topk: pow2(min(budget, n)) keys + 4 floats
+// workspace of pfa_chunk_topk: pow2(min(budget, n)) keys, then the radix
+// select's state (about 4n + 10 KB bytes)
+static size_t chunk_keys_bytes(int64_t limit) { return ((size_t)pow2_ceil(limit > 0 ? limit : 1) * 8 + 255) / 256 * 256; }
+
 extern "C" int pfa_chunk_topk_workspace_size(int64_t n, int budget, size_t* bytes) {
   clear_error();
   PFA_CHECK_ARG(bytes && n >= 0 && budget >= 0, "pfa_chunk_topk_workspace_size: bad arguments");
   const int64_t limit = n < budget ? n : budget;
-  *bytes = (size_t)pow2_ceil(limit > 0 ? limit : 1) * 8 + 16;
+  *bytes = chunk_keys_bytes(limit) + rsel::segment_bytes(n);
   return PFA_OK;
 }
 
@@ -504,22 +576,33 @@ extern "C" int pfa_chunk_topk(const float* scores, const uint8_t* keep_mask, int
   PFA_CHECK_ARG(workspace && ws_bytes >= need, "pfa_chunk_topk: workspace of %zu bytes required", need);
   if (limit <= 0) {
     // nothing can be selected: count 0 (written by a one-lane emit)
-    chunk_emit_kernel<<<1, kSelThreads, 0, s>>>(scores, keep_mask, n, nullptr, 0, top_p, nullptr, 0, 0, values_out,
-                                                 indices_out, count_out);
+    chunk_emit_kernel<<<1, kSelThreads, 0, s>>>(scores, keep_mask, n, nullptr, 0, 0, 0, top_p, nullptr, 0, 0, 0,
+                                                 values_out, indices_out, count_out);
     PFA_CHECK_LAUNCH("pfa_chunk_topk");
     return PFA_OK;
   }
   PFA_CHECK_ARG(scores && values_out && indices_out, "pfa_chunk_topk: null pointer");
   const int64_t lp = pow2_ceil(limit);
   uint64_t* keys = (uint64_t*)workspace;
-  float* stats = (float*)((char*)workspace + lp * 8);
-  chunk_collect_kernel<<<1, kSelThreads, 0, s>>>(scores, keep_mask, n, (int)limit, lp, top_p < 1.0f ? 1 : 0, keys,
-                                                   stats);
-  PFA_CHECK_LAUNCH("pfa_chunk_topk/collect");
-  int rc = sort_u64(keys, lp, s, "pfa_chunk_topk/sort");
+  unsigned char* sel_ws = (unsigned char*)workspace + chunk_keys_bytes(limit);
+  const size_t seg = rsel::segment_bytes(n);
+  const ChunkKeys src{scores, keep_mask};
+  rsel::init_kernel<ChunkKeys><<<1, rsel::kThreads, 0, s>>>(sel_ws, seg, limit);
+  PFA_CHECK_LAUNCH("pfa_chunk_topk/init");
+  int rc = rsel::run_passes(src, n, 1, sel_ws, seg, s, "pfa_chunk_topk/select");
   if (rc != PFA_OK) return rc;
-  chunk_emit_kernel<<<1, kSelThreads, 0, s>>>(scores, keep_mask, n, keys, (int)limit, top_p, stats, index_offset,
-                                               drop_nonfinite ? 1 : 0, values_out, indices_out, count_out);
+  chunk_keys_kernel<<<(unsigned)rsel::groups_of(n), rsel::kThreads, 0, s>>>(src, n, lp, sel_ws, keys);
+  PFA_CHECK_LAUNCH("pfa_chunk_topk/keys");
+  const int groups = (int)rsel::groups_of(n);
+  const uint32_t* wstat = (const uint32_t*)(sel_ws + rsel::layout(groups).wstat);
+  const bool sort_here = lp <= kSortTile;
+  if (!sort_here) {
+    rc = sort_u64(keys, lp, s, "pfa_chunk_topk/sort");
+    if (rc != PFA_OK) return rc;
+  }
+  chunk_emit_kernel<<<1, kSelThreads, 0, s>>>(scores, keep_mask, n, keys, (int)limit, (int)lp, sort_here ? 1 : 0,
+                                               top_p, wstat, groups, index_offset, drop_nonfinite ? 1 : 0, values_out,
+                                               indices_out, count_out);
   PFA_CHECK_LAUNCH("pfa_chunk_topk/emit");
   return PFA_OK;
 }

@@ -1,19 +1,17 @@
 // Token top-k (radix select) and row packing.
 #include "pfa_common.h"
+#include "pfa_radix.h"
 
 #include <mutex>
 
 namespace pfa {
 
 // ---------------------------------------------------------------------
-// Token top-k.  One workgroup per batch row.  The `need` largest values are
-// found with a 4 x 8-bit radix select on order-preserving 32-bit keys; of the
-// values equal to the cut value, the lowest indices are taken (an ordered
-// scan over the row).  Replaces the per-batch torch.topk loop of
-// aspa.py:823-840.
+// Token top-k.  Per batch row, the `need` largest values are found by the
+// multi-workgroup radix select of pfa_radix.h on order-preserving 32-bit
+// keys; of the values equal to the cut value, the lowest indices are taken.
+// Replaces the per-batch torch.topk loop of aspa.py:823-840.
 // ---------------------------------------------------------------------
-constexpr int kTopkThreads = 1024;
-
 __device__ __forceinline__ uint32_t order_key(float f) {
   uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -32,91 +30,71 @@ __device__ __forceinline__ int block_sum_int(int v, int* red) {
   return s;
 }
 
-__global__ void __launch_bounds__(kTopkThreads)
-token_topk_kernel(const float* __restrict__ imp, int64_t T, int64_t keep_count, int guard, float threshold,
-                  uint8_t* __restrict__ mask) {
-  __shared__ int hist[256];
-  __shared__ int red[16];
-  __shared__ uint32_t s_prefix;
-  __shared__ int64_t s_remaining;
-  const int b = blockIdx.x;
-  const float* row = imp + (int64_t)b * T;
-  uint8_t* mrow = mask + (int64_t)b * T;
+struct ImportanceKeys {
+  const float* imp;
+  int64_t T;
+  __device__ __forceinline__ uint32_t key(int b, int64_t i) const { return order_key(imp[(int64_t)b * T + i]); }
+};
 
+// need = max(keep_count, #(imp >= threshold), guard) clamped to [1, T], when
+// the threshold makes it data dependent.  grid = (groups, B); the last
+// workgroup of a row finalises the row's state.
+__global__ void __launch_bounds__(rsel::kThreads) topk_need_kernel(const float* __restrict__ imp, int64_t T,
+                                                                   float threshold, int64_t keep_count, int guard,
+                                                                   unsigned char* ws, size_t seg_bytes) {
+  __shared__ int red[rsel::kThreads / 64];
+  __shared__ int s_last;
+  const int b = blockIdx.y;
+  rsel::State* st = reinterpret_cast<rsel::State*>(ws + (size_t)b * seg_bytes);
+  const int64_t i0 = (int64_t)blockIdx.x * rsel::kSpan + (int64_t)threadIdx.x * rsel::kPer;
+  int c = 0;
+#pragma unroll
+  for (int e = 0; e < rsel::kPer; ++e)
+    if (i0 + e < T) c += imp[(int64_t)b * T + i0 + e] >= threshold ? 1 : 0;
+  c = block_sum_int(c, red);
+  if (threadIdx.x == 0 && c != 0)
+    __hip_atomic_fetch_add(&st->count, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!rsel::arrive(&st->done, gridDim.x, &s_last) || threadIdx.x != 0) return;
+  const int64_t cnt = (int64_t)__hip_atomic_load(&st->count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int64_t need = keep_count;
-  if (threshold > 0.f) {
-    int cnt = 0;
-    for (int64_t i = threadIdx.x; i < T; i += blockDim.x) cnt += (row[i] >= threshold) ? 1 : 0;
-    int64_t c = block_sum_int(cnt, red);
-    if (c > need) need = c;
-  }
+  if (cnt > need) need = cnt;
   if (guard > need) need = guard;
   if (need < 1) need = 1;
   if (need > T) need = T;
+  st->need = (int32_t)need;
+  st->remaining = (int32_t)need;
+  st->done = 0u;
+}
 
-  if (need >= T) {
-    for (int64_t i = threadIdx.x; i < T; i += blockDim.x) mrow[i] = 1;
+// The mask: keys above the cut, the first `remaining` keys equal to it (by
+// index), and the first `guard` tokens.  grid = (groups, B).
+__global__ void __launch_bounds__(rsel::kThreads) topk_mask_kernel(ImportanceKeys src, int guard,
+                                                                   const unsigned char* ws, size_t seg_bytes,
+                                                                   uint8_t* __restrict__ mask) {
+  __shared__ uint32_t sm[rsel::kThreads / 64];
+  const int b = blockIdx.y, w = blockIdx.x;
+  const int64_t T = src.T;
+  const unsigned char* base = ws + (size_t)b * seg_bytes;
+  const rsel::State* st = reinterpret_cast<const rsel::State*>(base);
+  const int32_t* tiebase = reinterpret_cast<const int32_t*>(base + rsel::layout(gridDim.x).tiebase);
+  uint8_t* mrow = mask + (int64_t)b * T;
+  const int64_t i0 = (int64_t)w * rsel::kSpan + (int64_t)threadIdx.x * rsel::kPer;
+  const int need = st->need;
+  if ((int64_t)need >= T) {
+#pragma unroll
+    for (int e = 0; e < rsel::kPer; ++e)
+      if (i0 + e < T) mrow[i0 + e] = 1;
     return;
   }
-
-  uint32_t prefix = 0, pmask = 0;
-  int64_t remaining = need;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
-    __syncthreads();
-    for (int64_t i = threadIdx.x; i < T; i += blockDim.x) {
-      uint32_t k = order_key(row[i]);
-      if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 0xffu], 1);
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int64_t acc = 0;
-      int bin = 0;
-      for (bin = 255; bin >= 0; --bin) {
-        if (acc + hist[bin] >= remaining) break;
-        acc += hist[bin];
-      }
-      s_prefix = prefix | ((uint32_t)bin << shift);
-      s_remaining = remaining - acc;
-    }
-    __syncthreads();
-    prefix = s_prefix;
-    remaining = s_remaining;
-    pmask |= 0xffu << shift;
-    __syncthreads();
-  }
-  // prefix == key of the need-th largest value; `remaining` elements equal
-  // to it are taken, lowest index first.
-  const uint32_t cut = prefix;
-  int64_t carry = 0;
-  __shared__ int wave_tot[16];
-  for (int64_t base = 0; base < T; base += blockDim.x) {
-    int64_t i = base + threadIdx.x;
-    uint32_t k = (i < T) ? order_key(row[i]) : 0u;
-    int eq = (i < T && k == cut) ? 1 : 0;
-    // inclusive scan of eq across the block
-    int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    int v = eq;
-    for (int off = 1; off < 64; off <<= 1) {
-      int n = __shfl_up(v, off, 64);
-      if (lane >= off) v += n;
-    }
-    if (lane == 63) wave_tot[wid] = v;
-    __syncthreads();
-    int before = 0, total = 0;
-    int nw = blockDim.x >> 6;
-    for (int w = 0; w < nw; ++w) {
-      if (w < wid) before += wave_tot[w];
-      total += wave_tot[w];
-    }
-    int64_t rank = carry + before + v - eq;  // exclusive rank among equal keys
-    if (i < T) {
-      bool sel = (k > cut) || (eq && rank < remaining) || (i < guard);
-      mrow[i] = sel ? 1 : 0;
-    }
-    carry += total;
-    __syncthreads();
-  }
+  uint32_t kv[rsel::kPer];
+#pragma unroll
+  for (int e = 0; e < rsel::kPer; ++e) kv[e] = i0 + e < T ? src.key(b, i0 + e) : 0u;
+  bool sel[rsel::kPer], above[rsel::kPer];
+  uint32_t rank[rsel::kPer];
+  rsel::select_keys(kv, i0, T, st->prefix, st->remaining, tiebase[w], sm, sel, above, rank);
+#pragma unroll
+  for (int e = 0; e < rsel::kPer; ++e)
+    if (i0 + e < T) mrow[i0 + e] = (sel[e] || i0 + e < guard) ? 1 : 0;
 }
 
 // ---------------------------------------------------------------------
@@ -534,14 +512,45 @@ static PackWs carve(void* ws, int64_t BH, int nblk) {
 
 using namespace pfa;
 
-extern "C" int pfa_token_topk(const float* importance, int B, int64_t T, int64_t keep_count, int guard,
-                              float threshold, uint8_t* mask_out, void* stream) {
+extern "C" int pfa_token_topk_workspace_size(int B, int64_t T, size_t* bytes) {
   clear_error();
-  PFA_CHECK_ARG(importance && mask_out && B >= 0 && T >= 0, "pfa_token_topk: bad arguments");
+  PFA_CHECK_ARG(bytes && B >= 0 && T >= 0, "pfa_token_topk_workspace_size: bad arguments");
+  *bytes = (size_t)(B > 0 ? B : 1) * rsel::segment_bytes(T);
+  return PFA_OK;
+}
+
+extern "C" int pfa_token_topk(const float* importance, int B, int64_t T, int64_t keep_count, int guard,
+                              float threshold, uint8_t* mask_out, void* workspace, size_t ws_bytes, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(B >= 0 && T >= 0 && T < INT32_MAX, "pfa_token_topk: bad sizes B=%d T=%lld", B, (long long)T);
   if (B == 0 || T == 0) return PFA_OK;
-  token_topk_kernel<<<B, kTopkThreads, 0, as_stream(stream)>>>(importance, T, keep_count, guard < 0 ? 0 : guard,
-                                                                threshold, mask_out);
-  PFA_CHECK_LAUNCH("pfa_token_topk");
+  PFA_CHECK_ARG(importance && mask_out, "pfa_token_topk: null pointer");
+  size_t need_ws = 0;
+  pfa_token_topk_workspace_size(B, T, &need_ws);
+  PFA_CHECK_ARG(workspace && ws_bytes >= need_ws, "pfa_token_topk: workspace of %zu bytes required", need_ws);
+  hipStream_t s = as_stream(stream);
+  unsigned char* ws = (unsigned char*)workspace;
+  const size_t seg = rsel::segment_bytes(T);
+  const int g = guard < 0 ? 0 : guard;
+  const bool thr = threshold > 0.f;
+  int64_t need = keep_count;
+  if (!thr) {
+    if (g > need) need = g;
+    if (need < 1) need = 1;
+    if (need > T) need = T;
+  }
+  rsel::init_kernel<ImportanceKeys><<<(unsigned)B, rsel::kThreads, 0, s>>>(ws, seg, need);
+  PFA_CHECK_LAUNCH("pfa_token_topk/init");
+  const dim3 grid((unsigned)rsel::groups_of(T), (unsigned)B);
+  if (thr) {
+    topk_need_kernel<<<grid, rsel::kThreads, 0, s>>>(importance, T, threshold, keep_count, g, ws, seg);
+    PFA_CHECK_LAUNCH("pfa_token_topk/need");
+  }
+  const ImportanceKeys src{importance, T};
+  int rc = rsel::run_passes(src, T, B, ws, seg, s, "pfa_token_topk/select");
+  if (rc != PFA_OK) return rc;
+  topk_mask_kernel<<<grid, rsel::kThreads, 0, s>>>(src, g, ws, seg, mask_out);
+  PFA_CHECK_LAUNCH("pfa_token_topk/mask");
   return PFA_OK;
 }
 

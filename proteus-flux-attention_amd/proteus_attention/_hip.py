@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "pfa_proto_partial_count",
     "pfa_proto_accumulate",
     "pfa_proto_partial_reduce",
+    "pfa_token_topk_workspace_size",
     "pfa_token_topk",
     "pfa_pack_workspace_size",
     "pfa_pack_rows",
@@ -100,7 +101,8 @@ _SIGNATURES = {
     "pfa_proto_partial_count": ([_i64, ctypes.POINTER(_i32)], _i32),
     "pfa_proto_accumulate": ([_vp, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _vp], _i32),
     "pfa_proto_partial_reduce": ([_vp, _i32, _i32, _i32, _vp, _vp], _i32),
-    "pfa_token_topk": ([_vp, _i32, _i64, _i64, _i32, _f32, _vp, _vp], _i32),
+    "pfa_token_topk_workspace_size": ([_i32, _i64, ctypes.POINTER(_sz)], _i32),
+    "pfa_token_topk": ([_vp, _i32, _i64, _i64, _i32, _f32, _vp, _vp, _sz, _vp], _i32),
     "pfa_pack_workspace_size": ([_i32, _i32, _i64, ctypes.POINTER(_sz)], _i32),
     "pfa_pack_rows": ([_vp, _i32, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_pack_rows_static": ([_vp, _i32, _vp, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),

@@ -846,8 +846,10 @@ class AdaptiveSparseAttention(nn.Module):
         _hip.require_device(importance, what="_select_active_tokens")
         imp = importance.to(torch.float32).contiguous()
         mask8 = torch.empty(B, T, dtype=torch.uint8, device=device)
-        rc = _hip.lib().pfa_token_topk(_hip.ptr(imp), B, T, keep, guard, float(self.token_keep_threshold),
-                                       _hip.ptr(mask8), _hip.stream_ptr(device))
+        lib = _hip.lib()
+        ws = _sa._workspace(_sa._size_out(lib.pfa_token_topk_workspace_size, B, T), device)
+        rc = lib.pfa_token_topk(_hip.ptr(imp), B, T, keep, guard, float(self.token_keep_threshold),
+                                _hip.ptr(mask8), _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device))
         _hip.check(rc, "pfa_token_topk")
         mask = mask8.view(torch.bool)
         self._last_token_mask = mask

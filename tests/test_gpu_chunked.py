@@ -36,7 +36,8 @@ def test_chunk_topk_golden(dev, golden):
 @pytest.mark.parametrize("n,budget,top_p,ties,masked", [
     (4096, 512, 1.0, False, True), (65536, 512, 1.0, False, True), (65536, 512, 1.0, True, True),
     (1000, 5000, 1.0, True, False), (70000, 9000, 1.0, True, True), (3000, 700, 0.5, False, True),
-    (1, 1, 1.0, False, False), (257, 3, 0.999, True, True)])
+    (1, 1, 1.0, False, False), (257, 3, 0.999, True, True), (20000, 3000, 0.95, True, True),
+    (262144, 512, 1.0, False, False)])
 def test_chunk_topk_vs_oracle(dev, n, budget, top_p, ties, masked):
     from proteus_attention.tools import chunk_select
 

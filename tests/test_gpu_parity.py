@@ -475,6 +475,29 @@ def test_token_topk_vs_oracle(dev):
     assert torch.equal(mask, exp)
 
 
+@pytest.mark.parametrize("B,T,ratio,guard,threshold,levels", [
+    (2, 70000, 0.1, 4, 0.0, 40), (1, 65536, 0.25, 0, 0.0, 0), (3, 1000, 0.5, 7, 0.95, 10), (1, 1, 0.5, 0, 0.0, 0),
+    (2, 300000, 0.02, 16, 0.999, 1000)])
+def test_token_topk_sizes_vs_oracle(dev, B, T, ratio, guard, threshold, levels):
+    """The multi-workgroup selection at sizes from one token to several
+    hundred workgroups: heavy ties (values on a grid of `levels`, or
+    continuous with levels = 0), a guard, a threshold."""
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    _say(f"token top-k B={B} T={T} ratio={ratio} guard={guard} threshold={threshold}")
+    g = torch.Generator().manual_seed(T + B)
+    imp = torch.rand(B, T, generator=g)
+    if levels:
+        imp = torch.floor(imp * levels) / levels
+    m = AdaptiveSparseAttention(ModelConfig(d_model=64, n_head=4, attn_h_total=4, attn_token_sparse=True,
+                                            attn_token_keep_ratio=ratio, attn_token_keep_guard=guard,
+                                            attn_token_keep_threshold=threshold))
+    m._token_keep_ratio_runtime = ratio
+    mask = m._select_active_tokens(imp.to(dev)).cpu()
+    exp = O.select_active_tokens(imp, ratio, m.token_keep_min, guard, threshold)
+    assert torch.equal(mask, exp)
+
+
 def test_token_topk_golden(dev, golden):
     from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
 
