@@ -477,12 +477,14 @@ int pfa_rope_rows_inplace(void* x, int dtype, int64_t n_rows, int64_t row_stride
  * point lets every one of T query tokens attend to the S shortlisted keys,
  * causal by original position when `causal` (key j visible to query t iff
  * key_pos[j] <= t; key_pos ascending).  K/V are int8 (H, S, D) with
- * per-(head, row) scales (H, S) from pfa_quantize_rows_int8, dequantised
- * to bf16 inside each LDS tile.  q/out are bf16 [h][t][d] through
- * pfa_tensor4 strides (s_b unused: one sequence).  A query with no
- * visible key gets a zero row.  S >= 1.
+ * per-(head, row) scales (H, S) from pfa_quantize_rows_int8 (k8/v8
+ * 16-byte aligned), dequantised once per call to bf16 (x8 * scale, round
+ * to nearest even) into the workspace, which therefore holds 4*H*S*D
+ * bytes plus the query tiles' key ranges.  q/out are bf16 [h][t][d]
+ * through pfa_tensor4 strides (s_b unused: one sequence).  A query with
+ * no visible key gets a zero row.  S >= 1.
  * ==================================================================== */
-int pfa_int8_kv_attn_workspace_size(int64_t T, size_t* bytes);
+int pfa_int8_kv_attn_workspace_size(int64_t T, int H, int S, size_t* bytes);
 int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, int H, int D,
                          const int8_t* k8, const int8_t* v8, const float* k_scale,
                          const float* v_scale, const int32_t* key_pos, int S,

@@ -286,4 +286,25 @@ struct SwzTile {
   }
 };
 
+// One 64-key tile by DMA into a SwzTile (256 threads): thread tid moves chunk
+// slot tid%8 of key rows tid/8 and tid/8 + 32 (keys key0, key1) of K and of
+// V: four 16-byte transfers, each wave filling 1 KB runs of chunk slots.
+// lds_w is the tile's LDS byte address plus 1 KB per wave index
+// (wave-uniform); kb/vb are bf16 rows with token strides ks_t/vs_t.
+constexpr int kDmaPerTile = 4;
+__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
+                                         uint32_t ks_t, uint32_t vs_t, int key0, int key1, uint32_t lds_w) {
+  const int tid = threadIdx.x;
+  const int c = 8 * ((tid & 7) ^ tile_swz(tid >> 3));  // rows tid/8 and tid/8 + 32 share the swizzle
+  // element offsets: one 32 x 32 -> 64-bit multiply each (keys and row
+  // strides are below 2^31)
+  const uint64_t k0 = (uint64_t)(uint32_t)key0 * ks_t, k1 = (uint64_t)(uint32_t)key1 * ks_t;
+  const uint64_t v0 = (uint64_t)(uint32_t)key0 * vs_t, v1 = (uint64_t)(uint32_t)key1 * vs_t;
+  lds_dma16(kb + c + k0, lds_w);
+  lds_dma16(kb + c + k1, lds_w + 4096);
+  lds_dma16(vb + c + v0, lds_w + 2 * kSwzTileElems);
+  lds_dma16(vb + c + v1, lds_w + 2 * kSwzTileElems + 4096);
+}
+
+
 }  // namespace pfa

@@ -2,12 +2,17 @@
 // shortlist pipeline (config 5).  Every query token t of one sequence
 // attends to the S shortlisted keys; with `causal`, only to keys whose
 // original position key_pos[j] <= t.  K and V of the shortlist are int8 with
-// one symmetric scale per (head, key row); they are dequantised inside the
-// tile: each staged 64-key tile is converted k8 * k_scale -> bf16 (and
-// likewise V) into the swizzled 128-byte-row layout of the bf16 attention
-// kernels (each thread writes two 16-byte chunks of K and two of V; the V^T
-// operand comes from the LDS transpose read), then S = Q K^T and O += P V run
-// on v_mfma_f32_16x16x32_bf16 with an online softmax in f32 registers.
+// one symmetric scale per (head, key row).
+//
+// Every key is read by every 128-query tile of its head (8,192 tiles at
+// T = 2^20), so the shortlist is dequantised once per call, k8 * k_scale ->
+// bf16 (the bits the tile conversion would give), into a working copy in
+// the workspace (16 MB at H = 8, S = 8,192); the attention then streams
+// 64-key tiles of it by LDS DMA into the swizzled 128-byte-row layout of the
+// bf16 attention kernels (the V^T operand from the LDS transpose read), and
+// S = Q K^T and O += P V run on v_mfma_f32_16x16x32_bf16 with an online
+// softmax in f32 registers.  (Dequantising inside every tile spent about 2 ms
+// of VALU time at config 5.)
 //
 // Workgroup: 4 waves, 128 consecutive query tokens of one head (32 per wave
 // in two 16-query MFMA column groups).  The shortlist is sorted by
@@ -15,7 +20,7 @@
 // rng.x (position < first token of the tile) are visible to every query and
 // run unmasked; the at most few keys in [rng.x, rng.y) are masked per
 // (query, key).  Block b handles head b % H, so on 8 XCDs each XCD's L2
-// holds one head's int8 K/V; tiles run heaviest first.
+// holds one head's K/V; tiles run heaviest first.
 #include "pfa_common.h"
 
 namespace pfa {
@@ -28,15 +33,18 @@ constexpr int kTile = kSwzKeys;  // keys per tile
 constexpr int kD = 64;
 constexpr float kRescaleLog2 = 0.0f;  // rescale only when some row's max rises
 
+#ifndef PFA_FIN_STAGES
+#define PFA_FIN_STAGES 2
+#endif
+constexpr int kStages = PFA_FIN_STAGES;  // LDS ring of K/V tiles
+
 struct Args {
   const uint16_t* q;
   int64_t q_sh, q_st;
   uint16_t* out;
   int64_t o_sh, o_st;
-  const int8_t* k8;
-  const int8_t* v8;
-  const float* ks;
-  const float* vs;
+  const uint16_t* kb;  // dequantised shortlist, bf16 (H, S, 64)
+  const uint16_t* vb;
   const int32_t* kpos;
   const int2* rng;
   int H, S, causal, nqt;
@@ -49,55 +57,43 @@ struct St {
   f32x4_t acc[4];
 };
 
-// one 64-key tile staged by 256 threads: thread -> key tid/4, elements
-// 16*(tid%4) .. +15 of that key's K and V rows
-struct Fetch {
-  uint4 k, v;
-  float kscale, vscale;
-  int pos;
-};
-
-__device__ __forceinline__ Fetch fetch(const int8_t* kb, const int8_t* vb, const float* ksb, const float* vsb,
-                                       const int32_t* kpos, int key) {
-  const int qd = threadIdx.x & 3;
-  Fetch f;
-  f.k = *reinterpret_cast<const uint4*>(kb + (int64_t)key * kD + 16 * qd);
-  f.v = *reinterpret_cast<const uint4*>(vb + (int64_t)key * kD + 16 * qd);
-  f.kscale = ksb[key];
-  f.vscale = vsb[key];
-  f.pos = kpos[key];
-  return f;
-}
-
 __device__ __forceinline__ float i8f(uint32_t w, int e) { return (float)(int)(int8_t)((w >> (8 * e)) & 0xffu); }
 
-// the thread's 16 K and 16 V elements (key tid/4, dims 16*(tid%4) ..+15) are
-// chunks 2*(tid%4) and 2*(tid%4)+1 of the key's row
-__device__ __forceinline__ void store(const Fetch& f, uint16_t* tile_base, int32_t* kp) {
-  const int j = threadIdx.x >> 2, qd = threadIdx.x & 3;
-  const int sw = tile_swz(j);
-  const uint32_t kw4[4] = {f.k.x, f.k.y, f.k.z, f.k.w};
-  const uint32_t vw4[4] = {f.v.x, f.v.y, f.v.z, f.v.w};
+// bf16(x8 * scale) for the (H*S, 64) rows of K and V: thread -> row idx/4,
+// elements 16*(idx%4) .. +15.
+__global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__ k8, const int8_t* __restrict__ v8,
+                                                      const float* __restrict__ ks, const float* __restrict__ vs,
+                                                      int64_t rows, uint16_t* __restrict__ kb,
+                                                      uint16_t* __restrict__ vb) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * 4) return;
+  const int64_t row = idx >> 2;
+  const int qd = (int)(idx & 3);
+  const uint4 k = *reinterpret_cast<const uint4*>(k8 + row * kD + 16 * qd);
+  const uint4 v = *reinterpret_cast<const uint4*>(v8 + row * kD + 16 * qd);
+  const float kscale = ks[row], vscale = vs[row];
+  const uint32_t kw4[4] = {k.x, k.y, k.z, k.w};
+  const uint32_t vw4[4] = {v.x, v.y, v.z, v.w};
   __bf16 kd[16], vd[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    kd[e] = (__bf16)(i8f(kw4[e >> 2], e & 3) * f.kscale);
-    vd[e] = (__bf16)(i8f(vw4[e >> 2], e & 3) * f.vscale);
+    kd[e] = (__bf16)(i8f(kw4[e >> 2], e & 3) * kscale);
+    vd[e] = (__bf16)(i8f(vw4[e >> 2], e & 3) * vscale);
   }
   uint4 kw[2], vw[2];
   __builtin_memcpy(kw, kd, 32);
   __builtin_memcpy(vw, vd, 32);
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int slot = 8 * j + ((2 * qd + h) ^ sw);
-    *reinterpret_cast<uint4*>(tile_base + 8 * slot) = kw[h];
-    *reinterpret_cast<uint4*>(tile_base + kSwzTileElems + 8 * slot) = vw[h];
-  }
-  if (qd == 0) kp[j] = f.pos;
+  uint4* ko = reinterpret_cast<uint4*>(kb + row * kD + 16 * qd);
+  uint4* vo = reinterpret_cast<uint4*>(vb + row * kD + 16 * qd);
+  ko[0] = kw[0];
+  ko[1] = kw[1];
+  vo[0] = vw[0];
+  vo[1] = vw[1];
 }
 
+// kpos: the shortlist's positions (global; read only in masked tiles)
 template <bool MASKED>
-__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& tl, const int32_t* kp, int key0,
+__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& tl, const int32_t* kpos, int key0,
                                      int S, int causal, const int (&tq)[2], float sl2, St (&st)[2]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   float s[2][16];
@@ -113,8 +109,9 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if constexpr (MASKED) {
-          const int kl = 16 * kb + 4 * g + i;
-          const bool ok = key0 + kl < S && (!causal || kp[kl] <= tq[gr]);
+          const int key = key0 + 16 * kb + 4 * g + i;
+          const int pos = kpos[key < S ? key : S - 1];
+          const bool ok = key < S && (!causal || pos <= tq[gr]);
           s[gr][4 * kb + i] = ok ? c[i] : -INFINITY;
         } else {
           s[gr][4 * kb + i] = c[i];
@@ -206,9 +203,12 @@ __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restri
 }
 
 // at most 168 VGPRs: three 4-wave workgroups per CU
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) final_attn_kernel(Args a) {
-  __shared__ __align__(16) uint16_t ring[2][2 * kSwzTileElems];
-  __shared__ int32_t kp[2][kTile];
+#ifndef PFA_FIN_WAVES
+#define PFA_FIN_WAVES 3
+#endif
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PFA_FIN_WAVES, 8)))
+final_attn_kernel(Args a) {
+  __shared__ __align__(16) uint16_t ring[kStages][2 * kSwzTileElems];
 
   const int bid = blockIdx.x;
   const int h = bid % a.H;
@@ -227,6 +227,20 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
     qv[gr] = t < a.T;
     tq[gr] = (int)(qv[gr] ? t : a.T - 1);
   }
+  const uint16_t* kbh = a.kb + (int64_t)h * a.S * kD;
+  const uint16_t* vbh = a.vb + (int64_t)h * a.S * kD;
+  const int ntile = (rg.y + kTile - 1) / kTile;
+  const int drow = tid >> 3;  // this thread's DMA rows: drow and drow + 32
+  const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + 1024u * (uint32_t)wid);
+  constexpr uint32_t kStageBytes = 2 * kSwzTileElems * 2;
+  auto request = [&](int i) {
+    const int k0 = kTile * i;
+    dma_tile(kbh, vbh, kD, kD, min(k0 + drow, a.S - 1), min(k0 + drow + 32, a.S - 1),
+             ring_w + kStageBytes * (uint32_t)(i % kStages));
+  };
+#pragma unroll
+  for (int i = 0; i < kStages - 1; ++i)
+    if (i < ntile) request(i);
   const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
   bf16x8_t qf[2][2];
 #pragma unroll
@@ -236,6 +250,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
       const uint4 w = *reinterpret_cast<const uint4*>(qh + (int64_t)tq[gr] * a.q_st + 32 * dc + 8 * g);
       __builtin_memcpy(&qf[gr][dc], &w, 16);
     }
+  // settle the q fragments here: the tile loop then holds no load of the
+  // compiler's own to wait for (its wait would also drain the tile requests)
+  asm volatile("" : "+v"(qf[0][0]), "+v"(qf[0][1]), "+v"(qf[1][0]), "+v"(qf[1][1]));
   St st[2];
 #pragma unroll
   for (int gr = 0; gr < 2; ++gr) {
@@ -244,25 +261,18 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
 #pragma unroll
     for (int db = 0; db < 4; ++db) st[gr].acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  const int8_t* kb = a.k8 + (int64_t)h * a.S * kD;
-  const int8_t* vb = a.v8 + (int64_t)h * a.S * kD;
-  const float* ksb = a.ks + (int64_t)h * a.S;
-  const float* vsb = a.vs + (int64_t)h * a.S;
-  const int ntile = (rg.y + kTile - 1) / kTile;
-  const int jrow = tid >> 2;
-  if (ntile > 0) store(fetch(kb, vb, ksb, vsb, a.kpos, min(jrow, a.S - 1)), ring[0], kp[0]);
-  __syncthreads();
   for (int i = 0; i < ntile; ++i) {
-    const int cur = i & 1;
-    const bool more = i + 1 < ntile;
-    Fetch nxt;
-    if (more) nxt = fetch(kb, vb, ksb, vsb, a.kpos, min(kTile * (i + 1) + jrow, a.S - 1));
+    // tile i has landed (tiles i+1 .. i+kStages-2 may still be in flight) and
+    // every wave is done with tile i-1, whose stage takes tile i+kStages-1
+    if (kStages == 3 && i + 1 < ntile)
+      dma_wait_barrier<kDmaPerTile>();
+    else
+      dma_wait_barrier<0>();
+    if (i + kStages - 1 < ntile) request(i + kStages - 1);
     const int key0 = kTile * i;
-    const SwzTile tl{ring[cur], L};
-    if (key0 + kTile <= rg.x) tile<false>(qf, tl, kp[cur], key0, a.S, a.causal, tq, a.scale_log2, st);
-    else tile<true>(qf, tl, kp[cur], key0, a.S, a.causal, tq, a.scale_log2, st);
-    if (more) store(nxt, ring[cur ^ 1], kp[cur ^ 1]);
-    __syncthreads();
+    const SwzTile tl{ring[i % kStages], L};
+    if (key0 + kTile <= rg.x) tile<false>(qf, tl, a.kpos, key0, a.S, a.causal, tq, a.scale_log2, st);
+    else tile<true>(qf, tl, a.kpos, key0, a.S, a.causal, tq, a.scale_log2, st);
   }
   uint16_t* oh = a.out + (int64_t)h * a.o_sh;
 #pragma unroll
@@ -289,11 +299,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
 
 using namespace pfa;
 
-extern "C" int pfa_int8_kv_attn_workspace_size(int64_t T, size_t* bytes) {
-  clear_error();
-  PFA_CHECK_ARG(bytes && T >= 0, "pfa_int8_kv_attn_workspace_size: bad arguments");
+// workspace: the query tiles' key ranges, then the bf16 K and V copies
+static size_t fin_rng_bytes(int64_t T) {
   const int64_t nqt = (T + fin::kQ - 1) / fin::kQ;
-  *bytes = (size_t)(nqt > 0 ? nqt : 1) * sizeof(int2);
+  return ((size_t)(nqt > 0 ? nqt : 1) * sizeof(int2) + 255) / 256 * 256;
+}
+static size_t fin_copy_bytes(int H, int S) { return ((size_t)H * (size_t)S * fin::kD * 2 + 255) / 256 * 256; }
+
+extern "C" int pfa_int8_kv_attn_workspace_size(int64_t T, int H, int S, size_t* bytes) {
+  clear_error();
+  PFA_CHECK_ARG(bytes && T >= 0 && H >= 0 && S >= 0, "pfa_int8_kv_attn_workspace_size: bad arguments");
+  *bytes = fin_rng_bytes(T) + 2 * fin_copy_bytes(H, S);
   return PFA_OK;
 }
 
@@ -312,12 +328,18 @@ extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, i
   hipStream_t s = as_stream(stream);
   PFA_CHECK_ARG(S > 0, "pfa_int8_kv_attn_fwd: empty shortlist (S must be >= 1)");
   PFA_CHECK_ARG(k8 && v8 && k_scale && v_scale && key_pos, "pfa_int8_kv_attn_fwd: null shortlist pointer");
-  PFA_CHECK_ARG(((uintptr_t)k8 % 8) == 0 && ((uintptr_t)v8 % 8) == 0, "pfa_int8_kv_attn_fwd: k8/v8 must be 8-byte aligned");
+  PFA_CHECK_ARG(((uintptr_t)k8 % 16) == 0 && ((uintptr_t)v8 % 16) == 0, "pfa_int8_kv_attn_fwd: k8/v8 must be 16-byte aligned");
+  PFA_CHECK_ARG((int64_t)S * fin::kD < INT32_MAX, "pfa_int8_kv_attn_fwd: S too large (%d)", S);
   size_t need = 0;
-  pfa_int8_kv_attn_workspace_size(T, &need);
+  pfa_int8_kv_attn_workspace_size(T, H, S, &need);
   PFA_CHECK_ARG(workspace && ws_bytes >= need, "pfa_int8_kv_attn_fwd: workspace of %zu bytes required", need);
   const int nqt = (int)((T + fin::kQ - 1) / fin::kQ);
   int2* rng = (int2*)workspace;
+  uint16_t* kbf = (uint16_t*)((char*)workspace + fin_rng_bytes(T));
+  uint16_t* vbf = (uint16_t*)((char*)kbf + fin_copy_bytes(H, S));
+  const int64_t rows = (int64_t)H * S;
+  fin::dequant_kernel<<<(unsigned)((rows * 4 + 255) / 256), 256, 0, s>>>(k8, v8, k_scale, v_scale, rows, kbf, vbf);
+  PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/dequant");
   fin::key_ranges_kernel<<<(unsigned)((nqt + 255) / 256), 256, 0, s>>>(key_pos, S, T, nqt, causal ? 1 : 0, rng);
   PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/ranges");
   fin::Args a;
@@ -327,10 +349,8 @@ extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, i
   a.out = (uint16_t*)out.ptr;
   a.o_sh = out.s_h;
   a.o_st = out.s_t;
-  a.k8 = k8;
-  a.v8 = v8;
-  a.ks = k_scale;
-  a.vs = v_scale;
+  a.kb = kbf;
+  a.vb = vbf;
   a.kpos = key_pos;
   a.rng = rng;
   a.H = H;

@@ -105,25 +105,6 @@ __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); 
 
 constexpr int kTileElems = kSwzTileElems;  // one unpadded K or V tile, bf16 elements
 
-// One 64-key tile by DMA into a SwzTile: thread tid moves chunk slot tid%8
-// of key rows tid/8 and tid/8 + 32 (keys key0, key1) of K and of V: four
-// 16-byte transfers, each wave filling 1 KB runs of chunk slots.  lds_w is
-// the tile's LDS byte address plus 1 KB per wave index (wave-uniform).
-constexpr int kDmaPerTile = 4;
-__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
-                                         uint32_t ks_t, uint32_t vs_t, int key0, int key1, uint32_t lds_w) {
-  const int tid = threadIdx.x;
-  const int c = 8 * ((tid & 7) ^ tile_swz(tid >> 3));  // rows tid/8 and tid/8 + 32 share the swizzle
-  // element offsets: one 32 x 32 -> 64-bit multiply each (keys and row
-  // strides are below 2^31)
-  const uint64_t k0 = (uint64_t)(uint32_t)key0 * ks_t, k1 = (uint64_t)(uint32_t)key1 * ks_t;
-  const uint64_t v0 = (uint64_t)(uint32_t)key0 * vs_t, v1 = (uint64_t)(uint32_t)key1 * vs_t;
-  lds_dma16(kb + c + k0, lds_w);
-  lds_dma16(kb + c + k1, lds_w + 4096);
-  lds_dma16(vb + c + v0, lds_w + 2 * kTileElems);
-  lds_dma16(vb + c + v1, lds_w + 2 * kTileElems + 4096);
-}
-
 // One 64-key tile for the 16 query rows of this wave, in three stages that
 // every tile kind shares: qk_tile (the scores), a mask (keys of the tile
 // that are not candidates of the lane's row get -inf), softmax_pv (online

@@ -132,7 +132,7 @@ _SIGNATURES = {
     "pfa_shortlist_finalise": ([_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_quantize_rows_int8": ([_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
     "pfa_rope_rows_inplace": ([_vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _vp], _i32),
-    "pfa_int8_kv_attn_workspace_size": ([_i64, ctypes.POINTER(_sz)], _i32),
+    "pfa_int8_kv_attn_workspace_size": ([_i64, _i32, _i32, ctypes.POINTER(_sz)], _i32),
     "pfa_int8_kv_attn_fwd": ([Tensor4, Tensor4, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp,
                               _sz, _vp], _i32),
 }

@@ -102,7 +102,7 @@ def int8_shortlist_attention(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor
         return out.zero_()
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
     lib = _hip.lib()
-    ws = _workspace(_size_out(lib.pfa_int8_kv_attn_workspace_size, T), device)
+    ws = _workspace(_size_out(lib.pfa_int8_kv_attn_workspace_size, T, H, S), device)
     kp = key_pos.to(torch.int32).contiguous()
     t4q = _hip.Tensor4(_hip.ptr(q), 0, q.stride(1), q.stride(0))
     t4o = _hip.Tensor4(_hip.ptr(out), 0, out.stride(1), out.stride(0))
