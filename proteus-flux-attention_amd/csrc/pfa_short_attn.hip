@@ -665,17 +665,32 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     // tile ord[i], ord[i] < 0 prototype tile -1 - ord[i]
     const int np = (plen + kTile - 1) / kTile;
     const int ntile = nw + np;
-    if (tid == 0) {
-      int pos = 0, pj = 0;
-      for (int sl2 = 0; sl2 < kSlots; ++sl2) {
-        int k = wA + ((sl2 - wA) & (kSlots - 1));
-        if (k <= wB) {
-          for (; k <= wB; k += kSlots) ord[pos++] = k;
-        } else if (pj < np) {
-          ord[pos++] = -1 - pj++;
-        }
+    // built by the first wave, one lane per slot: slot i takes window tiles
+    // k = i (mod kSlots) in [wA, wB], or else, if it has none, the next
+    // prototype tile; prototype tiles left over go last
+    if (wid == 0) {
+      const int sl_i = lane & (kSlots - 1);
+      const int k0 = wA + ((sl_i - wA) & (kSlots - 1));
+      const bool win = k0 <= wB;
+      const uint64_t empty = __ballot(lane < kSlots && !win);
+      const int e = __popcll(empty & ((1ull << lane) - 1ull));  // empty slots before this one
+      const int cnt = lane < kSlots ? (win ? (wB - k0) / kSlots + 1 : (e < np ? 1 : 0)) : 0;
+      int incl = cnt;
+#pragma unroll
+      for (int o = 1; o < kSlots; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
       }
-      while (pj < np) ord[pos++] = -1 - pj++;
+      const int pos = incl - cnt;
+      if (lane < kSlots) {
+        if (win)
+          for (int j = 0; j < cnt; ++j) ord[pos + j] = k0 + kSlots * j;
+        else if (cnt)
+          ord[pos] = -1 - e;
+      }
+      const int n_empty = __popcll(empty);
+      const int placed = __shfl(incl, kSlots - 1, 64);
+      for (int j = n_empty + lane; j < np; j += 64) ord[placed + (j - n_empty)] = -1 - j;
     }
     __syncthreads();
     auto key_of = [&](int i, int r) -> int {
