@@ -467,6 +467,7 @@ class ChunkedShortlistRunner:
             scores_all: List[torch.Tensor] = []
             idx_all: List[torch.Tensor] = []
             summaries: List[ChunkSummary] = []
+            pending_summaries: List[Tuple[int, int, int, torch.Tensor, torch.Tensor]] = []
             used_fallback = False
             ev_c0 = ev_c1 = None
             if cfg.report_latency and device.type == "cuda":
@@ -510,13 +511,18 @@ class ChunkedShortlistRunner:
                     stager.release(ci)
                 scores_all.append(sc)
                 idx_all.append(ix)
-                summaries.append(ChunkSummary(index=ci, start=s, end=e, promoted=ix.tolist(),
-                                              scores=[float(v) for v in sc.tolist()]))
+                # the per-chunk summaries are read only after the run: their
+                # host lists are built after the loop, so that no chunk waits
+                # for its own device-to-host copy
+                pending_summaries.append((ci, s, e, ix, sc))
                 t_chunks = time.perf_counter()
             if not scores_all:
                 raise RuntimeError("Chunked pipeline selected zero tokens; adjust per_chunk_budget or sparse ratios.")
             if ev_c1 is not None:
                 ev_c1.record()
+            for p_ci, p_s, p_e, p_ix, p_sc in pending_summaries:
+                summaries.append(ChunkSummary(index=p_ci, start=p_s, end=p_e, promoted=p_ix.tolist(),
+                                              scores=[float(v) for v in p_sc.tolist()]))
             keep_idx, keep_scores = _finalise_indices(torch.cat(scores_all), torch.cat(idx_all),
                                                       max_tokens=cfg.buffer_tokens)
             reduced = st["gather"](keep_idx.to(torch.long)).to(device, non_blocking=st["pinned"])
