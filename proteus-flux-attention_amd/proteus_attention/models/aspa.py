@@ -1206,7 +1206,10 @@ class AdaptiveSparseAttention(nn.Module):
         # nucleus / alpha blend below can only shrink k, and the first k of a
         # ranked list are the top-k under the same total order.
         gate, sim, blend, imp, hidx_all, hsc_all = self._route_device(x2d, dense_topk)
-        if self.router_top_p > 0.0:
+        # (when dense_topk is already the floor h_active_min, the nucleus count
+        # cannot change k: max(h_min, min(dense_topk, n)) = dense_topk, and
+        # its host readback is skipped)
+        if self.router_top_p > 0.0 and dense_topk > self.h_active_min:
             head_probs = gate.view(B, T, -1) @ self.gate_to_head_onehot.to(device=device, dtype=gate.dtype)
             nucleus_k = self._nucleus_head_count(head_probs, self.router_top_p, dense_topk)
             adaptive_topk = max(self.h_active_min, min(dense_topk, nucleus_k))
