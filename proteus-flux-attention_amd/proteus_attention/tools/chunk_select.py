@@ -1,7 +1,9 @@
 """Chunk salience selection and global shortlist merge on the device.
 
 nucleus_select  -- reference chunked_shortlist.py:175-208 (and the masking
-                   and finite filter of _select_top_tokens, :140-172)
+                   and finite filter of _select_top_tokens, :140-172);
+                   nucleus_select_device is the same selection with the
+                   count left on the device
 finalise        -- reference chunked_shortlist.py:211-254
 
 Both run as HIP kernels of libpfa_hip.so (``pfa_chunk_topk``: radix select
@@ -20,16 +22,14 @@ from .. import _hip
 from ..kernels.sparse_attn import _size_out, _workspace
 
 
-def nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float,
-                   keep_mask: Optional[torch.Tensor] = None, index_offset: int = 0,
-                   drop_nonfinite: bool = False) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
-    """Top tokens of one chunk by score with nucleus (top-p) truncation.
-
-    Positions where ``keep_mask`` is False score -inf.  Returns
-    ``(selected_scores, selected_positions + index_offset)`` in selection
-    order (int64 positions), or None when nothing is finite or nothing is
-    selected.  ``drop_nonfinite`` removes selected entries whose score is
-    not finite (the filter _select_top_tokens applies)."""
+def nucleus_select_device(scores: torch.Tensor, max_tokens: int, top_p: float,
+                          keep_mask: Optional[torch.Tensor] = None, index_offset: int = 0,
+                          drop_nonfinite: bool = False
+                          ) -> Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:
+    """As nucleus_select, with no host synchronisation: (values, indices,
+    count) with the buffers sized to min(max_tokens, n) and the count an
+    int32 device tensor (entries beyond it are unused), or None when nothing
+    can be selected (max_tokens or n is 0)."""
 
     if scores.ndim != 1:
         raise ValueError("scores tensor must be 1-D for nucleus selection.")
@@ -54,6 +54,23 @@ def nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float,
     _hip.check(lib.pfa_chunk_topk(_hip.ptr(sc), _hip.ptr(mk), n, limit, float(top_p), int(index_offset),
                                   1 if drop_nonfinite else 0, _hip.ptr(vals), _hip.ptr(idx), _hip.ptr(cnt),
                                   _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device)), "pfa_chunk_topk")
+    return vals, idx, cnt
+
+
+def nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float, keep_mask: Optional[torch.Tensor] = None,
+                   index_offset: int = 0, drop_nonfinite: bool = False):
+    """Reference chunked_shortlist.py:175-208 (+ the masking / finite filter
+    of _select_top_tokens, 140-172) on the device: (values, indices) in
+    selection order (int64 positions), or None when nothing is finite or
+    nothing is selected.  ``drop_nonfinite`` removes selected entries whose
+    score is not finite (the filter _select_top_tokens applies).  Reads the
+    count back: nucleus_select_device leaves it on the device."""
+
+    out = nucleus_select_device(scores, max_tokens, top_p, keep_mask=keep_mask, index_offset=index_offset,
+                                drop_nonfinite=drop_nonfinite)
+    if out is None:
+        return None
+    vals, idx, cnt = out
     c = int(cnt.item())
     if c == 0:
         return None

@@ -89,9 +89,12 @@ def _build_model_config(seq_len: int, d_model: int, *, heads: int, sparse_ratio:
 
 
 def _select_top_tokens(model: AdaptiveSparseAttention, global_offset: int, *, per_chunk_budget: int,
-                       nucleus_top_p: float) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+                       nucleus_top_p: float) -> Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:
     """Chunk salience (reference chunked_shortlist.py:140-172): the chunk
-    model's importance, non-kept tokens at -inf, nucleus-selected."""
+    model's importance, non-kept tokens at -inf, nucleus-selected.  Returns
+    (values, positions, count) with the count left on the device (the first
+    ``count`` entries are the selection; a count of 0 is the reference's
+    "nothing finite selected" case), or None without importance or budget."""
 
     importance = getattr(model, "_last_token_importance", None)
     if importance is None or importance.device.type != "cuda":
@@ -99,10 +102,10 @@ def _select_top_tokens(model: AdaptiveSparseAttention, global_offset: int, *, pe
     scores = importance.squeeze(0).to(torch.float32)
     mask = getattr(model, "_last_token_mask", None)
     # masking, nucleus selection and the finite filter run in one kernel
-    # (pfa_chunk_topk); None when nothing finite is selected
-    return chunk_select.nucleus_select(scores, per_chunk_budget, nucleus_top_p,
-                                       keep_mask=mask.squeeze(0) if mask is not None else None,
-                                       index_offset=int(global_offset), drop_nonfinite=True)
+    # (pfa_chunk_topk)
+    return chunk_select.nucleus_select_device(scores, per_chunk_budget, nucleus_top_p,
+                                              keep_mask=mask.squeeze(0) if mask is not None else None,
+                                              index_offset=int(global_offset), drop_nonfinite=True)
 
 
 def _nucleus_select(scores: torch.Tensor, max_tokens: int, top_p: float):
@@ -464,10 +467,11 @@ class ChunkedShortlistRunner:
                 chunk_model(torch.randn(1, cfg.chunk_len, cfg.d_model, device=device, dtype=base_dtype))
             if device.type == "cuda":
                 torch.cuda.synchronize()
-            scores_all: List[torch.Tensor] = []
-            idx_all: List[torch.Tensor] = []
             summaries: List[ChunkSummary] = []
-            pending_summaries: List[Tuple[int, int, int, torch.Tensor, torch.Tensor]] = []
+            # (chunk, start, end, values, positions, count or None): a chunk's
+            # selection count stays on the device until the loop is done, so
+            # no chunk waits for its own selection
+            pending: List[Tuple[int, int, int, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]] = []
             used_fallback = False
             ev_c0 = ev_c1 = None
             if cfg.report_latency and device.type == "cuda":
@@ -482,6 +486,19 @@ class ChunkedShortlistRunner:
                 stager = _ChunkStager(st, chunks, cfg.chunk_len, cfg.d_model, device, base_dtype)
                 st["stager"] = stager
                 stager.start(0)
+
+            def norm_fallback(ci: int, xc: torch.Tensor) -> None:
+                # reference chunked_shortlist.py:632-646: the chunk's token
+                # norms when its importance selects nothing
+                nonlocal used_fallback
+                s, e = chunks[ci]
+                sel = _nucleus_select(xc[0].detach().norm(dim=-1).to(torch.float32),
+                                      cfg.per_chunk_budget, cfg.nucleus_top_p)
+                if sel is not None:
+                    vals, rel = sel
+                    pending.append((ci, s, e, vals, rel.to(torch.long) + s, None))
+                    used_fallback = True
+
             for ci, (s, e) in enumerate(chunks):
                 if direct:
                     xc = st["fetch"](s, e)
@@ -496,33 +513,46 @@ class ChunkedShortlistRunner:
                 promoted = _select_top_tokens(chunk_model, s, per_chunk_budget=cfg.per_chunk_budget,
                                               nucleus_top_p=cfg.nucleus_top_p)
                 if promoted is None:
-                    sel = _nucleus_select(xc[0].detach().norm(dim=-1).to(torch.float32),
-                                          cfg.per_chunk_budget, cfg.nucleus_top_p)
-                    if sel is None:
-                        if stager is not None:
-                            stager.release(ci)
-                        continue
-                    vals, rel = sel
-                    sc, ix = vals, rel.to(torch.long) + s
-                    used_fallback = True
+                    norm_fallback(ci, xc)
                 else:
-                    sc, ix = promoted
+                    pending.append((ci, s, e) + tuple(promoted))
                 if stager is not None:
                     stager.release(ci)
-                scores_all.append(sc)
-                idx_all.append(ix)
-                # the per-chunk summaries are read only after the run: their
-                # host lists are built after the loop, so that no chunk waits
-                # for its own device-to-host copy
-                pending_summaries.append((ci, s, e, ix, sc))
                 t_chunks = time.perf_counter()
-            if not scores_all:
-                raise RuntimeError("Chunked pipeline selected zero tokens; adjust per_chunk_budget or sparse ratios.")
             if ev_c1 is not None:
                 ev_c1.record()
-            for p_ci, p_s, p_e, p_ix, p_sc in pending_summaries:
+            # one readback for every chunk's count; a chunk whose selection is
+            # empty takes the norm fallback on its data fetched again
+            dev_counts = [p[5] for p in pending if p[5] is not None]
+            counts = torch.cat(dev_counts).tolist() if dev_counts else []
+            selected: List[Tuple[int, int, int, torch.Tensor, torch.Tensor]] = []
+            redo: List[int] = []
+            for p_ci, p_s, p_e, p_sc, p_ix, p_cnt in pending:
+                if p_cnt is None:
+                    selected.append((p_ci, p_s, p_e, p_sc, p_ix))
+                    continue
+                c = int(counts.pop(0))
+                if c > 0:
+                    selected.append((p_ci, p_s, p_e, p_sc[:c], p_ix[:c]))
+                else:
+                    redo.append(p_ci)
+            if redo:
+                pending.clear()
+                for ci in redo:
+                    s, e = chunks[ci]
+                    with torch.inference_mode():
+                        norm_fallback(ci, st["fetch"](s, e).to(device))
+                selected.extend((p[0], p[1], p[2], p[3], p[4]) for p in pending)
+                selected.sort(key=lambda p: p[0])
+                if ev_c1 is not None:
+                    ev_c1.record()
+            if not selected:
+                raise RuntimeError("Chunked pipeline selected zero tokens; adjust per_chunk_budget or sparse ratios.")
+            for p_ci, p_s, p_e, p_sc, p_ix in selected:
                 summaries.append(ChunkSummary(index=p_ci, start=p_s, end=p_e, promoted=p_ix.tolist(),
                                               scores=[float(v) for v in p_sc.tolist()]))
+            scores_all = [p[3] for p in selected]
+            idx_all = [p[4] for p in selected]
             keep_idx, keep_scores = _finalise_indices(torch.cat(scores_all), torch.cat(idx_all),
                                                       max_tokens=cfg.buffer_tokens)
             reduced = st["gather"](keep_idx.to(torch.long)).to(device, non_blocking=st["pinned"])

@@ -201,3 +201,54 @@ def test_chunked_runner_host_staging_matches_device(dev, source):
     assert [c.promoted for c in res.chunks] == [c.promoted for c in ref.chunks]
     assert res.metrics.h2d_time_ms is not None and res.metrics.h2d_time_ms > 0.0
     assert res.metrics.h2d_stall_ms is not None and res.metrics.h2d_stall_ms >= 0.0
+
+
+@pytest.mark.parametrize("storage", ["device", "cpu", "disk"])
+def test_chunked_runner_norm_fallback(dev, monkeypatch, storage):
+    """A chunk whose selection is empty (count 0, known only after the chunk
+    loop) and a chunk with no importance (known at once) both take the
+    reference's token-norm fallback (chunked_shortlist.py:632-646): the
+    first on its data fetched again from the staging, the second on the
+    chunk in hand.  Every other chunk keeps its importance selection."""
+    from proteus_attention.tools import chunked_shortlist as cs
+    from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
+
+    T, C, chunk, budget = 8192, 512, 2048, 128
+    print(f"chunked runner norm fallback storage={storage}", flush=True)
+    x = torch.randn(1, T, C, generator=torch.Generator().manual_seed(22)).to(torch.bfloat16)
+    orig = cs._select_top_tokens
+    seen = {}
+
+    def patched(model, offset, **kw):
+        out = orig(model, offset, **kw)
+        c = int(out[2].item())
+        seen[offset] = (out[0][:c].cpu(), out[1][:c].cpu())
+        if offset == 0:
+            return out[0], out[1], torch.zeros_like(out[2])
+        if offset == 2 * chunk:
+            return None
+        return out
+
+    monkeypatch.setattr(cs, "_select_top_tokens", patched)
+    kw = dict(seq_len=T, d_model=C, chunk_len=chunk, buffer_tokens=T, per_chunk_budget=budget, device=dev, heads=8,
+              nucleus_top_p=1.0, run_final_pass=False)
+    src = x.to(dev) if storage == "device" else x
+    res = ChunkedShortlistRunner(ChunkedShortlistConfig(storage="cpu" if storage == "device" else storage,
+                                                        **kw)).run(src)
+    assert res.metrics.storage_mode == storage and res.metrics.used_fallback
+    assert [ch.index for ch in res.chunks] == [0, 1, 2, 3]
+    xd = x.to(dev)
+    all_s, all_i = [], []
+    for ch in res.chunks:
+        s = ch.start
+        if s in (0, 2 * chunk):
+            norms = xd[0, s:s + chunk].norm(dim=-1).to(torch.float32).cpu()
+            ev, ei = O.nucleus_select(norms, budget, 1.0, index_offset=s)
+        else:
+            ev, ei = seen[s]
+        assert ch.promoted == ei.tolist(), f"chunk at {s}"
+        assert torch.equal(torch.tensor(ch.scores, dtype=torch.float32), ev), f"chunk at {s}"
+        all_s.append(ev)
+        all_i.append(ei)
+    ki, ks = O.finalise_indices(torch.cat(all_s), torch.cat(all_i), T)
+    assert torch.equal(res.keep_indices.cpu(), ki) and torch.equal(res.keep_scores.cpu(), ks)

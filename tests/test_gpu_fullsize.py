@@ -141,7 +141,8 @@ def test_chunked_pipeline_config5_vs_oracle(dev, monkeypatch):
         imp = model._last_token_importance.squeeze(0).float().cpu()
         mask = model._last_token_mask.squeeze(0).cpu()
         out = orig(model, offset, **kw)
-        seen.append((offset, imp, mask, None if out is None else (out[0].cpu(), out[1].cpu())))
+        c = None if out is None else int(out[2].item())
+        seen.append((offset, imp, mask, None if out is None else (out[0][:c].cpu(), out[1][:c].cpu())))
         return out
 
     monkeypatch.setattr(cs, "_select_top_tokens", spy)
