@@ -364,18 +364,21 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
 }
 
 // ---------------------------------------------------------------------
-// bf16 router on MFMA (8 gates)
+// bf16 router on MFMA (8 or 16 gates)
 // ---------------------------------------------------------------------
 // Each wave owns one group of 64 tokens (4 tiles of 16) and computes, with
-// v_mfma_f32_16x16x32_bf16, the 16 x 64 product of an operand table with the
-// tokens' rows: table rows 0-7 are the gate weights (already rounded to
-// bf16) and rows 8-15 the normalised prototypes.  An f32 prototype entry is
-// split into three bf16 parts, p = hi + mid + lo (hi = bf16(p), mid =
-// bf16(p - hi), lo = bf16(p - hi - mid); every difference is exact in f32 and
-// the three parts carry p's 24-bit significand), so with bf16 token values
-// every product is exact in f32 and the prototype dots are f32 dots
-// accumulated in a different order.  Table A0 = [W | hi], table A1 =
-// [mid | lo], each multiplied into its own accumulator.
+// v_mfma_f32_16x16x32_bf16, the product of 16-row operand tables with the
+// tokens' rows.  The operand rows are, in this order, the GP gate weights
+// (already rounded to bf16) and three bf16 parts of each normalised
+// prototype: an f32 entry p is split as p = hi + mid + lo (hi = bf16(p),
+// mid = bf16(p - hi), lo = bf16(p - hi - mid); every difference is exact in
+// f32 and the three parts carry p's 24-bit significand), so with bf16 token
+// values every product is exact in f32 and the prototype dots are f32 dots
+// accumulated in a different order.  Operand row v (kind v / GP: weight, hi,
+// mid, lo; gate v % GP) is row v % 16 of table v / 16: with 8 gates the
+// tables are [W | hi] and [mid | lo], with 16 gates W, hi, mid and lo each
+// fill a table.  Each table has its own accumulator.  Without prototypes
+// only the weight table is multiplied.
 //
 // Channel order: lane (c16, g) of tile n holds the 32 consecutive channels
 // 128q + 32g .. +31 of token 16n + c16 (four 16-byte loads, a whole 128-byte
@@ -384,51 +387,70 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
 // ch(s, g, j) = 128*(s/4) + 32g + 8*(s%4) + j.  The sum over channels does
 // not depend on the order, only the two operands must agree.
 constexpr int kRmWaves = 4;
-constexpr int kRmEpW = 33;  // staged floats per token: 8 logits, 8 hi, 8 mid, 8 lo, sum of squares
+constexpr int kRmEpW = 33;  // staged floats per token: GP logits, GP prototype dot parts, sum of squares
 
-__host__ __device__ constexpr int rm_region0(int C) {
-  return (64 * C > kRmWaves * 64 * kRmEpW * 4) ? 64 * C : kRmWaves * 64 * kRmEpW * 4;
-}
+__host__ __device__ constexpr int rm_tables(int GP, bool proto) { return proto ? GP / 4 : 1; }
 
 // Prototype EMA statistics of one 64-token group, one wave, on MFMA:
 // part[g][c] = sum_t gate[t][g] * x[t][c].  D = A.B with v_mfma_f32_16x16x32_bf16,
 // A = gates (rows) x tokens (k), B = tokens (k) x 16 channels.  A gate
 // g = hi + mid + lo is split into three bf16 parts (as the router's
 // prototype table: every difference exact, the parts carry g's whole
-// significand), so every product with a bf16 x is exact in f32; A1 holds hi
-// in rows 0-7 and mid in rows 8-15, A2 lo in rows 0-7.  The x rows are
-// staged in LDS 64 channels at a time (rows padded to kXsLd elements: the
-// four rows of a transpose read fall in disjoint banks) and read as B by the
-// LDS transpose read; gl holds the wave's gates [token][GP].
+// significand), so every product with a bf16 x is exact in f32.  With 8
+// gates A1 holds hi in rows 0-7 and mid in rows 8-15, A2 lo in rows 0-7;
+// with 16 gates A1, A2 and A3 hold hi, mid and lo.  Each gate's sum is
+// (hi + mid) + lo.  The x rows are staged in LDS 64 channels at a time (rows
+// padded to kXsLd elements: the four rows of a transpose read fall in
+// disjoint banks) and read as B by the LDS transpose read; gl holds the
+// wave's gates [token][GP].
 constexpr int kXsLd = 80;                          // staged x row, bf16 elements
 constexpr int kXsWave = 64 * kXsLd * 2;            // bytes per wave
-__host__ __device__ constexpr int rm_region_a(int C) {
-  return rm_region0(C) > kRmWaves * kXsWave ? rm_region0(C) : kRmWaves * kXsWave;
+
+// LDS of the MFMA router: the operand tables (main loop), then the staged
+// epilogue rows, then the gate rows and x staging of the EMA statistics, all
+// in the same bytes.
+__host__ __device__ constexpr int rm_lds_bytes(int C, int GP, bool proto) {
+  const int table = 32 * C * rm_tables(GP, proto);
+  const int stage = kRmWaves * 64 * kRmEpW * 4;
+  const int ema = kRmWaves * 64 * GP * 4 + kRmWaves * kXsWave;
+  const int m = table > stage ? table : stage;
+  return m > ema ? m : ema;
 }
+
+static_assert(rm_lds_bytes(768, 8, true) <= 65536 && rm_lds_bytes(512, 16, true) <= 65536,
+              "MFMA router LDS within 64 KiB at the widest rows it is launched for");
+
+template <int GP>
 __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, int64_t tok0, int nt, int C, int G,
                                                const float* gl, float* __restrict__ part, uint16_t* xs) {
   typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
   typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
   typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
-  constexpr int GP = 8;
+  constexpr int NA = GP == 8 ? 2 : 3;
   const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
   // A operands for the two 32-token k-steps
-  bf16x8 a1[2], a2[2];
+  bf16x8 a[NA][2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    uint16_t h1[8], h2[8];
+    uint16_t h[NA][8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float gv = gl[(32 * ks + 8 * kg + j) * GP + (m & 7)];
+      const float gv = gl[(32 * ks + 8 * kg + j) * GP + (GP == 8 ? (m & 7) : m)];
       const uint16_t hi = f32_to_bf16(gv);
       const float r1 = gv - bf16_to_f32(hi);
       const uint16_t mid = f32_to_bf16(r1);
       const uint16_t lo = f32_to_bf16(r1 - bf16_to_f32(mid));
-      h1[j] = m < 8 ? hi : mid;
-      h2[j] = m < 8 ? lo : (uint16_t)0;
+      if constexpr (GP == 8) {
+        h[0][j] = m < 8 ? hi : mid;
+        h[1][j] = m < 8 ? lo : (uint16_t)0;
+      } else {
+        h[0][j] = hi;
+        h[1][j] = mid;
+        h[NA - 1][j] = lo;
+      }
     }
-    __builtin_memcpy(&a1[ks], h1, 16);
-    __builtin_memcpy(&a2[ks], h2, 16);
+#pragma unroll
+    for (int t = 0; t < NA; ++t) __builtin_memcpy(&a[t][ks], h[t], 16);
   }
   // staging: lane l moves 16 bytes (channels 8*(l%8) ..+7) of tokens 8i + l/8
   const int srow = lane >> 3, scol = 8 * (lane & 7);
@@ -450,7 +472,9 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
     wave_sync();
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-      f32x4 d1 = {0.f, 0.f, 0.f, 0.f}, d2 = {0.f, 0.f, 0.f, 0.f};
+      f32x4 d[NA];
+#pragma unroll
+      for (int t = 0; t < NA; ++t) d[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         // lane (n, kg) gets x[32ks + 8kg + 0..7][16ct + n]
@@ -461,17 +485,22 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
         bf16x8 b;
         __builtin_memcpy(&b, &lo4, 8);
         __builtin_memcpy(reinterpret_cast<char*>(&b) + 8, &hi4, 8);
-        d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[ks], b, d1, 0, 0, 0);
-        d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[ks], b, d2, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < NA; ++t) d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][ks], b, d[t], 0, 0, 0);
       }
-      // lanes 0-31 hold rows 4*(lane/16) + i: hi (d1) and lo (d2) of gates
-      // 0-7; the mid of the same gates is in d1 of lane + 32
       const int c = 64 * cc + 16 * ct + m;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d1[i]), __float_as_uint(d1[i]), false, false);
         const int g = 4 * kg + i;
-        if (lane < 32 && g < G) part[(int64_t)g * (C + 1) + c] = (d1[i] + __uint_as_float(sw[1])) + d2[i];
+        if constexpr (GP == 8) {
+          // lanes 0-31 hold rows 4*(lane/16) + i: hi (d[0]) and lo (d[1]) of
+          // gates 0-7; the mid of the same gates is in d[0] of lane + 32
+          const auto sw =
+              __builtin_amdgcn_permlane32_swap(__float_as_uint(d[0][i]), __float_as_uint(d[0][i]), false, false);
+          if (lane < 32 && g < G) part[(int64_t)g * (C + 1) + c] = (d[0][i] + __uint_as_float(sw[1])) + d[1][i];
+        } else {
+          if (g < G) part[(int64_t)g * (C + 1) + c] = (d[0][i] + d[1][i]) + d[NA - 1][i];
+        }
       }
     }
     if (cc + 1 < nc) {
@@ -481,7 +510,7 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
   }
 }
 
-template <bool PROTO>
+template <int GP, bool PROTO>
 __global__ void __launch_bounds__(64 * kRmWaves)
 router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, const float* __restrict__ wpk,
                    const float* __restrict__ conf_weight, const float* __restrict__ usage_bias,
@@ -491,38 +520,45 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
                    int32_t* __restrict__ head_idx, float* __restrict__ head_score, float* __restrict__ stats,
                    float* __restrict__ ema_part) {
   PFA_CRITICAL_CHAIN_PRIORITY();
-  constexpr int GP = 8;
+  static_assert(GP == 8 || GP == 16, "MFMA router tables hold 8 or 16 gates");
+  constexpr int NT = rm_tables(GP, PROTO);
   typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
   typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
   extern __shared__ __align__(16) unsigned char rm_lds[];
-  uint16_t* tab = reinterpret_cast<uint16_t*>(rm_lds);  // [C/32][2][64 lanes][8]
+  uint16_t* tab = reinterpret_cast<uint16_t*>(rm_lds);  // [C/32][NT][64 lanes][8]
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c16 = lane & 15, g4 = lane >> 4;
 
-  // operand table from the packed f32 rows (wpk[c][0..8) = W, wpk[c][8..16) = P)
+  // operand tables from the packed f32 rows (wpk[c][0..GP) = W, wpk[c][GP..2GP) = P)
   for (int ch = tid; ch < C; ch += 64 * kRmWaves) {
     const float4* src = reinterpret_cast<const float4*>(wpk + (int64_t)ch * 2 * GP);
-    const float4 w0 = src[0], w1 = src[1];
-    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-    float pv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if constexpr (PROTO) {
-      const float4 p0 = src[2], p1 = src[3];
-      pv[0] = p0.x; pv[1] = p0.y; pv[2] = p0.z; pv[3] = p0.w;
-      pv[4] = p1.x; pv[5] = p1.y; pv[6] = p1.z; pv[7] = p1.w;
+    float wv[GP], pv[GP];
+#pragma unroll
+    for (int k = 0; k < GP / 4; ++k) {
+      const float4 w4 = src[k];
+      wv[4 * k] = w4.x; wv[4 * k + 1] = w4.y; wv[4 * k + 2] = w4.z; wv[4 * k + 3] = w4.w;
+      if constexpr (PROTO) {
+        const float4 p4 = src[GP / 4 + k];
+        pv[4 * k] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
+      }
     }
     const int st = 4 * (ch >> 7) + ((ch >> 3) & 3), g = (ch >> 5) & 3, j = ch & 7;
-    uint16_t* t0 = tab + ((int64_t)(2 * st) * 64 + 16 * g) * 8 + j;
-    uint16_t* t1 = t0 + 64 * 8;
+    uint16_t* base = tab + ((int64_t)st * NT * 64 + 16 * g) * 8 + j;
+    auto put = [&](int v, uint16_t val) { base[(v >> 4) * 64 * 8 + (v & 15) * 8] = val; };
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const uint16_t hi = f32_to_bf16(pv[r]);
-      const float r1 = pv[r] - bf16_to_f32(hi);
-      const uint16_t mid = f32_to_bf16(r1);
-      const uint16_t lo = f32_to_bf16(r1 - bf16_to_f32(mid));
-      t0[r * 8] = f32_to_bf16(wv[r]);
-      t0[(8 + r) * 8] = hi;
-      t1[r * 8] = mid;
-      t1[(8 + r) * 8] = lo;
+    for (int r = 0; r < GP; ++r) {
+      put(r, f32_to_bf16(wv[r]));
+      if constexpr (PROTO) {
+        const uint16_t hi = f32_to_bf16(pv[r]);
+        const float r1 = pv[r] - bf16_to_f32(hi);
+        const uint16_t mid = f32_to_bf16(r1);
+        const uint16_t lo = f32_to_bf16(r1 - bf16_to_f32(mid));
+        put(GP + r, hi);
+        put(2 * GP + r, mid);
+        put(3 * GP + r, lo);
+      } else if constexpr (GP == 8) {
+        put(GP + r, 0);  // unused rows 8-15 of the weight table
+      }
     }
   }
   __syncthreads();
@@ -537,12 +573,12 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
     t = t < n_tok ? t : n_tok - 1;
     xr[n] = x + t * C + 32 * g4;
   }
-  f32x4 acc0[4], acc1[4];
+  f32x4 acc[NT][4];
   float ss[4];
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
-    acc0[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc1[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][n] = f32x4{0.f, 0.f, 0.f, 0.f};
     ss[n] = 0.f;
   }
   const int nq = C / 128;
@@ -561,15 +597,16 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
     }
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      const uint16_t* tf = tab + ((int64_t)(2 * (4 * q + h)) * 64 + lane) * 8;
-      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(tf);
-      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(tf + 64 * 8);
+      const uint16_t* tf = tab + ((int64_t)(4 * q + h) * NT * 64 + lane) * 8;
+      bf16x8 a[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) a[t] = *reinterpret_cast<const bf16x8*>(tf + t * 64 * 8);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         bf16x8 b;
         __builtin_memcpy(&b, &cur[n][h], 16);
-        acc0[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, acc0[n], 0, 0, 0);
-        if constexpr (PROTO) acc1[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, acc1[n], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], b, acc[t][n], 0, 0, 0);
         const uint32_t w[4] = {cur[n][h].x, cur[n][h].y, cur[n][h].z, cur[n][h].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -591,7 +628,10 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
     ss[n] += __shfl_xor(ss[n], 16, 64);
     ss[n] += __shfl_xor(ss[n], 32, 64);
   }
-  // token-per-lane staging (reuses the table space once every wave is done)
+  // token-per-lane staging (reuses the table space once every wave is done).
+  // Row layout: [0, 16) table-0 rows (the logits, and with 8 gates the hi
+  // parts in 8-15), [16, 32) with 8 gates table 1 (mid, lo), with 16 gates
+  // the prototype dots (lo + mid) + hi, [32] the sum of squares.
   __syncthreads();
   float* ep = reinterpret_cast<float*>(rm_lds) + wid * 64 * kRmEpW;
 #pragma unroll
@@ -599,31 +639,38 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
     float* e = ep + (16 * n + c16) * kRmEpW;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      e[4 * g4 + i] = acc0[n][i];
-      e[16 + 4 * g4 + i] = PROTO ? acc1[n][i] : 0.f;
+      e[4 * g4 + i] = acc[0][n][i];
+      float pd = 0.f;
+      if constexpr (PROTO) {
+        if constexpr (GP == 8) pd = acc[NT - 1][n][i];
+        else pd = (acc[NT - 1][n][i] + acc[NT - 2][n][i]) + acc[1][n][i];
+      }
+      e[16 + 4 * g4 + i] = pd;
     }
     if (g4 == 0) e[32] = ss[n];
   }
   __syncthreads();
-  float acc[2 * GP + 1];
+  float acc_t[2 * GP + 1];
   {
     const float* e = ep + lane * kRmEpW;
 #pragma unroll
     for (int g = 0; g < GP; ++g) {
-      acc[g] = e[g];
-      acc[GP + g] = (e[24 + g] + e[16 + g]) + e[8 + g];
+      acc_t[g] = e[g];
+      if constexpr (GP == 8) acc_t[GP + g] = (e[24 + g] + e[16 + g]) + e[8 + g];
+      else acc_t[GP + g] = e[16 + g];
     }
-    acc[2 * GP] = e[32];
+    acc_t[2 * GP] = e[32];
   }
   const int64_t tok = tok0 + lane;
   const bool live = tok < n_tok;
   float gate[GP];
-  router_epilogue<PFA_BF16, GP, PROTO>(acc, tok, live, group, G, conf_weight, usage_bias, gate_to_head, H, topk,
+  router_epilogue<PFA_BF16, GP, PROTO>(acc_t, tok, live, group, G, conf_weight, usage_bias, gate_to_head, H, topk,
                                        proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim_out,
                                        blend_out, importance, head_idx, head_score,
                                        group < n_groups ? stats : nullptr, gate);
   if (ema_part != nullptr) {
-    float* gl = reinterpret_cast<float*>(rm_lds + rm_region_a(C)) + wid * 64 * GP;
+    __syncthreads();  // every wave has read its staged rows: the gate rows and x staging reuse those bytes
+    float* gl = reinterpret_cast<float*>(rm_lds) + wid * 64 * GP;
 #pragma unroll
     for (int g = 0; g < GP; ++g) gl[lane * GP + g] = (live && g < G) ? gate[g] : 0.f;
     __syncthreads();
@@ -634,9 +681,8 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
         for (int u = 0; u < 64; ++u) cs += gl[u * GP + lane];
         part[(int64_t)lane * (C + 1) + C] = cs;
       }
-      // the table / staging region is free again: each wave stages its x rows there
-      ema_accum_mfma(x, tok0, (int)min<int64_t>(64, n_tok - tok0), C, G, gl, part,
-                     reinterpret_cast<uint16_t*>(rm_lds + wid * kXsWave));
+      ema_accum_mfma<GP>(x, tok0, (int)min<int64_t>(64, n_tok - tok0), C, G, gl, part,
+                         reinterpret_cast<uint16_t*>(rm_lds + kRmWaves * 64 * GP * 4 + wid * kXsWave));
     }
   }
 }
@@ -909,13 +955,14 @@ static void launch_router_gp(const void* x, int64_t n_tok, int C, int G, const f
                              float* stats, float* ema, hipStream_t s) {
   using ET = typename Elem<DT>::T;
   unsigned blocks = (unsigned)((n_tok + kRouterTok - 1) / kRouterTok);
-  if constexpr (DT == PFA_BF16 && GP == 8) {
-    if (C % 128 == 0 && C <= 768) {
+  if constexpr (DT == PFA_BF16 && (GP == 8 || GP == 16)) {
+    // the operand tables stay within 64 KiB of LDS
+    if (C % 128 == 0 && C <= (GP == 8 ? 768 : 512)) {
       const unsigned mb = (blocks + kRmWaves - 1) / kRmWaves;
-      const size_t lds = (size_t)rm_region_a(C) + (size_t)kRmWaves * 64 * GP * sizeof(float);
-      router_mfma_kernel<PROTO><<<mb, 64 * kRmWaves, lds, s>>>((const uint16_t*)x, n_tok, C, G, wpk, cw, ub, g2h, H,
-                                                               topk, temp, thr, pb, boost, gp, sim, bl, imp, hi, hs,
-                                                               stats, ema);
+      const size_t lds = (size_t)rm_lds_bytes(C, GP, PROTO);
+      router_mfma_kernel<GP, PROTO><<<mb, 64 * kRmWaves, lds, s>>>((const uint16_t*)x, n_tok, C, G, wpk, cw, ub, g2h,
+                                                                   H, topk, temp, thr, pb, boost, gp, sim, bl, imp,
+                                                                   hi, hs, stats, ema);
       return;
     }
   }

@@ -381,7 +381,8 @@ def test_proto_ema_sums_vs_f64(dev, n_tok, C, G, dt):
 
 @pytest.mark.parametrize("n_tok,C,G,dt", [(300_000, 512, 8, torch.bfloat16), (5000, 1024, 12, torch.float32),
                                           (37, 64, 3, torch.float16), (1000, 200, 20, torch.bfloat16),
-                                          (3000, 512, 8, torch.bfloat16), (777, 384, 5, torch.bfloat16)])
+                                          (3000, 512, 8, torch.bfloat16), (777, 384, 5, torch.bfloat16),
+                                          (70_000, 512, 16, torch.bfloat16), (777, 384, 13, torch.bfloat16)])
 def test_router_fused_ema_sums_vs_f64(dev, n_tok, C, G, dt):
     """The EMA statistics the router accumulates in its own pass over x
     (ema_partial of pfa_router_topk, reduced with pfa_proto_partial_reduce)
@@ -991,17 +992,29 @@ def test_chunked_runner_small_gpu(dev):
     del seq
 
 
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_router_without_prototypes_vs_oracle(dev, dt):
+def _head_probs(gate: torch.Tensor, G: int, H: int) -> torch.Tensor:
+    """gate_probs @ onehot(gate_to_head), summed gate by gate in index order
+    (the order the router's epilogue adds them)."""
+    g2h = O.default_gate_map(G, H)
+    hp = torch.zeros(gate.size(0), H, dtype=torch.float32)
+    for gi in range(G):
+        hp[:, int(g2h[gi])] += gate[:, gi]
+    return hp
+
+
+@pytest.mark.parametrize("dt,G", [(torch.float32, 8), (torch.bfloat16, 8), (torch.bfloat16, 16),
+                                  (torch.bfloat16, 12)])
+def test_router_without_prototypes_vs_oracle(dev, dt, G):
     """use_proto == 0: gates are the router softmax alone; the packed table
     keeps its (C, 2*Gp) layout and only the weight columns are read.  3000
     tokens leave the last 64-token group partial (and, in bf16, the last
-    workgroup with a group past the end)."""
+    workgroup with a group past the end).  16 and 12 gates (two gates per
+    head on 8 heads) take the 16-gate MFMA tables."""
     from proteus_attention import _hip
     from proteus_attention.models.aspa import pack_router_weights
 
     g = torch.Generator().manual_seed(12)
-    n, C, G, H = 3000, 512, 8, 8
+    n, C, H = 3000, 512, 8
     x = torch.randn(n, C, generator=g).to(dt)
     w = (torch.randn(G, C, generator=g) * 0.05).to(dt)
     lib = _hip.lib()
@@ -1025,8 +1038,51 @@ def test_router_without_prototypes_vs_oracle(dev, dt):
 
         bad = (gate.cpu() != og).any(1)
         assert int((bad & ~torch.from_numpy(_at_boundary(x, w))).sum()) == 0
-    _, oidx = O.topk_lowest(gate.cpu(), 2)
+    _, oidx = O.topk_lowest(_head_probs(gate.cpu(), G, H), 2)
     assert torch.equal(hidx.cpu().long(), oidx)
+
+
+@pytest.mark.parametrize("n,C,G", [(3000, 512, 16), (4096, 384, 13), (1000, 128, 9), (130, 512, 16)])
+def test_router_sixteen_gates_bf16_vs_oracle(dev, n, C, G):
+    """bf16 router with 9-16 gates and prototypes (the 16-gate MFMA tables:
+    weights, and the hi / mid / lo parts of each prototype, in four 16-row
+    tables) against the oracle.  The first tokens are made close to a
+    prototype so that their prior blend is live.  Prototype similarities to
+    f32 accumulation order; gates bit for bit where the blend is zero (the
+    router softmax alone) except at a bf16 rounding boundary, within 1e-5
+    where it is live; head top-k exactly the lowest-index top-k of the
+    router's own head probabilities."""
+    from routing_parity import _at_boundary
+
+    H, topk = 8, 2
+    _say(f"router G={G} n={n} C={C} bf16")
+    g = torch.Generator().manual_seed(40 + G)
+    x = torch.randn(n, C, generator=g).to(torch.bfloat16)
+    w = (torch.randn(G, C, generator=g) * 0.05).to(torch.bfloat16)
+    protos = torch.randn(G, C, generator=g).to(torch.bfloat16)
+    near = min(4, G)
+    protos[:near] = (x[:near].float() + 0.3 * torch.randn(near, C, generator=g)).to(torch.bfloat16)
+    conf = torch.zeros(G, dtype=torch.bfloat16)
+    gate, sim, bl, imp, hidx, hsc = _run_router(dev, x, w, protos.float(), conf, torch.bfloat16, topk, H)
+    og, osim, obl, oimp = O.route_tokens(x, w, protos, conf, None, proto_temp=0.2, proto_threshold=0.25,
+                                         proto_blend=0.6, usage_boost=0.0)
+    og, osim, obl, oimp = og.reshape(n, G), osim.reshape(n), obl.reshape(n), oimp.reshape(n)
+    assert torch.allclose(sim, osim, atol=2e-6, rtol=0)
+    assert torch.allclose(bl, obl, atol=1e-5, rtol=0)
+    live = (bl > 0) | (obl > 0)
+    assert bool(live[:near].all())
+    bad = (gate != og).any(1) & ~live
+    assert int((bad & ~torch.from_numpy(_at_boundary(x, w))).sum()) == 0
+    assert torch.allclose(gate[live], og[live], atol=1e-5, rtol=0)
+    # importance (largest gate, blended with the similarity) wherever the
+    # gates agree; the rest are the bf16 rounding-boundary tokens
+    close = (gate - og).abs().amax(1) <= 1e-5
+    assert float(close.float().mean()) > 0.9
+    assert torch.allclose(imp[close], oimp[close], atol=1e-5, rtol=0)
+    hp = _head_probs(gate, G, H)
+    hv, oidx = O.topk_lowest(hp, topk)
+    assert torch.equal(hidx.long(), oidx)
+    assert torch.equal(hsc, hv)
 
 
 # ---------------------------------------------------------------------------
