@@ -247,6 +247,10 @@ int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T,
  *
  *   rows (N) int32 (tokens, each in [0, seq_len)), row_batch (N) int32 or
  *     NULL (batch 0)
+ *   n_rows_dev: NULL, or a device int32 holding the row count: then only
+ *     rows [0, min(N, *n_rows_dev)) are built and N is a capacity (the
+ *     packing summary's N, read on the device by a caller that does not
+ *     wait for it)
  *   local_w: effective window min(linear_window, L, local_cap), 0 = no
  *     local piece;  anchor_slots: min(anchor_cap, L, max(1, seq_len)),
  *     0 = no anchors (sparse_attn.py:413-429)
@@ -256,7 +260,7 @@ int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T,
  *   cand_out (N, L) int32 or int64 (cand_is_i64), len_out (N) int32/int64
  * ==================================================================== */
 int pfa_shortlist_build(const int32_t* rows, const int32_t* row_batch, int64_t N,
-                        int64_t seq_len, int L, int local_w, int anchor_stride,
+                        const int32_t* n_rows_dev, int64_t seq_len, int L, int local_w, int anchor_stride,
                         int anchor_slots, const int32_t* proto_sets,
                         int proto_k, int64_t proto_len, const int32_t* extra,
                         const int32_t* extra_len, int extra_width,
@@ -276,7 +280,8 @@ int pfa_shortlist_build(const int32_t* rows, const int32_t* row_batch, int64_t N
  *   addr(bh, t, d) = base + (bh / H) * s_b + (bh % H) * s_h + t * s_t + d
  * Row r (packed) belongs to compact head row_head[r] whose global index is
  * head_map[row_head[r]] (head_map NULL: identity) and queries token
- * token_idx[r].
+ * token_idx[r].  n_rows_dev (NULL, or a device int32 row count) bounds the
+ * rows to [0, min(N, *n_rows_dev)), as for pfa_shortlist_build.
  *
  * Key set of row r:
  *   cand != NULL : cand[r, 0 .. len[r])                (candidate branch)
@@ -297,7 +302,8 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                         int in_dtype, pfa_tensor4 out, int out_dtype, int H,
                         int64_t T, int D, const int32_t* token_idx,
                         const int32_t* row_head, const int32_t* head_map,
-                        int64_t N, const int32_t* cand, int64_t cand_stride,
+                        int64_t N, const int32_t* n_rows_dev,
+                        const int32_t* cand, int64_t cand_stride,
                         const int32_t* cand_len, const void* mask,
                         int mask_dtype, const int32_t* head_max_token,
                         float scale, const float* q_scale, const float* k_scale,

@@ -38,7 +38,8 @@ struct AttnArgs {
   const int32_t* token_idx;
   const int32_t* row_head;
   const int32_t* head_map;
-  int64_t N;
+  int64_t N;                // rows launched
+  const int32_t* n_rows;    // device row count bounding N, or null
   const int32_t* cand;
   int64_t cand_stride;
   const int32_t* cand_len;
@@ -51,6 +52,12 @@ struct AttnArgs {
   const float* v_scale;
   int mode;
 };
+
+// Rows to process: the launch size, bounded by the device row count when one
+// is given.
+__device__ __forceinline__ int64_t attn_rows(const AttnArgs& a) {
+  return a.n_rows ? min<int64_t>(a.N, (int64_t)a.n_rows[0]) : a.N;
+}
 
 // The grid is launched with a multiple of 8 workgroups, so this is a
 // bijection on [0, gridDim.x).
@@ -74,7 +81,7 @@ sparse_attn_row_kernel(AttnArgs a) {
   const int64_t nblk = gridDim.x;
   const int64_t lb = remap_block(blockIdx.x, nblk);
   const int64_t r = lb * kAttnWaves + (threadIdx.x >> 6);
-  if (r >= a.N) return;
+  if (r >= attn_rows(a)) return;
 
   const int64_t t = a.token_idx[r];
   const int hp = a.row_head[r];
@@ -192,7 +199,7 @@ sparse_attn_generic_kernel(AttnArgs a, int D) {
   float* accs = qs + D;                // D
   const int lane = threadIdx.x;
   const int64_t r = blockIdx.x;
-  if (r >= a.N) return;
+  if (r >= attn_rows(a)) return;
   const int64_t t = a.token_idx[r];
   const int hp = a.row_head[r];
   const int bh = a.head_map ? a.head_map[hp] : hp;
@@ -283,7 +290,8 @@ using namespace pfa;
 
 extern "C" int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, int in_dtype, pfa_tensor4 out,
                                    int out_dtype, int H, int64_t T, int D, const int32_t* token_idx,
-                                   const int32_t* row_head, const int32_t* head_map, int64_t N, const int32_t* cand,
+                                   const int32_t* row_head, const int32_t* head_map, int64_t N,
+                                   const int32_t* n_rows_dev, const int32_t* cand,
                                    int64_t cand_stride, const int32_t* cand_len, const void* mask, int mask_dtype,
                                    const int32_t* head_max_token, float scale, const float* q_scale,
                                    const float* k_scale, const float* v_scale, void* stream) {
@@ -301,6 +309,7 @@ extern "C" int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, 
   AttnArgs a;
   a.q = q; a.k = k; a.v = v; a.out = out;
   a.H = H; a.T = T; a.token_idx = token_idx; a.row_head = row_head; a.head_map = head_map; a.N = N;
+  a.n_rows = n_rows_dev;
   a.cand = cand; a.cand_stride = cand_stride; a.cand_len = cand_len; a.mask = mask; a.mask_dtype = mask_dtype;
   a.head_max = head_max_token; a.scale = scale; a.q_scale = q_scale; a.k_scale = k_scale; a.v_scale = v_scale;
   a.mode = cand ? kModeCand : (mask ? kModeMasked : kModeCausal);

@@ -526,7 +526,7 @@ struct Anchors {
 template <bool I64C, bool I64L>
 __global__ void __launch_bounds__(64 * kBuildWaves)
 shortlist_build_kernel(const int32_t* __restrict__ rows, const int32_t* __restrict__ row_batch, int64_t N,
-                       int64_t seq_len, int L, int local_w, int stride, int slots,
+                       const int32_t* __restrict__ n_rows_dev, int64_t seq_len, int L, int local_w, int stride, int slots,
                        const int32_t* __restrict__ proto_sets, int K, int64_t proto_len,
                        const int32_t* __restrict__ extra, const int32_t* __restrict__ extra_len, int ew,
                        int qcap, int bcap, int fcap, void* __restrict__ cand_out, void* __restrict__ len_out) {
@@ -535,7 +535,9 @@ shortlist_build_kernel(const int32_t* __restrict__ rows, const int32_t* __restri
   int32_t* Q = lds_i + wid * (qcap + bcap + fcap / 4);
   int32_t* Bb = Q + qcap;
   const int64_t r = (int64_t)blockIdx.x * kBuildWaves + wid;
-  if (r >= N) return;
+  // N is the launch size; a device row count, when given, bounds it
+  const int64_t n = n_rows_dev ? min<int64_t>(N, (int64_t)n_rows_dev[0]) : N;
+  if (r >= n) return;
   const int64_t t = rows[r];
   const int64_t b = row_batch ? row_batch[r] : 0;
 
@@ -892,7 +894,8 @@ extern "C" int pfa_proto_prefix_topk(const float* proto_scores, int B, int64_t T
   return PFA_OK;
 }
 
-extern "C" int pfa_shortlist_build(const int32_t* rows, const int32_t* row_batch, int64_t N, int64_t seq_len, int L,
+extern "C" int pfa_shortlist_build(const int32_t* rows, const int32_t* row_batch, int64_t N,
+                                   const int32_t* n_rows_dev, int64_t seq_len, int L,
                                    int local_w, int anchor_stride, int anchor_slots, const int32_t* proto_sets,
                                    int proto_k, int64_t proto_len, const int32_t* extra, const int32_t* extra_len,
                                    int extra_width, void* cand_out, int cand_is_i64, void* len_out, int len_is_i64,
@@ -922,7 +925,7 @@ extern "C" int pfa_shortlist_build(const int32_t* rows, const int32_t* row_batch
   hipStream_t s = as_stream(stream);
 #define PFA_BUILD(C64, L64)                                                                                   \
   shortlist_build_kernel<C64, L64><<<blocks, 64 * kBuildWaves, lds, s>>>(                                     \
-      rows, row_batch, N, seq_len, L, local_w, anchor_stride, anchor_slots, proto_sets, proto_sets ? proto_k : 0, \
+      rows, row_batch, N, n_rows_dev, seq_len, L, local_w, anchor_stride, anchor_slots, proto_sets, proto_sets ? proto_k : 0, \
       proto_len, extra, extra_len, extra ? extra_width : 0, qcap, bcap, fcap, cand_out, len_out)
   if (cand_is_i64) {
     if (len_is_i64) PFA_BUILD(true, true); else PFA_BUILD(true, false);

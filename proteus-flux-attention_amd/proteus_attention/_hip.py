@@ -110,10 +110,10 @@ _SIGNATURES = {
     "pfa_proto_prefix_workspace_size": ([_i32, _i64, _i32, ctypes.POINTER(_sz)], _i32),
     "pfa_proto_prefix_topk": ([_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_proto_prefix_blocks": ([_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp], _i32),
-    "pfa_shortlist_build": ([_vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i64, _vp, _vp, _i32,
+    "pfa_shortlist_build": ([_vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i64, _vp, _vp, _i32,
                              _vp, _i32, _vp, _i32, _vp], _i32),
     "pfa_sparse_attn_fwd": ([Tensor4, Tensor4, Tensor4, _i32, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp,
-                             _i64, _vp, _i64, _vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp], _i32),
+                             _i64, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp], _i32),
     "pfa_shortlist_attn_part_floats": ([], _i32),
     "pfa_shortlist_attn_fwd": ([Tensor4, Tensor4, Tensor4, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp, _i64,
                                 _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp, _vp,

@@ -201,7 +201,11 @@ def _shortlist_build_device(
     extra_len: Optional[torch.Tensor] = None,
     out_dtype: torch.dtype = torch.int32,
     len_dtype: torch.dtype = torch.int32,
+    n_rows_dev: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Candidate lists of the rows (pfa_shortlist_build).  With n_rows_dev
+    (a device int32 row count) only rows [0, min(N, count)) are built; the
+    rest of cand / lens is left unwritten."""
     lib = _hip.lib()
     device = rows_i32.device
     N = rows_i32.numel()
@@ -212,7 +216,7 @@ def _shortlist_build_device(
     ew = int(extra.size(1)) if extra is not None else 0
     with _hip.TIMER.timed("shortlist_build"):
         rc = lib.pfa_shortlist_build(
-        _hip.ptr(rows_i32), _hip.ptr(row_batch_i32), N, int(seq_len), int(L), int(local_w), int(anchor_stride),
+        _hip.ptr(rows_i32), _hip.ptr(row_batch_i32), N, _hip.ptr(n_rows_dev), int(seq_len), int(L), int(local_w), int(anchor_stride),
         int(slots), _hip.ptr(proto_sets), K, plen, _hip.ptr(extra), _hip.ptr(extra_len), ew, _hip.ptr(cand),
         1 if out_dtype == torch.int64 else 0, _hip.ptr(lens), 1 if len_dtype == torch.int64 else 0,
         _hip.stream_ptr(device))
@@ -363,13 +367,15 @@ def _attn_launch(
     scale: float,
     scales: Tuple[Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor]],
     device: torch.device,
+    n_rows_dev: Optional[torch.Tensor] = None,
 ) -> None:
     lib = _hip.lib()
     mask_tag = _hip.dtype_tag(mask.dtype) if mask is not None else 0
     with _hip.TIMER.timed("sparse_attn_fwd"):
         rc = lib.pfa_sparse_attn_fwd(
         q4, k4, v4, _hip.dtype_tag(in_dtype), out4, _hip.dtype_tag(out_dtype), int(H), int(T), int(D),
-        _hip.ptr(token_idx), _hip.ptr(row_head), _hip.ptr(head_map), int(token_idx.numel()), _hip.ptr(cand),
+        _hip.ptr(token_idx), _hip.ptr(row_head), _hip.ptr(head_map), int(token_idx.numel()), _hip.ptr(n_rows_dev),
+        _hip.ptr(cand),
         int(cand.stride(0)) if cand is not None else 0, _hip.ptr(cand_len), _hip.ptr(mask), mask_tag,
         _hip.ptr(head_max), float(scale), _hip.ptr(scales[0]), _hip.ptr(scales[1]), _hip.ptr(scales[2]),
         _hip.stream_ptr(device))

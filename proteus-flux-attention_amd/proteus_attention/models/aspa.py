@@ -836,6 +836,7 @@ class AdaptiveSparseAttention(nn.Module):
         if ratio >= 0.999 and self.token_keep_threshold <= 0.0:
             mask = torch.ones(B, T, dtype=torch.bool, device=device)
             self._last_token_mask = mask
+            self._token_keep_cap = T
             return mask
         guard = min(max(0, self.token_keep_guard), T)
         min_keep = max(min(max(0, self.token_keep_min), T), guard)
@@ -853,6 +854,9 @@ class AdaptiveSparseAttention(nn.Module):
         _hip.check(rc, "pfa_token_topk")
         mask = mask8.view(torch.bool)
         self._last_token_mask = mask
+        # kept tokens per batch row: without a threshold, the top `keep`
+        # plus at most `guard` leading tokens; with one, data dependent
+        self._token_keep_cap = min(T, keep + guard) if self.token_keep_threshold <= 0.0 else None
         return mask
 
     def _ema_active(self) -> bool:
@@ -1296,12 +1300,27 @@ class AdaptiveSparseAttention(nn.Module):
         # between the router and the attention launches).
         # The int8 mode needs P on the host as well: its per-head EMA buffers
         # have one entry per active head (aspa.py:1347-1357).
+        # With a token mask whose kept count is bounded on the host (no
+        # threshold: at most keep + guard tokens per batch row) and the
+        # materialised-candidate path, the rows are launched for that bound
+        # and the kernels read the exact count from the summary on the
+        # device (rows_dev); the structured path takes the exact count.
         use_quant = bool(self.quantize_sparse_int8 and not self.training)
-        need_summary = (density_threshold is not None or self.force_dense_when_full or token_mask is not None
-                        or use_quant)
+        need_summary = density_threshold is not None or self.force_dense_when_full or use_quant
+        rows_dev = None
+        plan_early = None
+        if token_mask is not None and not need_summary:
+            cap = self.__dict__.get("_token_keep_cap")
+            plan_early = self._shortlist_plan(B, T, alpha, qkv.dtype)
+            if cap is None or plan_early["structured"]:
+                need_summary = True
+            else:
+                rows_dev = summary[1:2]
         if need_summary:
             summ = summary.cpu()
             P, N, max_rows = int(summ[0]), int(summ[1]), int(summ[2])
+        elif rows_dev is not None:
+            P, N, max_rows = -1, B * cap * topk, -1
         else:
             P, N, max_rows = -1, B * T * topk, -1
         self._pending_summary = None if need_summary else summary
@@ -1323,7 +1342,7 @@ class AdaptiveSparseAttention(nn.Module):
             force_dense = False
 
         shortlist_path = not force_dense and not (P == 0 or N == 0 or (not need_summary and B * T == 0))
-        plan = self._shortlist_plan(B, T, alpha, qkv.dtype) if shortlist_path else None
+        plan = (plan_early or self._shortlist_plan(B, T, alpha, qkv.dtype)) if shortlist_path else None
         structured = plan is not None and plan["structured"]
         with torch.cuda.stream(fork_s):
             # the structured kernel rotates q rows as it loads them: only k is
@@ -1379,7 +1398,7 @@ class AdaptiveSparseAttention(nn.Module):
             heads = active_heads[:P] if P >= 0 else active_heads
             self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets, alpha, row_of, summary,
                                        plan=plan, q_rope=q_rope, streams=None if join_early else (main_s, fork_s),
-                                       before_join=None if join_early else ema)
+                                       before_join=None if join_early else ema, rows_dev=rows_dev)
             backend_info = self._last_shortlist_backend_info or get_last_backend_info()
             state = {
                 "mode": mode_label, "backend": str(backend_info.get("name", "shortlist")),
@@ -1457,7 +1476,7 @@ class AdaptiveSparseAttention(nn.Module):
 
     def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha, row_of,
                               summary, plan: Optional[Dict[str, Any]] = None, q_rope=None, streams=None,
-                              before_join=None) -> None:
+                              before_join=None, rows_dev: Optional[torch.Tensor] = None) -> None:
         """Candidate attention (aspa.py:1175-1310).
 
         When no row can be truncated to L, bf16 with D=64 and no int8 path,
@@ -1474,7 +1493,10 @@ class AdaptiveSparseAttention(nn.Module):
         paths are entered with the fork stream already joined.  The
         prototype tables are queued before the anchor pass so that, in a
         captured graph, they follow the packing on its queue instead of
-        starting on another one."""
+        starting on another one.
+
+        rows_dev (materialised path only): a device int32 row count; the
+        token_idx / row_head given are then a capacity, valid up to it."""
         H, D = self.h_total, self.d_head
         device = qkv.device
         if plan is None:
@@ -1484,6 +1506,8 @@ class AdaptiveSparseAttention(nn.Module):
         if q_rope is not None and not structured:
             raise RuntimeError("q rows left unrotated for a path that does not rotate them")
         q5 = qkv.view(B, T, 3, H, D)
+        if structured and rows_dev is not None:
+            raise RuntimeError("the structured shortlist path takes the exact row count")
         if structured:
             qkv_scales = None
             if use_quant:
@@ -1544,8 +1568,13 @@ class AdaptiveSparseAttention(nn.Module):
         row_batch = None
         if K > 0:
             sets = _sa._proto_prefix_sets(self._last_token_similarity, K)
-            row_batch = (heads.index_select(0, row_head) // H).to(torch.int32) if B > 1 else None
-        cand, lens = _sa._shortlist_build_device(token_idx, row_batch, T, L, local_w, stride, slots, sets)
+            if B > 1:
+                # rows past a device row count hold arbitrary values: clamp
+                # them into range (the builder does not read those rows)
+                rh = row_head.clamp(0, heads.numel() - 1) if rows_dev is not None else row_head
+                row_batch = (heads.index_select(0, rh) // H).to(torch.int32)
+        cand, lens = _sa._shortlist_build_device(token_idx, row_batch, T, L, local_w, stride, slots, sets,
+                                                 n_rows_dev=rows_dev)
         self._last_shortlist_lengths = lens
         out4 = _hip.tensor4(attn.view(B, T, H, D), H, "bthd")
         if use_quant:
@@ -1557,11 +1586,12 @@ class AdaptiveSparseAttention(nn.Module):
             _sa._attn_launch(_hip.tensor4(q8[:, :, 0], H, "bthd"), _hip.tensor4(q8[:, :, 1], H, "bthd"),
                              _hip.tensor4(q8[:, :, 2], H, "bthd"), torch.int8, out4, qkv.dtype, H, T, D, token_idx,
                              row_head, heads, cand, lens, None, None, 1.0 / math.sqrt(D),
-                             (scales[0], scales[1], scales[2]), device)
+                             (scales[0], scales[1], scales[2]), device, n_rows_dev=rows_dev)
         else:
             _sa._attn_launch(_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
                              _hip.tensor4(q5[:, :, 2], H, "bthd"), qkv.dtype, out4, qkv.dtype, H, T, D, token_idx,
-                             row_head, heads, cand, lens, None, None, 1.0 / math.sqrt(D), (None, None, None), device)
+                             row_head, heads, cand, lens, None, None, 1.0 / math.sqrt(D), (None, None, None), device,
+                             n_rows_dev=rows_dev)
         _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
                         quantized=use_quant, candidates=True, structured=False)
         self._last_shortlist_backend_info = get_last_backend_info()
@@ -1653,6 +1683,10 @@ class AdaptiveSparseAttention(nn.Module):
                 if "active_head_indices" in st:
                     st["active_head_indices"] = st["active_head_indices"][:P_].to(torch.int64)
                     st["row_offsets"] = st["row_offsets"][:P_ + 1]
+                if "token_idx" in st:
+                    # launched for a row capacity when the count stayed on the device
+                    st["token_idx"] = st["token_idx"][:N_]
+                    st["head_idx"] = st["head_idx"][:N_]
             hs = {
                 "top_k": int(topk),
                 "mean_gate_prob": float(score_sum / max(1.0, float(N_))),

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_library_reports_argument_errors_without_gpu():
     lib = _hip.load_library()
-    rc = lib.pfa_shortlist_build(None, None, 4, 0, 0, 0, 0, 0, None, 0, 0, None, None, 0, None, 0, None, 0, None)
+    rc = lib.pfa_shortlist_build(None, None, 4, None, 0, 0, 0, 0, 0, None, 0, 0, None, None, 0, None, 0, None, 0, None)
     assert rc == -1
     assert b"bad sizes" in lib.pfa_last_error_string()
     size = ctypes.c_size_t(0)
