@@ -32,6 +32,7 @@ training-mode attention dropout.
 """
 from __future__ import annotations
 
+import gc
 import math
 import time
 import warnings
@@ -1040,12 +1041,30 @@ class AdaptiveSparseAttention(nn.Module):
         return ent["x"]
 
     def _graph_eligible(self, x: torch.Tensor) -> bool:
-        return (x.dim() == 3 and not self.training and not torch.is_grad_enabled()
-                and self._dense_threshold is None and not self.force_dense_when_full and not self.token_sparse
-                and self.router_top_p <= 0.0 and not self.linear_mem_budget_mb
-                and self.linear_latency_budget_ms is None and not self.quantize_sparse_int8
+        """No host decision of the forward depends on device results: no
+        density threshold, memory or latency budget, int8 mode; the nucleus
+        head count only where the head count is already at its floor (its
+        readback is skipped there); token masks only without a keep
+        threshold (the kept count is bounded on the host) and on the
+        materialised-candidate path, which reads the exact row count on the
+        device."""
+        if not (x.dim() == 3 and not self.training and not torch.is_grad_enabled()
+                and self._dense_threshold is None and not self.force_dense_when_full
+                and not self.linear_mem_budget_mb and self.linear_latency_budget_ms is None
+                and not self.quantize_sparse_int8
                 and not (self.small_seq_dense and x.shape[1] <= self.small_seq_dense)
-                and x.dtype in (torch.float32, torch.bfloat16, torch.float16))
+                and x.dtype in (torch.float32, torch.bfloat16, torch.float16)):
+            return False
+        B, T = int(x.shape[0]), int(x.shape[1])
+        if self.router_top_p > 0.0 and self._choose_active_k(T) > self.h_active_min:
+            return False
+        if self.token_sparse:
+            if self.token_keep_threshold > 0.0:
+                return False
+            sims = bool(self.proto_enabled and self.routing_prototypes is not None)
+            if self._shortlist_plan(B, T, self._compute_cvt_alpha(T), x.dtype, sims=sims)["structured"]:
+                return False
+        return True
 
     _GRAPH_STATE = ("_last_batch_size", "_current_alpha", "_token_keep_ratio_runtime", "_last_target_k",
                     "_last_gate_probs", "_last_token_similarity", "_last_token_blend", "_last_token_importance",
@@ -1055,15 +1074,19 @@ class AdaptiveSparseAttention(nn.Module):
 
     def _graph_key(self, x: torch.Tensor):
         T = int(x.shape[1])
-        return (tuple(x.shape), tuple(x.stride()), x.dtype, x.device, float(self._compute_cvt_alpha(T)),
+        # the graph reads its own contiguous input buffer, into which any
+        # layout of x is copied: the key does not depend on x's strides
+        return (tuple(x.shape), x.dtype, x.device, float(self._compute_cvt_alpha(T)),
                 int(self.linear_L), float(self._linear_L_scale_runtime), self._shortlist_alpha_override,
-                str(self.mode_setting))
+                str(self.mode_setting), int(self._choose_active_k(T)),
+                (float(self.token_keep_ratio_base), int(self.token_keep_min), int(self.token_keep_guard),
+                 str(self.linear_token_keep_schedule)) if self.token_sparse else None)
 
     def _capture_graph(self, x: torch.Tensor, key) -> dict:
         self._resolve_stats()
         device = x.device
         bufs = {n: b.detach().clone() for n, b in self.named_buffers()}
-        xs = x.detach().clone()
+        xs = x.detach().clone(memory_format=torch.contiguous_format)
         timer_on = _hip.TIMER.enabled
         _hip.TIMER.enabled = False
         try:
@@ -1085,9 +1108,20 @@ class AdaptiveSparseAttention(nn.Module):
             # are held by the graph: a later rebuild of a cache must not free
             # memory a replay still reads
             self._capture_keep = []
-            with torch.cuda.graph(graph, pool=self._hip_graph_pool):
-                attn, stats_args, label = self._forward_impl(xs, capture=True)
-                y_static = self.dropout(self.proj(attn)) if self._hip_graph_static_output else None
+            # no garbage collection inside the capture: a dead object that
+            # owns device resources (pinned host memory, events) would be
+            # freed while the stream captures, which is not allowed; dead
+            # cycles are collected first
+            gc.collect()
+            gc_was_on = gc.isenabled()
+            gc.disable()
+            try:
+                with torch.cuda.graph(graph, pool=self._hip_graph_pool):
+                    attn, stats_args, label = self._forward_impl(xs, capture=True)
+                    y_static = self.dropout(self.proj(attn)) if self._hip_graph_static_output else None
+            finally:
+                if gc_was_on:
+                    gc.enable()
             keep = self._capture_keep
         finally:
             _hip.TIMER.enabled = timer_on
@@ -1440,19 +1474,24 @@ class AdaptiveSparseAttention(nn.Module):
                 self.adjust_linear_L_scale(self.linear_latency_growth)
         return y
 
-    def _shortlist_plan(self, B: int, T: int, alpha: float, dtype: torch.dtype) -> Dict[str, Any]:
+    def _shortlist_plan(self, B: int, T: int, alpha: float, dtype: torch.dtype,
+                        sims: Optional[bool] = None) -> Dict[str, Any]:
         """Shortlist sizes of this forward (aspa.py:1175-1210) and whether the
-        structured kernel serves it (bf16, D=64, no row truncated)."""
+        structured kernel serves it (bf16, D=64, no row truncated).  `sims`:
+        whether the router gives prototype similarities (default: whether
+        this forward's router gave them)."""
         D = self.d_head
+        if sims is None:
+            sims = self._last_token_similarity is not None
         runtime = self._prepare_linear_runtime(T, B, alpha)
         L = int(runtime["effective_L"])
         stride = int(runtime["anchor_stride"])
         local_w, slots, proto_cap_val = _sa._resolve_caps(
             L, runtime["window"], stride, self.linear_use_local, self.linear_use_anchors,
-            self.linear_use_proto and self._last_token_similarity is not None, T, runtime["local_cap"],
+            self.linear_use_proto and sims, T, runtime["local_cap"],
             runtime["anchor_cap"], runtime["proto_cap"])
         K = 0
-        if self.linear_use_proto and self._last_token_similarity is not None and proto_cap_val > 0:
+        if self.linear_use_proto and sims and proto_cap_val > 0:
             K = min(L, proto_cap_val, T)
         use_quant = bool(self.quantize_sparse_int8 and not self.training)
         anchors = stride > 0 and slots > 0

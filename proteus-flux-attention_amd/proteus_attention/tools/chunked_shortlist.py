@@ -204,6 +204,11 @@ class ChunkedShortlistConfig:
     # final_causal (tools/final_pass.py).
     final_mode: Literal["reduced", "all_queries"] = "reduced"
     final_causal: bool = True
+    # replay the chunk model's forward from a captured HIP graph (one
+    # capture per chunk length, during the warm-up forward) where the
+    # forward has no host decision on device results; otherwise it runs
+    # eagerly
+    chunk_graph: bool = True
 
     def validate(self) -> None:
         """Reference chunked_shortlist.py:337-366."""
@@ -455,6 +460,9 @@ class ChunkedShortlistRunner:
                                                                                          dtype=base_dtype).eval()
             chunk_model.use_sdpa = False
             chunk_model.set_shortlist_alpha(float(cfg.shortlist_alpha))
+            if cfg.chunk_graph and device.type == "cuda":
+                # the forward's output is the graph's own buffer (unused here)
+                chunk_model.enable_hip_graph(True, static_output=True)
             direct = st["mode"] == "device"
             chunks = list(_chunk_iter(cfg.seq_len, cfg.chunk_len))
             final_model = None
@@ -463,8 +471,17 @@ class ChunkedShortlistRunner:
                 final_model = self._final_model(cfg.buffer_tokens, base_dtype)
                 all_q = AllQueryFinalPass(final_model, cfg.seq_len, device, base_dtype, causal=cfg.final_causal)
             self.last_final_pass = all_q
+            self.last_chunk_model = chunk_model
             with torch.inference_mode():
                 chunk_model(torch.randn(1, cfg.chunk_len, cfg.d_model, device=device, dtype=base_dtype))
+                tail = cfg.seq_len % cfg.chunk_len
+                if tail and cfg.seq_len > cfg.chunk_len and chunk_model._hip_graph_enabled:
+                    # capture the short last chunk's graph now, not inside the
+                    # chunk loop (capturing restores the module state: no
+                    # prototype update)
+                    xt = torch.zeros(1, tail, cfg.d_model, device=device, dtype=base_dtype)
+                    if chunk_model._graph_eligible(xt):
+                        chunk_model.hip_graph_input(xt)
             if device.type == "cuda":
                 torch.cuda.synchronize()
             summaries: List[ChunkSummary] = []
@@ -625,8 +642,13 @@ class ChunkedShortlistRunner:
                                           metrics=metrics, chunks=summaries, final_output=final_out,
                                           final_stats=final_stats, backend_info=backend_info)
         finally:
-            if st.get("stager") is not None:
-                st["stager"].close()
+            # the stager refers back to st: take it out so that neither
+            # outlives this call in a reference cycle (holding pinned memory
+            # and events until a garbage collection)
+            stager_ = st.pop("stager", None)
+            if stager_ is not None:
+                stager_.close()
+                stager_.st = None
             if st.get("memmap") is not None:
                 st["memmap"].flush()
             if st.get("path") is not None:

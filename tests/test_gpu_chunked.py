@@ -252,3 +252,35 @@ def test_chunked_runner_norm_fallback(dev, monkeypatch, storage):
         all_i.append(ei)
     ki, ks = O.finalise_indices(torch.cat(all_s), torch.cat(all_i), T)
     assert torch.equal(res.keep_indices.cpu(), ki) and torch.equal(res.keep_scores.cpu(), ks)
+
+
+@pytest.mark.parametrize("storage", ["device", "cpu"])
+def test_chunked_runner_graph_matches_eager(dev, storage):
+    """The chunk model replayed from a captured HIP graph selects exactly
+    what the eager chunk model selects, chunk by chunk, and gives the same
+    shortlist and final output.  60,000 tokens in chunks of 24,576: the two
+    full chunks replay the graph (materialised candidates); the 10,848-token
+    last chunk takes the structured path, which reads its row count, and
+    runs eagerly between them and the selection."""
+    from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
+
+    T, C, chunk = 60000, 512, 24576
+    print(f"chunked runner graph vs eager storage={storage}", flush=True)
+    x = torch.randn(1, T, C, generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    kw = dict(seq_len=T, d_model=C, chunk_len=chunk, buffer_tokens=600, per_chunk_budget=256, device=dev, heads=8,
+              nucleus_top_p=1.0, final_mode="all_queries", storage="cpu")
+    src = x.to(dev) if storage == "device" else x
+    res, graphs = {}, {}
+    for graph in (False, True):
+        torch.manual_seed(5)
+        runner = ChunkedShortlistRunner(ChunkedShortlistConfig(chunk_graph=graph, **kw))
+        res[graph] = runner.run(src)
+        graphs[graph] = len(runner.last_chunk_model._hip_graphs)
+    assert graphs[True] == 1 and graphs[False] == 0
+    assert res[True].metrics.storage_mode == storage
+    for a, b in zip(res[False].chunks, res[True].chunks):
+        assert a.promoted == b.promoted and a.scores == b.scores, f"chunk {a.index}"
+    assert torch.equal(res[False].keep_indices, res[True].keep_indices)
+    assert torch.equal(res[False].keep_scores, res[True].keep_scores)
+    assert torch.equal(res[False].final_output.cpu(), res[True].final_output.cpu())
+

@@ -922,6 +922,64 @@ def test_module_hip_graph_static_output_matches_eager(dev):
     m.enable_hip_graph(False)
 
 
+def test_module_hip_graph_token_mask_matches_eager(dev):
+    """Graph mode with a token mask (the chunked pipeline's chunk model:
+    token top-k without a threshold, materialised candidates, top-p routing
+    at the head-count floor): the forward reads no count back, so it is
+    captured; every replay's importance, mask, attention output, prototype
+    EMA and returned buffer equal the eager forward's, and the deferred
+    telemetry trims the packed rows to the device count.  At T = 24,576 the
+    window plus anchors exceed L = 256, so the candidates are materialised
+    (shorter chunks take the structured path, which reads the exact count
+    and stays eager)."""
+    from proteus_attention.models.aspa import AdaptiveSparseAttention
+    from proteus_attention.tools.chunked_shortlist import _build_model_config
+
+    T, C, H = 24576, 512, 8
+    _say(f"hip graph token mask vs eager, T={T}")
+    torch.manual_seed(0)
+    m = AdaptiveSparseAttention(_build_model_config(T, C, heads=H, sparse_ratio=0.05, shortlist_alpha=0.0,
+                                                    router_top_p=1.0)).to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(1, T, C, generator=g).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        assert m._graph_eligible(x)
+        assert not m._graph_eligible(x[:, :4096])  # structured: eager
+    init = {n: b.detach().clone() for n, b in m.named_buffers()}
+    xs = [x, (x * 0.5).contiguous(), torch.roll(x, 11, dims=1).contiguous(), x]
+
+    def run(graph: bool):
+        for n, b in m.named_buffers():
+            b.copy_(init[n])
+        m.enable_hip_graph(graph, static_output=graph)
+        outs = []
+        with torch.no_grad():
+            for xi in xs:
+                y = m(xi).float().cpu()
+                imp = m._last_token_importance.float().cpu().clone()
+                mask = m._last_token_mask.cpu().clone()
+                a = m.last_head_consensus.float().cpu().clone()
+                st = m._last_sparse_state
+                rows = (int(st["token_idx"].numel()), float(m.last_head_stats["mean_active_per_token"]),
+                        int(m._last_target_k))
+                junk = torch.randn(1 << 20, device=dev).sum()  # eager work between replays
+                torch.cuda.synchronize()
+                outs.append((y, imp, mask, a, m.routing_prototypes.float().cpu().clone(), rows, float(junk)))
+        return outs
+
+    eager = run(False)
+    graph = run(True)
+    assert len(m._hip_graphs) == 1
+    assert m._last_sparse_state["mode"] == "shortlist"
+    for i, (e, gr) in enumerate(zip(eager, graph)):
+        for j, what in enumerate(("output", "importance", "mask", "attention", "prototype EMA")):
+            assert torch.equal(e[j], gr[j]), f"forward {i}: {what} differs"
+        assert e[5] == gr[5], f"forward {i}: packed rows {e[5]} vs {gr[5]}"
+        kept = int(e[2].sum())
+        assert e[5][0] == kept * e[5][2]  # every kept token has its top-k heads
+    m.enable_hip_graph(False)
+
+
 def test_module_dense_paths_vs_oracle(dev):
     """subquad mode (force-dense) and the small-sequence dense fast path
     equal dense causal attention of the projected q/k/v."""
