@@ -5,9 +5,8 @@
 // one symmetric scale per (head, key row).
 //
 // Every key is read by every 128-query tile of its head (8,192 tiles at
-// T = 2^20), so the shortlist is dequantised once per call, k8 * k_scale ->
-// bf16 (the bits the tile conversion would give), into a working copy in
-// the workspace (16 MB at H = 8, S = 8,192); the attention then streams
+// T = 2^20), so the shortlist is dequantised once per call, into bf16
+// working copies in the workspace (16 MB at H = 8, S = 8,192); the attention then streams
 // 64-key tiles of it by LDS DMA into the swizzled 128-byte-row layout of the
 // bf16 attention kernels (the V^T operand from the LDS transpose read), and
 // S = Q K^T and O += P V run on v_mfma_f32_16x16x32_bf16 with an online
@@ -21,6 +20,18 @@
 // run unmasked; the at most few keys in [rng.x, rng.y) are masked per
 // (query, key).  Block b handles head b % H, so on 8 XCDs each XCD's L2
 // holds one head's K/V; tiles run heaviest first.
+//
+// Scores are in log2 units: the bf16 K copy carries the factor
+// scale * log2(e) (one rounding, of k8 * k_scale * scale * log2(e), where the
+// plain copy rounds k8 * k_scale).  An unmasked tile first runs without a
+// row maximum: the QK^T accumulators start at -m (m: the running reference
+// point of the row), so P = exp2(S) directly.  The tile is kept when every
+// lane's sum of its 16 P values lies in [2^-60, 2^20] (or the row already
+// has mass): no P overflows and none of the row's first mass underflows.
+// Otherwise the wave recomputes the tile on the exact path (tile maximum,
+// rescale of the accumulators when the maximum rises).  Either way
+// out = acc / l does not depend on m; only the bf16 rounding points of P
+// differ from a softmax taken at the exact maximum.
 #include "pfa_common.h"
 
 namespace pfa {
@@ -31,7 +42,9 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kQ = 32 * kWaves;  // queries per workgroup
 constexpr int kTile = kSwzKeys;  // keys per tile
 constexpr int kD = 64;
-constexpr float kRescaleLog2 = 0.0f;  // rescale only when some row's max rises
+constexpr float kRescaleLog2 = 0.0f;  // exact path: rescale when some row's max rises
+constexpr float kFastHi = 0x1p20f;     // fast path: largest lane sum of P kept
+constexpr float kFastLo = 0x1p-60f;    // fast path: smallest first mass of a row kept
 
 #ifndef PFA_FIN_STAGES
 #define PFA_FIN_STAGES 2
@@ -49,7 +62,6 @@ struct Args {
   const int2* rng;
   int H, S, causal, nqt;
   int64_t T;
-  float scale_log2;
 };
 
 struct St {
@@ -61,9 +73,10 @@ __device__ __forceinline__ float i8f(uint32_t w, int e) { return (float)(int)(in
 
 // bf16(x8 * scale) for the (H*S, 64) rows of K and V: thread -> row idx/4,
 // elements 16*(idx%4) .. +15.
+// K rows carry the factor kmul = scale * log2(e): bf16(x8 * (k_scale * kmul)).
 __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__ k8, const int8_t* __restrict__ v8,
                                                       const float* __restrict__ ks, const float* __restrict__ vs,
-                                                      int64_t rows, uint16_t* __restrict__ kb,
+                                                      int64_t rows, float kmul, uint16_t* __restrict__ kb,
                                                       uint16_t* __restrict__ vb) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= rows * 4) return;
@@ -71,7 +84,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__
   const int qd = (int)(idx & 3);
   const uint4 k = *reinterpret_cast<const uint4*>(k8 + row * kD + 16 * qd);
   const uint4 v = *reinterpret_cast<const uint4*>(v8 + row * kD + 16 * qd);
-  const float kscale = ks[row], vscale = vs[row];
+  const float kscale = ks[row] * kmul, vscale = vs[row];
   const uint32_t kw4[4] = {k.x, k.y, k.z, k.w};
   const uint32_t vw4[4] = {v.x, v.y, v.z, v.w};
   __bf16 kd[16], vd[16];
@@ -91,10 +104,42 @@ __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__
   vo[1] = vw[1];
 }
 
-// kpos: the shortlist's positions (global; read only in masked tiles)
+// O += P V for the tile (P rounded to bf16).
+__device__ __forceinline__ void pv_accumulate(const float (&s)[2][16], const SwzTile& tl, St (&st)[2]) {
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    bf16x8_t pb[2];
+#pragma unroll
+    for (int gr = 0; gr < 2; ++gr) {
+      __bf16 pv[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pv[i] = (__bf16)s[gr][8 * kc + i];
+        pv[4 + i] = (__bf16)s[gr][8 * kc + 4 + i];
+      }
+      __builtin_memcpy(&pb[gr], pv, 16);
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      // V^T: lane (dim 16db + lane%16, g) holds keys 32kc + 4g + (0..3) and
+      // 32kc + 16 + 4g + (0..3), matching pb
+      const i16x4_t lo = ds_tr4(tl.vtr(kc, 0, db));
+      const i16x4_t hi = ds_tr4(tl.vtr(kc, 1, db));
+      bf16x8_t va;
+      __builtin_memcpy(&va, &lo, 8);
+      __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
+#pragma unroll
+      for (int gr = 0; gr < 2; ++gr)
+        st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gr], st[gr].acc[db], 0, 0, 0);
+    }
+  }
+}
+
+// Exact path: the tile's row maxima, rescaling when one rises.  kpos: the
+// shortlist's positions (global; read only in masked tiles).
 template <bool MASKED>
 __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& tl, const int32_t* kpos, int key0,
-                                     int S, int causal, const int (&tq)[2], float sl2, St (&st)[2]) {
+                                     int S, int causal, const int (&tq)[2], St (&st)[2]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   float s[2][16];
 #pragma unroll
@@ -126,8 +171,7 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& 
     float tmax = s[gr][0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[gr][i]);
-    tmax = max_over_rows4(tmax);
-    const float tm = tmax * sl2;
+    const float tm = max_over_rows4(tmax);
     if (__ballot(tm > st[gr].m + kRescaleLog2) != 0) {
       const float mn = fmaxf(st[gr].m, tm);
       const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(st[gr].m - mn);  // m == -inf -> 0
@@ -142,38 +186,56 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& 
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      s[gr][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[gr][i], sl2, -moff));  // -inf -> 0
+      s[gr][i] = __builtin_amdgcn_exp2f(s[gr][i] - moff);  // -inf -> 0
       psum += s[gr][i];
     }
     st[gr].l += psum;
   }
+  pv_accumulate(s, tl, st);
+}
+
+// Fast path of an unmasked tile: no row maximum.  Returns false, with the
+// state untouched, when some lane's P fall outside the kept range (the
+// caller then runs the exact path on the same tile).
+__device__ __forceinline__ bool tile_fast(const bf16x8_t (&qf)[2][2], const SwzTile& tl, St (&st)[2]) {
+  // the QK^T accumulators start at -m (0 while m is -inf)
+  f32x4_t negm[2];
 #pragma unroll
-  for (int kc = 0; kc < 2; ++kc) {
-    bf16x8_t pb[2];
+  for (int gr = 0; gr < 2; ++gr) {
+    const float nm = st[gr].m == -INFINITY ? 0.f : -st[gr].m;
+    negm[gr] = f32x4_t{nm, nm, nm, nm};
+  }
+  float s[2][16];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 0));
+    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 1));
 #pragma unroll
     for (int gr = 0; gr < 2; ++gr) {
-      __bf16 pv[8];
+      f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[gr][0], negm[gr], 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[gr][1], c, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pv[i] = (__bf16)s[gr][8 * kc + i];
-        pv[4 + i] = (__bf16)s[gr][8 * kc + 4 + i];
-      }
-      __builtin_memcpy(&pb[gr], pv, 16);
-    }
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      // V^T: lane (dim 16db + lane%16, g) holds keys 32kc + 4g + (0..3) and
-      // 32kc + 16 + 4g + (0..3), matching pb
-      const i16x4_t lo = ds_tr4(tl.vtr(kc, 0, db));
-      const i16x4_t hi = ds_tr4(tl.vtr(kc, 1, db));
-      bf16x8_t va;
-      __builtin_memcpy(&va, &lo, 8);
-      __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
-#pragma unroll
-      for (int gr = 0; gr < 2; ++gr)
-        st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gr], st[gr].acc[db], 0, 0, 0);
+      for (int i = 0; i < 4; ++i) s[gr][4 * kb + i] = __builtin_amdgcn_exp2f(c[i]);
     }
   }
+  float psum[2];
+  bool bad = false;
+#pragma unroll
+  for (int gr = 0; gr < 2; ++gr) {
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a += s[gr][i];
+    psum[gr] = a;
+    bad = bad || !(a <= kFastHi) || (a < kFastLo && st[gr].l == 0.f);
+  }
+  if (__ballot(bad) != 0) return false;
+#pragma unroll
+  for (int gr = 0; gr < 2; ++gr) {
+    st[gr].l += psum[gr];
+    if (st[gr].m == -INFINITY) st[gr].m = 0.f;  // the reference point 0 was used
+  }
+  pv_accumulate(s, tl, st);
+  return true;
 }
 
 __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restrict__ kpos, int S, int64_t T,
@@ -271,8 +333,11 @@ final_attn_kernel(Args a) {
     if (i + kStages - 1 < ntile) request(i + kStages - 1);
     const int key0 = kTile * i;
     const SwzTile tl{ring[i % kStages], L};
-    if (key0 + kTile <= rg.x) tile<false>(qf, tl, a.kpos, key0, a.S, a.causal, tq, a.scale_log2, st);
-    else tile<true>(qf, tl, a.kpos, key0, a.S, a.causal, tq, a.scale_log2, st);
+    if (key0 + kTile <= rg.x) {
+      if (!tile_fast(qf, tl, st)) tile<false>(qf, tl, a.kpos, key0, a.S, a.causal, tq, st);
+    } else {
+      tile<true>(qf, tl, a.kpos, key0, a.S, a.causal, tq, st);
+    }
   }
   uint16_t* oh = a.out + (int64_t)h * a.o_sh;
 #pragma unroll
@@ -338,7 +403,8 @@ extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, i
   uint16_t* kbf = (uint16_t*)((char*)workspace + fin_rng_bytes(T));
   uint16_t* vbf = (uint16_t*)((char*)kbf + fin_copy_bytes(H, S));
   const int64_t rows = (int64_t)H * S;
-  fin::dequant_kernel<<<(unsigned)((rows * 4 + 255) / 256), 256, 0, s>>>(k8, v8, k_scale, v_scale, rows, kbf, vbf);
+  fin::dequant_kernel<<<(unsigned)((rows * 4 + 255) / 256), 256, 0, s>>>(k8, v8, k_scale, v_scale, rows,
+                                                                       scale * 1.4426950408889634f, kbf, vbf);
   PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/dequant");
   fin::key_ranges_kernel<<<(unsigned)((nqt + 255) / 256), 256, 0, s>>>(key_pos, S, T, nqt, causal ? 1 : 0, rng);
   PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/ranges");
@@ -358,7 +424,6 @@ extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, i
   a.causal = causal ? 1 : 0;
   a.nqt = nqt;
   a.T = T;
-  a.scale_log2 = scale * 1.4426950408889634f;
   const int64_t blocks = (int64_t)nqt * H;
   PFA_CHECK_ARG(blocks < INT32_MAX, "pfa_int8_kv_attn_fwd: too many query tiles");
   fin::final_attn_kernel<<<(unsigned)blocks, fin::kThreads, 0, s>>>(a);
