@@ -226,6 +226,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 __device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_wave) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_wave) : "memory", "m0");
 }
+// The same from a wave-uniform 64-bit base (scalar registers) plus a 32-bit
+// byte offset per lane: no 64-bit address in vector registers.
+__device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t off, uint32_t lds_wave) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_wave)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 // Wait until at most N of this wave's vector memory operations are
 // outstanding and its LDS reads are done, then meet the other waves.
@@ -304,6 +310,19 @@ __device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ kb, const 
   lds_dma16(kb + c + k1, lds_w + 4096);
   lds_dma16(vb + c + v0, lds_w + 2 * kSwzTileElems);
   lds_dma16(vb + c + v1, lds_w + 2 * kSwzTileElems + 4096);
+}
+
+// dma_tile for K and V with 64-element rows (row stride 64) from
+// wave-uniform bases, every key below 2^24 (byte offsets fit in 32 bits).
+__device__ __forceinline__ void dma_tile_rows64(const uint16_t* kb, const uint16_t* vb, int key0, int key1,
+                                                uint32_t lds_w) {
+  const int tid = threadIdx.x;
+  const uint32_t c = 8u * (uint32_t)((tid & 7) ^ tile_swz(tid >> 3));
+  const uint32_t o0 = ((uint32_t)key0 * 64u + c) * 2u, o1 = ((uint32_t)key1 * 64u + c) * 2u;
+  lds_dma16_s(kb, o0, lds_w);
+  lds_dma16_s(kb, o1, lds_w + 4096);
+  lds_dma16_s(vb, o0, lds_w + 2 * kSwzTileElems);
+  lds_dma16_s(vb, o1, lds_w + 2 * kSwzTileElems + 4096);
 }
 
 
