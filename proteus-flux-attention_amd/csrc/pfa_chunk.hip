@@ -545,6 +545,31 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(typename Elem<DT>::T* x,
   store_f<DT>(base + 1, round_to<DT>(round_to<DT>(xo * co) + round_to<DT>(xe * so)));
 }
 
+// The same, 8 elements (4 pairs) per thread with 16-byte loads and stores,
+// for D a multiple of 8 and 16-byte aligned rows and tables (rope_rotate8:
+// the bits of the pair formula above).
+template <int DT>
+__global__ void __launch_bounds__(256) rope_rows8_kernel(typename Elem<DT>::T* x, int64_t n_rows,
+                                                         int64_t row_stride, int H, int D,
+                                                         const typename Elem<DT>::T* cos_tab,
+                                                         const typename Elem<DT>::T* sin_tab,
+                                                         const int32_t* positions, int64_t pos_offset) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_row = H * (D / 8);
+  if (i >= n_rows * per_row) return;
+  const int64_t r = i / per_row;
+  const int e = (int)(i - r * per_row) * 8;  // element offset within the row's H*D
+  const int d = e % D;
+  const int64_t t = positions ? (int64_t)positions[r] : pos_offset + r;
+  typename Elem<DT>::T* base = x + r * row_stride + e;
+  float xv[8], cv[8], sv[8], o[8];
+  load8<DT>(base, xv);
+  load8<DT>(cos_tab + t * D + d, cv);
+  load8<DT>(sin_tab + t * D + d, sv);
+  rope_rotate8<DT>(xv, cv, sv, o);
+  store8<DT>(base, o);
+}
+
 }  // namespace pfa
 
 using namespace pfa;
@@ -688,6 +713,25 @@ extern "C" int pfa_rope_rows_inplace(void* x, int dtype, int64_t n_rows, int64_t
   if (n_rows == 0) return PFA_OK;
   PFA_CHECK_ARG(x && cos_tab && sin_tab, "pfa_rope_rows_inplace: null pointer");
   hipStream_t s = as_stream(stream);
+  const bool vec = D % 8 == 0 && row_stride % 8 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)cos_tab % 16) == 0 &&
+                   ((uintptr_t)sin_tab % 16) == 0 && (dtype == PFA_F32 || dtype == PFA_BF16 || dtype == PFA_F16);
+  if (vec) {
+    const int64_t work8 = n_rows * H * (D / 8);
+    const unsigned blocks8 = (unsigned)((work8 + 255) / 256);
+    if (dtype == PFA_F32)
+      rope_rows8_kernel<PFA_F32><<<blocks8, 256, 0, s>>>((float*)x, n_rows, row_stride, H, D, (const float*)cos_tab,
+                                                          (const float*)sin_tab, positions, pos_offset);
+    else if (dtype == PFA_BF16)
+      rope_rows8_kernel<PFA_BF16><<<blocks8, 256, 0, s>>>((uint16_t*)x, n_rows, row_stride, H, D,
+                                                           (const uint16_t*)cos_tab, (const uint16_t*)sin_tab,
+                                                           positions, pos_offset);
+    else
+      rope_rows8_kernel<PFA_F16><<<blocks8, 256, 0, s>>>((uint16_t*)x, n_rows, row_stride, H, D,
+                                                          (const uint16_t*)cos_tab, (const uint16_t*)sin_tab,
+                                                          positions, pos_offset);
+    PFA_CHECK_LAUNCH("pfa_rope_rows_inplace");
+    return PFA_OK;
+  }
   const int64_t work = n_rows * H * (D / 2);
   const unsigned blocks = (unsigned)((work + 255) / 256);
   switch (dtype) {

@@ -97,14 +97,18 @@ def test_quantize_rows_bitwise(dev, dt):
     assert torch.equal(s.cpu(), rs) and torch.equal(q.cpu(), rq)
 
 
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_rope_rows_bitwise(dev, dt):
+@pytest.mark.parametrize("dt,D,pad", [(torch.float32, 64, 0), (torch.bfloat16, 64, 0), (torch.bfloat16, 24, 0),
+                                      (torch.bfloat16, 64, 2), (torch.float32, 20, 0), (torch.float16, 64, 0)])
+def test_rope_rows_bitwise(dev, dt, D, pad):
+    """RoPE on strided rows: the 8-element vector kernel (D a multiple of 8,
+    16-byte aligned rows) and the per-pair kernel (D = 20, or a row stride
+    that is not a multiple of 8 elements) both give the oracle's bits."""
     from proteus_attention.tools.final_pass import rope_rows_
 
     g = torch.Generator().manual_seed(4)
-    T, H, D, n = 5000, 4, 64, 300
+    T, H, n = 5000, 4, 300
     cos, sin = O.rope_tables(T, D, 10000.0, dt)
-    x = torch.randn(n, 2 * H * D, generator=g).to(dt)
+    x = torch.randn(n, 2 * H * D + pad, generator=g).to(dt)
     pos = torch.randint(0, T, (n,), generator=g)
     xd = x.to(dev)
     rope_rows_(xd[:, : H * D], H, cos.to(dev), sin.to(dev), positions=pos.to(dev))
