@@ -161,3 +161,37 @@ def test_nucleus_head_count_matches_reference(golden):
     got = [[m._nucleus_head_count(p, float(tp), int(cap)) for tp in z["target_p"] for cap in z["caps"]]
            for p in probs]
     assert got == z["k"].tolist()
+
+
+def test_graph_eligibility_follows_host_decisions():
+    """A forward is captured in a HIP graph only when no host decision reads
+    a device result: the chunked pipeline's chunk model at 65,536 tokens
+    (token mask without a keep threshold, materialised candidates, top-p
+    routing with the head count at its floor) is eligible; a keep
+    threshold, a head count above its floor with top-p routing, a length
+    served by the structured kernel (which reads the exact row count), a
+    density threshold or grad mode are not."""
+    from proteus_attention.tools.chunked_shortlist import _build_model_config
+
+    def model(T, **over):
+        cfg = _build_model_config(T, 512, heads=8, sparse_ratio=0.05, shortlist_alpha=0.0, router_top_p=1.0)
+        for k, v in over.items():
+            setattr(cfg, k, v)
+        return AdaptiveSparseAttention(cfg).to(torch.bfloat16).eval()
+
+    x = torch.zeros(1, 65536, 512, dtype=torch.bfloat16)
+    with torch.no_grad():
+        assert model(65536)._graph_eligible(x)
+        assert not model(65536, attn_token_keep_threshold=0.5)._graph_eligible(x)
+        # a floor of 2 heads: at 65,536 tokens (>= seq_high) k is the floor and
+        # the nucleus count is skipped; with seq_high beyond T, k stays above it
+        assert model(65536, attn_h_active_min=2)._graph_eligible(x)
+        assert not model(65536, attn_h_active_min=2, attn_active_seq_high=1 << 20)._graph_eligible(x)
+        assert not model(65536, attn_force_dense_threshold=0.9)._graph_eligible(x)
+        # 4,096 tokens: window + anchors fit in L, the structured kernel serves it
+        assert not model(4096)._graph_eligible(torch.zeros(1, 4096, 512, dtype=torch.bfloat16))
+        m = model(65536)
+        m.token_sparse = False
+        m.router_top_p = 0.0
+        assert m._graph_eligible(x)
+    assert not model(65536)._graph_eligible(x)  # grad mode on
