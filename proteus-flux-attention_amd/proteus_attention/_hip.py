@@ -242,6 +242,29 @@ def is_available() -> bool:
     return bool(torch.cuda.is_available())
 
 
+class _TimedBlock:
+    """One ``_KernelTimer.timed`` block: an event pair on the current stream
+    when the timer is enabled, nothing otherwise."""
+
+    __slots__ = ("timer", "name", "e0")
+
+    def __init__(self, timer: "_KernelTimer", name: str) -> None:
+        self.timer, self.name, self.e0 = timer, name, None
+
+    def __enter__(self):
+        if self.timer.enabled:
+            self.e0 = torch.cuda.Event(enable_timing=True)
+            self.e0.record()
+        return self
+
+    def __exit__(self, *exc):
+        if self.e0 is not None:
+            e1 = torch.cuda.Event(enable_timing=True)
+            e1.record()
+            self.timer.events.setdefault(self.name, []).append((self.e0, e1))
+        return False
+
+
 class _KernelTimer:
     """Optional per-stage HIP event timing on torch's current stream (the
     stream every launch of this package uses).  Disabled by default; when
@@ -254,24 +277,8 @@ class _KernelTimer:
     def reset(self) -> None:
         self.events = {}
 
-    def timed(self, name: str):
-        timer = self
-
-        class _Ctx:
-            def __enter__(self_inner):
-                if timer.enabled:
-                    self_inner.e0 = torch.cuda.Event(enable_timing=True)
-                    self_inner.e1 = torch.cuda.Event(enable_timing=True)
-                    self_inner.e0.record()
-                return self_inner
-
-            def __exit__(self_inner, *exc):
-                if timer.enabled:
-                    self_inner.e1.record()
-                    timer.events.setdefault(name, []).append((self_inner.e0, self_inner.e1))
-                return False
-
-        return _Ctx()
+    def timed(self, name: str) -> _TimedBlock:
+        return _TimedBlock(self, name)
 
     def summary_ms(self) -> dict:
         torch.cuda.synchronize()

@@ -51,6 +51,25 @@ from ..kernels.sparse_attn import (
 )
 
 
+# Side streams (default priority) shared by every module in the process, one
+# per (device, role): "fork" carries a forward's second dependency chain,
+# "capture" a graph capture's warm-up forward, "copy" the chunked runner's
+# host-to-device chunk copies.  torch keeps a GEMM workspace
+# (hipBLASLt) for every stream a GEMM has run on until the process ends, so a
+# stream per module instance would leave one workspace behind per instance.
+# Every use is bracketed by stream waits in both directions, so sharing adds
+# no dependency a forward does not already have.
+_SIDE_STREAMS: Dict[Tuple[int, str], torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device, role: str) -> torch.cuda.Stream:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    st = _SIDE_STREAMS.get((index, role))
+    if st is None:
+        st = torch.cuda.Stream(device=torch.device("cuda", index))
+        _SIDE_STREAMS[(index, role)] = st
+    return st
+
 class ModelConfig:
     """Attribute bag with the reference defaults (aspa.py:33-72)."""
 
@@ -530,7 +549,11 @@ class AdaptiveSparseAttention(nn.Module):
 
     def _defer(self, fn) -> None:
         """Queue a telemetry step that needs device results; it runs at the
-        next _resolve_stats (a telemetry read or the next forward)."""
+        next _resolve_stats (a telemetry read or the next forward) as
+        fn(module).  The steps take the module as their argument rather than
+        closing over it: a queued closure holding the module would make a
+        reference cycle, and a dropped module (with its device buffers and
+        graphs) would then live until Python's cycle collector ran."""
         self.__dict__.setdefault("_pending_stats", []).append(fn)
 
     def _resolve_stats(self) -> None:
@@ -539,7 +562,7 @@ class AdaptiveSparseAttention(nn.Module):
             return
         self.__dict__["_pending_stats"] = []
         for fn in pend:
-            fn()
+            fn(self)
 
     def _update_density(self, value: float) -> None:
         value = float(max(0.0, value))
@@ -1090,7 +1113,7 @@ class AdaptiveSparseAttention(nn.Module):
         timer_on = _hip.TIMER.enabled
         _hip.TIMER.enabled = False
         try:
-            side = torch.cuda.Stream(device=device)
+            side = _side_stream(device, "capture")
             side.wait_stream(torch.cuda.current_stream(device))
             with torch.cuda.stream(side):
                 self._forward_impl(xs, capture=True)  # warm-up: library handles, lazy allocations
@@ -1163,7 +1186,7 @@ class AdaptiveSparseAttention(nn.Module):
         if self.track_latency and ev0 is not None:
             ev1.record()
 
-            def latency(st=st_now):
+            def latency(self, st=st_now):
                 ev1.synchronize()
                 ms = float(ev0.elapsed_time(ev1))
                 prev = self.__dict__.get("_lazy__latency_ema")
@@ -1176,7 +1199,7 @@ class AdaptiveSparseAttention(nn.Module):
 
             self._defer(latency)
 
-        def labels(st=st_now):
+        def labels(self, st=st_now):
             hs = self.__dict__.get("_lazy_last_head_stats")
             if hs is not None:
                 hs["mode_setting"] = self.mode_setting
@@ -1503,15 +1526,8 @@ class AdaptiveSparseAttention(nn.Module):
                 "w_eff": w_eff, "structured": structured}
 
     def _fork_stream(self, device: torch.device) -> torch.cuda.Stream:
-        """The forward's second stream on `device` (default priority), created
-        once per device."""
-        streams = self.__dict__.setdefault("_fork_streams", {})
-        key = (device.type, device.index)
-        st = streams.get(key)
-        if st is None:
-            st = torch.cuda.Stream(device=device)
-            streams[key] = st
-        return st
+        """The forward's second stream on `device` (default priority)."""
+        return _side_stream(device, "fork")
 
     def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha, row_of,
                               summary, plan: Optional[Dict[str, Any]] = None, q_rope=None, streams=None,
@@ -1699,7 +1715,7 @@ class AdaptiveSparseAttention(nn.Module):
                                                            int(self.linear_anchor_stride)),
             proto=self._last_token_similarity is not None, mode_setting=self.mode_setting)
 
-        def build() -> None:
+        def build(self) -> None:
             nonlocal mode_label
             done.synchronize()
             part = host[0].tolist()

@@ -31,7 +31,7 @@ import numpy as np
 import torch
 
 from ..kernels.sparse_attn import _record_backend, get_last_backend_info
-from ..models.aspa import AdaptiveSparseAttention, ModelConfig
+from ..models.aspa import AdaptiveSparseAttention, ModelConfig, _side_stream
 from . import chunk_select
 from .final_pass import AllQueryFinalPass
 
@@ -206,8 +206,11 @@ class ChunkedShortlistConfig:
     final_causal: bool = True
     # replay the chunk model's forward from a captured HIP graph (one
     # capture per chunk length, during the warm-up forward) where the
-    # forward has no host decision on device results; otherwise it runs
-    # eagerly
+    # forward has no host decision on device results and the sequence is
+    # resident on the device; otherwise it runs eagerly (with host staging
+    # the stage is bound by the chunk copies, and graph replays beside them
+    # slowed the copies from pinned memory, measured 19.2 -> 23.4 ms for
+    # 1 GiB, the chunk stage 20.0 -> 24.4 ms)
     chunk_graph: bool = True
 
     def validate(self) -> None:
@@ -241,6 +244,21 @@ class ChunkedShortlistConfig:
             raise ValueError("final_mode must be 'reduced' or 'all_queries'.")
 
 
+# memmap element types for rows stored in their own dtype (bf16 as its raw
+# 16-bit pattern)
+_MEMMAP_NP = {torch.float32: np.float32, torch.float16: np.float16, torch.bfloat16: np.int16}
+
+
+def _memmap_view(t: torch.Tensor) -> np.ndarray:
+    """A (rows, d_model) CPU tensor as the memmap's element type."""
+    return t.view(torch.int16).numpy() if t.dtype == torch.bfloat16 else t.numpy()
+
+
+def _memmap_rows(a: np.ndarray, store: torch.dtype) -> torch.Tensor:
+    """Memmap rows as a CPU tensor of the stored dtype."""
+    t = torch.from_numpy(np.asarray(a))
+    return t.view(torch.bfloat16) if store == torch.bfloat16 else t
+
 class _ChunkStager:
     """Double-buffered host-to-device chunk streaming (reference
     chunked_shortlist.py:617-625, 688-689 copy each chunk with a blocking
@@ -251,16 +269,29 @@ class _ChunkStager:
     released that buffer (chunk i-2); take(i) makes the compute stream wait
     for it; release(i) marks the compute stream's use of the buffer done.
     Pinned staging ("cpu" mode) copies straight from the pinned sequence;
-    disk staging reads chunk rows from the memmap into one of two pinned
-    buffers on a worker thread (chunk i+1 is read while chunk i is copied
-    and computed), each buffer reused only after its previous copy is done.
+    disk staging reads chunk rows from the memmap into pinned buffers on a
+    worker thread, up to HOST_BUFFERS chunks ahead of the copies, each
+    buffer reused only after its previous copy is done (with two buffers
+    the worker ran one chunk ahead and the copies waited on its reads).
     Copy time and the compute stream's waits are measured with events."""
+
+    HOST_BUFFERS = 3
+    # threads that copy one chunk's rows out of the memmap (numpy copies,
+    # which release the GIL and block when idle: torch's own CPU copy runs
+    # on its OpenMP pool, whose threads spin between regions and slowed the
+    # host's launches, measured 39.7 ms chunk stage against 27.8 ms with
+    # the pool made passive)
+    FILL_THREADS = 4
 
     def __init__(self, st: Dict[str, Any], chunks: List[Tuple[int, int]], chunk_len: int, d_model: int,
                  device: torch.device, dtype: torch.dtype) -> None:
         self.st, self.chunks, self.device = st, chunks, device
         self.bufs = [torch.empty(1, chunk_len, d_model, device=device, dtype=dtype) for _ in range(2)]
-        self.copy_s = torch.cuda.Stream(device=device)
+        # one copy stream per device for the process: with a fresh pool
+        # stream per run, some runs' copies and the chunk model's kernels
+        # waited on each other (chunk stage 20.4-29.9 ms over six runs,
+        # 20.0 ms in every run with the one stream)
+        self.copy_s = _side_stream(device, "copy")
         self.ready = [torch.cuda.Event() for _ in range(2)]
         self.freed = [None, None]
         self.copy_ev = []
@@ -268,23 +299,41 @@ class _ChunkStager:
         self.disk = st.get("memmap") is not None
         self.pool = None
         if self.disk:
-            self.host = [torch.empty(1, chunk_len, d_model, dtype=dtype).pin_memory() for _ in range(2)]
-            self.h2d_done = [None, None]
+            nh = self.HOST_BUFFERS
+            self.host = [torch.empty(1, chunk_len, d_model, dtype=dtype, pin_memory=True) for _ in range(nh)]
+            self.h2d_done: List[Optional[torch.cuda.Event]] = [None] * nh
+            # numpy views of the pinned buffers (bf16 as its 16-bit pattern,
+            # the memmap's element type for bf16 rows); None for a dtype
+            # numpy has no type for, which takes torch's copy
+            try:
+                self.host_np = [_memmap_view(h[0]) for h in self.host]
+            except TypeError:
+                self.host_np = None
             self.pool = cf.ThreadPoolExecutor(max_workers=1)
+            self.copiers = cf.ThreadPoolExecutor(max_workers=self.FILL_THREADS)
             self.fills: Dict[int, cf.Future] = {}
-            self._fill(0)
+            for j in range(nh):
+                self._fill(j)
 
     def _fill(self, i: int) -> None:
         if i >= len(self.chunks) or i in self.fills:
             return
         s, e = self.chunks[i]
-        slot = i % 2
-        done = self.h2d_done[slot]
+        slot = i % self.HOST_BUFFERS
+        done = self.h2d_done[slot]  # the copy of chunk i - HOST_BUFFERS
 
         def work() -> None:
             if done is not None:
                 done.synchronize()  # the previous copy out of this pinned buffer
-            self.host[slot][:, :e - s].copy_(torch.from_numpy(np.asarray(self.st["memmap"][s:e])).unsqueeze(0))
+            if self.host_np is None:
+                self.host[slot][:, :e - s].copy_(self.st["rows"](s, e).unsqueeze(0))
+                return
+            src, dst, n = self.st["memmap"], self.host_np[slot], e - s
+            step = -(-n // self.FILL_THREADS)
+            parts = [self.copiers.submit(np.copyto, dst[a:min(n, a + step)], src[s + a:s + min(n, a + step)])
+                     for a in range(0, n, step)]
+            for f in parts:
+                f.result()
 
         self.fills[i] = self.pool.submit(work)
 
@@ -294,7 +343,7 @@ class _ChunkStager:
         if self.disk:
             self._fill(i)
             self.fills.pop(i).result()
-            src = self.host[slot][:, :e - s]
+            src = self.host[i % self.HOST_BUFFERS][:, :e - s]
         else:
             src = self.st["fetch"](s, e)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -309,8 +358,8 @@ class _ChunkStager:
         if self.disk:
             ev = torch.cuda.Event()
             ev.record(self.copy_s)
-            self.h2d_done[slot] = ev
-            self._fill(i + 1)
+            self.h2d_done[i % self.HOST_BUFFERS] = ev
+            self._fill(i + self.HOST_BUFFERS)
 
     def take(self, i: int) -> torch.Tensor:
         s, e = self.chunks[i]
@@ -337,6 +386,7 @@ class _ChunkStager:
     def close(self) -> None:
         if self.pool is not None:
             self.pool.shutdown(wait=True)
+            self.copiers.shutdown(wait=True)
 
 
 class ChunkedShortlistRunner:
@@ -429,22 +479,30 @@ class ChunkedShortlistRunner:
                                                  delete=False)
             handle.close()
             path = Path(handle.name)
-            mm = np.memmap(path, dtype=np.float32, mode="w+", shape=(cfg.seq_len, cfg.d_model))
-            rows = max(1, min(cfg.chunk_len, int((64 * 1024 * 1024) / max(cfg.d_model * 4, 1))))
+            # rows are stored in the sequence's own dtype where a float32
+            # round trip (the reference's float32 memmap) is exact -- bf16,
+            # fp16, fp32: the same values in half the bytes for 16-bit
+            # sequences -- and in float32 otherwise (its rounding kept)
+            store = base_dtype if base_dtype in _MEMMAP_NP else torch.float32
+            mm = np.memmap(path, dtype=_MEMMAP_NP[store], mode="w+", shape=(cfg.seq_len, cfg.d_model))
+            item = mm.dtype.itemsize
+            rows = max(1, min(cfg.chunk_len, int((64 * 1024 * 1024) / max(cfg.d_model * item, 1))))
             gen = torch.Generator(device="cpu")
             if cfg.seed is not None:
                 gen.manual_seed(int(cfg.seed))
             for s in range(0, cfg.seq_len, rows):
                 e = min(cfg.seq_len, s + rows)
                 if source is not None:
-                    mm[s:e] = source[:, s:e].to("cpu", dtype=torch.float32).squeeze(0).numpy()
+                    block = source[:, s:e].to("cpu").squeeze(0)
                 else:
-                    mm[s:e] = torch.randn(e - s, cfg.d_model, generator=gen).to(torch.float32).numpy()
+                    block = torch.randn(e - s, cfg.d_model, generator=gen)
+                mm[s:e] = _memmap_view(block.to(store))
             mm.flush()
-            st.update(memmap=mm, path=path, allocated=int(rows * cfg.d_model * 4),
-                      dataset=int(cfg.seq_len * cfg.d_model * 4))
-            st["fetch"] = lambda s, e: torch.from_numpy(np.asarray(mm[s:e])).to(base_dtype).unsqueeze(0)
-            st["gather"] = lambda idx: torch.from_numpy(np.asarray(mm[idx.cpu().numpy()])).to(base_dtype).unsqueeze(0)
+            st.update(memmap=mm, path=path, allocated=int(rows * cfg.d_model * item),
+                      dataset=int(cfg.seq_len * cfg.d_model * item))
+            st["rows"] = lambda s, e: _memmap_rows(mm[s:e], store)
+            st["fetch"] = lambda s, e: _memmap_rows(mm[s:e], store).to(base_dtype).unsqueeze(0)
+            st["gather"] = lambda idx: _memmap_rows(mm[idx.cpu().numpy()], store).to(base_dtype).unsqueeze(0)
         return st
 
     def run(self, sequence: Optional[torch.Tensor] = None) -> ChunkedShortlistResult:
@@ -460,7 +518,7 @@ class ChunkedShortlistRunner:
                                                                                          dtype=base_dtype).eval()
             chunk_model.use_sdpa = False
             chunk_model.set_shortlist_alpha(float(cfg.shortlist_alpha))
-            if cfg.chunk_graph and device.type == "cuda":
+            if cfg.chunk_graph and device.type == "cuda" and st["mode"] == "device":
                 # the forward's output is the graph's own buffer (unused here)
                 chunk_model.enable_hip_graph(True, static_output=True)
             direct = st["mode"] == "device"

@@ -265,7 +265,9 @@ def test_chunked_runner_graph_matches_eager(dev, storage):
     shortlist and final output.  60,000 tokens in chunks of 24,576: the two
     full chunks replay the graph (materialised candidates); the 10,848-token
     last chunk takes the structured path, which reads its row count, and
-    runs eagerly between them and the selection."""
+    runs eagerly between them and the selection.  With the sequence staged
+    from host memory the chunk model stays eager (graph replays slowed the
+    staging copies), so the flag changes nothing there."""
     from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
 
     T, C, chunk = 60000, 512, 24576
@@ -280,7 +282,7 @@ def test_chunked_runner_graph_matches_eager(dev, storage):
         runner = ChunkedShortlistRunner(ChunkedShortlistConfig(chunk_graph=graph, **kw))
         res[graph] = runner.run(src)
         graphs[graph] = len(runner.last_chunk_model._hip_graphs)
-    assert graphs[True] == 1 and graphs[False] == 0
+    assert graphs[True] == (1 if storage == "device" else 0) and graphs[False] == 0
     assert res[True].metrics.storage_mode == storage
     for a, b in zip(res[False].chunks, res[True].chunks):
         assert a.promoted == b.promoted and a.scores == b.scores, f"chunk {a.index}"
@@ -288,3 +290,93 @@ def test_chunked_runner_graph_matches_eager(dev, storage):
     assert torch.equal(res[False].keep_scores, res[True].keep_scores)
     assert torch.equal(res[False].final_output.cpu(), res[True].final_output.cpu())
 
+
+
+@pytest.mark.parametrize("storage", ["device", "cpu", "disk"])
+def test_chunked_runner_frees_its_models_without_cycle_collector(dev, storage):
+    """A finished run leaves no reference cycle behind: with Python's cycle
+    collector off, dropping the runner and its result returns every device
+    byte the run allocated (chunk and final models, captured graph, staging
+    buffers) by reference counting alone.  A cycle would keep each run's
+    models alive until the collector happened to run, so back-to-back runs
+    would grow the device footprint run by run."""
+    import gc
+    import weakref
+
+    from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
+
+    T, C, chunk = 60000, 512, 24576
+    print(f"chunked runner frees its models storage={storage}", flush=True)
+    x = torch.randn(1, T, C, generator=torch.Generator().manual_seed(29)).to(torch.bfloat16)
+    cfg = ChunkedShortlistConfig(seq_len=T, d_model=C, chunk_len=chunk, buffer_tokens=600, per_chunk_budget=256,
+                                 device=dev, heads=8, nucleus_top_p=1.0, final_mode="all_queries",
+                                 storage="disk" if storage == "disk" else "cpu")
+    src = x.to(dev) if storage == "device" else x
+    ChunkedShortlistRunner(cfg).run(src)  # warm-up: library workspaces, GEMM handles
+    gc.collect()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
+    gc.disable()
+    try:
+        runner = ChunkedShortlistRunner(cfg)
+        res = runner.run(src)
+        assert res.keep_indices.numel() > 0
+        model = weakref.ref(runner.last_chunk_model)
+        del runner, res
+        torch.cuda.synchronize()
+        assert model() is None
+        assert torch.cuda.memory_allocated(dev) == base
+    finally:
+        gc.enable()
+
+
+def test_module_freed_without_cycle_collector(dev):
+    """Dropping a module after eager or graph-replayed forwards returns
+    every device byte its forwards allocated, by reference counting alone:
+    the telemetry steps a forward defers (run at the next forward or
+    telemetry read) do not keep the module alive, and its side streams are
+    shared, so no per-instance GEMM workspace stays behind."""
+    import gc
+    import weakref
+
+    from proteus_attention.models.aspa import AdaptiveSparseAttention
+    from proteus_attention.tools.chunked_shortlist import _build_model_config
+
+    T = 24576
+    x = torch.randn(1, T, 512, generator=torch.Generator().manual_seed(31)).to(torch.bfloat16).to(dev)
+
+    def make():
+        m = AdaptiveSparseAttention(_build_model_config(T, 512, heads=8, sparse_ratio=0.05, shortlist_alpha=0.0,
+                                                        router_top_p=1.0)).to(dev, torch.bfloat16).eval()
+        m.use_sdpa = False
+        return m
+
+    for graph in (False, True):
+        print(f"module freed without cycle collector graph={graph}", flush=True)
+        warm = make()
+        warm.enable_hip_graph(graph)
+        with torch.inference_mode():
+            warm(x)  # library handles and workspaces
+        del warm
+        gc.collect()
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated(dev)
+        gc.disable()
+        try:
+            m = make()
+            if graph:
+                with torch.no_grad():
+                    assert m._graph_eligible(x)
+            m.enable_hip_graph(graph)
+            with torch.inference_mode():
+                for _ in range(3):
+                    m(x)
+            assert len(m._hip_graphs) == (1 if graph else 0)
+            assert m.__dict__.get("_pending_stats")
+            ref = weakref.ref(m)
+            del m
+            torch.cuda.synchronize()
+            assert ref() is None
+            assert torch.cuda.memory_allocated(dev) == base
+        finally:
+            gc.enable()

@@ -195,3 +195,27 @@ def test_graph_eligibility_follows_host_decisions():
         m.router_top_p = 0.0
         assert m._graph_eligible(x)
     assert not model(65536)._graph_eligible(x)  # grad mode on
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32, torch.float64])
+def test_disk_staging_rows_equal_float32_round_trip(tmp_path, dt):
+    """The disk memmap keeps bf16/fp16/fp32 rows in their own dtype and
+    other dtypes in float32: every fetched row (a slice or a gather) equals
+    the reference's float32 memmap round trip (chunked_shortlist.py:506-553)
+    bit for bit."""
+    import numpy as np
+
+    from proteus_attention.tools import chunked_shortlist as CS
+
+    x = (torch.randn(1, 1000, 48, dtype=torch.float64, generator=torch.Generator().manual_seed(3)) * 300).to(dt)
+    x[0, 3, :4] = torch.tensor([float("inf"), float("-inf"), -0.0, 1e-30], dtype=torch.float64).to(dt)
+    store = dt if dt in CS._MEMMAP_NP else torch.float32
+    mm = np.memmap(tmp_path / "rows.mmap", dtype=CS._MEMMAP_NP[store], mode="w+", shape=(1000, 48))
+    mm[:] = CS._memmap_view(x.squeeze(0).to(store))
+    assert mm.dtype.itemsize == (4 if store == torch.float32 else 2)
+    ref = x[0].to(torch.float32).to(dt)
+    got = CS._memmap_rows(mm[10:500], store).to(dt)
+    assert torch.equal(got.view(torch.uint8), ref[10:500].contiguous().view(torch.uint8))
+    idx = torch.tensor([5, 999, 0, 3, 7])
+    got = CS._memmap_rows(mm[idx.numpy()], store).to(dt)
+    assert torch.equal(got.view(torch.uint8), ref[idx].contiguous().view(torch.uint8))
