@@ -66,6 +66,7 @@ struct ShortArgs {
   const uint16_t* rcos;  // (T, 64) RoPE tables applied to q rows on load, or null
   const uint16_t* rsin;
   float scale_log2;
+  int off32;  // every K/V byte offset of the sequence fits in 32 bits
   // per global head (b*H + h) int8 scales of q, k, v, or null: q, k, v then
   // hold the integer values (exact in bf16) of the per-head int8
   // quantisation, scores are scaled by q_scale*k_scale and outputs by v_scale
@@ -105,11 +106,12 @@ __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); 
 
 constexpr int kTileElems = kSwzTileElems;  // one unpadded K or V tile, bf16 elements
 
-// One 64-key tile for the 16 query rows of this wave, in three stages that
-// every tile kind shares: qk_tile (the scores), a mask (keys of the tile
-// that are not candidates of the lane's row get -inf), softmax_pv (online
-// softmax and the P.V product).  One accumulation path for all tile kinds
-// keeps the running state in the same registers across tiles.
+// One 64-key tile for the 16 query rows of this wave, in two stages that
+// every tile kind shares: the scores (qk_tile, or qk_tile_b with the mask
+// -- -inf for keys of the tile that are not candidates of the lane's row --
+// as the MFMA's initial accumulator) and softmax_pv (online softmax and
+// the P.V product).  One accumulation path for all tile kinds keeps the
+// running state in the same registers across tiles.
 //
 // S^T = K Q^T: s[kb][i] is the raw score of tile key 16kb + 4g + i against
 // the lane's query row (the scale is applied in the exp argument).
@@ -133,38 +135,81 @@ __device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[2], const Tile& t, 
     for (int i = 0; i < 4; ++i) s[kb][i] = c[kb][i];
 }
 
-// Range mask: the lane's candidates in the tile are the keys kl in
-// [lo, hi]; lo4 = lo - 4g and hi4 = hi - 4g, so each element is one compare
-// against a constant (16kb + i) and a select.  LO / HI pick which bounds can
-// cut this tile (a wave-uniform choice).
-template <bool LO, bool HI, bool COUNT>
-__device__ __forceinline__ void mask_range(float (&s)[4][4], int lo4, int hi4, int& cnt) {
+// The same product with the accumulator started at bias[kb] (0 for a
+// candidate, -inf for a key the row does not take): the mask rides on the
+// MFMA's C operand, so a masked tile needs no select after the product.
+// For finite q and k the scores are those of qk_tile with -inf in the
+// masked places.
+template <typename Tile>
+__device__ __forceinline__ void qk_tile_b(const bf16x8_t (&qf)[2], const Tile& t, const f32x4_t (&bias)[4],
+                                          float (&s)[4][4]) {
+  bf16x8_t a[2][4];
+#pragma unroll
+  for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) a[dc][kb] = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, dc));
+  f32x4_t c[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0][kb], qf[0], bias[kb], 0, 0, 0);
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1][kb], qf[1], c[kb], 0, 0, 0);
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[kb][i] = c[kb][i];
+}
+
+// Window bias: keys kl of the tile in [lo, hi] (tile-local) get 0, the
+// others -inf; lo4 = lo - 4g and hi4 = hi - 4g, so each element is one
+// compare against a constant (16kb + i).  LO / HI pick which bounds can cut
+// this tile (a wave-uniform choice).
+template <bool LO, bool HI>
+__device__ __forceinline__ void bias_range(f32x4_t (&b)[4], int lo4, int hi4) {
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = 16 * kb + i;
       bool ok = true;
-      if constexpr (LO) ok = ok && c >= lo4;
-      if constexpr (HI) ok = ok && c <= hi4;
-      s[kb][i] = ok ? s[kb][i] : -INFINITY;
-      if constexpr (COUNT) cnt += ok ? 1 : 0;
+      if constexpr (LO) ok = ok & (c >= lo4);
+      if constexpr (HI) ok = ok & (c <= hi4);
+      b[kb][i] = ok ? 0.f : -INFINITY;
     }
 }
 
-// The lane's candidates in the tile are [lo, hi] (tile-local, lo > hi for
-// none); need_lo / need_hi (wave-uniform) say whether some row of the wave
-// is cut by that bound in this tile.
-template <bool COUNT>
-__device__ __forceinline__ void mask_window(float (&s)[4][4], bool need_lo, bool need_hi, int lo, int hi, int& cnt) {
+// Candidates counted from a masked tile's scores: the masked places are
+// -inf, every other score is finite (finite q and k).
+__device__ __forceinline__ int count_finite(const float (&s)[4][4]) {
+  int n = 0;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n += s[kb][i] != -INFINITY ? 1 : 0;
+  return n;
+}
+
+// Scores of a window tile whose lane's candidates are the keys kl in
+// [lo, hi] (tile-local, lo > hi for none); need_lo / need_hi say whether
+// some row of the wave is cut by that bound in this tile.  Uncut tiles take
+// the plain product.
+template <bool COUNT, typename Tile>
+__device__ __forceinline__ void window_qk(const bf16x8_t (&qf)[2], const Tile& t, bool need_lo, bool need_hi, int lo,
+                                          int hi, int& cnt, float (&s)[4][4]) {
   const int g4 = 4 * ((threadIdx.x & 63) >> 4);
   // the conditions are wave-uniform: scalar branches
   need_lo = __builtin_amdgcn_readfirstlane(need_lo ? 1 : 0) != 0;
   need_hi = __builtin_amdgcn_readfirstlane(need_hi ? 1 : 0) != 0;
-  if (need_lo && need_hi) mask_range<true, true, COUNT>(s, lo - g4, hi - g4, cnt);
-  else if (need_lo) mask_range<true, false, COUNT>(s, lo - g4, 0, cnt);
-  else if (need_hi) mask_range<false, true, COUNT>(s, 0, hi - g4, cnt);
-  else if (COUNT) cnt += 16;
+  if (!need_lo && !need_hi) {
+    if constexpr (COUNT) cnt += 16;
+    qk_tile(qf, t, s);
+    return;
+  }
+  f32x4_t bias[4];
+  if (need_lo && need_hi) bias_range<true, true>(bias, lo - g4, hi - g4);
+  else if (need_lo) bias_range<true, false>(bias, lo - g4, 0);
+  else bias_range<false, true>(bias, 0, hi - g4);
+  qk_tile_b(qf, t, bias, s);
+  if constexpr (COUNT) cnt += count_finite(s);
 }
 
 // Online softmax (exp2 on v_exp_f32 directly: arguments are <= 0, -inf
@@ -233,15 +278,23 @@ __device__ __forceinline__ bf16x8_t v_frag(const Tile& t, int kc, int db) {
 }
 
 // Softmax and O^T += V^T P^T for one 16-row group.
+// The sixteen transpose reads of V^T are issued before the softmax, so
+// their latency overlaps the exponentials instead of sitting between the
+// P.V products.
 template <typename Tile>
 __device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, float scale_log2, QState& st) {
+  bf16x8_t va[2][4];
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) va[kc][db] = v_frag(t, kc, db);
   bf16x8_t pb[2];
   softmax_p(s, scale_log2, st, pb);
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
     for (int db = 0; db < 4; ++db)
-      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_frag(t, kc, db), pb[kc], st.acc[db], 0, 0, 0);
+      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[kc][db], pb[kc], st.acc[db], 0, 0, 0);
 }
 
 __device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[2]) {
@@ -280,6 +333,20 @@ __device__ __forceinline__ void load_q_row(const ShortArgs& a, const uint16_t* q
     load_q_rope(qb + t * a.q.s_t, a.rcos + t * 64, a.rsin + t * 64, qf);
   else
     load_q(qb + t * a.q.s_t, qf);
+}
+
+// dma_tile from wave-uniform K/V bases with 32-bit byte offsets per lane
+// (the caller checks that every offset of the sequence fits in 32 bits):
+// no 64-bit address arithmetic per tile.
+__device__ __forceinline__ void dma_tile32(const uint16_t* kb, const uint16_t* vb, uint32_t ks_t, uint32_t vs_t,
+                                           int key0, int key1, uint32_t lds_w) {
+  const int tid = threadIdx.x;
+  const uint32_t c = 2u * 8u * (uint32_t)((tid & 7) ^ tile_swz(tid >> 3));
+  const uint32_t k2 = 2u * ks_t, v2 = 2u * vs_t;
+  lds_dma16_s(kb, (uint32_t)key0 * k2 + c, lds_w);
+  lds_dma16_s(kb, (uint32_t)key1 * k2 + c, lds_w + 4096);
+  lds_dma16_s(vb, (uint32_t)key0 * v2 + c, lds_w + 2 * kSwzTileElems);
+  lds_dma16_s(vb, (uint32_t)key1 * v2 + c, lds_w + 2 * kSwzTileElems + 4096);
 }
 
 __device__ __forceinline__ void init_state(QState& st) {
@@ -392,8 +459,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
     const int ntile = mhi >= mlo ? (int)((mhi - mlo) / kTile + 1) : 0;
     auto request = [&](int i) {
       const int m0 = (int)mlo + kTile * i;
-      dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, c + s * min(m0 + drow, (int)mhi),
-               c + s * min(m0 + drow + 32, (int)mhi), ring_w + kStageBytes * (uint32_t)(i % S));
+      const int ka = c + s * min(m0 + drow, (int)mhi), kz = c + s * min(m0 + drow + 32, (int)mhi);
+      if (a.off32)
+        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S));
+      else
+        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S));
     };
 #pragma unroll
     for (int i = 0; i < S - 1; ++i)
@@ -420,8 +490,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
         float sc[4][4];
         int unused = 0;
         const SwzTile tl{ring[i % S], L};
-        qk_tile(qf, tl, sc);
-        mask_window<false>(sc, need_lo, need_hi, lo, hi, unused);
+        window_qk<false>(qf, tl, need_lo, need_hi, lo, hi, unused, sc);
         softmax_pv(sc, tl, sl2, st);
       }
     }
@@ -560,8 +629,13 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     const int k_slot0 = wA + ((0 - wA) & (kSlots - 1));
     const bool early = k_slot0 <= wB;
     if (early)
-      dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, min(kTile * k_slot0 + drow, t_last),
-               min(kTile * k_slot0 + drow + 32, t_last), ring_w);
+    {
+      const int ka = min(kTile * k_slot0 + drow, t_last), kz = min(kTile * k_slot0 + drow + 32, t_last);
+      if (a.off32)
+        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w);
+      else
+        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w);
+    }
     const bool qv = qs >= s0 && qs < s1;
     const int tq = qv ? r_t[qs] : t_first;
 
@@ -699,8 +773,11 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
       return pk[min((-1 - d) * kTile + r, plen - 1)];
     };
     auto request = [&](int i) {
-      dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, key_of(i, drow), key_of(i, drow + 32),
-               ring_w + kStageBytes * (uint32_t)(i % S));
+      const int ka = key_of(i, drow), kz = key_of(i, drow + 32);
+      if (a.off32)
+        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S));
+      else
+        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S));
     };
     if (!early) request(0);
 #pragma unroll
@@ -737,13 +814,21 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
       const bool active = is_win ? (wave_rows && k0 <= w_thi && k0 + kTile - 1 >= w_llo) : wave_rows;
       if (active) {
         float sc[4][4];
-        qk_tile(qf, tl, sc);
+        f32x4_t bias[4];
+        bool plain = false;
         if (is_win) {
-          // the row's window keys in the tile: [loq - k0, tq - k0]
-          const bool need_lo = !wave_full || k0 < w_lhi;
-          const bool need_hi = !wave_full || k0 + kTile - 1 > w_tlo;
-          mask_window<COUNT>(sc, need_lo, need_hi, qv ? loq - k0 : kTile, tq - k0, st.cnt);
+          // the row's window keys in the tile: [loq - k0, tq - k0]; which
+          // bounds cut the tile is wave-uniform
+          const bool need_lo = __builtin_amdgcn_readfirstlane((!wave_full || k0 < w_lhi) ? 1 : 0) != 0;
+          const bool need_hi = __builtin_amdgcn_readfirstlane((!wave_full || k0 + kTile - 1 > w_tlo) ? 1 : 0) != 0;
+          const int lo4 = (qv ? loq - k0 : kTile) - 4 * g, hi4 = tq - k0 - 4 * g;
+          if (need_lo && need_hi) bias_range<true, true>(bias, lo4, hi4);
+          else if (need_lo) bias_range<true, false>(bias, lo4, 0);
+          else if (need_hi) bias_range<false, true>(bias, 0, hi4);
+          else plain = true;
         } else {
+          // the prototype test of each key (bitwise, no short-circuit
+          // branches around the LDS reads)
           const int j0 = (-1 - d) * kTile + 4 * g;
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb) {
@@ -754,12 +839,18 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
                       kmv[4] = {km.x, km.y, km.z, km.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              bool ok = kpv[e] <= p_tw && kev[e] > tq && !(kmv[e] == p_tmod && kpv[e] >= p_ts);
-              if (kb == 0 && e == 0) ok = ok || (p_zero && j0 == 0 && p_tw >= 0);
-              sc[kb][e] = ok ? sc[kb][e] : -INFINITY;
-              if constexpr (COUNT) st.cnt += ok ? 1 : 0;
+              bool ok = (kpv[e] <= p_tw) & (kev[e] > tq) & !((kmv[e] == p_tmod) & (kpv[e] >= p_ts));
+              if (kb == 0 && e == 0) ok = ok | (p_zero & (j0 == 0) & (p_tw >= 0));
+              bias[kb][e] = ok ? 0.f : -INFINITY;
             }
           }
+        }
+        if (plain) {
+          qk_tile(qf, tl, sc);
+          if constexpr (COUNT) st.cnt += 16;
+        } else {
+          qk_tile_b(qf, tl, bias, sc);
+          if constexpr (COUNT) st.cnt += count_finite(sc);
         }
         softmax_pv(sc, tl, sl2, st);
       }
@@ -864,6 +955,11 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
   a.row_of = row_of; a.summary = summary; a.part = partials; a.lengths = lengths;
   a.rcos = (const uint16_t*)q_rope_cos; a.rsin = (const uint16_t*)q_rope_sin;
   a.scale_log2 = scale * 1.4426950408889634f;
+  {
+    // byte offsets key * s_t * 2 + 112 of every key below T, K and V
+    const uint64_t mx = (uint64_t)(T - 1) * (uint64_t)(k.s_t > v.s_t ? k.s_t : v.s_t) * 2u + 128u;
+    a.off32 = mx < 0xFFFFFFFFull ? 1 : 0;
+  }
   a.qsc = q_scale; a.ksc = k_scale; a.vsc = v_scale;
   hipStream_t s = as_stream(stream);
   if (anchors && (passes & 1)) {
