@@ -106,6 +106,11 @@ __device__ __forceinline__ uint16_t bf16_bits(float f) { return f32_to_bf16(f); 
 
 constexpr int kTileElems = kSwzTileElems;  // one unpadded K or V tile, bf16 elements
 
+// Waves raise their issue priority (s_setprio, arbitration only) while
+// they issue a tile's QK^T and P.V products, so that a wave with matrix
+// work ready issues it ahead of the softmax arithmetic of the other waves
+// on its SIMD (the matrix unit would otherwise idle behind it).
+//
 // One 64-key tile for the 16 query rows of this wave, in two stages that
 // every tile kind shares: the scores (qk_tile, or qk_tile_b with the mask
 // -- -inf for keys of the tile that are not candidates of the lane's row --
@@ -124,11 +129,13 @@ __device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[2], const Tile& t, 
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) a[dc][kb] = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, dc));
   f32x4_t c[4];
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
     c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0][kb], qf[0], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1][kb], qf[1], c[kb], 0, 0, 0);
+  __builtin_amdgcn_s_setprio(0);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -149,10 +156,12 @@ __device__ __forceinline__ void qk_tile_b(const bf16x8_t (&qf)[2], const Tile& t
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) a[dc][kb] = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, dc));
   f32x4_t c[4];
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0][kb], qf[0], bias[kb], 0, 0, 0);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1][kb], qf[1], c[kb], 0, 0, 0);
+  __builtin_amdgcn_s_setprio(0);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -290,11 +299,13 @@ __device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, floa
     for (int db = 0; db < 4; ++db) va[kc][db] = v_frag(t, kc, db);
   bf16x8_t pb[2];
   softmax_p(s, scale_log2, st, pb);
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
     for (int db = 0; db < 4; ++db)
       st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[kc][db], pb[kc], st.acc[db], 0, 0, 0);
+  __builtin_amdgcn_s_setprio(0);
 }
 
 __device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[2]) {
