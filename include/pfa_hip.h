@@ -378,6 +378,12 @@ int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
  * pfa_shortlist_attn_fwd's int8 mode.  ema: (P) f32, read and written in
  * mode 2 only.  The workspace is sized by pfa_quantize_heads_workspace_size
  * for the same P_cap, T, D and mode.
+ * Size limit of the reference (modes 1 and 2): the reference takes
+ * torch.quantile over the whole (P, T*D) tensor at once, which raises
+ * "quantile() input tensor is too large" above 2^24 elements (P*T*D >
+ * 16,777,216, e.g. 8 active heads x T = 65,536 x D = 64).  This entry point
+ * returns values there; they have no reference counterpart, and the oracle
+ * and golden cases stay below that size.
  * ==================================================================== */
 int pfa_quantize_heads_workspace_size(int P_cap, int64_t T, int D, int mode,
                                       size_t* bytes);

@@ -389,9 +389,14 @@ def quantize_per_head_int8(t: torch.Tensor, mode: str = "max", percentile: float
 # RoPE (aspa.py:576-618)
 # ---------------------------------------------------------------------------
 
-def rope_tables(T: int, D: int, base: float, dtype: torch.dtype):
-    inv = 1.0 / (base ** (torch.arange(0, D, 2, dtype=torch.float32) / max(D, 1)))
-    ang = torch.outer(torch.arange(T, dtype=torch.float32), inv)
+def rope_tables(T: int, D: int, base: float, dtype: torch.dtype, freq_dtype: torch.dtype = torch.float32):
+    """(cos, sin) of shape (T, D) in `dtype` (aspa.py:240-246, 576-604).
+    freq_dtype: the dtype of the module's inverse-frequency buffer, in which
+    the positions and angles are computed; a module cast to bf16 holds it in
+    bf16 (the buffer follows the module's dtype), so positions above 256
+    round before the angles are formed."""
+    inv = (1.0 / (base ** (torch.arange(0, D, 2, dtype=torch.float32) / max(D, 1)))).to(freq_dtype)
+    ang = torch.outer(torch.arange(T, dtype=freq_dtype), inv)
     return (torch.repeat_interleave(ang.cos(), 2, dim=-1).to(dtype),
             torch.repeat_interleave(ang.sin(), 2, dim=-1).to(dtype))
 

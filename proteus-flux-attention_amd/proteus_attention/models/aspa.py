@@ -1103,7 +1103,9 @@ class AdaptiveSparseAttention(nn.Module):
                 int(self.linear_L), float(self._linear_L_scale_runtime), self._shortlist_alpha_override,
                 str(self.mode_setting), int(self._choose_active_k(T)),
                 (float(self.token_keep_ratio_base), int(self.token_keep_min), int(self.token_keep_guard),
-                 str(self.linear_token_keep_schedule)) if self.token_sparse else None)
+                 str(self.linear_token_keep_schedule), int(self.linear_token_keep_ratio_ref),
+                 float(self.linear_token_keep_ratio_min), float(self._linear_token_keep_ratio(T)))
+                if self.token_sparse else None)
 
     def _capture_graph(self, x: torch.Tensor, key) -> dict:
         self._resolve_stats()

@@ -220,6 +220,40 @@ def chunk_cases(ref) -> None:
           keep_idx=ki, keep_scores=ks)
 
 
+def rope_case(ref) -> None:
+    """RoPE tables and rotation (aspa.py:226-247, 576-618) as the reference
+    module computes them on CPU: _rope_factors and _apply_rope_embedding of
+    modules cast to f32 and to bf16 (the cast turns the inverse-frequency
+    buffer into bf16 too, so positions above 256 round), head dims 64 and 32,
+    T = 1024.  The tables are stored whole; the seeded q/k (1, T, 2, D) and
+    their rotations at every 8th position.  bf16 arrays are stored as their
+    int16 bit patterns."""
+    ModelConfig = ref.models.aspa.ModelConfig
+    ASPA = ref.models.aspa.AdaptiveSparseAttention
+    g = torch.Generator().manual_seed(17)
+    T = 1024
+
+    def bits(t: torch.Tensor) -> np.ndarray:
+        t = t.detach().cpu().contiguous()
+        return t.view(torch.int16).numpy() if t.dtype == torch.bfloat16 else t.numpy()
+
+    arrays = {}
+    for D in (64, 32):
+        H = 256 // D
+        for dtype, tag in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+            m = ASPA(ModelConfig(d_model=256, n_head=H, attn_h_total=H, attn_gates=H)).to(dtype=dtype).eval()
+            cos, sin = m._rope_factors(T, torch.device("cpu"), dtype)
+            q = torch.randn(1, T, 2, D, generator=g).to(dtype)
+            k = torch.randn(1, T, 2, D, generator=g).to(dtype)
+            m.d_head = D
+            with torch.no_grad():
+                qo, ko = m._apply_rope_embedding(q, k)
+            key = f"D{D}_{tag}"
+            arrays.update({f"{key}_cos": bits(cos), f"{key}_sin": bits(sin), f"{key}_q": bits(q[:, ::8]),
+                           f"{key}_k": bits(k[:, ::8]), f"{key}_qo": bits(qo[:, ::8]), f"{key}_ko": bits(ko[:, ::8])})
+    _save("rope_tables", T=np.int64(T), base=np.float64(10000.0), every=np.int64(8), **arrays)
+
+
 def main() -> None:
     ref_root = Path(sys.argv[1]) if len(sys.argv) > 1 else Path("/root/reference")
     sys.path.insert(0, str(ref_root / "src"))
@@ -281,6 +315,7 @@ def module_cases():
             outlier=0.01, token_stride=8),
         # the drop-in module with its defaults, and in linear (shortlist) mode
         "nucleus_head_count": nucleus_case,
+        "rope_tables": rope_case,
         "dropin_mha_auto": lambda ref: dropin_case(ref, "dropin_mha_auto", 96, 70),
         "dropin_mha_linear": lambda ref: dropin_case(ref, "dropin_mha_linear", 300, 250, attn_mode="linear",
                                                      attn_linear_L=64, attn_linear_window=32),

@@ -88,6 +88,7 @@ def test_shortlist_forward_full_size_vs_oracle(dev, T, L, row_every, attn_every)
     ref = torch.zeros(B * T, H, dtype=torch.bool).scatter_(1, oidx, True)
     rep = check_routing(ours, ref, gates, og.reshape(B * T, H), x.reshape(B * T, C), w_router, 2)
     _say(f"T={T} routing vs oracle: {rep}")
+    rep.assert_boundary_sets_at_most(1e-3)
     N = int(tok.numel())
     assert N == 2 * B * T
 
@@ -174,3 +175,45 @@ def test_chunked_pipeline_config5_vs_oracle(dev, monkeypatch):
     _say(f"final pass on {qsel.numel()} sampled queries: max-abs err {err:.3e}")
     assert err <= TOL_BF16
     assert res.final_output.shape == (1, T, C) and bool(torch.isfinite(res.final_output.float()).all())
+
+
+def test_config5_final_pass_with_outlier_rows_vs_oracle(dev):
+    """Config 5 on config 3's outlier recipe: 1% of the input rows scaled by
+    4, so query-key scores between outlier rows are ~16x those of N(0,1)
+    rows and single keys dominate their queries' softmax.  The all-query
+    final pass computes tiles without a row maximum and keeps them only when
+    every lane's P sum lies in a safe range; the dominant-key rows must
+    still meet the bf16 bound.  The pipeline runs at full size (T = 2^20);
+    the sampled queries are every 1024th token plus the first 1,024 outlier
+    tokens."""
+    from configs import make_inputs
+
+    from proteus_attention.tools.chunked_shortlist import ChunkedShortlistConfig, ChunkedShortlistRunner
+
+    T, C, H, chunk, budget, buf = 1 << 20, 512, 8, 65536, 512, 8192
+    _say(f"chunked pipeline T={T} with 1% outlier rows x4")
+    x, g = make_inputs(1, T, C, seed=5, outlier_frac=0.01)
+    # the outlier positions, regenerated from the recipe (randperm after randn)
+    g2 = torch.Generator().manual_seed(5)
+    torch.randn(1, T, C, generator=g2)
+    outliers = torch.sort(torch.randperm(T, generator=g2)[: int(round(0.01 * T))]).values
+    xd = x.to(torch.bfloat16).to(dev)
+    del x
+    torch.manual_seed(7)
+    cfg = ChunkedShortlistConfig(seq_len=T, d_model=C, chunk_len=chunk, buffer_tokens=buf, per_chunk_budget=budget,
+                                 device=dev, heads=H, nucleus_top_p=1.0, final_mode="all_queries")
+    runner = ChunkedShortlistRunner(cfg)
+    res = runner.run(xd)
+    fp = runner.last_final_pass
+    k8, ksc, v8, vsc, pos = (t.cpu() for t in fp.last_shortlist)
+    kept_out = int(torch.isin(pos.long(), outliers).sum())
+    qsel = torch.unique(torch.cat([torch.arange(0, T, 1024), outliers[:1024]]))
+    q = fp.q_all[0].view(T, H, 64)[qsel.to(dev)].cpu()
+    ref = O.int8_kv_attention(q, k8, v8, ksc, vsc, pos, q_pos=qsel)
+    got = fp.last_attn.view(T, H, 64)[qsel.to(dev)].float().cpu()
+    err = float((got - ref).abs().max())
+    qmax = float(q.float().abs().max())
+    _say(f"outlier final pass: {kept_out} outlier tokens in the shortlist, |q| max {qmax:.2f}, "
+         f"{qsel.numel()} sampled queries: max-abs err {err:.3e}")
+    assert err <= TOL_BF16
+    assert bool(torch.isfinite(res.final_output.float()).all())

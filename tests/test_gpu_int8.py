@@ -166,6 +166,7 @@ def test_module_int8_vs_golden(dev, golden, name, dt, extra, structured):
                             torch.from_numpy(z["gate_probs"]).reshape(T, H), x.cpu().reshape(T, C),
                             m.head_router.linear.weight.detach().cpu(), 2)
         _say(f"{name}: {rep}")
+        rep.assert_boundary_sets_at_most(1e-3)
     sel = same[:, ::stride]
     refs = ([torch.from_numpy(z["y_first1"])] if n_fwd == 2 else []) + [torch.from_numpy(z["y"])]
     for i, (yo, yr) in enumerate(zip(ys, refs)):
@@ -178,3 +179,59 @@ def test_module_int8_vs_golden(dev, golden, name, dt, extra, structured):
             exp = torch.from_numpy(z[nm])
             assert got.shape == exp.shape
             assert torch.allclose(got, exp, rtol=1e-5, atol=1e-6), nm
+
+
+@pytest.mark.parametrize("mode,extra", [("max", {}),
+                                        ("ema_percentile", dict(attn_quantize_int8_mode="ema_percentile",
+                                                                attn_quantize_int8_percentile=0.99,
+                                                                attn_quantize_int8_ema_decay=0.8))])
+def test_module_int8_f32_same_inputs_vs_oracle(dev, mode, extra):
+    """The f32 int8 module path at the f32 bound (1e-4) on the same inputs:
+    the oracle is fed the device's own projection (the forward's GEMM), so
+    no int8 value can sit on the other side of a rounding boundary.  The
+    oracle then rotates q/k, quantises the active heads per head (first
+    forward: the EMA starts at the absmax), builds the candidates with the
+    C builder from this forward's similarities and rows, and attends in f32
+    (sparse_attention, the reference fallback with per-head scales).  Every
+    active row is compared; the golden comparison above covers the
+    reference's own projection."""
+    from configs import shortlist_cfg
+
+    from oracle import c_oracle
+
+    _say(f"module int8 f32 same inputs, {mode}")
+    B, T, C, H, D = 1, 2048, 512, 8, 64
+    cfg = dict(shortlist_cfg(T, C, H, 512, 128, 32), attn_quantize_int8=True, **extra)
+    m, x = _module(cfg, B, T, C, torch.float32, dev, 0.01)
+    with torch.no_grad():
+        m(x)
+        qkv = m.qkv(x).view(B, T, 3, H, D).cpu()
+        cos, sin = (t.cpu() for t in m._rope_factors(T, dev, torch.float32))
+    torch.cuda.synchronize()
+    st = m._last_sparse_state
+    tok = st["token_idx"].cpu().long()
+    offs = st["row_offsets"].cpu().long()
+    heads = st["active_head_indices"].cpu().long()
+    P = heads.numel()
+    row_head = torch.repeat_interleave(torch.arange(P), offs[1:] - offs[:-1])
+    q = O.apply_rope(qkv[:, :, 0], cos, sin).permute(0, 2, 1, 3).reshape(B * H, T, D)[heads]
+    k = O.apply_rope(qkv[:, :, 1], cos, sin).permute(0, 2, 1, 3).reshape(B * H, T, D)[heads]
+    v = qkv[:, :, 2].permute(0, 2, 1, 3).reshape(B * H, T, D)[heads]
+    pct = float(m.quantize_sparse_int8_percentile)
+    decay = float(m.quantize_sparse_int8_ema_decay)
+    q8, qs, _ = O.quantize_per_head_int8(q, mode, pct, None, decay)
+    k8, ks, _ = O.quantize_per_head_int8(k, mode, pct, None, decay)
+    v8, vs, _ = O.quantize_per_head_int8(v, mode, pct, None, decay)
+    plan = m._shortlist_plan(B, T, 1.0, torch.float32)
+    assert not plan["structured"]
+    sims = m._last_token_similarity.float().cpu()
+    cand, lens = c_oracle.shortlist_build(tok.numpy().astype(np.int32), None, T, plan["L"], plan["local_w"],
+                                          plan["stride"], plan["slots"], sims.numpy(), plan["K"])
+    ref = O.sparse_attention(q8, k8, v8, q_scale=qs, k_scale=ks, v_scale=vs,
+                             prepacked=(row_head, tok, offs.to(torch.int32), int((offs[1:] - offs[:-1]).max())),
+                             shortlist_candidates=torch.from_numpy(cand).long(),
+                             shortlist_lengths=torch.from_numpy(lens).long())
+    got = m.last_head_consensus.view(B, T, H, D).float().cpu().permute(0, 2, 1, 3).reshape(B * H, T, D)[heads]
+    err = float((got[row_head, tok] - ref[row_head, tok]).abs().max())
+    _say(f"int8 f32 {mode}: {tok.numel()} rows of {P} heads, max-abs err {err:.3e}")
+    assert err <= 1e-4

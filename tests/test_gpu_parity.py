@@ -345,6 +345,7 @@ def test_router_vs_golden_and_oracle(dev, golden, name, B, T, C, dt, outlier):
         ref_sets = torch.zeros(n, 8, dtype=torch.bool).scatter_(1, ridx, True)
         rep = check_routing(ours, ref_sets, gate, ref_g, x.to(dt).reshape(n, C), ws[0].to(dt), 2)
         _say(f"router {name}: {rep}")
+        rep.assert_boundary_sets_at_most(1e-3)
 
 
 @pytest.mark.parametrize("n_tok,C,G,dt", [(300_000, 512, 8, torch.bfloat16), (5000, 1025, 12, torch.float32),
@@ -807,6 +808,7 @@ def test_module_forward_vs_golden(dev, golden, name, maker, B, T, C, dt, outlier
                             torch.from_numpy(z["gate_probs"]).reshape(B * T, 8), x.cpu().reshape(B * T, C),
                             m.head_router.linear.weight.detach().cpu(), 2, tm)
         _say(f"{name}: {rep}")
+        rep.assert_boundary_sets_at_most(1e-3)
     stride = int(z["token_stride"])
     yr = torch.from_numpy(z["y"])
     yo = y.float().cpu()[:, ::stride]

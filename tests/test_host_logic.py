@@ -219,3 +219,27 @@ def test_disk_staging_rows_equal_float32_round_trip(tmp_path, dt):
     idx = torch.tensor([5, 999, 0, 3, 7])
     got = CS._memmap_rows(mm[idx.numpy()], store).to(dt)
     assert torch.equal(got.view(torch.uint8), ref[idx].contiguous().view(torch.uint8))
+
+
+def test_graph_key_follows_token_keep_schedule_knobs():
+    """A captured graph fixes the token keep count of a token-masked
+    forward; the key it is stored under changes with every knob the keep
+    ratio reads (linear_token_keep_ratio_ref and _min included), so a
+    changed knob captures a new graph instead of replaying the old count."""
+    from proteus_attention.tools.chunked_shortlist import _build_model_config
+
+    T = 24576
+    m = AdaptiveSparseAttention(_build_model_config(T, 512, heads=8, sparse_ratio=0.05, shortlist_alpha=0.0,
+                                                    router_top_p=1.0))
+    m.linear_token_keep_schedule = "sqrt"
+    m.linear_token_keep_ratio_min = 0.001
+    m.linear_token_keep_ratio_ref = 2048
+    x = torch.zeros(1, T, 512)
+    k0 = m._graph_key(x)
+    r0 = m._linear_token_keep_ratio(T)
+    m.linear_token_keep_ratio_ref = 4 * 2048
+    r1 = m._linear_token_keep_ratio(T)
+    assert r1 != r0 and m._graph_key(x) != k0
+    k1 = m._graph_key(x)
+    m.linear_token_keep_ratio_min = 0.04
+    assert m._linear_token_keep_ratio(T) != r1 and m._graph_key(x) != k1

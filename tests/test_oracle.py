@@ -367,3 +367,37 @@ def test_int8_kv_attention_oracle_matches_sdpa_and_brute_force():
     # non-causal: every key visible
     nc = O.int8_kv_attention(q, k8, v8, ks, vs, pos, causal=False)
     assert torch.allclose(nc.permute(1, 0, 2), F.scaled_dot_product_attention(q.permute(1, 0, 2), k, v), atol=1e-6)
+
+
+def _rope_golden(z, D, tag, name):
+    arr = torch.from_numpy(np.ascontiguousarray(z[f"D{D}_{tag}_{name}"]))
+    return arr.view(torch.bfloat16) if tag == "bf16" else arr
+
+
+@pytest.mark.parametrize("D", [64, 32])
+@pytest.mark.parametrize("tag", ["f32", "bf16"])
+def test_rope_oracle_and_module_tables_match_reference(golden, D, tag):
+    """oracle.rope_tables / apply_rope and the module's _rope_factors bit for
+    bit against the reference module's _rope_factors / _apply_rope_embedding
+    (aspa.py:226-247, 576-618) in f32 and in bf16 (the cast module computes
+    positions and angles in bf16), T = 1024."""
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    z = golden("rope_tables")
+    T, base, every = int(z["T"]), float(z["base"]), int(z["every"])
+    dt = torch.bfloat16 if tag == "bf16" else torch.float32
+    cos, sin = O.rope_tables(T, D, base, dt, freq_dtype=dt)
+    assert torch.equal(cos, _rope_golden(z, D, tag, "cos")) and torch.equal(sin, _rope_golden(z, D, tag, "sin"))
+    for a, b in (("q", "qo"), ("k", "ko")):
+        x = _rope_golden(z, D, tag, a)
+        got = O.apply_rope(x, cos[::every], sin[::every])
+        assert torch.equal(got, _rope_golden(z, D, tag, b)), (a, D, tag)
+    H = 256 // D
+    m = AdaptiveSparseAttention(ModelConfig(d_model=256, n_head=H, attn_h_total=H, attn_gates=H)).to(dt)
+    mc, ms = m._rope_factors(T, torch.device("cpu"), dt)
+    assert torch.equal(mc, cos) and torch.equal(ms, sin)
+    if tag == "bf16":
+        # planted mistake: angles formed in f32 (the buffer left in f32)
+        # round differently above position 256 and must not match
+        c32, _ = O.rope_tables(T, D, base, dt, freq_dtype=torch.float32)
+        assert not torch.equal(c32, _rope_golden(z, D, tag, "cos"))

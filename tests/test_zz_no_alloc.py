@@ -2,10 +2,13 @@
 
 Its per-(head, block) counts live in a static device array instead of a
 caller workspace.  The GPU test calls it through the C ABI and checks every
-output against pfa_pack_rows on the same input, on two calls in a row (the
-second with a smaller input, so stale scratch contents of the first call
-would show).  The CPU test checks that sizes beyond the static maximum are
-rejected before any device work.
+output against pfa_pack_rows on the same input, on calls in a row, each
+smaller than the one before (stale scratch contents of an earlier call
+would show), with sizes on both sides of the fused-scan limit (4,096
+(head, block) counts), so that the totals and compact-id regions of the
+static array are exercised as well as the block counts.  The CPU test
+checks that sizes beyond the static maximum are rejected before any device
+work.
 """
 from __future__ import annotations
 
@@ -60,8 +63,11 @@ def test_pack_rows_static_matches_workspace_entry_point(dev):
     from proteus_attention import _hip
 
     lib = _hip.lib()
-    # second call smaller than the first (fewer heads, blocks and rows)
-    for B, T, H, topk, masked, seed in ((2, 70_000, 8, 2, True, 1), (1, 3001, 6, 3, False, 2),
+    # each call smaller than the one before it (fewer heads, blocks or
+    # rows); the first two take the separate scan kernel (more than 4,096
+    # (head, block) counts: 4,688 and 4,416), the rest the fused scan
+    for B, T, H, topk, masked, seed in ((1, 600_000, 8, 2, True, 4), (4, 70_000, 16, 3, False, 5),
+                                        (2, 70_000, 8, 2, True, 1), (1, 3001, 6, 3, False, 2),
                                         (1, 65_536, 8, 2, False, 3)):
         print(f"[no_alloc] pack B={B} T={T} H={H} topk={topk} masked={masked}", flush=True)
         hidx, tmask = _routing(B, T, H, topk, masked, seed)
