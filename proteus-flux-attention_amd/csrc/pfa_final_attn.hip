@@ -6,9 +6,9 @@
 //
 // Every key is read by every 128-query tile of its head (8,192 tiles at
 // T = 2^20), so the shortlist is dequantised once per call, into bf16
-// working copies in the workspace (16 MB at H = 8, S = 8,192); the attention then streams
-// 64-key tiles of it by LDS DMA into the swizzled 128-byte-row layout of the
-// bf16 attention kernels (the V^T operand from the LDS transpose read), and
+// working copies in the workspace; the attention then streams 64-key tiles
+// of them by LDS DMA into the swizzled 128-byte-row layout of the bf16
+// attention kernels (the V^T operand from the LDS transpose read), and
 // S = Q K^T and O += P V run on v_mfma_f32_16x16x32_bf16 with an online
 // softmax in f32 registers.  (Dequantising inside every tile spent about 2 ms
 // of VALU time at config 5.)
@@ -21,17 +21,16 @@
 // (query, key).  Block b handles head b % H, so on 8 XCDs each XCD's L2
 // holds one head's K/V; tiles run heaviest first.
 //
-// Scores are in log2 units: the bf16 K copy carries the factor
-// scale * log2(e) (one rounding, of k8 * k_scale * scale * log2(e), where the
-// plain copy rounds k8 * k_scale).  An unmasked tile first runs without a
-// row maximum: the QK^T accumulators start at -m (m: the running reference
-// point of the row), so P = exp2(S) directly.  The tile is kept when every
-// lane's sum of its 16 P values lies in [2^-60, 2^20] (or the row already
-// has mass): no P overflows and none of the row's first mass underflows.
-// Otherwise the wave recomputes the tile on the exact path (tile maximum,
-// rescale of the accumulators when the maximum rises).  Either way
-// out = acc / l does not depend on m; only the bf16 rounding points of P
-// differ from a softmax taken at the exact maximum.
+// Precision.  Scores are in log2 units: K carries the factor
+// c = k_scale * scale * log2(e).  A single bf16 copy of k8 * c would round
+// every key element to 8 bits, and with large scores (rows of 4x the
+// typical norm, whose single keys dominate their queries) that moves a
+// score by tenths and the output by more than the bf16 tolerance.  So K is
+// held as two bf16 parts, hi = bf16(k8 * c) and lo = bf16(k8 * c - hi)
+// (their sum is k8 * c to about 2^-17), and every QK^T product is the sum of
+// two MFMA products; V likewise (hi/lo of v8 * v_scale).  The softmax takes
+// the exact row maximum (the dominant key's P is exactly 1), so what
+// remains is the bf16 rounding of P for the P.V product.
 #include "pfa_common.h"
 
 namespace pfa {
@@ -42,9 +41,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kQ = 32 * kWaves;  // queries per workgroup
 constexpr int kTile = kSwzKeys;  // keys per tile
 constexpr int kD = 64;
-constexpr float kRescaleLog2 = 0.0f;  // exact path: rescale when some row's max rises
-constexpr float kFastHi = 0x1p20f;     // fast path: largest lane sum of P kept
-constexpr float kFastLo = 0x1p-60f;    // fast path: smallest first mass of a row kept
+constexpr float kRescaleLog2 = 0.0f;  // rescale when some row's max rises
 
 #ifndef PFA_FIN_STAGES
 #define PFA_FIN_STAGES 2
@@ -56,8 +53,10 @@ struct Args {
   int64_t q_sh, q_st;
   uint16_t* out;
   int64_t o_sh, o_st;
-  const uint16_t* kb;  // dequantised shortlist, bf16 (H, S, 64)
+  const uint16_t* kb;  // dequantised shortlist, bf16 (H, S, 64): hi parts
   const uint16_t* vb;
+  const uint16_t* kl;  // lo parts
+  const uint16_t* vl;
   const int32_t* kpos;
   const int2* rng;
   int H, S, causal, nqt;
@@ -71,13 +70,15 @@ struct St {
 
 __device__ __forceinline__ float i8f(uint32_t w, int e) { return (float)(int)(int8_t)((w >> (8 * e)) & 0xffu); }
 
-// bf16(x8 * scale) for the (H*S, 64) rows of K and V: thread -> row idx/4,
-// elements 16*(idx%4) .. +15.
-// K rows carry the factor kmul = scale * log2(e): bf16(x8 * (k_scale * kmul)).
+// hi = bf16(x8 * scale) and lo = bf16(x8 * scale - hi) for the (H*S, 64)
+// rows of K and V: thread -> row idx/4, elements 16*(idx%4) .. +15.  K rows
+// carry the factor kmul = scale * log2(e): x8 * (k_scale * kmul).
 __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__ k8, const int8_t* __restrict__ v8,
                                                       const float* __restrict__ ks, const float* __restrict__ vs,
-                                                      int64_t rows, float kmul, uint16_t* __restrict__ kb,
-                                                      uint16_t* __restrict__ vb) {
+                                                      int64_t rows, float kmul, uint16_t* __restrict__ kh,
+                                                      uint16_t* __restrict__ vh, uint16_t* __restrict__ kl,
+                                                      uint16_t* __restrict__ vl) {
+#pragma clang fp contract(off)
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= rows * 4) return;
   const int64_t row = idx >> 2;
@@ -87,25 +88,27 @@ __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__
   const float kscale = ks[row] * kmul, vscale = vs[row];
   const uint32_t kw4[4] = {k.x, k.y, k.z, k.w};
   const uint32_t vw4[4] = {v.x, v.y, v.z, v.w};
-  __bf16 kd[16], vd[16];
+  __bf16 kd[16], vd[16], kr[16], vr[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    kd[e] = (__bf16)(i8f(kw4[e >> 2], e & 3) * kscale);
-    vd[e] = (__bf16)(i8f(vw4[e >> 2], e & 3) * vscale);
+    const float kf = i8f(kw4[e >> 2], e & 3) * kscale;
+    const float vf = i8f(vw4[e >> 2], e & 3) * vscale;
+    kd[e] = (__bf16)kf;
+    vd[e] = (__bf16)vf;
+    kr[e] = (__bf16)(kf - (float)kd[e]);  // exact difference, rounded once
+    vr[e] = (__bf16)(vf - (float)vd[e]);
   }
-  uint4 kw[2], vw[2];
-  __builtin_memcpy(kw, kd, 32);
-  __builtin_memcpy(vw, vd, 32);
-  uint4* ko = reinterpret_cast<uint4*>(kb + row * kD + 16 * qd);
-  uint4* vo = reinterpret_cast<uint4*>(vb + row * kD + 16 * qd);
-  ko[0] = kw[0];
-  ko[1] = kw[1];
-  vo[0] = vw[0];
-  vo[1] = vw[1];
+  const int64_t off = row * kD + 16 * qd;
+  __builtin_memcpy(kh + off, kd, 32);
+  __builtin_memcpy(vh + off, vd, 32);
+  __builtin_memcpy(kl + off, kr, 32);
+  __builtin_memcpy(vl + off, vr, 32);
 }
 
-// O += P V for the tile (P rounded to bf16).
-__device__ __forceinline__ void pv_accumulate(const float (&s)[2][16], const SwzTile& tl, St (&st)[2]) {
+// O += P V for the tile (P rounded to bf16), V as the sum of its hi part
+// (tile th) and lo part (tile tl).
+__device__ __forceinline__ void pv_accumulate(const float (&s)[2][16], const SwzTile& th, const SwzTile& tl,
+                                              St (&st)[2]) {
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
     bf16x8_t pb[2];
@@ -120,35 +123,46 @@ __device__ __forceinline__ void pv_accumulate(const float (&s)[2][16], const Swz
       __builtin_memcpy(&pb[gr], pv, 16);
     }
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      // V^T: lane (dim 16db + lane%16, g) holds keys 32kc + 4g + (0..3) and
-      // 32kc + 16 + 4g + (0..3), matching pb
-      const i16x4_t lo = ds_tr4(tl.vtr(kc, 0, db));
-      const i16x4_t hi = ds_tr4(tl.vtr(kc, 1, db));
-      bf16x8_t va;
-      __builtin_memcpy(&va, &lo, 8);
-      __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
+    for (int part = 0; part < 2; ++part) {
+      const SwzTile& t = part ? tl : th;
 #pragma unroll
-      for (int gr = 0; gr < 2; ++gr)
-        st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gr], st[gr].acc[db], 0, 0, 0);
+      for (int db = 0; db < 4; ++db) {
+        // V^T: lane (dim 16db + lane%16, g) holds keys 32kc + 4g + (0..3) and
+        // 32kc + 16 + 4g + (0..3), matching pb
+        const i16x4_t lo = ds_tr4(t.vtr(kc, 0, db));
+        const i16x4_t hi = ds_tr4(t.vtr(kc, 1, db));
+        bf16x8_t va;
+        __builtin_memcpy(&va, &lo, 8);
+        __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
+#pragma unroll
+        for (int gr = 0; gr < 2; ++gr)
+          st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gr], st[gr].acc[db], 0, 0, 0);
+      }
     }
   }
 }
 
-// Exact path: the tile's row maxima, rescaling when one rises.  kpos: the
-// shortlist's positions (global; read only in masked tiles).
+// One 64-key tile: scores from the hi and lo parts of K, the tile's row
+// maxima (rescaling when one rises), P, and the P.V products.  MASKED:
+// keys past S or (causal) after the query's position are dropped; kpos is
+// the shortlist's positions (global; read only in masked tiles).
 template <bool MASKED>
-__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& tl, const int32_t* kpos, int key0,
-                                     int S, int causal, const int (&tq)[2], St (&st)[2]) {
+__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& th, const SwzTile& tl,
+                                     const int32_t* kpos, int key0, int S, int causal, const int (&tq)[2],
+                                     St (&st)[2]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   float s[2][16];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 0));
-    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 1));
+    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(th.kfrag(kb, 0));
+    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(th.kfrag(kb, 1));
+    const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 0));
+    const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 1));
 #pragma unroll
     for (int gr = 0; gr < 2; ++gr) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b0, qf[gr][0], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b1, qf[gr][1], c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[gr][0], c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[gr][1], c, 0, 0, 0);
 #pragma unroll
@@ -191,51 +205,7 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& 
     }
     st[gr].l += psum;
   }
-  pv_accumulate(s, tl, st);
-}
-
-// Fast path of an unmasked tile: no row maximum.  Returns false, with the
-// state untouched, when some lane's P fall outside the kept range (the
-// caller then runs the exact path on the same tile).
-__device__ __forceinline__ bool tile_fast(const bf16x8_t (&qf)[2][2], const SwzTile& tl, St (&st)[2]) {
-  // the QK^T accumulators start at -m (0 while m is -inf)
-  f32x4_t negm[2];
-#pragma unroll
-  for (int gr = 0; gr < 2; ++gr) {
-    const float nm = st[gr].m == -INFINITY ? 0.f : -st[gr].m;
-    negm[gr] = f32x4_t{nm, nm, nm, nm};
-  }
-  float s[2][16];
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 0));
-    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 1));
-#pragma unroll
-    for (int gr = 0; gr < 2; ++gr) {
-      f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[gr][0], negm[gr], 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[gr][1], c, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[gr][4 * kb + i] = __builtin_amdgcn_exp2f(c[i]);
-    }
-  }
-  float psum[2];
-  bool bad = false;
-#pragma unroll
-  for (int gr = 0; gr < 2; ++gr) {
-    float a = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) a += s[gr][i];
-    psum[gr] = a;
-    bad = bad || !(a <= kFastHi) || (a < kFastLo && st[gr].l == 0.f);
-  }
-  if (__ballot(bad) != 0) return false;
-#pragma unroll
-  for (int gr = 0; gr < 2; ++gr) {
-    st[gr].l += psum[gr];
-    if (st[gr].m == -INFINITY) st[gr].m = 0.f;  // the reference point 0 was used
-  }
-  pv_accumulate(s, tl, st);
-  return true;
+  pv_accumulate(s, th, tl, st);
 }
 
 __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restrict__ kpos, int S, int64_t T,
@@ -264,14 +234,12 @@ __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restri
   rng[qt] = make_int2(below, lo);
 }
 
-// two 4-wave workgroups per CU (up to 256 VGPRs): measured 1.5% faster than
-// three with 168 VGPRs, where the fast and exact paths spill
-#ifndef PFA_FIN_WAVES
-#define PFA_FIN_WAVES 2
-#endif
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PFA_FIN_WAVES, 8)))
+// two 4-wave workgroups per CU: each holds two 32 KB stages of hi and lo
+// K/V tiles (64 KB of LDS), so two fit a CU
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
 final_attn_kernel(Args a) {
-  __shared__ __align__(16) uint16_t ring[kStages][2 * kSwzTileElems];
+  // a stage: K hi, V hi, K lo, V lo (64 rows of 128 bytes each)
+  __shared__ __align__(16) uint16_t ring[kStages][4 * kSwzTileElems];
 
   const int bid = blockIdx.x;
   const int h = bid % a.H;
@@ -291,16 +259,21 @@ final_attn_kernel(Args a) {
     tq[gr] = (int)(qv[gr] ? t : a.T - 1);
   }
   // per-head bases, wave-uniform (scalar registers for the DMA)
-  const uint16_t* kbh = a.kb + (int64_t)__builtin_amdgcn_readfirstlane(h) * a.S * kD;
-  const uint16_t* vbh = a.vb + (int64_t)__builtin_amdgcn_readfirstlane(h) * a.S * kD;
+  const int64_t hoff = (int64_t)__builtin_amdgcn_readfirstlane(h) * a.S * kD;
+  const uint16_t* kbh = a.kb + hoff;
+  const uint16_t* vbh = a.vb + hoff;
+  const uint16_t* klh = a.kl + hoff;
+  const uint16_t* vlh = a.vl + hoff;
   const int ntile = (rg.y + kTile - 1) / kTile;
   const int drow = tid >> 3;  // this thread's DMA rows: drow and drow + 32
   const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + 1024u * (uint32_t)wid);
-  constexpr uint32_t kStageBytes = 2 * kSwzTileElems * 2;
+  constexpr uint32_t kStageBytes = 4 * kSwzTileElems * 2;
   auto request = [&](int i) {
     const int k0 = kTile * i;
-    dma_tile_rows64(kbh, vbh, min(k0 + drow, a.S - 1), min(k0 + drow + 32, a.S - 1),
-                    ring_w + kStageBytes * (uint32_t)(i % kStages));
+    const int ka = min(k0 + drow, a.S - 1), kz = min(k0 + drow + 32, a.S - 1);
+    const uint32_t st0 = ring_w + kStageBytes * (uint32_t)(i % kStages);
+    dma_tile_rows64(kbh, vbh, ka, kz, st0);
+    dma_tile_rows64(klh, vlh, ka, kz, st0 + 4 * kSwzTileElems);
   };
 #pragma unroll
   for (int i = 0; i < kStages - 1; ++i)
@@ -329,7 +302,7 @@ final_attn_kernel(Args a) {
   // every wave is done with tile i-1, whose stage takes tile i+kStages-1
   auto next = [&](int i) {
     if (kStages == 3 && i + 1 < ntile)
-      dma_wait_barrier<kDmaPerTile>();
+      dma_wait_barrier<2 * kDmaPerTile>();
     else
       dma_wait_barrier<0>();
     if (i + kStages - 1 < ntile) request(i + kStages - 1);
@@ -339,13 +312,13 @@ final_attn_kernel(Args a) {
   const int nfull = min(rg.x / kTile, ntile);
   for (int i = 0; i < nfull; ++i) {
     next(i);
-    const SwzTile tl{ring[i % kStages], L};
-    if (!tile_fast(qf, tl, st)) tile<true>(qf, tl, a.kpos, kTile * i, a.S, a.causal, tq, st);
+    const SwzTile th{ring[i % kStages], L}, tl{ring[i % kStages] + 2 * kSwzTileElems, L};
+    tile<false>(qf, th, tl, a.kpos, kTile * i, a.S, a.causal, tq, st);
   }
   for (int i = nfull; i < ntile; ++i) {
     next(i);
-    const SwzTile tl{ring[i % kStages], L};
-    tile<true>(qf, tl, a.kpos, kTile * i, a.S, a.causal, tq, st);
+    const SwzTile th{ring[i % kStages], L}, tl{ring[i % kStages] + 2 * kSwzTileElems, L};
+    tile<true>(qf, th, tl, a.kpos, kTile * i, a.S, a.causal, tq, st);
   }
   uint16_t* oh = a.out + (int64_t)h * a.o_sh;
 #pragma unroll
@@ -373,6 +346,7 @@ final_attn_kernel(Args a) {
 using namespace pfa;
 
 // workspace: the query tiles' key ranges, then the bf16 K and V copies
+// (hi parts, then lo parts)
 static size_t fin_rng_bytes(int64_t T) {
   const int64_t nqt = (T + fin::kQ - 1) / fin::kQ;
   return ((size_t)(nqt > 0 ? nqt : 1) * sizeof(int2) + 255) / 256 * 256;
@@ -382,7 +356,7 @@ static size_t fin_copy_bytes(int H, int S) { return ((size_t)H * (size_t)S * fin
 extern "C" int pfa_int8_kv_attn_workspace_size(int64_t T, int H, int S, size_t* bytes) {
   clear_error();
   PFA_CHECK_ARG(bytes && T >= 0 && H >= 0 && S >= 0, "pfa_int8_kv_attn_workspace_size: bad arguments");
-  *bytes = fin_rng_bytes(T) + 2 * fin_copy_bytes(H, S);
+  *bytes = fin_rng_bytes(T) + 4 * fin_copy_bytes(H, S);
   return PFA_OK;
 }
 
@@ -410,9 +384,11 @@ extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, i
   int2* rng = (int2*)workspace;
   uint16_t* kbf = (uint16_t*)((char*)workspace + fin_rng_bytes(T));
   uint16_t* vbf = (uint16_t*)((char*)kbf + fin_copy_bytes(H, S));
+  uint16_t* klf = (uint16_t*)((char*)vbf + fin_copy_bytes(H, S));
+  uint16_t* vlf = (uint16_t*)((char*)klf + fin_copy_bytes(H, S));
   const int64_t rows = (int64_t)H * S;
-  fin::dequant_kernel<<<(unsigned)((rows * 4 + 255) / 256), 256, 0, s>>>(k8, v8, k_scale, v_scale, rows,
-                                                                       scale * 1.4426950408889634f, kbf, vbf);
+  fin::dequant_kernel<<<(unsigned)((rows * 4 + 255) / 256), 256, 0, s>>>(
+      k8, v8, k_scale, v_scale, rows, scale * 1.4426950408889634f, kbf, vbf, klf, vlf);
   PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/dequant");
   fin::key_ranges_kernel<<<(unsigned)((nqt + 255) / 256), 256, 0, s>>>(key_pos, S, T, nqt, causal ? 1 : 0, rng);
   PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/ranges");
@@ -425,6 +401,8 @@ extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, i
   a.o_st = out.s_t;
   a.kb = kbf;
   a.vb = vbf;
+  a.kl = klf;
+  a.vl = vlf;
   a.kpos = key_pos;
   a.rng = rng;
   a.H = H;

@@ -181,9 +181,10 @@ def test_config5_final_pass_with_outlier_rows_vs_oracle(dev):
     """Config 5 on config 3's outlier recipe: 1% of the input rows scaled by
     4, so query-key scores between outlier rows are ~16x those of N(0,1)
     rows and single keys dominate their queries' softmax.  The all-query
-    final pass computes tiles without a row maximum and keeps them only when
-    every lane's P sum lies in a safe range; the dominant-key rows must
-    still meet the bf16 bound.  The pipeline runs at full size (T = 2^20);
+    final pass holds K and V as hi/lo bf16 pairs and takes the exact row
+    maximum, so the dominant-key rows must still meet the bf16 bound (a
+    single bf16 copy of the scaled K moved such scores by tenths and the
+    outputs by ~0.1).  The pipeline runs at full size (T = 2^20);
     the sampled queries are every 1024th token plus the first 1,024 outlier
     tokens."""
     from configs import make_inputs
@@ -211,9 +212,19 @@ def test_config5_final_pass_with_outlier_rows_vs_oracle(dev):
     q = fp.q_all[0].view(T, H, 64)[qsel.to(dev)].cpu()
     ref = O.int8_kv_attention(q, k8, v8, ksc, vsc, pos, q_pos=qsel)
     got = fp.last_attn.view(T, H, 64)[qsel.to(dev)].float().cpu()
-    err = float((got - ref).abs().max())
+    # The output is bf16: around |out| = 8..10 its grid spacing is 2^-4, so
+    # the bf16 value nearest to the f32 result may itself be 2^-5 away.  Each
+    # element is held to the bf16 bound plus half the bf16 spacing at its
+    # reference value (the output's own rounding).
+    d = (got - ref).abs()
+    half_ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -126))) - 8.0)
+    excess = float((d - half_ulp).max())
+    err = float(d.max())
+    wi = int(d.argmax())
     qmax = float(q.float().abs().max())
     _say(f"outlier final pass: {kept_out} outlier tokens in the shortlist, |q| max {qmax:.2f}, "
-         f"{qsel.numel()} sampled queries: max-abs err {err:.3e}")
-    assert err <= TOL_BF16
+         f"{qsel.numel()} sampled queries: max-abs err {err:.3e} (got {float(got.flatten()[wi]):.5f}, "
+         f"ref {float(ref.flatten()[wi]):.5f}), |ref| max {float(ref.abs().max()):.3f}; beyond the output's own "
+         f"rounding {excess:.3e}; elements above 2e-2: {int((d > TOL_BF16).sum())} of {d.numel()}")
+    assert excess <= TOL_BF16
     assert bool(torch.isfinite(res.final_output.float()).all())
