@@ -3,20 +3,25 @@
 // Prototype prefix top-k (replaces the O(rows*T) masked torch.topk of
 // sparse_attn.py:260-300).  For batch b and token t the set S(t) is the
 // min(t+1, K) largest scores among positions 0..t under the order "larger
-// value first, equal values -> smaller index first".  Tokens are cut into
-// blocks of 64 and blocks into superblocks of `sbs` blocks:
-//   1. block_sort : each block's scores sorted best first (wave bitonic);
-//   2. sb_local   : per superblock, one workgroup folds its blocks in order:
-//                   Q[j] = top-K of the superblock's tokens up to block j;
-//   3. scan_round : a log-depth scan over the superblock totals (ceil(log2
-//                   nsb) rounds, every superblock in parallel):
-//                   R[s] = top-K of all tokens before superblock s;
-//   4. block_walk : per block j, P = top-K(R[s] U Q[j-1]) = S(64j - 1) is
-//                   written as the block's set table row (best first, or
-//                   sorted by index when the per-token sets are wanted), and
-//                   the block's tokens are resolved in parallel from exact
-//                   rank counts (below);
-//   5. expand     : (optional) S(t) for every token, sorted by index.
+// value first, equal values -> smaller index first".  Scores map to 64-bit
+// keys (order-preserving bits of the value, then the complemented index),
+// distinct and ordered as that rule orders them.  Tokens are cut into
+// blocks of 64 and blocks into superblocks of SB tokens; three launches:
+//   1. sb_top    : per superblock, its top-K keys (a radix select of the
+//                  K-th largest key over the superblock's keys, staged in
+//                  LDS, then every key at or above it), in any order;
+//   2. sb_prefix : per superblock s, R[s] = top-K of the earlier
+//                  superblocks' lists (= the set entering s) and its K-th
+//                  key th[s];
+//   3. walk      : per block j of superblock s, P = S(64j - 1) = top-K of
+//                  R[s] and the tokens of s before the block whose key is at
+//                  least th[s] (the K-th best key of a prefix only rises, so
+//                  no other token can be in P), selected in LDS and sorted
+//                  best first.  P is written as the block's set table row
+//                  (best first, or sorted by index when the per-token sets
+//                  are wanted), and the block's tokens are resolved in
+//                  parallel from exact rank counts (below);
+//   3. expand : (optional) S(t) for every token, sorted by index.
 //
 // Block walk without a sequential loop.  Let P be the set entering block j
 // (sorted best first, n = |P| <= K) and B the block's tokens.  A token t
@@ -42,353 +47,410 @@
 namespace pfa {
 
 constexpr int kBlk = 64;  // tokens per prefix block (one wave)
+constexpr int kBins = 2048;  // radix-select histogram bins (11-bit digits)
 
-// Superblock size: the local fold is a sequential chain of sbs merges, the
-// superblock scan takes ceil(log2(nb / sbs)) parallel rounds.
-static int64_t prefix_sbs(int64_t nb) {
-  return nb < 8 ? (nb > 0 ? nb : 1) : 8;
+// Superblock size: the smallest power of two in [1024, 4096] whose lists
+// (ceil(T/SB) of min(K, SB) keys) fit the LDS stage of sb_prefix; a sort of
+// SB keys runs in one workgroup, so smaller superblocks spread the sorting
+// over more CUs.
+constexpr int kPrefixStage = 16384;  // list keys staged in LDS by sb_prefix (128 KB)
+static int64_t prefix_sb_tokens(int64_t T, int K) {
+  for (int64_t sb = 1024; sb < 4096; sb <<= 1)
+    if ((T + sb - 1) / sb * (sb < K ? sb : (int64_t)K) <= kPrefixStage) return sb;
+  return 4096;
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct PrefixWs {
-  float* bval;
-  int32_t* bidx;
-  int32_t* blen;
-  float* qval;
-  int32_t* qidx;
-  int32_t* qlen;
-  float* rval;  // (B, nsb+1, K): row s+1 = top-K of superblocks 0..s, row 0 empty
-  int32_t* ridx;
-  int32_t* rlen;
-  float* r2val;  // ping-pong partner of rval/ridx/rlen for the log-depth scan
-  int32_t* r2idx;
-  int32_t* r2len;
+  uint64_t* skey;  // (B, nsb, SB) each superblock's keys, best first
+  uint64_t* rkey;  // (B, nsb, K) R[s]: top-K of the superblocks before s, best first
+  int32_t* rlen;   // (B, nsb)
   int32_t* blk;    // (B, nb, K) set table (used by pfa_proto_prefix_topk)
   int32_t* evict;  // (B, T) (used when the caller passes no evict array)
 };
 
-static size_t prefix_ws_bytes(int64_t B, int64_t T, int64_t nb, int64_t nsb, int64_t K, PrefixWs* w, char* base) {
+static size_t prefix_ws_bytes(int64_t B, int64_t T, int64_t nb, int64_t nsb, int64_t SB, int64_t K, PrefixWs* w,
+                              char* base) {
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return base ? base + o : nullptr; };
   char* p;
-  p = take((size_t)B * nb * kBlk * 4); if (w) w->bval = (float*)p;
-  p = take((size_t)B * nb * kBlk * 4); if (w) w->bidx = (int32_t*)p;
-  p = take((size_t)B * nb * 4);        if (w) w->blen = (int32_t*)p;
-  p = take((size_t)B * nb * K * 4);    if (w) w->qval = (float*)p;
-  p = take((size_t)B * nb * K * 4);    if (w) w->qidx = (int32_t*)p;
-  p = take((size_t)B * nb * 4);        if (w) w->qlen = (int32_t*)p;
-  p = take((size_t)B * (nsb + 1) * K * 4);   if (w) w->rval = (float*)p;
-  p = take((size_t)B * (nsb + 1) * K * 4);   if (w) w->ridx = (int32_t*)p;
-  p = take((size_t)B * (nsb + 1) * 4);       if (w) w->rlen = (int32_t*)p;
-  p = take((size_t)B * (nsb + 1) * K * 4);   if (w) w->r2val = (float*)p;
-  p = take((size_t)B * (nsb + 1) * K * 4);   if (w) w->r2idx = (int32_t*)p;
-  p = take((size_t)B * (nsb + 1) * 4);       if (w) w->r2len = (int32_t*)p;
+  p = take((size_t)B * nsb * SB * 8);  if (w) w->skey = (uint64_t*)p;
+  p = take((size_t)B * nsb * K * 8);   if (w) w->rkey = (uint64_t*)p;
+  p = take((size_t)B * nsb * 4);       if (w) w->rlen = (int32_t*)p;
   p = take((size_t)B * nb * K * 4);    if (w) w->blk = (int32_t*)p;
   p = take((size_t)B * T * 4);         if (w) w->evict = (int32_t*)p;
   return off;
 }
 
-// Sort (v, i) across the 64 lanes of a wave: best first.
-__device__ __forceinline__ void wave_bitonic_best_first(float& v, int& i) {
-  const int lane = threadIdx.x & 63;
+// Order-preserving key of (score, position): larger key = better under
+// `better` (value desc, then position asc; NaN below everything, two NaNs by
+// position; -0 and +0 equal).  Every real key is > 0 (the complemented
+// position is >= 2^31), so 0 pads.
+__device__ __forceinline__ uint64_t score_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t ord;
+  if (v != v) ord = 0u;
+  else if (v == 0.f) ord = 0x80000000u;
+  else ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(~(uint32_t)idx);
+}
+__device__ __forceinline__ int key_index(uint64_t k) { return (int)(~(uint32_t)k); }
+__device__ __forceinline__ float key_value(uint64_t k) {
+  const uint32_t ord = (uint32_t)(k >> 32);
+  const uint32_t u = (ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord;  // ord 0 -> a NaN
+  return __uint_as_float(u);
+}
+
+// Radix select over the keys get(i), i < n, in one workgroup of NT threads
+// (256 or 1024): returns a threshold th such that exactly `need` keys are
+// >= th (need <= the number of keys, keys distinct).  The digits start at
+// the highest bit in which the keys differ (found first: the OR of every key
+// XOR the first one), so that keys concentrated in a narrow value range
+// still spread over the bins; digits of 11 bits, down to bit 0, stopping at
+// the first digit whose chosen bin holds exactly the keys still needed.
+// hist: kBins LDS words; sh: NT/64 (at least 4) LDS words; sx: NT/64 LDS u64.
+template <int NT, typename Get>
+__device__ __forceinline__ uint64_t block_select(int n, int need, Get get, uint32_t* hist, int* sh, uint64_t* sx) {
+  constexpr int NW = NT / 64, BPT = kBins / NT;  // waves, bins per thread
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // highest differing bit
+  const uint64_t k0 = get(0);  // a real key (the first candidate always is)
+  uint64_t x = 0;
+  for (int i = tid; i < n; i += NT) {
+    const uint64_t k = get(i);
+    if (k != 0ull) x |= k ^ k0;  // padding (0) is below every real key and never selected
+  }
 #pragma unroll
-  for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      float pv = __shfl_xor(v, j, 64);
-      int pi = __shfl_xor(i, j, 64);
-      bool up = (lane & k) == 0;
-      bool lower = (lane & j) == 0;
-      bool self_better = better(v, i, pv, pi);
-      bool keep = (lower == up) ? self_better : !self_better;
-      if (!keep) { v = pv; i = pi; }
-    }
-  }
-}
-
-__global__ void __launch_bounds__(64)
-prefix_block_sort(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int K,
-                  float* __restrict__ oval, int32_t* __restrict__ oidx, int32_t* __restrict__ olen,
-                  int32_t* __restrict__ evict) {
-  PFA_CRITICAL_CHAIN_PRIORITY();
-  const int j = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  int64_t t = (int64_t)j * kBlk + lane;
-  if (t < T) evict[(int64_t)b * T + t] = INT32_MAX;
-  float v = -INFINITY;
-  int i = INT32_MAX;
-  if (t < T) { v = scores[(int64_t)b * stride + t]; i = (int)t; }
-  wave_bitonic_best_first(v, i);
-  int64_t n = T - (int64_t)j * kBlk;
-  if (n > kBlk) n = kBlk;
-  if (n > K) n = K;
-  int64_t base = ((int64_t)b * nb + j) * kBlk;
-  if (lane < n) { oval[base + lane] = v; oidx[base + lane] = i; }
-  if (lane == 0) olen[(int64_t)b * nb + j] = (int)n;
-}
-
-// Element p of top-K(a U c) for best-first lists a (na) and c (nc), by a
-// merge-path co-rank.  Either list may live in LDS or global memory.
-__device__ __forceinline__ void merge_at(int p, const float* av, const int32_t* ai, int na, const float* cv,
-                                         const int32_t* ci, int nc, float& ov, int32_t& oi) {
-  int lo = max(0, p - nc), hi = min(p, na);
-  while (lo < hi) {
-    int mid = (lo + hi) >> 1;
-    if (better(av[mid], ai[mid], cv[p - 1 - mid], ci[p - 1 - mid])) lo = mid + 1;
-    else hi = mid;
-  }
-  const int ia = lo, ic = p - lo;
-  const bool take_a = ia < na && (ic >= nc || better(av[ia], ai[ia], cv[ic], ci[ic]));
-  ov = take_a ? av[ia] : cv[ic];
-  oi = take_a ? ai[ia] : ci[ic];
-}
-
-// Q[j] = top-K(Q[j-1] U block j) within each superblock (one workgroup).
-// With `preload` every block list of the superblock is staged in LDS up
-// front (one burst of loads); otherwise the next block is fetched one step
-// ahead.  The sequential chain then runs on LDS only.
-__global__ void __launch_bounds__(256)
-prefix_sb_local(int nb, int sbs, int K, int preload, const float* __restrict__ bval,
-                const int32_t* __restrict__ bidx, const int32_t* __restrict__ blen, float* __restrict__ qval,
-                int32_t* __restrict__ qidx, int32_t* __restrict__ qlen) {
-  PFA_CRITICAL_CHAIN_PRIORITY();
-  extern __shared__ char smem[];
-  float* cv0 = (float*)smem;
-  int32_t* ci0 = (int32_t*)(cv0 + K);
-  float* cv1 = (float*)(ci0 + K);
-  int32_t* ci1 = (int32_t*)(cv1 + K);
-  const int nslot = preload ? sbs : 2;
-  float* kv = (float*)(ci1 + K);  // nslot x kBlk
-  int32_t* ki = (int32_t*)(kv + nslot * kBlk);
-  int32_t* kn = ki + nslot * kBlk;  // nslot lengths
-  const int sb = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int j0 = sb * sbs, j1 = min(nb, j0 + sbs);
-  if (j0 >= j1) return;
-  const int cnt = j1 - j0;
-  const int nfirst = preload ? cnt : 1;
-  for (int e = tid; e < nfirst * kBlk; e += 256) {
-    const int jj = e / kBlk, l = e % kBlk;
-    const int64_t row = (int64_t)b * nb + j0 + jj;
-    const int nbl = blen[row];
-    if (l < nbl) { kv[jj * kBlk + l] = bval[row * kBlk + l]; ki[jj * kBlk + l] = bidx[row * kBlk + l]; }
-    if (l == 0) kn[jj] = nbl;
-  }
+  for (int o = 32; o >= 1; o >>= 1) x |= __shfl_xor(x, o, 64);
+  if (lane == 0) sx[wid] = x;
   __syncthreads();
-  int n = 0, cur = 0;
-  for (int i = 0; i < cnt; ++i) {
-    const int j = j0 + i;
-    const int slot = preload ? i : (i & 1);
-    float pv = 0.f;
-    int32_t pi = 0;
-    int pn = 0;
-    if (!preload && i + 1 < cnt) {
-      const int64_t nrow = (int64_t)b * nb + j + 1;
-      pn = blen[nrow];
-      if (tid < pn) { pv = bval[nrow * kBlk + tid]; pi = bidx[nrow * kBlk + tid]; }
-    }
-    const int64_t row = (int64_t)b * nb + j;
-    const int nbl = kn[slot];
-    const float* bv = kv + slot * kBlk;
-    const int32_t* bi = ki + slot * kBlk;
-    const int m = min(K, n + nbl);
-    const float* av = cur ? cv1 : cv0;
-    const int32_t* ai = cur ? ci1 : ci0;
-    float* ov = cur ? cv0 : cv1;
-    int32_t* oi = cur ? ci0 : ci1;
-    for (int p = tid; p < m; p += 256) {
-      float vv;
-      int32_t ii;
-      merge_at(p, av, ai, n, bv, bi, nbl, vv, ii);
-      ov[p] = vv;
-      oi[p] = ii;
-      qval[row * K + p] = vv;
-      qidx[row * K + p] = ii;
-    }
-    if (tid == 0) qlen[row] = m;
-    if (!preload && i + 1 < cnt) {
-      const int ns = (i + 1) & 1;
-      if (tid < pn) { kv[ns * kBlk + tid] = pv; ki[ns * kBlk + tid] = pi; }
-      if (tid == 0) kn[ns] = pn;
+  x = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) x |= sx[w2];
+  __syncthreads();
+  int top = x ? 63 - __clzll((long long)x) : 0;  // digits cover bits top .. 0
+  uint64_t pmask = top < 63 ? ~((2ull << top) - 1ull) : 0ull;  // bits above top: common to every key
+  uint64_t pval = k0 & pmask;
+  while (true) {
+    const int bits = top + 1 < 11 ? top + 1 : 11;
+    const int shift = top + 1 - bits;
+    const uint32_t dmask = (1u << bits) - 1u;
+    for (int e = tid; e < kBins; e += NT) hist[e] = 0u;
+    __syncthreads();
+    for (int i = tid; i < n; i += NT) {
+      const uint64_t k = get(i);
+      if ((k & pmask) == pval) atomicAdd(&hist[(uint32_t)(k >> shift) & dmask], 1u);
     }
     __syncthreads();
-    cur ^= 1;
-    n = m;
-  }
-}
-
-// One round of a log-depth radix-R (Hillis-Steele) inclusive scan over
-// superblock totals: out[s] = top-K(in[s] U in[s-d] U ... U in[s-(R-1)d])
-// over the terms with a non-negative index (d = R^round, so after round r
-// row s covers superblocks s-R^(r+1)+1 .. s).  Rows are (nsb+1)-strided with
-// row s+1 holding superblock s (row 0 stays empty, so that the walk reads
-// row s as "everything before superblock s").  With `from_q` the input is
-// the superblock totals themselves: the local prefix of each superblock's
-// last block.  One workgroup per (superblock, batch): the (up to R <= 8)
-// lists are staged in LDS together and reduced by a tree of pairwise
-// co-rank merges (log2 R levels, the pairs of a level merged side by side,
-// the last level written straight to the output row).  Top-K under the
-// strict order `better` of distinct positions does not depend on the merge
-// order.
-__global__ void __launch_bounds__(256)
-prefix_scan_round(int nb, int sbs, int nsb, int K, int d, int radix, int from_q, const float* __restrict__ qval,
-                  const int32_t* __restrict__ qidx, const int32_t* __restrict__ qlen,
-                  const float* __restrict__ ival, const int32_t* __restrict__ iidx, const int32_t* __restrict__ ilen,
-                  float* __restrict__ oval, int32_t* __restrict__ oidx, int32_t* __restrict__ olen) {
-  PFA_CRITICAL_CHAIN_PRIORITY();
-  extern __shared__ char smem[];
-  // entry arrays: radix input lists, then level-1 outputs (radix/2 lists),
-  // then level-2 outputs (radix/4 lists); list i of a region at i*K
-  float* ev = (float*)smem;
-  const int cap_e = (radix + (radix > 2 ? radix / 2 : 0) + (radix > 4 ? radix / 4 : 0)) * K;
-  int32_t* ei = (int32_t*)(ev + cap_e);
-  __shared__ int s_off[8], s_len[8];
-  const int s = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int64_t rb = (int64_t)b * (nsb + 1);
-  // input row of superblock ss (entries at row * K) and its length
-  auto row_of_sb = [&](int ss) -> int64_t {
-    return from_q ? (int64_t)b * nb + min(nb, (ss + 1) * sbs) - 1 : rb + ss + 1;
-  };
-  const float* inv = from_q ? qval : ival;
-  const int32_t* ini = from_q ? qidx : iidx;
-  const int32_t* inl = from_q ? qlen : ilen;
-  float* ov = oval + (rb + s + 1) * K;
-  int32_t* oi = oidx + (rb + s + 1) * K;
-  if (s == 0 && tid == 0) olen[rb] = 0;
-  const int nl = min(radix, s / d + 1);  // terms s, s-d, ... that exist
-  // all lengths in one round of loads, then every entry in one flat loop
-  if (tid < nl) {
-    s_off[tid] = tid * K;
-    s_len[tid] = inl[row_of_sb(s - tid * d)];
-  }
-  __syncthreads();
-  if (nl == 1) {
-    const int64_t r0 = row_of_sb(s);
-    const int n0 = s_len[0];
-    for (int p = tid; p < n0; p += 256) { ov[p] = inv[r0 * K + p]; oi[p] = ini[r0 * K + p]; }
-    if (tid == 0) olen[rb + s + 1] = n0;
-    return;
-  }
-  for (int e = tid; e < nl * K; e += 256) {
-    const int k = e / K, p = e - k * K;
-    if (p < s_len[k]) {
-      const int64_t r = row_of_sb(s - k * d);
-      ev[e] = inv[r * K + p];
-      ei[e] = ini[r * K + p];
+    // bins from the top: thread t owns bins kBins-1-BPT*t .. kBins-BPT-BPT*t
+    uint32_t c[BPT];
+    uint32_t tot = 0;
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+      c[q] = hist[kBins - 1 - BPT * tid - q];
+      tot += c[q];
     }
-  }
-  __syncthreads();
-  int n = nl;
-  int region = radix * K;  // where level 1 writes
-  for (int level = 0; n > 1; ++level) {
-    const int np = n >> 1;
-    const bool last = n == 2;
-    const int tpp = 256 / np;  // threads per pair (np <= 4)
-    const int pr = tid / tpp, pt = tid % tpp;
-    int m = 0;
-    if (pr < np) {
-      const int oa = s_off[2 * pr], na = s_len[2 * pr];
-      const int oc = s_off[2 * pr + 1], nc = s_len[2 * pr + 1];
-      m = min(K, na + nc);
-      const int od = region + pr * K;
-      for (int p = pt; p < m; p += tpp) {
-        float vv;
-        int32_t ii;
-        merge_at(p, ev + oa, ei + oa, na, ev + oc, ei + oc, nc, vv, ii);
-        if (last) {
-          ov[p] = vv;
-          oi[p] = ii;
-        } else {
-          ev[od + p] = vv;
-          ei[od + p] = ii;
+    // inclusive scan of the thread totals (wave scans, then the wave sums)
+    uint32_t incl = tot;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) sh[wid] = (int)incl;
+    __syncthreads();
+    uint32_t before = incl - tot;
+    for (int w2 = 0; w2 < wid; ++w2) before += (uint32_t)sh[w2];
+    __syncthreads();
+    if (before < (uint32_t)need && before + tot >= (uint32_t)need) {
+      uint32_t acc = before;
+#pragma unroll
+      for (int q = 0; q < BPT; ++q) {
+        if (acc < (uint32_t)need && acc + c[q] >= (uint32_t)need) {
+          sh[0] = kBins - 1 - BPT * tid - q;  // chosen digit
+          sh[1] = need - (int)acc;            // still needed inside it
+          sh[2] = (int)c[q];                  // keys in it
         }
+        acc += c[q];
       }
     }
     __syncthreads();
-    if (last) {
-      if (tid == 0) olen[rb + s + 1] = m;
-      break;
-    }
-    // pair pr becomes list pr; an odd last list is carried as it is (the
-    // descriptors are read before any is rewritten)
-    int new_off = 0, new_len = 0, carry_off = 0, carry_len = 0;
-    if (tid < np) {
-      new_off = region + tid * K;
-      new_len = min(K, s_len[2 * tid] + s_len[2 * tid + 1]);
-    }
-    if (tid == 0 && (n & 1)) {
-      carry_off = s_off[n - 1];
-      carry_len = s_len[n - 1];
-    }
+    const uint32_t d = (uint32_t)sh[0];
+    const int still = sh[1], inbin = sh[2];
     __syncthreads();
-    if (tid < np) {
-      s_off[tid] = new_off;
-      s_len[tid] = new_len;
-    }
-    if (tid == 0 && (n & 1)) {
-      s_off[np] = carry_off;
-      s_len[np] = carry_len;
-    }
-    __syncthreads();
-    region += np * K;
-    n = np + (n & 1);
+    pmask |= (uint64_t)dmask << shift;
+    pval |= (uint64_t)d << shift;
+    need = still;
+    if (inbin == still || shift == 0) break;  // every key of the bin is taken: threshold = prefix
+    top = shift - 1;
   }
+  return pval;
 }
 
-// One workgroup (256 threads) per (block j, batch b).  LDS: the entering set
-// P best first (v, ix: cap entries each, cap = power of two >= K) and a
-// staging area of 2*cap floats + 2*cap ints that first holds R[s] and
-// Q[j-1] for the merge, then the index-sorted copy and the ranks of P.
+// Bitonic sort of cap = NT*V (V a power of two, 1..16) keys in LDS, largest
+// first, by a workgroup of NT threads.  Thread t holds the V keys
+// [V*t, V*t + V) in registers: strides below V are exchanged in registers,
+// strides below 64*V with the partner lane of the same wave (shuffles), and
+// the larger strides through LDS between barriers.  The caller has made the
+// keys visible to every thread (a barrier) before the call; they are in LDS,
+// sorted, and visible to every thread on return.
+template <int NT, int V>
+__device__ __forceinline__ void block_sort_desc_v(uint64_t* k) {
+  constexpr int cap = NT * V;
+  const int tid = threadIdx.x;
+  uint64_t r[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) r[i] = k[V * tid + i];
+  for (int kk = 2; kk <= cap; kk <<= 1) {
+    // strides of V and more: partner lanes (shuffles) or other waves (LDS)
+    for (int jj = kk >> 1; jj >= V; jj >>= 1) {
+      if (jj < 64 * V) {
+        const int lm = jj / V;  // partner lane distance (a power of two below 64)
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const uint64_t x = r[i];
+          const uint64_t y = __shfl_xor((unsigned long long)x, lm, 64);
+          const int e = V * tid + i;
+          const bool desc = (e & kk) == 0, lower = (e & jj) == 0;
+          const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+          r[i] = (lower == desc) ? hi : lo;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) k[V * tid + i] = r[i];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const int e = V * tid + i;
+          const uint64_t x = r[i], y = k[e ^ jj];
+          const bool desc = (e & kk) == 0, lower = (e & jj) == 0;
+          const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+          r[i] = (lower == desc) ? hi : lo;
+        }
+        __syncthreads();
+      }
+    }
+    // strides below V: inside the thread's registers (static indices)
+#pragma unroll
+    for (int jj = V >> 1; jj >= 1; jj >>= 1) {
+      if (jj < kk) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          if ((i & jj) == 0) {
+            const int pi = i | jj;
+            const int e = V * tid + i;
+            const bool desc = (e & kk) == 0;
+            const uint64_t x = r[i], y = r[pi];
+            const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+            r[i] = desc ? hi : lo;
+            r[pi] = desc ? lo : hi;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) k[V * tid + i] = r[i];
+  __syncthreads();
+}
+
+// Element p of top-K(a U c) for best-first (descending) key lists a (na)
+// and c (nc), by a merge-path co-rank.
+__device__ __forceinline__ uint64_t merge_key_at(int p, const uint64_t* a, int na, const uint64_t* c, int nc) {
+  int lo = max(0, p - nc), hi = min(p, na);
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] > c[p - 1 - mid]) lo = mid + 1;
+    else hi = mid;
+  }
+  const int ia = lo, ic = p - lo;
+  const bool take_a = ia < na && (ic >= nc || a[ia] > c[ic]);
+  return take_a ? a[ia] : c[ic];
+}
+
+// Launch 1: superblock s's keys sorted best first (SB entries; the first
+// K are its top-K), and the evict entries of its tokens initialised to
+// "still in the set".  One 1024-thread workgroup per (s, b) (few
+// superblocks: the sort's latency is hidden by four waves per SIMD), the
+// keys sorted in LDS.
+constexpr int kSbThreads = 1024;
+template <int V>  // SB = 1024 * V
+__global__ void __launch_bounds__(kSbThreads)
+prefix_sb_sort(const float* __restrict__ scores, int64_t T, int64_t stride, int nsb,
+               uint64_t* __restrict__ skey, int32_t* __restrict__ evict) {
+  constexpr int NT = kSbThreads;
+  constexpr int64_t SB = NT * V;
+  PFA_CRITICAL_CHAIN_PRIORITY();
+  extern __shared__ __align__(16) uint64_t stage[];
+  const int sb = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int64_t t0 = (int64_t)sb * SB;
+  const int n = (int)min<int64_t>(SB, T - t0);
+  const float* sc = scores + (int64_t)b * stride + t0;
+  float x[V];
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const int i = NT * u + tid;
+    x[u] = i < n ? sc[i] : 0.f;  // loads issued together
+  }
+#pragma unroll
+  for (int u = 0; u < V; ++u) {
+    const int i = NT * u + tid;
+    if (i < n) evict[(int64_t)b * T + t0 + i] = INT32_MAX;
+    stage[i] = i < n ? score_key(x[u], (int)(t0 + i)) : 0ull;
+  }
+  __syncthreads();
+  block_sort_desc_v<NT, V>(stage);
+  uint64_t* out = skey + ((int64_t)b * nsb + sb) * SB;
+  for (int i = tid; i < (int)SB; i += NT) out[i] = stage[i];
+}
+
+// Launch 2: R[s] = top-K of superblocks 0 .. s-1 (the set entering s),
+// sorted best first, rlen[s] = |R[s]|: the K-th largest key of the first
+// min(K, SB) entries of each earlier superblock's sorted list (radix
+// select; up to kPrefixStage entries are staged in LDS), then those at or
+// above it, sorted.  One 1024-thread workgroup per (s, b).
+template <int V>  // cap = 1024 * V >= K
+__global__ void __launch_bounds__(kSbThreads)
+prefix_sb_prefix(int nsb, int64_t SB, int K, const uint64_t* __restrict__ skey,
+                 uint64_t* __restrict__ rkey, int32_t* __restrict__ rlen) {
+  constexpr int NT = kSbThreads;
+  constexpr int cap = NT * V;
+  PFA_CRITICAL_CHAIN_PRIORITY();
+  extern __shared__ __align__(16) uint64_t dyn[];
+  uint64_t* keys = dyn;         // cap: the selected keys, then sorted
+  uint64_t* stage = dyn + cap;  // the staged list entries
+  __shared__ uint32_t hist[kBins];
+  __shared__ int sh[NT / 64];
+  __shared__ uint64_t sx[NT / 64];
+  __shared__ int s_cnt;
+  const int sb = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int per = (int)min<int64_t>(K, SB);  // entries taken from each earlier list
+  const int nl = sb * per;
+  const uint64_t* sk = skey + (int64_t)b * nsb * SB;
+  auto gslot = [&](int i) -> uint64_t {
+    const int q = i / per, e = i - q * per;
+    return sk[(int64_t)q * SB + e];
+  };
+  const bool staged = nl <= kPrefixStage;
+  if (staged) {
+    uint64_t x[kPrefixStage / NT];
+#pragma unroll
+    for (int u = 0; u < kPrefixStage / NT; ++u) {
+      const int i = NT * u + tid;
+      x[u] = i < nl ? gslot(i) : 0ull;  // loads issued together
+    }
+#pragma unroll
+    for (int u = 0; u < kPrefixStage / NT; ++u) {
+      const int i = NT * u + tid;
+      if (i < nl) stage[i] = x[u];
+    }
+  }
+  for (int p = tid; p < cap; p += NT) keys[p] = 0ull;
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  auto get = [&](int i) -> uint64_t { return staged ? stage[i] : gslot(i); };
+  uint64_t th = 1;  // every real key is > 0
+  if (nl > K) th = block_select<NT>(nl, K, get, hist, sh, sx);
+  for (int i = tid; i < nl; i += NT) {
+    const uint64_t k = get(i);
+    if (k >= th) keys[atomicAdd(&s_cnt, 1)] = k;
+  }
+  __syncthreads();
+  const int cnt = s_cnt;
+  block_sort_desc_v<NT, V>(keys);
+  uint64_t* out = rkey + ((int64_t)b * nsb + sb) * K;
+  for (int p = tid; p < K; p += NT) out[p] = keys[p];
+  if (tid == 0) rlen[(int64_t)b * nsb + sb] = cnt;
+}
+
+// Launch 3: one workgroup (256 threads) per (block j, batch b).  P =
+// S(64j - 1) = top-K(R[s] U Q) best first, Q = the tokens of superblock s
+// before the block, best first (the superblock's sorted list with its later
+// positions dropped, an ordered compaction), by a merge-path co-rank.
+// LDS: R[s], Q and P (cap keys each), P's positions, index-sorted copy and
+// ranks (cap each).
 template <bool SORT>
 __global__ void __launch_bounds__(256)
-prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int sbs, int nsb, int K,
-                  int cap, const float* __restrict__ qval, const int32_t* __restrict__ qidx,
-                  const int32_t* __restrict__ qlen, const float* __restrict__ rval, const int32_t* __restrict__ ridx,
+prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, int nb, int64_t SB, int nsb, int K,
+                  int cap, const uint64_t* __restrict__ skey, const uint64_t* __restrict__ rkey,
                   const int32_t* __restrict__ rlen, int32_t* __restrict__ blk_out, int32_t* __restrict__ evict) {
   PFA_CRITICAL_CHAIN_PRIORITY();
-  extern __shared__ char smem[];
-  float* v = (float*)smem;
-  int32_t* ix = (int32_t*)(v + cap);
-  float* sav = (float*)(ix + cap);        // staging: R values   (cap)
-  int32_t* sai = (int32_t*)(sav + cap);   //          R indices  (cap)
-  float* sqv = (float*)(sai + cap);       //          Q values   (cap)
-  int32_t* sqi = (int32_t*)(sqv + cap);   //          Q indices  (cap)
-  int32_t* srt = sai;                     // after the merge: index-sorted copy
-  int32_t* rk = sqi;                      //                  ranks of P
-  __shared__ float bv[kBlk];
-  __shared__ int32_t bi[kBlk];
+  extern __shared__ __align__(16) char smem[];
+  uint64_t* ra = (uint64_t*)smem;
+  uint64_t* qa = ra + cap;
+  uint64_t* pkey = qa + cap;  // P's keys, best first
+  int32_t* ix = (int32_t*)(pkey + cap);
+  int32_t* srt = ix + cap;  // index-sorted copy of P
+  int32_t* rk = srt + cap;  // ranks of P
+  __shared__ uint64_t bkey[kBlk];  // the block's keys by position
+  __shared__ uint64_t sbk[kBlk];   // and sorted best first
   __shared__ int32_t flag[kBlk];
   __shared__ int32_t ent[kBlk];
   __shared__ uint64_t s_fl;
   __shared__ int s_nent;
-  const int j = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int s = j / sbs, k = j % sbs;
-  const int64_t rrow = (int64_t)b * (nsb + 1) + s;  // row s: top-K of superblocks 0..s-1
-  const int64_t qrow = (int64_t)b * nb + j - 1;      // block j-1's local prefix (k > 0)
-  // both lengths in one round of loads, then the entries of both rows
-  const int na = rlen[rrow];
-  const int nq = k > 0 ? qlen[qrow] : 0;
-  for (int p = tid; p < K; p += 256) {
-    if (p < na) { sav[p] = rval[rrow * K + p]; sai[p] = ridx[rrow * K + p]; }
-    if (p < nq) { sqv[p] = qval[qrow * K + p]; sqi[p] = qidx[qrow * K + p]; }
-  }
+  __shared__ int s_wsum[4];
+  const int j = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t t0 = (int64_t)j * kBlk;
-  const int nB = (int)min<int64_t>(kBlk, T - t0);
-  float sv = -INFINITY;
-  int32_t st = INT32_MAX;
-  if (tid < kBlk) {
-    if (tid < nB) { sv = scores[(int64_t)b * stride + t0 + tid]; st = (int32_t)(t0 + tid); }
-    bv[tid] = sv;
-    bi[tid] = st;
-    flag[tid] = 0;
+  const int s = (int)(t0 / SB);
+  const float* sc = scores + (int64_t)b * stride;
+  const int64_t sr = (int64_t)b * nsb + s;
+  const int na = rlen[sr];
+  const uint64_t* rk0 = rkey + sr * K;
+  for (int i = tid; i < na; i += 256) ra[i] = rk0[i];
+  // Q: ordered compaction of the superblock's sorted keys with position < t0
+  // (thread t scans entries [t*E, t*E + E), E = SB / 256)
+  const int E = (int)(SB >> 8);  // at most 16 (SB <= 4096)
+  const uint64_t* sk = skey + sr * SB + (int64_t)tid * E;
+  uint64_t kv[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) kv[e] = e < E ? sk[e] : 0ull;  // loads issued together
+  int cnt = 0;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) cnt += (kv[e] != 0ull && key_index(kv[e]) < t0) ? 1 : 0;
+  int incl = cnt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) s_wsum[wid] = incl;
+  __syncthreads();
+  int pos = incl - cnt;
+  for (int w2 = 0; w2 < wid; ++w2) pos += s_wsum[w2];
+  const int nq_all = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    if (pos < K && kv[e] != 0ull && key_index(kv[e]) < t0) qa[pos++] = kv[e];
   }
   __syncthreads();
-  const int n = min(K, na + nq);
+  const int nq = min(K, nq_all);
+  const int n = (int)min<int64_t>(K, t0);  // |S(64j - 1)| = min(K, na + nq)
   for (int p = tid; p < n; p += 256) {
-    float vv;
-    int32_t ii;
-    merge_at(p, sav, sai, na, sqv, sqi, nq, vv, ii);
-    v[p] = vv;
-    ix[p] = ii;
+    const uint64_t k = merge_key_at(p, ra, na, qa, nq);
+    pkey[p] = k;
+    ix[p] = key_index(k);
+  }
+  const int nB = (int)min<int64_t>(kBlk, T - t0);
+  int32_t st = INT32_MAX;
+  uint64_t bk = 0ull;  // this token's key (wave 0); 0 past the sequence
+  if (tid < kBlk) {
+    if (tid < nB) { st = (int32_t)(t0 + tid); bk = score_key(sc[t0 + tid], st); }
+    bkey[tid] = bk;
+    flag[tid] = 0;
+    // the block's keys sorted best first across the wave (bitonic, shuffles)
+    uint64_t x = bk;
+#pragma unroll
+    for (int kk = 2; kk <= 64; kk <<= 1) {
+#pragma unroll
+      for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+        const uint64_t y = __shfl_xor((unsigned long long)x, jj, 64);
+        const bool desc = (tid & kk) == 0, lower = (tid & jj) == 0;
+        const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+        x = (lower == desc) ? hi : lo;
+      }
+    }
+    sbk[tid] = x;
   }
   __syncthreads();
   int32_t* orow = blk_out + ((int64_t)b * nb + j) * K;
@@ -410,36 +472,45 @@ prefix_block_walk(const float* __restrict__ scores, int64_t T, int64_t stride, i
     }
     for (int p = tid; p < K; p += 256) orow[p] = srt[p];
   } else {
-    // best first, as merged
+    // best first
     for (int p = tid; p < K; p += 256) orow[p] = p < n ? ix[p] : INT32_MAX;
   }
-  // ranks of P's elements in P U B (P is sorted best first)
+  // ranks of P's elements in P U B: p + the block keys above it (the block
+  // sorted best first, padding 0 below every real key: a binary search)
   for (int p = tid; p < n; p += 256) {
-    int c = 0;
-    for (int q = 0; q < nB; ++q) c += better(bv[q], bi[q], v[p], ix[p]) ? 1 : 0;
-    const int r = p + c;
+    const uint64_t kp = pkey[p];
+    int lo = 0, hi = kBlk;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sbk[mid] > kp) lo = mid + 1;
+      else hi = mid;
+    }
+    const int r = p + lo;
     rk[p] = r;
     if (r >= K) flag[r - K] = 1;
   }
-  // the block's tokens (wave 0)
+  // the block's tokens (wave 0): the keys of P above it (binary search),
+  // of the block above it (its place in the sorted block) and of the earlier
+  // block tokens above it
   bool enters = false;
   int rt = 0;
   if (tid < kBlk && tid < nB) {
     int lo = 0, hi = n;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (better(v[mid], ix[mid], sv, st)) lo = mid + 1;
+      if (pkey[mid] > bk) lo = mid + 1;
       else hi = mid;
     }
-    int ra = 0, rb = 0;
-    for (int q = 0; q < nB; ++q) {
-      if (better(bv[q], bi[q], sv, st)) {
-        ++ra;
-        if (q < tid) ++rb;
-      }
+    int la = 0, ha = kBlk;
+    while (la < ha) {
+      const int mid = (la + ha) >> 1;
+      if (sbk[mid] > bk) la = mid + 1;
+      else ha = mid;
     }
+    int rb = 0;
+    for (int q = 0; q < tid; ++q) rb += bkey[q] > bk ? 1 : 0;
     enters = lo + rb < K;
-    rt = lo + ra;
+    rt = lo + la;
     if (enters && rt >= K) flag[rt - K] = 1;
   }
   __syncthreads();
@@ -777,17 +848,8 @@ using namespace pfa;
 static constexpr int kPrefixMaxK = 2048;
 static constexpr size_t kPrefixLds = 60 * 1024;  // dynamic LDS budget per workgroup
 
-// Radix of the superblock scan: as many lists as fit the LDS budget (R
-// inputs plus the tree's intermediate lists, 8 bytes per entry), at most 8.
-static int prefix_round_entries(int radix) { return radix + (radix > 2 ? radix / 2 : 0) + (radix > 4 ? radix / 4 : 0); }
-static int prefix_radix(int K) {
-  for (int r = 8; r > 2; r >>= 1)
-    if ((size_t)prefix_round_entries(r) * K * 8 <= kPrefixLds) return r;
-  return 2;
-}
-
 static int prefix_cap(int K) {
-  int cap = 64;
+  int cap = 256;  // the LDS sort takes 256 .. 4096 keys
   while (cap < K) cap <<= 1;
   return cap;
 }
@@ -797,61 +859,62 @@ extern "C" int pfa_proto_prefix_workspace_size(int B, int64_t T, int K, size_t* 
   PFA_CHECK_ARG(bytes && B >= 0 && T >= 0 && K > 0, "pfa_proto_prefix_workspace_size: bad arguments");
   int64_t nb = (T + kBlk - 1) / kBlk;
   if (nb < 1) nb = 1;
-  const int64_t sbs = prefix_sbs(nb);
-  const int64_t nsb = (nb + sbs - 1) / sbs;
-  *bytes = prefix_ws_bytes(B, T, nb, nsb, K, nullptr, nullptr);
+  const int64_t SB = prefix_sb_tokens(T, K);
+  const int64_t nsb = (T + SB - 1) / SB > 0 ? (T + SB - 1) / SB : 1;
+  *bytes = prefix_ws_bytes(B, T, nb, nsb, SB, K, nullptr, nullptr);
   return PFA_OK;
 }
 
-// Steps 1-4: set table rows (B, nb, K) and evict (B, T).
+// Set table rows (B, nb, K) and evict (B, T): three launches.
 static int prefix_blocks(const float* scores, int B, int64_t T, int64_t stride, int K, int32_t* blk,
                          int32_t* evict, const PrefixWs& w, int64_t nb, bool sorted_rows, hipStream_t s) {
-  const int64_t sbs = prefix_sbs(nb);
-  const int64_t nsb = (nb + sbs - 1) / sbs;
+  const int64_t SB = prefix_sb_tokens(T, K);
+  const int64_t nsb = (T + SB - 1) / SB;
   const int cap = prefix_cap(K);
-  dim3 grid((unsigned)nb, (unsigned)B);
-  prefix_block_sort<<<grid, 64, 0, s>>>(scores, T, stride, (int)nb, K, w.bval, w.bidx, w.blen, evict);
-  PFA_CHECK_LAUNCH("pfa_proto_prefix/sort");
-  const int preload = (size_t)K * 16 + (size_t)sbs * (kBlk * 8 + 4) <= kPrefixLds ? 1 : 0;
-  const size_t lds_local = (size_t)K * 16 + (size_t)(preload ? sbs : 2) * (kBlk * 8 + 4);
-  prefix_sb_local<<<dim3((unsigned)nsb, (unsigned)B), 256, lds_local, s>>>(
-      (int)nb, (int)sbs, K, preload, w.bval, w.bidx, w.blen, w.qval, w.qidx, w.qlen);
-  PFA_CHECK_LAUNCH("pfa_proto_prefix/local");
-  // log-depth inclusive scan of the superblock totals (ping-pong between
-  // the two R buffers; the last round lands in the buffer the walk reads)
-  const int radix = prefix_radix(K);
-  int rounds = 0;
-  for (int64_t span = 1; span < nsb; span *= radix) ++rounds;
-  if (rounds == 0) rounds = 1;
-  const size_t lds_round = (size_t)prefix_round_entries(radix) * K * 8;
-  const float* fin_v = nullptr;
-  const int32_t* fin_i = nullptr;
-  const int32_t* fin_l = nullptr;
-  for (int r = 0; r < rounds; ++r) {
-    const bool to_primary = ((rounds - 1 - r) & 1) == 0;
-    float* ov = to_primary ? w.rval : w.r2val;
-    int32_t* oi = to_primary ? w.ridx : w.r2idx;
-    int32_t* ol = to_primary ? w.rlen : w.r2len;
-    const float* iv = to_primary ? w.r2val : w.rval;
-    const int32_t* ii = to_primary ? w.r2idx : w.ridx;
-    const int32_t* il = to_primary ? w.r2len : w.rlen;
-    int d = 1;
-    for (int q = 0; q < r; ++q) d *= radix;
-    prefix_scan_round<<<dim3((unsigned)nsb, (unsigned)B), 256, lds_round, s>>>(
-        (int)nb, (int)sbs, (int)nsb, K, d, radix, r == 0 ? 1 : 0, w.qval, w.qidx, w.qlen, iv, ii, il, ov, oi, ol);
-    PFA_CHECK_LAUNCH("pfa_proto_prefix/scan");
-    fin_v = ov;
-    fin_i = oi;
-    fin_l = ol;
+  const dim3 sgrid((unsigned)nsb, (unsigned)B);
+  // (past 48 KB of dynamic LDS a launch declares it; static arrays add ~8 KB)
+  auto lds_attr = [](const void* fn, size_t bytes) {
+    if (bytes > 48 * 1024) hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  };
+#define PFA_SB_SORT(V_)                                                                                   \
+  do {                                                                                                    \
+    lds_attr((const void*)prefix_sb_sort<V_>, (size_t)SB * 8);                                            \
+    prefix_sb_sort<V_><<<sgrid, kSbThreads, (size_t)SB * 8, s>>>(scores, T, stride, (int)nsb, w.skey, evict); \
+  } while (0)
+  switch (SB) {
+    case 1024: PFA_SB_SORT(1); break;
+    case 2048: PFA_SB_SORT(2); break;
+    default: PFA_SB_SORT(4); break;
   }
-  if (sorted_rows)
-    prefix_block_walk<true><<<grid, 256, (size_t)cap * 24, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K,
-                                                                cap, w.qval, w.qidx, w.qlen, fin_v, fin_i, fin_l,
-                                                                blk, evict);
-  else
-    prefix_block_walk<false><<<grid, 256, (size_t)cap * 24, s>>>(scores, T, stride, (int)nb, (int)sbs, (int)nsb, K,
-                                                                 cap, w.qval, w.qidx, w.qlen, fin_v, fin_i, fin_l,
-                                                                 blk, evict);
+#undef PFA_SB_SORT
+  PFA_CHECK_LAUNCH("pfa_proto_prefix/superblocks");
+  // the largest staged list-slot count of sb_prefix (superblocks whose
+  // lists exceed kPrefixStage slots read them from global memory)
+  const int64_t nl = (nsb - 1) * (SB < K ? SB : (int64_t)K);
+  const int pcap = cap < kSbThreads ? kSbThreads : cap;  // the sort takes multiples of 1024 keys
+  const size_t lds_pre = (size_t)pcap * 8 + (size_t)(nl < 1 ? 1 : (nl < kPrefixStage ? nl : kPrefixStage)) * 8;
+#define PFA_SB_PREFIX(V_)                                                                                 \
+  do {                                                                                                    \
+    lds_attr((const void*)prefix_sb_prefix<V_>, lds_pre);                                                 \
+    prefix_sb_prefix<V_><<<sgrid, kSbThreads, lds_pre, s>>>((int)nsb, SB, K, w.skey, w.rkey, w.rlen);     \
+  } while (0)
+  switch (pcap) {
+    case 1024: PFA_SB_PREFIX(1); break;
+    default: PFA_SB_PREFIX(2); break;
+  }
+#undef PFA_SB_PREFIX
+  PFA_CHECK_LAUNCH("pfa_proto_prefix/superblock prefix");
+  const size_t lds = (size_t)cap * 36;
+  dim3 grid((unsigned)nb, (unsigned)B);
+  if (sorted_rows) {
+    lds_attr((const void*)prefix_block_walk<true>, lds);
+    prefix_block_walk<true><<<grid, 256, lds, s>>>(scores, T, stride, (int)nb, SB, (int)nsb, K, cap, w.skey, w.rkey,
+                                                   w.rlen, blk, evict);
+  } else {
+    lds_attr((const void*)prefix_block_walk<false>, lds);
+    prefix_block_walk<false><<<grid, 256, lds, s>>>(scores, T, stride, (int)nb, SB, (int)nsb, K, cap, w.skey,
+                                                    w.rkey, w.rlen, blk, evict);
+  }
   PFA_CHECK_LAUNCH("pfa_proto_prefix/walk");
   return PFA_OK;
 }
@@ -862,15 +925,15 @@ static int prefix_blocks(const float* scores, int B, int64_t T, int64_t stride, 
                 NAME ": bad arguments (B=%d T=%lld K=%d, K <= %d)", B, (long long)T, K, kPrefixMaxK);       \
   PFA_CHECK_ARG(T < ((int64_t)1 << 31), NAME ": T too large");                                              \
   const int64_t nb = (T + kBlk - 1) / kBlk;                                                                 \
-  const int64_t sbs = prefix_sbs(nb);                                                                       \
-  const int64_t nsb = (nb + sbs - 1) / sbs;                                                                 \
-  const size_t need = prefix_ws_bytes(B, T, nb, nsb, K, nullptr, nullptr);                                  \
+  const int64_t SBt = prefix_sb_tokens(T, K);                                                               \
+  const int64_t nsb = (T + SBt - 1) / SBt;                                                                  \
+  const size_t need = prefix_ws_bytes(B, T, nb, nsb, SBt, K, nullptr, nullptr);                             \
   if (ws_bytes < need) {                                                                                    \
     set_error(NAME ": workspace %zu < %zu", ws_bytes, need);                                               \
     return PFA_E_WORKSPACE;                                                                                 \
   }                                                                                                         \
   PrefixWs w;                                                                                               \
-  prefix_ws_bytes(B, T, nb, nsb, K, &w, (char*)workspace);                                                  \
+  prefix_ws_bytes(B, T, nb, nsb, SBt, K, &w, (char*)workspace);                                             \
   hipStream_t s = as_stream(stream)
 
 extern "C" int pfa_proto_prefix_blocks(const float* proto_scores, int B, int64_t T, int64_t score_stride, int K,
