@@ -358,6 +358,38 @@ int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                            const float* q_scale, const float* k_scale,
                            const float* v_scale, int passes, void* stream);
 
+/* pfa_shortlist_attn_fwd (without the int8 scales) whose anchor pass also
+ * does work the module path otherwise launches separately before it:
+ *   PFA_FUSE_K_ROPE: rotates k in place, row by row, for the active heads
+ *     (head_map[0..P)) with the q_rope tables -- the bits of
+ *     pfa_rope_k_inplace on those heads (aspa.py:606-618, 1648-1649 for
+ *     k); q is rotated on load as with pfa_shortlist_attn_fwd.  k of the
+ *     other heads is left as it is (no kernel reads it).
+ *   PFA_FUSE_ZERO: writes zeros to out[b][h][t][:] for every (head, token)
+ *     pair without a packed row (row_of == -1, and every token of the
+ *     heads missing from head_map[0..P)), so out needs no zero fill first
+ *     (the x.new_zeros of aspa.py:1707 that the index_copy_ of
+ *     aspa.py:1762-1806 fills).
+ * Both ride on the anchor pass: anchors on and passes 1 or 3; head_map
+ * ascending (as pfa_pack_rows writes it) with P_cap = B*H; N may be 0 (the
+ * zero fill still runs).  The main pass then reads the rotated k.
+ * Replaces pfa_rope_k_inplace + pfa_zero_fill (aspa.py:1648-1649, 1707) on
+ * the structured module path. */
+#define PFA_FUSE_K_ROPE 1
+#define PFA_FUSE_ZERO 2
+int pfa_shortlist_attn_fwd_fused(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
+                                 pfa_tensor4 out, int dtype, int H, int64_t T,
+                                 int D, const int32_t* token_idx,
+                                 const int32_t* row_head,
+                                 const int32_t* head_map, int64_t N, int P_cap,
+                                 const int32_t* summary, const int32_t* row_of,
+                                 int local_w, int anchor_stride,
+                                 int anchor_slots, const int32_t* proto_blocks,
+                                 int proto_k, const int32_t* proto_evict,
+                                 float scale, float* partials, int32_t* lengths,
+                                 const void* q_rope_cos, const void* q_rope_sin,
+                                 int passes, int fuse, void* stream);
+
 /* ====================================================================
  * Per-head symmetric int8 quantisation of the active heads of q, k or v.
  * Replaces AdaptiveSparseAttention._quantize_per_head_int8

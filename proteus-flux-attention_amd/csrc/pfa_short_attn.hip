@@ -45,6 +45,17 @@ constexpr int kPartW = 68;  // floats per partial row: m, l, pad, pad, acc[64]
 constexpr int kMaxProto = 1024;
 constexpr int kMaxClassRows = 4096;
 constexpr float kRescaleLog2 = 0.0f;  // rescale only when some row's max rises
+// Anchor-pass fusions.  Workgroup (c, p) owns the tokens t = c (mod stride)
+// of global head head_map[p]: every (head, token) pair of the active heads
+// belongs to exactly one workgroup, and the P_cap - P workgroups past the
+// active heads take the inactive ones.
+//   kFuseKRope: rotate the k rows of the active heads in place with the q
+//     RoPE tables (the arithmetic of the RoPE kernels), before the class's
+//     anchor tiles are read;
+//   kFuseZero: write zeros to out for every (head, token) pair without a
+//     packed row (the rows the main pass does not write).
+constexpr int kFuseKRope = 1;
+constexpr int kFuseZero = 2;
 
 struct ShortArgs {
   pfa_tensor4 q, k, v, out;
@@ -73,6 +84,8 @@ struct ShortArgs {
   const float* qsc;
   const float* ksc;
   const float* vsc;
+  // work the anchor pass takes over from separate passes (kFuse* bits)
+  int fuse;
   __device__ __forceinline__ float head_scale_log2(int bh) const {
     return qsc ? scale_log2 * (qsc[bh] * ksc[bh]) : scale_log2;
   }
@@ -373,6 +386,69 @@ __device__ __forceinline__ int64_t xcd_block(int64_t P, int64_t nblk) {
   return (P % 8) * per + P / 8;
 }
 
+// The fused per-class work of the anchor pass, eight lanes per token (lane
+// group j of a pass takes token c + s*(M0 + j), each lane one 16-byte chunk
+// of the 64-element row, so a wave's accesses are whole 128-byte rows).
+// ROPE: rotate the k row of the token in place (rope_rotate8 on the lane's
+// four (even, odd) pairs: the bits of pfa_rope_k_inplace).  ZERO: write
+// zeros to the out row of the token (a head without rows).  The loads of
+// kFusedBatch passes are issued together before any of them is used (one
+// memory latency per batch).
+constexpr int kFusedBatch = 4;
+__device__ __forceinline__ void unpack8(const uint4& w, float (&o)[8]) {
+  const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __uint_as_float(v[i] << 16);
+    o[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+template <bool ROPE, bool ZERO>
+__device__ __forceinline__ void class_rows_fused(const ShortArgs& a, int64_t bb, int64_t hh, int c, int64_t Mmax) {
+  const int tid = threadIdx.x;
+  const int ch = tid & 7;
+  const int s = a.stride;
+  uint16_t* kb = (uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h + 8 * ch;
+  uint16_t* ob = (uint16_t*)a.out.ptr + bb * a.out.s_b + hh * a.out.s_h + 8 * ch;
+  for (int64_t M0 = 0; M0 <= Mmax; M0 += 32 * kFusedBatch) {
+    uint4 kx[kFusedBatch], kc[kFusedBatch], ks[kFusedBatch];
+    int64_t tt[kFusedBatch];
+    bool ok[kFusedBatch];
+#pragma unroll
+    for (int j = 0; j < kFusedBatch; ++j) {
+      const int64_t M = M0 + 32 * j + (tid >> 3);
+      ok[j] = M <= Mmax;
+      // past the class's last token the lane reloads token c (in range,
+      // unused): the loads stay unconditional, so none waits on another
+      tt[j] = c + (int64_t)s * (ok[j] ? M : 0);
+      if constexpr (ROPE) {
+        kx[j] = *reinterpret_cast<const uint4*>(kb + tt[j] * a.k.s_t);
+        kc[j] = *reinterpret_cast<const uint4*>(a.rcos + tt[j] * 64 + 8 * ch);
+        ks[j] = *reinterpret_cast<const uint4*>(a.rsin + tt[j] * 64 + 8 * ch);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kFusedBatch; ++j) {
+      if (!ok[j]) continue;
+      if constexpr (ROPE) {
+        float xv[8], cv[8], sv[8], o[8];
+        unpack8(kx[j], xv);
+        unpack8(kc[j], cv);
+        unpack8(ks[j], sv);
+        rope_rotate8<PFA_BF16>(xv, cv, sv, o);
+        uint4 w;
+        w.x = (uint32_t)f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+        w.y = (uint32_t)f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+        w.z = (uint32_t)f32_to_bf16(o[4]) | ((uint32_t)f32_to_bf16(o[5]) << 16);
+        w.w = (uint32_t)f32_to_bf16(o[6]) | ((uint32_t)f32_to_bf16(o[7]) << 16);
+        *reinterpret_cast<uint4*>(kb + tt[j] * a.k.s_t) = w;
+      }
+      if constexpr (ZERO) *reinterpret_cast<uint4*>(ob + tt[j] * a.out.s_t) = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------
 // Pass 1: anchors per (residue class, compact head)
 // ---------------------------------------------------------------------
@@ -396,14 +472,31 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   const int c = blockIdx.x;
   const int p = blockIdx.y;
   const int P = a.summary[0];
-  if (p >= P) return;
   const int s = a.stride;
   if (c >= s || (int64_t)c >= a.T) return;
+  const int64_t Mmax = (a.T - 1 - c) / s;
+  if (p >= P) {
+    // inactive heads: workgroup p takes the (p - P)-th global head missing
+    // from the ascending active list head_map[0..P)
+    if ((a.fuse & kFuseZero) == 0) return;
+    int g = p - P;
+    for (int j = 0; j < P; ++j) g += a.head_map[j] <= g ? 1 : 0;
+    if (g >= (int)gridDim.y) return;
+    class_rows_fused<false, true>(a, g / a.H, g % a.H, c, Mmax);
+    return;
+  }
   const int bh = a.head_map ? a.head_map[p] : p;
   const int64_t bb = bh / a.H, hh = bh % a.H;
   const float sl2 = a.head_scale_log2(bh);
-  const int64_t Mmax = (a.T - 1 - c) / s;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // The rotated k rows are read back below by this workgroup's own tile
+  // transfers (the class's keys are this workgroup's alone): the barrier of
+  // the row compaction (a workgroup-scope release/acquire, one CU and one
+  // L1) orders every wave's stores before them.  A device-scope fence here
+  // would write back the whole L2 from every wave.
+  // (the zeros of kFuseZero are written by the row compaction below, which
+  // reads every row_of entry of the class anyway)
+  if (a.fuse & kFuseKRope) class_rows_fused<true, false>(a, bb, hh, c, Mmax);
   SwzLane L;
   L.init();
   const int drow = tid >> 3;  // this thread's DMA rows: drow and drow + 32
@@ -418,6 +511,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
     int r = -1;
     if (M <= Mmax) r = a.row_of[(int64_t)bh * a.T + c + (int64_t)s * M];
     const bool act = r >= 0;
+    if ((a.fuse & kFuseZero) && M <= Mmax && !act) {
+      // the token has no row of this head: its out row is zero (stores only,
+      // nothing in this workgroup waits for them)
+      uint4* orow = reinterpret_cast<uint4*>((uint16_t*)a.out.ptr + bb * a.out.s_b + hh * a.out.s_h +
+                                             (c + (int64_t)s * M) * a.out.s_t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) orow[j] = make_uint4(0u, 0u, 0u, 0u);
+    }
     const uint64_t bal = __ballot(act);
     if (lane == 0) wave_cnt[wid] = __popcll(bal);
     __syncthreads();
@@ -923,22 +1024,34 @@ using namespace pfa;
 
 extern "C" int pfa_shortlist_attn_part_floats(void) { return kPartW; }
 
-extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_tensor4 out, int dtype, int H,
-                                      int64_t T, int D, const int32_t* token_idx, const int32_t* row_head,
-                                      const int32_t* head_map, int64_t N, int P_cap, const int32_t* summary,
-                                      const int32_t* row_of, int local_w, int anchor_stride, int anchor_slots,
-                                      const int32_t* proto_blocks, int proto_k, const int32_t* proto_evict,
-                                      float scale, float* partials, int32_t* lengths, const void* q_rope_cos,
-                                      const void* q_rope_sin, const float* q_scale, const float* k_scale,
-                                      const float* v_scale, int passes, void* stream) {
-  clear_error();
+static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_tensor4 out, int dtype, int H,
+                              int64_t T, int D, const int32_t* token_idx, const int32_t* row_head,
+                              const int32_t* head_map, int64_t N, int P_cap, const int32_t* summary,
+                              const int32_t* row_of, int local_w, int anchor_stride, int anchor_slots,
+                              const int32_t* proto_blocks, int proto_k, const int32_t* proto_evict, float scale,
+                              float* partials, int32_t* lengths, const void* q_rope_cos, const void* q_rope_sin,
+                              const float* q_scale, const float* k_scale, const float* v_scale, int passes,
+                              int fuse, void* stream) {
   PFA_CHECK_ARG(dtype == PFA_BF16 && D == 64, "pfa_shortlist_attn_fwd: bf16 and D=64 only (got dtype %d D %d)", dtype,
                 D);
   PFA_CHECK_ARG(H > 0 && T > 0 && T < INT32_MAX && N >= 0 && P_cap > 0 && local_w >= 1,
                 "pfa_shortlist_attn_fwd: bad sizes");
   PFA_CHECK_ARG(passes >= 1 && passes <= 3, "pfa_shortlist_attn_fwd: passes must be 1, 2 or 3 (got %d)", passes);
-  if (N == 0) return PFA_OK;
-  PFA_CHECK_ARG(q.ptr && k.ptr && v.ptr && out.ptr && token_idx && row_head && summary,
+  PFA_CHECK_ARG((fuse & ~(kFuseKRope | kFuseZero)) == 0, "pfa_shortlist_attn_fwd_fused: unknown fuse bits %d", fuse);
+  if (fuse != 0) {
+    // the fused work rides on the anchor pass: it must run in this call,
+    // even when there are no rows (the zero fill still applies)
+    PFA_CHECK_ARG(anchor_stride > 0 && anchor_slots > 0 && (passes & 1),
+                  "pfa_shortlist_attn_fwd_fused: fusions need the anchor pass (anchors on, passes 1 or 3)");
+    PFA_CHECK_ARG(head_map && summary && row_of && out.ptr && k.ptr,
+                  "pfa_shortlist_attn_fwd_fused: head_map, summary, row_of, k and out are required");
+    PFA_CHECK_ARG(P_cap % H == 0, "pfa_shortlist_attn_fwd_fused: P_cap (%d) must be B*H (a multiple of H=%d)", P_cap,
+                  H);
+    PFA_CHECK_ARG(!(fuse & kFuseKRope) || (q_rope_cos && q_rope_sin && !q_scale),
+                  "pfa_shortlist_attn_fwd_fused: the k rotation needs the RoPE tables and no int8 scales");
+  }
+  if (N == 0 && fuse == 0) return PFA_OK;
+  PFA_CHECK_ARG(q.ptr && k.ptr && v.ptr && out.ptr && (N == 0 || (token_idx && row_head)) && summary,
                 "pfa_shortlist_attn_fwd: null pointer");
   PFA_CHECK_ARG(proto_blocks == nullptr || (proto_k > 0 && proto_k <= kMaxProto && proto_evict),
                 "pfa_shortlist_attn_fwd: prototype table (K <= %d with evict) required", kMaxProto);
@@ -972,6 +1085,7 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
     a.off32 = mx < 0xFFFFFFFFull ? 1 : 0;
   }
   a.qsc = q_scale; a.ksc = k_scale; a.vsc = v_scale;
+  a.fuse = fuse;
   hipStream_t s = as_stream(stream);
   if (anchors && (passes & 1)) {
     dim3 grid((unsigned)((int64_t)anchor_stride < T ? (int64_t)anchor_stride : T), (unsigned)P_cap);
@@ -979,7 +1093,7 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
     short_anchor_kernel<<<grid, 256, (size_t)ccap * 6 + 16, s>>>(a, ccap);
     PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
   }
-  if (!(passes & 2)) return PFA_OK;
+  if (!(passes & 2) || N == 0) return PFA_OK;
   // prototype slots: key 0's slot, the set table row, the block's 64 tokens;
   // rounded up to whole tiles
   const int pcap = ((proto_blocks ? proto_k : 0) + 64 + 1 + kTile - 1) / kTile * kTile;
@@ -999,4 +1113,32 @@ extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 
     short_main_kernel<false, S><<<(unsigned)blocks, 256, dyn, s>>>(a, anchors ? 1 : 0, pcap);
   PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/main");
   return PFA_OK;
+}
+
+extern "C" int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_tensor4 out, int dtype, int H,
+                                      int64_t T, int D, const int32_t* token_idx, const int32_t* row_head,
+                                      const int32_t* head_map, int64_t N, int P_cap, const int32_t* summary,
+                                      const int32_t* row_of, int local_w, int anchor_stride, int anchor_slots,
+                                      const int32_t* proto_blocks, int proto_k, const int32_t* proto_evict,
+                                      float scale, float* partials, int32_t* lengths, const void* q_rope_cos,
+                                      const void* q_rope_sin, const float* q_scale, const float* k_scale,
+                                      const float* v_scale, int passes, void* stream) {
+  clear_error();
+  return shortlist_attn_run(q, k, v, out, dtype, H, T, D, token_idx, row_head, head_map, N, P_cap, summary, row_of,
+                            local_w, anchor_stride, anchor_slots, proto_blocks, proto_k, proto_evict, scale, partials,
+                            lengths, q_rope_cos, q_rope_sin, q_scale, k_scale, v_scale, passes, 0, stream);
+}
+
+extern "C" int pfa_shortlist_attn_fwd_fused(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_tensor4 out, int dtype,
+                                            int H, int64_t T, int D, const int32_t* token_idx,
+                                            const int32_t* row_head, const int32_t* head_map, int64_t N, int P_cap,
+                                            const int32_t* summary, const int32_t* row_of, int local_w,
+                                            int anchor_stride, int anchor_slots, const int32_t* proto_blocks,
+                                            int proto_k, const int32_t* proto_evict, float scale, float* partials,
+                                            int32_t* lengths, const void* q_rope_cos, const void* q_rope_sin,
+                                            int passes, int fuse, void* stream) {
+  clear_error();
+  return shortlist_attn_run(q, k, v, out, dtype, H, T, D, token_idx, row_head, head_map, N, P_cap, summary, row_of,
+                            local_w, anchor_stride, anchor_slots, proto_blocks, proto_k, proto_evict, scale, partials,
+                            lengths, q_rope_cos, q_rope_sin, nullptr, nullptr, nullptr, passes, fuse, stream);
 }

@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "pfa_sparse_attn_fwd",
     "pfa_shortlist_attn_part_floats",
     "pfa_shortlist_attn_fwd",
+    "pfa_shortlist_attn_fwd_fused",
     "pfa_head_max_token",
     "pfa_quantize_heads_workspace_size",
     "pfa_quantize_heads_int8",
@@ -118,6 +119,9 @@ _SIGNATURES = {
     "pfa_shortlist_attn_fwd": ([Tensor4, Tensor4, Tensor4, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp, _i64,
                                 _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp, _vp,
                                 _vp, _vp, _i32, _vp], _i32),
+    "pfa_shortlist_attn_fwd_fused": ([Tensor4, Tensor4, Tensor4, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp,
+                                      _i64, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp,
+                                      _vp, _i32, _i32, _vp], _i32),
     "pfa_head_max_token": ([_vp, _vp, _i32, _vp, _vp], _i32),
     "pfa_quantize_heads_workspace_size": ([_i32, _i64, _i32, _i32, ctypes.POINTER(_sz)], _i32),
     "pfa_quantize_heads_int8": ([Tensor4, _i32, _i32, _i64, _i32, _vp, _i32, _vp, _i32, _f32, ctypes.c_double, _vp,

@@ -387,6 +387,11 @@ def shortlist_partials(N: int, device: torch.device) -> torch.Tensor:
     return torch.empty(N, int(_hip.lib().pfa_shortlist_attn_part_floats()), dtype=torch.float32, device=device)
 
 
+# pfa_shortlist_attn_fwd_fused bits (include/pfa_hip.h)
+FUSE_K_ROPE = 1
+FUSE_ZERO = 2
+
+
 def _shortlist_attn_structured(
     q4: "_hip.Tensor4",
     k4: "_hip.Tensor4",
@@ -412,6 +417,7 @@ def _shortlist_attn_structured(
     passes: int = 3,
     part: Optional[torch.Tensor] = None,
     qkv_scales: Optional[torch.Tensor] = None,
+    fuse: int = 0,
 ) -> Optional[torch.Tensor]:
     """Module-path shortlist attention without materialised candidates
     (bf16, D=64); the prototype sets come as _proto_prefix_blocks tables of
@@ -422,7 +428,11 @@ def _shortlist_attn_structured(
     anchor pass and 2 only the main pass (the caller orders them and passes
     the same `part`, from shortlist_partials, to both); 3 runs both.
     qkv_scales: (3, B*H) f32 per-head int8 scales of q, k, v (the tensors
-    then hold the int8 values as bf16, from quantize_heads_int8), or None."""
+    then hold the int8 values as bf16, from quantize_heads_int8), or None.
+    fuse: FUSE_K_ROPE | FUSE_ZERO bits for pfa_shortlist_attn_fwd_fused (the
+    anchor pass rotates k of the active heads with the q_rope tables and
+    zeroes the out rows without a packed row); needs anchors, passes 1 or 3,
+    head_map from the packing (ascending, B*H entries) and no int8 scales."""
 
     lib = _hip.lib()
     N = int(token_idx.numel())
@@ -443,6 +453,18 @@ def _shortlist_attn_structured(
         if (rc_cos.dtype != torch.bfloat16 or rc_sin.dtype != torch.bfloat16 or tuple(rc_cos.shape) != (int(T), 64)
                 or tuple(rc_sin.shape) != (int(T), 64) or not rc_cos.is_contiguous() or not rc_sin.is_contiguous()):
             raise ValueError("q_rope tables must be contiguous bf16 (T, 64)")
+    if fuse:
+        if qkv_scales is not None:
+            raise ValueError("the fused anchor pass has no int8 mode")
+        with _hip.TIMER.timed("shortlist_attn_fwd"):
+            rc = lib.pfa_shortlist_attn_fwd_fused(
+                q4, k4, v4, out4, _hip.PFA_BF16, int(H), int(T), int(D), _hip.ptr(token_idx), _hip.ptr(row_head),
+                _hip.ptr(head_map), N, int(head_map.numel()), _hip.ptr(summary), _hip.ptr(row_of), int(local_w),
+                int(stride), int(slots), _hip.ptr(blocks), K, _hip.ptr(evict), float(scale), _hip.ptr(part),
+                _hip.ptr(lengths), _hip.ptr(rc_cos), _hip.ptr(rc_sin), int(passes), int(fuse),
+                _hip.stream_ptr(device))
+        _hip.check(rc, "pfa_shortlist_attn_fwd_fused")
+        return lengths
     with _hip.TIMER.timed("shortlist_attn_fwd"):
         rc = lib.pfa_shortlist_attn_fwd(
             q4, k4, v4, out4, _hip.PFA_BF16, int(H), int(T), int(D), _hip.ptr(token_idx), _hip.ptr(row_head),

@@ -476,6 +476,17 @@ class AdaptiveSparseAttention(nn.Module):
         # structured shortlist path: rotate q rows inside the attention kernel
         # (only k is rotated in the QKV buffer); False rotates q in the buffer
         self.fuse_q_rope = True
+        # structured path with anchors: fuse_anchor_pass makes the anchor pass
+        # write the zeros of the output rows without a packed row (no zero
+        # fill of the output); with fuse_k_rope as well (and q rotated on
+        # load) it also rotates k, so no RoPE pass runs either.  Both are off
+        # by default: the RoPE pass and the zero fill run on the forked stream
+        # while the router, the packing and the prototype tables run on the
+        # calling stream, and they are done before the packing is; the anchor
+        # pass waits for the packing, so work moved into it lengthens the
+        # forward (measured at configs 3 and 4).
+        self.fuse_anchor_pass = False
+        self.fuse_k_rope = False
         # The prototype EMA statistics (sum_t gate * x) are accumulated inside
         # the router pass (x is read from HBM once; MFMA with exact products);
         # False accumulates them by a separate pass over x in the router's
@@ -934,34 +945,69 @@ class AdaptiveSparseAttention(nn.Module):
         row_head = torch.arange(BH, device=device, dtype=torch.int32).repeat_interleave(T)
         return token_idx, row_head
 
-    def _attend_dense_causal(self, qkv: torch.Tensor, B: int, T: int, out: torch.Tensor) -> None:
+    def _masked_rows(self, token_mask: torch.Tensor, B: int, T: int, device: torch.device):
+        """Rows of every head for the tokens token_mask keeps, packed on the
+        device (pfa_pack_rows with each token's head list = all H heads):
+        token_idx / row_head at capacity B*H*T, -1 / 0 past the device row
+        count, the compact head list and the packing summary ({P, N, ...})."""
+        H = self.h_total
+        BH = B * H
+        lib = _hip.lib()
+        hidx = torch.arange(H, dtype=torch.int32, device=device).repeat(B * T)
+        mask8 = torch.empty(BH, T, dtype=torch.uint8, device=device)
+        heads = torch.empty(BH, dtype=torch.int32, device=device)
+        row_offsets = torch.empty(BH + 1, dtype=torch.int32, device=device)
+        token_idx = torch.full((BH * T,), -1, dtype=torch.int32, device=device)
+        row_head = torch.zeros(BH * T, dtype=torch.int32, device=device)
+        summary = torch.empty(4, dtype=torch.int32, device=device)
+        ws = _sa._workspace(_sa._size_out(lib.pfa_pack_workspace_size, B, H, T), device)
+        tm8 = token_mask.contiguous().view(torch.uint8)
+        rc = lib.pfa_pack_rows(_hip.ptr(hidx), H, _hip.ptr(tm8), B, H, T, _hip.ptr(mask8), _hip.ptr(heads),
+                               _hip.ptr(row_offsets), _hip.ptr(token_idx), _hip.ptr(row_head), None,
+                               _hip.ptr(summary), _hip.ptr(ws), ws.numel(), _hip.stream_ptr(device))
+        _hip.check(rc, "pfa_pack_rows")
+        return token_idx, row_head, heads, summary
+
+    def _attend_dense_causal(self, qkv: torch.Tensor, B: int, T: int, out: torch.Tensor,
+                             token_mask: Optional[torch.Tensor] = None) -> None:
         """Every head and token, keys 0..t (force-dense / dense fast path).
         Equivalent to the reference's (T,T) triu(-inf) mask without
-        materialising it (aspa.py:1664-1677, 1365-1396)."""
+        materialising it (aspa.py:1664-1677, 1365-1396).  With token_mask
+        (B, T) only the rows of the kept tokens are attended and `out`
+        keeps its zeros elsewhere: the reference's dense output times the
+        token mask (aspa.py:1841-1842) without the multiply."""
         H, D = self.h_total, self.d_head
-        token_idx, row_head = self._full_rows(B, T, qkv.device)
+        head_map = n_dev = None
+        if token_mask is None:
+            token_idx, row_head = self._full_rows(B, T, qkv.device)
+        else:
+            token_idx, row_head, head_map, summary = self._masked_rows(token_mask, B, T, qkv.device)
+            n_dev = summary[1:2]
         q5 = qkv.view(B, T, 3, H, D)
         out4 = out.view(B, T, H, D)
         t4 = (_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
               _hip.tensor4(q5[:, :, 2], H, "bthd"), _hip.tensor4(out4, H, "bthd"))
         if out.dtype == qkv.dtype and _sa._mfma_causal_ok(qkv.dtype, D, *t4):
-            # flash-style causal tiles on MFMA (64 queries x 64 keys)
-            _sa._causal_attn_mfma(*t4, H, T, D, token_idx, row_head, None, qkv.device)
+            # flash-style causal tiles on MFMA (64 queries x 64 keys); rows
+            # past the device count carry token -1, which the kernel skips
+            _sa._causal_attn_mfma(*t4, H, T, D, token_idx, row_head, head_map, qkv.device)
             return
         _sa._attn_launch(_hip.tensor4(q5[:, :, 0], H, "bthd"), _hip.tensor4(q5[:, :, 1], H, "bthd"),
                          _hip.tensor4(q5[:, :, 2], H, "bthd"), qkv.dtype, _hip.tensor4(out4, H, "bthd"), out.dtype,
-                         H, T, D, token_idx, row_head, None, None, None, None, None, 1.0 / math.sqrt(D),
-                         (None, None, None), qkv.device)
+                         H, T, D, token_idx, row_head, head_map, None, None, None, None, 1.0 / math.sqrt(D),
+                         (None, None, None), qkv.device, n_rows_dev=n_dev)
 
     def _project_qkv(self, x: torch.Tensor) -> torch.Tensor:
         qkv = self.qkv(x).contiguous()  # (B, T, 3C) = (B, T, 3, H, D)
         self._rope_inplace(qkv, rotate_q=True)
         return qkv
 
-    def _rope_inplace(self, qkv: torch.Tensor, rotate_q: bool):
+    def _rope_inplace(self, qkv: torch.Tensor, rotate_q: bool, rotate_k: bool = True):
         """RoPE of the QKV buffer (aspa.py:606-618).  With rotate_q=False only
         k is rotated and the (cos, sin) tables are returned for a kernel that
-        rotates q rows as it loads them (pfa_shortlist_attn_fwd)."""
+        rotates q rows as it loads them (pfa_shortlist_attn_fwd); with
+        rotate_k=False as well nothing is launched and the tables are
+        returned for the fused anchor pass, which rotates k too."""
         if not self.use_rope:
             return None
         B, T = qkv.shape[0], qkv.shape[1]
@@ -970,6 +1016,10 @@ class AdaptiveSparseAttention(nn.Module):
         keep = self.__dict__.get("_capture_keep")
         if keep is not None:
             keep.extend((cos, sin))
+        if not rotate_q and not rotate_k:
+            return cos, sin
+        if rotate_q and not rotate_k:
+            raise ValueError("q alone is never rotated by the RoPE kernels")
         fn = _hip.lib().pfa_rope_qk_inplace if rotate_q else _hip.lib().pfa_rope_k_inplace
         with _hip.TIMER.timed("rope_qk"):
             rc = fn(_hip.ptr(qkv), _hip.dtype_tag(qkv.dtype), B, T, self.h_total, self.d_head, _hip.ptr(cos),
@@ -1048,6 +1098,10 @@ class AdaptiveSparseAttention(nn.Module):
     def reset_hip_graphs(self) -> None:
         self._resolve_stats()
         self._hip_graphs = {}
+        # the graphs' private memory pool goes with the last graph that used
+        # it: the next capture opens a new one (capturing into a released
+        # pool's handle fails inside the caching allocator)
+        self._hip_graph_pool = None
 
     def hip_graph_input(self, x: torch.Tensor) -> torch.Tensor:
         """The static input buffer of the graph that serves inputs shaped like
@@ -1403,11 +1457,20 @@ class AdaptiveSparseAttention(nn.Module):
         shortlist_path = not force_dense and not (P == 0 or N == 0 or (not need_summary and B * T == 0))
         plan = (plan_early or self._shortlist_plan(B, T, alpha, qkv.dtype)) if shortlist_path else None
         structured = plan is not None and plan["structured"]
+        # The structured kernel rotates q rows as it loads them; with anchors
+        # and fuse_anchor_pass its anchor pass (on the forked stream) writes
+        # the zeros of the rows without a packed row (no zero fill) and, with
+        # fuse_k_rope, rotates k as well (no RoPE pass).
+        q_fused = structured and self.fuse_q_rope and not use_quant
+        fuse = 0
+        if q_fused and self.fuse_anchor_pass and plan["stride"] > 0 and plan["slots"] > 0:
+            fuse = _sa.FUSE_ZERO | (_sa.FUSE_K_ROPE if (self.use_rope and self.fuse_k_rope) else 0)
         with torch.cuda.stream(fork_s):
-            # the structured kernel rotates q rows as it loads them: only k is
-            # rotated here
-            q_rope = self._rope_inplace(qkv, rotate_q=not (structured and self.fuse_q_rope and not use_quant))
-            attn = torch.zeros(B, T, C, dtype=qkv.dtype, device=device)
+            q_rope = self._rope_inplace(qkv, rotate_q=not q_fused, rotate_k=not (fuse & _sa.FUSE_K_ROPE))
+            if fuse:
+                attn = torch.empty(B, T, C, dtype=qkv.dtype, device=device)
+            else:
+                attn = torch.zeros(B, T, C, dtype=qkv.dtype, device=device)
         if not capture:
             # the forked stream's tensors are used (and freed) on this stream
             qkv.record_stream(main_s)
@@ -1423,7 +1486,9 @@ class AdaptiveSparseAttention(nn.Module):
         if force_dense:
             self._cached_active_mask = None
             self._cached_packing = None
-            self._attend_dense_causal(qkv, B, T, attn)
+            # a token mask keeps the rows of the kept tokens only; the others
+            # stay zero (attn starts zeroed)
+            self._attend_dense_causal(qkv, B, T, attn, token_mask=token_mask)
             if dense_reason == "alpha":
                 mode_label = "dense_alpha"
             else:
@@ -1457,7 +1522,7 @@ class AdaptiveSparseAttention(nn.Module):
             heads = active_heads[:P] if P >= 0 else active_heads
             self._run_shortlist_device(qkv, attn, B, T, tok, rh, heads, row_offsets, alpha, row_of, summary,
                                        plan=plan, q_rope=q_rope, streams=None if join_early else (main_s, fork_s),
-                                       before_join=None if join_early else ema, rows_dev=rows_dev)
+                                       before_join=None if join_early else ema, rows_dev=rows_dev, fuse=fuse)
             backend_info = self._last_shortlist_backend_info or get_last_backend_info()
             state = {
                 "mode": mode_label, "backend": str(backend_info.get("name", "shortlist")),
@@ -1478,8 +1543,6 @@ class AdaptiveSparseAttention(nn.Module):
                 for key, val in det.items():
                     state[f"linear_shortlist_{key}"] = val
             self._last_sparse_state = state
-        if force_dense and token_mask is not None:
-            attn.view(B, T, H, D).mul_(token_mask.view(B, T, 1, 1).to(attn.dtype))
         self.last_head_consensus = None if self.training else attn.detach()
         self.last_router_reg = router_reg
         stats_args = (token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
@@ -1533,7 +1596,7 @@ class AdaptiveSparseAttention(nn.Module):
 
     def _run_shortlist_device(self, qkv, attn, B, T, token_idx, row_head, heads, row_offsets, alpha, row_of,
                               summary, plan: Optional[Dict[str, Any]] = None, q_rope=None, streams=None,
-                              before_join=None, rows_dev: Optional[torch.Tensor] = None) -> None:
+                              before_join=None, rows_dev: Optional[torch.Tensor] = None, fuse: int = 0) -> None:
         """Candidate attention (aspa.py:1175-1310).
 
         When no row can be truncated to L, bf16 with D=64 and no int8 path,
@@ -1553,7 +1616,11 @@ class AdaptiveSparseAttention(nn.Module):
         starting on another one.
 
         rows_dev (materialised path only): a device int32 row count; the
-        token_idx / row_head given are then a capacity, valid up to it."""
+        token_idx / row_head given are then a capacity, valid up to it.
+
+        fuse (structured path with anchors only): FUSE_* bits of the anchor
+        pass -- k still unrotated (FUSE_K_ROPE) and attn not zero-filled
+        (FUSE_ZERO): the anchor pass does both."""
         H, D = self.h_total, self.d_head
         device = qkv.device
         if plan is None:
@@ -1562,6 +1629,8 @@ class AdaptiveSparseAttention(nn.Module):
         use_quant, w_eff, structured = plan["use_quant"], plan["w_eff"], plan["structured"]
         if q_rope is not None and not structured:
             raise RuntimeError("q rows left unrotated for a path that does not rotate them")
+        if fuse and not (structured and stride > 0 and slots > 0 and not use_quant):
+            raise RuntimeError("the anchor-pass fusions need the structured path with anchors")
         q5 = qkv.view(B, T, 3, H, D)
         if structured and rows_dev is not None:
             raise RuntimeError("the structured shortlist path takes the exact row count")
@@ -1597,7 +1666,7 @@ class AdaptiveSparseAttention(nn.Module):
                 # runs beside it
                 with torch.cuda.stream(fork_s):
                     _sa._shortlist_attn_structured(*t4, *args, None, None, scale, device, want_lengths=False,
-                                                   q_rope=q_rope, passes=1, part=part)
+                                                   q_rope=q_rope, passes=1, part=part, fuse=fuse)
                     anchored = torch.cuda.Event()
                     anchored.record(fork_s)
                     if before_join is not None:
@@ -1612,7 +1681,7 @@ class AdaptiveSparseAttention(nn.Module):
             passes = 2 if (part is not None and streams is not None) else 3
             lens = _sa._shortlist_attn_structured(
                 *t4, *args, blocks, evict, scale, device, want_lengths=bool(self.record_shortlist_lengths),
-                q_rope=q_rope, passes=passes, part=part, qkv_scales=qkv_scales)
+                q_rope=q_rope, passes=passes, part=part, qkv_scales=qkv_scales, fuse=fuse if passes == 3 else 0)
             if tail_on_fork:
                 # join: the forward ends after the tail
                 streams[0].wait_stream(streams[1])

@@ -672,6 +672,56 @@ def test_structured_fused_q_rope_bitwise(dev, T, L, w, s, B):
     assert torch.equal(outs[0][0], outs[1][0])
 
 
+@pytest.mark.parametrize("T,L,w,s,B,heads,krope", [(4096, 1024, 256, 64, 1, None, True),
+                                                    (3000, 700, 100, 37, 2, 3, True),
+                                                    (3000, 700, 100, 37, 2, 3, False),
+                                                    (65536, 2048, 512, 256, 1, None, True),
+                                                    (65536, 2048, 512, 256, 1, None, False)])
+def test_structured_fused_anchor_pass_bitwise(dev, T, L, w, s, B, heads, krope):
+    """The anchor pass that writes the zeros of the rows without a packed
+    row, and (krope) rotates k (pfa_shortlist_attn_fwd_fused), gives exactly
+    the bits of the separate zero fill and RoPE pass: attention rows,
+    output, and the zeros.  With the gates mapped onto the first `heads`
+    heads the other heads have no rows at all (the workgroups past the
+    active heads zero them); the output buffer is left to start from NaN
+    garbage."""
+    import torch.nn.functional as F
+
+    from configs import shortlist_cfg
+
+    _say(f"fused anchor pass T={T} B={B} heads={heads} k-rope={krope}")
+    cfg = shortlist_cfg(T, 512, 8, L, w, s)
+    m, x = _module(cfg, B, T, 512, torch.bfloat16, dev, 0.01)
+    if heads is not None:
+        with torch.no_grad():
+            m.gate_to_head.copy_(torch.arange(m.attn_gates, device=dev) % heads)
+            m.gate_to_head_onehot.copy_(F.one_hot(m.gate_to_head, 8).to(m.gate_to_head_onehot.dtype))
+    snap = {n: b.detach().clone() for n, b in m.named_buffers() if n.startswith("routing_")}
+    outs = []
+    with torch.no_grad():
+        for fuse in (True, False):
+            for n, b in snap.items():
+                getattr(m, n).copy_(b)
+            m.fuse_anchor_pass = fuse
+            m.fuse_k_rope = fuse and krope
+            # NaN in the allocator's free blocks: an output row the fused
+            # pass failed to write would keep it
+            junk = torch.full((4 * B * T * 512,), float("nan"), dtype=torch.bfloat16, device=dev)
+            del junk
+            y = m(x)
+            st = m._last_sparse_state
+            assert st["linear_shortlist_structured"] is True
+            outs.append((y.clone(), m.last_head_consensus.clone(), st["active_head_indices"].cpu().clone()))
+    assert torch.equal(outs[0][2], outs[1][2])
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][0], outs[1][0])
+    if heads is not None:
+        act = outs[0][2].tolist()
+        assert len(act) == B * heads and all(bh % 8 < heads for bh in act)
+        attn4 = outs[0][1].view(B, T, 8, 64)
+        assert bool((attn4[:, :, heads:] == 0).all())
+
+
 # ---------------------------------------------------------------------------
 # attention operator
 # ---------------------------------------------------------------------------
@@ -922,6 +972,18 @@ def test_module_hip_graph_static_output_matches_eager(dev):
     for i, (e, g) in enumerate(zip(eager, graph)):
         assert torch.equal(e[0], g[0]), f"forward {i}: output differs"
     m.enable_hip_graph(False)
+    # graph mode switched off and on again, with and without the captured
+    # projection, captures anew each time (each capture after a reset opens
+    # a new memory pool)
+    for static in (False, True, False):
+        for n, b in m.named_buffers():
+            b.copy_(init[n])
+        m.enable_hip_graph(True, static_output=static)
+        with torch.no_grad():
+            for i, xi in enumerate(xs):
+                y = m(xi).float().cpu()
+                assert torch.equal(y, eager[i][0]), f"recapture (static={static}) forward {i}: output differs"
+        m.enable_hip_graph(False)
 
 
 def test_module_hip_graph_token_mask_matches_eager(dev):
@@ -1247,33 +1309,46 @@ def test_operator_causal_branch_mfma_vs_oracle(dev, BH, T, p):
     assert torch.count_nonzero(o[~mask]) == 0
 
 
-def test_module_force_dense_mfma_vs_oracle(dev):
-    """subquad mode (force-dense, aspa.py:1624-1677) at T = 8,192 in bf16:
-    the attention output equals causal attention of the module's own
-    projected and rotated q/k/v."""
+@pytest.mark.parametrize("B,T,dt,keep", [(1, 8192, torch.bfloat16, None), (2, 4096, torch.bfloat16, 0.3),
+                                         (2, 2048, torch.float32, 0.3)])
+def test_module_force_dense_mfma_vs_oracle(dev, B, T, dt, keep):
+    """subquad mode (force-dense, aspa.py:1624-1677): the attention output
+    equals causal attention of the module's own projected and rotated
+    q/k/v (bf16 on the MFMA causal tiles, f32 on the row kernel).  With
+    token sparsity (keep) only the kept tokens' rows are attended and the
+    others are exactly zero: the reference's dense output times the token
+    mask (aspa.py:1841-1842)."""
     from configs import COMMON
 
     from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
 
-    B, T, C, H = 1, 8192, 512, 8
-    _say(f"module force-dense T={T}")
+    C, H = 512, 8
+    _say(f"module force-dense B={B} T={T} {dt} keep={keep}")
     torch.manual_seed(0)
+    extra = dict(attn_token_sparse=False) if keep is None else dict(
+        attn_token_sparse=True, attn_token_keep_ratio=keep, attn_linear_token_keep_schedule="fixed")
     m = AdaptiveSparseAttention(ModelConfig(**dict(COMMON, d_model=C, n_head=H, attn_h_total=H, attn_gates=H,
-                                                   attn_mode="subquad", attn_token_sparse=False)))
-    m = m.to(dev, torch.bfloat16).eval()
-    x = torch.randn(B, T, C, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(dev)
+                                                   attn_mode="subquad", **extra)))
+    m = m.to(dev, dt).eval()
+    x = torch.randn(B, T, C, generator=torch.Generator().manual_seed(3)).to(dt).to(dev)
     with torch.no_grad():
         m(x)
         qkv = m.qkv(x).view(B, T, 3, H, 64).cpu()
     assert m._last_sparse_state["mode"].startswith("dense")
-    cos, sin = (t.cpu() for t in m._rope_factors(T, dev, torch.bfloat16))
+    cos, sin = (t.cpu() for t in m._rope_factors(T, dev, dt))
     q = O.apply_rope(qkv[:, :, 0], cos, sin)
     k = O.apply_rope(qkv[:, :, 1], cos, sin)
     qh, kh, vh = (a.permute(0, 2, 1, 3).reshape(B * H, T, 64) for a in (q, k, qkv[:, :, 2]))
     ref = O.causal_attention_f32(qh, kh, vh).view(B, H, T, 64).permute(0, 2, 1, 3).reshape(B, T, C)
-    err = float((m.last_head_consensus.float().cpu() - ref).abs().max())
+    got = m.last_head_consensus.float().cpu()
+    if keep is not None:
+        tm = m._last_token_mask.cpu()
+        assert 0 < int(tm.sum()) < B * T
+        ref = ref * tm.view(B, T, 1).float()
+        assert bool((got[~tm] == 0).all())
+    err = float((got - ref).abs().max())
     _say(f"max-abs err {err:.3e}")
-    assert err <= TOL_BF16
+    assert err <= (TOL_BF16 if dt == torch.bfloat16 else TOL_F32)
 
 
 def test_operator_rejects_out_of_range_prepacked_rows(dev):
