@@ -1230,17 +1230,21 @@ class AdaptiveSparseAttention(nn.Module):
             self.__dict__[k] = v
         st = ent["sparse_state"]
         self._last_sparse_state = dict(st) if st is not None else None
-        self._finish_stats(*ent["stats_args"])
-        self._finish_forward(ent["label"], ev0, ev1)
+        # the latency's end event, recorded after the telemetry copy, also
+        # marks that copy done (one event after the replay instead of two)
+        self._finish_stats(*ent["stats_args"], done=ev1)
+        self._finish_forward(ent["label"], ev0, ev1, ended=ev1 is not None)
         return y
 
     # ------------------------------------------------------------------
-    def _finish_forward(self, label: str, ev0, ev1) -> None:
+    def _finish_forward(self, label: str, ev0, ev1, ended: bool = False) -> None:
         """Latency and mode labels of this forward, deferred with its other
-        statistics (the latency needs the end event)."""
+        statistics (the latency needs the end event; ended: ev1 is already
+        recorded)."""
         st_now = self.__dict__.get("_lazy__last_sparse_state")
         if self.track_latency and ev0 is not None:
-            ev1.record()
+            if not ended:
+                ev1.record()
 
             def latency(self, st=st_now):
                 ev1.synchronize()
@@ -1552,8 +1556,9 @@ class AdaptiveSparseAttention(nn.Module):
             return attn, stats_args, label
         y = self.dropout(self.proj(attn))
 
-        self._finish_stats(*stats_args)
-        finish(label)
+        # the latency's end event also marks the telemetry copy done
+        self._finish_stats(*stats_args, done=ev1)
+        self._finish_forward(label, ev0, ev1, ended=ev1 is not None)
         if self.linear_mem_budget_mb and device.type == "cuda":
             allocated = torch.cuda.memory_allocated(device) / (1024 * 1024)
             if allocated > self.linear_mem_budget_mb * 1.1:
@@ -1754,14 +1759,16 @@ class AdaptiveSparseAttention(nn.Module):
         return self.router_reg_lambda * total
 
     def _finish_stats(self, token_mask, topk, adaptive_topk, P, N, max_rows, density_threshold, alpha, mode_label,
-                      dense_reason, B, T, active_heads, row_offsets, summary, comb) -> None:
+                      dense_reason, B, T, active_heads, row_offsets, summary, comb, done=None) -> None:
         """Telemetry dictionaries (aspa.py:1857-1916) from the router's
         statistics and the packing summary.  `comb` (the reduced router
         statistics, the summary and the active heads, under a hundred bytes
         for the usual head counts) is copied into pinned host memory without
         waiting -- a large device-to-host copy would make the host wait for
         the device -- and the dictionaries are built when first read (or at
-        the next forward), so the forward never stalls the device queue."""
+        the next forward), so the forward never stalls the device queue.
+        done: an event of the caller's, not yet recorded, that is recorded
+        here after the copy (the caller's latency end event), or None."""
         self._resolve_stats()
         H = self.h_total
         with torch.no_grad():
@@ -1773,10 +1780,11 @@ class AdaptiveSparseAttention(nn.Module):
                 self.__dict__["_stats_host"] = h
             h.copy_(comb, non_blocking=True)
             host = (h[:16].view(torch.float64), h[16:20], h[20:])
-            done = self.__dict__.get("_stats_event")
             if done is None:
-                done = torch.cuda.Event()
-                self.__dict__["_stats_event"] = done
+                done = self.__dict__.get("_stats_event")
+                if done is None:
+                    done = torch.cuda.Event()
+                    self.__dict__["_stats_event"] = done
             done.record()
         # everything the dictionaries need from the host side, as of now
         st = self.__dict__.get("_lazy__last_sparse_state")
