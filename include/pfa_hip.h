@@ -446,6 +446,16 @@ int pfa_rope_qk_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D,
 int pfa_rope_k_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D,
                        const void* cos_tab, const void* sin_tab, void* stream);
 
+/* pfa_rope_k_inplace that also writes zeros to zero_out, the (B, T, H*D)
+ * attention output of the same dtype (16-byte aligned), in the same pass:
+ * the module's zero-initialised output (aspa.py:1707, the tensor the
+ * attention fills only at active (head, token) rows) without a separate
+ * fill over it.  The RoPE bits are those of pfa_rope_k_inplace; shapes
+ * other than D = 64 rotate first and then fill. */
+int pfa_rope_k_zero_inplace(void* qkv, int dtype, int B, int64_t T, int H,
+                            int D, const void* cos_tab, const void* sin_tab,
+                            void* zero_out, void* stream);
+
 /* ====================================================================
  * Fill: write zeros into `bytes` of device memory with a vector-store
  * kernel (usable where memset nodes are not wanted).

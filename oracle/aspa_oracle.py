@@ -17,6 +17,8 @@ Pinning (what checks each function beyond re-reading the formula):
   select_active_tokens         golden vectors + brute force
   pack_active_rows             closed form (nonzero order, bincount, scan)
   proto_prefix_sets            brute force per token on tiny T; C oracle
+  proto_prefix_evict           membership p <= t < evict[p] against
+                               proto_prefix_sets on small T with ties
   build_shortlist              golden vectors from the reference builders,
                                the reference test's independent restatement
                                semantics (local/anchor closed forms), C oracle
@@ -174,6 +176,50 @@ def proto_prefix_sets(scores: torch.Tensor, K: int) -> torch.Tensor:
         row[:c] = torch.sort(idx).values
         out[t] = row
     return out
+
+
+def proto_prefix_evict(scores: torch.Tensor, K: int) -> torch.Tensor:
+    """(T,) scores -> (T,) int64 evict[p]: the first t at which p is no
+    longer in the prefix top-K set S(t) of proto_prefix_sets (sparse_attn.py
+    :260-300), p when it never enters, 2^31 - 1 when it is in S(T - 1).
+
+    Under the order of topk_lowest (value descending, then index ascending)
+    p is in S(t) exactly while p <= t and fewer than K positions q <= t are
+    better than p; that count only grows with t, so p leaves at the position
+    of the K-th better element.  The positions of the better elements are
+    those seen before p in key order: a Fenwick tree over positions gives the
+    K-th smallest of them.  O(T log T), for sequences too long for the brute
+    force (pinned against proto_prefix_sets on small T with ties)."""
+
+    v = scores.detach().to(torch.float64).cpu().tolist()
+    T = len(v)
+    order = sorted(range(T), key=lambda i: (-v[i], i))
+    tree = [0] * (T + 1)
+    log = 1
+    while (1 << log) <= T:
+        log += 1
+    out = [0] * T
+    seen = 0
+    big = 2 ** 31 - 1
+    for p in order:
+        if seen >= K:
+            # K-th smallest seen position: binary lifting over the tree
+            pos, rem = 0, K
+            for b in range(log, -1, -1):
+                nxt = pos + (1 << b)
+                if nxt <= T and tree[nxt] < rem:
+                    pos = nxt
+                    rem -= tree[nxt]
+            tau = pos  # 0-based position of the K-th better element
+            out[p] = tau if tau > p else p
+        else:
+            out[p] = big
+        i = p + 1
+        while i <= T:
+            tree[i] += 1
+            i += i & -i
+        seen += 1
+    return torch.tensor(out, dtype=torch.long)
 
 
 def build_shortlist(

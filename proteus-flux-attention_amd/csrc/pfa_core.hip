@@ -69,10 +69,13 @@ __global__ void __launch_bounds__(256) rope8_kernel(typename Elem<DT>::T* qkv, i
 // share one table row.  A 256-thread workgroup rotates 256 / groups whole
 // rows (one row, looping, when a row has more groups than threads).  Index
 // math is shifts and one compare per group (no 64-bit division per element).
+// zout (k only, or null): the (rows, H*64) attention output, whose row bt
+// gets zeros from the same threads (group e writes elements 8e .. 8e+7).
 template <int DT>
 __global__ void __launch_bounds__(256) rope64_row_kernel(typename Elem<DT>::T* qkv, int64_t rows, int64_t T,
                                                          int H, const typename Elem<DT>::T* cos_tab,
-                                                         const typename Elem<DT>::T* sin_tab, int nparts) {
+                                                         const typename Elem<DT>::T* sin_tab, int nparts,
+                                                         typename Elem<DT>::T* zout) {
   const int groups = nparts * H * 8;
   const bool wide = groups >= 256;
   const int rpw = wide ? 1 : 256 / groups;
@@ -96,6 +99,10 @@ __global__ void __launch_bounds__(256) rope64_row_kernel(typename Elem<DT>::T* q
     load8<DT>(sin_tab + t * 64 + 8 * g8, sv);
     rope_rotate8<DT>(xv, cv, sv, o);
     store8<DT>(row + off, o);
+    if (zout != nullptr) {
+      const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      store8<DT>(zout + bt * (int64_t)C + 8 * e, z);
+    }
   }
 }
 
@@ -161,15 +168,29 @@ extern "C" int pfa_zero_fill(void* ptr, size_t bytes, void* stream) {
   return PFA_OK;
 }
 
+// zero_out (k only, or null): a (B, T, H*D) output to fill with zeros in the
+// same pass (D = 64 row kernel) or by pfa_zero_fill after it.
+static int rope_inplace_impl(void* qkv, int dtype, int B, int64_t T, int H, int D, const void* cos_tab,
+                             const void* sin_tab, int nparts, void* stream, void* zero_out, bool* zeroed);
 static int rope_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D, const void* cos_tab,
-                        const void* sin_tab, int nparts, void* stream) {
+                        const void* sin_tab, int nparts, void* stream, void* zero_out = nullptr) {
+  bool zeroed = false;
+  const int rc = rope_inplace_impl(qkv, dtype, B, T, H, D, cos_tab, sin_tab, nparts, stream, zero_out, &zeroed);
+  if (rc != PFA_OK || zero_out == nullptr || zeroed) return rc;
+  const size_t esz = dtype == PFA_F32 ? 4 : 2;
+  return pfa_zero_fill(zero_out, (size_t)B * (size_t)T * (size_t)H * (size_t)D * esz, stream);
+}
+static int rope_inplace_impl(void* qkv, int dtype, int B, int64_t T, int H, int D, const void* cos_tab,
+                             const void* sin_tab, int nparts, void* stream, void* zero_out, bool* zeroed) {
   PFA_CHECK_ARG(qkv && cos_tab && sin_tab, "pfa_rope_qk_inplace: null pointer");
+  PFA_CHECK_ARG(zero_out == nullptr || nparts == 1, "pfa_rope_qk_inplace: the zero output goes with k only");
   PFA_CHECK_ARG(B >= 0 && T >= 0 && H > 0 && D > 0 && D % 2 == 0,
                 "pfa_rope_qk_inplace: bad shape B=%d T=%lld H=%d D=%d", B, (long long)T, H, D);
   hipStream_t s = as_stream(stream);
   const bool vec = (D % 8) == 0 && ((uintptr_t)qkv % 16) == 0 && ((uintptr_t)cos_tab % 16) == 0 &&
                    ((uintptr_t)sin_tab % 16) == 0;
-  if (vec && D == 64 && (int64_t)B * T < INT32_MAX && H <= 256) {
+  const bool zvec = zero_out == nullptr || ((uintptr_t)zero_out % 16) == 0;
+  if (vec && zvec && D == 64 && (int64_t)B * T < INT32_MAX && H <= 256) {
     const int64_t rows = (int64_t)B * T;
     if (rows == 0) return PFA_OK;
     const int groups = nparts * H * 8;
@@ -179,21 +200,25 @@ static int rope_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D, co
     switch (dtype) {
       case PFA_F32:
         rope64_row_kernel<PFA_F32><<<nblk, threads, 0, s>>>((float*)qkv, rows, T, H, (const float*)cos_tab,
-                                                                      (const float*)sin_tab, nparts);
+                                                                      (const float*)sin_tab, nparts,
+                                                                      (float*)zero_out);
         break;
       case PFA_BF16:
         rope64_row_kernel<PFA_BF16><<<nblk, threads, 0, s>>>((uint16_t*)qkv, rows, T, H, (const uint16_t*)cos_tab,
-                                                                       (const uint16_t*)sin_tab, nparts);
+                                                                       (const uint16_t*)sin_tab, nparts,
+                                                                       (uint16_t*)zero_out);
         break;
       case PFA_F16:
         rope64_row_kernel<PFA_F16><<<nblk, threads, 0, s>>>((uint16_t*)qkv, rows, T, H, (const uint16_t*)cos_tab,
-                                                                      (const uint16_t*)sin_tab, nparts);
+                                                                      (const uint16_t*)sin_tab, nparts,
+                                                                      (uint16_t*)zero_out);
         break;
       default:
         set_error("pfa_rope_qk_inplace: unsupported dtype %d", dtype);
         return PFA_E_UNSUPPORTED;
     }
     PFA_CHECK_LAUNCH("pfa_rope_qk_inplace");
+    *zeroed = true;
     return PFA_OK;
   }
   if (vec) {
@@ -254,4 +279,11 @@ extern "C" int pfa_rope_k_inplace(void* qkv, int dtype, int B, int64_t T, int H,
                                   const void* sin_tab, void* stream) {
   clear_error();
   return rope_inplace(qkv, dtype, B, T, H, D, cos_tab, sin_tab, 1, stream);
+}
+
+extern "C" int pfa_rope_k_zero_inplace(void* qkv, int dtype, int B, int64_t T, int H, int D, const void* cos_tab,
+                                       const void* sin_tab, void* zero_out, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(zero_out != nullptr, "pfa_rope_k_zero_inplace: null output");
+  return rope_inplace(qkv, dtype, B, T, H, D, cos_tab, sin_tab, 1, stream, zero_out);
 }

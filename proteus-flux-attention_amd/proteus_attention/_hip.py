@@ -54,6 +54,7 @@ EXPORTED_SYMBOLS = (
     "pfa_quantize_heads_int8",
     "pfa_rope_qk_inplace",
     "pfa_rope_k_inplace",
+    "pfa_rope_k_zero_inplace",
     "pfa_router_stats_reduce",
     "pfa_zero_fill",
     "pfa_chunk_topk_workspace_size",
@@ -128,6 +129,7 @@ _SIGNATURES = {
                                  _i32, Tensor4, _i32, _vp, _vp, _sz, _vp], _i32),
     "pfa_rope_qk_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
     "pfa_rope_k_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp], _i32),
+    "pfa_rope_k_zero_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "pfa_router_stats_reduce": ([_vp, _i32, _vp, _vp], _i32),
     "pfa_zero_fill": ([_vp, _sz, _vp], _i32),
     "pfa_chunk_topk_workspace_size": ([_i64, _i32, ctypes.POINTER(_sz)], _i32),

@@ -1002,13 +1002,18 @@ class AdaptiveSparseAttention(nn.Module):
         self._rope_inplace(qkv, rotate_q=True)
         return qkv
 
-    def _rope_inplace(self, qkv: torch.Tensor, rotate_q: bool, rotate_k: bool = True):
+    def _rope_inplace(self, qkv: torch.Tensor, rotate_q: bool, rotate_k: bool = True,
+                      zero_out: Optional[torch.Tensor] = None):
         """RoPE of the QKV buffer (aspa.py:606-618).  With rotate_q=False only
         k is rotated and the (cos, sin) tables are returned for a kernel that
         rotates q rows as it loads them (pfa_shortlist_attn_fwd); with
         rotate_k=False as well nothing is launched and the tables are
-        returned for the fused anchor pass, which rotates k too."""
+        returned for the fused anchor pass, which rotates k too.  zero_out
+        (k alone rotated): the attention output, filled with zeros by the same
+        pass (pfa_rope_k_zero_inplace); with RoPE off it is filled here."""
         if not self.use_rope:
+            if zero_out is not None:
+                zero_out.zero_()
             return None
         B, T = qkv.shape[0], qkv.shape[1]
         cos, sin = self._rope_factors(T, qkv.device, qkv.dtype)
@@ -1020,11 +1025,19 @@ class AdaptiveSparseAttention(nn.Module):
             return cos, sin
         if rotate_q and not rotate_k:
             raise ValueError("q alone is never rotated by the RoPE kernels")
-        fn = _hip.lib().pfa_rope_qk_inplace if rotate_q else _hip.lib().pfa_rope_k_inplace
+        if zero_out is not None and (rotate_q or not rotate_k):
+            raise ValueError("the output zero fill rides on the k-only RoPE pass")
+        lib = _hip.lib()
+        args = (_hip.ptr(qkv), _hip.dtype_tag(qkv.dtype), B, T, self.h_total, self.d_head, _hip.ptr(cos),
+                _hip.ptr(sin))
         with _hip.TIMER.timed("rope_qk"):
-            rc = fn(_hip.ptr(qkv), _hip.dtype_tag(qkv.dtype), B, T, self.h_total, self.d_head, _hip.ptr(cos),
-                    _hip.ptr(sin), _hip.stream_ptr(qkv.device))
-        _hip.check(rc, "pfa_rope_qk_inplace" if rotate_q else "pfa_rope_k_inplace")
+            if zero_out is not None:
+                name = "pfa_rope_k_zero_inplace"
+                rc = lib.pfa_rope_k_zero_inplace(*args, _hip.ptr(zero_out), _hip.stream_ptr(qkv.device))
+            else:
+                name = "pfa_rope_qk_inplace" if rotate_q else "pfa_rope_k_inplace"
+                rc = getattr(lib, name)(*args, _hip.stream_ptr(qkv.device))
+        _hip.check(rc, name)
         return None if rotate_q else (cos, sin)
 
     def _forward_dense_fastpath(self, x: torch.Tensor) -> torch.Tensor:
@@ -1470,10 +1483,16 @@ class AdaptiveSparseAttention(nn.Module):
         if q_fused and self.fuse_anchor_pass and plan["stride"] > 0 and plan["slots"] > 0:
             fuse = _sa.FUSE_ZERO | (_sa.FUSE_K_ROPE if (self.use_rope and self.fuse_k_rope) else 0)
         with torch.cuda.stream(fork_s):
-            q_rope = self._rope_inplace(qkv, rotate_q=not q_fused, rotate_k=not (fuse & _sa.FUSE_K_ROPE))
+            rot_k = not (fuse & _sa.FUSE_K_ROPE)
             if fuse:
                 attn = torch.empty(B, T, C, dtype=qkv.dtype, device=device)
+                q_rope = self._rope_inplace(qkv, rotate_q=not q_fused, rotate_k=rot_k)
+            elif q_fused and rot_k:
+                # k rotated alone: the same pass writes the output's zeros
+                attn = torch.empty(B, T, C, dtype=qkv.dtype, device=device)
+                q_rope = self._rope_inplace(qkv, rotate_q=False, rotate_k=True, zero_out=attn)
             else:
+                q_rope = self._rope_inplace(qkv, rotate_q=not q_fused, rotate_k=rot_k)
                 attn = torch.zeros(B, T, C, dtype=qkv.dtype, device=device)
         if not capture:
             # the forked stream's tensors are used (and freed) on this stream

@@ -167,6 +167,36 @@ def test_proto_evict_matches_prefix_sets(dev):
             assert torch.equal(member, by_evict), (T, K, b)
 
 
+@pytest.mark.parametrize("T,K,tied", [(65536, 205, False), (65536, 900, True), (40000, 1700, False),
+                                       (70000, 205, True), (70000, 1100, False)])
+def test_proto_prefix_tables_long_vs_evict_oracle(dev, T, K, tied):
+    """Long sequences (one to four superblock sizes, K below and above the
+    1,024-key sort): evict equals the O(T log T) evict oracle for every
+    position, and every block's set table row is the set
+    {p < 64j : evict[p] >= 64j} best first."""
+    from proteus_attention.kernels import sparse_attn as sa
+
+    _say(f"prefix tables vs evict oracle T={T} K={K} tied={tied}")
+    g = torch.Generator().manual_seed(41 + T + K)
+    s = torch.randint(0, 50, (1, T), generator=g).float() if tied else torch.rand(1, T, generator=g)
+    blk, ev = sa._proto_prefix_blocks(s.to(dev), K)
+    ev = ev.cpu().long()[0]
+    exp = O.proto_prefix_evict(s[0], K)
+    assert torch.equal(ev, exp)
+    blk = blk.cpu().long()[0].numpy()
+    evn = exp.numpy()
+    sc = s[0].numpy()
+    nb = (T + 63) // 64
+    for j in list(range(0, nb, max(1, nb // 61))) + [nb - 1]:
+        t0 = 64 * j
+        want = np.nonzero(evn[:t0] >= t0)[0] if t0 > 0 else np.zeros(0, dtype=np.int64)
+        row = blk[j][blk[j] != 2 ** 31 - 1]
+        assert len(row) == len(want) == min(K, t0), (j, len(row), len(want))
+        assert np.array_equal(np.sort(row), want), j
+        keys = [(-float(sc[v]), int(v)) for v in row]
+        assert keys == sorted(keys), j
+
+
 def test_proto_prefix_blocks_match_sets(dev):
     """Block tables: row j is the set of token 64j-1 (best first), and
     set(t) = {p in row t/64 U [64(t/64), t] : evict[p] > t}; evict agrees with
@@ -618,6 +648,33 @@ def test_rope_kernel_bitwise(dev, dt, B, T, H, D, k_only):
         assert torch.equal(got[:, :, 0], O.apply_rope(ref[:, :, 0], cos, sin))
     assert torch.equal(got[:, :, 1], O.apply_rope(ref[:, :, 1], cos, sin))
     assert torch.equal(got[:, :, 2], ref[:, :, 2])
+
+
+@pytest.mark.parametrize("dt,B,T,H,D", [(torch.bfloat16, 1, 4099, 8, 64), (torch.bfloat16, 2, 333, 40, 64),
+                                         (torch.float32, 1, 517, 4, 64), (torch.bfloat16, 1, 300, 4, 16),
+                                         (torch.float16, 2, 77, 3, 12)])
+def test_rope_k_zero_bitwise(dev, dt, B, T, H, D):
+    """pfa_rope_k_zero_inplace: k gets exactly the bits of pfa_rope_k_inplace
+    and the (B, T, H*D) output, poisoned with NaN, comes out all zeros; the
+    D=64 token-row kernel writes the zeros itself (H=40: rows wider than a
+    workgroup), other shapes rotate and then fill."""
+    from proteus_attention import _hip
+
+    g = torch.Generator().manual_seed(15)
+    qkv = torch.randn(B, T, 3 * H * D, generator=g).to(dt)
+    cos, sin = O.rope_tables(T, D, 10000.0, dt)
+    cd, sd = cos.to(dev), sin.to(dev)
+    a = qkv.to(dev).contiguous()
+    b = qkv.to(dev).contiguous()
+    out = torch.full((B, T, H * D), float("nan"), dtype=dt, device=dev)
+    lib = _hip.lib()
+    _hip.check(lib.pfa_rope_k_inplace(_hip.ptr(a), _hip.dtype_tag(dt), B, T, H, D, _hip.ptr(cd), _hip.ptr(sd),
+                                      _hip.stream_ptr(dev)), "rope_k")
+    _hip.check(lib.pfa_rope_k_zero_inplace(_hip.ptr(b), _hip.dtype_tag(dt), B, T, H, D, _hip.ptr(cd), _hip.ptr(sd),
+                                           _hip.ptr(out), _hip.stream_ptr(dev)), "rope_k_zero")
+    assert torch.equal(a.cpu().view(torch.int8), b.cpu().view(torch.int8))
+    assert bool((out == 0).all())
+    assert torch.equal(b.cpu().view(B, T, 3, H, D)[:, :, 1], O.apply_rope(qkv.view(B, T, 3, H, D)[:, :, 1], cos, sin))
 
 
 @pytest.mark.parametrize("T,B", [(4096, 1), (3000, 2)])

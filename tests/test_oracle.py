@@ -125,6 +125,33 @@ def test_proto_prefix_sets_brute_force():
         assert sets[t, :c].tolist() == sorted(best)
 
 
+def test_proto_prefix_evict_matches_brute_force_sets():
+    """p is in S(t) exactly when p <= t < evict[p], for the evict oracle
+    against the brute-force sets, with heavy ties, K above and below T; a
+    planted mistake (the (K+1)-th better element taken for the K-th) must
+    fail."""
+    g = torch.Generator().manual_seed(31)
+    for T, K in ((300, 7), (130, 64), (200, 200), (65, 1), (257, 64), (90, 300)):
+        s = torch.randint(0, 7, (T,), generator=g).float()
+        ev = O.proto_prefix_evict(s, K)
+        exp = O.proto_prefix_sets(s, K)
+        member = torch.zeros(T, T, dtype=torch.bool)
+        for t in range(T):
+            member[t, exp[t, : min(t + 1, K)]] = True
+        pos = torch.arange(T)
+        assert torch.equal(member, (pos[None, :] <= pos[:, None]) & (ev[None, :] > pos[:, None])), (T, K)
+    # planted mistake: the (K+1)-th better element taken for the K-th
+    T, K = 150, 6
+    s = torch.randint(0, 4, (T,), generator=g).float()
+    exp = O.proto_prefix_sets(s, K)
+    member = torch.zeros(T, T, dtype=torch.bool)
+    for t in range(T):
+        member[t, exp[t, : min(t + 1, K)]] = True
+    pos = torch.arange(T)
+    off = O.proto_prefix_evict(s, K + 1)
+    assert not torch.equal(member, (pos[None, :] <= pos[:, None]) & (off[None, :] > pos[:, None]))
+
+
 def test_c_oracle_matches_torch_oracle_with_ties():
     g = torch.Generator().manual_seed(9)
     T = 500
