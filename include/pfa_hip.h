@@ -115,6 +115,29 @@ int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G,
                     float* head_score, float* stats_partial, float* ema_partial,
                     void* stream);
 
+/* pfa_router_topk with its inputs built inside the router's workgroups
+ * instead of by pfa_router_prepare (the same arithmetic, thread map and
+ * reduction order, so the same bits): w_router (G, C) and the buffers
+ * protos (G, C) (NULL: no prototype prior), confidence and usage (G)
+ * (NULL: unused) as they are.  One launch fewer at the head of the router
+ * chain (aspa.py:636-663 + 628-690).  Supported when
+ * pfa_router_raw_supported(...) returns 1: bf16 x, weights and buffers,
+ * G <= 16, C a multiple of 128 up to 768 (G <= 8) or 512; otherwise
+ * PFA_E_UNSUPPORTED. */
+int pfa_router_raw_supported(int x_dtype, int w_dtype, int buf_dtype, int G,
+                             int C, int use_proto);
+int pfa_router_topk_raw(const void* x, int x_dtype, int64_t n_tok, int C,
+                        int G, const void* w_router, int w_dtype,
+                        const void* protos, const void* confidence,
+                        const void* usage, int buf_dtype,
+                        const int32_t* gate_to_head, int H, int topk,
+                        float proto_temp, float proto_threshold,
+                        float proto_blend, float usage_boost,
+                        float* gate_probs, float* sim, float* blend,
+                        float* importance, int32_t* head_idx,
+                        float* head_score, float* stats_partial,
+                        float* ema_partial, void* stream);
+
 /* ====================================================================
  * Prototype EMA statistics (aspa.py:692-718): per slice of tokens the
  * partial sums  sum_t gate[t,g]*x[t,c]  (columns 0..C-1) and

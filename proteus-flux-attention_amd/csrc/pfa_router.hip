@@ -387,6 +387,17 @@ router_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t n_tok, int C, 
 // ch(s, g, j) = 128*(s/4) + 32g + 8*(s%4) + j.  The sum over channels does
 // not depend on the order, only the two operands must agree.
 constexpr int kRmWaves = 4;
+constexpr int kPrepThreads = 256;  // router_prepare_kernel's workgroup
+// Raw router inputs (bf16) for router_mfma_kernel<..., RAWIN = true>, which
+// builds the pfa_router_prepare outputs itself: the (G, C) gate weights, the
+// (G, C) prototypes (null without them), the confidence and usage (G) (null
+// when unused).
+struct RouterRaw {
+  const uint16_t* w;
+  const uint16_t* p;
+  const uint16_t* conf;
+  const uint16_t* usage;
+};
 constexpr int kRmEpW = 33;  // staged floats per token: GP logits, GP prototype dot parts, sum of squares
 
 __host__ __device__ constexpr int rm_tables(int GP, bool proto) { return proto ? GP / 4 : 1; }
@@ -510,7 +521,7 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
   }
 }
 
-template <int GP, bool PROTO>
+template <int GP, bool PROTO, bool RAWIN>
 __global__ void __launch_bounds__(64 * kRmWaves)
 router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, const float* __restrict__ wpk,
                    const float* __restrict__ conf_weight, const float* __restrict__ usage_bias,
@@ -518,7 +529,7 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
                    float proto_threshold, float proto_blend, float usage_boost, float* __restrict__ gate_probs,
                    float* __restrict__ sim_out, float* __restrict__ blend_out, float* __restrict__ importance,
                    int32_t* __restrict__ head_idx, float* __restrict__ head_score, float* __restrict__ stats,
-                   float* __restrict__ ema_part) {
+                   float* __restrict__ ema_part, RouterRaw raw) {
   PFA_CRITICAL_CHAIN_PRIORITY();
   static_assert(GP == 8 || GP == 16, "MFMA router tables hold 8 or 16 gates");
   constexpr int NT = rm_tables(GP, PROTO);
@@ -528,18 +539,79 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
   uint16_t* tab = reinterpret_cast<uint16_t*>(rm_lds);  // [C/32][NT][64 lanes][8]
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int c16 = lane & 15, g4 = lane >> 4;
+  // RAWIN: the router inputs of pfa_router_prepare built here from the bf16
+  // weights, prototypes, confidence and usage (router_prepare_kernel's
+  // arithmetic, thread-to-channel map and reduction order: the same bits)
+  __shared__ float r_wsum[kRmWaves][RAWIN ? GP : 1];
+  __shared__ float r_den[RAWIN ? GP : 1];
+  __shared__ float r_cw[RAWIN ? GP : 1];
+  __shared__ float r_ub[RAWIN ? GP : 1];
+  if constexpr (RAWIN) {
+    static_assert(64 * kRmWaves == kPrepThreads, "router_prepare_kernel's thread map");
+    if (wid == kRmWaves - 1) {
+      const bool has = lane < G;
+      if (raw.conf != nullptr) {
+        const float v = has ? round_to<PFA_BF16>(bf16_to_f32(raw.conf[lane]) + 1e-6f) : 1.f;
+        if (lane < GP) r_cw[lane] = v;
+      }
+      if (raw.usage != nullptr) {
+        const float v = has ? -round_to<PFA_BF16>(bf16_to_f32(raw.usage[lane]) + 1e-6f) : -INFINITY;
+        float m = v;
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float e = has ? expf(v - m) : 0.f;
+        float sum = e;
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        if (lane < GP) r_ub[lane] = has ? round_to<PFA_BF16>(e / sum) : 0.f;
+      }
+    }
+    if constexpr (PROTO) {
+      float acc[GP];
+#pragma unroll
+      for (int g = 0; g < GP; ++g) acc[g] = 0.f;
+      for (int ch = tid; ch < C; ch += 64 * kRmWaves) {
+        // unconditional loads (padding gates re-read gate G-1 and are masked)
+        float v[GP];
+#pragma unroll
+        for (int g = 0; g < GP; ++g) v[g] = bf16_to_f32(raw.p[(int64_t)(g < G ? g : G - 1) * C + ch]);
+#pragma unroll
+        for (int g = 0; g < GP; ++g) acc[g] = g < G ? __builtin_fmaf(v[g], v[g], acc[g]) : 0.f;
+      }
+#pragma unroll
+      for (int g = 0; g < GP; ++g) {
+        float a = acc[g];
+        for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+        if (lane == 0) r_wsum[wid][g] = a;
+      }
+      __syncthreads();
+      if (tid < GP) {
+        float t = 0.f;
+        for (int k = 0; k < kRmWaves; ++k) t += r_wsum[k][tid];
+        r_den[tid] = fmaxf(sqrtf(t), 1e-6f);
+      }
+    }
+    __syncthreads();
+  }
 
   // operand tables from the packed f32 rows (wpk[c][0..GP) = W, wpk[c][GP..2GP) = P)
   for (int ch = tid; ch < C; ch += 64 * kRmWaves) {
-    const float4* src = reinterpret_cast<const float4*>(wpk + (int64_t)ch * 2 * GP);
     float wv[GP], pv[GP];
+    if constexpr (RAWIN) {
 #pragma unroll
-    for (int k = 0; k < GP / 4; ++k) {
-      const float4 w4 = src[k];
-      wv[4 * k] = w4.x; wv[4 * k + 1] = w4.y; wv[4 * k + 2] = w4.z; wv[4 * k + 3] = w4.w;
-      if constexpr (PROTO) {
-        const float4 p4 = src[GP / 4 + k];
-        pv[4 * k] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
+      for (int g = 0; g < GP; ++g) {
+        const int64_t gi = (int64_t)(g < G ? g : G - 1) * C + ch;
+        wv[g] = g < G ? bf16_to_f32(raw.w[gi]) : 0.f;  // bf16 weights: already rounded to the x dtype
+        if constexpr (PROTO) pv[g] = g < G ? bf16_to_f32(raw.p[gi]) / r_den[g] : 0.f;
+      }
+    } else {
+      const float4* src = reinterpret_cast<const float4*>(wpk + (int64_t)ch * 2 * GP);
+#pragma unroll
+      for (int k = 0; k < GP / 4; ++k) {
+        const float4 w4 = src[k];
+        wv[4 * k] = w4.x; wv[4 * k + 1] = w4.y; wv[4 * k + 2] = w4.z; wv[4 * k + 3] = w4.w;
+        if constexpr (PROTO) {
+          const float4 p4 = src[GP / 4 + k];
+          pv[4 * k] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
+        }
       }
     }
     const int st = 4 * (ch >> 7) + ((ch >> 3) & 3), g = (ch >> 5) & 3, j = ch & 7;
@@ -664,7 +736,13 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
   const int64_t tok = tok0 + lane;
   const bool live = tok < n_tok;
   float gate[GP];
-  router_epilogue<PFA_BF16, GP, PROTO>(acc_t, tok, live, group, G, conf_weight, usage_bias, gate_to_head, H, topk,
+  const float* cw_in = conf_weight;
+  const float* ub_in = usage_bias;
+  if constexpr (RAWIN) {
+    cw_in = raw.conf != nullptr ? r_cw : nullptr;
+    ub_in = raw.usage != nullptr ? r_ub : nullptr;
+  }
+  router_epilogue<PFA_BF16, GP, PROTO>(acc_t, tok, live, group, G, cw_in, ub_in, gate_to_head, H, topk,
                                        proto_temp, proto_threshold, proto_blend, usage_boost, gate_probs, sim_out,
                                        blend_out, importance, head_idx, head_score,
                                        group < n_groups ? stats : nullptr, gate);
@@ -870,8 +948,6 @@ static int gate_pad(int G) { return G <= 8 ? 8 : G <= 16 ? 16 : G <= 32 ? 32 : 6
 // confidence weights (confidence + 1e-6, rounded to the buffer dtype as the
 // reference's tensor add) and the usage bias softmax(-(usage + 1e-6)) in the
 // buffer dtype (aspa.py:636-663).
-constexpr int kPrepThreads = 256;
-
 template <int WDT, int PDT, int XDT, int GP>
 __global__ void __launch_bounds__(kPrepThreads)
 router_prepare_kernel(const typename Elem<WDT>::T* __restrict__ w, const typename Elem<PDT>::T* __restrict__ protos,
@@ -960,9 +1036,9 @@ static void launch_router_gp(const void* x, int64_t n_tok, int C, int G, const f
     if (C % 128 == 0 && C <= (GP == 8 ? 768 : 512)) {
       const unsigned mb = (blocks + kRmWaves - 1) / kRmWaves;
       const size_t lds = (size_t)rm_lds_bytes(C, GP, PROTO);
-      router_mfma_kernel<GP, PROTO><<<mb, 64 * kRmWaves, lds, s>>>((const uint16_t*)x, n_tok, C, G, wpk, cw, ub, g2h,
-                                                                   H, topk, temp, thr, pb, boost, gp, sim, bl, imp,
-                                                                   hi, hs, stats, ema);
+      router_mfma_kernel<GP, PROTO, false><<<mb, 64 * kRmWaves, lds, s>>>(
+          (const uint16_t*)x, n_tok, C, G, wpk, cw, ub, g2h, H, topk, temp, thr, pb, boost, gp, sim, bl, imp, hi, hs,
+          stats, ema, RouterRaw{nullptr, nullptr, nullptr, nullptr});
       return;
     }
   }
@@ -1123,6 +1199,58 @@ extern "C" int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C,
       set_error("pfa_router_topk: unsupported dtype %d", x_dtype);
       return PFA_E_UNSUPPORTED;
   }
+}
+
+// The MFMA router with its inputs built in each workgroup: bf16 x, weights
+// and prototype buffers, at most 16 gates, C a multiple of 128 up to 768
+// (8 gates) or 512 (16 gates).
+static bool router_raw_ok(int x_dtype, int w_dtype, int buf_dtype, int G, int C, bool proto) {
+  if (x_dtype != PFA_BF16 || w_dtype != PFA_BF16 || (proto && buf_dtype != PFA_BF16)) return false;
+  if (G < 1 || G > 16 || C <= 0 || C % 128 != 0) return false;
+  return C <= (gate_pad(G) == 8 ? 768 : 512);
+}
+
+extern "C" int pfa_router_raw_supported(int x_dtype, int w_dtype, int buf_dtype, int G, int C, int use_proto) {
+  return router_raw_ok(x_dtype, w_dtype, buf_dtype, G, C, use_proto != 0) ? 1 : 0;
+}
+
+extern "C" int pfa_router_topk_raw(const void* x, int x_dtype, int64_t n_tok, int C, int G, const void* w_router,
+                                   int w_dtype, const void* protos, const void* confidence, const void* usage,
+                                   int buf_dtype, const int32_t* gate_to_head, int H, int topk, float proto_temp,
+                                   float proto_threshold, float proto_blend, float usage_boost, float* gate_probs,
+                                   float* sim, float* blend, float* importance, int32_t* head_idx, float* head_score,
+                                   float* stats_partial, float* ema_partial, void* stream) {
+  clear_error();
+  PFA_CHECK_ARG(n_tok >= 0 && C > 0 && G > 0 && G <= 64 && H > 0 && H <= G && topk >= 1 && topk <= H,
+                "pfa_router_topk_raw: bad sizes n_tok=%lld C=%d G=%d H=%d topk=%d", (long long)n_tok, C, G, H, topk);
+  PFA_CHECK_ARG(x && w_router && gate_to_head && importance && head_idx, "pfa_router_topk_raw: null pointer");
+  const bool pr = protos != nullptr;
+  if (!router_raw_ok(x_dtype, w_dtype, buf_dtype, G, C, pr)) {
+    set_error("pfa_router_topk_raw: unsupported (x dtype %d, weight dtype %d, buffer dtype %d, G=%d, C=%d)", x_dtype,
+              w_dtype, buf_dtype, G, C);
+    return PFA_E_UNSUPPORTED;
+  }
+  if (n_tok == 0) return PFA_OK;
+  hipStream_t s = as_stream(stream);
+  const RouterRaw raw{(const uint16_t*)w_router, (const uint16_t*)protos, pr ? (const uint16_t*)confidence : nullptr,
+                      pr ? (const uint16_t*)usage : nullptr};
+  const unsigned blocks = (unsigned)((n_tok + kRouterTok - 1) / kRouterTok);
+  const unsigned mb = (blocks + kRmWaves - 1) / kRmWaves;
+#define PFA_RR(GPV, PV)                                                                                          \
+  router_mfma_kernel<GPV, PV, true><<<mb, 64 * kRmWaves, (size_t)rm_lds_bytes(C, GPV, PV), s>>>(                  \
+      (const uint16_t*)x, n_tok, C, G, nullptr, nullptr, nullptr, gate_to_head, H, topk, proto_temp,              \
+      proto_threshold, proto_blend, usage_boost, gate_probs, sim, blend, importance, head_idx, head_score,        \
+      stats_partial, ema_partial, raw)
+  if (gate_pad(G) == 8) {
+    if (pr) PFA_RR(8, true);
+    else PFA_RR(8, false);
+  } else {
+    if (pr) PFA_RR(16, true);
+    else PFA_RR(16, false);
+  }
+#undef PFA_RR
+  PFA_CHECK_LAUNCH("pfa_router_topk_raw");
+  return PFA_OK;
 }
 
 extern "C" int pfa_router_stats_reduce(const float* stats_partial, int n_blocks, double* out, void* stream) {

@@ -777,12 +777,9 @@ class AdaptiveSparseAttention(nn.Module):
     # ------------------------------------------------------------------
     # device stages
     # ------------------------------------------------------------------
-    def _router_inputs(self, device: torch.device, x_dtype: torch.dtype):
-        """Router weight table, prototype prior inputs (aspa.py:636-663) in one
-        launch (pfa_router_prepare): (w_packed, conf_weight, usage_bias,
-        use_proto)."""
-        lib = _hip.lib()
-        G, C = self.attn_gates, self.d_model
+    def _router_raw_inputs(self, device: torch.device):
+        """The router's weight and prototype-prior buffers as they are:
+        (w, protos, confidence, usage, buf_dtype, use_proto)."""
         w = self.head_router.linear.weight.detach()
         if w.device != device:
             w = w.to(device)
@@ -800,6 +797,15 @@ class AdaptiveSparseAttention(nn.Module):
             for t in (conf_b, usage_b):
                 if t is not None and t.dtype != buf_dtype:
                     raise ValueError("routing_prototypes / routing_confidence / routing_usage_ema must share one dtype")
+        return w, protos, conf_b, usage_b, buf_dtype, use_proto
+
+    def _router_inputs(self, device: torch.device, x_dtype: torch.dtype):
+        """Router weight table, prototype prior inputs (aspa.py:636-663) in one
+        launch (pfa_router_prepare): (w_packed, conf_weight, usage_bias,
+        use_proto)."""
+        lib = _hip.lib()
+        G, C = self.attn_gates, self.d_model
+        w, protos, conf_b, usage_b, buf_dtype, use_proto = self._router_raw_inputs(device)
         Gp = int(lib.pfa_router_gate_pad(G))
         wpk = torch.empty(C, 2 * Gp, dtype=torch.float32, device=device)
         conf = torch.empty(G, dtype=torch.float32, device=device) if conf_b is not None else None
@@ -829,7 +835,17 @@ class AdaptiveSparseAttention(nn.Module):
         device = x2d.device
         n_tok, C = x2d.shape
         G, H = self.attn_gates, self.h_total
-        wpk, conf, usage, use_proto = self._router_inputs(device, x2d.dtype)
+        # bf16 shapes of the MFMA router build their inputs inside the router
+        # (pfa_router_topk_raw); the others take pfa_router_prepare first
+        w, protos, conf_b, usage_b, buf_dtype, use_proto = self._router_raw_inputs(device)
+        raw = bool(lib.pfa_router_raw_supported(_hip.dtype_tag(x2d.dtype), _hip.dtype_tag(w.dtype),
+                                                _hip.dtype_tag(buf_dtype), G, C, 1 if use_proto else 0))
+        if raw:
+            keep = self.__dict__.get("_capture_keep")
+            if keep is not None:
+                keep.extend(t for t in (w, protos, conf_b, usage_b) if t is not None)
+        else:
+            wpk, conf, usage, use_proto = self._router_inputs(device, x2d.dtype)
         gate = torch.empty(n_tok, G, dtype=torch.float32, device=device)
         imp = torch.empty(n_tok, dtype=torch.float32, device=device)
         sim = torch.empty(n_tok, dtype=torch.float32, device=device) if use_proto else None
@@ -847,14 +863,22 @@ class AdaptiveSparseAttention(nn.Module):
             ema = torch.empty(max(1, nblk.value), G, C + 1, dtype=torch.float32, device=device)
         self._ema_partial = (ema, x2d.data_ptr(), n_tok) if ema is not None else None
         g2h = self._gate_to_head_i32(device)
+        tail = (_hip.ptr(g2h), H, topk, float(self.proto_temp), float(self.proto_threshold),
+                float(self.proto_blend), float(self.proto_usage_boost), _hip.ptr(gate), _hip.ptr(sim),
+                _hip.ptr(blend), _hip.ptr(imp), _hip.ptr(hidx), _hip.ptr(hsc), _hip.ptr(stats), _hip.ptr(ema),
+                _hip.stream_ptr(device))
         with _hip.TIMER.timed("router_topk"):
-            rc = lib.pfa_router_topk(
-            _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(wpk), 1 if use_proto else 0,
-            _hip.ptr(conf),
-            _hip.ptr(usage), _hip.ptr(g2h), H, topk, float(self.proto_temp), float(self.proto_threshold),
-            float(self.proto_blend), float(self.proto_usage_boost), _hip.ptr(gate), _hip.ptr(sim), _hip.ptr(blend),
-            _hip.ptr(imp), _hip.ptr(hidx), _hip.ptr(hsc), _hip.ptr(stats), _hip.ptr(ema), _hip.stream_ptr(device))
-        _hip.check(rc, "pfa_router_topk")
+            if raw:
+                name = "pfa_router_topk_raw"
+                rc = lib.pfa_router_topk_raw(
+                    _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(w), _hip.dtype_tag(w.dtype),
+                    _hip.ptr(protos), _hip.ptr(conf_b), _hip.ptr(usage_b), _hip.dtype_tag(buf_dtype), *tail)
+            else:
+                name = "pfa_router_topk"
+                rc = lib.pfa_router_topk(
+                    _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(wpk), 1 if use_proto else 0,
+                    _hip.ptr(conf), _hip.ptr(usage), *tail)
+        _hip.check(rc, name)
         self._router_stats = stats
         return gate, sim, blend, imp, hidx, hsc
 

@@ -339,6 +339,62 @@ def _run_router(dev, x, w, protos, conf, dt, topk, H, temp=0.2, thr=0.25, blend=
     return [o.cpu() for o in outs]
 
 
+@pytest.mark.parametrize("G,H,C,n,proto,usage,ema", [(8, 8, 512, 4096, True, True, True),
+                                                     (8, 8, 768, 3000, True, False, False),
+                                                     (16, 16, 512, 2500, True, True, True),
+                                                     (5, 4, 384, 777, True, True, False),
+                                                     (12, 8, 256, 1030, False, False, False)])
+def test_router_raw_inputs_bitwise(dev, G, H, C, n, proto, usage, ema):
+    """pfa_router_topk_raw (router inputs built inside the router's
+    workgroups) gives exactly the bits of pfa_router_prepare +
+    pfa_router_topk: gates, similarity, blend, importance, head indices and
+    scores, telemetry partials and the fused EMA partial sums."""
+    from proteus_attention import _hip
+
+    lib = _hip.lib()
+    bf = torch.bfloat16
+    g = torch.Generator().manual_seed(61 + G + C)
+    x = (torch.randn(n, C, generator=g) * (1.0 + 3.0 * (torch.rand(n, 1, generator=g) < 0.01))).to(bf).to(dev)
+    w = (torch.randn(G, C, generator=g) * 0.05).to(bf).to(dev)
+    protos = (torch.randn(G, C, generator=g) * 0.02).to(bf).to(dev) if proto else None
+    conf = (torch.rand(G, generator=g) * 3).to(bf).to(dev) if proto else None
+    use = (torch.rand(G, generator=g) * 5).to(bf).to(dev) if (proto and usage) else None
+    g2h = O.default_gate_map(G, H).to(torch.int32).to(dev)
+    topk = 2
+    assert lib.pfa_router_raw_supported(_hip.PFA_BF16, _hip.PFA_BF16, _hip.PFA_BF16, G, C, int(proto)) == 1
+    nblk = _hip.ctypes.c_int(0)
+    _hip.check(lib.pfa_router_block_count(n, _hip.ctypes.byref(nblk)), "block_count")
+    nb = max(1, nblk.value)
+
+    def outs():
+        return [torch.empty(n, G, device=dev), torch.empty(n, device=dev), torch.empty(n, device=dev),
+                torch.empty(n, device=dev), torch.empty(n, topk, device=dev, dtype=torch.int32),
+                torch.empty(n, topk, device=dev), torch.empty(nb, 8, device=dev),
+                torch.empty(nb, G, C + 1, device=dev) if ema else None]
+
+    Gp = int(lib.pfa_router_gate_pad(G))
+    wpk = torch.empty(C, 2 * Gp, device=dev)
+    cw = torch.empty(G, device=dev) if conf is not None else None
+    ub = torch.empty(G, device=dev) if use is not None else None
+    _hip.check(lib.pfa_router_prepare(_hip.ptr(w), _hip.PFA_BF16, _hip.ptr(protos), _hip.ptr(conf), _hip.ptr(use),
+                                      _hip.PFA_BF16, G, C, _hip.PFA_BF16, _hip.ptr(wpk), _hip.ptr(cw), _hip.ptr(ub),
+                                      _hip.stream_ptr(dev)), "prepare")
+    a, b = outs(), outs()
+    args = (H, topk, 0.3, 0.2, 0.5, 0.25)
+    _hip.check(lib.pfa_router_topk(_hip.ptr(x), _hip.PFA_BF16, n, C, G, _hip.ptr(wpk), int(proto), _hip.ptr(cw),
+                                   _hip.ptr(ub), _hip.ptr(g2h), *args, *[_hip.ptr(o) for o in a],
+                                   _hip.stream_ptr(dev)), "router")
+    _hip.check(lib.pfa_router_topk_raw(_hip.ptr(x), _hip.PFA_BF16, n, C, G, _hip.ptr(w), _hip.PFA_BF16,
+                                       _hip.ptr(protos), _hip.ptr(conf), _hip.ptr(use), _hip.PFA_BF16, _hip.ptr(g2h),
+                                       *args, *[_hip.ptr(o) for o in b], _hip.stream_ptr(dev)), "router_raw")
+    for i, (u, v) in enumerate(zip(a, b)):
+        if u is None or (i in (1, 2) and not proto):
+            continue
+        if i == 6:  # telemetry partials: columns 0..4 of each row are written
+            u, v = u[:, :5], v[:, :5]
+        assert torch.equal(u.cpu().contiguous().view(torch.int32), v.cpu().contiguous().view(torch.int32)), i
+
+
 @pytest.mark.parametrize("name,B,T,C,dt,outlier", [
     ("module_cfg1", 1, 1024, 256, torch.float32, 0.0),
     ("module_cfg2_T2048", 2, 2048, 512, torch.bfloat16, 0.0),
