@@ -5,13 +5,13 @@
 // one symmetric scale per (head, key row).
 //
 // Every key is read by every 128-query tile of its head (8,192 tiles at
-// T = 2^20), so the shortlist is dequantised once per call, into bf16
-// working copies in the workspace; the attention then streams 64-key tiles
-// of them by LDS DMA into the swizzled 128-byte-row layout of the bf16
-// attention kernels (the V^T operand from the LDS transpose read), and
-// S = Q K^T and O += P V run on v_mfma_f32_16x16x32_bf16 with an online
-// softmax in f32 registers.  (Dequantising inside every tile spent about 2 ms
-// of VALU time at config 5.)
+// T = 2^20), so the shortlist is converted once per call into bf16 working
+// copies in the workspace; the attention then streams 64-key tiles of them
+// by LDS DMA into the swizzled 128-byte-row layout of the bf16 attention
+// kernels (the V^T operand from the LDS transpose read), and S = Q K^T and
+// O += P V run on v_mfma_f32_16x16x32_bf16 with an online softmax in f32
+// registers.  (Dequantising inside every tile spent about 2 ms of VALU time
+// at config 5.)
 //
 // Workgroup: 4 waves, 128 consecutive query tokens of one head (32 per wave
 // in two 16-query MFMA column groups).  The shortlist is sorted by
@@ -21,16 +21,21 @@
 // (query, key).  Block b handles head b % H, so on 8 XCDs each XCD's L2
 // holds one head's K/V; tiles run heaviest first.
 //
-// Precision.  Scores are in log2 units: K carries the factor
-// c = k_scale * scale * log2(e).  A single bf16 copy of k8 * c would round
-// every key element to 8 bits, and with large scores (rows of 4x the
-// typical norm, whose single keys dominate their queries) that moves a
-// score by tenths and the output by more than the bf16 tolerance.  So K is
-// held as two bf16 parts, hi = bf16(k8 * c) and lo = bf16(k8 * c - hi)
-// (their sum is k8 * c to about 2^-17), and every QK^T product is the sum of
-// two MFMA products; V likewise (hi/lo of v8 * v_scale).  The softmax takes
-// the exact row maximum (the dominant key's P is exactly 1), so what
-// remains is the bf16 rounding of P for the P.V product.
+// Precision.  The working copies hold the int8 values themselves, which
+// bf16 represents exactly; the per-key scales stay in f32 and travel with
+// each tile (512 bytes beside its 16 KB of K and V).  Scores are in log2
+// units: the MFMA gives q . k8 (exact products, f32 sums) and each is
+// multiplied by c_j = k_scale[j] * scale * log2(e).  So a score is as
+// accurate as an f32 dot product, with no rounding of the scaled K (a bf16
+// copy of k8 * c moved the scores of rows with 4x the typical norm by
+// tenths).  The softmax takes the exact row maximum (a dominant key's P is
+// exactly 1) and the row sum l sums the unrounded P in f32.  The P.V
+// product takes the weights w_j = P_j * v_scale[j] against the exact v8:
+// on a tile where some weight exceeds 1/8 of its row's running sum, as two
+// bf16 parts (hi + lo, w to ~2^-17), else rounded once to bf16, whose
+// independent errors of <= 2^-9 relative on weights that are each a small
+// share of the row largely cancel.  QK^T and P.V are 32 MFMAs per 64-key
+// tile and wave, 48 on the tiles that take the lo parts.
 #include "pfa_common.h"
 
 namespace pfa {
@@ -42,24 +47,35 @@ constexpr int kQ = 32 * kWaves;  // queries per workgroup
 constexpr int kTile = kSwzKeys;  // keys per tile
 constexpr int kD = 64;
 constexpr float kRescaleLog2 = 0.0f;  // rescale when some row's max rises
+#ifndef PFA_FIN_LO_FRAC
+#define PFA_FIN_LO_FRAC 0.125f
+#endif
+// a tile's P.V weights take their lo parts when one of them exceeds this
+// fraction of its lane's running row sum
+constexpr float kLoFrac = PFA_FIN_LO_FRAC;
 
 #ifndef PFA_FIN_STAGES
 #define PFA_FIN_STAGES 2
 #endif
 constexpr int kStages = PFA_FIN_STAGES;  // LDS ring of K/V tiles
+// a stage: K tile, V tile (64 rows of 128 bytes each), then the tile's 64
+// K scales and 64 V scales (f32)
+constexpr int kScaleOff = 2 * kSwzTileElems;           // uint16 elements into a stage
+constexpr int kStageElems = kScaleOff + 2 * kTile * 2;  // + 512 bytes
+constexpr int kDmaPerStage = kDmaPerTile + 1;           // per wave: four tile rows and one scale chunk
 
 struct Args {
   const uint16_t* q;
   int64_t q_sh, q_st;
   uint16_t* out;
   int64_t o_sh, o_st;
-  const uint16_t* kb;  // dequantised shortlist, bf16 (H, S, 64): hi parts
+  const uint16_t* kb;  // shortlist K and V as bf16 integers (H, S, 64)
   const uint16_t* vb;
-  const uint16_t* kl;  // lo parts
-  const uint16_t* vl;
+  const float* ksc;  // (H, Sp): k_scale * scale * log2(e), zero past S
+  const float* vsc;  // (H, Sp): v_scale, zero past S
   const int32_t* kpos;
   const int2* rng;
-  int H, S, causal, nqt;
+  int H, S, Sp, causal, nqt;
   int64_t T;
 };
 
@@ -70,116 +86,130 @@ struct St {
 
 __device__ __forceinline__ float i8f(uint32_t w, int e) { return (float)(int)(int8_t)((w >> (8 * e)) & 0xffu); }
 
-// hi = bf16(x8 * scale) and lo = bf16(x8 * scale - hi) for the (H*S, 64)
-// rows of K and V: thread -> row idx/4, elements 16*(idx%4) .. +15.  K rows
-// carry the factor kmul = scale * log2(e): x8 * (k_scale * kmul).
+// bf16 copies of the int8 K and V rows (exact) and the padded f32 scale
+// rows: thread -> row idx/4 of (H, Sp), elements 16*(idx%4) .. +15.  K
+// scales carry the factor kmul = scale * log2(e).
 __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__ k8, const int8_t* __restrict__ v8,
                                                       const float* __restrict__ ks, const float* __restrict__ vs,
-                                                      int64_t rows, float kmul, uint16_t* __restrict__ kh,
-                                                      uint16_t* __restrict__ vh, uint16_t* __restrict__ kl,
-                                                      uint16_t* __restrict__ vl) {
-#pragma clang fp contract(off)
+                                                      int S, int Sp, int64_t rows, float kmul,
+                                                      uint16_t* __restrict__ kh, uint16_t* __restrict__ vh,
+                                                      float* __restrict__ kso, float* __restrict__ vso) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= rows * 4) return;
-  const int64_t row = idx >> 2;
+  const int64_t prow = idx >> 2;
   const int qd = (int)(idx & 3);
+  const int h = (int)(prow / Sp), j = (int)(prow - (int64_t)h * Sp);
+  const int64_t row = (int64_t)h * S + j;
+  if (qd == 0) {
+    kso[prow] = j < S ? ks[row] * kmul : 0.f;
+    vso[prow] = j < S ? vs[row] : 0.f;
+  }
+  if (j >= S) return;
   const uint4 k = *reinterpret_cast<const uint4*>(k8 + row * kD + 16 * qd);
   const uint4 v = *reinterpret_cast<const uint4*>(v8 + row * kD + 16 * qd);
-  const float kscale = ks[row] * kmul, vscale = vs[row];
   const uint32_t kw4[4] = {k.x, k.y, k.z, k.w};
   const uint32_t vw4[4] = {v.x, v.y, v.z, v.w};
-  __bf16 kd[16], vd[16], kr[16], vr[16];
+  __bf16 kd[16], vd[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    const float kf = i8f(kw4[e >> 2], e & 3) * kscale;
-    const float vf = i8f(vw4[e >> 2], e & 3) * vscale;
-    kd[e] = (__bf16)kf;
-    vd[e] = (__bf16)vf;
-    kr[e] = (__bf16)(kf - (float)kd[e]);  // exact difference, rounded once
-    vr[e] = (__bf16)(vf - (float)vd[e]);
+    kd[e] = (__bf16)i8f(kw4[e >> 2], e & 3);
+    vd[e] = (__bf16)i8f(vw4[e >> 2], e & 3);
   }
   const int64_t off = row * kD + 16 * qd;
   __builtin_memcpy(kh + off, kd, 32);
   __builtin_memcpy(vh + off, vd, 32);
-  __builtin_memcpy(kl + off, kr, 32);
-  __builtin_memcpy(vl + off, vr, 32);
 }
 
-// O += P V for the tile (P rounded to bf16), V as the sum of its hi part
-// (tile th) and lo part (tile tl).
-__device__ __forceinline__ void pv_accumulate(const float (&s)[2][16], const SwzTile& th, const SwzTile& tl,
+// O += (P * v_scale) V8 for the tile, the weight w = P * v_scale in bf16.
+// LO: w enters as two bf16 parts, hi = bf16(w) and lo = bf16(w - hi)
+// (their sum is w to about 2^-17), so a key that dominates its row adds
+// v8 * v_scale at f32 accuracy.  Without LO the weights are rounded once
+// (relative error <= 2^-9 each); the caller takes that path only on tiles
+// where every weight is a small fraction of its row's sum, whose rounding
+// errors are independent and largely cancel.
+template <bool LO>
+__device__ __forceinline__ void pv_accumulate(const float (&s)[2][16], const float (&vsj)[16], const SwzTile& t,
                                               St (&st)[2]) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
-    bf16x8_t pb[2];
+    bf16x8_t ph[2], pl[2];
 #pragma unroll
     for (int gr = 0; gr < 2; ++gr) {
-      __bf16 pv[8];
+      __bf16 hv[8], lv[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pv[i] = (__bf16)s[gr][8 * kc + i];
-        pv[4 + i] = (__bf16)s[gr][8 * kc + 4 + i];
+      for (int i = 0; i < 8; ++i) {
+        const float w = s[gr][8 * kc + i] * vsj[8 * kc + i];
+        hv[i] = (__bf16)w;
+        if constexpr (LO) lv[i] = (__bf16)(w - (float)hv[i]);  // exact difference, rounded once
       }
-      __builtin_memcpy(&pb[gr], pv, 16);
+      __builtin_memcpy(&ph[gr], hv, 16);
+      if constexpr (LO) __builtin_memcpy(&pl[gr], lv, 16);
     }
 #pragma unroll
-    for (int part = 0; part < 2; ++part) {
-      const SwzTile& t = part ? tl : th;
+    for (int db = 0; db < 4; ++db) {
+      // V^T: lane (dim 16db + lane%16, g) holds keys 32kc + 4g + (0..3) and
+      // 32kc + 16 + 4g + (0..3), matching the weights
+      const i16x4_t lo = ds_tr4(t.vtr(kc, 0, db));
+      const i16x4_t hi = ds_tr4(t.vtr(kc, 1, db));
+      bf16x8_t va;
+      __builtin_memcpy(&va, &lo, 8);
+      __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        // V^T: lane (dim 16db + lane%16, g) holds keys 32kc + 4g + (0..3) and
-        // 32kc + 16 + 4g + (0..3), matching pb
-        const i16x4_t lo = ds_tr4(t.vtr(kc, 0, db));
-        const i16x4_t hi = ds_tr4(t.vtr(kc, 1, db));
-        bf16x8_t va;
-        __builtin_memcpy(&va, &lo, 8);
-        __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
-#pragma unroll
-        for (int gr = 0; gr < 2; ++gr)
-          st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[gr], st[gr].acc[db], 0, 0, 0);
+      for (int gr = 0; gr < 2; ++gr) {
+        if constexpr (LO) st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[gr], st[gr].acc[db], 0, 0, 0);
+        st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[gr], st[gr].acc[db], 0, 0, 0);
       }
     }
   }
 }
 
-// One 64-key tile: scores from the hi and lo parts of K, the tile's row
+// One 64-key tile: scores q . k8 times the keys' scales, the tile's row
 // maxima (rescaling when one rises), P, and the P.V products.  MASKED:
 // keys past S or (causal) after the query's position are dropped; kpos is
-// the shortlist's positions (global; read only in masked tiles).
+// the shortlist's positions (global; read only in masked tiles).  sc: the
+// tile's K scales (64 floats) followed by its V scales.
 template <bool MASKED>
-__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& th, const SwzTile& tl,
+__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& t, const float* sc,
                                      const int32_t* kpos, int key0, int S, int causal, const int (&tq)[2],
                                      St (&st)[2]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
+  // the lane's keys 16kb + 4g + i: scores s[.][4kb + i]
+  float ksj[16], vsj[16];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const float4 a = *reinterpret_cast<const float4*>(sc + 16 * kb + 4 * g);
+    const float4 b = *reinterpret_cast<const float4*>(sc + kTile + 16 * kb + 4 * g);
+    ksj[4 * kb] = a.x, ksj[4 * kb + 1] = a.y, ksj[4 * kb + 2] = a.z, ksj[4 * kb + 3] = a.w;
+    vsj[4 * kb] = b.x, vsj[4 * kb + 1] = b.y, vsj[4 * kb + 2] = b.z, vsj[4 * kb + 3] = b.w;
+  }
   float s[2][16];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(th.kfrag(kb, 0));
-    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(th.kfrag(kb, 1));
-    const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 0));
-    const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(tl.kfrag(kb, 1));
+    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, 0));
+    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, 1));
 #pragma unroll
     for (int gr = 0; gr < 2; ++gr) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b0, qf[gr][0], c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b1, qf[gr][1], c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[gr][0], c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[gr][1], c, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        const float v = c[i] * ksj[4 * kb + i];
         if constexpr (MASKED) {
           const int key = key0 + 16 * kb + 4 * g + i;
           const int pos = kpos[key < S ? key : S - 1];
           const bool ok = key < S && (!causal || pos <= tq[gr]);
-          s[gr][4 * kb + i] = ok ? c[i] : -INFINITY;
+          s[gr][4 * kb + i] = ok ? v : -INFINITY;
         } else {
-          s[gr][4 * kb + i] = c[i];
+          s[gr][4 * kb + i] = v;
         }
       }
     }
   }
   // lazy rescaling: the accumulators are rescaled only on tiles where some
   // row of the wave sees a new maximum; m stays the exact running max
+  bool lo_needed = false;
 #pragma unroll
   for (int gr = 0; gr < 2; ++gr) {
     float tmax = s[gr][0];
@@ -197,15 +227,22 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& 
       st[gr].m = mn;
     }
     const float moff = st[gr].m == -INFINITY ? 0.f : st[gr].m;
-    float psum = 0.f;
+    float psum = 0.f, pmax = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       s[gr][i] = __builtin_amdgcn_exp2f(s[gr][i] - moff);  // -inf -> 0
       psum += s[gr][i];
+      pmax = fmaxf(pmax, s[gr][i]);
     }
+    // the lane's partial sum so far is at most its row's sum, so a weight
+    // below kLoFrac of it is below kLoFrac of the row's final sum
+    lo_needed |= pmax > kLoFrac * st[gr].l;
     st[gr].l += psum;
   }
-  pv_accumulate(s, th, tl, st);
+  if (__ballot(lo_needed) != 0)
+    pv_accumulate<true>(s, vsj, t, st);
+  else
+    pv_accumulate<false>(s, vsj, t, st);
 }
 
 __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restrict__ kpos, int S, int64_t T,
@@ -234,12 +271,13 @@ __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restri
   rng[qt] = make_int2(below, lo);
 }
 
-// two 4-wave workgroups per CU: each holds two 32 KB stages of hi and lo
-// K/V tiles (64 KB of LDS), so two fit a CU
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
+#ifndef PFA_FIN_WAVES_PER_EU
+#define PFA_FIN_WAVES_PER_EU 2
+#endif
+// a workgroup's ring is kStages x 16.5 KB of LDS
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PFA_FIN_WAVES_PER_EU, 8)))
 final_attn_kernel(Args a) {
-  // a stage: K hi, V hi, K lo, V lo (64 rows of 128 bytes each)
-  __shared__ __align__(16) uint16_t ring[kStages][4 * kSwzTileElems];
+  __shared__ __align__(16) uint16_t ring[kStages][kStageElems];
 
   const int bid = blockIdx.x;
   const int h = bid % a.H;
@@ -259,21 +297,27 @@ final_attn_kernel(Args a) {
     tq[gr] = (int)(qv[gr] ? t : a.T - 1);
   }
   // per-head bases, wave-uniform (scalar registers for the DMA)
-  const int64_t hoff = (int64_t)__builtin_amdgcn_readfirstlane(h) * a.S * kD;
+  const int hu = __builtin_amdgcn_readfirstlane(h);
+  const int64_t hoff = (int64_t)hu * a.S * kD;
   const uint16_t* kbh = a.kb + hoff;
   const uint16_t* vbh = a.vb + hoff;
-  const uint16_t* klh = a.kl + hoff;
-  const uint16_t* vlh = a.vl + hoff;
+  // this wave's scale chunk: waves 0, 1 move K scales 0..31, 32..63 of the
+  // tile, waves 2, 3 the V scales (lanes 0..7, 16 bytes each)
+  const int wu = __builtin_amdgcn_readfirstlane(wid);
+  const float* sch = (wu < 2 ? a.ksc : a.vsc) + (int64_t)hu * a.Sp + 32 * (wu & 1);
   const int ntile = (rg.y + kTile - 1) / kTile;
   const int drow = tid >> 3;  // this thread's DMA rows: drow and drow + 32
-  const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + 1024u * (uint32_t)wid);
-  constexpr uint32_t kStageBytes = 4 * kSwzTileElems * 2;
+  const uint32_t ring0 = lds_addr(&ring[0][0]);
+  const uint32_t ring_w = __builtin_amdgcn_readfirstlane(ring0 + 1024u * (uint32_t)wid);
+  const uint32_t scl_w = __builtin_amdgcn_readfirstlane(ring0 + 2u * kScaleOff + 128u * (uint32_t)wid);
+  constexpr uint32_t kStageBytes = kStageElems * 2;
   auto request = [&](int i) {
     const int k0 = kTile * i;
     const int ka = min(k0 + drow, a.S - 1), kz = min(k0 + drow + 32, a.S - 1);
-    const uint32_t st0 = ring_w + kStageBytes * (uint32_t)(i % kStages);
-    dma_tile_rows64(kbh, vbh, ka, kz, st0);
-    dma_tile_rows64(klh, vlh, ka, kz, st0 + 4 * kSwzTileElems);
+    const uint32_t so = kStageBytes * (uint32_t)(i % kStages);
+    dma_tile_rows64(kbh, vbh, ka, kz, ring_w + so);
+    // the scale rows are padded to a multiple of 64 keys: always in bounds
+    if (lane < 8) lds_dma16_s(sch, (uint32_t)(k0 + 4 * lane) * 4u, scl_w + so);
   };
 #pragma unroll
   for (int i = 0; i < kStages - 1; ++i)
@@ -302,7 +346,7 @@ final_attn_kernel(Args a) {
   // every wave is done with tile i-1, whose stage takes tile i+kStages-1
   auto next = [&](int i) {
     if (kStages == 3 && i + 1 < ntile)
-      dma_wait_barrier<2 * kDmaPerTile>();
+      dma_wait_barrier<kDmaPerStage>();
     else
       dma_wait_barrier<0>();
     if (i + kStages - 1 < ntile) request(i + kStages - 1);
@@ -312,13 +356,15 @@ final_attn_kernel(Args a) {
   const int nfull = min(rg.x / kTile, ntile);
   for (int i = 0; i < nfull; ++i) {
     next(i);
-    const SwzTile th{ring[i % kStages], L}, tl{ring[i % kStages] + 2 * kSwzTileElems, L};
-    tile<false>(qf, th, tl, a.kpos, kTile * i, a.S, a.causal, tq, st);
+    const uint16_t* stg = ring[i % kStages];
+    const SwzTile t{stg, L};
+    tile<false>(qf, t, reinterpret_cast<const float*>(stg + kScaleOff), a.kpos, kTile * i, a.S, a.causal, tq, st);
   }
   for (int i = nfull; i < ntile; ++i) {
     next(i);
-    const SwzTile th{ring[i % kStages], L}, tl{ring[i % kStages] + 2 * kSwzTileElems, L};
-    tile<true>(qf, th, tl, a.kpos, kTile * i, a.S, a.causal, tq, st);
+    const uint16_t* stg = ring[i % kStages];
+    const SwzTile t{stg, L};
+    tile<true>(qf, t, reinterpret_cast<const float*>(stg + kScaleOff), a.kpos, kTile * i, a.S, a.causal, tq, st);
   }
   uint16_t* oh = a.out + (int64_t)h * a.o_sh;
 #pragma unroll
@@ -345,18 +391,20 @@ final_attn_kernel(Args a) {
 
 using namespace pfa;
 
-// workspace: the query tiles' key ranges, then the bf16 K and V copies
-// (hi parts, then lo parts)
+// workspace: the query tiles' key ranges, the bf16 K and V copies, then the
+// K and V scale rows (H, Sp) with Sp = S rounded up to 64 keys
 static size_t fin_rng_bytes(int64_t T) {
   const int64_t nqt = (T + fin::kQ - 1) / fin::kQ;
   return ((size_t)(nqt > 0 ? nqt : 1) * sizeof(int2) + 255) / 256 * 256;
 }
+static int fin_padded(int S) { return (S + fin::kTile - 1) / fin::kTile * fin::kTile; }
 static size_t fin_copy_bytes(int H, int S) { return ((size_t)H * (size_t)S * fin::kD * 2 + 255) / 256 * 256; }
+static size_t fin_scale_bytes(int H, int S) { return ((size_t)H * (size_t)fin_padded(S) * 4 + 255) / 256 * 256; }
 
 extern "C" int pfa_int8_kv_attn_workspace_size(int64_t T, int H, int S, size_t* bytes) {
   clear_error();
   PFA_CHECK_ARG(bytes && T >= 0 && H >= 0 && S >= 0, "pfa_int8_kv_attn_workspace_size: bad arguments");
-  *bytes = fin_rng_bytes(T) + 4 * fin_copy_bytes(H, S);
+  *bytes = fin_rng_bytes(T) + 2 * fin_copy_bytes(H, S) + 2 * fin_scale_bytes(H, S);
   return PFA_OK;
 }
 
@@ -376,19 +424,20 @@ extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, i
   PFA_CHECK_ARG(S > 0, "pfa_int8_kv_attn_fwd: empty shortlist (S must be >= 1)");
   PFA_CHECK_ARG(k8 && v8 && k_scale && v_scale && key_pos, "pfa_int8_kv_attn_fwd: null shortlist pointer");
   PFA_CHECK_ARG(((uintptr_t)k8 % 16) == 0 && ((uintptr_t)v8 % 16) == 0, "pfa_int8_kv_attn_fwd: k8/v8 must be 16-byte aligned");
-  PFA_CHECK_ARG((int64_t)S * fin::kD < INT32_MAX, "pfa_int8_kv_attn_fwd: S too large (%d)", S);
+  PFA_CHECK_ARG((int64_t)fin_padded(S) * fin::kD < INT32_MAX, "pfa_int8_kv_attn_fwd: S too large (%d)", S);
   size_t need = 0;
   pfa_int8_kv_attn_workspace_size(T, H, S, &need);
   PFA_CHECK_ARG(workspace && ws_bytes >= need, "pfa_int8_kv_attn_fwd: workspace of %zu bytes required", need);
   const int nqt = (int)((T + fin::kQ - 1) / fin::kQ);
+  const int Sp = fin_padded(S);
   int2* rng = (int2*)workspace;
   uint16_t* kbf = (uint16_t*)((char*)workspace + fin_rng_bytes(T));
   uint16_t* vbf = (uint16_t*)((char*)kbf + fin_copy_bytes(H, S));
-  uint16_t* klf = (uint16_t*)((char*)vbf + fin_copy_bytes(H, S));
-  uint16_t* vlf = (uint16_t*)((char*)klf + fin_copy_bytes(H, S));
-  const int64_t rows = (int64_t)H * S;
+  float* ksf = (float*)((char*)vbf + fin_copy_bytes(H, S));
+  float* vsf = (float*)((char*)ksf + fin_scale_bytes(H, S));
+  const int64_t rows = (int64_t)H * Sp;
   fin::dequant_kernel<<<(unsigned)((rows * 4 + 255) / 256), 256, 0, s>>>(
-      k8, v8, k_scale, v_scale, rows, scale * 1.4426950408889634f, kbf, vbf, klf, vlf);
+      k8, v8, k_scale, v_scale, S, Sp, rows, scale * 1.4426950408889634f, kbf, vbf, ksf, vsf);
   PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/dequant");
   fin::key_ranges_kernel<<<(unsigned)((nqt + 255) / 256), 256, 0, s>>>(key_pos, S, T, nqt, causal ? 1 : 0, rng);
   PFA_CHECK_LAUNCH("pfa_int8_kv_attn_fwd/ranges");
@@ -401,12 +450,13 @@ extern "C" int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, i
   a.o_st = out.s_t;
   a.kb = kbf;
   a.vb = vbf;
-  a.kl = klf;
-  a.vl = vlf;
+  a.ksc = ksf;
+  a.vsc = vsf;
   a.kpos = key_pos;
   a.rng = rng;
   a.H = H;
   a.S = S;
+  a.Sp = Sp;
   a.causal = causal ? 1 : 0;
   a.nqt = nqt;
   a.T = T;

@@ -181,10 +181,11 @@ def test_config5_final_pass_with_outlier_rows_vs_oracle(dev):
     """Config 5 on config 3's outlier recipe: 1% of the input rows scaled by
     4, so query-key scores between outlier rows are ~16x those of N(0,1)
     rows and single keys dominate their queries' softmax.  The all-query
-    final pass holds K and V as hi/lo bf16 pairs and takes the exact row
-    maximum, so the dominant-key rows must still meet the bf16 bound (a
-    single bf16 copy of the scaled K moved such scores by tenths and the
-    outputs by ~0.1).  The pipeline runs at full size (T = 2^20);
+    final pass scores against the exact int8 keys with f32 scales, takes
+    the exact row maximum and adds a dominant key's weight unrounded, so
+    the dominant-key rows must still meet the bf16 bound (a single bf16
+    copy of the scaled K moved such scores by tenths and the outputs by
+    ~0.1).  The pipeline runs at full size (T = 2^20);
     the sampled queries are every 1024th token plus the first 1,024 outlier
     tokens."""
     from configs import make_inputs
