@@ -43,7 +43,11 @@ namespace fin {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kQ = 32 * kWaves;  // queries per workgroup
+#ifndef PFA_FIN_NG
+#define PFA_FIN_NG 2
+#endif
+constexpr int kNG = PFA_FIN_NG;        // 16-query MFMA column groups per wave
+constexpr int kQ = 16 * kNG * kWaves;  // queries per workgroup
 constexpr int kTile = kSwzKeys;  // keys per tile
 constexpr int kD = 64;
 constexpr float kRescaleLog2 = 0.0f;  // rescale when some row's max rises
@@ -120,82 +124,108 @@ __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__
   __builtin_memcpy(vh + off, vd, 32);
 }
 
-// O += (P * v_scale) V8 for the tile, the weight w = P * v_scale in bf16.
-// LO: w enters as two bf16 parts, hi = bf16(w) and lo = bf16(w - hi)
-// (their sum is w to about 2^-17), so a key that dominates its row adds
-// v8 * v_scale at f32 accuracy.  Without LO the weights are rounded once
-// (relative error <= 2^-9 each); the caller takes that path only on tiles
-// where every weight is a small fraction of its row's sum, whose rounding
-// errors are independent and largely cancel.
-template <bool LO>
-__device__ __forceinline__ void pv_accumulate(const float (&s)[2][16], const float (&vsj)[16], const SwzTile& t,
-                                              St (&st)[2]) {
+// The softmax and P.V half of a tile: P = exp2(s - m) (the row sums take
+// the unrounded P), the weights w = P * v_scale, and O += W V8 with W
+// rounded to bf16.  lo (wave-uniform): each weight also enters by its
+// rounding residue, bf16(w - bf16(w)), in a second product (hi + lo is w
+// to about 2^-17), so a key that dominates its row adds v8 * v_scale at
+// f32 accuracy.  With hi alone the weights are rounded once (relative
+// error <= 2^-9 each); the caller sets lo on the tiles where some weight
+// is a large fraction of its row's sum, and leaves it clear where every
+// weight is a small share of the row, whose rounding errors are
+// independent and largely cancel.  (One code path with a branch around
+// the lo products per 32 keys: two whole paths, with and without them,
+// took ~60 more registers.)
+__device__ __forceinline__ void softmax_pv(float (&s)[kNG][16], const float (&moff)[kNG], const float* vsc,
+                                           const SwzTile& t, St (&st)[kNG], bool lo) {
 #pragma clang fp contract(off)
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int gr = 0; gr < kNG; ++gr) {
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const float4 v4 = *reinterpret_cast<const float4*>(vsc + 16 * kb + 4 * g);
+      const float vsj[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(s[gr][4 * kb + i] - moff[gr]);  // -inf -> 0
+        psum += p;
+        s[gr][4 * kb + i] = p * vsj[i];
+      }
+    }
+    st[gr].l += psum;
+  }
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
-    bf16x8_t ph[2], pl[2];
+    bf16x8_t ph[kNG];
 #pragma unroll
-    for (int gr = 0; gr < 2; ++gr) {
-      __bf16 hv[8], lv[8];
+    for (int gr = 0; gr < kNG; ++gr) {
+      __bf16 hv[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float w = s[gr][8 * kc + i] * vsj[8 * kc + i];
-        hv[i] = (__bf16)w;
-        if constexpr (LO) lv[i] = (__bf16)(w - (float)hv[i]);  // exact difference, rounded once
-      }
+      for (int i = 0; i < 8; ++i) hv[i] = (__bf16)s[gr][8 * kc + i];
       __builtin_memcpy(&ph[gr], hv, 16);
-      if constexpr (LO) __builtin_memcpy(&pl[gr], lv, 16);
     }
+    bf16x8_t va[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       // V^T: lane (dim 16db + lane%16, g) holds keys 32kc + 4g + (0..3) and
       // 32kc + 16 + 4g + (0..3), matching the weights
-      const i16x4_t lo = ds_tr4(t.vtr(kc, 0, db));
-      const i16x4_t hi = ds_tr4(t.vtr(kc, 1, db));
-      bf16x8_t va;
-      __builtin_memcpy(&va, &lo, 8);
-      __builtin_memcpy(reinterpret_cast<char*>(&va) + 8, &hi, 8);
+      const i16x4_t lo4 = ds_tr4(t.vtr(kc, 0, db));
+      const i16x4_t hi4 = ds_tr4(t.vtr(kc, 1, db));
+      __builtin_memcpy(&va[db], &lo4, 8);
+      __builtin_memcpy(reinterpret_cast<char*>(&va[db]) + 8, &hi4, 8);
 #pragma unroll
-      for (int gr = 0; gr < 2; ++gr) {
-        if constexpr (LO) st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[gr], st[gr].acc[db], 0, 0, 0);
-        st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[gr], st[gr].acc[db], 0, 0, 0);
+      for (int gr = 0; gr < kNG; ++gr)
+        st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], ph[gr], st[gr].acc[db], 0, 0, 0);
+    }
+    if (lo) {
+      bf16x8_t pl[kNG];
+#pragma unroll
+      for (int gr = 0; gr < kNG; ++gr) {
+        __bf16 lv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float w = s[gr][8 * kc + i];
+          lv[i] = (__bf16)(w - (float)(__bf16)w);  // exact difference, rounded once
+        }
+        __builtin_memcpy(&pl[gr], lv, 16);
       }
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int gr = 0; gr < kNG; ++gr)
+          st[gr].acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], pl[gr], st[gr].acc[db], 0, 0, 0);
     }
   }
 }
 
 // One 64-key tile: scores q . k8 times the keys' scales, the tile's row
-// maxima (rescaling when one rises), P, and the P.V products.  MASKED:
-// keys past S or (causal) after the query's position are dropped; kpos is
-// the shortlist's positions (global; read only in masked tiles).  sc: the
-// tile's K scales (64 floats) followed by its V scales.
+// maxima (rescaling when one rises), then softmax_pv.  MASKED: keys past S
+// or (causal) after the query's position are dropped; kpos is the
+// shortlist's positions (global; read only in masked tiles).  sc: the
+// tile's K scales (64 floats) followed by its V scales.  The lane's keys
+// are 16kb + 4g + i, scores s[.][4kb + i].
 template <bool MASKED>
-__device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& t, const float* sc,
-                                     const int32_t* kpos, int key0, int S, int causal, const int (&tq)[2],
-                                     St (&st)[2]) {
+__device__ __forceinline__ void tile(const bf16x8_t (&qf)[kNG][2], const SwzTile& t, const float* sc,
+                                     const int32_t* kpos, int key0, int S, int causal, const int (&tq)[kNG],
+                                     St (&st)[kNG]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
-  // the lane's keys 16kb + 4g + i: scores s[.][4kb + i]
-  float ksj[16], vsj[16];
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    const float4 a = *reinterpret_cast<const float4*>(sc + 16 * kb + 4 * g);
-    const float4 b = *reinterpret_cast<const float4*>(sc + kTile + 16 * kb + 4 * g);
-    ksj[4 * kb] = a.x, ksj[4 * kb + 1] = a.y, ksj[4 * kb + 2] = a.z, ksj[4 * kb + 3] = a.w;
-    vsj[4 * kb] = b.x, vsj[4 * kb + 1] = b.y, vsj[4 * kb + 2] = b.z, vsj[4 * kb + 3] = b.w;
-  }
-  float s[2][16];
+  float s[kNG][16];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, 0));
     const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, 1));
+    const float4 k4 = *reinterpret_cast<const float4*>(sc + 16 * kb + 4 * g);
+    const float ksj[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
-    for (int gr = 0; gr < 2; ++gr) {
+    for (int gr = 0; gr < kNG; ++gr) {
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[gr][0], c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[gr][1], c, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float v = c[i] * ksj[4 * kb + i];
+        const float v = c[i] * ksj[i];
         if constexpr (MASKED) {
           const int key = key0 + 16 * kb + 4 * g + i;
           const int pos = kpos[key < S ? key : S - 1];
@@ -210,8 +240,9 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& 
   // lazy rescaling: the accumulators are rescaled only on tiles where some
   // row of the wave sees a new maximum; m stays the exact running max
   bool lo_needed = false;
+  float moff[kNG];
 #pragma unroll
-  for (int gr = 0; gr < 2; ++gr) {
+  for (int gr = 0; gr < kNG; ++gr) {
     float tmax = s[gr][0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[gr][i]);
@@ -226,23 +257,14 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[2][2], const SwzTile& 
         for (int i = 0; i < 4; ++i) st[gr].acc[db][i] *= alpha;
       st[gr].m = mn;
     }
-    const float moff = st[gr].m == -INFINITY ? 0.f : st[gr].m;
-    float psum = 0.f, pmax = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s[gr][i] = __builtin_amdgcn_exp2f(s[gr][i] - moff);  // -inf -> 0
-      psum += s[gr][i];
-      pmax = fmaxf(pmax, s[gr][i]);
-    }
-    // the lane's partial sum so far is at most its row's sum, so a weight
-    // below kLoFrac of it is below kLoFrac of the row's final sum
-    lo_needed |= pmax > kLoFrac * st[gr].l;
-    st[gr].l += psum;
+    moff[gr] = st[gr].m == -INFINITY ? 0.f : st[gr].m;
+    // the lane's largest P against its partial row sum so far: that sum is
+    // at most the row's, so a weight below kLoFrac of it is below kLoFrac of
+    // the row's final sum (v_scale aside, which every key of the row shares
+    // up to its own factor)
+    lo_needed |= __builtin_amdgcn_exp2f(tmax - moff[gr]) > kLoFrac * st[gr].l;
   }
-  if (__ballot(lo_needed) != 0)
-    pv_accumulate<true>(s, vsj, t, st);
-  else
-    pv_accumulate<false>(s, vsj, t, st);
+  softmax_pv(s, moff, sc + kTile, t, st, __ballot(lo_needed) != 0);
 }
 
 __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restrict__ kpos, int S, int64_t T,
@@ -272,7 +294,7 @@ __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restri
 }
 
 #ifndef PFA_FIN_WAVES_PER_EU
-#define PFA_FIN_WAVES_PER_EU 2
+#define PFA_FIN_WAVES_PER_EU 3
 #endif
 // a workgroup's ring is kStages x 16.5 KB of LDS
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PFA_FIN_WAVES_PER_EU, 8)))
@@ -288,11 +310,11 @@ final_attn_kernel(Args a) {
   L.init();
   const int2 rg = a.rng[qt];
   const int64_t t_base = (int64_t)qt * kQ;
-  int tq[2];
-  bool qv[2];
+  int tq[kNG];
+  bool qv[kNG];
 #pragma unroll
-  for (int gr = 0; gr < 2; ++gr) {
-    const int64_t t = t_base + 32 * wid + 16 * gr + r16;
+  for (int gr = 0; gr < kNG; ++gr) {
+    const int64_t t = t_base + 16 * kNG * wid + 16 * gr + r16;
     qv[gr] = t < a.T;
     tq[gr] = (int)(qv[gr] ? t : a.T - 1);
   }
@@ -323,9 +345,9 @@ final_attn_kernel(Args a) {
   for (int i = 0; i < kStages - 1; ++i)
     if (i < ntile) request(i);
   const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
-  bf16x8_t qf[2][2];
+  bf16x8_t qf[kNG][2];
 #pragma unroll
-  for (int gr = 0; gr < 2; ++gr)
+  for (int gr = 0; gr < kNG; ++gr)
 #pragma unroll
     for (int dc = 0; dc < 2; ++dc) {
       const uint4 w = *reinterpret_cast<const uint4*>(qh + (int64_t)tq[gr] * a.q_st + 32 * dc + 8 * g);
@@ -333,10 +355,11 @@ final_attn_kernel(Args a) {
     }
   // settle the q fragments here: the tile loop then holds no load of the
   // compiler's own to wait for (its wait would also drain the tile requests)
-  asm volatile("" : "+v"(qf[0][0]), "+v"(qf[0][1]), "+v"(qf[1][0]), "+v"(qf[1][1]));
-  St st[2];
 #pragma unroll
-  for (int gr = 0; gr < 2; ++gr) {
+  for (int gr = 0; gr < kNG; ++gr) asm volatile("" : "+v"(qf[gr][0]), "+v"(qf[gr][1]));
+  St st[kNG];
+#pragma unroll
+  for (int gr = 0; gr < kNG; ++gr) {
     st[gr].m = -INFINITY;
     st[gr].l = 0.f;
 #pragma unroll
@@ -368,7 +391,7 @@ final_attn_kernel(Args a) {
   }
   uint16_t* oh = a.out + (int64_t)h * a.o_sh;
 #pragma unroll
-  for (int gr = 0; gr < 2; ++gr) {
+  for (int gr = 0; gr < kNG; ++gr) {
     float l = st[gr].l;
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
