@@ -24,18 +24,18 @@
 // Precision.  The working copies hold the int8 values themselves, which
 // bf16 represents exactly; the per-key scales stay in f32 and travel with
 // each tile (512 bytes beside its 16 KB of K and V).  Scores are in log2
-// units: the MFMA gives q . k8 (exact products, f32 sums) and each is
-// multiplied by c_j = k_scale[j] * scale * log2(e).  So a score is as
-// accurate as an f32 dot product, with no rounding of the scaled K (a bf16
-// copy of k8 * c moved the scores of rows with 4x the typical norm by
-// tenths).  The softmax takes the exact row maximum (a dominant key's P is
-// exactly 1) and the row sum l sums the unrounded P in f32.  The P.V
-// product takes the weights w_j = P_j * v_scale[j] against the exact v8:
-// on a tile where some weight exceeds 1/8 of its row's running sum, as two
-// bf16 parts (hi + lo, w to ~2^-17), else rounded once to bf16, whose
-// independent errors of <= 2^-9 relative on weights that are each a small
-// share of the row largely cancel.  QK^T and P.V are 32 MFMAs per 64-key
-// tile and wave, 48 on the tiles that take the lo parts.
+// units: the MFMA gives q . k8 (exact products, f32 sums) and one fma
+// takes it to q . k8 * c_j - m, c_j = k_scale[j] * scale * log2(e) and m
+// the row's reference maximum.  So a score is as accurate as an f32 dot
+// product, with no rounding of the scaled K (a bf16 copy of k8 * c moved
+// the scores of rows with 4x the typical norm by tenths).  m moves lazily
+// (P <= 2^8 between moves) and the row sum l sums the unrounded P in f32.
+// The P.V product takes the weights w_j = P_j * v_scale[j] against the
+// exact v8: on a tile where some weight exceeds 1/8 of its row's running
+// sum, as two bf16 parts (hi + lo, w to ~2^-17), else rounded once to
+// bf16, whose independent errors of <= 2^-9 relative on weights that are
+// each a small share of the row largely cancel.  QK^T and P.V are 32 MFMAs
+// per 64-key tile and wave, 48 on the tiles that take the lo parts.
 #include "pfa_common.h"
 
 namespace pfa {
@@ -50,7 +50,10 @@ constexpr int kNG = PFA_FIN_NG;        // 16-query MFMA column groups per wave
 constexpr int kQ = 16 * kNG * kWaves;  // queries per workgroup
 constexpr int kTile = kSwzKeys;  // keys per tile
 constexpr int kD = 64;
-constexpr float kRescaleLog2 = 0.0f;  // rescale when some row's max rises
+#ifndef PFA_FIN_LAZY_LOG2
+#define PFA_FIN_LAZY_LOG2 8.0f
+#endif
+constexpr float kLazyLog2 = PFA_FIN_LAZY_LOG2;  // P <= 2^kLazyLog2 between rescales
 #ifndef PFA_FIN_LO_FRAC
 #define PFA_FIN_LO_FRAC 0.125f
 #endif
@@ -124,8 +127,8 @@ __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__
   __builtin_memcpy(vh + off, vd, 32);
 }
 
-// The softmax and P.V half of a tile: P = exp2(s - m) (the row sums take
-// the unrounded P), the weights w = P * v_scale, and O += W V8 with W
+// The softmax and P.V half of a tile: P = exp2(s), s the scores relative
+// to the row's reference maximum (the row sums take the unrounded P), the weights w = P * v_scale, and O += W V8 with W
 // rounded to bf16.  lo (wave-uniform): each weight also enters by its
 // rounding residue, bf16(w - bf16(w)), in a second product (hi + lo is w
 // to about 2^-17), so a key that dominates its row adds v8 * v_scale at
@@ -136,8 +139,8 @@ __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__
 // independent and largely cancel.  (One code path with a branch around
 // the lo products per 32 keys: two whole paths, with and without them,
 // took ~60 more registers.)
-__device__ __forceinline__ void softmax_pv(float (&s)[kNG][16], const float (&moff)[kNG], const float* vsc,
-                                           const SwzTile& t, St (&st)[kNG], bool lo) {
+__device__ __forceinline__ void softmax_pv(float (&s)[kNG][16], const float* vsc, const SwzTile& t, St (&st)[kNG],
+                                           bool lo) {
 #pragma clang fp contract(off)
   const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
@@ -149,7 +152,7 @@ __device__ __forceinline__ void softmax_pv(float (&s)[kNG][16], const float (&mo
       const float vsj[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(s[gr][4 * kb + i] - moff[gr]);  // -inf -> 0
+        const float p = __builtin_amdgcn_exp2f(s[gr][4 * kb + i]);  // -inf -> 0
         psum += p;
         s[gr][4 * kb + i] = p * vsj[i];
       }
@@ -200,17 +203,25 @@ __device__ __forceinline__ void softmax_pv(float (&s)[kNG][16], const float (&mo
   }
 }
 
-// One 64-key tile: scores q . k8 times the keys' scales, the tile's row
-// maxima (rescaling when one rises), then softmax_pv.  MASKED: keys past S
-// or (causal) after the query's position are dropped; kpos is the
-// shortlist's positions (global; read only in masked tiles).  sc: the
-// tile's K scales (64 floats) followed by its V scales.  The lane's keys
-// are 16kb + 4g + i, scores s[.][4kb + i].
+// One 64-key tile: scores q . k8 times the keys' scales, relative to the
+// row's reference maximum m, then softmax_pv.  MASKED: keys past S or
+// (causal) after the query's position are dropped; kpos is the shortlist's
+// positions (global; read only in masked tiles).  sc: the tile's K scales
+// (64 floats) followed by its V scales.  The lane's keys are 16kb + 4g + i,
+// scores s[.][4kb + i].
+//
+// The reference moves lazily: only on a row's first visible key, or when
+// one of its scores exceeds m by more than kLazyLog2 (then m becomes the
+// row's maximum and the accumulators are rescaled).  Between moves P stays
+// <= 2^kLazyLog2, and a score is one fma, q.k8 * c - m.
 template <bool MASKED>
 __device__ __forceinline__ void tile(const bf16x8_t (&qf)[kNG][2], const SwzTile& t, const float* sc,
                                      const int32_t* kpos, int key0, int S, int causal, const int (&tq)[kNG],
                                      St (&st)[kNG]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
+  float mneg[kNG];
+#pragma unroll
+  for (int gr = 0; gr < kNG; ++gr) mneg[gr] = st[gr].m == -INFINITY ? 0.f : -st[gr].m;
   float s[kNG][16];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
@@ -225,7 +236,7 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[kNG][2], const SwzTile
       c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[gr][1], c, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float v = c[i] * ksj[i];
+        const float v = __builtin_fmaf(c[i], ksj[i], mneg[gr]);
         if constexpr (MASKED) {
           const int key = key0 + 16 * kb + 4 * g + i;
           const int pos = kpos[key < S ? key : S - 1];
@@ -237,34 +248,37 @@ __device__ __forceinline__ void tile(const bf16x8_t (&qf)[kNG][2], const SwzTile
       }
     }
   }
-  // lazy rescaling: the accumulators are rescaled only on tiles where some
-  // row of the wave sees a new maximum; m stays the exact running max
   bool lo_needed = false;
-  float moff[kNG];
 #pragma unroll
   for (int gr = 0; gr < kNG; ++gr) {
     float tmax = s[gr][0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[gr][i]);
-    const float tm = max_over_rows4(tmax);
-    if (__ballot(tm > st[gr].m + kRescaleLog2) != 0) {
-      const float mn = fmaxf(st[gr].m, tm);
-      const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(st[gr].m - mn);  // m == -inf -> 0
-      st[gr].l *= alpha;
+    const bool fresh = st[gr].m == -INFINITY;
+    if (__ballot(fresh ? tmax > -INFINITY : tmax > kLazyLog2) != 0) {
+      const float tm = max_over_rows4(tmax);  // the row's maximum, relative
+      const bool mv = fresh ? tm > -INFINITY : tm > kLazyLog2;
+      const float d = mv ? tm : 0.f;
+      if (mv && !fresh) {  // a fresh row's accumulators are still zero
+        const float alpha = __builtin_amdgcn_exp2f(-d);
+        st[gr].l *= alpha;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[gr].acc[db][i] *= alpha;
-      st[gr].m = mn;
+          for (int i = 0; i < 4; ++i) st[gr].acc[db][i] *= alpha;
+      }
+      if (mv) st[gr].m = -mneg[gr] + d;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[gr][i] -= d;
+      tmax -= d;
     }
-    moff[gr] = st[gr].m == -INFINITY ? 0.f : st[gr].m;
     // the lane's largest P against its partial row sum so far: that sum is
     // at most the row's, so a weight below kLoFrac of it is below kLoFrac of
     // the row's final sum (v_scale aside, which every key of the row shares
     // up to its own factor)
-    lo_needed |= __builtin_amdgcn_exp2f(tmax - moff[gr]) > kLoFrac * st[gr].l;
+    lo_needed |= __builtin_amdgcn_exp2f(tmax) > kLoFrac * st[gr].l;
   }
-  softmax_pv(s, moff, sc + kTile, t, st, __ballot(lo_needed) != 0);
+  softmax_pv(s, sc + kTile, t, st, __ballot(lo_needed) != 0);
 }
 
 __global__ void __launch_bounds__(256) key_ranges_kernel(const int32_t* __restrict__ kpos, int S, int64_t T,
