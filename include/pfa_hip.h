@@ -555,14 +555,11 @@ int pfa_rope_rows_inplace(void* x, int dtype, int64_t n_rows, int64_t row_stride
  * causal by original position when `causal` (key j visible to query t iff
  * key_pos[j] <= t; key_pos ascending).  K/V are int8 (H, S, D) with
  * per-(head, row) scales (H, S) from pfa_quantize_rows_int8 (k8/v8
- * 16-byte aligned; scales finite).  Once per call the int8 values are
- * copied to bf16 (exact) and the scales to f32 rows padded to 64 keys, so
- * the workspace holds 4*H*S*D bytes plus 8*H*ceil(S/64)*64 bytes plus the
- * query tiles' key ranges.  Scores are q . k8 * k_scale in f32; the
- * weights P * v_scale meet the exact v8 as bf16 (hi + lo parts on tiles
- * where one weight is a large share of its row).  q/out are bf16
- * [h][t][d] through pfa_tensor4 strides (s_b unused: one sequence).  A
- * query with no visible key gets a zero row.  S >= 1.
+ * 16-byte aligned), dequantised once per call to bf16 (x8 * scale, round
+ * to nearest even) into the workspace, which therefore holds 4*H*S*D
+ * bytes plus the query tiles' key ranges.  q/out are bf16 [h][t][d]
+ * through pfa_tensor4 strides (s_b unused: one sequence).  A query with
+ * no visible key gets a zero row.  S >= 1.
  * ==================================================================== */
 int pfa_int8_kv_attn_workspace_size(int64_t T, int H, int S, size_t* bytes);
 int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, int H, int D,
@@ -570,25 +567,6 @@ int pfa_int8_kv_attn_fwd(pfa_tensor4 q, pfa_tensor4 out, int64_t T, int H, int D
                          const float* v_scale, const int32_t* key_pos, int S,
                          int causal, float scale, void* workspace,
                          size_t ws_bytes, void* stream);
-
-/* ====================================================================
- * The forward's projection GEMMs, y (M, N) = x (M, K) W (N, K)^T (+ bias
- * (N,)), all bf16 row-major with f32 accumulation: the QKV projection
- * (self.qkv(x), aspa.py:1641) and the output projection (self.proj(attn),
- * aspa.py:1852-1855).  hipBLASLt computes the product; the first call for
- * a shape outside graph capture times hipBLASLt's leading heuristic
- * candidates on `stream` (synchronising it) and keeps the fastest whose
- * output is bitwise the same on two runs; later calls, captured ones
- * included, reuse that kernel.  A shape first met inside a capture takes
- * the heuristic's first pick until a call outside a capture times it.
- * The first call on a device allocates a 64 MiB workspace and so must not
- * be inside a capture (PFA_E_INVALID).  Only dtype PFA_BF16
- * (PFA_E_UNSUPPORTED otherwise).
- * pfa_linear_tuned: 1 when the shape's kernel has been chosen by timing.
- * ==================================================================== */
-int pfa_linear(const void* x, int dtype, int64_t M, int K, const void* w, int N,
-               const void* bias, void* y, void* stream);
-int pfa_linear_tuned(int64_t M, int N, int K, int has_bias);
 
 #ifdef __cplusplus
 }

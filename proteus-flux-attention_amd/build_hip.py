@@ -58,8 +58,7 @@ def build(verbose: bool = False) -> Path:
         for f in futs:
             f.result()
     tmp = OUT_DIR / (LIB_NAME + ".tmp")
-    # hipBLASLt: the projection GEMMs (pfa_gemm.hip)
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-lhipblaslt", "-o", str(tmp)]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

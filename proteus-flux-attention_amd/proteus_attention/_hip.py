@@ -67,8 +67,6 @@ EXPORTED_SYMBOLS = (
     "pfa_rope_rows_inplace",
     "pfa_int8_kv_attn_workspace_size",
     "pfa_int8_kv_attn_fwd",
-    "pfa_linear",
-    "pfa_linear_tuned",
 )
 
 
@@ -139,8 +137,6 @@ _SIGNATURES = {
     "pfa_rope_k_zero_inplace": ([_vp, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "pfa_router_stats_reduce": ([_vp, _i32, _vp, _vp], _i32),
     "pfa_zero_fill": ([_vp, _sz, _vp], _i32),
-    "pfa_linear": ([_vp, _i32, _i64, _i32, _vp, _i32, _vp, _vp, _vp], _i32),
-    "pfa_linear_tuned": ([_i64, _i32, _i32, _i32], _i32),
     "pfa_chunk_topk_workspace_size": ([_i64, _i32, ctypes.POINTER(_sz)], _i32),
     "pfa_chunk_topk": ([_vp, _vp, _i64, _i32, _f32, _i64, _i32, _vp, _vp, _vp, _vp, _sz, _vp], _i32),
     "pfa_shortlist_finalise_workspace_size": ([_i64, ctypes.POINTER(_sz)], _i32),

@@ -1021,27 +1021,8 @@ class AdaptiveSparseAttention(nn.Module):
                          H, T, D, token_idx, row_head, head_map, None, None, None, None, 1.0 / math.sqrt(D),
                          (None, None, None), qkv.device, n_rows_dev=n_dev)
 
-    @staticmethod
-    def _linear(layer: nn.Linear, x: torch.Tensor) -> torch.Tensor:
-        """layer(x) for the projections (aspa.py:1641, 1853).  bf16 without
-        autograd runs on the library's hipBLASLt GEMM, whose kernel is chosen
-        by timing per shape (pfa_linear); anything else on torch's."""
-        w, b = layer.weight, layer.bias
-        if (x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or not x.is_cuda
-                or (b is not None and b.dtype != torch.bfloat16)
-                or (torch.is_grad_enabled() and (x.requires_grad or w.requires_grad
-                                                 or (b is not None and b.requires_grad)))):
-            return layer(x)
-        xc = x.contiguous()
-        K, N = int(xc.shape[-1]), int(w.shape[0])
-        y = torch.empty(*xc.shape[:-1], N, dtype=torch.bfloat16, device=x.device)
-        _hip.check(_hip.lib().pfa_linear(_hip.ptr(xc), _hip.PFA_BF16, xc.numel() // K, K, _hip.ptr(w.contiguous()), N,
-                                         None if b is None else _hip.ptr(b.contiguous()), _hip.ptr(y),
-                                         _hip.stream_ptr(x.device)), "pfa_linear")
-        return y
-
     def _project_qkv(self, x: torch.Tensor) -> torch.Tensor:
-        qkv = self._linear(self.qkv, x).contiguous()  # (B, T, 3C) = (B, T, 3, H, D)
+        qkv = self.qkv(x).contiguous()  # (B, T, 3C) = (B, T, 3, H, D)
         self._rope_inplace(qkv, rotate_q=True)
         return qkv
 
@@ -1090,7 +1071,7 @@ class AdaptiveSparseAttention(nn.Module):
         qkv = self._project_qkv(x)
         attn = torch.empty(B, T, C, dtype=qkv.dtype, device=x.device)
         self._attend_dense_causal(qkv, B, T, attn)
-        y = self.dropout(self._linear(self.proj, attn))
+        y = self.dropout(self.proj(attn))
         self._last_target_k = self.h_total
         self._last_sparse_state = {
             "mode": "dense_fastpath", "backend": "hip_dense", "max_rows": T, "density": 1.0,
@@ -1228,11 +1209,12 @@ class AdaptiveSparseAttention(nn.Module):
             side = _side_stream(device, "capture")
             side.wait_stream(torch.cuda.current_stream(device))
             with torch.cuda.stream(side):
-                # warm-up: library handles, lazy allocations, the projection
-                # GEMMs' kernel choice (timed outside the capture)
+                # warm-up: library handles, lazy allocations; with the output
+                # projection captured it runs here too, so that its GEMM sets
+                # up the library's handle and workspace outside the capture
                 attn_w = self._forward_impl(xs, capture=True)[0]
                 if self._hip_graph_static_output:
-                    self._linear(self.proj, attn_w)
+                    self.dropout(self.proj(attn_w))
                 del attn_w
             torch.cuda.current_stream(device).wait_stream(side)
             with torch.no_grad():
@@ -1258,7 +1240,7 @@ class AdaptiveSparseAttention(nn.Module):
             try:
                 with torch.cuda.graph(graph, pool=self._hip_graph_pool):
                     attn, stats_args, label = self._forward_impl(xs, capture=True)
-                    y_static = self.dropout(self._linear(self.proj, attn)) if self._hip_graph_static_output else None
+                    y_static = self.dropout(self.proj(attn)) if self._hip_graph_static_output else None
             finally:
                 if gc_was_on:
                     gc.enable()
@@ -1286,7 +1268,7 @@ class AdaptiveSparseAttention(nn.Module):
         if x.data_ptr() != xs.data_ptr():
             xs.copy_(x)
         ent["graph"].replay()
-        y = ent["y"] if ent["y"] is not None else self.dropout(self._linear(self.proj, ent["attn"]))
+        y = ent["y"] if ent["y"] is not None else self.dropout(self.proj(ent["attn"]))
         for k, v in ent["state"].items():
             self.__dict__[k] = v
         st = ent["sparse_state"]
@@ -1365,7 +1347,7 @@ class AdaptiveSparseAttention(nn.Module):
         fork_s = self._fork_stream(device)
         fork_s.wait_stream(main_s)
         with torch.cuda.stream(fork_s):
-            qkv = self._linear(self.qkv, x).contiguous()  # (B, T, 3C) = (B, T, 3, H, D)
+            qkv = self.qkv(x).contiguous()  # (B, T, 3C) = (B, T, 3, H, D)
 
         alpha = self._compute_cvt_alpha(T)
         self._current_alpha = alpha
@@ -1621,7 +1603,7 @@ class AdaptiveSparseAttention(nn.Module):
         label = f"cvt(alpha={alpha:.2f})::{mode_label}"
         if capture:
             return attn, stats_args, label
-        y = self.dropout(self._linear(self.proj, attn))
+        y = self.dropout(self.proj(attn))
 
         # the latency's end event also marks the telemetry copy done
         self._finish_stats(*stats_args, done=ev1)
