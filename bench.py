@@ -274,7 +274,9 @@ def bench_forward(args, workload: str) -> dict:
                 # traffic: not measured in this run -- HBM bytes per forward
                 # from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded
                 # in the profiles file named here
-                "traffic_source": "profiles/cfg3_hbm_traffic.md" if dk["traffic"] is not None else None}
+                "traffic_source": ("recorded, not measured in this run: profiles/cfg3_hbm_traffic.md "
+                                   "(rocprofv3 FETCH_SIZE + WRITE_SIZE passes over this bench, scaled by a copy "
+                                   "of known size)") if dk["traffic"] is not None else None}
     cpu = None
     if workload == "cfg3" and not args.no_cpu_baseline:
         log("cpu baseline (oracle pipeline on host cores)")
