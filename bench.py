@@ -4,7 +4,7 @@
 dominant kernel and the CPU oracle pipeline timed on the host beside it.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-                    [--workload cfg3|cfg4|cfg5]
+                    [--workload cfg1|cfg2|cfg3|cfg4|cfg5]
 
 Prints exactly one JSON line on stdout.  A "step" is one module forward of
 config 3 (router, head top-k, packing, QKV projection + RoPE, prototype
@@ -17,7 +17,9 @@ timed with HIP events, whose ms/step is reported as eager_ms_per_step.
 --workload cfg4 times the same forward at T=524,288 with L=4096 (single
 pass, no chunking); --workload cfg5 times one run of the chunked shortlist
 pipeline at T=1,048,576 (16 chunks of 65,536, top-512 per chunk, 8,192-token
-int8 shortlist, all-query final pass).  Neither is the headline line.
+int8 shortlist, all-query final pass); --workload cfg1 / cfg2 time the
+token-sparse forward of BASELINE.json's two parity configurations.  None of
+these is the headline line.
 """
 from __future__ import annotations
 
@@ -37,6 +39,8 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
+CFG1 = dict(B=1, T=1024, C=256, H=8, keep=0.25, dtype="f32")
+CFG2 = dict(B=2, T=8192, C=512, H=8, keep=0.25, dtype="bf16")
 CFG3 = dict(B=1, T=65536, C=512, H=8, L=2048, window=512, stride=256, outlier=0.01)
 CFG4 = dict(B=1, T=524288, C=512, H=8, L=4096, window=512, stride=256, outlier=0.0)
 CFG5 = dict(T=1 << 20, C=512, H=8, chunk=65536, budget=512, buffer=8192)
@@ -310,6 +314,96 @@ def bench_forward(args, workload: str) -> dict:
     }
 
 
+def bench_sparse(args, workload: str) -> dict:
+    """Configs 1 and 2 (BASELINE.json's parity configurations, timed on
+    request): the token-sparse module forward (router, token top-k, packing,
+    gathered causal attention over the kept rows), graph replay timed, eager
+    forwards for per-entry-point events."""
+    import torch
+    from configs import init_weights, make_inputs, sparse_cfg
+
+    from proteus_attention import _hip
+    from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
+
+    c = CFG1 if workload == "cfg1" else CFG2
+    dtype = torch.float32 if c["dtype"] == "f32" else torch.bfloat16
+    dev = torch.device("cuda:0")
+    log(f"building {workload} module (B={c['B']} T={c['T']} {c['dtype']})")
+    torch.manual_seed(1234)
+    m = AdaptiveSparseAttention(ModelConfig(**sparse_cfg(c["T"], c["C"], c["H"], c["keep"])))
+    x_cpu, g = make_inputs(c["B"], c["T"], c["C"], seed=0)
+    init_weights(m, g)
+    m = m.to(device=dev, dtype=dtype).eval()
+    x = x_cpu.to(dtype).to(dev)
+    snap = {n: b.detach().clone() for n, b in m.named_buffers() if n.startswith("routing_")}
+
+    def restore():
+        for n, b in snap.items():
+            getattr(m, n).copy_(b)
+
+    m.enable_hip_graph(not args.eager, static_output=not args.fresh_output)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            restore()
+            m(x)
+        graph = not args.eager
+        if graph:
+            try:
+                x = m.hip_graph_input(x)
+            except RuntimeError:  # the forward's shape is not graph-eligible: timed eagerly
+                graph = False
+                m.enable_hip_graph(False)
+        restore()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            m(x)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        m.enable_hip_graph(False)
+        restore()
+        m(x)
+        _hip.TIMER.reset()
+        _hip.TIMER.enabled = True
+        torch.cuda.synchronize()
+        e0 = time.perf_counter()
+        for _ in range(args.steps):
+            restore()
+            m(x)
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - e0) * 1000.0 / args.steps
+        _hip.TIMER.enabled = False
+    stages = {k: sum(v) / args.steps for k, v in _hip.TIMER.summary_ms().items()}
+    tokens = c["B"] * c["T"]
+    dominant = max(stages, key=stages.get) if stages else None
+    return {
+        "metric": f"sparse fwd tokens/s @T={c['T']} {c['dtype']}, 1 GPU",
+        "value": round(tokens * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1000.0 / args.steps, 4),
+        "eager_ms_per_step": round(eager_ms, 4),
+        "timed_as": "graph replay" if graph else "eager forwards",
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": c["dtype"],
+        "data": "synthetic: x~N(0,1) seed 0, Xavier-normal weights from the same generator",
+        "config": {"workload": (f"config {workload[-1]}: ASPA sparse forward, B={c['B']} T={c['T']} "
+                                f"d_model={c['C']} H={c['H']} D={c['C'] // c['H']} token keep {c['keep']} "
+                                "top-2 heads, causal"),
+                   "global_batch": c["B"], "seq_len": c["T"], "parallelism": "single GPU"},
+        # per-entry-point HIP-event times of the eager forward; the dominant
+        # kernel's algorithmic work is not reported for these parity configs
+        "roofline": None,
+        "kernels": {k: {"ms": round(v, 4)} for k, v in stages.items()},
+        "dominant_kernel": dominant,
+        "cpu_baseline": None,
+    }
+
+
 def bench_cfg5(args) -> dict:
     """Config 5: one run of the chunked shortlist pipeline; the last of
     warmup + steps runs is reported.  --cfg5-source device: the sequence is
@@ -396,7 +490,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=("cfg3", "cfg4", "cfg5"), default="cfg3")
+    ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3", "cfg4", "cfg5"), default="cfg3",
+                    help="cfg3 is the bench line; cfg1/cfg2 are BASELINE's parity configurations, timed on request")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cfg5-source", choices=("device", "pinned", "disk"), default="device",
                     help="where config 5's sequence lives (--workload cfg5)")
@@ -434,7 +529,12 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
         return 0
-    line = bench_cfg5(args) if args.workload == "cfg5" else bench_forward(args, args.workload)
+    if args.workload == "cfg5":
+        line = bench_cfg5(args)
+    elif args.workload in ("cfg1", "cfg2"):
+        line = bench_sparse(args, args.workload)
+    else:
+        line = bench_forward(args, args.workload)
     print(json.dumps(line), flush=True)
     return 0
 
