@@ -43,7 +43,7 @@ constexpr int kRows = 64;   // query rows per workgroup
 constexpr int kTile = 64;   // keys per tile
 constexpr int kPartW = 68;  // floats per partial row: m, l, pad, pad, acc[64]
 constexpr int kMaxProto = 1024;
-constexpr int kMaxClassRows = 4096;
+constexpr int kClassChunk = 2048;  // anchor pass: class rows compacted per round
 constexpr float kRescaleLog2 = 0.0f;  // rescale only when some row's max rises
 // Anchor-pass fusions.  Workgroup (c, p) owns the tokens t = c (mod stride)
 // of global head head_map[p]: every (head, token) pair of the active heads
@@ -461,11 +461,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
                                                                                                      int ccap) {
   constexpr int S = kAnchorStages;
   __shared__ __align__(16) uint16_t ring[S][2 * kTileElems];
-  // active rows of the class: row index and class position M (M < ccap <=
-  // kMaxClassRows), sized to the class length (dynamic LDS)
+  // active rows of the class, compacted ccap at a time (a multiple of 256,
+  // at most kClassChunk; dynamic LDS): row index and class position M
   extern __shared__ int32_t cls_dyn[];
   int32_t* cls_r = cls_dyn;
-  uint16_t* cls_m = reinterpret_cast<uint16_t*>(cls_dyn + ccap);
+  int32_t* cls_m = cls_dyn + ccap;
   __shared__ int s_count;
   __shared__ int wave_cnt[4];
 
@@ -503,11 +503,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + 1024u * (uint32_t)wid);
   constexpr uint32_t kStageBytes = 2 * kTileElems * 2;
 
-  // compact the active rows of this class (ascending M)
+  const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
+  const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
+  const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
+
+  // The class's active rows in rounds: compact the rows of the next class
+  // positions (ascending M) until the list holds ccap - 256 or more, then
+  // attend them.  A row's keys depend on its own M only, so the rounds
+  // compute what one list of every row would.
+  int64_t scan = 0;  // the next class position to compact (uniform)
+  for (;;) {
   if (tid == 0) s_count = 0;
   __syncthreads();
-  for (int64_t base = 0; base <= Mmax; base += 256) {
-    const int64_t M = base + tid;
+  for (; scan <= Mmax && s_count + 256 <= ccap; scan += 256) {
+    const int64_t M = scan + tid;
     int r = -1;
     if (M <= Mmax) r = a.row_of[(int64_t)bh * a.T + c + (int64_t)s * M];
     const bool act = r >= 0;
@@ -526,7 +535,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
     for (int w = 0; w < wid; ++w) before += wave_cnt[w];
     if (act) {
       const int pos = before + __popcll(bal & ((1ull << lane) - 1ull));
-      cls_m[pos] = (uint16_t)M;
+      cls_m[pos] = (int32_t)M;
       cls_r[pos] = r;
     }
     __syncthreads();
@@ -534,9 +543,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
     __syncthreads();
   }
   const int nrows = s_count;
-  const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
-  const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
-  const uint16_t* qb = (const uint16_t*)a.q.ptr + bb * a.q.s_b + hh * a.q.s_h;
+  __syncthreads();  // every wave has read the count before the next round clears it
 
   for (int c0 = 0; c0 < nrows; c0 += kRows) {
     const int qs = 16 * wid + (lane & 15);
@@ -619,6 +626,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
     }
     // every wave is done with the ring before the next chunk's requests
     __syncthreads();
+  }
+  if (scan > Mmax) break;
   }
 }
 
@@ -1057,8 +1066,6 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
                 "pfa_shortlist_attn_fwd: prototype table (K <= %d with evict) required", kMaxProto);
   const bool anchors = anchor_stride > 0 && anchor_slots > 0;
   PFA_CHECK_ARG(!anchors || (row_of && partials), "pfa_shortlist_attn_fwd: anchors need row_of and partials");
-  PFA_CHECK_ARG(!anchors || (T - 1) / anchor_stride + 1 <= kMaxClassRows,
-                "pfa_shortlist_attn_fwd: T/stride exceeds %d", kMaxClassRows);
   auto al = [](const pfa_tensor4& x) {
     return ((uintptr_t)x.ptr % 16) == 0 && x.s_b % 8 == 0 && x.s_h % 8 == 0 && x.s_t % 8 == 0;
   };
@@ -1089,8 +1096,11 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
   hipStream_t s = as_stream(stream);
   if (anchors && (passes & 1)) {
     dim3 grid((unsigned)((int64_t)anchor_stride < T ? (int64_t)anchor_stride : T), (unsigned)P_cap);
-    const int ccap = (int)((T - 1) / anchor_stride + 1);
-    short_anchor_kernel<<<grid, 256, (size_t)ccap * 6 + 16, s>>>(a, ccap);
+    // class positions rounded up to the 256 of one compaction step, at most
+    // kClassChunk (longer classes are attended in rounds)
+    const int64_t npos = ((T - 1) / anchor_stride + 1 + 255) / 256 * 256;
+    const int ccap = (int)(npos < kClassChunk ? npos : kClassChunk);
+    short_anchor_kernel<<<grid, 256, (size_t)ccap * 8 + 16, s>>>(a, ccap);
     PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
   }
   if (!(passes & 2) || N == 0) return PFA_OK;

@@ -1640,7 +1640,7 @@ class AdaptiveSparseAttention(nn.Module):
         w_eff = max(1, local_w)
         bound = w_eff + ((min(slots, (T - 1) // stride) + 1) if anchors else 0) + K
         structured = (dtype == torch.bfloat16 and D == 64 and bound <= L and K <= 1024
-                      and (not anchors or (T - 1) // stride + 1 <= 4096) and not _hip.env_flag("PFA_FORCE_GENERIC"))
+                      and not _hip.env_flag("PFA_FORCE_GENERIC"))
         return {"L": L, "stride": stride, "local_w": local_w, "slots": slots, "K": K, "use_quant": use_quant,
                 "w_eff": w_eff, "structured": structured}
 

@@ -256,12 +256,15 @@ def test_proto_prefix_sets_large_vs_c_oracle(dev):
 
 
 @pytest.mark.parametrize("T,L,w,s,B,outlier", [(4096, 1024, 256, 64, 1, 0.01), (3000, 700, 100, 37, 2, 0.0),
-                                               (65536, 2048, 512, 256, 1, 0.01), (524288, 4096, 512, 256, 1, 0.0)])
+                                               (65536, 2048, 512, 256, 1, 0.01), (524288, 4096, 512, 256, 1, 0.0),
+                                               (65536, 2048, 512, 4, 1, 0.01), (20000, 1024, 128, 3, 2, 0.0)])
 def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, monkeypatch):
     """The structure-driven MFMA path and the builder + gather path give the
     same candidate counts per row and the same outputs (bf16 tolerance).
     The T=524,288 case is config 4 at full size, single pass: the
-    materialised path holds all 1,048,576 x 4,096 int32 candidates."""
+    materialised path holds all 1,048,576 x 4,096 int32 candidates.  The
+    stride-4 and stride-3 cases have residue classes of 16,384 and 6,667
+    positions, whose rows the anchor pass compacts and attends in rounds."""
     from configs import shortlist_cfg
 
     _say(f"structured vs materialised T={T} L={L} w={w} s={s} B={B}")
