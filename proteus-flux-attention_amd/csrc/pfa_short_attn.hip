@@ -457,6 +457,11 @@ __device__ __forceinline__ void class_rows_fused(const ShortArgs& a, int64_t bb,
 // workgroups (about 100 KB of LDS with a two-stage ring) leave LDS and wave
 // slots for them.
 constexpr int kAnchorStages = 2;
+// Row groups per wave: NG = 2 (32 rows per wave, 128 per chunk) for long
+// residue classes, whose chunks each stream long key bands: the tile
+// transfers and barriers are then shared by twice the rows.
+constexpr int kAnchorNG2Positions = 1024;  // class positions from which NG = 2 is launched
+template <int NG>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) short_anchor_kernel(ShortArgs a,
                                                                                                      int ccap) {
   constexpr int S = kAnchorStages;
@@ -545,30 +550,40 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   const int nrows = s_count;
   __syncthreads();  // every wave has read the count before the next round clears it
 
-  for (int c0 = 0; c0 < nrows; c0 += kRows) {
-    const int qs = 16 * wid + (lane & 15);
-    const bool qv = c0 + qs < nrows;
-    const int Mq = qv ? cls_m[c0 + qs] : 0;
-    const int rq = qv ? cls_r[c0 + qs] : 0;
-    const int64_t tq = c + (int64_t)s * Mq;
-    const int j0 = (int)((tq - win_lo(tq, a.local_w)) / s) + 1;
-    const int hi_q = qv ? Mq - j0 : -1;
-    const int lo_q = Mq - a.slots > 0 ? Mq - a.slots : 0;
-    // wave rows ascending in M: lo_q and hi_q are non-decreasing
-    const int fr = 16 * wid, lr = min(nrows - c0, 16 * wid + 16) - 1;
-    const bool wave_rows = fr <= lr;
-    const bool wave_full = lr == 16 * wid + 15;
-    int w_lolo = 0, w_lohi = 0, w_hilo = -1, w_hihi = -1;
-    if (wave_rows) {
-      const int Ma = cls_m[c0 + fr], Mb = cls_m[c0 + lr];
-      const int64_t ta = c + (int64_t)s * Ma, tb = c + (int64_t)s * Mb;
-      w_lolo = Ma - a.slots > 0 ? Ma - a.slots : 0;
-      w_lohi = Mb - a.slots > 0 ? Mb - a.slots : 0;
-      w_hilo = Ma - ((int)((ta - win_lo(ta, a.local_w)) / s) + 1);
-      w_hihi = Mb - ((int)((tb - win_lo(tb, a.local_w)) / s) + 1);
+  // chunks of 64 * NG rows: wave w takes rows 16 * (NG * w + g) + r16 of
+  // the chunk in its row groups g < NG, every group against the same tiles
+  constexpr int kChunk = kRows * NG;
+  for (int c0 = 0; c0 < nrows; c0 += kChunk) {
+    bool qv[NG], wave_rows[NG], wave_full[NG];
+    int Mq[NG], rq[NG], hi_q[NG], lo_q[NG], w_lolo[NG], w_lohi[NG], w_hilo[NG], w_hihi[NG];
+    int64_t tq[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int base = 16 * (NG * wid + g);
+      const int qs = base + (lane & 15);
+      qv[g] = c0 + qs < nrows;
+      Mq[g] = qv[g] ? cls_m[c0 + qs] : 0;
+      rq[g] = qv[g] ? cls_r[c0 + qs] : 0;
+      tq[g] = c + (int64_t)s * Mq[g];
+      const int j0 = (int)((tq[g] - win_lo(tq[g], a.local_w)) / s) + 1;
+      hi_q[g] = qv[g] ? Mq[g] - j0 : -1;
+      lo_q[g] = Mq[g] - a.slots > 0 ? Mq[g] - a.slots : 0;
+      // group rows ascending in M: lo_q and hi_q are non-decreasing
+      const int fr = base, lr = min(nrows - c0, base + 16) - 1;
+      wave_rows[g] = fr <= lr;
+      wave_full[g] = lr == base + 15;
+      w_lolo[g] = 0, w_lohi[g] = 0, w_hilo[g] = -1, w_hihi[g] = -1;
+      if (wave_rows[g]) {
+        const int Ma = cls_m[c0 + fr], Mb = cls_m[c0 + lr];
+        const int64_t ta = c + (int64_t)s * Ma, tb = c + (int64_t)s * Mb;
+        w_lolo[g] = Ma - a.slots > 0 ? Ma - a.slots : 0;
+        w_lohi[g] = Mb - a.slots > 0 ? Mb - a.slots : 0;
+        w_hilo[g] = Ma - ((int)((ta - win_lo(ta, a.local_w)) / s) + 1);
+        w_hihi[g] = Mb - ((int)((tb - win_lo(tb, a.local_w)) / s) + 1);
+      }
     }
     // key range of the chunk (lo/hi are non-decreasing in M)
-    const int last = min(nrows, c0 + kRows) - 1;
+    const int last = min(nrows, c0 + kChunk) - 1;
     const int64_t Mf = cls_m[c0], Ml = cls_m[last];
     const int64_t mlo = Mf - a.slots > 0 ? Mf - a.slots : 0;
     const int64_t tl = c + (int64_t)s * Ml;
@@ -587,11 +602,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
 #pragma unroll
     for (int i = 0; i < S - 1; ++i)
       if (i < ntile) request(i);
-    bf16x8_t qf[2];
-    load_q_row(a, qb, tq, qf);
-    asm volatile("" : "+v"(qf[0]), "+v"(qf[1]));  // no load left for the tile loop to wait on
-    QState st;
-    init_state(st);
+    bf16x8_t qf[NG][2];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      load_q_row(a, qb, tq[g], qf[g]);
+      asm volatile("" : "+v"(qf[g][0]), "+v"(qf[g][1]));  // no load left for the tile loop to wait on
+    }
+    QState st[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) init_state(st[g]);
     for (int i = 0; i < ntile; ++i) {
       if (S == 3 && i + 1 < ntile)
         dma_wait_barrier<kDmaPerTile>();
@@ -599,30 +618,36 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
         dma_wait_barrier<0>();
       if (i + S - 1 < ntile) request(i + S - 1);
       const int m0 = (int)mlo + kTile * i;
-      const bool empty = !wave_rows || m0 > w_hihi || m0 + kTile - 1 < w_lolo;
-      if (!empty) {
-        // the row's keys m in [lo_q, min(hi_q, mhi)], tile-local
-        const bool need_lo = !wave_full || m0 < w_lohi;
-        const bool need_hi = !wave_full || m0 + kTile - 1 > min(w_hilo, (int)mhi);
-        const int lo = qv ? lo_q - m0 : kTile;
-        const int hi = min(hi_q, (int)mhi) - m0;
-        float sc[4][4];
-        int unused = 0;
-        const SwzTile tl{ring[i % S], L};
-        window_qk<false>(qf, tl, need_lo, need_hi, lo, hi, unused, sc);
-        softmax_pv(sc, tl, sl2, st);
+      const SwzTile tl{ring[i % S], L};
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const bool empty = !wave_rows[g] || m0 > w_hihi[g] || m0 + kTile - 1 < w_lolo[g];
+        if (!empty) {
+          // the row's keys m in [lo_q, min(hi_q, mhi)], tile-local
+          const bool need_lo = !wave_full[g] || m0 < w_lohi[g];
+          const bool need_hi = !wave_full[g] || m0 + kTile - 1 > min(w_hilo[g], (int)mhi);
+          const int lo = qv[g] ? lo_q[g] - m0 : kTile;
+          const int hi = min(hi_q[g], (int)mhi) - m0;
+          float sc[4][4];
+          int unused = 0;
+          window_qk<false>(qf[g], tl, need_lo, need_hi, lo, hi, unused, sc);
+          softmax_pv(sc, tl, sl2, st[g]);
+        }
       }
     }
-    float lt = st.l;
-    lt += __shfl_xor(lt, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
-    if (qv) {
-      float* pr = a.part + (int64_t)rq * kPartW;
-      const int g = lane >> 4;
-      if (g == 0) { pr[0] = st.m; pr[1] = lt; }
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-        *reinterpret_cast<f32x4_t*>(pr + 4 + 16 * db + 4 * g) = st.acc[db];
+    for (int g = 0; g < NG; ++g) {
+      float lt = st[g].l;
+      lt += __shfl_xor(lt, 16, 64);
+      lt += __shfl_xor(lt, 32, 64);
+      if (qv[g]) {
+        float* pr = a.part + (int64_t)rq[g] * kPartW;
+        const int gq = lane >> 4;
+        if (gq == 0) { pr[0] = st[g].m; pr[1] = lt; }
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          *reinterpret_cast<f32x4_t*>(pr + 4 + 16 * db + 4 * gq) = st[g].acc[db];
+      }
     }
     // every wave is done with the ring before the next chunk's requests
     __syncthreads();
@@ -1100,7 +1125,10 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
     // kClassChunk (longer classes are attended in rounds)
     const int64_t npos = ((T - 1) / anchor_stride + 1 + 255) / 256 * 256;
     const int ccap = (int)(npos < kClassChunk ? npos : kClassChunk);
-    short_anchor_kernel<<<grid, 256, (size_t)ccap * 8 + 16, s>>>(a, ccap);
+    if (npos >= kAnchorNG2Positions)
+      short_anchor_kernel<2><<<grid, 256, (size_t)ccap * 8 + 16, s>>>(a, ccap);
+    else
+      short_anchor_kernel<1><<<grid, 256, (size_t)ccap * 8 + 16, s>>>(a, ccap);
     PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
   }
   if (!(passes & 2) || N == 0) return PFA_OK;
