@@ -460,7 +460,7 @@ constexpr int kAnchorStages = 2;
 // Row groups per wave: NG = 2 (32 rows per wave, 128 per chunk) for long
 // residue classes, whose chunks each stream long key bands: the tile
 // transfers and barriers are then shared by twice the rows.
-constexpr int kAnchorNG2Positions = 1024;  // class positions from which NG = 2 is launched
+constexpr int kAnchorNG2Positions = 256;  // class positions from which NG = 2 is launched
 template <int NG>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) short_anchor_kernel(ShortArgs a,
                                                                                                      int ccap) {
