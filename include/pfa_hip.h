@@ -333,7 +333,9 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                         const float* v_scale, void* stream);
 
 /* ====================================================================
- * Shortlist attention without materialised candidates (bf16, D = 64).
+ * Shortlist attention without materialised candidates (bf16, D = 16, 32
+ * or 64; q_rope_cos / q_rope_sin and the fused variant's fuse bits need
+ * D = 64).
  * Same result as pfa_shortlist_build followed by pfa_sparse_attn_fwd for the
  * module's packed rows when no row is truncated (local_w + anchors below the
  * window + proto_k + 1 <= L, checked by the caller): each row attends to its

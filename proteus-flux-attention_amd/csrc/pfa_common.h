@@ -297,11 +297,15 @@ struct SwzTile {
 // V: four 16-byte transfers, each wave filling 1 KB runs of chunk slots.
 // lds_w is the tile's LDS byte address plus 1 KB per wave index
 // (wave-uniform); kb/vb are bf16 rows with token strides ks_t/vs_t.
+// cmask (D/8 - 1 for rows of D <= 64 elements, a power of two): the chunk
+// slots of logical chunks past D/8 receive source chunk (c & cmask), a
+// finite copy of the row's own data that a zero q chunk cancels.
 constexpr int kDmaPerTile = 4;
 __device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb,
-                                         uint32_t ks_t, uint32_t vs_t, int key0, int key1, uint32_t lds_w) {
+                                         uint32_t ks_t, uint32_t vs_t, int key0, int key1, uint32_t lds_w,
+                                         uint32_t cmask = 7u) {
   const int tid = threadIdx.x;
-  const int c = 8 * ((tid & 7) ^ tile_swz(tid >> 3));  // rows tid/8 and tid/8 + 32 share the swizzle
+  const int c = 8 * (int)((uint32_t)((tid & 7) ^ tile_swz(tid >> 3)) & cmask);  // rows tid/8, tid/8 + 32: one swizzle
   // element offsets: one 32 x 32 -> 64-bit multiply each (keys and row
   // strides are below 2^31)
   const uint64_t k0 = (uint64_t)(uint32_t)key0 * ks_t, k1 = (uint64_t)(uint32_t)key1 * ks_t;

@@ -86,6 +86,11 @@ struct ShortArgs {
   const float* vsc;
   // work the anchor pass takes over from separate passes (kFuse* bits)
   int fuse;
+  // head dim D (16, 32 or 64) and cmask = D/8 - 1: rows narrower than 64
+  // are attended as 64-wide rows whose q dims past D are zero (their K/V
+  // tile chunks hold copies of the row's own chunks, see dma_tile)
+  int dh;
+  uint32_t cmask;
   __device__ __forceinline__ float head_scale_log2(int bh) const {
     return qsc ? scale_log2 * (qsc[bh] * ksc[bh]) : scale_log2;
   }
@@ -321,11 +326,14 @@ __device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, floa
   __builtin_amdgcn_s_setprio(0);
 }
 
-__device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[2]) {
+// The lane's q chunks 4dc + g (dims 32dc + 8g ..+7); chunks past cmask (a
+// row narrower than 64) are zero.
+__device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[2], uint32_t cmask) {
   const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
   for (int dc = 0; dc < 2; ++dc) {
-    uint4 w = *reinterpret_cast<const uint4*>(qrow + 32 * dc + 8 * g);
+    uint4 w = make_uint4(0u, 0u, 0u, 0u);
+    if ((uint32_t)(4 * dc + g) <= cmask) w = *reinterpret_cast<const uint4*>(qrow + 32 * dc + 8 * g);
     __builtin_memcpy(&qf[dc], &w, 16);
   }
 }
@@ -352,20 +360,21 @@ __device__ __forceinline__ void load_q_rope(const uint16_t* qrow, const uint16_t
   }
 }
 
-__device__ __forceinline__ void load_q_row(const ShortArgs& a, const uint16_t* qb, int64_t t, bf16x8_t (&qf)[2]) {
+__device__ __forceinline__ void load_q_row(const ShortArgs& a, const uint16_t* qb, int64_t t, bf16x8_t (&qf)[2],
+                                           uint32_t cmask) {
   if (a.rcos != nullptr)
     load_q_rope(qb + t * a.q.s_t, a.rcos + t * 64, a.rsin + t * 64, qf);
   else
-    load_q(qb + t * a.q.s_t, qf);
+    load_q(qb + t * a.q.s_t, qf, cmask);
 }
 
 // dma_tile from wave-uniform K/V bases with 32-bit byte offsets per lane
 // (the caller checks that every offset of the sequence fits in 32 bits):
 // no 64-bit address arithmetic per tile.
 __device__ __forceinline__ void dma_tile32(const uint16_t* kb, const uint16_t* vb, uint32_t ks_t, uint32_t vs_t,
-                                           int key0, int key1, uint32_t lds_w) {
+                                           int key0, int key1, uint32_t lds_w, uint32_t cmask) {
   const int tid = threadIdx.x;
-  const uint32_t c = 2u * 8u * (uint32_t)((tid & 7) ^ tile_swz(tid >> 3));
+  const uint32_t c = 2u * 8u * ((uint32_t)((tid & 7) ^ tile_swz(tid >> 3)) & cmask);
   const uint32_t k2 = 2u * ks_t, v2 = 2u * vs_t;
   lds_dma16_s(kb, (uint32_t)key0 * k2 + c, lds_w);
   lds_dma16_s(kb, (uint32_t)key1 * k2 + c, lds_w + 4096);
@@ -461,9 +470,11 @@ constexpr int kAnchorStages = 2;
 // residue classes, whose chunks each stream long key bands: the tile
 // transfers and barriers are then shared by twice the rows.
 constexpr int kAnchorNG2Positions = 256;  // class positions from which NG = 2 is launched
-template <int NG>
+// NARROW: rows of D = 16 or 32 elements (a.cmask); otherwise D = 64.
+template <int NG, bool NARROW>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) short_anchor_kernel(ShortArgs a,
                                                                                                      int ccap) {
+  const uint32_t cm = NARROW ? a.cmask : 7u;
   constexpr int S = kAnchorStages;
   __shared__ __align__(16) uint16_t ring[S][2 * kTileElems];
   // active rows of the class, compacted ccap at a time (a multiple of 256,
@@ -595,9 +606,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
       const int m0 = (int)mlo + kTile * i;
       const int ka = c + s * min(m0 + drow, (int)mhi), kz = c + s * min(m0 + drow + 32, (int)mhi);
       if (a.off32)
-        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S));
+        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S),
+                   cm);
       else
-        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S));
+        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S),
+                 cm);
     };
 #pragma unroll
     for (int i = 0; i < S - 1; ++i)
@@ -605,7 +618,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
     bf16x8_t qf[NG][2];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      load_q_row(a, qb, tq[g], qf[g]);
+      load_q_row(a, qb, tq[g], qf[g], cm);
       asm volatile("" : "+v"(qf[g][0]), "+v"(qf[g][1]));  // no load left for the tile loop to wait on
     }
     QState st[NG];
@@ -681,9 +694,10 @@ struct MainOcc<3> {
   static constexpr int kWaves = 3;
 };
 
-template <bool COUNT, int S>
+template <bool COUNT, int S, bool NARROW>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MainOcc<S>::kWaves, 8)))
 short_main_kernel(ShortArgs a, int use_part, int pcap) {
+  const uint32_t cm = NARROW ? a.cmask : 7u;  // NARROW: rows of D = 16 or 32 elements
   constexpr int kSlots = 16;  // tile slots of the shared window-tile schedule
   __shared__ __align__(16) uint16_t ring[S][2 * kTileElems];
   __shared__ int32_t r_t[kRows];
@@ -778,9 +792,9 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     {
       const int ka = min(kTile * k_slot0 + drow, t_last), kz = min(kTile * k_slot0 + drow + 32, t_last);
       if (a.off32)
-        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w);
+        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w, cm);
       else
-        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w);
+        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w, cm);
     }
     const bool qv = qs >= s0 && qs < s1;
     const int tq = qv ? r_t[qs] : t_first;
@@ -921,16 +935,18 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     auto request = [&](int i) {
       const int ka = key_of(i, drow), kz = key_of(i, drow + 32);
       if (a.off32)
-        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S));
+        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S),
+                   cm);
       else
-        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S));
+        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S),
+                 cm);
     };
     if (!early) request(0);
 #pragma unroll
     for (int i = 1; i < S - 1; ++i)
       if (i < ntile) request(i);
     bf16x8_t qf[2];
-    load_q_row(a, qb, tq, qf);
+    load_q_row(a, qb, tq, qf, cm);
     // settle the q fragments here: the tile loop then holds no load the
     // compiler would wait for (its wait would also drain the tile requests)
     asm volatile("" : "+v"(qf[0]), "+v"(qf[1]));
@@ -1031,6 +1047,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
       uint16_t* op = (uint16_t*)a.out.ptr + bb * a.out.s_b + hh * a.out.s_h + (int64_t)tq * a.out.s_t;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
+        if (NARROW && 16 * db + 4 * g >= a.dh) break;  // dims past D
         uint16_t o4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) o4[i] = f32_to_bf16((st.acc[db][i] * fa + pacc[db][i] * fb) * inv);
@@ -1066,8 +1083,11 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
                               float* partials, int32_t* lengths, const void* q_rope_cos, const void* q_rope_sin,
                               const float* q_scale, const float* k_scale, const float* v_scale, int passes,
                               int fuse, void* stream) {
-  PFA_CHECK_ARG(dtype == PFA_BF16 && D == 64, "pfa_shortlist_attn_fwd: bf16 and D=64 only (got dtype %d D %d)", dtype,
-                D);
+  PFA_CHECK_ARG(dtype == PFA_BF16 && (D == 16 || D == 32 || D == 64),
+                "pfa_shortlist_attn_fwd: bf16 with D = 16, 32 or 64 only (got dtype %d D %d)", dtype, D);
+  // the q RoPE tables and the anchor-pass fusions work on 64-wide rows
+  PFA_CHECK_ARG(D == 64 || (q_rope_cos == nullptr && fuse == 0),
+                "pfa_shortlist_attn_fwd: q RoPE on load and the anchor-pass fusions need D=64 (got D %d)", D);
   PFA_CHECK_ARG(H > 0 && T > 0 && T < INT32_MAX && N >= 0 && P_cap > 0 && local_w >= 1,
                 "pfa_shortlist_attn_fwd: bad sizes");
   PFA_CHECK_ARG(passes >= 1 && passes <= 3, "pfa_shortlist_attn_fwd: passes must be 1, 2 or 3 (got %d)", passes);
@@ -1118,6 +1138,8 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
   }
   a.qsc = q_scale; a.ksc = k_scale; a.vsc = v_scale;
   a.fuse = fuse;
+  a.dh = D;
+  a.cmask = (uint32_t)(D / 8 - 1);
   hipStream_t s = as_stream(stream);
   if (anchors && (passes & 1)) {
     dim3 grid((unsigned)((int64_t)anchor_stride < T ? (int64_t)anchor_stride : T), (unsigned)P_cap);
@@ -1125,10 +1147,15 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
     // kClassChunk (longer classes are attended in rounds)
     const int64_t npos = ((T - 1) / anchor_stride + 1 + 255) / 256 * 256;
     const int ccap = (int)(npos < kClassChunk ? npos : kClassChunk);
-    if (npos >= kAnchorNG2Positions)
-      short_anchor_kernel<2><<<grid, 256, (size_t)ccap * 8 + 16, s>>>(a, ccap);
-    else
-      short_anchor_kernel<1><<<grid, 256, (size_t)ccap * 8 + 16, s>>>(a, ccap);
+    const size_t lds = (size_t)ccap * 8 + 16;
+    const bool ng2 = npos >= kAnchorNG2Positions;
+    if (D == 64) {
+      if (ng2) short_anchor_kernel<2, false><<<grid, 256, lds, s>>>(a, ccap);
+      else short_anchor_kernel<1, false><<<grid, 256, lds, s>>>(a, ccap);
+    } else {
+      if (ng2) short_anchor_kernel<2, true><<<grid, 256, lds, s>>>(a, ccap);
+      else short_anchor_kernel<1, true><<<grid, 256, lds, s>>>(a, ccap);
+    }
     PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
   }
   if (!(passes & 2) || N == 0) return PFA_OK;
@@ -1145,10 +1172,14 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
   const int64_t wspan = (int64_t)2 * local_w < T ? (int64_t)2 * local_w : T;
   const int ordcap = (int)((wspan + kTile - 1) / kTile) + 2 + pcap / kTile;
   const size_t dyn = (size_t)pcap * 12 + (size_t)ordcap * 4;
-  if (lengths != nullptr)
-    short_main_kernel<true, S><<<(unsigned)blocks, 256, dyn, s>>>(a, anchors ? 1 : 0, pcap);
-  else
-    short_main_kernel<false, S><<<(unsigned)blocks, 256, dyn, s>>>(a, anchors ? 1 : 0, pcap);
+  const int up = anchors ? 1 : 0;
+  if (D == 64) {
+    if (lengths != nullptr) short_main_kernel<true, S, false><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+    else short_main_kernel<false, S, false><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+  } else {
+    if (lengths != nullptr) short_main_kernel<true, S, true><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+    else short_main_kernel<false, S, true><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+  }
   PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/main");
   return PFA_OK;
 }

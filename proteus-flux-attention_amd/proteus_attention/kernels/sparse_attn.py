@@ -448,6 +448,8 @@ def _shortlist_attn_structured(
         if evict is None or int(evict.size(1)) != int(T) or int(blocks.size(1)) != (int(T) + 63) // 64:
             raise ValueError("prototype block tables must cover the T tokens of the sequence")
     rc_cos = rc_sin = None
+    if (q_rope is not None or fuse) and int(D) != 64:
+        raise ValueError("q RoPE on load and the anchor-pass fusions need D = 64")
     if q_rope is not None:
         rc_cos, rc_sin = q_rope
         if (rc_cos.dtype != torch.bfloat16 or rc_sin.dtype != torch.bfloat16 or tuple(rc_cos.shape) != (int(T), 64)
@@ -478,9 +480,15 @@ def _shortlist_attn_structured(
     return lengths
 
 
+# Head dims of the structured MFMA kernel: rows of 16 or 32 elements are
+# attended as 64-wide rows whose q dims past D are zero.
+STRUCTURED_HEAD_DIMS = (16, 32, 64)
+
+
 def _mfma_causal_ok(dtype: torch.dtype, D: int, *t4s: "_hip.Tensor4") -> bool:
-    """The structured MFMA kernel serves bf16, D = 64, 16-byte aligned rows."""
-    if dtype != torch.bfloat16 or D != 64:
+    """The structured MFMA kernel serves bf16, D in STRUCTURED_HEAD_DIMS,
+    16-byte aligned rows."""
+    if dtype != torch.bfloat16 or D not in STRUCTURED_HEAD_DIMS:
         return False
     for t in t4s:
         if int(t.ptr or 0) % 16 or t.s_b % 8 or t.s_h % 8 or t.s_t % 8 or t.s_t <= 0 or t.s_t >= 2 ** 31:

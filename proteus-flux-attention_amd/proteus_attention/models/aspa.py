@@ -1508,7 +1508,7 @@ class AdaptiveSparseAttention(nn.Module):
         # and fuse_anchor_pass its anchor pass (on the forked stream) writes
         # the zeros of the rows without a packed row (no zero fill) and, with
         # fuse_k_rope, rotates k as well (no RoPE pass).
-        q_fused = structured and self.fuse_q_rope and not use_quant
+        q_fused = structured and self.fuse_q_rope and not use_quant and self.d_head == 64
         fuse = 0
         if q_fused and self.fuse_anchor_pass and plan["stride"] > 0 and plan["slots"] > 0:
             fuse = _sa.FUSE_ZERO | (_sa.FUSE_K_ROPE if (self.use_rope and self.fuse_k_rope) else 0)
@@ -1639,7 +1639,7 @@ class AdaptiveSparseAttention(nn.Module):
         anchors = stride > 0 and slots > 0
         w_eff = max(1, local_w)
         bound = w_eff + ((min(slots, (T - 1) // stride) + 1) if anchors else 0) + K
-        structured = (dtype == torch.bfloat16 and D == 64 and bound <= L and K <= 1024
+        structured = (dtype == torch.bfloat16 and D in _sa.STRUCTURED_HEAD_DIMS and bound <= L and K <= 1024
                       and not _hip.env_flag("PFA_FORCE_GENERIC"))
         return {"L": L, "stride": stride, "local_w": local_w, "slots": slots, "K": K, "use_quant": use_quant,
                 "w_eff": w_eff, "structured": structured}

@@ -255,20 +255,25 @@ def test_proto_prefix_sets_large_vs_c_oracle(dev):
         assert u == exp[r].tolist(), t
 
 
-@pytest.mark.parametrize("T,L,w,s,B,outlier", [(4096, 1024, 256, 64, 1, 0.01), (3000, 700, 100, 37, 2, 0.0),
-                                               (65536, 2048, 512, 256, 1, 0.01), (524288, 4096, 512, 256, 1, 0.0),
-                                               (65536, 2048, 512, 4, 1, 0.01), (20000, 1024, 128, 3, 2, 0.0)])
-def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, monkeypatch):
+@pytest.mark.parametrize("T,L,w,s,B,outlier,H", [(4096, 1024, 256, 64, 1, 0.01, 8), (3000, 700, 100, 37, 2, 0.0, 8),
+                                                 (65536, 2048, 512, 256, 1, 0.01, 8),
+                                                 (524288, 4096, 512, 256, 1, 0.0, 8),
+                                                 (65536, 2048, 512, 4, 1, 0.01, 8), (20000, 1024, 128, 3, 2, 0.0, 8),
+                                                 (4096, 1024, 256, 64, 1, 0.01, 32), (3000, 700, 100, 37, 2, 0.0, 16),
+                                                 (65536, 2048, 512, 256, 1, 0.01, 16)])
+def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, H, monkeypatch):
     """The structure-driven MFMA path and the builder + gather path give the
     same candidate counts per row and the same outputs (bf16 tolerance).
     The T=524,288 case is config 4 at full size, single pass: the
     materialised path holds all 1,048,576 x 4,096 int32 candidates.  The
     stride-4 and stride-3 cases have residue classes of 16,384 and 6,667
-    positions, whose rows the anchor pass compacts and attends in rounds."""
+    positions, whose rows the anchor pass compacts and attends in rounds.
+    H = 32 and 16 over d_model 512 give heads of 16 and 32 dims (q rotated
+    by the RoPE pass, not on load)."""
     from configs import shortlist_cfg
 
-    _say(f"structured vs materialised T={T} L={L} w={w} s={s} B={B}")
-    cfg = shortlist_cfg(T, 512, 8, L, w, s)
+    _say(f"structured vs materialised T={T} L={L} w={w} s={s} B={B} H={H}")
+    cfg = shortlist_cfg(T, 512, H, L, w, s)
     m, x = _module(cfg, B, T, 512, torch.bfloat16, dev, outlier)
     m.record_shortlist_lengths = True
     snap = {n: b.detach().clone() for n, b in m.named_buffers() if n.startswith("routing_")}
@@ -1402,17 +1407,18 @@ def test_dropin_mha_fallbacks_match_torch(dev):
 # the operator's implicit-causal branch)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("BH,T,p", [(8, 8192, 1.0), (6, 3001, 0.35), (3, 65, 1.0)])
-def test_operator_causal_branch_mfma_vs_oracle(dev, BH, T, p):
+@pytest.mark.parametrize("BH,T,p,D", [(8, 8192, 1.0, 64), (6, 3001, 0.35, 64), (3, 65, 1.0, 64),
+                                       (5, 3001, 0.5, 16), (4, 2049, 0.7, 32), (2, 40, 1.0, 16)])
+def test_operator_causal_branch_mfma_vs_oracle(dev, BH, T, p, D):
     """aspa_sparse_attention without candidates or mask (each active row
-    attends to keys 0..t, sparse_attn.py:1016-1043) in bf16, D = 64, runs
-    the MFMA causal tiles; every active row against f32 causal attention,
-    inactive rows zero."""
+    attends to keys 0..t, sparse_attn.py:1016-1043) in bf16, D = 16, 32 or
+    64, runs the MFMA causal tiles; every active row against f32 causal
+    attention, inactive rows zero."""
     from proteus_attention.kernels.sparse_attn import aspa_sparse_attention, get_last_backend_info
 
-    _say(f"operator causal mfma BH={BH} T={T} p={p}")
+    _say(f"operator causal mfma BH={BH} T={T} p={p} D={D}")
     g = torch.Generator().manual_seed(T + BH)
-    q, k, v = (torch.randn(BH, T, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+    q, k, v = (torch.randn(BH, T, D, generator=g).to(torch.bfloat16) for _ in range(3))
     mask = torch.rand(BH, T, generator=g) < p
     out = aspa_sparse_attention(q.to(dev), k.to(dev), v.to(dev), active_mask=mask.to(dev))
     info = get_last_backend_info()
