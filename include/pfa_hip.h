@@ -333,8 +333,8 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                         const float* v_scale, void* stream);
 
 /* ====================================================================
- * Shortlist attention without materialised candidates (bf16, D = 16, 32
- * or 64; q_rope_cos / q_rope_sin and the fused variant's fuse bits need
+ * Shortlist attention without materialised candidates (bf16, D = 16, 32,
+ * 64 or 128; q_rope_cos / q_rope_sin and the fused variant's fuse bits need
  * D = 64).
  * Same result as pfa_shortlist_build followed by pfa_sparse_attn_fwd for the
  * module's packed rows when no row is truncated (local_w + anchors below the
@@ -348,7 +348,8 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
  * (aspa.py:1269-1302).
  *   row_of (B*H, T) from pfa_pack_rows; summary from pfa_pack_rows ({P,...});
  *   head_map (P_cap) compact -> b*H+h; partials (N, pfa_shortlist_attn_part_
- *   floats()) f32 scratch for the anchor pass; lengths (N) int32 or NULL
+ *   floats_for(D)) f32 scratch for the anchor pass (pfa_shortlist_attn_part_
+ *   floats() is the width for D <= 64); lengths (N) int32 or NULL
  *   receives each row's candidate count (the builder's lengths).
  *   q_rope_cos / q_rope_sin: NULL, or the bf16 (T, 64) RoPE tables of
  *   pfa_rope_qk_inplace; q rows are then rotated as they are loaded (the
@@ -370,6 +371,7 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
  *   1538-1541 applied inside the tile.  All three or none.
  * ==================================================================== */
 int pfa_shortlist_attn_part_floats(void);
+int pfa_shortlist_attn_part_floats_for(int head_dim);
 int pfa_shortlist_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
                            pfa_tensor4 out, int dtype, int H, int64_t T, int D,
                            const int32_t* token_idx, const int32_t* row_head,

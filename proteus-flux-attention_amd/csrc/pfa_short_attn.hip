@@ -41,7 +41,9 @@ namespace pfa {
 
 constexpr int kRows = 64;   // query rows per workgroup
 constexpr int kTile = 64;   // keys per tile
-constexpr int kPartW = 68;  // floats per partial row: m, l, pad, pad, acc[64]
+// floats per partial row: m, l, pad, pad, acc[64 * NH] (NH 64-dim halves)
+__host__ __device__ constexpr int part_w(int NH) { return 4 + 64 * NH; }
+constexpr int kPartW = part_w(1);
 constexpr int kMaxProto = 1024;
 constexpr int kClassChunk = 2048;  // anchor pass: class rows compacted per round
 constexpr float kRescaleLog2 = 0.0f;  // rescale only when some row's max rises
@@ -72,7 +74,7 @@ struct ShortArgs {
   const int32_t* evict;  // (B, T) or null
   const int32_t* row_of; // (B*H, T)
   const int32_t* summary;
-  float* part;           // (N, kPartW)
+  float* part;           // (N, part_w(NH))
   int32_t* lengths;      // (N) or null
   const uint16_t* rcos;  // (T, 64) RoPE tables applied to q rows on load, or null
   const uint16_t* rsin;
@@ -97,10 +99,29 @@ struct ShortArgs {
   __device__ __forceinline__ float head_out_scale(int bh) const { return vsc ? vsc[bh] : 1.f; }
 };
 
+// NH: 64-dim halves of the head (1, or 2 for D = 128); acc[4 * NH] holds
+// the lane's output dims 16db + 4g .. +3.
+template <int NH>
 struct QState {
   float m, l;
-  f32x4_t acc[4];
+  f32x4_t acc[4 * NH];
   int cnt;
+};
+
+// K/V tile of 64 keys and NH 64-dim halves in LDS: the K halves at base +
+// h * kSwzTileElems, then the V halves, each a swizzled 64 x 64 tile
+// (SwzTile's layout); kfrag / vtr as SwzTile's, with dc < 2 * NH and
+// db < 4 * NH.
+template <int NH>
+struct SwzTileH {
+  const uint16_t* base;
+  const SwzLane& L;
+  __device__ __forceinline__ const uint16_t* kfrag(int kb, int dc) const {
+    return base + (dc >> 1) * kSwzTileElems + 1024 * kb + L.ko[dc & 1];
+  }
+  __device__ __forceinline__ const uint16_t* vtr(int kc, int h, int db) const {
+    return base + (NH + (db >> 2)) * kSwzTileElems + 64 * (32 * kc + 16 * h) + L.vo[db & 3];
+  }
 };
 
 __device__ __forceinline__ int64_t win_lo(int64_t t, int w) {
@@ -138,12 +159,12 @@ constexpr int kTileElems = kSwzTileElems;  // one unpadded K or V tile, bf16 ele
 //
 // S^T = K Q^T: s[kb][i] is the raw score of tile key 16kb + 4g + i against
 // the lane's query row (the scale is applied in the exp argument).
-template <typename Tile>
-__device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[2], const Tile& t, float (&s)[4][4]) {
-  // all eight fragment reads first, then four independent MFMA chains
-  bf16x8_t a[2][4];
+template <int NQ, typename Tile>
+__device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[NQ], const Tile& t, float (&s)[4][4]) {
+  // all the fragment reads first, then four independent MFMA chains
+  bf16x8_t a[NQ][4];
 #pragma unroll
-  for (int dc = 0; dc < 2; ++dc)
+  for (int dc = 0; dc < NQ; ++dc)
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) a[dc][kb] = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, dc));
   f32x4_t c[4];
@@ -152,7 +173,9 @@ __device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[2], const Tile& t, 
   for (int kb = 0; kb < 4; ++kb)
     c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0][kb], qf[0], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1][kb], qf[1], c[kb], 0, 0, 0);
+  for (int dc = 1; dc < NQ; ++dc)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[dc][kb], qf[dc], c[kb], 0, 0, 0);
   __builtin_amdgcn_s_setprio(0);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
@@ -165,12 +188,12 @@ __device__ __forceinline__ void qk_tile(const bf16x8_t (&qf)[2], const Tile& t, 
 // MFMA's C operand, so a masked tile needs no select after the product.
 // For finite q and k the scores are those of qk_tile with -inf in the
 // masked places.
-template <typename Tile>
-__device__ __forceinline__ void qk_tile_b(const bf16x8_t (&qf)[2], const Tile& t, const f32x4_t (&bias)[4],
+template <int NQ, typename Tile>
+__device__ __forceinline__ void qk_tile_b(const bf16x8_t (&qf)[NQ], const Tile& t, const f32x4_t (&bias)[4],
                                           float (&s)[4][4]) {
-  bf16x8_t a[2][4];
+  bf16x8_t a[NQ][4];
 #pragma unroll
-  for (int dc = 0; dc < 2; ++dc)
+  for (int dc = 0; dc < NQ; ++dc)
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) a[dc][kb] = *reinterpret_cast<const bf16x8_t*>(t.kfrag(kb, dc));
   f32x4_t c[4];
@@ -178,7 +201,9 @@ __device__ __forceinline__ void qk_tile_b(const bf16x8_t (&qf)[2], const Tile& t
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0][kb], qf[0], bias[kb], 0, 0, 0);
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1][kb], qf[1], c[kb], 0, 0, 0);
+  for (int dc = 1; dc < NQ; ++dc)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[dc][kb], qf[dc], c[kb], 0, 0, 0);
   __builtin_amdgcn_s_setprio(0);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
@@ -219,8 +244,8 @@ __device__ __forceinline__ int count_finite(const float (&s)[4][4]) {
 // [lo, hi] (tile-local, lo > hi for none); need_lo / need_hi say whether
 // some row of the wave is cut by that bound in this tile.  Uncut tiles take
 // the plain product.
-template <bool COUNT, typename Tile>
-__device__ __forceinline__ void window_qk(const bf16x8_t (&qf)[2], const Tile& t, bool need_lo, bool need_hi, int lo,
+template <bool COUNT, int NQ, typename Tile>
+__device__ __forceinline__ void window_qk(const bf16x8_t (&qf)[NQ], const Tile& t, bool need_lo, bool need_hi, int lo,
                                           int hi, int& cnt, float (&s)[4][4]) {
   const int g4 = 4 * ((threadIdx.x & 63) >> 4);
   // the conditions are wave-uniform: scalar branches
@@ -244,7 +269,8 @@ __device__ __forceinline__ void window_qk(const bf16x8_t (&qf)[2], const Tile& t
 // the max rises) and returns P rounded to bf16 (v_cvt_pk_bf16_f32, round to
 // nearest even) as the two B operands of the P.V product, pb[kc] holding
 // keys 32kc + 4g + (0..3) and 32kc + 16 + 4g + (0..3).
-__device__ __forceinline__ void softmax_p(float (&s)[4][4], float scale_log2, QState& st, bf16x8_t (&pb)[2]) {
+template <int NH>
+__device__ __forceinline__ void softmax_p(float (&s)[4][4], float scale_log2, QState<NH>& st, bf16x8_t (&pb)[2]) {
   float tmax = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
@@ -261,7 +287,7 @@ __device__ __forceinline__ void softmax_p(float (&s)[4][4], float scale_log2, QS
     const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(st.m - mn);  // st.m == -inf -> 0
     st.l *= alpha;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4 * NH; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i) st.acc[db][i] *= alpha;
     st.m = mn;
@@ -308,8 +334,10 @@ __device__ __forceinline__ bf16x8_t v_frag(const Tile& t, int kc, int db) {
 // The sixteen transpose reads of V^T are issued before the softmax, so
 // their latency overlaps the exponentials instead of sitting between the
 // P.V products.
-template <typename Tile>
-__device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, float scale_log2, QState& st) {
+// With two 64-dim halves the second half's V^T reads follow the first
+// half's products (the registers of one half's operands at a time).
+template <int NH, typename Tile>
+__device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, float scale_log2, QState<NH>& st) {
   bf16x8_t va[2][4];
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc)
@@ -317,23 +345,33 @@ __device__ __forceinline__ void softmax_pv(float (&s)[4][4], const Tile& t, floa
     for (int db = 0; db < 4; ++db) va[kc][db] = v_frag(t, kc, db);
   bf16x8_t pb[2];
   softmax_p(s, scale_log2, st, pb);
-  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-  for (int kc = 0; kc < 2; ++kc)
+  for (int h = 0; h < NH; ++h) {
+    if (h > 0) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-      st.acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[kc][db], pb[kc], st.acc[db], 0, 0, 0);
-  __builtin_amdgcn_s_setprio(0);
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) va[kc][db] = v_frag(t, kc, 4 * h + db);
+    }
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        st.acc[4 * h + db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[kc][db], pb[kc], st.acc[4 * h + db], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
+  }
 }
 
-// The lane's q chunks 4dc + g (dims 32dc + 8g ..+7); chunks past cmask (a
-// row narrower than 64) are zero.
-__device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[2], uint32_t cmask) {
+// The lane's q chunks 4dc + g (dims 32dc + 8g ..+7); with NARROW the
+// chunks past cmask (a row of 16 or 32 dims) are zero.
+template <int NQ, bool NARROW>
+__device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[NQ], uint32_t cmask) {
   const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
-  for (int dc = 0; dc < 2; ++dc) {
+  for (int dc = 0; dc < NQ; ++dc) {
     uint4 w = make_uint4(0u, 0u, 0u, 0u);
-    if ((uint32_t)(4 * dc + g) <= cmask) w = *reinterpret_cast<const uint4*>(qrow + 32 * dc + 8 * g);
+    if (!NARROW || (uint32_t)(4 * dc + g) <= cmask) w = *reinterpret_cast<const uint4*>(qrow + 32 * dc + 8 * g);
     __builtin_memcpy(&qf[dc], &w, 16);
   }
 }
@@ -360,34 +398,74 @@ __device__ __forceinline__ void load_q_rope(const uint16_t* qrow, const uint16_t
   }
 }
 
-__device__ __forceinline__ void load_q_row(const ShortArgs& a, const uint16_t* qb, int64_t t, bf16x8_t (&qf)[2],
-                                           uint32_t cmask) {
-  if (a.rcos != nullptr)
-    load_q_rope(qb + t * a.q.s_t, a.rcos + t * 64, a.rsin + t * 64, qf);
-  else
-    load_q(qb + t * a.q.s_t, qf, cmask);
+// NARROW: a row of 16 or 32 dims (a.cmask); otherwise 32 * NQ dims.  The
+// RoPE tables on load are for 64-dim rows (NQ = 2, checked by the host).
+template <int NQ, bool NARROW>
+__device__ __forceinline__ void load_q_row(const ShortArgs& a, const uint16_t* qb, int64_t t, bf16x8_t (&qf)[NQ]) {
+  if constexpr (NQ == 2) {
+    if (a.rcos != nullptr) {
+      load_q_rope(qb + t * a.q.s_t, a.rcos + t * 64, a.rsin + t * 64, qf);
+      return;
+    }
+  }
+  load_q<NQ, NARROW>(qb + t * a.q.s_t, qf, NARROW ? a.cmask : 0u);
 }
 
 // dma_tile from wave-uniform K/V bases with 32-bit byte offsets per lane
 // (the caller checks that every offset of the sequence fits in 32 bits):
 // no 64-bit address arithmetic per tile.
+// NH = 2: the second 64-dim half of each row (source + 128 bytes) fills
+// the second K and V tiles of the stage (SwzTileH's layout).
+template <int NH>
 __device__ __forceinline__ void dma_tile32(const uint16_t* kb, const uint16_t* vb, uint32_t ks_t, uint32_t vs_t,
                                            int key0, int key1, uint32_t lds_w, uint32_t cmask) {
   const int tid = threadIdx.x;
   const uint32_t c = 2u * 8u * ((uint32_t)((tid & 7) ^ tile_swz(tid >> 3)) & cmask);
   const uint32_t k2 = 2u * ks_t, v2 = 2u * vs_t;
-  lds_dma16_s(kb, (uint32_t)key0 * k2 + c, lds_w);
-  lds_dma16_s(kb, (uint32_t)key1 * k2 + c, lds_w + 4096);
-  lds_dma16_s(vb, (uint32_t)key0 * v2 + c, lds_w + 2 * kSwzTileElems);
-  lds_dma16_s(vb, (uint32_t)key1 * v2 + c, lds_w + 2 * kSwzTileElems + 4096);
+  constexpr uint32_t kT = 2 * kSwzTileElems;  // bytes of one 64 x 64 tile
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    lds_dma16_s(kb, (uint32_t)key0 * k2 + c + 128u * h, lds_w + kT * h);
+    lds_dma16_s(kb, (uint32_t)key1 * k2 + c + 128u * h, lds_w + kT * h + 4096);
+  }
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    lds_dma16_s(vb, (uint32_t)key0 * v2 + c + 128u * h, lds_w + kT * (NH + h));
+    lds_dma16_s(vb, (uint32_t)key1 * v2 + c + 128u * h, lds_w + kT * (NH + h) + 4096);
+  }
+}
+// dma_tile (64-bit addresses) for NH halves.
+template <int NH>
+__device__ __forceinline__ void dma_tile_h(const uint16_t* kb, const uint16_t* vb, uint32_t ks_t, uint32_t vs_t,
+                                           int key0, int key1, uint32_t lds_w, uint32_t cmask) {
+  constexpr uint32_t kT = 2 * kSwzTileElems;
+  if constexpr (NH == 1) {
+    dma_tile(kb, vb, ks_t, vs_t, key0, key1, lds_w, cmask);
+  } else {
+    const int tid = threadIdx.x;
+    const int c = 8 * (int)((uint32_t)((tid & 7) ^ tile_swz(tid >> 3)) & cmask);
+    const uint64_t k0 = (uint64_t)(uint32_t)key0 * ks_t, k1 = (uint64_t)(uint32_t)key1 * ks_t;
+    const uint64_t v0 = (uint64_t)(uint32_t)key0 * vs_t, v1 = (uint64_t)(uint32_t)key1 * vs_t;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      lds_dma16(kb + c + 64 * h + k0, lds_w + kT * h);
+      lds_dma16(kb + c + 64 * h + k1, lds_w + kT * h + 4096);
+    }
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      lds_dma16(vb + c + 64 * h + v0, lds_w + kT * (NH + h));
+      lds_dma16(vb + c + 64 * h + v1, lds_w + kT * (NH + h) + 4096);
+    }
+  }
 }
 
-__device__ __forceinline__ void init_state(QState& st) {
+template <int NH>
+__device__ __forceinline__ void init_state(QState<NH>& st) {
   st.m = -INFINITY;
   st.l = 0.f;
   st.cnt = 0;
 #pragma unroll
-  for (int db = 0; db < 4; ++db) st.acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < 4 * NH; ++db) st.acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 }
 
 __device__ __forceinline__ int64_t xcd_block(int64_t P, int64_t nblk) {
@@ -470,13 +548,15 @@ constexpr int kAnchorStages = 2;
 // residue classes, whose chunks each stream long key bands: the tile
 // transfers and barriers are then shared by twice the rows.
 constexpr int kAnchorNG2Positions = 256;  // class positions from which NG = 2 is launched
-// NARROW: rows of D = 16 or 32 elements (a.cmask); otherwise D = 64.
-template <int NG, bool NARROW>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))) short_anchor_kernel(ShortArgs a,
-                                                                                                     int ccap) {
+// NARROW: rows of D = 16 or 32 elements (a.cmask); otherwise D = 64 * NH.
+// cm masks the tile DMA's chunk within a 64-dim half.
+template <int NG, bool NARROW, int NH>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NH == 1 ? 3 : 2, 8)))
+short_anchor_kernel(ShortArgs a, int ccap) {
   const uint32_t cm = NARROW ? a.cmask : 7u;
+  constexpr int PW = part_w(NH);
   constexpr int S = kAnchorStages;
-  __shared__ __align__(16) uint16_t ring[S][2 * kTileElems];
+  __shared__ __align__(16) uint16_t ring[S][2 * NH * kTileElems];
   // active rows of the class, compacted ccap at a time (a multiple of 256,
   // at most kClassChunk; dynamic LDS): row index and class position M
   extern __shared__ int32_t cls_dyn[];
@@ -517,7 +597,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   L.init();
   const int drow = tid >> 3;  // this thread's DMA rows: drow and drow + 32
   const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + 1024u * (uint32_t)wid);
-  constexpr uint32_t kStageBytes = 2 * kTileElems * 2;
+  constexpr uint32_t kStageBytes = 2 * NH * kTileElems * 2;
 
   const uint16_t* kb = (const uint16_t*)a.k.ptr + bb * a.k.s_b + hh * a.k.s_h;
   const uint16_t* vb = (const uint16_t*)a.v.ptr + bb * a.v.s_b + hh * a.v.s_h;
@@ -606,32 +686,34 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
       const int m0 = (int)mlo + kTile * i;
       const int ka = c + s * min(m0 + drow, (int)mhi), kz = c + s * min(m0 + drow + 32, (int)mhi);
       if (a.off32)
-        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S),
-                   cm);
+        dma_tile32<NH>(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz,
+                       ring_w + kStageBytes * (uint32_t)(i % S), cm);
       else
-        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S),
-                 cm);
+        dma_tile_h<NH>(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz,
+                       ring_w + kStageBytes * (uint32_t)(i % S), cm);
     };
 #pragma unroll
     for (int i = 0; i < S - 1; ++i)
       if (i < ntile) request(i);
-    bf16x8_t qf[NG][2];
+    bf16x8_t qf[NG][2 * NH];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      load_q_row(a, qb, tq[g], qf[g], cm);
-      asm volatile("" : "+v"(qf[g][0]), "+v"(qf[g][1]));  // no load left for the tile loop to wait on
+      load_q_row<2 * NH, NARROW>(a, qb, tq[g], qf[g]);
+#pragma unroll
+      for (int dc = 0; dc < 2 * NH; ++dc)
+        asm volatile("" : "+v"(qf[g][dc]));  // no load left for the tile loop to wait on
     }
-    QState st[NG];
+    QState<NH> st[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) init_state(st[g]);
     for (int i = 0; i < ntile; ++i) {
       if (S == 3 && i + 1 < ntile)
-        dma_wait_barrier<kDmaPerTile>();
+        dma_wait_barrier<kDmaPerTile * NH>();
       else
         dma_wait_barrier<0>();
       if (i + S - 1 < ntile) request(i + S - 1);
       const int m0 = (int)mlo + kTile * i;
-      const SwzTile tl{ring[i % S], L};
+      const SwzTileH<NH> tl{ring[i % S], L};
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         const bool empty = !wave_rows[g] || m0 > w_hihi[g] || m0 + kTile - 1 < w_lolo[g];
@@ -654,11 +736,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
       lt += __shfl_xor(lt, 16, 64);
       lt += __shfl_xor(lt, 32, 64);
       if (qv[g]) {
-        float* pr = a.part + (int64_t)rq[g] * kPartW;
+        float* pr = a.part + (int64_t)rq[g] * PW;
         const int gq = lane >> 4;
         if (gq == 0) { pr[0] = st[g].m; pr[1] = lt; }
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < 4 * NH; ++db)
           *reinterpret_cast<f32x4_t*>(pr + 4 + 16 * db + 4 * gq) = st[g].acc[db];
       }
     }
@@ -694,12 +776,15 @@ struct MainOcc<3> {
   static constexpr int kWaves = 3;
 };
 
-template <bool COUNT, int S, bool NARROW>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MainOcc<S>::kWaves, 8)))
+// NARROW: rows of D = 16 or 32 elements; otherwise D = 64 * NH (cm as in
+// the anchor pass).
+template <bool COUNT, int S, bool NARROW, int NH>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NH == 1 ? MainOcc<S>::kWaves : 2, 8)))
 short_main_kernel(ShortArgs a, int use_part, int pcap) {
-  const uint32_t cm = NARROW ? a.cmask : 7u;  // NARROW: rows of D = 16 or 32 elements
+  const uint32_t cm = NARROW ? a.cmask : 7u;
+  constexpr int PW = part_w(NH);
   constexpr int kSlots = 16;  // tile slots of the shared window-tile schedule
-  __shared__ __align__(16) uint16_t ring[S][2 * kTileElems];
+  __shared__ __align__(16) uint16_t ring[S][2 * NH * kTileElems];
   __shared__ int32_t r_t[kRows];
   __shared__ int32_t r_p[kRows];
   __shared__ int32_t seg_begin[kRows + 1];
@@ -763,7 +848,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
   const int drow = tid >> 3;  // this thread's DMA rows: drow and drow + 32
   // LDS byte address of stage 0 plus this wave's 1 KB run (wave-uniform)
   const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + 1024u * (uint32_t)wid);
-  constexpr uint32_t kStageBytes = 2 * kTileElems * 2;
+  constexpr uint32_t kStageBytes = 2 * NH * kTileElems * 2;
 
   for (int sg = 0; sg < nseg; ++sg) {
     const int s0 = seg_begin[sg], s1 = seg_begin[sg + 1];
@@ -792,9 +877,9 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     {
       const int ka = min(kTile * k_slot0 + drow, t_last), kz = min(kTile * k_slot0 + drow + 32, t_last);
       if (a.off32)
-        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w, cm);
+        dma_tile32<NH>(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w, cm);
       else
-        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w, cm);
+        dma_tile_h<NH>(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w, cm);
     }
     const bool qv = qs >= s0 && qs < s1;
     const int tq = qv ? r_t[qs] : t_first;
@@ -935,22 +1020,23 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
     auto request = [&](int i) {
       const int ka = key_of(i, drow), kz = key_of(i, drow + 32);
       if (a.off32)
-        dma_tile32(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S),
-                   cm);
+        dma_tile32<NH>(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz,
+                       ring_w + kStageBytes * (uint32_t)(i % S), cm);
       else
-        dma_tile(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz, ring_w + kStageBytes * (uint32_t)(i % S),
-                 cm);
+        dma_tile_h<NH>(kb, vb, (uint32_t)a.k.s_t, (uint32_t)a.v.s_t, ka, kz,
+                       ring_w + kStageBytes * (uint32_t)(i % S), cm);
     };
     if (!early) request(0);
 #pragma unroll
     for (int i = 1; i < S - 1; ++i)
       if (i < ntile) request(i);
-    bf16x8_t qf[2];
-    load_q_row(a, qb, tq, qf, cm);
+    bf16x8_t qf[2 * NH];
+    load_q_row<2 * NH, NARROW>(a, qb, tq, qf);
     // settle the q fragments here: the tile loop then holds no load the
     // compiler would wait for (its wait would also drain the tile requests)
-    asm volatile("" : "+v"(qf[0]), "+v"(qf[1]));
-    QState st;
+#pragma unroll
+    for (int dc = 0; dc < 2 * NH; ++dc) asm volatile("" : "+v"(qf[dc]));
+    QState<NH> st;
     init_state(st);
 
     // the rows of this wave are ascending in token: their key ranges lie in
@@ -965,11 +1051,11 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
       // tile i has landed (tiles i+1 .. i+S-2 may still be in flight) and
       // every wave is done with tile i-1, whose stage takes tile i+S-1
       if (S == 3 && i + 1 < ntile)
-        dma_wait_barrier<kDmaPerTile>();
+        dma_wait_barrier<kDmaPerTile * NH>();
       else
         dma_wait_barrier<0>();
       if (i + S - 1 < ntile) request(i + S - 1);
-      const SwzTile tl{ring[i % S], L};
+      const SwzTileH<NH> tl{ring[i % S], L};
       const int d = ord[i];
       const bool is_win = d >= 0;
       const int k0 = kTile * d;
@@ -1031,13 +1117,15 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
       const int64_t r = r0 + qs;
       float m = st.m;
       float fa = 1.f, fb = 0.f, lp = 0.f;
-      f32x4_t pacc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      f32x4_t pacc[4 * NH];
+#pragma unroll
+      for (int db = 0; db < 4 * NH; ++db) pacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       if (use_part) {
-        const float* pr = a.part + r * kPartW;
+        const float* pr = a.part + r * PW;
         const float ma = pr[0];
         lp = pr[1];
 #pragma unroll
-        for (int db = 0; db < 4; ++db) pacc[db] = *reinterpret_cast<const f32x4_t*>(pr + 4 + 16 * db + 4 * g);
+        for (int db = 0; db < 4 * NH; ++db) pacc[db] = *reinterpret_cast<const f32x4_t*>(pr + 4 + 16 * db + 4 * g);
         const float mm = fmaxf(m, ma);
         fa = (m == -INFINITY) ? 0.f : exp2f(m - mm);
         fb = (ma == -INFINITY) ? 0.f : exp2f(ma - mm);
@@ -1046,7 +1134,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
       const float inv = a.head_out_scale(bh) / den;
       uint16_t* op = (uint16_t*)a.out.ptr + bb * a.out.s_b + hh * a.out.s_h + (int64_t)tq * a.out.s_t;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
+      for (int db = 0; db < 4 * NH; ++db) {
         if (NARROW && 16 * db + 4 * g >= a.dh) break;  // dims past D
         uint16_t o4[4];
 #pragma unroll
@@ -1074,6 +1162,7 @@ short_main_kernel(ShortArgs a, int use_part, int pcap) {
 using namespace pfa;
 
 extern "C" int pfa_shortlist_attn_part_floats(void) { return kPartW; }
+extern "C" int pfa_shortlist_attn_part_floats_for(int head_dim) { return part_w(head_dim > 64 ? 2 : 1); }
 
 static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_tensor4 out, int dtype, int H,
                               int64_t T, int D, const int32_t* token_idx, const int32_t* row_head,
@@ -1083,8 +1172,8 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
                               float* partials, int32_t* lengths, const void* q_rope_cos, const void* q_rope_sin,
                               const float* q_scale, const float* k_scale, const float* v_scale, int passes,
                               int fuse, void* stream) {
-  PFA_CHECK_ARG(dtype == PFA_BF16 && (D == 16 || D == 32 || D == 64),
-                "pfa_shortlist_attn_fwd: bf16 with D = 16, 32 or 64 only (got dtype %d D %d)", dtype, D);
+  PFA_CHECK_ARG(dtype == PFA_BF16 && (D == 16 || D == 32 || D == 64 || D == 128),
+                "pfa_shortlist_attn_fwd: bf16 with D = 16, 32, 64 or 128 only (got dtype %d D %d)", dtype, D);
   // the q RoPE tables and the anchor-pass fusions work on 64-wide rows
   PFA_CHECK_ARG(D == 64 || (q_rope_cos == nullptr && fuse == 0),
                 "pfa_shortlist_attn_fwd: q RoPE on load and the anchor-pass fusions need D=64 (got D %d)", D);
@@ -1132,8 +1221,9 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
   a.rcos = (const uint16_t*)q_rope_cos; a.rsin = (const uint16_t*)q_rope_sin;
   a.scale_log2 = scale * 1.4426950408889634f;
   {
-    // byte offsets key * s_t * 2 + 112 of every key below T, K and V
-    const uint64_t mx = (uint64_t)(T - 1) * (uint64_t)(k.s_t > v.s_t ? k.s_t : v.s_t) * 2u + 128u;
+    // byte offsets key * s_t * 2 + 240 of every key below T, K and V (the
+    // last chunk of a 128-dim row)
+    const uint64_t mx = (uint64_t)(T - 1) * (uint64_t)(k.s_t > v.s_t ? k.s_t : v.s_t) * 2u + 256u;
     a.off32 = mx < 0xFFFFFFFFull ? 1 : 0;
   }
   a.qsc = q_scale; a.ksc = k_scale; a.vsc = v_scale;
@@ -1149,12 +1239,15 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
     const int ccap = (int)(npos < kClassChunk ? npos : kClassChunk);
     const size_t lds = (size_t)ccap * 8 + 16;
     const bool ng2 = npos >= kAnchorNG2Positions;
-    if (D == 64) {
-      if (ng2) short_anchor_kernel<2, false><<<grid, 256, lds, s>>>(a, ccap);
-      else short_anchor_kernel<1, false><<<grid, 256, lds, s>>>(a, ccap);
+    if (D == 128) {
+      // one row group per wave: two groups of 128-dim rows exceed the registers
+      short_anchor_kernel<1, false, 2><<<grid, 256, lds, s>>>(a, ccap);
+    } else if (D == 64) {
+      if (ng2) short_anchor_kernel<2, false, 1><<<grid, 256, lds, s>>>(a, ccap);
+      else short_anchor_kernel<1, false, 1><<<grid, 256, lds, s>>>(a, ccap);
     } else {
-      if (ng2) short_anchor_kernel<2, true><<<grid, 256, lds, s>>>(a, ccap);
-      else short_anchor_kernel<1, true><<<grid, 256, lds, s>>>(a, ccap);
+      if (ng2) short_anchor_kernel<2, true, 1><<<grid, 256, lds, s>>>(a, ccap);
+      else short_anchor_kernel<1, true, 1><<<grid, 256, lds, s>>>(a, ccap);
     }
     PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/anchors");
   }
@@ -1173,12 +1266,15 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
   const int ordcap = (int)((wspan + kTile - 1) / kTile) + 2 + pcap / kTile;
   const size_t dyn = (size_t)pcap * 12 + (size_t)ordcap * 4;
   const int up = anchors ? 1 : 0;
-  if (D == 64) {
-    if (lengths != nullptr) short_main_kernel<true, S, false><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
-    else short_main_kernel<false, S, false><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+  if (D == 128) {
+    if (lengths != nullptr) short_main_kernel<true, S, false, 2><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+    else short_main_kernel<false, S, false, 2><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+  } else if (D == 64) {
+    if (lengths != nullptr) short_main_kernel<true, S, false, 1><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+    else short_main_kernel<false, S, false, 1><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
   } else {
-    if (lengths != nullptr) short_main_kernel<true, S, true><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
-    else short_main_kernel<false, S, true><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+    if (lengths != nullptr) short_main_kernel<true, S, true, 1><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
+    else short_main_kernel<false, S, true, 1><<<(unsigned)blocks, 256, dyn, s>>>(a, up, pcap);
   }
   PFA_CHECK_LAUNCH("pfa_shortlist_attn_fwd/main");
   return PFA_OK;

@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "pfa_shortlist_build",
     "pfa_sparse_attn_fwd",
     "pfa_shortlist_attn_part_floats",
+    "pfa_shortlist_attn_part_floats_for",
     "pfa_shortlist_attn_fwd",
     "pfa_shortlist_attn_fwd_fused",
     "pfa_head_max_token",
@@ -122,6 +123,7 @@ _SIGNATURES = {
     "pfa_sparse_attn_fwd": ([Tensor4, Tensor4, Tensor4, _i32, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp,
                              _i64, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp], _i32),
     "pfa_shortlist_attn_part_floats": ([], _i32),
+    "pfa_shortlist_attn_part_floats_for": ([_i32], _i32),
     "pfa_shortlist_attn_fwd": ([Tensor4, Tensor4, Tensor4, Tensor4, _i32, _i32, _i64, _i32, _vp, _vp, _vp, _i64,
                                 _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _vp, _vp, _vp, _vp,
                                 _vp, _vp, _i32, _vp], _i32),

@@ -382,9 +382,10 @@ def _attn_launch(
     _hip.check(rc, "pfa_sparse_attn_fwd")
 
 
-def shortlist_partials(N: int, device: torch.device) -> torch.Tensor:
-    """f32 (N, pfa_shortlist_attn_part_floats()) anchor-pass partials."""
-    return torch.empty(N, int(_hip.lib().pfa_shortlist_attn_part_floats()), dtype=torch.float32, device=device)
+def shortlist_partials(N: int, device: torch.device, D: int = 64) -> torch.Tensor:
+    """f32 (N, pfa_shortlist_attn_part_floats_for(D)) anchor-pass partials."""
+    return torch.empty(N, int(_hip.lib().pfa_shortlist_attn_part_floats_for(int(D))), dtype=torch.float32,
+                       device=device)
 
 
 # pfa_shortlist_attn_fwd_fused bits (include/pfa_hip.h)
@@ -420,7 +421,7 @@ def _shortlist_attn_structured(
     fuse: int = 0,
 ) -> Optional[torch.Tensor]:
     """Module-path shortlist attention without materialised candidates
-    (bf16, D=64); the prototype sets come as _proto_prefix_blocks tables of
+    (bf16, D in STRUCTURED_HEAD_DIMS); the prototype sets come as _proto_prefix_blocks tables of
     the T-token scores.  Returns each row's candidate count (int32, (N,)),
     or None when want_lengths is False (the kernel then skips the counting).
     q_rope = (cos, sin) bf16 (T, 64) tables: q is still unrotated and its
@@ -441,7 +442,12 @@ def _shortlist_attn_structured(
     if anchors and part is None:
         if passes != 3:
             raise ValueError("split anchor/main passes need a shared partials buffer")
-        part = shortlist_partials(N, device)
+        part = shortlist_partials(N, device, D)
+    if anchors:
+        pw = int(_hip.lib().pfa_shortlist_attn_part_floats_for(int(D)))
+        if part.dtype != torch.float32 or part.dim() != 2 or part.size(0) < N or part.size(1) != pw \
+                or not part.is_contiguous():
+            raise ValueError(f"partials must be contiguous f32 (>= {N}, {pw}) for D = {D}")
     K = 0
     if blocks is not None:
         K = int(blocks.size(2))
@@ -481,8 +487,9 @@ def _shortlist_attn_structured(
 
 
 # Head dims of the structured MFMA kernel: rows of 16 or 32 elements are
-# attended as 64-wide rows whose q dims past D are zero.
-STRUCTURED_HEAD_DIMS = (16, 32, 64)
+# attended as 64-wide rows whose q dims past D are zero, rows of 128 as two
+# 64-dim halves of each tile.
+STRUCTURED_HEAD_DIMS = (16, 32, 64, 128)
 
 
 def _mfma_causal_ok(dtype: torch.dtype, D: int, *t4s: "_hip.Tensor4") -> bool:

@@ -1701,7 +1701,7 @@ class AdaptiveSparseAttention(nn.Module):
             part = None
             anchors = stride > 0 and slots > 0
             if anchors:
-                part = _sa.shortlist_partials(int(token_idx.numel()), device)
+                part = _sa.shortlist_partials(int(token_idx.numel()), device, D)
             packed = None
             if anchors and streams is not None:
                 packed = torch.cuda.Event()

@@ -260,7 +260,9 @@ def test_proto_prefix_sets_large_vs_c_oracle(dev):
                                                  (524288, 4096, 512, 256, 1, 0.0, 8),
                                                  (65536, 2048, 512, 4, 1, 0.01, 8), (20000, 1024, 128, 3, 2, 0.0, 8),
                                                  (4096, 1024, 256, 64, 1, 0.01, 32), (3000, 700, 100, 37, 2, 0.0, 16),
-                                                 (65536, 2048, 512, 256, 1, 0.01, 16)])
+                                                 (65536, 2048, 512, 256, 1, 0.01, 16),
+                                                 (4096, 1024, 256, 64, 1, 0.01, 4), (3000, 700, 100, 37, 2, 0.0, 4),
+                                                 (65536, 2048, 512, 256, 1, 0.01, 4)])
 def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, H, monkeypatch):
     """The structure-driven MFMA path and the builder + gather path give the
     same candidate counts per row and the same outputs (bf16 tolerance).
@@ -268,8 +270,8 @@ def test_structured_shortlist_matches_materialised(dev, T, L, w, s, B, outlier, 
     materialised path holds all 1,048,576 x 4,096 int32 candidates.  The
     stride-4 and stride-3 cases have residue classes of 16,384 and 6,667
     positions, whose rows the anchor pass compacts and attends in rounds.
-    H = 32 and 16 over d_model 512 give heads of 16 and 32 dims (q rotated
-    by the RoPE pass, not on load)."""
+    H = 32, 16 and 4 over d_model 512 give heads of 16, 32 and 128 dims (q
+    rotated by the RoPE pass, not on load)."""
     from configs import shortlist_cfg
 
     _say(f"structured vs materialised T={T} L={L} w={w} s={s} B={B} H={H}")
@@ -1408,11 +1410,12 @@ def test_dropin_mha_fallbacks_match_torch(dev):
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("BH,T,p,D", [(8, 8192, 1.0, 64), (6, 3001, 0.35, 64), (3, 65, 1.0, 64),
-                                       (5, 3001, 0.5, 16), (4, 2049, 0.7, 32), (2, 40, 1.0, 16)])
+                                       (5, 3001, 0.5, 16), (4, 2049, 0.7, 32), (2, 40, 1.0, 16),
+                                       (3, 3001, 0.5, 128), (2, 65, 1.0, 128)])
 def test_operator_causal_branch_mfma_vs_oracle(dev, BH, T, p, D):
     """aspa_sparse_attention without candidates or mask (each active row
-    attends to keys 0..t, sparse_attn.py:1016-1043) in bf16, D = 16, 32 or
-    64, runs the MFMA causal tiles; every active row against f32 causal
+    attends to keys 0..t, sparse_attn.py:1016-1043) in bf16, D = 16, 32, 64
+    or 128, runs the MFMA causal tiles; every active row against f32 causal
     attention, inactive rows zero."""
     from proteus_attention.kernels.sparse_attn import aspa_sparse_attention, get_last_backend_info
 
