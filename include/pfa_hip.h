@@ -121,9 +121,17 @@ int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C, int G,
  * protos (G, C) (NULL: no prototype prior), confidence and usage (G)
  * (NULL: unused) as they are.  One launch fewer at the head of the router
  * chain (aspa.py:636-663 + 628-690).  Supported when
- * pfa_router_raw_supported(...) returns 1: bf16 x, weights and buffers,
- * G <= 16, C a multiple of 128 up to 768 (G <= 8) or 512; otherwise
- * PFA_E_UNSUPPORTED. */
+ * pfa_router_raw_supported(...) returns 1 and G <= 16: bf16 x, weights and
+ * buffers, C a multiple of 128 up to 768 (G <= 8) or 512; otherwise
+ * PFA_E_UNSUPPORTED.
+ * pfa_router_topk_raw_ws serves every shape pfa_router_raw_supported
+ * accepts, G up to 64: with G <= 16 it is pfa_router_topk_raw (the
+ * workspace unused); with 17-64 gates it runs the 16-gate MFMA tables once
+ * per block of 16 gates, writing each token's logits, prototype dots and
+ * sum of squares to the workspace ((2G + 1) * n_tok f32, 16-byte aligned:
+ * pfa_router_raw_workspace_size), then the same epilogue and prototype EMA
+ * statistics in a second launch.  Same outputs as pfa_router_topk (the
+ * prototype dots in another f32 summation order). */
 int pfa_router_raw_supported(int x_dtype, int w_dtype, int buf_dtype, int G,
                              int C, int use_proto);
 int pfa_router_topk_raw(const void* x, int x_dtype, int64_t n_tok, int C,
@@ -137,6 +145,19 @@ int pfa_router_topk_raw(const void* x, int x_dtype, int64_t n_tok, int C,
                         float* importance, int32_t* head_idx,
                         float* head_score, float* stats_partial,
                         float* ema_partial, void* stream);
+int pfa_router_raw_workspace_size(int64_t n_tok, int G, size_t* bytes);
+int pfa_router_topk_raw_ws(const void* x, int x_dtype, int64_t n_tok, int C,
+                           int G, const void* w_router, int w_dtype,
+                           const void* protos, const void* confidence,
+                           const void* usage, int buf_dtype,
+                           const int32_t* gate_to_head, int H, int topk,
+                           float proto_temp, float proto_threshold,
+                           float proto_blend, float usage_boost,
+                           float* gate_probs, float* sim, float* blend,
+                           float* importance, int32_t* head_idx,
+                           float* head_score, float* stats_partial,
+                           float* ema_partial, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* ====================================================================
  * Prototype EMA statistics (aspa.py:692-718): per slice of tokens the

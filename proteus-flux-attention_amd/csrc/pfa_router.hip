@@ -438,15 +438,17 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
   typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
   typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
   constexpr int NA = GP == 8 ? 2 : 3;
+  constexpr int NB = GP <= 16 ? 1 : GP / 16;  // 16-gate blocks (32 or 64 gates: A rows 16b .. 16b + 15)
   const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
   // A operands for the two 32-token k-steps
-  bf16x8 a[NA][2];
+  bf16x8 a[NB][NA][2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int bk = 0; bk < 2 * NB; ++bk) {
+    const int b = bk >> 1, ks = bk & 1;
     uint16_t h[NA][8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float gv = gl[(32 * ks + 8 * kg + j) * GP + (GP == 8 ? (m & 7) : m)];
+      const float gv = gl[(32 * ks + 8 * kg + j) * GP + (GP == 8 ? (m & 7) : 16 * b + m)];
       const uint16_t hi = f32_to_bf16(gv);
       const float r1 = gv - bf16_to_f32(hi);
       const uint16_t mid = f32_to_bf16(r1);
@@ -461,7 +463,7 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
       }
     }
 #pragma unroll
-    for (int t = 0; t < NA; ++t) __builtin_memcpy(&a[t][ks], h[t], 16);
+    for (int t = 0; t < NA; ++t) __builtin_memcpy(&a[b][t][ks], h[t], 16);
   }
   // staging: lane l moves 16 bytes (channels 8*(l%8) ..+7) of tokens 8i + l/8
   const int srow = lane >> 3, scol = 8 * (lane & 7);
@@ -483,9 +485,7 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
     wave_sync();
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-      f32x4 d[NA];
-#pragma unroll
-      for (int t = 0; t < NA; ++t) d[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      bf16x8 bx[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         // lane (n, kg) gets x[32ks + 8kg + 0..7][16ct + n]
@@ -493,24 +493,32 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
         const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p0));
         const s16x4 hi4 =
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p0 + 4 * kXsLd));
-        bf16x8 b;
-        __builtin_memcpy(&b, &lo4, 8);
-        __builtin_memcpy(reinterpret_cast<char*>(&b) + 8, &hi4, 8);
-#pragma unroll
-        for (int t = 0; t < NA; ++t) d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][ks], b, d[t], 0, 0, 0);
+        __builtin_memcpy(&bx[ks], &lo4, 8);
+        __builtin_memcpy(reinterpret_cast<char*>(&bx[ks]) + 8, &hi4, 8);
       }
       const int c = 64 * cc + 16 * ct + m;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int g = 4 * kg + i;
-        if constexpr (GP == 8) {
-          // lanes 0-31 hold rows 4*(lane/16) + i: hi (d[0]) and lo (d[1]) of
-          // gates 0-7; the mid of the same gates is in d[0] of lane + 32
-          const auto sw =
-              __builtin_amdgcn_permlane32_swap(__float_as_uint(d[0][i]), __float_as_uint(d[0][i]), false, false);
-          if (lane < 32 && g < G) part[(int64_t)g * (C + 1) + c] = (d[0][i] + __uint_as_float(sw[1])) + d[1][i];
-        } else {
-          if (g < G) part[(int64_t)g * (C + 1) + c] = (d[0][i] + d[1][i]) + d[NA - 1][i];
+      for (int gbk = 0; gbk < NB; ++gbk) {
+        f32x4 d[NA];
+#pragma unroll
+        for (int t = 0; t < NA; ++t) d[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int t = 0; t < NA; ++t)
+            d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[gbk][t][ks], bx[ks], d[t], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int g = 16 * gbk + 4 * kg + i;
+          if constexpr (GP == 8) {
+            // lanes 0-31 hold rows 4*(lane/16) + i: hi (d[0]) and lo (d[1]) of
+            // gates 0-7; the mid of the same gates is in d[0] of lane + 32
+            const auto sw =
+                __builtin_amdgcn_permlane32_swap(__float_as_uint(d[0][i]), __float_as_uint(d[0][i]), false, false);
+            if (lane < 32 && g < G) part[(int64_t)g * (C + 1) + c] = (d[0][i] + __uint_as_float(sw[1])) + d[1][i];
+          } else {
+            if (g < G) part[(int64_t)g * (C + 1) + c] = (d[0][i] + d[1][i]) + d[NA - 1][i];
+          }
         }
       }
     }
@@ -521,7 +529,33 @@ __device__ __forceinline__ void ema_accum_mfma(const uint16_t* __restrict__ x, i
   }
 }
 
-template <int GP, bool PROTO, bool RAWIN>
+// Confidence weights and usage bias of pfa_router_prepare (G <= 64 gates,
+// one lane each, one wave): r_cw[g] = bf16(conf[g] + 1e-6) and r_ub =
+// bf16(softmax(-bf16(usage + 1e-6))), for g < GP (padding gates 1 and 0).
+template <int GP>
+__device__ __forceinline__ void rm_conf_usage(const RouterRaw& raw, int G, float* r_cw, float* r_ub) {
+  const int lane = threadIdx.x & 63;
+  const bool has = lane < G;
+  if (raw.conf != nullptr) {
+    const float v = has ? round_to<PFA_BF16>(bf16_to_f32(raw.conf[lane]) + 1e-6f) : 1.f;
+    if (lane < GP) r_cw[lane] = v;
+  }
+  if (raw.usage != nullptr) {
+    const float v = has ? -round_to<PFA_BF16>(bf16_to_f32(raw.usage[lane]) + 1e-6f) : -INFINITY;
+    float m = v;
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const float e = has ? expf(v - m) : 0.f;
+    float sum = e;
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane < GP) r_ub[lane] = has ? round_to<PFA_BF16>(e / sum) : 0.f;
+  }
+}
+
+// DOTS: one 16-gate block (blockIdx.y) of a router with up to 64 gates
+// (RAWIN, GP = 16): the block's gate logits, prototype dots and (block 0)
+// the tokens' sums of squares go to rl, (2G + 1, n_tok) f32 (rows g, G + g
+// and 2G), for router_epi_kernel; no epilogue.
+template <int GP, bool PROTO, bool RAWIN, bool DOTS = false>
 __global__ void __launch_bounds__(64 * kRmWaves)
 router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, const float* __restrict__ wpk,
                    const float* __restrict__ conf_weight, const float* __restrict__ usage_bias,
@@ -529,9 +563,18 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
                    float proto_threshold, float proto_blend, float usage_boost, float* __restrict__ gate_probs,
                    float* __restrict__ sim_out, float* __restrict__ blend_out, float* __restrict__ importance,
                    int32_t* __restrict__ head_idx, float* __restrict__ head_score, float* __restrict__ stats,
-                   float* __restrict__ ema_part, RouterRaw raw) {
+                   float* __restrict__ ema_part, RouterRaw raw, float* __restrict__ rl = nullptr) {
   PFA_CRITICAL_CHAIN_PRIORITY();
   static_assert(GP == 8 || GP == 16, "MFMA router tables hold 8 or 16 gates");
+  static_assert(!DOTS || (GP == 16 && RAWIN), "gate blocks take the 16-gate tables from the raw weights");
+  // DOTS: gates gb .. gb + Gk - 1 of G
+  const int gb = DOTS ? 16 * (int)blockIdx.y : 0;
+  const int Gall = G;
+  if constexpr (DOTS) {
+    G = min(16, Gall - gb);
+    raw.w += (int64_t)gb * C;
+    if (raw.p != nullptr) raw.p += (int64_t)gb * C;
+  }
   constexpr int NT = rm_tables(GP, PROTO);
   typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
   typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
@@ -548,22 +591,7 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
   __shared__ float r_ub[RAWIN ? GP : 1];
   if constexpr (RAWIN) {
     static_assert(64 * kRmWaves == kPrepThreads, "router_prepare_kernel's thread map");
-    if (wid == kRmWaves - 1) {
-      const bool has = lane < G;
-      if (raw.conf != nullptr) {
-        const float v = has ? round_to<PFA_BF16>(bf16_to_f32(raw.conf[lane]) + 1e-6f) : 1.f;
-        if (lane < GP) r_cw[lane] = v;
-      }
-      if (raw.usage != nullptr) {
-        const float v = has ? -round_to<PFA_BF16>(bf16_to_f32(raw.usage[lane]) + 1e-6f) : -INFINITY;
-        float m = v;
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        const float e = has ? expf(v - m) : 0.f;
-        float sum = e;
-        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-        if (lane < GP) r_ub[lane] = has ? round_to<PFA_BF16>(e / sum) : 0.f;
-      }
-    }
+    if (!DOTS && wid == kRmWaves - 1) rm_conf_usage<GP>(raw, G, r_cw, r_ub);
     if constexpr (PROTO) {
       float acc[GP];
 #pragma unroll
@@ -735,6 +763,18 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
   }
   const int64_t tok = tok0 + lane;
   const bool live = tok < n_tok;
+  if constexpr (DOTS) {
+    if (live) {
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+        if (g < G) {
+          rl[(int64_t)(gb + g) * n_tok + tok] = acc_t[g];
+          if constexpr (PROTO) rl[(int64_t)(Gall + gb + g) * n_tok + tok] = acc_t[GP + g];
+        }
+      if (blockIdx.y == 0) rl[(int64_t)2 * Gall * n_tok + tok] = acc_t[2 * GP];
+    }
+    return;
+  }
   float gate[GP];
   const float* cw_in = conf_weight;
   const float* ub_in = usage_bias;
@@ -764,6 +804,66 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
     }
   }
 }
+
+// Epilogue of the router with 17-64 gates: a token per lane, 64 tokens per
+// wave (router_mfma_kernel's groups), from the logits, prototype dots and
+// sums of squares that router_mfma_kernel<16, PROTO, true, true> wrote to rl
+// ((2G + 1, n_tok) f32); then the prototype EMA statistics of the wave's
+// tokens on MFMA (ema_accum_mfma over 16-gate blocks).  The arithmetic of
+// the 16-gate router: the same epilogue on the same f32 inputs.
+template <int GP, bool PROTO>
+__global__ void __launch_bounds__(64 * kRmWaves)
+router_epi_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, const float* __restrict__ rl,
+                  const int32_t* __restrict__ gate_to_head, int H, int topk, float proto_temp, float proto_threshold,
+                  float proto_blend, float usage_boost, float* __restrict__ gate_probs, float* __restrict__ sim_out,
+                  float* __restrict__ blend_out, float* __restrict__ importance, int32_t* __restrict__ head_idx,
+                  float* __restrict__ head_score, float* __restrict__ stats, float* __restrict__ ema_part,
+                  RouterRaw raw) {
+  PFA_CRITICAL_CHAIN_PRIORITY();
+  static_assert(GP == 32 || GP == 64, "the gate-block epilogue takes 32 or 64 padded gates");
+  extern __shared__ __align__(16) unsigned char rm_lds[];
+  __shared__ float r_cw[GP];
+  __shared__ float r_ub[GP];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  if (wid == 0) rm_conf_usage<GP>(raw, G, r_cw, r_ub);
+  __syncthreads();
+  const int64_t group = (int64_t)blockIdx.x * kRmWaves + wid;
+  const int64_t n_groups = (n_tok + kRouterTok - 1) / kRouterTok;
+  const int64_t tok0 = group * kRouterTok;
+  const int64_t tok = tok0 + lane;
+  const bool live = tok < n_tok;
+  float acc_t[2 * GP + 1];
+#pragma unroll
+  for (int g = 0; g < GP; ++g) {
+    acc_t[g] = (live && g < G) ? rl[(int64_t)g * n_tok + tok] : 0.f;
+    acc_t[GP + g] = (PROTO && live && g < G) ? rl[(int64_t)(G + g) * n_tok + tok] : 0.f;
+  }
+  acc_t[2 * GP] = live ? rl[(int64_t)2 * G * n_tok + tok] : 0.f;
+  float gate[GP];
+  router_epilogue<PFA_BF16, GP, PROTO>(acc_t, tok, live, group, G, raw.conf != nullptr ? r_cw : nullptr,
+                                       raw.usage != nullptr ? r_ub : nullptr, gate_to_head, H, topk, proto_temp,
+                                       proto_threshold, proto_blend, usage_boost, gate_probs, sim_out, blend_out,
+                                       importance, head_idx, head_score, group < n_groups ? stats : nullptr, gate);
+  if (ema_part != nullptr) {
+    float* gl = reinterpret_cast<float*>(rm_lds) + wid * 64 * GP;
+#pragma unroll
+    for (int g = 0; g < GP; ++g) gl[lane * GP + g] = (live && g < G) ? gate[g] : 0.f;
+    __syncthreads();
+    if (group < n_groups) {
+      float* part = ema_part + group * G * (C + 1);
+      if (lane < G) {
+        float cs = 0.f;  // column C: sum of gate g over the group's tokens, in token order
+        for (int u = 0; u < 64; ++u) cs += gl[u * GP + lane];
+        part[(int64_t)lane * (C + 1) + C] = cs;
+      }
+      ema_accum_mfma<GP>(x, tok0, (int)min<int64_t>(64, n_tok - tok0), C, G, gl, part,
+                         reinterpret_cast<uint16_t*>(rm_lds + kRmWaves * 64 * GP * 4 + wid * kXsWave));
+    }
+  }
+}
+
+// LDS of router_epi_kernel: the gate rows and x staging of the EMA statistics.
+constexpr int rm_epi_lds_bytes(int GP, bool ema) { return ema ? kRmWaves * 64 * GP * 4 + kRmWaves * kXsWave : 0; }
 
 // Prototype EMA partial sums: part p accumulates, for a slice of at most
 // kEmaTok tokens, sum_t gate[t,g]*x[t,c] (columns 0..C-1) and sum_t gate[t,g]
@@ -1202,16 +1302,25 @@ extern "C" int pfa_router_topk(const void* x, int x_dtype, int64_t n_tok, int C,
 }
 
 // The MFMA router with its inputs built in each workgroup: bf16 x, weights
-// and prototype buffers, at most 16 gates, C a multiple of 128 up to 768
-// (8 gates) or 512 (16 gates).
-static bool router_raw_ok(int x_dtype, int w_dtype, int buf_dtype, int G, int C, bool proto) {
+// and prototype buffers, C a multiple of 128 up to 768 (8 gates) or 512
+// (9-64 gates: 16-gate tables); up to 16 gates in one fused launch
+// (pfa_router_topk_raw), 17-64 in 16-gate blocks and an epilogue launch
+// (pfa_router_topk_raw_ws).
+static bool router_raw_ok(int x_dtype, int w_dtype, int buf_dtype, int G, int C, bool proto, int max_g) {
   if (x_dtype != PFA_BF16 || w_dtype != PFA_BF16 || (proto && buf_dtype != PFA_BF16)) return false;
-  if (G < 1 || G > 16 || C <= 0 || C % 128 != 0) return false;
+  if (G < 1 || G > max_g || C <= 0 || C % 128 != 0) return false;
   return C <= (gate_pad(G) == 8 ? 768 : 512);
 }
 
 extern "C" int pfa_router_raw_supported(int x_dtype, int w_dtype, int buf_dtype, int G, int C, int use_proto) {
-  return router_raw_ok(x_dtype, w_dtype, buf_dtype, G, C, use_proto != 0) ? 1 : 0;
+  return router_raw_ok(x_dtype, w_dtype, buf_dtype, G, C, use_proto != 0, 64) ? 1 : 0;
+}
+
+extern "C" int pfa_router_raw_workspace_size(int64_t n_tok, int G, size_t* bytes) {
+  clear_error();
+  PFA_CHECK_ARG(bytes != nullptr && n_tok >= 0 && G > 0 && G <= 64, "pfa_router_raw_workspace_size: bad arguments");
+  *bytes = G > 16 ? (size_t)(2 * G + 1) * (size_t)n_tok * sizeof(float) : 0;
+  return PFA_OK;
 }
 
 extern "C" int pfa_router_topk_raw(const void* x, int x_dtype, int64_t n_tok, int C, int G, const void* w_router,
@@ -1225,9 +1334,9 @@ extern "C" int pfa_router_topk_raw(const void* x, int x_dtype, int64_t n_tok, in
                 "pfa_router_topk_raw: bad sizes n_tok=%lld C=%d G=%d H=%d topk=%d", (long long)n_tok, C, G, H, topk);
   PFA_CHECK_ARG(x && w_router && gate_to_head && importance && head_idx, "pfa_router_topk_raw: null pointer");
   const bool pr = protos != nullptr;
-  if (!router_raw_ok(x_dtype, w_dtype, buf_dtype, G, C, pr)) {
-    set_error("pfa_router_topk_raw: unsupported (x dtype %d, weight dtype %d, buffer dtype %d, G=%d, C=%d)", x_dtype,
-              w_dtype, buf_dtype, G, C);
+  if (!router_raw_ok(x_dtype, w_dtype, buf_dtype, G, C, pr, 16)) {
+    set_error("pfa_router_topk_raw: unsupported (x dtype %d, weight dtype %d, buffer dtype %d, G=%d, C=%d; "
+              "17-64 gates take pfa_router_topk_raw_ws)", x_dtype, w_dtype, buf_dtype, G, C);
     return PFA_E_UNSUPPORTED;
   }
   if (n_tok == 0) return PFA_OK;
@@ -1250,6 +1359,69 @@ extern "C" int pfa_router_topk_raw(const void* x, int x_dtype, int64_t n_tok, in
   }
 #undef PFA_RR
   PFA_CHECK_LAUNCH("pfa_router_topk_raw");
+  return PFA_OK;
+}
+
+extern "C" int pfa_router_topk_raw_ws(const void* x, int x_dtype, int64_t n_tok, int C, int G, const void* w_router,
+                                      int w_dtype, const void* protos, const void* confidence, const void* usage,
+                                      int buf_dtype, const int32_t* gate_to_head, int H, int topk, float proto_temp,
+                                      float proto_threshold, float proto_blend, float usage_boost, float* gate_probs,
+                                      float* sim, float* blend, float* importance, int32_t* head_idx,
+                                      float* head_score, float* stats_partial, float* ema_partial, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  if (G <= 16)
+    return pfa_router_topk_raw(x, x_dtype, n_tok, C, G, w_router, w_dtype, protos, confidence, usage, buf_dtype,
+                               gate_to_head, H, topk, proto_temp, proto_threshold, proto_blend, usage_boost,
+                               gate_probs, sim, blend, importance, head_idx, head_score, stats_partial, ema_partial,
+                               stream);
+  clear_error();
+  PFA_CHECK_ARG(n_tok >= 0 && C > 0 && G > 0 && G <= 64 && H > 0 && H <= G && topk >= 1 && topk <= H,
+                "pfa_router_topk_raw_ws: bad sizes n_tok=%lld C=%d G=%d H=%d topk=%d", (long long)n_tok, C, G, H,
+                topk);
+  PFA_CHECK_ARG(x && w_router && gate_to_head && importance && head_idx, "pfa_router_topk_raw_ws: null pointer");
+  const bool pr = protos != nullptr;
+  if (!router_raw_ok(x_dtype, w_dtype, buf_dtype, G, C, pr, 64)) {
+    set_error("pfa_router_topk_raw_ws: unsupported (x dtype %d, weight dtype %d, buffer dtype %d, G=%d, C=%d)",
+              x_dtype, w_dtype, buf_dtype, G, C);
+    return PFA_E_UNSUPPORTED;
+  }
+  if (n_tok == 0) return PFA_OK;
+  const size_t need = (size_t)(2 * G + 1) * (size_t)n_tok * sizeof(float);
+  PFA_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace % 16) == 0,
+                "pfa_router_topk_raw_ws: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
+                workspace_bytes);
+  hipStream_t s = as_stream(stream);
+  const RouterRaw raw{(const uint16_t*)w_router, (const uint16_t*)protos, pr ? (const uint16_t*)confidence : nullptr,
+                      pr ? (const uint16_t*)usage : nullptr};
+  float* rl = reinterpret_cast<float*>(workspace);
+  const unsigned blocks = (unsigned)((n_tok + kRouterTok - 1) / kRouterTok);
+  const unsigned mb = (blocks + kRmWaves - 1) / kRmWaves;
+  const dim3 gd(mb, (unsigned)((G + 15) / 16));
+  // 16-gate blocks: logits, prototype dots and sums of squares into rl
+  if (pr)
+    router_mfma_kernel<16, true, true, true><<<gd, 64 * kRmWaves, (size_t)rm_lds_bytes(C, 16, true), s>>>(
+        (const uint16_t*)x, n_tok, C, G, nullptr, nullptr, nullptr, gate_to_head, H, topk, proto_temp,
+        proto_threshold, proto_blend, usage_boost, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+        nullptr, raw, rl);
+  else
+    router_mfma_kernel<16, false, true, true><<<gd, 64 * kRmWaves, (size_t)rm_lds_bytes(C, 16, false), s>>>(
+        (const uint16_t*)x, n_tok, C, G, nullptr, nullptr, nullptr, gate_to_head, H, topk, proto_temp,
+        proto_threshold, proto_blend, usage_boost, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+        nullptr, raw, rl);
+  PFA_CHECK_LAUNCH("pfa_router_topk_raw_ws/dots");
+#define PFA_RE(GPV, PV)                                                                                          \
+  router_epi_kernel<GPV, PV><<<mb, 64 * kRmWaves, (size_t)rm_epi_lds_bytes(GPV, ema_partial != nullptr), s>>>(  \
+      (const uint16_t*)x, n_tok, C, G, rl, gate_to_head, H, topk, proto_temp, proto_threshold, proto_blend,      \
+      usage_boost, gate_probs, sim, blend, importance, head_idx, head_score, stats_partial, ema_partial, raw)
+  if (G <= 32) {
+    if (pr) PFA_RE(32, true);
+    else PFA_RE(32, false);
+  } else {
+    if (pr) PFA_RE(64, true);
+    else PFA_RE(64, false);
+  }
+#undef PFA_RE
+  PFA_CHECK_LAUNCH("pfa_router_topk_raw_ws/epilogue");
   return PFA_OK;
 }
 

@@ -33,6 +33,8 @@ EXPORTED_SYMBOLS = (
     "pfa_router_topk",
     "pfa_router_raw_supported",
     "pfa_router_topk_raw",
+    "pfa_router_raw_workspace_size",
+    "pfa_router_topk_raw_ws",
     "pfa_proto_ema_update",
     "pfa_proto_partial_count",
     "pfa_proto_accumulate",
@@ -105,6 +107,10 @@ _SIGNATURES = {
     "pfa_router_raw_supported": ([_i32, _i32, _i32, _i32, _i32, _i32], _i32),
     "pfa_router_topk_raw": ([_vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _i32, _i32,
                              _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
+    "pfa_router_raw_workspace_size": ([_i64, _i32, ctypes.POINTER(_sz)], _i32),
+    "pfa_router_topk_raw_ws": ([_vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _i32, _i32,
+                                _f32, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+                               _i32),
     "pfa_proto_ema_update": ([_vp, _i32, _i32, _f32, _vp, _vp, _vp, _i32, _vp], _i32),
     "pfa_proto_partial_count": ([_i64, ctypes.POINTER(_i32)], _i32),
     "pfa_proto_accumulate": ([_vp, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _vp], _i32),

@@ -868,7 +868,16 @@ class AdaptiveSparseAttention(nn.Module):
                 _hip.ptr(blend), _hip.ptr(imp), _hip.ptr(hidx), _hip.ptr(hsc), _hip.ptr(stats), _hip.ptr(ema),
                 _hip.stream_ptr(device))
         with _hip.TIMER.timed("router_topk"):
-            if raw:
+            if raw and G > 16:
+                # 17-64 gates: 16-gate MFMA blocks into a workspace, then the epilogue
+                name = "pfa_router_topk_raw_ws"
+                nbytes = _sa._size_out(lib.pfa_router_raw_workspace_size, n_tok, G)
+                ws = _sa._workspace(nbytes, device)
+                rc = lib.pfa_router_topk_raw_ws(
+                    _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(w), _hip.dtype_tag(w.dtype),
+                    _hip.ptr(protos), _hip.ptr(conf_b), _hip.ptr(usage_b), _hip.dtype_tag(buf_dtype), *tail[:-1],
+                    _hip.ptr(ws), ws.numel(), tail[-1])
+            elif raw:
                 name = "pfa_router_topk_raw"
                 rc = lib.pfa_router_topk_raw(
                     _hip.ptr(x2d), _hip.dtype_tag(x2d.dtype), n_tok, C, G, _hip.ptr(w), _hip.dtype_tag(w.dtype),

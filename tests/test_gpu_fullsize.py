@@ -50,12 +50,31 @@ def _module(cfg, B, T, C, dt, dev, outlier):
 
 @pytest.mark.parametrize("T,L,row_every,attn_every", [(65536, 2048, 1, 64), (524288, 4096, 16, 512)])
 def test_shortlist_forward_full_size_vs_oracle(dev, T, L, row_every, attn_every):
+    _check_shortlist_forward(dev, T, L, row_every, attn_every, H=8, G=8, window=512, stride=256,
+                             outlier=0.01 if T == 65536 else 0.0)
+
+
+@pytest.mark.parametrize("T,H,G,window,stride", [(16384, 32, 64, 256, 64), (16384, 4, 4, 512, 128),
+                                                 (16384, 16, 32, 256, 64)])
+def test_shortlist_forward_head_shapes_vs_oracle(dev, T, H, G, window, stride):
+    """The same checks at the shapes off the BASELINE configs: 32 heads of
+    16 dims with 64 gates (the reference's tinytoy recipe,
+    kernels/tinytoy.py:307-325), 4 heads of 128 dims, 16 heads of 32 dims
+    with 32 gates -- the MFMA router in 16-gate blocks and the structured
+    attention at those head widths."""
+    _check_shortlist_forward(dev, T, 1024, 1, 16, H=H, G=G, window=window, stride=stride, outlier=0.01)
+
+
+def _check_shortlist_forward(dev, T, L, row_every, attn_every, H, G, window, stride, outlier):
     from configs import shortlist_cfg
     from routing_parity import check_routing
 
-    _say(f"shortlist forward T={T} L={L}")
-    B, C, H, D = 1, 512, 8, 64
-    m, x = _module(shortlist_cfg(T, C, H, L), B, T, C, torch.bfloat16, dev, 0.01 if T == 65536 else 0.0)
+    B, C = 1, 512
+    D = C // H
+    _say(f"shortlist forward T={T} L={L} H={H} D={D} G={G}")
+    cfg = shortlist_cfg(T, C, H, L, window, stride)
+    cfg["attn_gates"] = G
+    m, x = _module(cfg, B, T, C, torch.bfloat16, dev, outlier)
     m.record_shortlist_lengths = True
     w_router = m.head_router.linear.weight.detach().cpu()
     protos = m.routing_prototypes.detach().cpu()
@@ -72,7 +91,8 @@ def test_shortlist_forward_full_size_vs_oracle(dev, T, L, row_every, attn_every)
     heads = st["active_head_indices"].cpu().long()
     lens = m._last_shortlist_lengths.cpu().numpy()
     sims = m._last_token_similarity.float().cpu()
-    gates = m._last_gate_probs.float().cpu().reshape(B * T, H)
+    gates = m._last_gate_probs.float().cpu().reshape(B * T, G)
+    g2h = m.gate_to_head.cpu()
     attn = m.last_head_consensus.view(B, T, H, D).float().cpu()
 
     # routing against the oracle router on the same inputs
@@ -84,9 +104,10 @@ def test_shortlist_forward_full_size_vs_oracle(dev, T, L, row_every, attn_every)
     ours = torch.zeros(B * H, T, dtype=torch.bool)
     ours[heads[row_head], tok] = True
     ours = ours.view(B, H, T).permute(0, 2, 1).reshape(B * T, H)
-    _, oidx = O.topk_lowest(og.reshape(B * T, H), 2)
+    _, oidx = O.topk_lowest(O.head_probs_from_gates(og.reshape(B * T, G), g2h, H), 2)
     ref = torch.zeros(B * T, H, dtype=torch.bool).scatter_(1, oidx, True)
-    rep = check_routing(ours, ref, gates, og.reshape(B * T, H), x.reshape(B * T, C), w_router, 2)
+    rep = check_routing(ours, ref, gates, og.reshape(B * T, G), x.reshape(B * T, C), w_router, 2,
+                        gate_to_head=None if G == H else g2h, sum_ulps=0 if G <= 8 else G)
     _say(f"T={T} routing vs oracle: {rep}")
     rep.assert_boundary_sets_at_most(1e-3)
     N = int(tok.numel())

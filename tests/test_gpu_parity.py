@@ -1330,6 +1330,115 @@ def test_router_sixteen_gates_bf16_vs_oracle(dev, n, C, G):
     assert torch.equal(hsc, hv)
 
 
+def _router_raw_ws(dev, x, w, protos, conf, use, g2h, H, topk, args, ema):
+    """pfa_router_topk_raw_ws on bf16 device tensors: (gate, sim, blend,
+    importance, head_idx, head_score, telemetry partials, EMA partials)."""
+    from proteus_attention import _hip
+    from proteus_attention.kernels.sparse_attn import _size_out, _workspace
+
+    lib = _hip.lib()
+    n, C = x.shape
+    G = w.size(0)
+    nblk = _hip.ctypes.c_int(0)
+    _hip.check(lib.pfa_router_block_count(n, _hip.ctypes.byref(nblk)), "block_count")
+    nb = max(1, nblk.value)
+    out = [torch.empty(n, G, device=dev), torch.empty(n, device=dev), torch.empty(n, device=dev),
+           torch.empty(n, device=dev), torch.empty(n, topk, device=dev, dtype=torch.int32),
+           torch.empty(n, topk, device=dev), torch.empty(nb, 8, device=dev),
+           torch.empty(nb, G, C + 1, device=dev) if ema else None]
+    ws = _workspace(_size_out(lib.pfa_router_raw_workspace_size, n, G), dev)
+    bf = _hip.PFA_BF16
+    _hip.check(lib.pfa_router_topk_raw_ws(_hip.ptr(x), bf, n, C, G, _hip.ptr(w), bf, _hip.ptr(protos), _hip.ptr(conf),
+                                          _hip.ptr(use), bf, _hip.ptr(g2h), H, topk, *args,
+                                          *[_hip.ptr(o) for o in out], _hip.ptr(ws), ws.numel(),
+                                          _hip.stream_ptr(dev)), "router_raw_ws")
+    return out
+
+
+@pytest.mark.parametrize("n,C,G,H,ema", [(3000, 512, 64, 32, True), (2500, 384, 32, 16, True),
+                                         (1000, 256, 24, 8, False), (4097, 512, 48, 16, True),
+                                         (130, 128, 17, 8, True), (20_000, 512, 64, 32, True)])
+def test_router_gate_blocks_bf16_vs_oracle(dev, n, C, G, H, ema):
+    """bf16 router with 17-64 gates (pfa_router_topk_raw_ws: the 16-gate
+    MFMA tables once per block of 16 gates, then the epilogue) against the
+    oracle, as the 16-gate router is tested: prototype similarities to f32
+    accumulation order, gates bit for bit where the blend is zero except at
+    a bf16 rounding boundary of a logit or softmax output, within 1e-5
+    where it is live, head top-k exactly the lowest-index top-k of the
+    router's own head probabilities; the fused EMA statistics against a
+    float64 product of the router's own gates; and the same head sets as
+    the VALU router (pfa_router_prepare + pfa_router_topk) wherever the two
+    routers' gates agree."""
+    from proteus_attention import _hip
+    from routing_parity import _at_boundary
+
+    _say(f"router gate blocks G={G} H={H} n={n} C={C} bf16")
+    lib = _hip.lib()
+    bf = torch.bfloat16
+    topk = 2
+    g = torch.Generator().manual_seed(70 + G)
+    x = torch.randn(n, C, generator=g).to(bf)
+    w = (torch.randn(G, C, generator=g) * 0.05).to(bf)
+    protos = torch.randn(G, C, generator=g).to(bf)
+    near = 4
+    protos[:near] = (x[:near].float() + 0.3 * torch.randn(near, C, generator=g)).to(bf)
+    conf = (torch.rand(G, generator=g) * 3).to(bf)
+    use = (torch.rand(G, generator=g) * 5).to(bf)
+    assert lib.pfa_router_raw_supported(_hip.PFA_BF16, _hip.PFA_BF16, _hip.PFA_BF16, G, C, 1) == 1
+    g2h = O.default_gate_map(G, H).to(torch.int32).to(dev)
+    xd, wd, pd, cd, ud = (t.to(dev) for t in (x, w, protos, conf, use))
+    args = (0.2, 0.25, 0.6, 0.0)
+    out = _router_raw_ws(dev, xd, wd, pd, cd, ud, g2h, H, topk, args, ema)
+    gate, sim, bl, imp, hidx, hsc = (o.cpu() for o in out[:6])
+    og, osim, obl, oimp = O.route_tokens(x, w, protos, conf, None, proto_temp=0.2, proto_threshold=0.25,
+                                         proto_blend=0.6, usage_boost=0.0)
+    og, osim, obl, oimp = og.reshape(n, G), osim.reshape(n), obl.reshape(n), oimp.reshape(n)
+    assert torch.allclose(sim, osim, atol=2e-6, rtol=0)
+    assert torch.allclose(bl, obl, atol=1e-5, rtol=0)
+    live = (bl > 0) | (obl > 0)
+    assert bool(live[:near].all())
+    bad = (gate != og).any(1) & ~live
+    assert int((bad & ~torch.from_numpy(_at_boundary(x, w))).sum()) == 0
+    assert torch.allclose(gate[live], og[live], atol=1e-5, rtol=0)
+    close = (gate - og).abs().amax(1) <= 1e-5
+    assert float(close.float().mean()) > 0.9
+    assert torch.allclose(imp[close], oimp[close], atol=1e-5, rtol=0)
+    hv, oidx = O.topk_lowest(_head_probs(gate, G, H), topk)
+    assert torch.equal(hidx.long(), oidx)
+    assert torch.equal(hsc, hv)
+    if ema:
+        nb = out[7].size(0)
+        sums = torch.empty(G, C + 1, device=dev)
+        _hip.check(lib.pfa_proto_partial_reduce(_hip.ptr(out[7]), nb, G, C, _hip.ptr(sums), _hip.stream_ptr(dev)),
+                   "reduce")
+        gp, got = gate.double(), sums.cpu().double()
+        ref = torch.cat([gp.t() @ x.double(), gp.sum(0).unsqueeze(1)], dim=1)
+        scale = torch.cat([(gp.t() @ x.double().abs()).clamp_min(1.0), gp.sum(0).unsqueeze(1).clamp_min(1.0)], dim=1)
+        err = float(((got - ref).abs() / scale).max())
+        _say(f"EMA sums max scaled error {err:.2e}")
+        assert err < 1e-5
+    # the VALU router on the same inputs (usage bias on, conf weights on)
+    Gp = int(lib.pfa_router_gate_pad(G))
+    wpk = torch.empty(C, 2 * Gp, device=dev)
+    cw, ub = torch.empty(G, device=dev), torch.empty(G, device=dev)
+    _hip.check(lib.pfa_router_prepare(_hip.ptr(wd), _hip.PFA_BF16, _hip.ptr(pd), _hip.ptr(cd), _hip.ptr(ud),
+                                      _hip.PFA_BF16, G, C, _hip.PFA_BF16, _hip.ptr(wpk), _hip.ptr(cw), _hip.ptr(ub),
+                                      _hip.stream_ptr(dev)), "prepare")
+    args_u = (0.2, 0.25, 0.6, 0.3)
+    mine = _router_raw_ws(dev, xd, wd, pd, cd, ud, g2h, H, topk, args_u, False)
+    valu = [torch.empty_like(t) if t is not None else None for t in mine]
+    _hip.check(lib.pfa_router_topk(_hip.ptr(xd), _hip.PFA_BF16, n, C, G, _hip.ptr(wpk), 1, _hip.ptr(cw), _hip.ptr(ub),
+                                   _hip.ptr(g2h), H, topk, *args_u, *[_hip.ptr(o) for o in valu],
+                                   _hip.stream_ptr(dev)), "router_valu")
+    ga, gb_ = mine[0].cpu(), valu[0].cpu()
+    agree = (ga - gb_).abs().amax(1) <= 1e-5
+    _say(f"gates within 1e-5 of the VALU router on {float(agree.float().mean()):.4f} of tokens")
+    assert float(agree.float().mean()) > 0.9
+    assert torch.allclose(mine[1].cpu(), valu[1].cpu(), atol=2e-6, rtol=0)
+    same = (ga == gb_).all(1)
+    assert torch.equal(mine[4].cpu()[same], valu[4].cpu()[same])
+
+
 # ---------------------------------------------------------------------------
 # drop-in nn.MultiheadAttention replacement (reference tests/test_dropin_attention.py)
 # ---------------------------------------------------------------------------
