@@ -90,7 +90,12 @@ __device__ __forceinline__ void router_ema_accum(const typename Elem<DT>::T* __r
 // squares of the token row.  Writes the token's outputs and the workgroup's
 // telemetry partials (row `group` of stats) and returns the final gate
 // probabilities in gate.
-template <int DT, int GP, bool PROTO>
+// hp_lds (HPLDS): the wave's (GP, 64) f32 LDS region, lane l's head
+// probabilities in column l: the per-head sums then take one LDS add per
+// gate instead of a register array indexed by every (gate, head) pair, in
+// the same order (the same bits); the per-gate inputs are read where used.
+// For 32 or 64 gates, where the register form spills.
+template <int DT, int GP, bool PROTO, bool HPLDS = false>
 __device__ __forceinline__ void router_epilogue(float (&acc)[2 * GP + 1], int64_t tok, bool live, int64_t group, int G,
                                                 const float* __restrict__ conf_weight,
                                                 const float* __restrict__ usage_bias,
@@ -100,20 +105,31 @@ __device__ __forceinline__ void router_epilogue(float (&acc)[2 * GP + 1], int64_
                                                 float* __restrict__ sim_out, float* __restrict__ blend_out,
                                                 float* __restrict__ importance, int32_t* __restrict__ head_idx,
                                                 float* __restrict__ head_score, float* __restrict__ stats,
-                                                float (&gate)[GP]) {
+                                                float (&gate)[GP], float* hp_lds = nullptr) {
   constexpr int NV = 2 * GP + 1;
   const int lane = threadIdx.x & 63;
   // per-gate inputs loaded unconditionally (padding gates re-read gate G-1
   // and are never used) so that the loads are issued together
-  float cwv[GP], ubv[GP];
-  int hgv[GP];
+  constexpr int NP = HPLDS ? 1 : GP;
+  float cwv[NP], ubv[NP];
+  int hgv[NP];
+  if constexpr (!HPLDS) {
 #pragma unroll
-  for (int g = 0; g < GP; ++g) {
-    const int gc = g < G ? g : G - 1;
-    cwv[g] = conf_weight != nullptr ? conf_weight[gc] : 1.f;
-    ubv[g] = usage_bias != nullptr ? usage_bias[gc] : 0.f;
-    hgv[g] = gate_to_head[gc];
+    for (int g = 0; g < GP; ++g) {
+      const int gc = g < G ? g : G - 1;
+      cwv[g] = conf_weight != nullptr ? conf_weight[gc] : 1.f;
+      ubv[g] = usage_bias != nullptr ? usage_bias[gc] : 0.f;
+      hgv[g] = gate_to_head[gc];
+    }
   }
+  auto cw_of = [&](int g) -> float {
+    if constexpr (HPLDS) return conf_weight != nullptr ? conf_weight[g] : 1.f;
+    else return cwv[g];
+  };
+  auto ub_of = [&](int g) -> float {
+    if constexpr (HPLDS) return usage_bias != nullptr ? usage_bias[g] : 0.f;
+    else return ubv[g];
+  };
   float* logit = acc;
   float* dotp = acc + GP;
   const float sq = acc[NV - 1];
@@ -159,7 +175,7 @@ __device__ __forceinline__ void router_epilogue(float (&acc)[2 * GP + 1], int64_
       float cs = 0.f;
 #pragma unroll
       for (int g = 0; g < GP; ++g)
-        if (g < G) { pp[g] = pp[g] * cwv[g]; cs = cs + pp[g]; }
+        if (g < G) { pp[g] = pp[g] * cw_of(g); cs = cs + pp[g]; }
       cs = fmaxf(cs, 1e-6f);
 #pragma unroll
       for (int g = 0; g < GP; ++g)
@@ -174,7 +190,7 @@ __device__ __forceinline__ void router_epilogue(float (&acc)[2 * GP + 1], int64_
       float scale_u = (1.0f - blend_scalar) * usage_boost;
 #pragma unroll
       for (int g = 0; g < GP; ++g)
-        if (g < G) gate[g] = gate[g] + ubv[g] * scale_u;
+        if (g < G) gate[g] = gate[g] + ub_of(g) * scale_u;
     }
     float gs = 0.f;
 #pragma unroll
@@ -204,18 +220,29 @@ __device__ __forceinline__ void router_epilogue(float (&acc)[2 * GP + 1], int64_
     importance[tok] = imp;
 
     // head_probs = gate_probs @ onehot(gate_to_head); top-k (ties -> lower head).
-    float hp[GP];
+    float hp[HPLDS ? 1 : GP];
+    if constexpr (HPLDS) {
+      for (int h = 0; h < H; ++h) hp_lds[h * 64 + lane] = 0.f;
 #pragma unroll
-    for (int h = 0; h < GP; ++h) hp[h] = 0.f;
+      for (int g = 0; g < GP; ++g)
+        if (g < G) hp_lds[gate_to_head[g] * 64 + lane] += gate[g];
+    } else {
 #pragma unroll
-    for (int g = 0; g < GP; ++g) {
-      if (g < G) {
-        const int hg = hgv[g];
+      for (int h = 0; h < GP; ++h) hp[h] = 0.f;
 #pragma unroll
-        for (int h = 0; h < GP; ++h)
-          if (h == hg) hp[h] = hp[h] + gate[g];
+      for (int g = 0; g < GP; ++g) {
+        if (g < G) {
+          const int hg = hgv[g];
+#pragma unroll
+          for (int h = 0; h < GP; ++h)
+            if (h == hg) hp[h] = hp[h] + gate[g];
+        }
       }
     }
+    auto hp_of = [&](int h) -> float {
+      if constexpr (HPLDS) return hp_lds[h * 64 + lane];
+      else return hp[h];
+    };
     uint64_t taken = 0;
     for (int j = 0; j < topk; ++j) {
       float bv = 0.f;
@@ -223,7 +250,8 @@ __device__ __forceinline__ void router_epilogue(float (&acc)[2 * GP + 1], int64_
 #pragma unroll
       for (int h = 0; h < GP; ++h) {
         if (h < H && !((taken >> h) & 1ull)) {
-          if (bi < 0 || better(hp[h], h, bv, bi)) { bv = hp[h]; bi = h; }
+          const float v = hp_of(h);
+          if (bi < 0 || better(v, h, bv, bi)) { bv = v; bi = h; }
         }
       }
       taken |= 1ull << bi;
@@ -811,6 +839,11 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
 // ((2G + 1, n_tok) f32); then the prototype EMA statistics of the wave's
 // tokens on MFMA (ema_accum_mfma over 16-gate blocks).  The arithmetic of
 // the 16-gate router: the same epilogue on the same f32 inputs.
+// LDS of router_epi_kernel per wave: (GP, 64) f32 head probabilities /
+// (64, GP) gate rows, or the x staging of the EMA statistics if larger.
+__host__ __device__ constexpr int rm_epi_wave_bytes(int GP) { return 64 * GP * 4 > kXsWave ? 64 * GP * 4 : kXsWave; }
+__host__ __device__ constexpr int rm_epi_lds_bytes(int GP) { return kRmWaves * rm_epi_wave_bytes(GP); }
+
 template <int GP, bool PROTO>
 __global__ void __launch_bounds__(64 * kRmWaves)
 router_epi_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, const float* __restrict__ rl,
@@ -839,16 +872,29 @@ router_epi_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, c
     acc_t[GP + g] = (PROTO && live && g < G) ? rl[(int64_t)(G + g) * n_tok + tok] : 0.f;
   }
   acc_t[2 * GP] = live ? rl[(int64_t)2 * G * n_tok + tok] : 0.f;
+  // the wave's LDS region: the head probabilities of the epilogue, then the
+  // gate rows of the EMA statistics, then (once the MFMA operands are built
+  // from them) its x staging
+  float* gl = reinterpret_cast<float*>(rm_lds + wid * rm_epi_wave_bytes(GP));
   float gate[GP];
-  router_epilogue<PFA_BF16, GP, PROTO>(acc_t, tok, live, group, G, raw.conf != nullptr ? r_cw : nullptr,
-                                       raw.usage != nullptr ? r_ub : nullptr, gate_to_head, H, topk, proto_temp,
-                                       proto_threshold, proto_blend, usage_boost, gate_probs, sim_out, blend_out,
-                                       importance, head_idx, head_score, group < n_groups ? stats : nullptr, gate);
-  if (ema_part != nullptr) {
-    float* gl = reinterpret_cast<float*>(rm_lds) + wid * 64 * GP;
+  // gate_probs is written below from the gate rows in LDS, a whole row per
+  // store instruction
+  router_epilogue<PFA_BF16, GP, PROTO, true>(acc_t, tok, live, group, G, raw.conf != nullptr ? r_cw : nullptr,
+                                             raw.usage != nullptr ? r_ub : nullptr, gate_to_head, H, topk,
+                                             proto_temp, proto_threshold, proto_blend, usage_boost, nullptr,
+                                             sim_out, blend_out, importance, head_idx, head_score,
+                                             group < n_groups ? stats : nullptr, gate, gl);
+  if (gate_probs == nullptr && ema_part == nullptr) return;
+  wave_sync();  // the epilogue's reads of the region are done
 #pragma unroll
-    for (int g = 0; g < GP; ++g) gl[lane * GP + g] = (live && g < G) ? gate[g] : 0.f;
-    __syncthreads();
+  for (int g = 0; g < GP; ++g) gl[lane * GP + g] = (live && g < G) ? gate[g] : 0.f;
+  wave_sync();
+  if (gate_probs != nullptr && group < n_groups) {
+    const int nt = (int)min<int64_t>(64, n_tok - tok0);
+    for (int t = 0; t < nt; ++t)
+      if (lane < G) gate_probs[(tok0 + t) * G + lane] = gl[t * GP + lane];
+  }
+  if (ema_part != nullptr) {
     if (group < n_groups) {
       float* part = ema_part + group * G * (C + 1);
       if (lane < G) {
@@ -856,14 +902,13 @@ router_epi_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, c
         for (int u = 0; u < 64; ++u) cs += gl[u * GP + lane];
         part[(int64_t)lane * (C + 1) + C] = cs;
       }
+      // ema_accum_mfma reads the gate rows into its operands before its
+      // first wave_sync and x staging write
       ema_accum_mfma<GP>(x, tok0, (int)min<int64_t>(64, n_tok - tok0), C, G, gl, part,
-                         reinterpret_cast<uint16_t*>(rm_lds + kRmWaves * 64 * GP * 4 + wid * kXsWave));
+                         reinterpret_cast<uint16_t*>(gl));
     }
   }
 }
-
-// LDS of router_epi_kernel: the gate rows and x staging of the EMA statistics.
-constexpr int rm_epi_lds_bytes(int GP, bool ema) { return ema ? kRmWaves * 64 * GP * 4 + kRmWaves * kXsWave : 0; }
 
 // Prototype EMA partial sums: part p accumulates, for a slice of at most
 // kEmaTok tokens, sum_t gate[t,g]*x[t,c] (columns 0..C-1) and sum_t gate[t,g]
@@ -1410,7 +1455,7 @@ extern "C" int pfa_router_topk_raw_ws(const void* x, int x_dtype, int64_t n_tok,
         nullptr, raw, rl);
   PFA_CHECK_LAUNCH("pfa_router_topk_raw_ws/dots");
 #define PFA_RE(GPV, PV)                                                                                          \
-  router_epi_kernel<GPV, PV><<<mb, 64 * kRmWaves, (size_t)rm_epi_lds_bytes(GPV, ema_partial != nullptr), s>>>(  \
+  router_epi_kernel<GPV, PV><<<mb, 64 * kRmWaves, (size_t)rm_epi_lds_bytes(GPV), s>>>(                        \
       (const uint16_t*)x, n_tok, C, G, rl, gate_to_head, H, topk, proto_temp, proto_threshold, proto_blend,      \
       usage_boost, gate_probs, sim, blend, importance, head_idx, head_score, stats_partial, ema_partial, raw)
   if (G <= 32) {
