@@ -1399,24 +1399,13 @@ class AdaptiveSparseAttention(nn.Module):
         self._last_gate_probs = gate_probs
         # the prototype EMA (aspa.py:692-718) reads only this forward's router
         # outputs and is read only by the next forward's router: it is queued
-        # last before the streams join (on the structured path, on the forked
-        # stream after the anchor pass, beside the main pass)
-
-
+        # last before the streams join (on the structured path beside the
+        # anchor and main passes, which run on the forked stream)
         heads64 = [None]
 
-        def ema(stream: Optional[torch.cuda.Stream] = None) -> None:
+        def ema() -> None:
             # the router's tail: the prototype EMA and the telemetry reduction
-            # (both read only router outputs; neither is read in this forward).
-            # `stream`: queued on that (forked) stream, which then also uses
-            # tensors allocated on this one
-            if stream is not None and not capture:
-                fused = getattr(self, "_ema_partial", None)
-                if fused is not None:
-                    fused[0].record_stream(stream)
-                comb.record_stream(stream)
-                x.record_stream(stream)
-                gate_probs.record_stream(stream)
+            # (both read only router outputs; neither is read in this forward)
             self._update_routing_prototypes(x, gate_probs)
             # the int64 active-head list of the sparse state, made here (off the
             # critical path) rather than when the telemetry is read
@@ -1662,19 +1651,19 @@ class AdaptiveSparseAttention(nn.Module):
                               before_join=None, rows_dev: Optional[torch.Tensor] = None, fuse: int = 0) -> None:
         """Candidate attention (aspa.py:1175-1310).
 
-        When no row can be truncated to L, bf16 with D=64 and no int8 path,
-        the candidate sets are used through their structure (window, strided
+        When no row can be truncated to L, in bf16 with D in
+        STRUCTURED_HEAD_DIMS, the candidate sets are used through their structure (window, strided
         anchors, prototype prefix sets) by pfa_shortlist_attn_fwd; otherwise
         the candidates are materialised (pfa_shortlist_build) and attended by
         pfa_sparse_attn_fwd.  Both give the reference's candidate sets.
 
         streams = (main, fork): qkv and attn come from work queued on the
         fork stream; the structured path queues its anchor pass there too
-        (after the packing on main) followed by `before_join(fork)`, while
-        main builds the prototype tables; main waits for the anchor pass
-        before the main pass and joins the fork stream after it.  The other
-        paths are entered with the fork stream already joined.  The
-        prototype tables are queued before the anchor pass so that, in a
+        (after the packing on main) and then its main pass (after the
+        prototype tables, built on main meanwhile), while `before_join()`
+        runs on main beside them; main joins the fork stream at the end.
+        The other paths are entered with the fork stream already joined.
+        The prototype tables are queued before the anchor pass so that, in a
         captured graph, they follow the packing on its queue instead of
         starting on another one.
 
@@ -1720,34 +1709,37 @@ class AdaptiveSparseAttention(nn.Module):
             blocks = evict = None
             if K > 0:
                 blocks, evict = _sa._proto_prefix_blocks(self._last_token_similarity, K)
-            tail_on_fork = False
             if packed is not None:
+                # anchor and main pass back to back on the fork stream (one
+                # hardware queue: no cross-queue wait between them); the main
+                # pass also waits for the prototype tables, queued on this
+                # stream, and `before_join` (the tail) runs here beside both
                 fork_s = streams[1]
                 fork_s.wait_event(packed)
-                # anchor pass on the fork stream, then `before_join` there:
-                # the main pass waits for the anchor pass only, and the tail
-                # runs beside it
                 with torch.cuda.stream(fork_s):
                     _sa._shortlist_attn_structured(*t4, *args, None, None, scale, device, want_lengths=False,
                                                    q_rope=q_rope, passes=1, part=part, fuse=fuse)
-                    anchored = torch.cuda.Event()
-                    anchored.record(fork_s)
-                    if before_join is not None:
-                        before_join(fork_s)
-                        tail_on_fork = True
-                streams[0].wait_event(anchored)
+                tables = torch.cuda.Event()
+                tables.record(streams[0])
+                if before_join is not None:
+                    before_join()
+                fork_s.wait_event(tables)
+                with torch.cuda.stream(fork_s):
+                    lens = _sa._shortlist_attn_structured(
+                        *t4, *args, blocks, evict, scale, device, want_lengths=bool(self.record_shortlist_lengths),
+                        q_rope=q_rope, passes=2, part=part, qkv_scales=qkv_scales, fuse=0)
+                if lens is not None and not torch.cuda.is_current_stream_capturing():
+                    lens.record_stream(streams[0])  # allocated on the fork stream, used and freed on this one
+                # join: the forward ends after the main pass
+                streams[0].wait_stream(fork_s)
             else:
                 if before_join is not None:
                     before_join()
                 if streams is not None:
                     streams[0].wait_stream(streams[1])
-            passes = 2 if (part is not None and streams is not None) else 3
-            lens = _sa._shortlist_attn_structured(
-                *t4, *args, blocks, evict, scale, device, want_lengths=bool(self.record_shortlist_lengths),
-                q_rope=q_rope, passes=passes, part=part, qkv_scales=qkv_scales, fuse=fuse if passes == 3 else 0)
-            if tail_on_fork:
-                # join: the forward ends after the tail
-                streams[0].wait_stream(streams[1])
+                lens = _sa._shortlist_attn_structured(
+                    *t4, *args, blocks, evict, scale, device, want_lengths=bool(self.record_shortlist_lengths),
+                    q_rope=q_rope, passes=3, part=part, qkv_scales=qkv_scales, fuse=fuse)
             self._last_shortlist_lengths = lens
             _record_backend("hip", device=str(device), tokens=T, rows=int(token_idx.numel()), L=L,
                             quantized=use_quant, candidates=True, structured=True)
