@@ -480,11 +480,11 @@ class AdaptiveSparseAttention(nn.Module):
         # write the zeros of the output rows without a packed row (no zero
         # fill of the output); with fuse_k_rope as well (and q rotated on
         # load) it also rotates k, so no RoPE pass runs either.  Both are off
-        # by default: the RoPE pass and the zero fill run on the forked stream
-        # while the router, the packing and the prototype tables run on the
-        # calling stream, and they are done before the packing is; the anchor
-        # pass waits for the packing, so work moved into it lengthens the
-        # forward (measured at configs 3 and 4).
+        # by default: the anchor pass's share of that work costs more than
+        # the pass it replaces (measured at configs 3 and 4; config 3 on one
+        # box: 0.4037 ms/step unfused, 0.4099 with the zeros in the anchor
+        # pass, 0.4425 with k's rotation as well -- each anchor workgroup
+        # rotates its class's rows before its first tile).
         self.fuse_anchor_pass = False
         self.fuse_k_rope = False
         # The prototype EMA statistics (sum_t gate * x) are accumulated inside
