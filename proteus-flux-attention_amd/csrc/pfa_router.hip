@@ -579,10 +579,12 @@ __device__ __forceinline__ void rm_conf_usage(const RouterRaw& raw, int G, float
   }
 }
 
-// DOTS: one 16-gate block (blockIdx.y) of a router with up to 64 gates
-// (RAWIN, GP = 16): the block's gate logits, prototype dots and (block 0)
-// the tokens' sums of squares go to rl, (2G + 1, n_tok) f32 (rows g, G + g
-// and 2G), for router_epi_kernel; no epilogue.
+// DOTS: one 16-gate block of a router with up to 64 gates (RAWIN, GP =
+// 16): the block's gate logits, prototype dots and (block 0) the tokens'
+// sums of squares go to rl, (2G + 1, n_tok) f32 (rows g, G + g and 2G), for
+// router_epi_kernel; no epilogue.  The grid is 1-D, XCD-aware: workgroup L
+// runs on XCD L mod 8, and the gate blocks of one token group take
+// consecutive slots of one XCD, so x is read once into that XCD's L2.
 template <int GP, bool PROTO, bool RAWIN, bool DOTS = false>
 __global__ void __launch_bounds__(64 * kRmWaves)
 router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, const float* __restrict__ wpk,
@@ -595,8 +597,18 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
   PFA_CRITICAL_CHAIN_PRIORITY();
   static_assert(GP == 8 || GP == 16, "MFMA router tables hold 8 or 16 gates");
   static_assert(!DOTS || (GP == 16 && RAWIN), "gate blocks take the 16-gate tables from the raw weights");
-  // DOTS: gates gb .. gb + Gk - 1 of G
-  const int gb = DOTS ? 16 * (int)blockIdx.y : 0;
+  // DOTS: token group bx, gates gb .. gb + G - 1 of Gall
+  int64_t bx = blockIdx.x;
+  int gbk = 0;
+  if constexpr (DOTS) {
+    const int ngb = (G + 15) / 16;
+    const int64_t slot = (int64_t)(blockIdx.x >> 3);
+    gbk = (int)(slot % ngb);
+    bx = (slot / ngb) * 8 + (blockIdx.x & 7);
+    const int64_t n_wg = ((n_tok + kRouterTok - 1) / kRouterTok + kRmWaves - 1) / kRmWaves;
+    if (bx >= n_wg) return;  // the grid is rounded up to whole slots of the eight XCDs
+  }
+  const int gb = 16 * gbk;
   const int Gall = G;
   if constexpr (DOTS) {
     G = min(16, Gall - gb);
@@ -691,7 +703,7 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
   }
   __syncthreads();
 
-  const int64_t group = (int64_t)blockIdx.x * kRmWaves + wid;
+  const int64_t group = bx * kRmWaves + wid;
   const int64_t n_groups = (n_tok + kRouterTok - 1) / kRouterTok;
   const int64_t tok0 = group * kRouterTok;
   const uint16_t* xr[4];
@@ -799,7 +811,7 @@ router_mfma_kernel(const uint16_t* __restrict__ x, int64_t n_tok, int C, int G, 
           rl[(int64_t)(gb + g) * n_tok + tok] = acc_t[g];
           if constexpr (PROTO) rl[(int64_t)(Gall + gb + g) * n_tok + tok] = acc_t[GP + g];
         }
-      if (blockIdx.y == 0) rl[(int64_t)2 * Gall * n_tok + tok] = acc_t[2 * GP];
+      if (gbk == 0) rl[(int64_t)2 * Gall * n_tok + tok] = acc_t[2 * GP];
     }
     return;
   }
@@ -1441,7 +1453,9 @@ extern "C" int pfa_router_topk_raw_ws(const void* x, int x_dtype, int64_t n_tok,
   float* rl = reinterpret_cast<float*>(workspace);
   const unsigned blocks = (unsigned)((n_tok + kRouterTok - 1) / kRouterTok);
   const unsigned mb = (blocks + kRmWaves - 1) / kRmWaves;
-  const dim3 gd(mb, (unsigned)((G + 15) / 16));
+  // XCD-aware 1-D grid (router_mfma_kernel's DOTS mapping): whole slots of
+  // the eight XCDs, each slot the gate blocks of one token group
+  const dim3 gd((unsigned)(((mb + 7) / 8) * 8 * ((G + 15) / 16)));
   // 16-gate blocks: logits, prototype dots and sums of squares into rl
   if (pr)
     router_mfma_kernel<16, true, true, true><<<gd, 64 * kRmWaves, (size_t)rm_lds_bytes(C, 16, true), s>>>(
