@@ -224,8 +224,10 @@ __device__ __forceinline__ void router_epilogue(float (&acc)[2 * GP + 1], int64_
     if constexpr (HPLDS) {
       for (int h = 0; h < H; ++h) hp_lds[h * 64 + lane] = 0.f;
 #pragma unroll
-      for (int g = 0; g < GP; ++g)
-        if (g < G) hp_lds[gate_to_head[g] * 64 + lane] += gate[g];
+      for (int g = 0; g < GP; ++g) {
+        const int hg = g < G ? gate_to_head[g] : -1;
+        if ((unsigned)hg < (unsigned)H) hp_lds[hg * 64 + lane] += gate[g];  // heads outside [0, H) take nothing
+      }
     } else {
 #pragma unroll
       for (int h = 0; h < GP; ++h) hp[h] = 0.f;
