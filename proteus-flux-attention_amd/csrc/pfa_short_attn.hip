@@ -760,7 +760,10 @@ short_anchor_kernel(ShortArgs a, int ccap) {
 // Occupancy: S = 2 stages (32 KB) allow four workgroups per CU and 128
 // VGPRs; S = 3 (48 KB) three workgroups and 168 VGPRs.  Measured at
 // config 3, four workgroups of two stages beat three of three: the pass is
-// bound by instruction latency more than by the tile transfers.
+// bound by instruction latency more than by the tile transfers.  Two stages
+// at three waves per SIMD (161 VGPRs, no spills; four waves spill 44-56
+// bytes per lane) were slower too, at configs 3 and 4 (the spill traffic
+// costs less than the fourth wave gains).
 #ifndef PFA_MAIN_STAGES
 #define PFA_MAIN_STAGES 2
 #endif
