@@ -4,7 +4,7 @@
 dominant kernel and the CPU oracle pipeline timed on the host beside it.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-                    [--workload cfg1|cfg2|cfg3|cfg4|cfg5]
+                    [--workload cfg1|cfg2|cfg3|cfg4|cfg5|tinytoy]
 
 Prints exactly one JSON line on stdout.  A "step" is one module forward of
 config 3 (router, head top-k, packing, QKV projection + RoPE, prototype
@@ -18,7 +18,9 @@ timed with HIP events, whose ms/step is reported as eager_ms_per_step.
 pass, no chunking); --workload cfg5 times one run of the chunked shortlist
 pipeline at T=1,048,576 (16 chunks of 65,536, top-512 per chunk, 8,192-token
 int8 shortlist, all-query final pass); --workload cfg1 / cfg2 time the
-token-sparse forward of BASELINE.json's two parity configurations.  None of
+token-sparse forward of BASELINE.json's two parity configurations;
+--workload tinytoy times config 3's forward with the head and gate shape of
+the reference's tinytoy recipe (32 heads of 16 dims, 64 gates).  None of
 these is the headline line.
 """
 from __future__ import annotations
@@ -43,6 +45,11 @@ CFG1 = dict(B=1, T=1024, C=256, H=8, keep=0.25, dtype="f32")
 CFG2 = dict(B=2, T=8192, C=512, H=8, keep=0.25, dtype="bf16")
 CFG3 = dict(B=1, T=65536, C=512, H=8, L=2048, window=512, stride=256, outlier=0.01)
 CFG4 = dict(B=1, T=524288, C=512, H=8, L=4096, window=512, stride=256, outlier=0.0)
+# the head and gate shape of the reference's tinytoy recipe (32 heads of 16
+# dims, 64 gates; kernels/tinytoy.py:307-325) on config 3's length and
+# candidate policy (not a BASELINE config: a measurement of the 16-dim
+# structured attention and the 64-gate MFMA router)
+CFG_TT = dict(B=1, T=65536, C=512, H=32, G=64, L=2048, window=512, stride=256, outlier=0.01)
 CFG5 = dict(T=1 << 20, C=512, H=8, chunk=65536, budget=512, buffer=8192)
 
 
@@ -71,7 +78,9 @@ def build_module(dev, dtype, c):
     from proteus_attention.models.aspa import AdaptiveSparseAttention, ModelConfig
 
     torch.manual_seed(1234)
-    m = AdaptiveSparseAttention(ModelConfig(**shortlist_cfg(c["T"], c["C"], c["H"], c["L"], c["window"], c["stride"])))
+    cfg = shortlist_cfg(c["T"], c["C"], c["H"], c["L"], c["window"], c["stride"])
+    cfg["attn_gates"] = c.get("G", c["H"])
+    m = AdaptiveSparseAttention(ModelConfig(**cfg))
     x, g = make_inputs(c["B"], c["T"], c["C"], seed=0, outlier_frac=c["outlier"])
     init_weights(m, g)
     weights_cpu = {n: t.detach().clone() for n, t in (("w_router", m.head_router.linear.weight),
@@ -155,7 +164,7 @@ def bench_forward(args, workload: str) -> dict:
     from proteus_attention import _hip
     from proteus_attention.kernels import sparse_attn as sa
 
-    c = CFG3 if workload == "cfg3" else CFG4
+    c = {"cfg3": CFG3, "cfg4": CFG4, "tinytoy": CFG_TT}[workload]
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16
     log(f"building {workload} module (T={c['T']})")
@@ -263,7 +272,8 @@ def bench_forward(args, workload: str) -> dict:
         "sparse_attn_fwd": ("mfma", 4.0 * sum_len * D, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", 1e12),
         "shortlist_attn_fwd": ("mfma", 4.0 * sum_len * D, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", 1e12),
         "shortlist_build": ("hbm", N * (4.0 * L + 12) + tokens * 4.0, HBM_PEAK_GBS, "GB/s", 1e9),
-        "router_topk": ("hbm", tokens * (c["C"] * E + 8 * 2 + 12) + 8 * c["C"] * (E + 4), HBM_PEAK_GBS, "GB/s", 1e9),
+        "router_topk": ("hbm", tokens * (c["C"] * E + 8 * 2 + 12) + c.get("G", c["H"]) * c["C"] * (E + 4), HBM_PEAK_GBS,
+                        "GB/s", 1e9),
         # the module path builds the compact tables: scores in, per-64-token
         # block set rows and per-token evict entries out
         "proto_prefix_blocks": ("hbm", tokens * 8.0 + ((c["T"] + 63) // 64) * c["B"] * K * 4.0, HBM_PEAK_GBS,
@@ -285,8 +295,10 @@ def bench_forward(args, workload: str) -> dict:
     if workload == "cfg3" and not args.no_cpu_baseline:
         log("cpu baseline (oracle pipeline on host cores)")
         cpu = cpu_baseline(x_cpu, weights, dtype, c, caps)
-    metric = ("shortlist fwd tokens/s @T=64K bf16 + % of HBM/MFMA roofline, 1 GPU" if workload == "cfg3" else
-              "shortlist fwd tokens/s @T=512K bf16 single pass, 1 GPU")
+    metric = {"cfg3": "shortlist fwd tokens/s @T=64K bf16 + % of HBM/MFMA roofline, 1 GPU",
+              "cfg4": "shortlist fwd tokens/s @T=512K bf16 single pass, 1 GPU",
+              "tinytoy": "shortlist fwd tokens/s @T=64K bf16, 32 heads x 16 dims, 64 gates, 1 GPU"}[workload]
+    name = f"config {workload[-1]}" if workload.startswith("cfg") else "tinytoy shape"
     return {
         "metric": metric,
         "value": round(value, 1),
@@ -302,9 +314,9 @@ def bench_forward(args, workload: str) -> dict:
         "dtype": "bf16",
         "data": (f"synthetic: x~N(0,1) seed 0{' with 1% rows x4' if c['outlier'] else ''}, Xavier-normal weights "
                  "from the same generator"),
-        "config": {"workload": (f"config {workload[-1]}: ASPA shortlist forward, B=1 T={c['T']} d_model=512 H=8 D=64 "
-                                f"L={L} window={local_w} anchor_stride={stride} policy=local+anchors+proto top-2 "
-                                "heads"),
+        "config": {"workload": (f"{name}: ASPA shortlist forward, B=1 T={c['T']} d_model={c['C']} H={c['H']} D={D} "
+                                f"gates={c.get('G', c['H'])} L={L} window={local_w} anchor_stride={stride} "
+                                "policy=local+anchors+proto top-2 heads"),
                    "rows": N, "sum_candidates": sum_len, "global_batch": 1, "seq_len": c["T"],
                    "peak_mem_gib": round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 2),
                    "parallelism": "single GPU"},
@@ -490,7 +502,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3", "cfg4", "cfg5"), default="cfg3",
+    ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "tinytoy"), default="cfg3",
                     help="cfg3 is the bench line; cfg1/cfg2 are BASELINE's parity configurations, timed on request")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cfg5-source", choices=("device", "pinned", "disk"), default="device",
