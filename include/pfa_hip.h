@@ -355,8 +355,8 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
 
 /* ====================================================================
  * Shortlist attention without materialised candidates (bf16, D = 16, 32,
- * 64 or 128; q_rope_cos / q_rope_sin and the fused variant's fuse bits need
- * D = 64).
+ * 64 or 128; q_rope_cos / q_rope_sin need D <= 64 and the fused variant's
+ * fuse bits D = 64).
  * Same result as pfa_shortlist_build followed by pfa_sparse_attn_fwd for the
  * module's packed rows when no row is truncated (local_w + anchors below the
  * window + proto_k + 1 <= L, checked by the caller): each row attends to its
@@ -372,7 +372,7 @@ int pfa_sparse_attn_fwd(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v,
  *   floats_for(D)) f32 scratch for the anchor pass (pfa_shortlist_attn_part_
  *   floats() is the width for D <= 64); lengths (N) int32 or NULL
  *   receives each row's candidate count (the builder's lengths).
- *   q_rope_cos / q_rope_sin: NULL, or the bf16 (T, 64) RoPE tables of
+ *   q_rope_cos / q_rope_sin: NULL, or the bf16 (T, D) RoPE tables (D <= 64) of
  *   pfa_rope_qk_inplace; q rows are then rotated as they are loaded (the
  *   caller rotated only k, with pfa_rope_k_inplace), giving the same q bits
  *   as rotating the q tensor first.

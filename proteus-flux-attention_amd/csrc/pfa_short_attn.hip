@@ -380,11 +380,18 @@ __device__ __forceinline__ void load_q(const uint16_t* qrow, bf16x8_t (&qf)[NQ],
 // (even, odd) pairs, rotated with the same arithmetic as the RoPE kernels
 // (rope_rotate8), so the fragments hold exactly the bits a rotated q tensor
 // would hold.
+// NARROW: chunks past cmask (a row of 16 or 32 dims, tables of that width)
+// are zero.
+template <bool NARROW>
 __device__ __forceinline__ void load_q_rope(const uint16_t* qrow, const uint16_t* crow, const uint16_t* srow,
-                                            bf16x8_t (&qf)[2]) {
+                                            bf16x8_t (&qf)[2], uint32_t cmask) {
   const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
   for (int dc = 0; dc < 2; ++dc) {
+    if (NARROW && (uint32_t)(4 * dc + g) > cmask) {
+      qf[dc] = bf16x8_t{};
+      continue;
+    }
     const int d0 = 32 * dc + 8 * g;
     float xv[8], cv[8], sv[8], o[8];
     load8<PFA_BF16>(qrow + d0, xv);
@@ -399,12 +406,14 @@ __device__ __forceinline__ void load_q_rope(const uint16_t* qrow, const uint16_t
 }
 
 // NARROW: a row of 16 or 32 dims (a.cmask); otherwise 32 * NQ dims.  The
-// RoPE tables on load are for 64-dim rows (NQ = 2, checked by the host).
+// RoPE tables on load are (T, D) for rows of at most 64 dims (NQ = 2,
+// checked by the host).
 template <int NQ, bool NARROW>
 __device__ __forceinline__ void load_q_row(const ShortArgs& a, const uint16_t* qb, int64_t t, bf16x8_t (&qf)[NQ]) {
   if constexpr (NQ == 2) {
     if (a.rcos != nullptr) {
-      load_q_rope(qb + t * a.q.s_t, a.rcos + t * 64, a.rsin + t * 64, qf);
+      const int64_t tw = NARROW ? (int64_t)a.dh : 64;  // table row width
+      load_q_rope<NARROW>(qb + t * a.q.s_t, a.rcos + t * tw, a.rsin + t * tw, qf, NARROW ? a.cmask : 7u);
       return;
     }
   }
@@ -1177,9 +1186,10 @@ static int shortlist_attn_run(pfa_tensor4 q, pfa_tensor4 k, pfa_tensor4 v, pfa_t
                               int fuse, void* stream) {
   PFA_CHECK_ARG(dtype == PFA_BF16 && (D == 16 || D == 32 || D == 64 || D == 128),
                 "pfa_shortlist_attn_fwd: bf16 with D = 16, 32, 64 or 128 only (got dtype %d D %d)", dtype, D);
-  // the q RoPE tables and the anchor-pass fusions work on 64-wide rows
-  PFA_CHECK_ARG(D == 64 || (q_rope_cos == nullptr && fuse == 0),
-                "pfa_shortlist_attn_fwd: q RoPE on load and the anchor-pass fusions need D=64 (got D %d)", D);
+  // q RoPE on load takes rows of at most 64 dims, the anchor-pass fusions 64
+  PFA_CHECK_ARG((D <= 64 || q_rope_cos == nullptr) && (D == 64 || fuse == 0),
+                "pfa_shortlist_attn_fwd: q RoPE on load needs D <= 64 and the anchor-pass fusions D = 64 (got D %d)",
+                D);
   PFA_CHECK_ARG(H > 0 && T > 0 && T < INT32_MAX && N >= 0 && P_cap > 0 && local_w >= 1,
                 "pfa_shortlist_attn_fwd: bad sizes");
   PFA_CHECK_ARG(passes >= 1 && passes <= 3, "pfa_shortlist_attn_fwd: passes must be 1, 2 or 3 (got %d)", passes);

@@ -424,7 +424,7 @@ def _shortlist_attn_structured(
     (bf16, D in STRUCTURED_HEAD_DIMS); the prototype sets come as _proto_prefix_blocks tables of
     the T-token scores.  Returns each row's candidate count (int32, (N,)),
     or None when want_lengths is False (the kernel then skips the counting).
-    q_rope = (cos, sin) bf16 (T, 64) tables: q is still unrotated and its
+    q_rope = (cos, sin) bf16 (T, D) tables (D <= 64): q is still unrotated and its
     rows are rotated as the kernel loads them.  passes = 1 runs only the
     anchor pass and 2 only the main pass (the caller orders them and passes
     the same `part`, from shortlist_partials, to both); 3 runs both.
@@ -454,13 +454,14 @@ def _shortlist_attn_structured(
         if evict is None or int(evict.size(1)) != int(T) or int(blocks.size(1)) != (int(T) + 63) // 64:
             raise ValueError("prototype block tables must cover the T tokens of the sequence")
     rc_cos = rc_sin = None
-    if (q_rope is not None or fuse) and int(D) != 64:
-        raise ValueError("q RoPE on load and the anchor-pass fusions need D = 64")
+    if (q_rope is not None and int(D) > 64) or (fuse and int(D) != 64):
+        raise ValueError("q RoPE on load needs D <= 64 and the anchor-pass fusions D = 64")
     if q_rope is not None:
         rc_cos, rc_sin = q_rope
-        if (rc_cos.dtype != torch.bfloat16 or rc_sin.dtype != torch.bfloat16 or tuple(rc_cos.shape) != (int(T), 64)
-                or tuple(rc_sin.shape) != (int(T), 64) or not rc_cos.is_contiguous() or not rc_sin.is_contiguous()):
-            raise ValueError("q_rope tables must be contiguous bf16 (T, 64)")
+        if (rc_cos.dtype != torch.bfloat16 or rc_sin.dtype != torch.bfloat16 or tuple(rc_cos.shape) != (int(T), int(D))
+                or tuple(rc_sin.shape) != (int(T), int(D)) or not rc_cos.is_contiguous()
+                or not rc_sin.is_contiguous()):
+            raise ValueError("q_rope tables must be contiguous bf16 (T, D)")
     if fuse:
         if qkv_scales is not None:
             raise ValueError("the fused anchor pass has no int8 mode")

@@ -1506,9 +1506,9 @@ class AdaptiveSparseAttention(nn.Module):
         # and fuse_anchor_pass its anchor pass (on the forked stream) writes
         # the zeros of the rows without a packed row (no zero fill) and, with
         # fuse_k_rope, rotates k as well (no RoPE pass).
-        q_fused = structured and self.fuse_q_rope and not use_quant and self.d_head == 64
+        q_fused = structured and self.fuse_q_rope and not use_quant and self.d_head <= 64
         fuse = 0
-        if q_fused and self.fuse_anchor_pass and plan["stride"] > 0 and plan["slots"] > 0:
+        if q_fused and self.d_head == 64 and self.fuse_anchor_pass and plan["stride"] > 0 and plan["slots"] > 0:
             fuse = _sa.FUSE_ZERO | (_sa.FUSE_K_ROPE if (self.use_rope and self.fuse_k_rope) else 0)
         with torch.cuda.stream(fork_s):
             rot_k = not (fuse & _sa.FUSE_K_ROPE)
